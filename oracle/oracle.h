@@ -1,0 +1,81 @@
+/* CPU oracle for the newch hot path -- TEST INFRASTRUCTURE ONLY.
+ *
+ * A from-scratch C restatement of the reference engine's arithmetic on this path, used by tests/,
+ * __graft_entry__.smoke() and bench.py's cpu_baseline leg as the checker.  The product library
+ * (newch_amd/libnc.so) never links or calls it.
+ *
+ * Every function follows the reference's evaluation order op for op (file:line cited at each
+ * definition in oracle.c), so on the same inputs it reproduces the reference bit for bit,
+ * including its sequential fp32 summation orders.  Pinning: tests/test_oracle.py checks each
+ * function against the fixtures in tests/golden/ (written by the compiled reference), against
+ * oracle/_ref/libnc_ref.so when it is built, against the reference's own known-answer tests and
+ * against closed forms / fp64 brute force.
+ *
+ * Layout conventions: all tensors are float32 unless noted; strides are in elements; "contiguous"
+ * means row-major.
+ */
+#ifndef NC_ORACLE_H
+#define NC_ORACLE_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* unary kinds (same numbering as the HIP layer's NC_HIP_UN_*) */
+enum {
+    OR_UN_RELU = 0, OR_UN_LEAKY_RELU, OR_UN_RELU6, OR_UN_HARDSIGMOID, OR_UN_HARDSWISH,
+    OR_UN_SILU, OR_UN_GELU, OR_UN_GELU_TANH, OR_UN_SIGMOID, OR_UN_TANH, OR_UN_EXP,
+    OR_UN_NEG, OR_UN_SCALE, OR_UN_ADD_SCALAR, OR_UN_COUNT
+};
+enum { OR_BIN_ADD = 0, OR_BIN_SUB, OR_BIN_MUL, OR_BIN_DIV };
+enum { OR_RED_SUM = 0, OR_RED_MEAN, OR_RED_MAX, OR_RED_ARGMAX };
+
+/* vector-tier transcendentals, one element at a time */
+float or_exp(float x);
+float or_sigmoid(float x);
+float or_tanh(float x);
+float or_erf(float x);
+void or_map(int fn, int64_t n, const float *x, float *y); /* fn: 0 exp, 1 sigmoid, 2 tanh, 3 erf */
+
+float or_sum_f32(int64_t n, const float *x);
+void or_axpy(int64_t n, float alpha, const float *x, float *y);
+
+/* activations: y = f(x); gi += f'(x) * g  (x and y both given; each kind reads what it needs) */
+void or_unary_fwd(int kind, float s, const float *x, float *y, int64_t n);
+void or_unary_bwd(int kind, float s, const float *x, const float *y, const float *g, float *gi, int64_t n);
+
+/* broadcast binary forward over an output of `nd` dims; sa/sb are broadcast strides (0 on
+ * broadcast dims), so = output strides */
+void or_binary_fwd(int op, int nd, const int64_t *shape, const float *a, const int64_t *sa, const float *b,
+                   const int64_t *sb, float *o, const int64_t *so);
+
+/* binary backward (sum-to-shape).  a/b are given by data + ndim + shape + strides (a view may be
+ * strided); g is the contiguous output grad; ga/gb are contiguous grads of a's and b's shapes,
+ * accumulated into (NULL = not needed). */
+void or_binary_bwd(int op, int a_nd, const int64_t *a_shape, const int64_t *a_stride, const float *a, int b_nd,
+                   const int64_t *b_shape, const int64_t *b_stride, const float *b, const float *g, float *ga,
+                   float *gb);
+
+/* reductions over x viewed as [outer, R, inner] (contiguous); arg may be NULL for sum/mean */
+void or_reduce_fwd(int kind, int64_t outer, int64_t R, int64_t inner, const float *x, float *y, int32_t *arg);
+void or_reduce_bwd(int kind, int64_t outer, int64_t R, int64_t inner, const float *g, const int32_t *arg,
+                   float *gi);
+
+void or_softmax_fwd(int log_form, int64_t rows, int64_t C, const float *x, float *y);
+void or_softmax_bwd(int log_form, int64_t rows, int64_t C, const float *y, const float *g, float *gi);
+
+/* stats: [rows][2] = {mean, rstd}; w/b may be NULL; gx/gw/gb may be NULL and accumulate */
+void or_layer_norm_fwd(int64_t rows, int64_t D, const float *x, const float *w, const float *b, float eps,
+                       float *y, float *stats);
+void or_layer_norm_bwd(int64_t rows, int64_t D, const float *x, const float *w, const float *stats,
+                       const float *g, float *gx, float *gw, float *gb);
+
+void or_quantize_rows(int64_t rows, int64_t cols, const float *w, int8_t *q, float *scale);
+void or_dequantize_rows(int64_t rows, int64_t cols, const int8_t *q, const float *scale, float *w);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

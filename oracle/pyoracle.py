@@ -1,0 +1,224 @@
+"""numpy wrappers over the C oracle (oracle/_build/liboracle.so) -- TEST INFRASTRUCTURE ONLY.
+
+Imported by tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg, as the checker / CPU
+baseline.  The product library never uses it.  Function semantics: see oracle.h.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import subprocess
+from ctypes import c_float, c_int, c_int64, c_void_p
+from pathlib import Path
+
+import numpy as np
+
+HERE = Path(__file__).resolve().parent
+LIB = HERE / "_build" / "liboracle.so"
+REF_LIB = HERE / "_ref" / "libnc_ref.so"
+
+UN = {"relu": 0, "leaky_relu": 1, "relu6": 2, "hardsigmoid": 3, "hardswish": 4, "silu": 5, "gelu": 6,
+      "gelu_tanh": 7, "sigmoid": 8, "tanh": 9, "exp": 10, "neg": 11, "scale": 12, "add_scalar": 13}
+BIN = {"add": 0, "sub": 1, "mul": 2, "div": 3}
+RED = {"sum": 0, "mean": 1, "max": 2, "argmax": 3}
+
+_lib = None
+
+
+def build() -> Path:
+    subprocess.run(["make", "-s", "-C", str(HERE), "port"], check=True)
+    return LIB
+
+
+def lib() -> ctypes.CDLL:
+    global _lib
+    if _lib is None:
+        if not LIB.exists():
+            build()
+        L = ctypes.CDLL(str(LIB))
+        for nm in ("or_exp", "or_sigmoid", "or_tanh", "or_erf"):
+            getattr(L, nm).restype = c_float
+            getattr(L, nm).argtypes = [c_float]
+        L.or_sum_f32.restype = c_float
+        _lib = L
+    return _lib
+
+
+def _p(a):
+    return None if a is None else a.ctypes.data_as(c_void_p)
+
+
+def _f32(a):
+    return np.ascontiguousarray(a, dtype=np.float32)
+
+
+def _i64(v):
+    v = list(v)
+    return (c_int64 * max(len(v), 1))(*v)
+
+
+def vmap(fn: str, x):
+    x = _f32(x)
+    y = np.empty_like(x)
+    lib().or_map(c_int({"exp": 0, "sigmoid": 1, "tanh": 2, "erf": 3}[fn]), c_int64(x.size), _p(x), _p(y))
+    return y
+
+
+def sum_f32(x):
+    x = _f32(x)
+    return np.float32(lib().or_sum_f32(c_int64(x.size), _p(x)))
+
+
+def unary_fwd(kind: str, x, s: float = 0.0):
+    x = _f32(x)
+    y = np.empty_like(x)
+    lib().or_unary_fwd(c_int(UN[kind]), c_float(s), _p(x), _p(y), c_int64(x.size))
+    return y
+
+
+def unary_bwd(kind: str, x, y, g, gi=None, s: float = 0.0):
+    x, g = _f32(x), _f32(g)
+    y = None if y is None else _f32(y)
+    gi = np.zeros_like(g) if gi is None else _f32(gi).copy()
+    lib().or_unary_bwd(c_int(UN[kind]), c_float(s), _p(x), _p(y), _p(g), _p(gi), c_int64(g.size))
+    return gi
+
+
+def broadcast_shape(*shapes):
+    nd = max(len(s) for s in shapes)
+    out = []
+    for i in range(nd):
+        dims = [s[i - (nd - len(s))] if i - (nd - len(s)) >= 0 else 1 for s in shapes]
+        d = max(dims)
+        out.append(d if all(x in (1, d) for x in dims) else None)
+    if None in out:
+        raise ValueError(f"shapes {shapes} are not broadcastable")
+    return tuple(out)
+
+
+def _elem_strides(a: np.ndarray):
+    return tuple(s // a.itemsize for s in a.strides)
+
+
+def _bcast_strides(shape, strides, out_shape):
+    nd = len(out_shape)
+    res = []
+    for i in range(nd):
+        j = i - (nd - len(shape))
+        res.append(0 if j < 0 or (shape[j] == 1 and out_shape[i] != 1) else strides[j])
+    return res
+
+
+def _base_and_offset(a: np.ndarray):
+    """(flat float32 base array, element offset of a[0,...]) for a view into a contiguous base."""
+    base = a
+    while base.base is not None and isinstance(base.base, np.ndarray):
+        base = base.base
+    off = (a.__array_interface__["data"][0] - base.__array_interface__["data"][0]) // a.itemsize
+    return base, off
+
+
+def binary_fwd(op: str, a, b):
+    """a, b: float32 numpy arrays, possibly strided views (a view's strides are honoured)."""
+    out_shape = broadcast_shape(a.shape, b.shape)
+    o = np.empty(out_shape, np.float32)
+    sa = _bcast_strides(a.shape, _elem_strides(a), out_shape)
+    sb = _bcast_strides(b.shape, _elem_strides(b), out_shape)
+    so = _elem_strides(o) if o.ndim else ()
+    nd = len(out_shape)
+    # pass a pointer to element 0 of each (possibly strided) view
+    lib().or_binary_fwd(c_int(BIN[op]), c_int(nd), _i64(out_shape), c_void_p(a.__array_interface__["data"][0]),
+                        _i64(sa), c_void_p(b.__array_interface__["data"][0]), _i64(sb), _p(o), _i64(so))
+    return o
+
+
+def binary_bwd(op: str, a, b, g, need_a=True, need_b=True):
+    """Grads (in a's and b's logical shapes, contiguous) of sum(op(a, b) * g)."""
+    g = _f32(g)
+    ga = np.zeros(a.shape, np.float32) if need_a else None
+    gb = np.zeros(b.shape, np.float32) if need_b else None
+    lib().or_binary_bwd(c_int(BIN[op]), c_int(a.ndim), _i64(a.shape), _i64(_elem_strides(a)),
+                        c_void_p(a.__array_interface__["data"][0]), c_int(b.ndim), _i64(b.shape),
+                        _i64(_elem_strides(b)), c_void_p(b.__array_interface__["data"][0]), _p(g), _p(ga), _p(gb))
+    return ga, gb
+
+
+def reduce_dims(shape, axis):
+    if axis is None or axis == -128:
+        return 1, int(np.prod(shape)), 1
+    axis = axis % len(shape)
+    outer = int(np.prod(shape[:axis]))
+    inner = int(np.prod(shape[axis + 1:]))
+    return outer, int(shape[axis]), inner
+
+
+def reduce_fwd(kind: str, x, axis):
+    x = _f32(x)
+    outer, R, inner = reduce_dims(x.shape, axis)
+    y = np.empty(outer * inner, np.float32)
+    arg = np.empty(outer * inner, np.int32)
+    lib().or_reduce_fwd(c_int(RED[kind]), c_int64(outer), c_int64(R), c_int64(inner), _p(x), _p(y), _p(arg))
+    return (arg if kind == "argmax" else y), arg
+
+
+def reduce_bwd(kind: str, x_shape, axis, g, arg=None, gi=None):
+    outer, R, inner = reduce_dims(x_shape, axis)
+    g = _f32(g)
+    gi = np.zeros(int(np.prod(x_shape)), np.float32) if gi is None else _f32(gi).copy().ravel()
+    lib().or_reduce_bwd(c_int(RED[kind]), c_int64(outer), c_int64(R), c_int64(inner), _p(g),
+                        _p(None if arg is None else np.ascontiguousarray(arg, np.int32)), _p(gi))
+    return gi.reshape(x_shape)
+
+
+def softmax_fwd(x, log_form=False):
+    x = _f32(x)
+    C = x.shape[-1]
+    y = np.empty_like(x)
+    lib().or_softmax_fwd(c_int(int(log_form)), c_int64(x.size // max(C, 1)), c_int64(C), _p(x), _p(y))
+    return y
+
+
+def softmax_bwd(y, g, log_form=False, gi=None):
+    y, g = _f32(y), _f32(g)
+    C = y.shape[-1]
+    gi = np.zeros_like(y) if gi is None else _f32(gi).copy()
+    lib().or_softmax_bwd(c_int(int(log_form)), c_int64(y.size // max(C, 1)), c_int64(C), _p(y), _p(g), _p(gi))
+    return gi
+
+
+def layer_norm_fwd(x, D, w=None, b=None, eps=1e-5):
+    x = _f32(x)
+    rows = x.size // D
+    y = np.empty_like(x)
+    stats = np.empty(2 * rows, np.float32)
+    lib().or_layer_norm_fwd(c_int64(rows), c_int64(D), _p(x), _p(None if w is None else _f32(w)),
+                            _p(None if b is None else _f32(b)), c_float(eps), _p(y), _p(stats))
+    return y, stats
+
+
+def layer_norm_bwd(x, D, stats, g, w=None, need_w=False, need_b=False):
+    x, g = _f32(x), _f32(g)
+    rows = x.size // D
+    gx = np.zeros_like(x)
+    gw = np.zeros(D, np.float32) if need_w else None
+    gb = np.zeros(D, np.float32) if need_b else None
+    lib().or_layer_norm_bwd(c_int64(rows), c_int64(D), _p(x), _p(None if w is None else _f32(w)), _p(_f32(stats)),
+                            _p(g), _p(gx), _p(gw), _p(gb))
+    return gx, gw, gb
+
+
+def quantize_rows(w):
+    w = _f32(w)
+    rows, cols = w.shape
+    q = np.empty((rows, cols), np.int8)
+    s = np.empty(rows, np.float32)
+    lib().or_quantize_rows(c_int64(rows), c_int64(cols), _p(w), _p(q), _p(s))
+    return q, s
+
+
+def dequantize_rows(q, scale):
+    q = np.ascontiguousarray(q, np.int8)
+    rows, cols = q.shape
+    w = np.empty((rows, cols), np.float32)
+    lib().or_dequantize_rows(c_int64(rows), c_int64(cols), _p(q), _p(_f32(scale)), _p(w))
+    return w

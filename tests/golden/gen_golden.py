@@ -1,0 +1,369 @@
+"""Writes the golden vectors in tests/golden/*.npz from the compiled reference engine.
+
+Run in a container that has the reference tree (oracle/_ref/libnc_ref.so is built from it by
+`make -C oracle ref`):
+
+    python tests/golden/gen_golden.py
+
+Every input is drawn here from numpy's seeded generator and stored next to the reference's outputs,
+so the fixtures are self-contained data.  Outputs come from the reference's public C API (nc.h),
+driven through ctypes exactly as its Python package drives it, and for the four vector
+transcendentals from its kernel table (oracle/ref_probe.c).  Backward values are obtained the way
+the reference computes them: loss = sum(out * G) and a retained backward pass, which seeds the
+output grad with exactly G.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import sys
+from ctypes import c_float, c_int64, c_void_p
+from pathlib import Path
+
+import numpy as np
+
+ROOT = Path(__file__).resolve().parents[2]
+sys.path.insert(0, str(ROOT))
+from newch_amd import abi  # noqa: E402
+
+OUT = Path(__file__).resolve().parent
+REF_LIB = ROOT / "oracle" / "_ref" / "libnc_ref.so"
+
+SPECIALS = np.array([0.0, -0.0, np.inf, -np.inf, np.nan, 1e-40, -1e-40, 1e-30, -1e-30, 1e-6, -1e-6,
+                     -87.3365448, -87.34, -87.33, -87.5, -95.0, -120.0, 88.5, 88.7, 88.72, 88.8, 100.0,
+                     0.25, 0.2499999, 0.2500001, -0.25, -0.2499999, 0.0625, -3.0, 3.0, -3.0000002, 3.0000002,
+                     -2.9999998, 2.9999998, 6.0, 5.9999995, 6.0000005, -6.0, 0.5, -0.5, 1.0, -1.0, 2.0, -2.0,
+                     -5.0, -7.5, -10.0, -13.0, -20.0, 5.0, 10.0, 20.0, 1e30, -1e30, 3.4e38, -3.4e38],
+                    dtype=np.float32)
+
+
+class Ref:
+    """A reference engine context with helpers to move numpy arrays in and out."""
+
+    def __init__(self, lib):
+        self.lib = lib
+        cfg = abi.Config(0, 1234, 0, 0)
+        self.ctx = lib.nc_init(ctypes.byref(cfg))
+
+    def check(self):
+        if not self.lib.nc_ok(self.ctx):
+            raise RuntimeError(self.lib.nc_error(self.ctx).decode())
+
+    def tensor(self, arr, dtype=abi.F32):
+        arr = np.ascontiguousarray(arr)
+        nd, shp = abi.shape_arg(arr.shape)
+        t = self.lib.nc_from_data(self.ctx, dtype, arr.ctypes.data_as(c_void_p), nd, shp)
+        self.check()
+        return t
+
+    def param(self, arr):
+        src = self.tensor(np.asarray(arr, np.float32))
+        nd, shp = abi.shape_arg(arr.shape)
+        p = self.lib.nc_parameter(self.ctx, src, nd, shp)
+        self.check()
+        return p
+
+    def read(self, t, dtype=np.float32):
+        self.check()
+        n = self.lib.nc_numel(t)
+        nd = self.lib.nc_ndim(t)
+        shape = tuple(self.lib.nc_shape(t)[i] for i in range(nd))
+        out = np.empty(n, dtype=dtype)
+        ok = self.lib.nc_copy_to(t, out.ctypes.data_as(c_void_p), out.nbytes)
+        if not ok:
+            raise RuntimeError("copy_to failed")
+        return out.reshape(shape)
+
+    def backward_with(self, out, G):
+        """loss = sum(out * G); retained backward, so the output grad is exactly G."""
+        loss = self.lib.nc_sum(self.lib.nc_mul(out, self.tensor(G.astype(np.float32))), abi.ALL_AXES, 0)
+        self.check()
+        st = self.lib.nc_backward_ex(loss, abi.BACKWARD_RETAIN, None, 0)
+        if st != 0:
+            raise RuntimeError(self.lib.nc_error(self.ctx).decode())
+
+    def grad(self, t):
+        g = self.lib.nc_grad(t)
+        if not g:
+            raise RuntimeError("no grad")
+        return self.read(g)
+
+    def step_end(self):
+        self.lib.nc_step_end(self.ctx)
+
+
+def gen_transcendentals(lib, rng):
+    grid = np.linspace(-100, 100, 2001, dtype=np.float32)
+    dense = np.linspace(-6, 6, 1201, dtype=np.float32)
+    rnd = (rng.standard_normal(2048) * 4).astype(np.float32)
+    bits = np.frombuffer(rng.integers(0, 2 ** 32, 2048, dtype=np.uint32).tobytes(), np.float32)
+    x = np.concatenate([SPECIALS, grid, dense, rnd, bits]).astype(np.float32)
+    res = {"x": x}
+    P = c_void_p
+    for nm in ("exp", "sigmoid", "tanh", "erf"):
+        y = np.empty_like(x)
+        getattr(lib, f"ncref_{nm}_f32")(c_int64(x.size), x.ctypes.data_as(P), y.ctypes.data_as(P))
+        res[nm] = y
+    sums = []
+    sx = rng.standard_normal(5000).astype(np.float32)
+    lib.ncref_sum_f32.restype = c_float
+    for n in (0, 1, 7, 15, 16, 17, 31, 32, 33, 100, 1000, 4999):
+        sums.append(lib.ncref_sum_f32(c_int64(n), sx.ctypes.data_as(P)))
+    res["sum_x"] = sx
+    res["sum_n"] = np.array([0, 1, 7, 15, 16, 17, 31, 32, 33, 100, 1000, 4999], np.int64)
+    res["sum_out"] = np.array(sums, np.float32)
+    np.savez_compressed(OUT / "transcendentals.npz", **res)
+
+
+UNARY = [  # name, kind (oracle numbering), nc.h call
+    ("relu", 0, lambda L, t: L.nc_relu(t)),
+    ("leaky_relu", 1, lambda L, t: L.nc_leaky_relu(t, 0.01)),
+    ("leaky_relu_02", 1, lambda L, t: L.nc_leaky_relu(t, 0.2)),
+    ("relu6", 2, lambda L, t: L.nc_relu6(t)),
+    ("hardsigmoid", 3, lambda L, t: L.nc_hardsigmoid(t)),
+    ("hardswish", 4, lambda L, t: L.nc_hardswish(t)),
+    ("silu", 5, lambda L, t: L.nc_silu(t)),
+    ("gelu", 6, lambda L, t: L.nc_gelu(t, 0)),
+    ("gelu_tanh", 7, lambda L, t: L.nc_gelu(t, 1)),
+    ("sigmoid", 8, lambda L, t: L.nc_sigmoid(t)),
+    ("tanh", 9, lambda L, t: L.nc_tanh(t)),
+    ("exp", 10, lambda L, t: L.nc_exp(t)),
+]
+
+
+def gen_unary(ref, rng):
+    x = np.concatenate([SPECIALS, (rng.standard_normal(1037) * 3).astype(np.float32),
+                        np.linspace(-8, 8, 513, dtype=np.float32)]).astype(np.float32)
+    g = rng.standard_normal(x.size).astype(np.float32)
+    res = {"x": x, "g": g}
+    for name, _, fn in UNARY:
+        p = ref.param(x)
+        y = fn(ref.lib, p)
+        res[f"{name}_y"] = ref.read(y)
+        ref.backward_with(y, g)
+        res[f"{name}_gx"] = ref.grad(p)
+        ref.step_end()
+    np.savez_compressed(OUT / "unary.npz", **res)
+
+
+def make_view(ref, storage, view):
+    """view: None | ('t', a0, a1) | ('t_reshape', a0, a1, shape)"""
+    p = ref.param(storage)
+    if view is None:
+        return p, p
+    v = ref.lib.nc_transpose(p, view[1], view[2])
+    if view[0] == "t_reshape":
+        nd, shp = abi.shape_arg(view[3])
+        v = ref.lib.nc_reshape(v, nd, shp)
+    ref.check()
+    return p, v
+
+
+BINARY_CASES = [
+    # name, a storage shape, a view, b storage shape, b view
+    ("bias4d", (4, 3, 5, 7), None, (1, 3, 1, 1), None),
+    ("row", (2, 3), None, (3,), None),
+    ("outer", (2, 1), None, (1, 3), None),
+    ("scalar_lhs", (), None, (3,), None),
+    ("scalar_rhs", (5, 4), None, (), None),
+    ("cfg2_small", (5, 6, 1, 8), None, (1, 1, 7, 8), None),
+    ("cfg2_batch_t", (6, 5, 1, 8), ("t", 0, 1), (1, 1, 7, 8), None),
+    ("cfg2_inner_strided", (5, 8, 6), ("t_reshape", 1, 2, (5, 6, 1, 8)), (1, 1, 7, 8), None),
+    ("same_flat", (17, 33), None, (17, 33), None),
+    ("same_a_t", (33, 17), ("t", 0, 1), (17, 33), None),
+    ("rank_mismatch", (3, 1, 5), None, (4, 1), None),
+    ("ragged", (3, 1, 37), None, (1, 11, 37), None),
+]
+
+
+def gen_binary(ref, rng):
+    res = {}
+    ops = [("add", ref.lib.nc_add), ("sub", ref.lib.nc_sub), ("mul", ref.lib.nc_mul), ("div", ref.lib.nc_div)]
+    for name, ash, aview, bsh, bview in BINARY_CASES:
+        A = rng.standard_normal(ash).astype(np.float32)
+        B = (0.5 + 1.5 * rng.random(bsh)).astype(np.float32)
+        res[f"{name}/a_storage"] = A
+        res[f"{name}/b_storage"] = B
+        for opname, fn in ops:
+            pa, va = make_view(ref, A, aview)
+            pb, vb = make_view(ref, B, bview)
+            out = fn(va, vb)
+            y = ref.read(out)
+            G = rng.standard_normal(y.shape).astype(np.float32)
+            ref.backward_with(out, G)
+            res[f"{name}/{opname}/out"] = y
+            res[f"{name}/{opname}/G"] = G
+            res[f"{name}/{opname}/ga"] = ref.grad(va)  # grad in the (view's) logical shape
+            res[f"{name}/{opname}/gb"] = ref.grad(vb)
+            ref.step_end()
+    np.savez_compressed(OUT / "binary.npz", **res)
+
+
+def gen_reduce(ref, rng):
+    res = {}
+    cases = {
+        "r2x3": rng.standard_normal((2, 3)).astype(np.float32),
+        "r4x5x6": rng.standard_normal((4, 5, 6)).astype(np.float32),
+        "r3x1000": (rng.standard_normal((3, 1000)) * 2).astype(np.float32),
+        "r5x13x9": rng.standard_normal((5, 13, 9)).astype(np.float32),
+    }
+    sp = rng.standard_normal((8, 9)).astype(np.float32)
+    sp[0, 4] = sp[0, 7] = 5.0                        # tie: first index wins
+    sp[1, 0] = np.nan                                # NaN first: sticky
+    sp[2, 3] = np.nan                                # NaN later: ignored
+    sp[3, :] = -np.inf                               # all -inf
+    sp[4, :] = 0.0; sp[4, 0] = -0.0                  # signed zero ties
+    sp[5, 2] = np.inf
+    sp[6, :] = np.nan
+    sp[7, 8] = 1e30
+    cases["special"] = sp
+    for cname, X in cases.items():
+        res[f"{cname}/x"] = X
+        axes = list(range(X.ndim)) + [abi.ALL_AXES]
+        for axis in axes:
+            for kname, fn in (("sum", ref.lib.nc_sum), ("mean", ref.lib.nc_mean), ("max", ref.lib.nc_max)):
+                if cname == "special" and kname != "max":
+                    continue
+                p = ref.param(X)
+                out = fn(p, axis, 0)
+                y = ref.read(out)
+                G = rng.standard_normal(y.shape).astype(np.float32)
+                ref.backward_with(out, G)
+                res[f"{cname}/{kname}/{axis}/y"] = y
+                res[f"{cname}/{kname}/{axis}/G"] = G
+                res[f"{cname}/{kname}/{axis}/gx"] = ref.grad(p)
+                ref.step_end()
+            t = ref.tensor(X)
+            res[f"{cname}/argmax/{axis}/y"] = ref.read(ref.lib.nc_argmax(t, axis), np.int32)
+            ref.step_end()
+    empty = ref.tensor(np.zeros((0, 3), np.float32))
+    res["empty/mean_all"] = ref.read(ref.lib.nc_mean(empty, abi.ALL_AXES, 0))
+    res["empty/mean_0"] = ref.read(ref.lib.nc_mean(empty, 0, 0))
+    res["empty/sum_0"] = ref.read(ref.lib.nc_sum(empty, 0, 0))
+    ref.step_end()
+    np.savez_compressed(OUT / "reduce.npz", **res)
+
+
+def gen_softmax(ref, rng):
+    res = {}
+    for rows, C in ((3, 1), (4, 7), (5, 64), (3, 100), (2, 1030), (6, 17)):
+        X = (rng.standard_normal((rows, C)) * 2).astype(np.float32)
+        if C >= 7:
+            X[0, 3] = -np.inf
+            X[1, 2] = X[1, 5] = X[1].max() + 1.0
+        key = f"{rows}x{C}"
+        res[f"{key}/x"] = X
+        for form, fn in (("softmax", ref.lib.nc_softmax), ("log_softmax", ref.lib.nc_log_softmax)):
+            p = ref.param(X)
+            out = fn(p)
+            y = ref.read(out)
+            G = rng.standard_normal(y.shape).astype(np.float32)
+            ref.backward_with(out, G)
+            res[f"{key}/{form}/y"] = y
+            res[f"{key}/{form}/G"] = G
+            res[f"{key}/{form}/gx"] = ref.grad(p)
+            ref.step_end()
+    np.savez_compressed(OUT / "softmax.npz", **res)
+
+
+def gen_layer_norm(ref, rng):
+    res = {}
+    for key, shape, k in (("6x10", (6, 10), 1), ("3x4x5", (3, 4, 5), 2), ("4x1024", (4, 1024), 1),
+                          ("2x3", (2, 3), 1)):
+        X = (rng.standard_normal(shape) * 2 + 0.5).astype(np.float32)
+        D = int(np.prod(shape[len(shape) - k:]))
+        W = (1 + 0.1 * rng.standard_normal(D)).astype(np.float32)
+        Bv = (0.1 * rng.standard_normal(D)).astype(np.float32)
+        res[f"{key}/x"] = X
+        res[f"{key}/w"] = W
+        res[f"{key}/b"] = Bv
+        res[f"{key}/k"] = np.array(k)
+        for variant in ("wb", "w", "none"):
+            px = ref.param(X)
+            pw = ref.param(W) if variant in ("wb", "w") else None
+            pb = ref.param(Bv) if variant == "wb" else None
+            out = ref.lib.nc_layer_norm(px, k, pw, pb, c_float(1e-5))
+            y = ref.read(out)
+            G = rng.standard_normal(y.shape).astype(np.float32)
+            ref.backward_with(out, G)
+            res[f"{key}/{variant}/y"] = y
+            res[f"{key}/{variant}/G"] = G
+            res[f"{key}/{variant}/gx"] = ref.grad(px)
+            if pw:
+                res[f"{key}/{variant}/gw"] = ref.grad(pw)
+            if pb:
+                res[f"{key}/{variant}/gb"] = ref.grad(pb)
+            ref.step_end()
+    np.savez_compressed(OUT / "layernorm.npz", **res)
+
+
+def gen_quant(ref, rng):
+    W = (rng.standard_normal((12, 70)) * 0.2).astype(np.float32)
+    idx = rng.choice(W.size, 8, replace=False)
+    W.flat[idx] *= 50
+    W[3, :] = 0.0                                             # zero row: scale 1
+    W[4, :9] = [127.0, 0.5, 1.5, 2.5, -0.5, -1.5, -2.5, 126.5, -126.5]  # exact ties, scale 1
+    W[4, 9:] = 0.25
+    W[5, 0] = np.nan                                          # NaN ignored by the absmax, quantizes to 0
+    W[6, 5] = np.inf                                          # inf absmax: scale inf, all zeros
+    W[7, :] = -3e-39                                          # denormal row
+    W[8, :] = np.linspace(-1, 1, 70, dtype=np.float32)
+    W[9, 0] = -5.0
+    res = {"w": W}
+    pw = ref.tensor(W)
+    sc = c_void_p()
+    q = ref.lib.nc_quantize_rows(pw, ctypes.byref(sc))
+    res["q"] = ref.read(q, np.int8)
+    res["scale"] = ref.read(sc.value)
+    qf = ref.lib.nc_to_dtype(q, abi.F32)
+    nd, shp = abi.shape_arg((W.shape[0], 1))
+    deq = ref.lib.nc_mul(qf, ref.lib.nc_reshape(sc.value, nd, shp))
+    res["deq"] = ref.read(deq)
+    ref.step_end()
+    np.savez_compressed(OUT / "quant.npz", **res)
+
+
+def gen_chain(ref, rng):
+    """The MNIST-CNN-shaped chain at a small batch: relu(x + bias).sum((2, 3)), with the reference
+    Python package's multi-dim reduction composition (one keepdim sum per dim, last dim first,
+    then a reshape: newch/tensor.py:701-717)."""
+    X = rng.uniform(-1, 1, (4, 16, 28, 28)).astype(np.float32)
+    Bv = rng.uniform(-0.1, 0.1, (1, 16, 1, 1)).astype(np.float32)
+    G = rng.standard_normal((4, 16)).astype(np.float32)
+    px, pb = ref.param(X), ref.param(Bv)
+    h = ref.lib.nc_relu(ref.lib.nc_add(px, pb))
+    s = ref.lib.nc_sum(ref.lib.nc_sum(h, 3, 1), 2, 1)
+    nd, shp = abi.shape_arg((4, 16))
+    y = ref.lib.nc_reshape(s, nd, shp)
+    out = ref.read(y)
+    ref.backward_with(y, G)
+    np.savez_compressed(OUT / "chain.npz", x=X, bias=Bv, G=G, y=out, gx=ref.grad(px), gbias=ref.grad(pb))
+    ref.step_end()
+
+
+def main():
+    lib = abi.load(REF_LIB)
+    lib.ncref_backend.restype = ctypes.c_char_p
+    backend = lib.ncref_backend().decode()
+    if backend != "avx2":
+        raise SystemExit(f"reference kernel tier is {backend!r}; fixtures must come from the avx2 tier")
+    rng = np.random.default_rng(20261201)
+    ref = Ref(lib)
+    gen_transcendentals(lib, rng)
+    gen_unary(ref, rng)
+    gen_binary(ref, rng)
+    gen_reduce(ref, rng)
+    gen_softmax(ref, rng)
+    gen_layer_norm(ref, rng)
+    gen_quant(ref, rng)
+    gen_chain(ref, rng)
+    (OUT / "PROVENANCE.txt").write_text(
+        "Written by tests/golden/gen_golden.py from oracle/_ref/libnc_ref.so, which oracle/Makefile builds\n"
+        "from the reference engine sources (engine/src/**/*.c) with gcc 11.4, -O2 -std=gnu11, x86-64\n"
+        f"baseline + AVX2/FMA target functions; kernel tier: {backend}; numpy seed 20261201.\n")
+    for f in sorted(OUT.glob("*.npz")):
+        print(f"{f.name}: {f.stat().st_size / 1024:.0f} KiB")
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,349 @@
+"""Pins the CPU oracle (oracle/oracle.c) before anything is checked against it.
+
+Three independent pins per function:
+  * the golden vectors in tests/golden/ (written by the compiled reference engine), bit for bit;
+  * the live reference library oracle/_ref/libnc_ref.so on fresh random inputs, when it is built;
+  * closed forms / invariants / the reference's own known answers (engine/tests/test_main.c,
+    tests/test_extras.py), chosen so a dropped term, wrong sign or wrong index fails.
+"""
+
+import math
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+from oracle import pyoracle as O
+
+GOLD = Path(__file__).resolve().parent / "golden"
+
+
+def load(name):
+    return np.load(GOLD / f"{name}.npz")
+
+
+def bits_equal(a, b):
+    a = np.asarray(a)
+    b = np.asarray(b)
+    assert a.shape == b.shape, (a.shape, b.shape)
+    if a.dtype.kind == "f":
+        nan = np.isnan(a) & np.isnan(b)
+        ok = (a.view(np.uint32) == b.view(np.uint32)) | nan
+        return bool(ok.all()), int((~ok).sum())
+    ok = a == b
+    return bool(ok.all()), int((~ok).sum())
+
+
+def assert_bits(a, b, what=""):
+    ok, nbad = bits_equal(a, b)
+    assert ok, f"{what}: {nbad} elements differ"
+
+
+# ------------------------------------------------------------------------------------------------
+# golden vectors
+# ------------------------------------------------------------------------------------------------
+def test_transcendentals_golden():
+    d = load("transcendentals")
+    for fn in ("exp", "sigmoid", "tanh", "erf"):
+        assert_bits(O.vmap(fn, d["x"]), d[fn], fn)
+    for n, want in zip(d["sum_n"], d["sum_out"]):
+        assert_bits(O.sum_f32(d["sum_x"][:n]), want, f"sum_f32 n={n}")
+
+
+UNARY = [("relu", "relu", 0.0), ("leaky_relu", "leaky_relu", 0.01), ("leaky_relu_02", "leaky_relu", 0.2),
+         ("relu6", "relu6", 0.0), ("hardsigmoid", "hardsigmoid", 0.0), ("hardswish", "hardswish", 0.0),
+         ("silu", "silu", 0.0), ("gelu", "gelu", 0.0), ("gelu_tanh", "gelu_tanh", 0.0),
+         ("sigmoid", "sigmoid", 0.0), ("tanh", "tanh", 0.0), ("exp", "exp", 0.0)]
+
+
+@pytest.mark.parametrize("name,kind,s", UNARY)
+def test_unary_golden(name, kind, s):
+    d = load("unary")
+    x, g = d["x"], d["g"]
+    y = O.unary_fwd(kind, x, s)
+    assert_bits(y, d[f"{name}_y"], f"{name} fwd")
+    gx = O.unary_bwd(kind, x, y, g, s=s)
+    assert_bits(gx, d[f"{name}_gx"], f"{name} bwd")
+
+
+def make_view(storage, view):
+    if view is None:
+        return storage
+    v = np.swapaxes(storage, view[1], view[2])
+    if view[0] == "t_reshape":
+        v = v.reshape(view[3])
+        assert not v.flags.c_contiguous and np.shares_memory(v, storage)
+    return v
+
+
+BINARY_CASES = [
+    ("bias4d", None, None), ("row", None, None), ("outer", None, None), ("scalar_lhs", None, None),
+    ("scalar_rhs", None, None), ("cfg2_small", None, None), ("cfg2_batch_t", ("t", 0, 1), None),
+    ("cfg2_inner_strided", ("t_reshape", 1, 2, (5, 6, 1, 8)), None), ("same_flat", None, None),
+    ("same_a_t", ("t", 0, 1), None), ("rank_mismatch", None, None), ("ragged", None, None)]
+
+
+@pytest.mark.parametrize("case,aview,bview", BINARY_CASES)
+@pytest.mark.parametrize("op", ["add", "sub", "mul", "div"])
+def test_binary_golden(case, aview, bview, op):
+    d = load("binary")
+    a = make_view(d[f"{case}/a_storage"], aview)
+    b = make_view(d[f"{case}/b_storage"], bview)
+    out = O.binary_fwd(op, a, b)
+    assert_bits(out, d[f"{case}/{op}/out"], f"{case} {op} fwd")
+    ga, gb = O.binary_bwd(op, a, b, d[f"{case}/{op}/G"])
+    assert_bits(ga, d[f"{case}/{op}/ga"], f"{case} {op} grad a")
+    assert_bits(gb, d[f"{case}/{op}/gb"], f"{case} {op} grad b")
+
+
+def _axes(x):
+    return list(range(x.ndim)) + [-128]
+
+
+@pytest.mark.parametrize("case", ["r2x3", "r4x5x6", "r3x1000", "r5x13x9", "special"])
+def test_reduce_golden(case):
+    d = load("reduce")
+    x = d[f"{case}/x"]
+    for axis in _axes(x):
+        for kind in ("sum", "mean", "max"):
+            key = f"{case}/{kind}/{axis}"
+            if f"{key}/y" not in d:
+                continue
+            y, arg = O.reduce_fwd(kind, x, axis)
+            want = d[f"{key}/y"]
+            assert_bits(y.reshape(want.shape), want, f"{key} fwd")
+            gx = O.reduce_bwd(kind, x.shape, axis, d[f"{key}/G"], arg)
+            assert_bits(gx, d[f"{key}/gx"], f"{key} bwd")
+        want = d[f"{case}/argmax/{axis}/y"]
+        got, _ = O.reduce_fwd("argmax", x, axis)
+        assert_bits(got.reshape(want.shape), want, f"{case} argmax {axis}")
+
+
+def test_reduce_empty_golden():
+    d = load("reduce")
+    y, _ = O.reduce_fwd("mean", np.zeros((0, 3), np.float32), -128)
+    assert np.isnan(y[0]) and np.isnan(d["empty/mean_all"])
+    y, _ = O.reduce_fwd("mean", np.zeros((0, 3), np.float32), 0)
+    assert_bits(y, d["empty/mean_0"])
+    y, _ = O.reduce_fwd("sum", np.zeros((0, 3), np.float32), 0)
+    assert_bits(y, d["empty/sum_0"])
+
+
+@pytest.mark.parametrize("key", ["3x1", "4x7", "5x64", "3x100", "2x1030", "6x17"])
+def test_softmax_golden(key):
+    d = load("softmax")
+    x = d[f"{key}/x"]
+    for form in ("softmax", "log_softmax"):
+        lf = form == "log_softmax"
+        y = O.softmax_fwd(x, lf)
+        assert_bits(y, d[f"{key}/{form}/y"], f"{key} {form}")
+        gx = O.softmax_bwd(y, d[f"{key}/{form}/G"], lf)
+        assert_bits(gx, d[f"{key}/{form}/gx"], f"{key} {form} bwd")
+
+
+@pytest.mark.parametrize("key", ["6x10", "3x4x5", "4x1024", "2x3"])
+def test_layer_norm_golden(key):
+    d = load("layernorm")
+    x, w, b, k = d[f"{key}/x"], d[f"{key}/w"], d[f"{key}/b"], int(d[f"{key}/k"])
+    D = int(np.prod(x.shape[x.ndim - k:]))
+    for variant in ("wb", "w", "none"):
+        ww = w if variant in ("wb", "w") else None
+        bb = b if variant == "wb" else None
+        y, stats = O.layer_norm_fwd(x, D, ww, bb, 1e-5)
+        assert_bits(y, d[f"{key}/{variant}/y"], f"{key} {variant} fwd")
+        gx, gw, gb = O.layer_norm_bwd(x, D, stats, d[f"{key}/{variant}/G"], ww, ww is not None, bb is not None)
+        assert_bits(gx, d[f"{key}/{variant}/gx"], f"{key} {variant} gx")
+        if ww is not None:
+            assert_bits(gw, d[f"{key}/{variant}/gw"], f"{key} {variant} gw")
+        if bb is not None:
+            assert_bits(gb, d[f"{key}/{variant}/gb"], f"{key} {variant} gb")
+
+
+def test_quant_golden():
+    d = load("quant")
+    q, s = O.quantize_rows(d["w"])
+    assert_bits(q, d["q"], "q")
+    assert_bits(s, d["scale"], "scale")
+    assert_bits(O.dequantize_rows(q, s), d["deq"], "dequant")
+
+
+def test_chain_golden():
+    """relu(x + bias).sum((2, 3)): the oracle composes add -> relu -> two keepdim sums."""
+    d = load("chain")
+    x, bias, G = d["x"], d["bias"], d["G"]
+    h0 = O.binary_fwd("add", x, bias)
+    h = O.unary_fwd("relu", h0)
+    s3, _ = O.reduce_fwd("sum", h, 3)
+    s3 = s3.reshape(4, 16, 28, 1)
+    s2, _ = O.reduce_fwd("sum", s3, 2)
+    assert_bits(s2.reshape(4, 16), d["y"], "chain fwd")
+    g3 = O.reduce_bwd("sum", s3.shape, 2, G.reshape(4, 16, 1, 1))
+    gh = O.reduce_bwd("sum", h.shape, 3, g3)
+    gh0 = O.unary_bwd("relu", h0, h, gh)
+    gx, gb = O.binary_bwd("add", x, bias, gh0)
+    assert_bits(gx, d["gx"], "chain grad x")
+    assert_bits(gb, d["gbias"], "chain grad bias")
+
+
+# ------------------------------------------------------------------------------------------------
+# the live reference (only where oracle/_ref was built: this container, or a box it travelled to)
+# ------------------------------------------------------------------------------------------------
+ref_only = pytest.mark.skipif(not O.REF_LIB.exists(), reason="oracle/_ref/libnc_ref.so not built")
+
+
+@ref_only
+def test_transcendentals_vs_live_reference():
+    import ctypes
+    L = ctypes.CDLL(str(O.REF_LIB))
+    rng = np.random.default_rng(7)
+    x = np.concatenate([rng.standard_normal(200_000).astype(np.float32) * 20,
+                        np.frombuffer(rng.integers(0, 2 ** 32, 200_000, dtype=np.uint32).tobytes(), np.float32)])
+    for fn in ("exp", "sigmoid", "tanh", "erf"):
+        y = np.empty_like(x)
+        getattr(L, f"ncref_{fn}_f32")(ctypes.c_int64(x.size), x.ctypes.data_as(ctypes.c_void_p),
+                                      y.ctypes.data_as(ctypes.c_void_p))
+        assert_bits(O.vmap(fn, x), y, fn)
+
+
+@ref_only
+@pytest.mark.parametrize("name,kind,s", UNARY)
+def test_unary_vs_live_reference(name, kind, s):
+    from tests.ncdrive import Engine
+    rng = np.random.default_rng(abs(hash(name)) % 2 ** 31)
+    x = (rng.standard_normal(4099) * 4).astype(np.float32)
+    g = rng.standard_normal(4099).astype(np.float32)
+    with Engine(O.REF_LIB) as ref:
+        y_ref, gx_ref = ref.unary(name, x, g, s)
+    y = O.unary_fwd(kind, x, s)
+    assert_bits(y, y_ref, name)
+    assert_bits(O.unary_bwd(kind, x, y, g, s=s), gx_ref, name + " bwd")
+
+
+# ------------------------------------------------------------------------------------------------
+# closed forms, invariants and the reference's own known answers
+# ------------------------------------------------------------------------------------------------
+def test_known_answers_from_reference_tests():
+    # engine/tests/test_main.c:335-341
+    t = np.array([-1.0, 0.5, 4.0], np.float32)
+    assert abs(O.unary_fwd("hardswish", t)[1] - 0.5 * 3.5 / 6.0) <= 1e-6
+    assert O.unary_fwd("relu6", t)[2] == 4.0
+    assert abs(O.unary_fwd("gelu", t)[0] - (-0.15865525)) <= 1e-6
+    assert abs(O.unary_fwd("gelu_tanh", t)[0] - (-0.15880801)) <= 1e-6
+    assert abs(O.unary_fwd("silu", t)[1] - 0.5 / (1.0 + math.exp(-0.5))) <= 1e-6
+    # :118-131 reductions
+    a = np.array([[1, 5, 3], [4, 2, 6]], np.float32)
+    assert O.reduce_fwd("sum", a, 0)[0][1] == 7
+    assert O.reduce_fwd("sum", a, 1)[0][1] == 12
+    assert abs(O.reduce_fwd("mean", a, -128)[0][0] - 3.5) <= 1e-6
+    assert O.reduce_fwd("max", a, 1)[0][0] == 5
+    assert O.reduce_fwd("argmax", a, 1)[0][1] == 2
+    # :82-95 broadcasting
+    A = np.arange(1, 7, dtype=np.float32).reshape(2, 3)
+    B = np.array([10, 20, 30], np.float32)
+    assert O.binary_fwd("add", A, B)[1, 2] == 36
+    assert O.binary_fwd("mul", np.array([[2], [3]], np.float32), B.reshape(1, 3))[1, 1] == 60
+    assert O.binary_fwd("sub", np.array(1.0, np.float32), B)[2] == -29
+    # :736-745 layer norm: zero mean, unit variance
+    y, _ = O.layer_norm_fwd(np.array([1, 2, 3, 6], np.float32), 4, eps=0.0)
+    assert abs(y.astype(np.float64).mean()) <= 1e-6 and abs(y.astype(np.float64).var() - 1) <= 1e-5
+    # :747-756 softmax of a -inf entry is exactly 0
+    p = O.softmax_fwd(np.array([[0.5, -np.inf, -2.0, -np.inf]], np.float32))
+    assert p[0, 1] == 0 and p[0, 3] == 0 and abs(p[0, 0] + p[0, 2] - 1) <= 1e-6
+
+
+def test_transcendental_accuracy_vs_libm():
+    """kernel parity bounds of engine/tests/test_main.c:818-869 against libm (math module)."""
+    x = np.linspace(-100, 100, 203, dtype=np.float32)
+    x[:5] = [0.0, 1e-6, -0.2, 0.249, 0.251]
+    e, s, t = O.vmap("exp", x), O.vmap("sigmoid", x), O.vmap("tanh", x)
+    for i, v in enumerate(x.astype(np.float64)):
+        if -87 <= v <= 88:
+            assert abs(e[i] - math.exp(v)) <= 1e-6 * math.exp(v)
+            sv = 1 / (1 + math.exp(-v))
+            assert abs(s[i] - sv) <= 1e-6 * sv
+        tv = math.tanh(v)
+        assert abs(t[i] - tv) <= 1e-5 * max(abs(tv), 1e-30)
+    xe = np.concatenate([x, np.linspace(-4, 3.8, 40, dtype=np.float32)])
+    er = O.vmap("erf", xe)
+    assert max(abs(er[i] - math.erf(float(v))) for i, v in enumerate(xe)) < 5e-7
+    assert abs(O.vmap("tanh", np.array([1e-6], np.float32))[0] - 1e-6) <= 1e-12
+    sp = O.vmap("exp", np.array([-np.inf, np.inf, np.nan, -95.0, 100.0], np.float32))
+    assert sp[0] == 0 and sp[1] == np.inf and np.isnan(sp[2]) and sp[3] == 0 and sp[4] == np.inf
+
+
+def test_sum_order_is_the_avx2_tree():
+    """A wrong lane pairing changes the rounding: pick values where only the exact tree gives the
+    stored golden answer, and check against an fp64 sum for the magnitude."""
+    x = np.array([1e8, 1, -1e8, 1, 3, 5, 7, 9, 1e8, 2, -1e8, 4, 6, 8, 10, 12, 0.5], np.float32)
+    s = O.sum_f32(x)
+    a0 = x[0:8].astype(np.float32)
+    a1 = x[8:16].astype(np.float32)
+    v = a0 + a1
+    want = np.float32(np.float32(np.float32(v[0] + v[4]) + np.float32(v[2] + v[6])) +
+                      np.float32(np.float32(v[1] + v[5]) + np.float32(v[3] + v[7])))
+    want = np.float32(want + x[16])
+    assert s == want
+
+
+def test_binary_bwd_against_fp64_brute_force():
+    rng = np.random.default_rng(3)
+    a = rng.standard_normal((4, 1, 6)).astype(np.float32)
+    b = (0.5 + rng.random((5, 1))).astype(np.float32)
+    g = rng.standard_normal((4, 5, 6)).astype(np.float32)
+    A, B, G = (v.astype(np.float64) for v in (a, b, g))
+    for op, da, db in (("add", G, G), ("sub", G, -G), ("mul", G * B, G * A), ("div", G / B, -G * A / (B * B))):
+        ga, gb = O.binary_bwd(op, a, b, g)
+        want_a = da.sum(axis=1, keepdims=True)
+        want_b = db.sum(axis=(0, 2)).reshape(5, 1)
+        np.testing.assert_allclose(ga, want_a, rtol=1e-5, atol=1e-5)
+        np.testing.assert_allclose(gb, want_b, rtol=1e-5, atol=1e-5)
+
+
+def test_softmax_and_layernorm_against_fp64():
+    rng = np.random.default_rng(5)
+    x = (rng.standard_normal((7, 300)) * 3).astype(np.float32)
+    X = x.astype(np.float64)
+    p = np.exp(X - X.max(1, keepdims=True))
+    p /= p.sum(1, keepdims=True)
+    np.testing.assert_allclose(O.softmax_fwd(x), p, rtol=2e-6, atol=1e-9)
+    np.testing.assert_allclose(O.softmax_fwd(x, True), np.log(p), rtol=1e-5, atol=1e-5)
+    g = rng.standard_normal(x.shape)
+    gx = O.softmax_bwd(O.softmax_fwd(x), g)
+    want = p * (g - (g * p).sum(1, keepdims=True))
+    np.testing.assert_allclose(gx, want, rtol=1e-4, atol=1e-6)
+    w = (1 + 0.1 * rng.standard_normal(300)).astype(np.float32)
+    b = (0.1 * rng.standard_normal(300)).astype(np.float32)
+    y, stats = O.layer_norm_fwd(x, 300, w, b)
+    mu = X.mean(1, keepdims=True)
+    xh = (X - mu) / np.sqrt(X.var(1, keepdims=True) + 1e-5)
+    np.testing.assert_allclose(y, xh * w + b, rtol=1e-5, atol=1e-5)
+    gx, gw, gb = O.layer_norm_bwd(x, 300, stats, g.astype(np.float32), w, True, True)
+    gh = g * w
+    want = (gh - gh.mean(1, keepdims=True) - xh * (gh * xh).mean(1, keepdims=True)) / np.sqrt(
+        X.var(1, keepdims=True) + 1e-5)
+    np.testing.assert_allclose(gx, want, rtol=1e-4, atol=1e-5)
+    np.testing.assert_allclose(gw, (g * xh).sum(0), rtol=1e-4, atol=1e-4)
+    np.testing.assert_allclose(gb, g.sum(0), rtol=1e-4, atol=1e-4)
+
+
+def test_quantize_closed_form():
+    rng = np.random.default_rng(9)
+    w = (rng.standard_normal((33, 65)) * 0.02).astype(np.float32)
+    w[0, 0] = 1.0
+    q, s = O.quantize_rows(w)
+    amax = np.abs(w).max(1)
+    s_want = (amax / np.float32(127)).astype(np.float32)
+    assert_bits(s, s_want)
+    inv = (np.float32(1) / s_want).astype(np.float32)
+    q_want = np.clip(np.rint((w * inv[:, None]).astype(np.float32)), -127, 127).astype(np.int8)
+    assert_bits(q, q_want)
+    assert q.min() >= -127
+    assert_bits(O.dequantize_rows(q, s), (q.astype(np.float32) * s[:, None]).astype(np.float32))
+
+
+def test_argmax_first_index_and_nan_rule():
+    x = np.array([[1, 3, 3, 2], [np.nan, 5, 6, 7], [1, np.nan, 9, 9], [-0.0, 0.0, -1, -2]], np.float32)
+    got, _ = O.reduce_fwd("argmax", x, 1)
+    assert list(got) == [1, 0, 2, 0]
+    mx, _ = O.reduce_fwd("max", x, 1)
+    assert mx[0] == 3 and np.isnan(mx[1]) and mx[2] == 9 and np.signbit(mx[3])
