@@ -1,0 +1,185 @@
+// Elementwise ops: broadcasting binary arithmetic and unary math / activations.
+// Reference: engine/src/ops/ops_elementwise.c (binary :60-204, unary :210-411).
+// Shape inference and error messages follow the reference; the arithmetic runs in the nc_hip_*
+// kernels (include/nc_hip.h) on the context's stream.
+#include <stdio.h>
+
+#include "engine.hpp"
+
+namespace nce {
+
+// ---- binary ----------------------------------------------------------------------------------------
+static nc_status binary_infer(nc_node *n, nc_dtype *dt, int *nd, int64_t *shape) {
+    nc_tensor *a = n->in[0], *b = n->in[1];
+    if (!expect_f32(n, 0) || !expect_f32(n, 1)) return NC_ERR_DTYPE;
+    const int r = a->ndim > b->ndim ? a->ndim : b->ndim;
+    for (int i = 0; i < r; i++) {
+        const int ia = i - (r - a->ndim), ib = i - (r - b->ndim);
+        const int64_t da = ia < 0 ? 1 : a->shape[ia], db = ib < 0 ? 1 : b->shape[ib];
+        if (da != db && da != 1 && db != 1) {
+            char sa[96], sb[96];
+            error(a->ctx, NC_ERR_SHAPE, "%s: shapes %s and %s are not broadcastable", n->op->name,
+                  shape_str(a->ndim, a->shape, sa, sizeof sa), shape_str(b->ndim, b->shape, sb, sizeof sb));
+            return NC_ERR_SHAPE;
+        }
+        shape[i] = da == 1 ? db : da;
+    }
+    *dt = NC_F32;
+    *nd = r;
+    return NC_OK;
+}
+
+static nc_status binary_fwd(nc_node *n) {
+    nc_tensor *a = n->in[0], *b = n->in[1], *o = n->out;
+    nc_ctx *ctx = o->ctx;
+    int64_t sa[NC_MAX_DIMS], sb[NC_MAX_DIMS];
+    bcast_strides(a, o->ndim, o->shape, sa);
+    bcast_strides(b, o->ndim, o->shape, sb);
+    float *pa = fptr(a), *pb = fptr(b), *po = fptr(o);
+    if (!pa || !pb || !po) return NC_ERR_STATE;
+    if (!hip_layer_ok(ctx, nc_hip_binary_fwd(n->op->kind, o->ndim, o->shape, pa, sa, pb, sb, po, o->stride, stream(ctx)),
+                      n->op->name))
+        return NC_ERR_STATE;
+    wrote_dev(o);
+    return NC_OK;
+}
+
+static void binary_bwd(nc_node *n) {
+    nc_tensor *a = n->in[0], *b = n->in[1], *o = n->out;
+    nc_ctx *ctx = o->ctx;
+    const int nd = o->ndim;
+    int64_t sa[NC_MAX_DIMS], sb[NC_MAX_DIMS];
+    bcast_strides(a, nd, o->shape, sa);
+    bcast_strides(b, nd, o->shape, sb);
+    float *g = fptr(o->grad), *pa = fptr(a), *pb = fptr(b);
+    if (!g || !pa || !pb) return;
+    for (int which = 0; which < 2; which++) {
+        nc_tensor *x = n->in[which];
+        if (!needs_grad(x)) continue;
+        if (!grad_buf(x)) return;
+        int64_t sgx[NC_MAX_DIMS];
+        bcast_strides_shape(x->ndim, x->shape, nd, o->shape, sgx);
+        const size_t ws_bytes = nc_hip_binary_bwd_workspace(nd, o->shape, sgx);
+        char *ws = ws_bytes ? arena_alloc(ctx, ws_bytes) : nullptr;
+        if (ws_bytes && !ws) return;
+        const int acc = grad_acc(x);
+        float *gx = fptr(x->grad);
+        if (!gx) return;
+        if (!hip_layer_ok(ctx,
+                          nc_hip_binary_bwd(n->op->kind, which, nd, o->shape, g, o->stride, pa, sa, pb, sb, gx, sgx,
+                                            acc, ws, ws_bytes, stream(ctx)),
+                          n->op->name))
+            return;
+        wrote_dev(x->grad);
+    }
+}
+
+const OpDef op_add = {"add", OPF_ELEMENTWISE, NC_HIP_BIN_ADD, binary_infer, nullptr, binary_fwd, binary_bwd};
+const OpDef op_sub = {"sub", OPF_ELEMENTWISE, NC_HIP_BIN_SUB, binary_infer, nullptr, binary_fwd, binary_bwd};
+const OpDef op_mul = {"mul", OPF_ELEMENTWISE, NC_HIP_BIN_MUL, binary_infer, nullptr, binary_fwd, binary_bwd};
+const OpDef op_div = {"div", OPF_ELEMENTWISE, NC_HIP_BIN_DIV, binary_infer, nullptr, binary_fwd, binary_bwd};
+
+static nc_tensor *binary(const OpDef *op, nc_tensor *a, nc_tensor *b) {
+    nc_tensor *in[2] = {a, b};
+    return apply(op, in, 2, nullptr);
+}
+
+// ---- unary -----------------------------------------------------------------------------------------
+static nc_status unary_infer(nc_node *n, nc_dtype *dt, int *nd, int64_t *shape) {
+    if (!expect_f32(n, 0)) return NC_ERR_DTYPE;
+    *dt = NC_F32;
+    *nd = n->in[0]->ndim;
+    memcpy(shape, n->in[0]->shape, sizeof(int64_t) * (size_t)*nd);
+    return NC_OK;
+}
+
+static nc_status unary_fwd(nc_node *n) {
+    nc_ctx *ctx = n->out->ctx;
+    float *x = contig_f32(n->in[0]), *y = fptr(n->out);
+    if (!x || !y) return NC_ERR_STATE;
+    if (!hip_layer_ok(ctx, nc_hip_unary_fwd(n->op->kind, n->p.f[0], x, y, nc_numel(n->out), stream(ctx)), n->op->name))
+        return NC_ERR_STATE;
+    wrote_dev(n->out);
+    return NC_OK;
+}
+
+static bool reads_y(int kind) {
+    return kind == NC_HIP_UN_SIGMOID || kind == NC_HIP_UN_TANH || kind == NC_HIP_UN_EXP || kind == NC_HIP_UN_SQRT;
+}
+static bool reads_x(int kind) {
+    return !reads_y(kind) && kind != NC_HIP_UN_NEG && kind != NC_HIP_UN_SCALE && kind != NC_HIP_UN_ADD_SCALAR;
+}
+
+static void unary_bwd(nc_node *n) {
+    nc_tensor *in = n->in[0];
+    nc_ctx *ctx = in->ctx;
+    const int kind = n->op->kind;
+    if (!grad_buf(in)) return;
+    float *x = reads_x(kind) ? contig_f32(in) : nullptr;
+    float *y = reads_y(kind) ? fptr(n->out) : nullptr;
+    float *g = fptr(n->out->grad);
+    if ((reads_x(kind) && !x) || (reads_y(kind) && !y) || !g) return;
+    const int acc = grad_acc(in);
+    float *gi = fptr(in->grad);
+    if (!gi) return;
+    if (!hip_layer_ok(ctx, nc_hip_unary_bwd(kind, n->p.f[0], x, y, g, gi, nc_numel(in), acc, stream(ctx)),
+                      n->op->name))
+        return;
+    wrote_dev(in->grad);
+}
+
+#define NC_UNARY_DEF(nm, KIND) \
+    const OpDef op_##nm = {#nm, OPF_ELEMENTWISE, KIND, unary_infer, nullptr, unary_fwd, unary_bwd};
+NC_UNARY_DEF(neg, NC_HIP_UN_NEG)
+NC_UNARY_DEF(exp, NC_HIP_UN_EXP)
+NC_UNARY_DEF(log, NC_HIP_UN_LOG)
+NC_UNARY_DEF(sqrt, NC_HIP_UN_SQRT)
+NC_UNARY_DEF(relu, NC_HIP_UN_RELU)
+NC_UNARY_DEF(sigmoid, NC_HIP_UN_SIGMOID)
+NC_UNARY_DEF(tanh, NC_HIP_UN_TANH)
+NC_UNARY_DEF(scale, NC_HIP_UN_SCALE)
+NC_UNARY_DEF(add_scalar, NC_HIP_UN_ADD_SCALAR)
+NC_UNARY_DEF(pow_scalar, NC_HIP_UN_POW)
+NC_UNARY_DEF(leaky_relu, NC_HIP_UN_LEAKY_RELU)
+NC_UNARY_DEF(relu6, NC_HIP_UN_RELU6)
+NC_UNARY_DEF(hardsigmoid, NC_HIP_UN_HARDSIGMOID)
+NC_UNARY_DEF(hardswish, NC_HIP_UN_HARDSWISH)
+NC_UNARY_DEF(silu, NC_HIP_UN_SILU)
+NC_UNARY_DEF(gelu, NC_HIP_UN_GELU)
+NC_UNARY_DEF(gelu_tanh, NC_HIP_UN_GELU_TANH)
+#undef NC_UNARY_DEF
+
+static nc_tensor *unary(const OpDef *op, nc_tensor *x, float s) {
+    Params p{};
+    p.f[0] = s;
+    return apply(op, &x, 1, &p);
+}
+
+}  // namespace nce
+
+using namespace nce;
+
+extern "C" {
+nc_tensor *nc_add(nc_tensor *a, nc_tensor *b) { return binary(&op_add, a, b); }
+nc_tensor *nc_sub(nc_tensor *a, nc_tensor *b) { return binary(&op_sub, a, b); }
+nc_tensor *nc_mul(nc_tensor *a, nc_tensor *b) { return binary(&op_mul, a, b); }
+nc_tensor *nc_div(nc_tensor *a, nc_tensor *b) { return binary(&op_div, a, b); }
+nc_tensor *nc_neg(nc_tensor *x) { return unary(&op_neg, x, 0); }
+nc_tensor *nc_exp(nc_tensor *x) { return unary(&op_exp, x, 0); }
+nc_tensor *nc_log(nc_tensor *x) { return unary(&op_log, x, 0); }
+nc_tensor *nc_sqrt(nc_tensor *x) { return unary(&op_sqrt, x, 0); }
+nc_tensor *nc_relu(nc_tensor *x) { return unary(&op_relu, x, 0); }
+nc_tensor *nc_sigmoid(nc_tensor *x) { return unary(&op_sigmoid, x, 0); }
+nc_tensor *nc_tanh(nc_tensor *x) { return unary(&op_tanh, x, 0); }
+nc_tensor *nc_scale(nc_tensor *x, float s) { return unary(&op_scale, x, s); }
+nc_tensor *nc_add_scalar(nc_tensor *x, float s) { return unary(&op_add_scalar, x, s); }
+nc_tensor *nc_pow_scalar(nc_tensor *x, float p) { return unary(&op_pow_scalar, x, p); }
+nc_tensor *nc_leaky_relu(nc_tensor *x, float negative_slope) { return unary(&op_leaky_relu, x, negative_slope); }
+nc_tensor *nc_relu6(nc_tensor *x) { return unary(&op_relu6, x, 0); }
+nc_tensor *nc_hardsigmoid(nc_tensor *x) { return unary(&op_hardsigmoid, x, 0); }
+nc_tensor *nc_hardswish(nc_tensor *x) { return unary(&op_hardswish, x, 0); }
+nc_tensor *nc_silu(nc_tensor *x) { return unary(&op_silu, x, 0); }
+nc_tensor *nc_gelu(nc_tensor *x, int approximate_tanh) {
+    return unary(approximate_tanh ? &op_gelu_tanh : &op_gelu, x, 0);
+}
+}

@@ -1,0 +1,94 @@
+// The rest of the reference ABI (engine/include/nc.h) outside this build's hot path: GEMM-based ops,
+// convolution, losses, masking, serialization, modules and optimizers.  Every symbol exists, so the
+// reference's ctypes bindings resolve all their names at import (newch/_lib.py:174-177), and every
+// call fails cleanly the reference way -- a sticky NC_ERR_STATE in the context and a NULL / error
+// result -- instead of computing anything on the host.
+#include "engine.hpp"
+
+using namespace nce;
+
+static nc_tensor *absent(nc_tensor *any, const char *name) {
+    if (any) error(any->ctx, NC_ERR_STATE, "%s: not in this build (the MI355X engine runs the elementwise, "
+                                          "reduction, normalization and int8 hot path)", name);
+    return nullptr;
+}
+
+static void absent_ctx(nc_ctx *ctx, const char *name) {
+    if (ctx) error(ctx, NC_ERR_STATE, "%s: not in this build", name);
+}
+
+extern "C" {
+
+nc_tensor *nc_matmul(nc_tensor *a, nc_tensor *b) { return absent(a ? a : b, "matmul"); }
+nc_tensor *nc_linear_fn(nc_tensor *x, nc_tensor *weight, nc_tensor *) { return absent(x ? x : weight, "linear"); }
+nc_tensor *nc_index_select(nc_tensor *x, nc_tensor *) { return absent(x, "index_select"); }
+nc_tensor *nc_conv2d(nc_tensor *x, nc_tensor *, nc_tensor *, int, int, int, int) { return absent(x, "conv2d"); }
+nc_tensor *nc_conv2d_ex(nc_tensor *x, nc_tensor *, nc_tensor *, int, int, int, int, int, int, int) {
+    return absent(x, "conv2d");
+}
+nc_tensor *nc_max_pool2d(nc_tensor *x, int, int, int, int, int, int) { return absent(x, "max_pool2d"); }
+nc_tensor *nc_avg_pool2d(nc_tensor *x, int, int, int, int, int, int) { return absent(x, "avg_pool2d"); }
+nc_tensor *nc_dropout(nc_tensor *x, float) { return absent(x, "dropout"); }
+nc_tensor *nc_batch_norm(nc_tensor *x, nc_tensor *, nc_tensor *, nc_tensor *, nc_tensor *, int, float, float) {
+    return absent(x, "batch_norm");
+}
+nc_tensor *nc_masked_fill(nc_tensor *x, nc_tensor *, float) { return absent(x, "masked_fill"); }
+nc_tensor *nc_cross_entropy(nc_tensor *logits, nc_tensor *) { return absent(logits, "cross_entropy"); }
+nc_tensor *nc_mse_loss(nc_tensor *pred, nc_tensor *) { return absent(pred, "mse_loss"); }
+nc_tensor *nc_nll_loss(nc_tensor *logp, nc_tensor *, int) { return absent(logp, "nll_loss"); }
+nc_tensor *nc_compare(nc_tensor *a, nc_tensor *b, nc_cmp) { return absent(a ? a : b, "compare"); }
+nc_tensor *nc_cat(int n, nc_tensor *const *xs, int) { return absent(n > 0 && xs ? xs[0] : nullptr, "cat"); }
+nc_tensor *nc_linear_int8(nc_tensor *x, nc_tensor *wq, nc_tensor *, nc_tensor *) {
+    return absent(x ? x : wq, "linear_int8");
+}
+
+nc_status nc_save(nc_ctx *ctx, const char *, int, const char *const *, nc_tensor *const *) {
+    absent_ctx(ctx, "nc_save");
+    return NC_ERR_STATE;
+}
+nc_status nc_load(nc_ctx *ctx, const char *, int, const char *const *, nc_tensor *const *) {
+    absent_ctx(ctx, "nc_load");
+    return NC_ERR_STATE;
+}
+
+nc_module *nc_linear(nc_ctx *ctx, int64_t, int64_t, int) {
+    absent_ctx(ctx, "nc_linear");
+    return nullptr;
+}
+nc_module *nc_act(nc_ctx *ctx, nc_activation) {
+    absent_ctx(ctx, "nc_act");
+    return nullptr;
+}
+nc_module *nc_sequential(nc_ctx *ctx, int, nc_module **) {
+    absent_ctx(ctx, "nc_sequential");
+    return nullptr;
+}
+nc_tensor *nc_forward(nc_module *, nc_tensor *x) { return absent(x, "nc_forward"); }
+int nc_parameters(nc_module *, nc_tensor **, int) { return 0; }
+const char *nc_module_name(const nc_module *) { return ""; }
+void nc_set_training(nc_module *, int) {}
+
+static nc_optim *no_optim(nc_ctx *ctx, const char *name) {
+    absent_ctx(ctx, name);
+    return nullptr;
+}
+nc_optim *nc_sgd(nc_ctx *ctx, nc_tensor **, int, nc_optim_opts) { return no_optim(ctx, "nc_sgd"); }
+nc_optim *nc_adam(nc_ctx *ctx, nc_tensor **, int, nc_optim_opts) { return no_optim(ctx, "nc_adam"); }
+nc_optim *nc_adamw(nc_ctx *ctx, nc_tensor **, int, nc_optim_opts) { return no_optim(ctx, "nc_adamw"); }
+nc_optim *nc_rmsprop(nc_ctx *ctx, nc_tensor **, int, nc_optim_opts, int) { return no_optim(ctx, "nc_rmsprop"); }
+void nc_optim_zero_grad(nc_optim *) {}
+void nc_optim_clear_grad(nc_optim *) {}
+void nc_optim_step(nc_optim *) {}
+void nc_optim_free(nc_optim *) {}
+void nc_optim_set_lr(nc_optim *, float) {}
+float *nc_optim_state(nc_optim *, int, int) { return nullptr; }
+int64_t nc_optim_get_step(const nc_optim *) { return 0; }
+void nc_optim_set_step(nc_optim *, int64_t) {}
+void nc_optim_set_opts(nc_optim *, nc_optim_opts) {}
+void nc_optim_set_accumulation(nc_optim *, int) {}
+float nc_clip_grad_norm(nc_tensor **params, int n, float) {
+    absent(n > 0 && params ? params[0] : nullptr, "nc_clip_grad_norm");
+    return 0.0f;
+}
+
+}  // extern "C"

@@ -1,0 +1,725 @@
+// Broadcast binary ops and their sum-to-shape gradients, strided copies, fills, conversions.
+//
+// Reference: ops_elementwise.c:19-54 (row functions), :108-186 (binary_fwd / binary_bwd),
+// tensor.c:313-373 (nc__iterate, nc__copy_strided), ops_shape.c:474-504 (to_dtype).
+//
+// The reference walks every broadcast with a serial odometer, one indirect call per innermost row.
+// Here the host coalesces dims (adjacent dims that are contiguous for every operand merge, size-1
+// dims vanish) and each lane computes its operand offsets with multiply-high divisions; when the
+// innermost output dim is unit-stride and a multiple of 4 long, a lane produces 4 outputs with one
+// 128-bit store and loads every operand as a 128-bit vector (unit stride), a splat (stride 0) or a
+// 4-element gather (any other stride).
+//
+// Gradients that are not reduced (an operand with the output's shape) are computed with the
+// reference's fp32 expressions and are bit-identical to it.  Reduced gradients (sum-to-shape) are
+// accumulated in fp64 over a fixed partition: partial sums per (kept index, chunk) then a fixed-order
+// combine, so the result does not depend on scheduling.
+#include "common.hpp"
+#include "intdiv.hpp"
+
+#include <string.h>
+
+namespace nchip {
+
+constexpr int kB = 256;
+
+// ------------------------------------------------------------------------------------------------
+// index maps
+// ------------------------------------------------------------------------------------------------
+template <int NOPS>
+struct IdxMap {
+    int nd;
+    uint32_t size[NC_HIP_MAX_DIMS];  // innermost dim counted in work units (elements or vectors)
+    IntDiv div[NC_HIP_MAX_DIMS];
+    int64_t st[NOPS][NC_HIP_MAX_DIMS];  // element strides; innermost already multiplied by the unit
+};
+
+// offsets of every operand for work item w (row-major, last dim fastest)
+template <int NOPS>
+__device__ __forceinline__ void offsets(const IdxMap<NOPS> &m, uint32_t w, int64_t *off) {
+#pragma unroll
+    for (int o = 0; o < NOPS; o++) off[o] = 0;
+#pragma unroll
+    for (int d = NC_HIP_MAX_DIMS - 1; d >= 0; d--) {
+        if (d < m.nd) {
+            const uint32_t q = m.div[d].div(w);
+            const uint32_t i = w - q * m.size[d];
+            w = q;
+#pragma unroll
+            for (int o = 0; o < NOPS; o++) off[o] += (int64_t)i * m.st[o][d];
+        }
+    }
+}
+
+// loads 4 consecutive (along the innermost dim) elements of an operand with inner stride `is`
+__device__ __forceinline__ f4 load4(const float *p, int64_t is, int mode) {
+    if (mode == 1) return *(const f4 *)p;
+    if (mode == 0) {
+        const float v = *p;
+        return f4{v, v, v, v};
+    }
+    return f4{p[0], p[is], p[2 * is], p[3 * is]};
+}
+
+template <int OP>
+__device__ __forceinline__ float bin(float x, float y) {
+    if constexpr (OP == NC_HIP_BIN_ADD) return x + y;
+    else if constexpr (OP == NC_HIP_BIN_SUB) return x - y;
+    else if constexpr (OP == NC_HIP_BIN_MUL) return x * y;
+    else return x / y;
+}
+
+struct VecModes {
+    int a, b;          // 0 splat, 1 vector, 2 gather
+    int64_t ia, ib;    // inner element strides (for gathers)
+};
+
+template <int OP, bool VEC>
+__global__ __launch_bounds__(kB) void k_binary_fwd(const float *__restrict__ a, const float *__restrict__ b,
+                                                   float *__restrict__ o, IdxMap<3> m, VecModes vm, uint32_t nwork) {
+    const uint32_t step = gridDim.x * kB;
+    for (uint32_t w = blockIdx.x * kB + threadIdx.x; w < nwork; w += step) {
+        int64_t off[3];
+        offsets<3>(m, w, off);
+        if constexpr (VEC) {
+            const f4 x = load4(a + off[0], vm.ia, vm.a);
+            const f4 y = load4(b + off[1], vm.ib, vm.b);
+            f4 r;
+            r.x = bin<OP>(x.x, y.x);
+            r.y = bin<OP>(x.y, y.y);
+            r.z = bin<OP>(x.z, y.z);
+            r.w = bin<OP>(x.w, y.w);
+            __builtin_nontemporal_store(r, (f4 *)(o + off[2]));
+        } else {
+            o[off[2]] = bin<OP>(a[off[0]], b[off[1]]);
+        }
+    }
+}
+
+// 64-bit fallback for outputs with 2^32 or more work items
+template <int OP>
+__global__ __launch_bounds__(kB) void k_binary_fwd_big(const float *__restrict__ a, const float *__restrict__ b,
+                                                       float *__restrict__ o, IdxMap<3> m, int64_t n) {
+    const int64_t step = (int64_t)gridDim.x * kB;
+    for (int64_t w = (int64_t)blockIdx.x * kB + threadIdx.x; w < n; w += step) {
+        int64_t rem = w, oa = 0, ob = 0, oo = 0;
+        for (int d = m.nd - 1; d >= 0; d--) {
+            const int64_t i = rem % m.size[d];
+            rem /= m.size[d];
+            oa += i * m.st[0][d];
+            ob += i * m.st[1][d];
+            oo += i * m.st[2][d];
+        }
+        o[oo] = bin<OP>(a[oa], b[ob]);
+    }
+}
+
+struct Prepared {
+    int nd;
+    int64_t shape[NC_HIP_MAX_DIMS];
+    int64_t st[4][NC_HIP_MAX_DIMS];
+    int64_t numel;
+};
+
+static int prepare(int nd, const int64_t *shape, int nops, const int64_t *const *strides, Prepared &p,
+                   const char *who) {
+    if (nd < 0 || nd > NC_HIP_MAX_DIMS) return set_error(NC_HIP_ERR_ARG, "%s: ndim %d out of range", who, nd);
+    p.numel = 1;
+    for (int d = 0; d < nd; d++) {
+        if (shape[d] < 0) return set_error(NC_HIP_ERR_ARG, "%s: negative dim", who);
+        p.shape[d] = shape[d];
+        p.numel *= shape[d];
+        for (int o = 0; o < nops; o++) p.st[o][d] = strides[o][d];
+    }
+    p.nd = p.numel ? coalesce(nd, p.shape, nops, p.st) : 0;
+    return NC_HIP_OK;
+}
+
+template <int NOPS>
+static void make_map(const Prepared &p, int unit, IdxMap<NOPS> &m) {
+    m.nd = p.nd;
+    for (int d = 0; d < p.nd; d++) {
+        const int64_t sz = d == p.nd - 1 ? p.shape[d] / unit : p.shape[d];
+        m.size[d] = (uint32_t)sz;
+        m.div[d] = IntDiv((uint32_t)sz);
+        for (int o = 0; o < NOPS; o++) m.st[o][d] = d == p.nd - 1 ? p.st[o][d] * unit : p.st[o][d];
+    }
+    for (int d = p.nd; d < NC_HIP_MAX_DIMS; d++) {
+        m.size[d] = 1;
+        m.div[d] = IntDiv(1);
+        for (int o = 0; o < NOPS; o++) m.st[o][d] = 0;
+    }
+}
+
+static int vec_mode(const float *base, const Prepared &p, int o) {
+    const int64_t is = p.st[o][p.nd - 1];
+    if (is == 0) return 0;
+    if (is != 1) return 2;
+    if (!aligned16(base)) return -1;
+    for (int d = 0; d < p.nd - 1; d++)
+        if (p.st[o][d] % 4) return -1;
+    return 1;
+}
+
+template <int OP>
+static int launch_fwd(const float *a, const float *b, float *o, const Prepared &p, hipStream_t st) {
+    if (p.numel == 0) return NC_HIP_OK;
+    if (p.nd == 0) {  // a single element
+        IdxMap<3> m;
+        Prepared q = p;
+        q.nd = 1;
+        q.shape[0] = 1;
+        q.st[0][0] = q.st[1][0] = q.st[2][0] = 0;
+        make_map<3>(q, 1, m);
+        hipLaunchKernelGGL((k_binary_fwd<OP, false>), dim3(1), dim3(kB), 0, st, a, b, o, m, VecModes{}, 1u);
+        return check_launch("nc_hip_binary_fwd");
+    }
+    const int inner = p.nd - 1;
+    int ma = vec_mode(a, p, 0), mb = vec_mode(b, p, 1);
+    const bool vec = p.st[2][inner] == 1 && p.shape[inner] % 4 == 0 && vec_mode(o, p, 2) == 1 && ma >= 0 && mb >= 0;
+    const int unit = vec ? 4 : 1;
+    const int64_t nwork = p.numel / unit;
+    if (nwork >= (int64_t)UINT32_MAX) {
+        IdxMap<3> m;
+        make_map<3>(p, 1, m);
+        hipLaunchKernelGGL(k_binary_fwd_big<OP>, dim3(stream_grid(p.numel, kB)), dim3(kB), 0, st, a, b, o, m,
+                           p.numel);
+        return check_launch("nc_hip_binary_fwd");
+    }
+    IdxMap<3> m;
+    make_map<3>(p, unit, m);
+    const unsigned grid = stream_grid(nwork, kB, 16);
+    if (vec) {
+        VecModes vm{ma, mb, p.st[0][inner], p.st[1][inner]};
+        hipLaunchKernelGGL((k_binary_fwd<OP, true>), dim3(grid), dim3(kB), 0, st, a, b, o, m, vm, (uint32_t)nwork);
+    } else {
+        hipLaunchKernelGGL((k_binary_fwd<OP, false>), dim3(grid), dim3(kB), 0, st, a, b, o, m, VecModes{},
+                           (uint32_t)nwork);
+    }
+    return check_launch("nc_hip_binary_fwd");
+}
+
+// ------------------------------------------------------------------------------------------------
+// gradients
+// ------------------------------------------------------------------------------------------------
+// fp32 term with the reference's association (unreduced grads: bit-identical)
+// mode: 0 alpha*g, 1 g*p1, 2 g/p1, 3 -(g*p1)/(p2*p2)
+template <int MODE>
+__device__ __forceinline__ float grad_f(float gi, float g, float p1, float p2, float alpha) {
+    if constexpr (MODE == 0) return fma_(alpha, g, gi);  // axpy_f32 (same-shape add/sub, ops_elementwise.c:162-164)
+    else if constexpr (MODE == 1) return gi + g * p1;
+    else if constexpr (MODE == 2) return gi + g / p1;
+    else return gi - (g * p1) / (p2 * p2);
+}
+
+// fp64 term for reduced grads
+template <int MODE>
+__device__ __forceinline__ double grad_d(double g, double p1, double p2, double alpha) {
+    if constexpr (MODE == 0) return alpha * g;
+    else if constexpr (MODE == 1) return g * p1;
+    else if constexpr (MODE == 2) return g / p1;
+    else return -(g * p1) / (p2 * p2);
+}
+
+// operand order in the maps: 0 g, 1 p1, 2 p2, 3 gx
+template <int MODE, bool ACC>
+__global__ __launch_bounds__(kB) void k_grad_elementwise(const float *__restrict__ g, const float *__restrict__ p1,
+                                                         const float *__restrict__ p2, float *__restrict__ gx,
+                                                         IdxMap<4> m, uint32_t nwork, float alpha) {
+    const uint32_t step = gridDim.x * kB;
+    for (uint32_t w = blockIdx.x * kB + threadIdx.x; w < nwork; w += step) {
+        int64_t off[4];
+        offsets<4>(m, w, off);
+        const float v1 = MODE == 1 || MODE == 2 || MODE == 3 ? p1[off[1]] : 0.0f;
+        const float v2 = MODE == 3 ? p2[off[2]] : 0.0f;
+        const float old = ACC ? gx[off[3]] : 0.0f;
+        gx[off[3]] = grad_f<MODE>(old, g[off[0]], v1, v2, alpha);
+    }
+}
+
+// Reduced grads.  The coalesced dims split into kept dims (gx stride != 0) and reduced dims.
+struct RedPlan {
+    IdxMap<4> kept;      // over the M kept indices (gx offsets in operand 3)
+    IdxMap<3> red;       // over the K reduced indices (g, p1, p2 offsets)
+    uint32_t M, K;
+    uint32_t chunk;      // reduced indices per partial
+    uint32_t P;          // partials per kept index
+    int inner_kept;      // 1: lanes <-> kept indices (column mode), 0: lanes <-> reduced (row mode)
+};
+
+// column mode: one lane per kept index, sequential over a chunk of reduced indices (odometer)
+template <int MODE>
+__global__ __launch_bounds__(kB) void k_grad_reduce_col(const float *__restrict__ g, const float *__restrict__ p1,
+                                                        const float *__restrict__ p2, RedPlan pl, double alpha,
+                                                        double *__restrict__ part) {
+    const uint64_t total = (uint64_t)pl.M * pl.P;
+    for (uint64_t item = (uint64_t)blockIdx.x * kB + threadIdx.x; item < total; item += (uint64_t)gridDim.x * kB) {
+    const uint32_t mi = (uint32_t)(item % pl.M);
+    const uint32_t p = (uint32_t)(item / pl.M);
+    int64_t ko[4];
+    offsets<4>(pl.kept, mi, ko);
+    const uint32_t k0 = p * pl.chunk;
+    const uint32_t k1 = min(pl.K, k0 + pl.chunk);
+    // starting reduced coordinates
+    uint32_t idx[NC_HIP_MAX_DIMS];
+    int64_t ro[3] = {0, 0, 0};
+    {
+        uint32_t w = k0;
+#pragma unroll
+        for (int d = NC_HIP_MAX_DIMS - 1; d >= 0; d--) {
+            if (d < pl.red.nd) {
+                const uint32_t q = pl.red.div[d].div(w);
+                idx[d] = w - q * pl.red.size[d];
+                w = q;
+#pragma unroll
+                for (int o = 0; o < 3; o++) ro[o] += (int64_t)idx[d] * pl.red.st[o][d];
+            }
+        }
+    }
+    const int inner = pl.red.nd - 1;
+    const int64_t s0 = pl.red.st[0][inner], s1 = pl.red.st[1][inner], s2 = pl.red.st[2][inner];
+    const uint32_t n_in = pl.red.size[inner];
+    double acc = 0.0;
+    uint32_t k = k0;
+    while (k < k1) {
+        // run along the innermost reduced dim without carries
+        const uint32_t run = min(k1 - k, n_in - idx[inner]);
+        const float *pg = g + ko[0] + ro[0];
+        const float *q1 = p1 + ko[1] + ro[1];
+        const float *q2 = p2 + ko[2] + ro[2];
+        for (uint32_t r = 0; r < run; r++) {
+            const double v1 = (MODE == 1 || MODE == 2 || MODE == 3) ? (double)q1[r * s1] : 0.0;
+            const double v2 = MODE == 3 ? (double)q2[r * s2] : 0.0;
+            acc += grad_d<MODE>((double)pg[r * s0], v1, v2, alpha);
+        }
+        k += run;
+        if (k >= k1) break;
+        // carry into the outer reduced dims
+        ro[0] += (int64_t)run * s0;
+        ro[1] += (int64_t)run * s1;
+        ro[2] += (int64_t)run * s2;
+        idx[inner] += run;
+        for (int d = inner; d >= 0; d--) {
+            if (idx[d] < pl.red.size[d]) break;
+            ro[0] -= (int64_t)idx[d] * pl.red.st[0][d];
+            ro[1] -= (int64_t)idx[d] * pl.red.st[1][d];
+            ro[2] -= (int64_t)idx[d] * pl.red.st[2][d];
+            idx[d] = 0;
+            if (d > 0) {
+                idx[d - 1]++;
+                ro[0] += pl.red.st[0][d - 1];
+                ro[1] += pl.red.st[1][d - 1];
+                ro[2] += pl.red.st[2][d - 1];
+            }
+        }
+    }
+    part[(size_t)p * pl.M + mi] = acc;
+    }
+}
+
+// row mode: one block per (kept index, chunk of reduced indices); lanes stride over the chunk
+template <int MODE>
+__global__ __launch_bounds__(kB) void k_grad_reduce_row(const float *__restrict__ g, const float *__restrict__ p1,
+                                                        const float *__restrict__ p2, RedPlan pl, double alpha,
+                                                        double *__restrict__ part) {
+    __shared__ double sh[kB / kWave];
+    const uint64_t total = (uint64_t)pl.M * pl.P;
+    for (uint64_t item = blockIdx.x; item < total; item += gridDim.x) {  // block-uniform loop
+        const uint32_t mi = (uint32_t)(item % pl.M);
+        const uint32_t p = (uint32_t)(item / pl.M);
+        int64_t ko[4];
+        offsets<4>(pl.kept, mi, ko);
+        const uint32_t k0 = p * pl.chunk;
+        const uint32_t k1 = min(pl.K, k0 + pl.chunk);
+        double acc = 0.0;
+        for (uint32_t k = k0 + threadIdx.x; k < k1; k += kB) {
+            int64_t ro[3];
+            offsets<3>(pl.red, k, ro);
+            const double v1 = (MODE == 1 || MODE == 2 || MODE == 3) ? (double)p1[ko[1] + ro[1]] : 0.0;
+            const double v2 = MODE == 3 ? (double)p2[ko[2] + ro[2]] : 0.0;
+            acc += grad_d<MODE>((double)g[ko[0] + ro[0]], v1, v2, alpha);
+        }
+        acc = wave_sum(acc);
+        if ((threadIdx.x & (kWave - 1)) == 0) sh[threadIdx.x / kWave] = acc;
+        __syncthreads();
+        if (threadIdx.x == 0) {
+            double t = 0.0;
+#pragma unroll
+            for (int i = 0; i < kB / kWave; i++) t += sh[i];
+            part[(size_t)p * pl.M + mi] = t;
+        }
+        __syncthreads();
+    }
+}
+
+// gx[kept m] (+)= sum over partials, in partial order
+template <bool ACC>
+__global__ __launch_bounds__(kB) void k_grad_finalize(const double *__restrict__ part, float *__restrict__ gx,
+                                                      IdxMap<4> kept, uint32_t M, uint32_t P) {
+    const uint32_t mi = blockIdx.x * kB + threadIdx.x;
+    if (mi >= M) return;
+    int64_t ko[4];
+    offsets<4>(kept, mi, ko);
+    double t = ACC ? (double)gx[ko[3]] : 0.0;
+    for (uint32_t p = 0; p < P; p++) t += part[(size_t)p * M + mi];
+    gx[ko[3]] = (float)t;
+}
+
+static int grad_mode(int op, int which) {
+    if (op == NC_HIP_BIN_ADD || op == NC_HIP_BIN_SUB) return 0;
+    if (op == NC_HIP_BIN_MUL || which == 0) return op == NC_HIP_BIN_MUL ? 1 : 2;
+    return 3;
+}
+
+// Builds the reduction plan; returns false when nothing is reduced.
+static bool plan_reduce(const Prepared &p, RedPlan &pl, size_t *ws_need) {
+    Prepared kp{}, rp{};
+    kp.nd = rp.nd = 0;
+    uint64_t M = 1, K = 1;
+    for (int d = 0; d < p.nd; d++) {
+        if (p.st[3][d] == 0) {
+            rp.shape[rp.nd] = p.shape[d];
+            for (int o = 0; o < 3; o++) rp.st[o][rp.nd] = p.st[o][d];
+            rp.nd++;
+            K *= (uint64_t)p.shape[d];
+        } else {
+            kp.shape[kp.nd] = p.shape[d];
+            for (int o = 0; o < 4; o++) kp.st[o][kp.nd] = p.st[o][d];
+            kp.nd++;
+            M *= (uint64_t)p.shape[d];
+        }
+    }
+    if (rp.nd == 0) return false;
+    if (kp.nd == 0) {  // full reduction: one kept index
+        kp.nd = 1;
+        kp.shape[0] = 1;
+        for (int o = 0; o < 4; o++) kp.st[o][0] = 0;
+    }
+    make_map<4>(kp, 1, pl.kept);
+    make_map<3>(rp, 1, pl.red);
+    pl.M = (uint32_t)M;
+    pl.K = (uint32_t)K;
+    pl.inner_kept = p.nd > 0 && p.st[3][p.nd - 1] != 0;
+    const uint64_t target = (uint64_t)num_cus() * 2048;  // lanes to keep every CU busy
+    if (pl.inner_kept) {
+        uint64_t P = (target + M - 1) / M;
+        uint64_t maxP = (K + 63) / 64;  // at least 64 terms per lane
+        if (P > maxP) P = maxP;
+        if (P < 1) P = 1;
+        pl.chunk = (uint32_t)((K + P - 1) / P);
+        pl.P = (uint32_t)((K + pl.chunk - 1) / pl.chunk);
+    } else {
+        uint64_t blocks_target = (uint64_t)num_cus() * 8;
+        uint64_t P = (blocks_target + M - 1) / M;
+        uint64_t maxP = (K + 4 * kB - 1) / (4 * kB);  // at least 4 terms per lane
+        if (P > maxP) P = maxP;
+        if (P < 1) P = 1;
+        pl.chunk = (uint32_t)((K + P - 1) / P);
+        pl.P = (uint32_t)((K + pl.chunk - 1) / pl.chunk);
+    }
+    *ws_need = (size_t)pl.P * pl.M * sizeof(double);
+    return true;
+}
+
+template <int MODE>
+static int launch_grad(const float *g, const float *p1, const float *p2, float *gx, const Prepared &p, float alpha,
+                       int acc, void *ws, size_t ws_bytes, hipStream_t st) {
+    if (p.numel == 0) return NC_HIP_OK;
+    RedPlan pl;
+    size_t need = 0;
+    if (!plan_reduce(p, pl, &need)) {
+        Prepared q = p;
+        if (q.nd == 0) {
+            q.nd = 1;
+            q.shape[0] = 1;
+            for (int o = 0; o < 4; o++) q.st[o][0] = 0;
+        }
+        IdxMap<4> m;
+        make_map<4>(q, 1, m);
+        if (p.numel >= (int64_t)UINT32_MAX) return set_error(NC_HIP_ERR_ARG, "grad: 2^32 or more elements");
+        const unsigned grid = stream_grid(p.numel, kB, 16);
+        if (acc)
+            hipLaunchKernelGGL((k_grad_elementwise<MODE, true>), dim3(grid), dim3(kB), 0, st, g, p1, p2, gx, m,
+                               (uint32_t)p.numel, alpha);
+        else
+            hipLaunchKernelGGL((k_grad_elementwise<MODE, false>), dim3(grid), dim3(kB), 0, st, g, p1, p2, gx, m,
+                               (uint32_t)p.numel, alpha);
+        return check_launch("nc_hip_binary_bwd");
+    }
+    if (p.numel >= (int64_t)UINT32_MAX)
+        return set_error(NC_HIP_ERR_ARG, "grad: sum-to-shape over 2^32 or more elements is not supported");
+    if (ws_bytes < need || (need && !ws))
+        return set_error(NC_HIP_ERR_WORKSPACE, "grad: workspace of %zu bytes needed, %zu given", need, ws_bytes);
+    double *part = (double *)ws;
+    const uint64_t items = (uint64_t)pl.M * pl.P;
+    if (pl.inner_kept) {
+        const uint64_t blocks = (items + kB - 1) / kB;
+        const unsigned grid = (unsigned)(blocks < 1048576 ? blocks : 1048576);
+        hipLaunchKernelGGL(k_grad_reduce_col<MODE>, dim3(grid), dim3(kB), 0, st, g, p1, p2, pl, (double)alpha, part);
+    } else {
+        const unsigned grid = (unsigned)(items < 1048576 ? items : 1048576);
+        hipLaunchKernelGGL(k_grad_reduce_row<MODE>, dim3(grid), dim3(kB), 0, st, g, p1, p2, pl, (double)alpha, part);
+    }
+    const unsigned fg = (pl.M + kB - 1) / kB;
+    if (acc)
+        hipLaunchKernelGGL(k_grad_finalize<true>, dim3(fg), dim3(kB), 0, st, part, gx, pl.kept, pl.M, pl.P);
+    else
+        hipLaunchKernelGGL(k_grad_finalize<false>, dim3(fg), dim3(kB), 0, st, part, gx, pl.kept, pl.M, pl.P);
+    return check_launch("nc_hip_binary_bwd");
+}
+
+static int prepare_grad(int op, int which, int nd, const int64_t *shape, const int64_t *sg, const int64_t *sa,
+                        const int64_t *sb, const int64_t *sgx, Prepared &p, int &mode, float &alpha,
+                        bool &p1_is_a) {
+    mode = grad_mode(op, which);
+    alpha = (op == NC_HIP_BIN_SUB && which == 1) ? -1.0f : 1.0f;
+    // p1 = other operand (mul), b (div wrt a), a (div wrt b); p2 = b (div wrt b)
+    p1_is_a = (op == NC_HIP_BIN_MUL && which == 1) || (op == NC_HIP_BIN_DIV && which == 1);
+    const int64_t *s1 = p1_is_a ? sa : sb;
+    const int64_t zeros[NC_HIP_MAX_DIMS] = {0, 0, 0, 0, 0, 0};
+    if (mode == 0) s1 = zeros;
+    const int64_t *s2 = mode == 3 ? sb : zeros;
+    const int64_t *strides[4] = {sg, s1, s2, sgx};
+    return prepare(nd, shape, 4, strides, p, "nc_hip_binary_bwd");
+}
+
+}  // namespace nchip
+
+using namespace nchip;
+
+extern "C" NC_HIP_API int nc_hip_binary_fwd(int op, int nd, const int64_t *shape, const float *a,
+                                            const int64_t *sa, const float *b, const int64_t *sb, float *o,
+                                            const int64_t *so, void *stream) {
+    Prepared p;
+    const int64_t *strides[3] = {sa, sb, so};
+    int rc = prepare(nd, shape, 3, strides, p, "nc_hip_binary_fwd");
+    if (rc) return rc;
+    if (p.numel && (!a || !b || !o)) return set_error(NC_HIP_ERR_ARG, "nc_hip_binary_fwd: NULL pointer");
+    hipStream_t st = as_stream(stream);
+    switch (op) {
+    case NC_HIP_BIN_ADD: return launch_fwd<NC_HIP_BIN_ADD>(a, b, o, p, st);
+    case NC_HIP_BIN_SUB: return launch_fwd<NC_HIP_BIN_SUB>(a, b, o, p, st);
+    case NC_HIP_BIN_MUL: return launch_fwd<NC_HIP_BIN_MUL>(a, b, o, p, st);
+    case NC_HIP_BIN_DIV: return launch_fwd<NC_HIP_BIN_DIV>(a, b, o, p, st);
+    default: return set_error(NC_HIP_ERR_ARG, "nc_hip_binary_fwd: unknown op %d", op);
+    }
+}
+
+extern "C" NC_HIP_API size_t nc_hip_binary_bwd_workspace(int nd, const int64_t *shape, const int64_t *sgx) {
+    if (nd < 0 || nd > NC_HIP_MAX_DIMS) return 0;
+    // the plan depends only on the shape and on which dims gx keeps: use unit strides elsewhere
+    int64_t cs[NC_HIP_MAX_DIMS], s = 1;
+    for (int d = nd - 1; d >= 0; d--) {
+        cs[d] = s;
+        s *= shape[d];
+    }
+    const int64_t *strides[4] = {cs, cs, cs, sgx};
+    Prepared p;
+    if (prepare(nd, shape, 4, strides, p, "nc_hip_binary_bwd_workspace") || p.numel == 0) return 0;
+    RedPlan pl;
+    size_t need = 0;
+    return plan_reduce(p, pl, &need) ? need : 0;
+}
+
+extern "C" NC_HIP_API int nc_hip_binary_bwd(int op, int which, int nd, const int64_t *shape, const float *g,
+                                            const int64_t *sg, const float *a, const int64_t *sa, const float *b,
+                                            const int64_t *sb, float *gx, const int64_t *sgx, int accumulate,
+                                            void *ws, size_t ws_bytes, void *stream) {
+    if (op < 0 || op > 3 || (which != 0 && which != 1))
+        return set_error(NC_HIP_ERR_ARG, "nc_hip_binary_bwd: bad op/which");
+    Prepared p;
+    int mode;
+    float alpha;
+    bool p1_is_a;
+    int rc = prepare_grad(op, which, nd, shape, sg, sa, sb, sgx, p, mode, alpha, p1_is_a);
+    if (rc) return rc;
+    const float *p1 = p1_is_a ? a : b;
+    const float *p2 = b;
+    hipStream_t st = as_stream(stream);
+    switch (mode) {
+    case 0: return launch_grad<0>(g, g, g, gx, p, alpha, accumulate, ws, ws_bytes, st);
+    case 1: return launch_grad<1>(g, p1, g, gx, p, alpha, accumulate, ws, ws_bytes, st);
+    case 2: return launch_grad<2>(g, p1, g, gx, p, alpha, accumulate, ws, ws_bytes, st);
+    default: return launch_grad<3>(g, p1, p2, gx, p, alpha, accumulate, ws, ws_bytes, st);
+    }
+}
+
+extern "C" NC_HIP_API size_t nc_hip_binary_bwd2_workspace(int nd, const int64_t *shape, const int64_t *sga,
+                                                          const int64_t *sgb) {
+    size_t wa = sga ? nc_hip_binary_bwd_workspace(nd, shape, sga) : 0;
+    size_t wb = sgb ? nc_hip_binary_bwd_workspace(nd, shape, sgb) : 0;
+    return wa > wb ? wa : wb;
+}
+
+extern "C" NC_HIP_API int nc_hip_binary_bwd2(int op, int nd, const int64_t *shape, const float *g,
+                                             const int64_t *sg, const float *a, const int64_t *sa, const float *b,
+                                             const int64_t *sb, float *ga, const int64_t *sga, float *gb,
+                                             const int64_t *sgb, int accumulate, void *ws, size_t ws_bytes,
+                                             void *stream) {
+    int rc = NC_HIP_OK;
+    if (ga) rc = nc_hip_binary_bwd(op, 0, nd, shape, g, sg, a, sa, b, sb, ga, sga, accumulate, ws, ws_bytes, stream);
+    if (rc == NC_HIP_OK && gb)
+        rc = nc_hip_binary_bwd(op, 1, nd, shape, g, sg, a, sa, b, sb, gb, sgb, accumulate, ws, ws_bytes, stream);
+    return rc;
+}
+
+// ------------------------------------------------------------------------------------------------
+// strided copies, fills, conversions
+// ------------------------------------------------------------------------------------------------
+namespace nchip {
+
+template <typename T>
+__global__ __launch_bounds__(kB) void k_gather(const T *__restrict__ src, T *__restrict__ dst, IdxMap<1> m,
+                                               uint32_t n) {
+    const uint32_t step = gridDim.x * kB;
+    for (uint32_t w = blockIdx.x * kB + threadIdx.x; w < n; w += step) {
+        int64_t off[1];
+        offsets<1>(m, w, off);
+        dst[w] = src[off[0]];
+    }
+}
+
+__global__ __launch_bounds__(kB) void k_scatter_add(const float *__restrict__ src, float *__restrict__ dst,
+                                                    IdxMap<1> m, uint32_t n) {
+    const uint32_t step = gridDim.x * kB;
+    for (uint32_t w = blockIdx.x * kB + threadIdx.x; w < n; w += step) {
+        int64_t off[1];
+        offsets<1>(m, w, off);
+        dst[off[0]] = dst[off[0]] + src[w];
+    }
+}
+
+__global__ __launch_bounds__(kB) void k_axpy(const float *__restrict__ x, float *__restrict__ y, int64_t n, float al) {
+    const int64_t step = (int64_t)gridDim.x * kB;
+    for (int64_t i = (int64_t)blockIdx.x * kB + threadIdx.x; i < n; i += step) y[i] = fma_(al, x[i], y[i]);
+}
+
+template <typename T>
+__global__ __launch_bounds__(kB) void k_fill(T *__restrict__ dst, T v, int64_t n) {
+    const int64_t step = (int64_t)gridDim.x * kB;
+    for (int64_t i = (int64_t)blockIdx.x * kB + threadIdx.x; i < n; i += step) dst[i] = v;
+}
+
+__global__ void k_add_at(float *p, float v) { p[0] = p[0] + v; }
+
+template <typename S>
+__device__ __forceinline__ double load_d(const S *p, int64_t i) { return (double)p[i]; }
+
+__device__ __forceinline__ double saturate(double v, double lo, double hi) {
+    if (v != v) return 0.0;
+    return v < lo ? lo : v > hi ? hi : v;
+}
+
+template <typename S, typename D>
+__global__ __launch_bounds__(kB) void k_convert(const S *__restrict__ src, D *__restrict__ dst, int64_t n) {
+    const int64_t step = (int64_t)gridDim.x * kB;
+    for (int64_t i = (int64_t)blockIdx.x * kB + threadIdx.x; i < n; i += step) {
+        const double v = (double)src[i];
+        if constexpr (sizeof(D) == 4 && D(0.5) != D(0)) dst[i] = (float)v;                 // f32
+        else if constexpr (sizeof(D) == 4) dst[i] = (int32_t)saturate(v, -2147483648.0, 2147483647.0);
+        else if constexpr (D(-1) < D(0)) dst[i] = (int8_t)saturate(v, -128.0, 127.0);       // i8
+        else dst[i] = (uint8_t)saturate(v, 0.0, 255.0);                                     // u8
+    }
+}
+
+}  // namespace nchip
+
+extern "C" NC_HIP_API int nc_hip_copy_strided(int elem_bytes, int nd, const int64_t *shape, const void *src,
+                                              const int64_t *ss, void *dst, void *stream) {
+    Prepared p;
+    int64_t cs[NC_HIP_MAX_DIMS];
+    const int64_t *strides[1] = {ss};
+    int rc = prepare(nd, shape, 1, strides, p, "nc_hip_copy_strided");
+    (void)cs;
+    if (rc) return rc;
+    if (p.numel == 0) return NC_HIP_OK;
+    hipStream_t st = as_stream(stream);
+    if (p.nd <= 1 && (p.nd == 0 || p.st[0][0] == 1)) {
+        if (hipMemcpyAsync(dst, src, (size_t)p.numel * elem_bytes, hipMemcpyDeviceToDevice, st) != hipSuccess)
+            return check_launch("nc_hip_copy_strided");
+        return NC_HIP_OK;
+    }
+    if (p.numel >= (int64_t)UINT32_MAX) return set_error(NC_HIP_ERR_ARG, "copy_strided: too many elements");
+    IdxMap<1> m;
+    make_map<1>(p, 1, m);
+    const unsigned grid = stream_grid(p.numel, kB, 16);
+    const uint32_t n = (uint32_t)p.numel;
+    switch (elem_bytes) {
+    case 1: hipLaunchKernelGGL(k_gather<uint8_t>, grid, kB, 0, st, (const uint8_t *)src, (uint8_t *)dst, m, n); break;
+    case 2: hipLaunchKernelGGL(k_gather<uint16_t>, grid, kB, 0, st, (const uint16_t *)src, (uint16_t *)dst, m, n); break;
+    case 4: hipLaunchKernelGGL(k_gather<uint32_t>, grid, kB, 0, st, (const uint32_t *)src, (uint32_t *)dst, m, n); break;
+    case 8: hipLaunchKernelGGL(k_gather<uint64_t>, grid, kB, 0, st, (const uint64_t *)src, (uint64_t *)dst, m, n); break;
+    default: return set_error(NC_HIP_ERR_ARG, "copy_strided: element size %d", elem_bytes);
+    }
+    return check_launch("nc_hip_copy_strided");
+}
+
+extern "C" NC_HIP_API int nc_hip_accumulate_strided(int nd, const int64_t *shape, const float *src, float *dst,
+                                                    const int64_t *sd, void *stream) {
+    Prepared p;
+    const int64_t *strides[1] = {sd};
+    int rc = prepare(nd, shape, 1, strides, p, "nc_hip_accumulate_strided");
+    if (rc) return rc;
+    if (p.numel == 0) return NC_HIP_OK;
+    if (p.numel >= (int64_t)UINT32_MAX) return set_error(NC_HIP_ERR_ARG, "accumulate_strided: too many elements");
+    if (p.nd == 0) {
+        p.nd = 1;
+        p.shape[0] = 1;
+        p.st[0][0] = 0;
+    }
+    IdxMap<1> m;
+    make_map<1>(p, 1, m);
+    hipLaunchKernelGGL(k_scatter_add, stream_grid(p.numel, kB, 16), kB, 0, as_stream(stream), src, dst, m,
+                       (uint32_t)p.numel);
+    return check_launch("nc_hip_accumulate_strided");
+}
+
+extern "C" NC_HIP_API int nc_hip_axpy(int64_t n, float alpha, const float *x, float *y, void *stream) {
+    if (n <= 0) return NC_HIP_OK;
+    hipLaunchKernelGGL(k_axpy, stream_grid(n, kB, 16), kB, 0, as_stream(stream), x, y, n, alpha);
+    return check_launch("nc_hip_axpy");
+}
+
+extern "C" NC_HIP_API int nc_hip_fill(void *dst, int elem_bytes, uint64_t pattern, int64_t n, void *stream) {
+    if (n <= 0) return NC_HIP_OK;
+    hipStream_t st = as_stream(stream);
+    const unsigned grid = stream_grid(n, kB, 16);
+    switch (elem_bytes) {
+    case 1: hipLaunchKernelGGL(k_fill<uint8_t>, grid, kB, 0, st, (uint8_t *)dst, (uint8_t)pattern, n); break;
+    case 2: hipLaunchKernelGGL(k_fill<uint16_t>, grid, kB, 0, st, (uint16_t *)dst, (uint16_t)pattern, n); break;
+    case 4: hipLaunchKernelGGL(k_fill<uint32_t>, grid, kB, 0, st, (uint32_t *)dst, (uint32_t)pattern, n); break;
+    case 8: hipLaunchKernelGGL(k_fill<uint64_t>, grid, kB, 0, st, (uint64_t *)dst, (uint64_t)pattern, n); break;
+    default: return set_error(NC_HIP_ERR_ARG, "fill: element size %d", elem_bytes);
+    }
+    return check_launch("nc_hip_fill");
+}
+
+extern "C" NC_HIP_API int nc_hip_add_scalar_at(float *p, float v, void *stream) {
+    hipLaunchKernelGGL(k_add_at, 1, 1, 0, as_stream(stream), p, v);
+    return check_launch("nc_hip_add_scalar_at");
+}
+
+extern "C" NC_HIP_API int nc_hip_convert(int from, int to, int64_t n, const void *src, void *dst, void *stream) {
+    if (n <= 0) return NC_HIP_OK;
+    hipStream_t st = as_stream(stream);
+    const unsigned grid = stream_grid(n, kB, 16);
+#define NC_CONV(S, D) hipLaunchKernelGGL((k_convert<S, D>), grid, kB, 0, st, (const S *)src, (D *)dst, n)
+#define NC_CONV_TO(S)                                          \
+    switch (to) {                                              \
+    case NC_HIP_F32: NC_CONV(S, float); break;                 \
+    case NC_HIP_I32: NC_CONV(S, int32_t); break;               \
+    case NC_HIP_I8: NC_CONV(S, int8_t); break;                 \
+    case NC_HIP_U8: NC_CONV(S, uint8_t); break;                \
+    default: return set_error(NC_HIP_ERR_ARG, "convert: target %d", to); \
+    }
+    switch (from) {
+    case NC_HIP_F32: NC_CONV_TO(float); break;
+    case NC_HIP_I32: NC_CONV_TO(int32_t); break;
+    case NC_HIP_I8: NC_CONV_TO(int8_t); break;
+    case NC_HIP_U8: NC_CONV_TO(uint8_t); break;
+    default: return set_error(NC_HIP_ERR_ARG, "convert: source %d", from);
+    }
+#undef NC_CONV_TO
+#undef NC_CONV
+    return check_launch("nc_hip_convert");
+}

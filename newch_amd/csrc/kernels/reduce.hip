@@ -1,0 +1,436 @@
+// Reductions over one axis or all (the reference's ops_reduce.c:13-163): x is viewed as
+// [outer, R, inner] and reduced over R.
+//
+// Layout-driven kernels:
+//   * inner == 1, many rows: one wave per row, 128-bit loads along the row, wave64 shuffle reduce;
+//   * inner == 1, few long rows (a full reduction is outer = 1): each row is split into fixed
+//     chunks, one workgroup per (row, chunk) writes an fp64 partial, a second kernel combines the
+//     partials of each row in chunk order (two-pass, deterministic);
+//   * inner > 1: lanes run along the contiguous inner dim (coalesced), each lane scans R (split into
+//     fixed chunks with a combine pass when outer * inner is too small to fill the GPU).
+// Sums accumulate in fp64.  max / argmax reproduce the reference's sequential strict-greater scan
+// exactly: the first maximal index wins, a NaN at r = 0 is sticky, any later NaN is skipped.
+#include "common.hpp"
+#include "intdiv.hpp"
+
+#include <float.h>
+
+namespace nchip {
+
+constexpr int kRB = 256;
+constexpr int kEmpty = 0x7fffffff;  // argmax state "no element yet"
+
+// (value, index) state of the sequential scan restricted to non-NaN elements
+struct ArgState {
+    float v;
+    int i;
+};
+
+__device__ __forceinline__ void arg_push(ArgState &s, float v, int i) {
+    // elements arrive in increasing index order within one lane
+    if (v != v) return;
+    if (s.i == kEmpty || v > s.v) {
+        s.v = v;
+        s.i = i;
+    }
+}
+
+__device__ __forceinline__ ArgState arg_combine(ArgState a, ArgState b) {
+    if (a.i == kEmpty) return b;
+    if (b.i == kEmpty) return a;
+    if (b.v > a.v) return b;
+    if (a.v > b.v) return a;
+    return a.i <= b.i ? a : b;  // equal (including -0 == +0): first index
+}
+
+__device__ __forceinline__ ArgState wave_arg(ArgState s) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+        ArgState t{__shfl_xor(s.v, o, kWave), __shfl_xor(s.i, o, kWave)};
+        s = arg_combine(s, t);
+    }
+    return s;
+}
+
+template <int KIND>
+struct Acc {
+    double sum;
+    ArgState a;
+    __device__ __forceinline__ void init() {
+        sum = 0.0;
+        a = ArgState{0.0f, kEmpty};
+    }
+    __device__ __forceinline__ void push(float v, int i) {
+        if constexpr (KIND == NC_HIP_RED_SUM || KIND == NC_HIP_RED_MEAN) sum += (double)v;
+        else arg_push(a, v, i);
+    }
+    __device__ __forceinline__ void combine(const Acc &o) {
+        if constexpr (KIND == NC_HIP_RED_SUM || KIND == NC_HIP_RED_MEAN) sum += o.sum;
+        else a = arg_combine(a, o.a);
+    }
+    __device__ __forceinline__ void wave() {
+        if constexpr (KIND == NC_HIP_RED_SUM || KIND == NC_HIP_RED_MEAN) sum = wave_sum(sum);
+        else a = wave_arg(a);
+    }
+};
+
+// writes the result of row `o` (column `i`) given the row's first element x0 (NaN rule)
+template <int KIND>
+__device__ __forceinline__ void emit(const Acc<KIND> &acc, float x0, float scale, float *y, int32_t *arg,
+                                     int64_t at) {
+    if constexpr (KIND == NC_HIP_RED_SUM || KIND == NC_HIP_RED_MEAN) {
+        y[at] = scale * (float)acc.sum;
+    } else {
+        ArgState s = acc.a;
+        if (x0 != x0 || s.i == kEmpty) s = ArgState{x0, 0};
+        if (KIND == NC_HIP_RED_MAX) y[at] = s.v;
+        arg[at] = s.i;
+    }
+}
+
+// --- inner == 1, one wave per row --------------------------------------------------------------------
+template <int KIND, bool VEC>
+__global__ __launch_bounds__(kRB) void k_rows_wave(const float *__restrict__ x, float *__restrict__ y,
+                                                   int32_t *__restrict__ arg, int64_t outer, int64_t R, float scale) {
+    const int lane = threadIdx.x & (kWave - 1);
+    const int64_t wave = ((int64_t)blockIdx.x * kRB + threadIdx.x) / kWave;
+    const int64_t nwaves = (int64_t)gridDim.x * (kRB / kWave);
+    for (int64_t o = wave; o < outer; o += nwaves) {
+        const float *row = x + o * R;
+        Acc<KIND> acc;
+        acc.init();
+        if constexpr (VEC) {
+            const int64_t nv = R / 4;
+            for (int64_t v = lane; v < nv; v += kWave) {
+                const f4 q = __builtin_nontemporal_load((const f4 *)row + v);
+                acc.push(q.x, (int)(4 * v));
+                acc.push(q.y, (int)(4 * v + 1));
+                acc.push(q.z, (int)(4 * v + 2));
+                acc.push(q.w, (int)(4 * v + 3));
+            }
+        } else {
+            for (int64_t r = lane; r < R; r += kWave) acc.push(row[r], (int)r);
+        }
+        acc.wave();
+        if (lane == 0) emit<KIND>(acc, row[0], scale, y, arg, o);
+    }
+}
+
+// --- inner == 1, few long rows: chunk partials then combine -------------------------------------------
+template <int KIND>
+__global__ __launch_bounds__(kRB) void k_rows_chunk(const float *__restrict__ x, int64_t R, int64_t chunk, int P,
+                                                    double *__restrict__ psum, ArgState *__restrict__ parg,
+                                                    bool vec) {
+    const int64_t o = blockIdx.y;
+    const int p = blockIdx.x;
+    const float *row = x + o * R;
+    const int64_t r0 = (int64_t)p * chunk, r1 = min(R, r0 + chunk);
+    Acc<KIND> acc;
+    acc.init();
+    if (vec) {  // chunk is a multiple of 4 and the row is 16-byte aligned
+        const f4 *v4 = (const f4 *)(row + r0);
+        const int64_t nv = (r1 - r0) / 4;
+        for (int64_t v = threadIdx.x; v < nv; v += kRB) {
+            const f4 q = __builtin_nontemporal_load(v4 + v);
+            const int base = (int)(r0 + 4 * v);
+            acc.push(q.x, base);
+            acc.push(q.y, base + 1);
+            acc.push(q.z, base + 2);
+            acc.push(q.w, base + 3);
+        }
+        for (int64_t r = r0 + nv * 4 + threadIdx.x; r < r1; r += kRB) acc.push(row[r], (int)r);
+    } else {
+        for (int64_t r = r0 + threadIdx.x; r < r1; r += kRB) acc.push(row[r], (int)r);
+    }
+    acc.wave();
+    __shared__ Acc<KIND> sh[kRB / kWave];
+    if ((threadIdx.x & (kWave - 1)) == 0) sh[threadIdx.x / kWave] = acc;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        Acc<KIND> t = sh[0];
+#pragma unroll
+        for (int i = 1; i < kRB / kWave; i++) t.combine(sh[i]);
+        if constexpr (KIND == NC_HIP_RED_SUM || KIND == NC_HIP_RED_MEAN) psum[o * P + p] = t.sum;
+        else parg[o * P + p] = t.a;
+    }
+}
+
+template <int KIND>
+__global__ __launch_bounds__(kRB) void k_rows_combine(const float *__restrict__ x, int64_t R, int P,
+                                                      const double *__restrict__ psum,
+                                                      const ArgState *__restrict__ parg, float *__restrict__ y,
+                                                      int32_t *__restrict__ arg, float scale) {
+    const int64_t o = blockIdx.x;
+    // fixed tree: each lane folds a strided subset of partials in order, then a fixed wave/block tree
+    Acc<KIND> acc;
+    acc.init();
+    for (int p = threadIdx.x; p < P; p += kRB) {
+        Acc<KIND> t;
+        t.init();
+        if constexpr (KIND == NC_HIP_RED_SUM || KIND == NC_HIP_RED_MEAN) t.sum = psum[o * P + p];
+        else t.a = parg[o * P + p];
+        acc.combine(t);
+    }
+    acc.wave();
+    __shared__ Acc<KIND> sh[kRB / kWave];
+    if ((threadIdx.x & (kWave - 1)) == 0) sh[threadIdx.x / kWave] = acc;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        Acc<KIND> t = sh[0];
+#pragma unroll
+        for (int i = 1; i < kRB / kWave; i++) t.combine(sh[i]);
+        emit<KIND>(t, x[o * R], scale, y, arg, o);
+    }
+}
+
+// --- inner > 1: lanes along inner, scan over R (optionally chunked) -------------------------------------
+template <int KIND>
+__global__ __launch_bounds__(kRB) void k_cols(const float *__restrict__ x, int64_t outer, int64_t R, int64_t inner,
+                                              int64_t chunk, int P, double *__restrict__ psum,
+                                              ArgState *__restrict__ parg, float *__restrict__ y,
+                                              int32_t *__restrict__ arg, float scale) {
+    const int64_t cols = outer * inner;
+    const int64_t total = cols * P;
+    for (int64_t t = (int64_t)blockIdx.x * kRB + threadIdx.x; t < total; t += (int64_t)gridDim.x * kRB) {
+        const int64_t c = t % cols;  // (o, i), i fastest
+        const int p = (int)(t / cols);
+        const int64_t o = c / inner, i = c % inner;
+        const float *base = x + o * R * inner + i;
+        const int64_t r0 = (int64_t)p * chunk, r1 = min(R, r0 + chunk);
+        Acc<KIND> acc;
+        acc.init();
+        for (int64_t r = r0; r < r1; r++) acc.push(base[r * inner], (int)r);
+        if (P == 1) {
+            emit<KIND>(acc, base[0], scale, y, arg, c);
+        } else {
+            if constexpr (KIND == NC_HIP_RED_SUM || KIND == NC_HIP_RED_MEAN) psum[(int64_t)p * cols + c] = acc.sum;
+            else parg[(int64_t)p * cols + c] = acc.a;
+        }
+    }
+}
+
+template <int KIND>
+__global__ __launch_bounds__(kRB) void k_cols_combine(const float *__restrict__ x, int64_t outer, int64_t R,
+                                                      int64_t inner, int P, const double *__restrict__ psum,
+                                                      const ArgState *__restrict__ parg, float *__restrict__ y,
+                                                      int32_t *__restrict__ arg, float scale) {
+    const int64_t cols = outer * inner;
+    for (int64_t c = (int64_t)blockIdx.x * kRB + threadIdx.x; c < cols; c += (int64_t)gridDim.x * kRB) {
+        Acc<KIND> acc;
+        acc.init();
+        for (int p = 0; p < P; p++) {
+            Acc<KIND> t;
+            t.init();
+            if constexpr (KIND == NC_HIP_RED_SUM || KIND == NC_HIP_RED_MEAN) t.sum = psum[(int64_t)p * cols + c];
+            else t.a = parg[(int64_t)p * cols + c];
+            acc.combine(t);
+        }
+        const int64_t o = c / inner, i = c % inner;
+        emit<KIND>(acc, x[o * R * inner + i], scale, y, arg, c);
+    }
+}
+
+__global__ void k_fill_f32(float *y, float v, int64_t n) {
+    for (int64_t i = (int64_t)blockIdx.x * kRB + threadIdx.x; i < n; i += (int64_t)gridDim.x * kRB) y[i] = v;
+}
+
+// Plan shared by the workspace query and the launch.
+struct RedShape {
+    int mode;  // 0 rows_wave, 1 rows_chunk, 2 cols
+    int64_t chunk;
+    int P;
+    size_t ws;
+};
+
+static RedShape plan(int kind, int64_t outer, int64_t R, int64_t inner) {
+    RedShape s{0, R, 1, 0};
+    const int64_t cus = num_cus();
+    const size_t elt = (kind == NC_HIP_RED_SUM || kind == NC_HIP_RED_MEAN) ? sizeof(double) : sizeof(ArgState);
+    if (inner == 1) {
+        if (outer >= cus * 16 || R <= 4096) {
+            s.mode = 0;
+            return s;
+        }
+        s.mode = 1;
+        int64_t want = (cus * 8 + outer - 1) / outer;       // workgroups per row
+        int64_t maxp = (R + 4 * 4 * kRB - 1) / (4 * 4 * kRB); // >= 4 vectors per lane
+        int64_t P = want < maxp ? want : maxp;
+        if (P < 1) P = 1;
+        if (P > 65535) P = 65535;
+        int64_t chunk = (R + P - 1) / P;
+        chunk = (chunk + 3) / 4 * 4;
+        s.chunk = chunk;
+        s.P = (int)((R + chunk - 1) / chunk);
+        s.ws = (size_t)outer * s.P * elt;
+        return s;
+    }
+    s.mode = 2;
+    const int64_t cols = outer * inner;
+    const int64_t target = cus * 2048;
+    int64_t P = cols >= target ? 1 : (target + cols - 1) / cols;
+    const int64_t maxp = (R + 31) / 32;
+    if (P > maxp) P = maxp;
+    if (P < 1) P = 1;
+    s.chunk = (R + P - 1) / P;
+    s.P = (int)((R + s.chunk - 1) / s.chunk);
+    s.ws = s.P > 1 ? (size_t)cols * s.P * elt : 0;
+    return s;
+}
+
+template <int KIND>
+static int launch(int64_t outer, int64_t R, int64_t inner, const float *x, float *y, int32_t *arg, void *ws,
+                  size_t ws_bytes, hipStream_t st) {
+    const float scale = KIND == NC_HIP_RED_MEAN ? 1.0f / (float)(R ? R : 1) : 1.0f;
+    const RedShape s = plan(KIND, outer, R, inner);
+    if (s.ws && (ws_bytes < s.ws || !ws))
+        return set_error(NC_HIP_ERR_WORKSPACE, "nc_hip_reduce_fwd: workspace of %zu bytes needed", s.ws);
+    double *psum = (double *)ws;
+    ArgState *parg = (ArgState *)ws;
+    if (s.mode == 0) {
+        const bool vec = R % 4 == 0 && aligned16(x);
+        const int64_t waves = outer;
+        const int64_t blocks64 = (waves + (kRB / kWave) - 1) / (kRB / kWave);
+        const unsigned grid = (unsigned)(blocks64 < num_cus() * 32 ? blocks64 : num_cus() * 32);
+        if (vec)
+            hipLaunchKernelGGL((k_rows_wave<KIND, true>), grid, kRB, 0, st, x, y, arg, outer, R, scale);
+        else
+            hipLaunchKernelGGL((k_rows_wave<KIND, false>), grid, kRB, 0, st, x, y, arg, outer, R, scale);
+    } else if (s.mode == 1) {
+        if (outer > 65535) return set_error(NC_HIP_ERR_ARG, "nc_hip_reduce_fwd: too many long rows");
+        const bool vec = R % 4 == 0 && aligned16(x);
+        hipLaunchKernelGGL(k_rows_chunk<KIND>, dim3(s.P, outer), kRB, 0, st, x, R, s.chunk, s.P, psum, parg, vec);
+        hipLaunchKernelGGL(k_rows_combine<KIND>, dim3(outer), kRB, 0, st, x, R, s.P, psum, parg, y, arg, scale);
+    } else {
+        const int64_t cols = outer * inner;
+        const int64_t items = cols * s.P;
+        const unsigned grid = stream_grid(items, kRB, 16);
+        hipLaunchKernelGGL(k_cols<KIND>, grid, kRB, 0, st, x, outer, R, inner, s.chunk, s.P, psum, parg, y, arg,
+                           scale);
+        if (s.P > 1)
+            hipLaunchKernelGGL(k_cols_combine<KIND>, stream_grid(cols, kRB, 16), kRB, 0, st, x, outer, R, inner, s.P,
+                               psum, parg, y, arg, scale);
+    }
+    return check_launch("nc_hip_reduce_fwd");
+}
+
+// --- backward ------------------------------------------------------------------------------------------
+// sum / mean: gi[o, r, i] (+)= scale * g[o, i].  inner == 1 follows the reference's `p[r] += v` with
+// v = scale * g (ops_reduce.c:136-138); inner > 1 its axpy (one fused rounding, :139).
+template <bool INNER1, bool ACC>
+__global__ __launch_bounds__(kRB) void k_red_bwd(const float *__restrict__ g, float *__restrict__ gi, int64_t n,
+                                                 uint32_t Rinner, IntDiv divRI, uint32_t inner, IntDiv divI,
+                                                 float scale) {
+    // n < 2^32 here; e = (o * R + r) * inner + i
+    const uint32_t step = gridDim.x * kRB;
+    for (uint32_t e = blockIdx.x * kRB + threadIdx.x; e < (uint32_t)n; e += step) {
+        const uint32_t o = divRI.div(e);
+        float gv;
+        if (INNER1) {
+            gv = g[o];
+            const float v = scale * gv;
+            gi[e] = (ACC ? gi[e] : 0.0f) + v;
+        } else {
+            const uint32_t i = e - divI.div(e) * inner;
+            gv = g[(int64_t)o * inner + i];
+            gi[e] = fma_(scale, gv, ACC ? gi[e] : 0.0f);
+        }
+    }
+}
+
+__global__ __launch_bounds__(kRB) void k_max_bwd(const float *__restrict__ g, const int32_t *__restrict__ arg,
+                                                 float *__restrict__ gi, int64_t outer, int64_t R, int64_t inner) {
+    const int64_t cols = outer * inner;
+    for (int64_t c = (int64_t)blockIdx.x * kRB + threadIdx.x; c < cols; c += (int64_t)gridDim.x * kRB) {
+        const int64_t o = c / inner, i = c % inner;
+        float *p = gi + (o * R + arg[c]) * inner + i;
+        *p = *p + g[c];
+    }
+}
+
+__global__ __launch_bounds__(kRB) void k_sum_i32(const int32_t *__restrict__ x, int32_t *__restrict__ y, int64_t outer,
+                                                 int64_t R, int64_t inner) {
+    const int64_t cols = outer * inner;
+    for (int64_t c = (int64_t)blockIdx.x * kRB + threadIdx.x; c < cols; c += (int64_t)gridDim.x * kRB) {
+        const int64_t o = c / inner, i = c % inner;
+        int64_t s = 0;
+        for (int64_t r = 0; r < R; r++) s += x[(o * R + r) * inner + i];
+        y[c] = (int32_t)s;
+    }
+}
+
+}  // namespace nchip
+
+using namespace nchip;
+
+extern "C" NC_HIP_API size_t nc_hip_reduce_workspace(int kind, int64_t outer, int64_t R, int64_t inner) {
+    if (outer <= 0 || R <= 0 || inner <= 0) return 0;
+    if (kind == NC_HIP_RED_ARGMAX) kind = NC_HIP_RED_MAX;
+    return plan(kind, outer, R, inner).ws;
+}
+
+extern "C" NC_HIP_API int nc_hip_reduce_fwd(int kind, int64_t outer, int64_t R, int64_t inner, const float *x,
+                                            float *y, int32_t *arg, void *ws, size_t ws_bytes, void *stream) {
+    if (outer < 0 || R < 0 || inner < 0) return set_error(NC_HIP_ERR_ARG, "nc_hip_reduce_fwd: negative size");
+    hipStream_t st = as_stream(stream);
+    const int64_t nout = outer * inner;
+    if (nout == 0) return NC_HIP_OK;
+    if (R == 0) {
+        if (kind == NC_HIP_RED_MAX || kind == NC_HIP_RED_ARGMAX)
+            return set_error(NC_HIP_ERR_ARG, "nc_hip_reduce_fwd: max of an empty axis");
+        hipLaunchKernelGGL(k_fill_f32, stream_grid(nout, kRB), kRB, 0, st, y,
+                           kind == NC_HIP_RED_MEAN ? __builtin_nanf("") : 0.0f, nout);
+        return check_launch("nc_hip_reduce_fwd");
+    }
+    if ((kind == NC_HIP_RED_SUM || kind == NC_HIP_RED_MEAN || kind == NC_HIP_RED_MAX) && !y)
+        return set_error(NC_HIP_ERR_ARG, "nc_hip_reduce_fwd: y is NULL");
+    if ((kind == NC_HIP_RED_MAX || kind == NC_HIP_RED_ARGMAX) && !arg)
+        return set_error(NC_HIP_ERR_ARG, "nc_hip_reduce_fwd: arg is NULL");
+    if (R > INT32_MAX && (kind == NC_HIP_RED_MAX || kind == NC_HIP_RED_ARGMAX))
+        return set_error(NC_HIP_ERR_ARG, "nc_hip_reduce_fwd: argmax over more than 2^31 elements");
+    switch (kind) {
+    case NC_HIP_RED_SUM: return launch<NC_HIP_RED_SUM>(outer, R, inner, x, y, arg, ws, ws_bytes, st);
+    case NC_HIP_RED_MEAN: return launch<NC_HIP_RED_MEAN>(outer, R, inner, x, y, arg, ws, ws_bytes, st);
+    case NC_HIP_RED_MAX: return launch<NC_HIP_RED_MAX>(outer, R, inner, x, y, arg, ws, ws_bytes, st);
+    case NC_HIP_RED_ARGMAX: return launch<NC_HIP_RED_ARGMAX>(outer, R, inner, x, y, arg, ws, ws_bytes, st);
+    default: return set_error(NC_HIP_ERR_ARG, "nc_hip_reduce_fwd: unknown kind %d", kind);
+    }
+}
+
+extern "C" NC_HIP_API int nc_hip_reduce_bwd(int kind, int64_t outer, int64_t R, int64_t inner, const float *g,
+                                            const int32_t *arg, float *gi, int accumulate, void *stream) {
+    hipStream_t st = as_stream(stream);
+    const int64_t n = outer * R * inner;
+    if (n <= 0) return NC_HIP_OK;
+    if (kind == NC_HIP_RED_MAX) {
+        if (!accumulate) hipLaunchKernelGGL(k_fill_f32, stream_grid(n, kRB, 16), kRB, 0, st, gi, 0.0f, n);
+        hipLaunchKernelGGL(k_max_bwd, stream_grid(outer * inner, kRB, 16), kRB, 0, st, g, arg, gi, outer, R, inner);
+        return check_launch("nc_hip_reduce_bwd");
+    }
+    if (kind != NC_HIP_RED_SUM && kind != NC_HIP_RED_MEAN)
+        return set_error(NC_HIP_ERR_ARG, "nc_hip_reduce_bwd: kind %d has no gradient", kind);
+    if (n >= (int64_t)UINT32_MAX) return set_error(NC_HIP_ERR_ARG, "nc_hip_reduce_bwd: 2^32 or more elements");
+    const float scale = kind == NC_HIP_RED_MEAN ? 1.0f / (float)(R ? R : 1) : 1.0f;
+    const uint32_t RI = (uint32_t)(R * inner);
+    const IntDiv dRI(RI), dI((uint32_t)inner);
+    const unsigned grid = stream_grid(n, kRB, 16);
+    if (inner == 1) {
+        if (accumulate)
+            hipLaunchKernelGGL((k_red_bwd<true, true>), grid, kRB, 0, st, g, gi, n, RI, dRI, (uint32_t)inner, dI, scale);
+        else
+            hipLaunchKernelGGL((k_red_bwd<true, false>), grid, kRB, 0, st, g, gi, n, RI, dRI, (uint32_t)inner, dI, scale);
+    } else {
+        if (accumulate)
+            hipLaunchKernelGGL((k_red_bwd<false, true>), grid, kRB, 0, st, g, gi, n, RI, dRI, (uint32_t)inner, dI, scale);
+        else
+            hipLaunchKernelGGL((k_red_bwd<false, false>), grid, kRB, 0, st, g, gi, n, RI, dRI, (uint32_t)inner, dI, scale);
+    }
+    return check_launch("nc_hip_reduce_bwd");
+}
+
+extern "C" NC_HIP_API int nc_hip_reduce_sum_i32(int64_t outer, int64_t R, int64_t inner, const int32_t *x,
+                                                int32_t *y, void *stream) {
+    const int64_t cols = outer * inner;
+    if (cols <= 0) return NC_HIP_OK;
+    hipLaunchKernelGGL(k_sum_i32, stream_grid(cols, kRB, 16), kRB, 0, as_stream(stream), x, y, outer, R, inner);
+    return check_launch("nc_hip_reduce_sum_i32");
+}

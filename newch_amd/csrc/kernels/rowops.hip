@@ -1,0 +1,605 @@
+// Row kernels: softmax / log_softmax (ops_nn.c:22-71) and LayerNorm (ops_nn.c:434-522).
+//
+// A row of up to 4096 floats is held in registers by one wave64 (VPL 128-bit vectors per lane),
+// so each op reads its inputs from HBM exactly once and writes its outputs once; the row
+// statistics (max, sums) are wave64 shuffle reductions.  Longer or unaligned rows take a
+// workgroup-per-row path that re-reads the row from global memory (L2-resident) per pass.
+//
+// Per element the fp32 expressions are the reference's (exp8 for the softmax exponentials, the
+// same association everywhere), so given the row statistics each output is the reference's
+// bit pattern; the statistics are accumulated in fp64 (the reference sums in fp32 for softmax and
+// fp64 for LayerNorm), which keeps every result within a few ulp of it.
+#include "common.hpp"
+
+namespace nchip {
+
+constexpr int kRowB = 256;             // 4 waves per workgroup, one row per wave
+constexpr int kWavesPerBlock = kRowB / kWave;
+
+// max of a row with the reference's scan semantics (ops_nn.c:23-25): NaN at index 0 wins, later
+// NaNs are skipped (fmaxf ignores them, order-free), otherwise the plain maximum.
+__device__ __forceinline__ float row_max_finish(float m_nonnan, float x0) { return x0 != x0 ? x0 : m_nonnan; }
+
+// ------------------------------------------------------------------------------------------------
+// softmax, register-resident rows
+// ------------------------------------------------------------------------------------------------
+template <int VPL, bool LOG>
+__global__ __launch_bounds__(kRowB) void k_softmax_fwd_reg(const float *__restrict__ x, float *__restrict__ y,
+                                                           int64_t rows, int C) {
+    const int lane = threadIdx.x & (kWave - 1);
+    const int nv = C / 4;
+    for (int64_t r = ((int64_t)blockIdx.x * kRowB + threadIdx.x) / kWave; r < rows;
+         r += (int64_t)gridDim.x * kWavesPerBlock) {
+        const f4 *xr = (const f4 *)(x + r * C);
+        f4 v[VPL];
+        float m = -__builtin_inff();
+#pragma unroll
+        for (int k = 0; k < VPL; k++) {
+            const int j = lane + k * kWave;
+            if (j < nv) {
+                v[k] = __builtin_nontemporal_load(xr + j);
+                m = __builtin_fmaxf(m, __builtin_fmaxf(__builtin_fmaxf(v[k].x, v[k].y), __builtin_fmaxf(v[k].z, v[k].w)));
+            }
+        }
+        m = wave_max_nan_skip(m);
+        m = row_max_finish(m, x[r * C]);
+        double s = 0.0;
+#pragma unroll
+        for (int k = 0; k < VPL; k++) {
+            const int j = lane + k * kWave;
+            if (j < nv) {
+                f4 e;
+                e.x = exp8(v[k].x - m);
+                e.y = exp8(v[k].y - m);
+                e.z = exp8(v[k].z - m);
+                e.w = exp8(v[k].w - m);
+                s += ((double)e.x + (double)e.y) + ((double)e.z + (double)e.w);
+                if (!LOG) v[k] = e;
+            }
+        }
+        const float sf = (float)wave_sum(s);
+        f4 *yr = (f4 *)(y + r * C);
+        if (LOG) {
+            const float ls = logf(sf);
+#pragma unroll
+            for (int k = 0; k < VPL; k++) {
+                const int j = lane + k * kWave;
+                if (j < nv) {
+                    f4 o;
+                    o.x = (v[k].x - m) - ls;
+                    o.y = (v[k].y - m) - ls;
+                    o.z = (v[k].z - m) - ls;
+                    o.w = (v[k].w - m) - ls;
+                    __builtin_nontemporal_store(o, yr + j);
+                }
+            }
+        } else {
+            const float inv = 1.0f / sf;
+#pragma unroll
+            for (int k = 0; k < VPL; k++) {
+                const int j = lane + k * kWave;
+                if (j < nv) {
+                    f4 o;
+                    o.x = inv * v[k].x;
+                    o.y = inv * v[k].y;
+                    o.z = inv * v[k].z;
+                    o.w = inv * v[k].w;
+                    __builtin_nontemporal_store(o, yr + j);
+                }
+            }
+        }
+    }
+}
+
+template <int VPL, bool LOG, bool ACC>
+__global__ __launch_bounds__(kRowB) void k_softmax_bwd_reg(const float *__restrict__ y, const float *__restrict__ g,
+                                                           float *__restrict__ gi, int64_t rows, int C) {
+    const int lane = threadIdx.x & (kWave - 1);
+    const int nv = C / 4;
+    for (int64_t r = ((int64_t)blockIdx.x * kRowB + threadIdx.x) / kWave; r < rows;
+         r += (int64_t)gridDim.x * kWavesPerBlock) {
+        const f4 *yr = (const f4 *)(y + r * C), *gr = (const f4 *)(g + r * C);
+        f4 *orow = (f4 *)(gi + r * C);
+        f4 vy[VPL], vg[VPL];
+        double s = 0.0;
+#pragma unroll
+        for (int k = 0; k < VPL; k++) {
+            const int j = lane + k * kWave;
+            if (j < nv) {
+                vy[k] = __builtin_nontemporal_load(yr + j);
+                vg[k] = __builtin_nontemporal_load(gr + j);
+                if (LOG) s += ((double)vg[k].x + (double)vg[k].y) + ((double)vg[k].z + (double)vg[k].w);
+                else
+                    s += ((double)(vg[k].x * vy[k].x) + (double)(vg[k].y * vy[k].y)) +
+                         ((double)(vg[k].z * vy[k].z) + (double)(vg[k].w * vy[k].w));
+            }
+        }
+        const float sf = (float)wave_sum(s);
+#pragma unroll
+        for (int k = 0; k < VPL; k++) {
+            const int j = lane + k * kWave;
+            if (j < nv) {
+                f4 o = ACC ? __builtin_nontemporal_load(orow + j) : f4{0.f, 0.f, 0.f, 0.f};
+                if (LOG) {
+                    o.x = o.x + (vg[k].x - expf(vy[k].x) * sf);
+                    o.y = o.y + (vg[k].y - expf(vy[k].y) * sf);
+                    o.z = o.z + (vg[k].z - expf(vy[k].z) * sf);
+                    o.w = o.w + (vg[k].w - expf(vy[k].w) * sf);
+                } else {
+                    o.x = o.x + vy[k].x * (vg[k].x - sf);
+                    o.y = o.y + vy[k].y * (vg[k].y - sf);
+                    o.z = o.z + vy[k].z * (vg[k].z - sf);
+                    o.w = o.w + vy[k].w * (vg[k].w - sf);
+                }
+                __builtin_nontemporal_store(o, orow + j);
+            }
+        }
+    }
+}
+
+// block-wide reductions for the workgroup-per-row paths
+__device__ __forceinline__ double block_sum(double v, double *sh) {
+    v = wave_sum(v);
+    __syncthreads();
+    if ((threadIdx.x & (kWave - 1)) == 0) sh[threadIdx.x / kWave] = v;
+    __syncthreads();
+    double t = 0.0;
+#pragma unroll
+    for (int i = 0; i < kWavesPerBlock; i++) t += sh[i];
+    return t;
+}
+__device__ __forceinline__ float block_max(float v, float *sh) {
+    v = wave_max_nan_skip(v);
+    __syncthreads();
+    if ((threadIdx.x & (kWave - 1)) == 0) sh[threadIdx.x / kWave] = v;
+    __syncthreads();
+    float t = sh[0];
+#pragma unroll
+    for (int i = 1; i < kWavesPerBlock; i++) t = __builtin_fmaxf(t, sh[i]);
+    return t;
+}
+
+template <bool LOG>
+__global__ __launch_bounds__(kRowB) void k_softmax_fwd_blk(const float *__restrict__ x, float *__restrict__ y,
+                                                           int64_t rows, int64_t C) {
+    __shared__ double shd[kWavesPerBlock];
+    __shared__ float shf[kWavesPerBlock];
+    for (int64_t r = blockIdx.x; r < rows; r += gridDim.x) {
+        const float *xr = x + r * C;
+        float *yr = y + r * C;
+        float m = -__builtin_inff();
+        for (int64_t c = threadIdx.x; c < C; c += kRowB) m = __builtin_fmaxf(m, xr[c]);
+        m = row_max_finish(block_max(m, shf), xr[0]);
+        double s = 0.0;
+        for (int64_t c = threadIdx.x; c < C; c += kRowB) s += (double)exp8(xr[c] - m);
+        const float sf = (float)block_sum(s, shd);
+        if (LOG) {
+            const float ls = logf(sf);
+            for (int64_t c = threadIdx.x; c < C; c += kRowB) yr[c] = (xr[c] - m) - ls;
+        } else {
+            const float inv = 1.0f / sf;
+            for (int64_t c = threadIdx.x; c < C; c += kRowB) yr[c] = inv * exp8(xr[c] - m);
+        }
+        __syncthreads();
+    }
+}
+
+template <bool LOG, bool ACC>
+__global__ __launch_bounds__(kRowB) void k_softmax_bwd_blk(const float *__restrict__ y, const float *__restrict__ g,
+                                                           float *__restrict__ gi, int64_t rows, int64_t C) {
+    __shared__ double shd[kWavesPerBlock];
+    for (int64_t r = blockIdx.x; r < rows; r += gridDim.x) {
+        const float *yr = y + r * C, *gr = g + r * C;
+        float *o = gi + r * C;
+        double s = 0.0;
+        for (int64_t c = threadIdx.x; c < C; c += kRowB) s += LOG ? (double)gr[c] : (double)(gr[c] * yr[c]);
+        const float sf = (float)block_sum(s, shd);
+        for (int64_t c = threadIdx.x; c < C; c += kRowB) {
+            const float old = ACC ? o[c] : 0.0f;
+            o[c] = LOG ? old + (gr[c] - expf(yr[c]) * sf) : old + yr[c] * (gr[c] - sf);
+        }
+        __syncthreads();
+    }
+}
+
+// ------------------------------------------------------------------------------------------------
+// LayerNorm
+// ------------------------------------------------------------------------------------------------
+template <int VPL>
+__global__ __launch_bounds__(kRowB) void k_ln_fwd_reg(const float *__restrict__ x, const float *__restrict__ w,
+                                                      const float *__restrict__ b, float eps, float *__restrict__ y,
+                                                      float *__restrict__ stats, int64_t rows, int D) {
+    const int lane = threadIdx.x & (kWave - 1);
+    const int nv = D / 4;
+    for (int64_t r = ((int64_t)blockIdx.x * kRowB + threadIdx.x) / kWave; r < rows;
+         r += (int64_t)gridDim.x * kWavesPerBlock) {
+        const f4 *xr = (const f4 *)(x + r * D);
+        f4 v[VPL];
+        double s = 0.0;
+#pragma unroll
+        for (int k = 0; k < VPL; k++) {
+            const int j = lane + k * kWave;
+            if (j < nv) {
+                v[k] = __builtin_nontemporal_load(xr + j);
+                s += ((double)v[k].x + (double)v[k].y) + ((double)v[k].z + (double)v[k].w);
+            }
+        }
+        const double mean = wave_sum(s) / (double)D;
+        double ss = 0.0;
+#pragma unroll
+        for (int k = 0; k < VPL; k++) {
+            const int j = lane + k * kWave;
+            if (j < nv) {
+                const double a = (double)v[k].x - mean, bb = (double)v[k].y - mean, c = (double)v[k].z - mean,
+                             d = (double)v[k].w - mean;
+                ss += (a * a + bb * bb) + (c * c + d * d);
+            }
+        }
+        ss = wave_sum(ss);
+        const float rstd = (float)(1.0 / sqrt(ss / (double)D + (double)eps));
+        const float mf = (float)mean;
+        if (lane == 0) {
+            stats[2 * r] = mf;
+            stats[2 * r + 1] = rstd;
+        }
+        f4 *yr = (f4 *)(y + r * D);
+#pragma unroll
+        for (int k = 0; k < VPL; k++) {
+            const int j = lane + k * kWave;
+            if (j < nv) {
+                const f4 ww = w ? ((const f4 *)w)[j] : f4{0.f, 0.f, 0.f, 0.f};
+                const f4 bv = b ? ((const f4 *)b)[j] : f4{0.f, 0.f, 0.f, 0.f};
+                f4 o;
+                float t;
+                t = (v[k].x - mf) * rstd; o.x = (w ? t * ww.x : t) + bv.x;
+                t = (v[k].y - mf) * rstd; o.y = (w ? t * ww.y : t) + bv.y;
+                t = (v[k].z - mf) * rstd; o.z = (w ? t * ww.z : t) + bv.z;
+                t = (v[k].w - mf) * rstd; o.w = (w ? t * ww.w : t) + bv.w;
+                __builtin_nontemporal_store(o, yr + j);
+            }
+        }
+    }
+}
+
+__global__ __launch_bounds__(kRowB) void k_ln_fwd_blk(const float *__restrict__ x, const float *__restrict__ w,
+                                                      const float *__restrict__ b, float eps, float *__restrict__ y,
+                                                      float *__restrict__ stats, int64_t rows, int64_t D) {
+    __shared__ double shd[kWavesPerBlock];
+    for (int64_t r = blockIdx.x; r < rows; r += gridDim.x) {
+        const float *xr = x + r * D;
+        double s = 0.0;
+        for (int64_t i = threadIdx.x; i < D; i += kRowB) s += (double)xr[i];
+        const double mean = block_sum(s, shd) / (double)D;
+        double ss = 0.0;
+        for (int64_t i = threadIdx.x; i < D; i += kRowB) {
+            const double d = (double)xr[i] - mean;
+            ss += d * d;
+        }
+        ss = block_sum(ss, shd);
+        const float rstd = (float)(1.0 / sqrt(ss / (double)D + (double)eps));
+        const float mf = (float)mean;
+        if (threadIdx.x == 0) {
+            stats[2 * r] = mf;
+            stats[2 * r + 1] = rstd;
+        }
+        for (int64_t i = threadIdx.x; i < D; i += kRowB) {
+            const float t = (xr[i] - mf) * rstd;
+            y[r * D + i] = (w ? t * w[i] : t) + (b ? b[i] : 0.0f);
+        }
+        __syncthreads();
+    }
+}
+
+// Backward, register rows.  Each workgroup owns a contiguous range of rows; its 4 waves take rows
+// round-robin, accumulate the gw / gb column partials of their rows in registers, combine them in
+// LDS in wave order and write one fp64 partial per workgroup; k_ln_cols_combine adds the workgroup
+// partials in workgroup order.
+template <int VPL, bool ACC>
+__global__ __launch_bounds__(kRowB) void k_ln_bwd_reg(const float *__restrict__ x, const float *__restrict__ w,
+                                                      const float *__restrict__ stats, const float *__restrict__ g,
+                                                      float *__restrict__ gx, double *__restrict__ part, int64_t rows,
+                                                      int D, int64_t rows_per_block) {
+    const int lane = threadIdx.x & (kWave - 1);
+    const int wv = threadIdx.x / kWave;
+    const int nv = D / 4;
+    const int64_t r0 = (int64_t)blockIdx.x * rows_per_block;
+    const int64_t r1 = min(rows, r0 + rows_per_block);
+    f4 aw[VPL], ab[VPL];
+#pragma unroll
+    for (int k = 0; k < VPL; k++) aw[k] = ab[k] = f4{0.f, 0.f, 0.f, 0.f};
+    for (int64_t r = r0 + wv; r < r1; r += kWavesPerBlock) {
+        const f4 *xr = (const f4 *)(x + r * D), *gr = (const f4 *)(g + r * D);
+        const float mean = stats[2 * r], rstd = stats[2 * r + 1];
+        f4 xh[VPL], gg[VPL], gw4[VPL];
+        double sg = 0.0, sgx = 0.0;
+#pragma unroll
+        for (int k = 0; k < VPL; k++) {
+            const int j = lane + k * kWave;
+            if (j < nv) {
+                const f4 xv = __builtin_nontemporal_load(xr + j);
+                gg[k] = __builtin_nontemporal_load(gr + j);
+                const f4 ww = w ? ((const f4 *)w)[j] : f4{1.f, 1.f, 1.f, 1.f};
+                xh[k].x = (xv.x - mean) * rstd;
+                xh[k].y = (xv.y - mean) * rstd;
+                xh[k].z = (xv.z - mean) * rstd;
+                xh[k].w = (xv.w - mean) * rstd;
+                gw4[k].x = w ? gg[k].x * ww.x : gg[k].x;
+                gw4[k].y = w ? gg[k].y * ww.y : gg[k].y;
+                gw4[k].z = w ? gg[k].z * ww.z : gg[k].z;
+                gw4[k].w = w ? gg[k].w * ww.w : gg[k].w;
+                sg += ((double)gw4[k].x + (double)gw4[k].y) + ((double)gw4[k].z + (double)gw4[k].w);
+                sgx += ((double)(gw4[k].x * xh[k].x) + (double)(gw4[k].y * xh[k].y)) +
+                       ((double)(gw4[k].z * xh[k].z) + (double)(gw4[k].w * xh[k].w));
+                aw[k].x += gg[k].x * xh[k].x;
+                aw[k].y += gg[k].y * xh[k].y;
+                aw[k].z += gg[k].z * xh[k].z;
+                aw[k].w += gg[k].w * xh[k].w;
+                ab[k] += gg[k];
+            }
+        }
+        if (gx) {
+            sg = wave_sum(sg);
+            sgx = wave_sum(sgx);
+            const float mg = (float)(sg / (double)D), mgx = (float)(sgx / (double)D);
+            f4 *dx = (f4 *)(gx + r * D);
+#pragma unroll
+            for (int k = 0; k < VPL; k++) {
+                const int j = lane + k * kWave;
+                if (j < nv) {
+                    f4 o = ACC ? __builtin_nontemporal_load(dx + j) : f4{0.f, 0.f, 0.f, 0.f};
+                    o.x = o.x + rstd * ((gw4[k].x - mg) - xh[k].x * mgx);
+                    o.y = o.y + rstd * ((gw4[k].y - mg) - xh[k].y * mgx);
+                    o.z = o.z + rstd * ((gw4[k].z - mg) - xh[k].z * mgx);
+                    o.w = o.w + rstd * ((gw4[k].w - mg) - xh[k].w * mgx);
+                    __builtin_nontemporal_store(o, dx + j);
+                }
+            }
+        }
+    }
+    if (!part) return;
+    // combine the 4 waves' column partials in LDS (wave order), write the workgroup partial
+    extern __shared__ double lds[];  // [2][D]
+    for (int i = threadIdx.x; i < 2 * D; i += kRowB) lds[i] = 0.0;
+    __syncthreads();
+    for (int wsel = 0; wsel < kWavesPerBlock; wsel++) {
+        if (wv == wsel) {
+#pragma unroll
+            for (int k = 0; k < VPL; k++) {
+                const int j = lane + k * kWave;
+                if (j < nv) {
+                    lds[4 * j + 0] += aw[k].x;
+                    lds[4 * j + 1] += aw[k].y;
+                    lds[4 * j + 2] += aw[k].z;
+                    lds[4 * j + 3] += aw[k].w;
+                    lds[D + 4 * j + 0] += ab[k].x;
+                    lds[D + 4 * j + 1] += ab[k].y;
+                    lds[D + 4 * j + 2] += ab[k].z;
+                    lds[D + 4 * j + 3] += ab[k].w;
+                }
+            }
+        }
+        __syncthreads();
+    }
+    double *out = part + (size_t)blockIdx.x * 2 * D;
+    for (int i = threadIdx.x; i < 2 * D; i += kRowB) out[i] = lds[i];
+}
+
+// Generic backward: one workgroup per row for gx, and column partials for gw/gb.
+template <bool ACC>
+__global__ __launch_bounds__(kRowB) void k_ln_bwd_blk(const float *__restrict__ x, const float *__restrict__ w,
+                                                      const float *__restrict__ stats, const float *__restrict__ g,
+                                                      float *__restrict__ gx, int64_t rows, int64_t D) {
+    __shared__ double shd[kWavesPerBlock];
+    for (int64_t r = blockIdx.x; r < rows; r += gridDim.x) {
+        const float *xr = x + r * D, *gr = g + r * D;
+        const float mean = stats[2 * r], rstd = stats[2 * r + 1];
+        double sg = 0.0, sgx = 0.0;
+        for (int64_t i = threadIdx.x; i < D; i += kRowB) {
+            const float xhat = (xr[i] - mean) * rstd, gi = w ? gr[i] * w[i] : gr[i];
+            sg += (double)gi;
+            sgx += (double)(gi * xhat);
+        }
+        sg = block_sum(sg, shd);
+        sgx = block_sum(sgx, shd);
+        const float mg = (float)(sg / (double)D), mgx = (float)(sgx / (double)D);
+        for (int64_t i = threadIdx.x; i < D; i += kRowB) {
+            const float xhat = (xr[i] - mean) * rstd, gi = w ? gr[i] * w[i] : gr[i];
+            const float old = ACC ? gx[r * D + i] : 0.0f;
+            gx[r * D + i] = old + rstd * ((gi - mg) - xhat * mgx);
+        }
+        __syncthreads();
+    }
+}
+
+// column partials for the generic path: part[p][2][D] over row chunk p
+__global__ __launch_bounds__(kRowB) void k_ln_cols_part(const float *__restrict__ x, const float *__restrict__ stats,
+                                                        const float *__restrict__ g, double *__restrict__ part,
+                                                        int64_t rows, int64_t D, int64_t chunk, int P) {
+    const int64_t total = D * P;
+    for (int64_t t = (int64_t)blockIdx.x * kRowB + threadIdx.x; t < total; t += (int64_t)gridDim.x * kRowB) {
+        const int64_t i = t % D;
+        const int p = (int)(t / D);
+        const int64_t r0 = (int64_t)p * chunk, r1 = min(rows, r0 + chunk);
+        double sw = 0.0, sb = 0.0;
+        for (int64_t r = r0; r < r1; r++) {
+            const float xhat = (x[r * D + i] - stats[2 * r]) * stats[2 * r + 1];
+            const float gv = g[r * D + i];
+            sw += (double)(gv * xhat);
+            sb += (double)gv;
+        }
+        part[(size_t)p * 2 * D + i] = sw;
+        part[(size_t)p * 2 * D + D + i] = sb;
+    }
+}
+
+__global__ __launch_bounds__(kRowB) void k_ln_cols_combine(const double *__restrict__ part, float *__restrict__ gw,
+                                                           float *__restrict__ gb, int64_t D, int P) {
+    for (int64_t i = (int64_t)blockIdx.x * kRowB + threadIdx.x; i < D; i += (int64_t)gridDim.x * kRowB) {
+        double sw = 0.0, sb = 0.0;
+        for (int p = 0; p < P; p++) {
+            sw += part[(size_t)p * 2 * D + i];
+            sb += part[(size_t)p * 2 * D + D + i];
+        }
+        if (gw) gw[i] = (float)((double)gw[i] + sw);
+        if (gb) gb[i] = (float)((double)gb[i] + sb);
+    }
+}
+
+static int vpl_for(int64_t C) {
+    const int64_t nv = C / 4;
+    if (nv <= 64) return 1;
+    if (nv <= 128) return 2;
+    if (nv <= 256) return 4;
+    if (nv <= 512) return 8;
+    if (nv <= 1024) return 16;
+    return 0;
+}
+
+static unsigned rows_grid(int64_t rows) {
+    const int64_t blocks = (rows + kWavesPerBlock - 1) / kWavesPerBlock;
+    const int64_t cap = (int64_t)num_cus() * 16;
+    return (unsigned)(blocks < cap ? blocks : cap);
+}
+
+#define NC_VPL_SWITCH(V, CALL)                      \
+    switch (V) {                                    \
+    case 1: { constexpr int VP = 1; CALL; } break;  \
+    case 2: { constexpr int VP = 2; CALL; } break;  \
+    case 4: { constexpr int VP = 4; CALL; } break;  \
+    case 8: { constexpr int VP = 8; CALL; } break;  \
+    default: { constexpr int VP = 16; CALL; } break; \
+    }
+
+// LayerNorm backward plan (shared by the workspace query and the launch)
+struct LnPlan {
+    bool reg;
+    int vpl;
+    int64_t blocks, rows_per_block;  // register path
+    int64_t chunk;
+    int P;                           // generic path
+    size_t ws;
+};
+
+static LnPlan ln_plan(int64_t rows, int64_t D, bool aligned) {
+    LnPlan p{};
+    p.vpl = (D % 4 == 0 && aligned) ? vpl_for(D) : 0;
+    p.reg = p.vpl != 0;
+    if (p.reg) {
+        int64_t want = (int64_t)num_cus() * 2;
+        int64_t rpb = (rows + want - 1) / want;
+        if (rpb < kWavesPerBlock) rpb = kWavesPerBlock;
+        p.rows_per_block = rpb;
+        p.blocks = (rows + rpb - 1) / rpb;
+        p.ws = (size_t)p.blocks * 2 * D * sizeof(double);
+    } else {
+        const int64_t target = (int64_t)num_cus() * 1024;
+        int64_t P = (target + D - 1) / D;
+        if (P > rows) P = rows;
+        if (P < 1) P = 1;
+        p.chunk = (rows + P - 1) / P;
+        p.P = (int)((rows + p.chunk - 1) / p.chunk);
+        p.ws = (size_t)p.P * 2 * D * sizeof(double);
+    }
+    return p;
+}
+
+}  // namespace nchip
+
+using namespace nchip;
+
+extern "C" NC_HIP_API int nc_hip_softmax_fwd(int log_form, int64_t rows, int64_t C, const float *x, float *y,
+                                             void *stream) {
+    if (rows < 0 || C < 0) return set_error(NC_HIP_ERR_ARG, "nc_hip_softmax_fwd: negative size");
+    if (rows == 0 || C == 0) return NC_HIP_OK;
+    hipStream_t st = as_stream(stream);
+    const int v = (C % 4 == 0 && aligned16(x) && aligned16(y)) ? vpl_for(C) : 0;
+    if (v) {
+        if (log_form) NC_VPL_SWITCH(v, hipLaunchKernelGGL((k_softmax_fwd_reg<VP, true>), rows_grid(rows), kRowB, 0, st, x, y, rows, (int)C))
+        else NC_VPL_SWITCH(v, hipLaunchKernelGGL((k_softmax_fwd_reg<VP, false>), rows_grid(rows), kRowB, 0, st, x, y, rows, (int)C))
+    } else {
+        const unsigned grid = (unsigned)(rows < num_cus() * 8 ? rows : num_cus() * 8);
+        if (log_form) hipLaunchKernelGGL(k_softmax_fwd_blk<true>, grid, kRowB, 0, st, x, y, rows, C);
+        else hipLaunchKernelGGL(k_softmax_fwd_blk<false>, grid, kRowB, 0, st, x, y, rows, C);
+    }
+    return check_launch("nc_hip_softmax_fwd");
+}
+
+extern "C" NC_HIP_API int nc_hip_softmax_bwd(int log_form, int64_t rows, int64_t C, const float *y, const float *g,
+                                             float *gi, int accumulate, void *stream) {
+    if (rows < 0 || C < 0) return set_error(NC_HIP_ERR_ARG, "nc_hip_softmax_bwd: negative size");
+    if (rows == 0 || C == 0) return NC_HIP_OK;
+    hipStream_t st = as_stream(stream);
+    const int v = (C % 4 == 0 && aligned16(y) && aligned16(g) && aligned16(gi)) ? vpl_for(C) : 0;
+    const unsigned rg = rows_grid(rows);
+    if (v) {
+        if (log_form && accumulate) NC_VPL_SWITCH(v, hipLaunchKernelGGL((k_softmax_bwd_reg<VP, true, true>), rg, kRowB, 0, st, y, g, gi, rows, (int)C))
+        else if (log_form) NC_VPL_SWITCH(v, hipLaunchKernelGGL((k_softmax_bwd_reg<VP, true, false>), rg, kRowB, 0, st, y, g, gi, rows, (int)C))
+        else if (accumulate) NC_VPL_SWITCH(v, hipLaunchKernelGGL((k_softmax_bwd_reg<VP, false, true>), rg, kRowB, 0, st, y, g, gi, rows, (int)C))
+        else NC_VPL_SWITCH(v, hipLaunchKernelGGL((k_softmax_bwd_reg<VP, false, false>), rg, kRowB, 0, st, y, g, gi, rows, (int)C))
+    } else {
+        const unsigned grid = (unsigned)(rows < num_cus() * 8 ? rows : num_cus() * 8);
+        if (log_form && accumulate) hipLaunchKernelGGL((k_softmax_bwd_blk<true, true>), grid, kRowB, 0, st, y, g, gi, rows, C);
+        else if (log_form) hipLaunchKernelGGL((k_softmax_bwd_blk<true, false>), grid, kRowB, 0, st, y, g, gi, rows, C);
+        else if (accumulate) hipLaunchKernelGGL((k_softmax_bwd_blk<false, true>), grid, kRowB, 0, st, y, g, gi, rows, C);
+        else hipLaunchKernelGGL((k_softmax_bwd_blk<false, false>), grid, kRowB, 0, st, y, g, gi, rows, C);
+    }
+    return check_launch("nc_hip_softmax_bwd");
+}
+
+extern "C" NC_HIP_API int nc_hip_layer_norm_fwd(int64_t rows, int64_t D, const float *x, const float *w,
+                                                const float *b, float eps, float *y, float *stats, void *stream) {
+    if (rows < 0 || D <= 0) return set_error(NC_HIP_ERR_ARG, "nc_hip_layer_norm_fwd: bad size");
+    if (rows == 0) return NC_HIP_OK;
+    hipStream_t st = as_stream(stream);
+    const bool al = aligned16(x) && aligned16(y) && (!w || aligned16(w)) && (!b || aligned16(b));
+    const int v = (D % 4 == 0 && al) ? vpl_for(D) : 0;
+    if (v) {
+        NC_VPL_SWITCH(v, hipLaunchKernelGGL(k_ln_fwd_reg<VP>, rows_grid(rows), kRowB, 0, st, x, w, b, eps, y, stats, rows, (int)D))
+    } else {
+        const unsigned grid = (unsigned)(rows < num_cus() * 8 ? rows : num_cus() * 8);
+        hipLaunchKernelGGL(k_ln_fwd_blk, grid, kRowB, 0, st, x, w, b, eps, y, stats, rows, D);
+    }
+    return check_launch("nc_hip_layer_norm_fwd");
+}
+
+extern "C" NC_HIP_API size_t nc_hip_layer_norm_bwd_workspace(int64_t rows, int64_t D) {
+    if (rows <= 0 || D <= 0) return 0;
+    return ln_plan(rows, D, true).ws > ln_plan(rows, D, false).ws ? ln_plan(rows, D, true).ws
+                                                                    : ln_plan(rows, D, false).ws;
+}
+
+extern "C" NC_HIP_API int nc_hip_layer_norm_bwd(int64_t rows, int64_t D, const float *x, const float *w,
+                                                const float *stats, const float *g, float *gx, float *gw, float *gb,
+                                                int accumulate, void *ws, size_t ws_bytes, void *stream) {
+    if (rows < 0 || D <= 0) return set_error(NC_HIP_ERR_ARG, "nc_hip_layer_norm_bwd: bad size");
+    if (rows == 0) return NC_HIP_OK;
+    hipStream_t st = as_stream(stream);
+    const bool al = aligned16(x) && aligned16(g) && (!gx || aligned16(gx)) && (!w || aligned16(w));
+    const LnPlan p = ln_plan(rows, D, al);
+    const bool cols = gw || gb;
+    if (cols && (ws_bytes < p.ws || !ws))
+        return set_error(NC_HIP_ERR_WORKSPACE, "nc_hip_layer_norm_bwd: workspace of %zu bytes needed", p.ws);
+    double *part = cols ? (double *)ws : nullptr;
+    if (p.reg) {
+        const size_t lds = cols ? (size_t)2 * D * sizeof(double) : 0;
+        if (lds > 65536) return set_error(NC_HIP_ERR_ARG, "nc_hip_layer_norm_bwd: D too large for LDS combine");
+        if (accumulate)
+            NC_VPL_SWITCH(p.vpl, hipLaunchKernelGGL((k_ln_bwd_reg<VP, true>), dim3(p.blocks), kRowB, lds, st, x, w, stats, g, gx, part, rows, (int)D, p.rows_per_block))
+        else
+            NC_VPL_SWITCH(p.vpl, hipLaunchKernelGGL((k_ln_bwd_reg<VP, false>), dim3(p.blocks), kRowB, lds, st, x, w, stats, g, gx, part, rows, (int)D, p.rows_per_block))
+        if (cols)
+            hipLaunchKernelGGL(k_ln_cols_combine, stream_grid(D, kRowB), kRowB, 0, st, part, gw, gb, D, (int)p.blocks);
+    } else {
+        const unsigned grid = (unsigned)(rows < num_cus() * 8 ? rows : num_cus() * 8);
+        if (gx) {
+            if (accumulate) hipLaunchKernelGGL(k_ln_bwd_blk<true>, grid, kRowB, 0, st, x, w, stats, g, gx, rows, D);
+            else hipLaunchKernelGGL(k_ln_bwd_blk<false>, grid, kRowB, 0, st, x, w, stats, g, gx, rows, D);
+        }
+        if (cols) {
+            hipLaunchKernelGGL(k_ln_cols_part, stream_grid(D * p.P, kRowB), kRowB, 0, st, x, stats, g, part, rows, D,
+                               p.chunk, p.P);
+            hipLaunchKernelGGL(k_ln_cols_combine, stream_grid(D, kRowB), kRowB, 0, st, part, gw, gb, D, p.P);
+        }
+    }
+    return check_launch("nc_hip_layer_norm_bwd");
+}

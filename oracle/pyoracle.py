@@ -132,11 +132,12 @@ def binary_fwd(op: str, a, b):
     return o
 
 
-def binary_bwd(op: str, a, b, g, need_a=True, need_b=True):
-    """Grads (in a's and b's logical shapes, contiguous) of sum(op(a, b) * g)."""
+def binary_bwd(op: str, a, b, g, need_a=True, need_b=True, ga0=None, gb0=None):
+    """Grads (in a's and b's logical shapes, contiguous) of sum(op(a, b) * g), accumulated onto
+    ga0 / gb0 (zeros when not given)."""
     g = _f32(g)
-    ga = np.zeros(a.shape, np.float32) if need_a else None
-    gb = np.zeros(b.shape, np.float32) if need_b else None
+    ga = (np.zeros(a.shape, np.float32) if ga0 is None else _f32(ga0).copy()) if need_a else None
+    gb = (np.zeros(b.shape, np.float32) if gb0 is None else _f32(gb0).copy()) if need_b else None
     lib().or_binary_bwd(c_int(BIN[op]), c_int(a.ndim), _i64(a.shape), _i64(_elem_strides(a)),
                         c_void_p(a.__array_interface__["data"][0]), c_int(b.ndim), _i64(b.shape),
                         _i64(_elem_strides(b)), c_void_p(b.__array_interface__["data"][0]), _p(g), _p(ga), _p(gb))

@@ -50,7 +50,7 @@ class Ref:
             raise RuntimeError(self.lib.nc_error(self.ctx).decode())
 
     def tensor(self, arr, dtype=abi.F32):
-        arr = np.ascontiguousarray(arr)
+        arr = np.array(arr, order="C", copy=True)  # keeps 0-d shapes (ascontiguousarray would not)
         nd, shp = abi.shape_arg(arr.shape)
         t = self.lib.nc_from_data(self.ctx, dtype, arr.ctypes.data_as(c_void_p), nd, shp)
         self.check()

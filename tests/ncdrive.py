@@ -50,7 +50,7 @@ class Engine:
 
     # tensors ---------------------------------------------------------------------------------------
     def tensor(self, arr, dtype=None):
-        arr = np.ascontiguousarray(arr)
+        arr = np.array(arr, order="C", copy=True)  # keeps 0-d shapes (ascontiguousarray would not)
         if dtype is None:
             dtype = {np.dtype(np.float32): abi.F32, np.dtype(np.int32): abi.I32, np.dtype(np.int8): abi.I8,
                      np.dtype(np.uint8): abi.U8}[arr.dtype]

@@ -1,0 +1,226 @@
+"""CPU tests of the engine library (no GPU): the C ABI loads and exports everything the headers
+declare, the reference's bindings resolve, host-side logic (shape inference, error messages, views,
+the RNG, the index divider) matches the compiled reference, and compute ops fail loudly without a
+HIP device instead of falling back to the host."""
+
+import ctypes
+import random
+import re
+from ctypes import c_float, c_uint32, c_void_p
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+from newch_amd import abi
+from oracle import pyoracle as O
+from tests.ncdrive import Engine, NcError
+
+ROOT = Path(__file__).resolve().parents[1]
+GOLD = Path(__file__).resolve().parent / "golden"
+
+
+def declared(header: Path) -> set[str]:
+    text = header.read_text()
+    return set(re.findall(r"^(?:NC_API|NC_HIP_API)\s+[^;]*?\b(nc_[a-z0-9_]+)\s*\(", text, flags=re.M))
+
+
+@pytest.fixture(scope="module")
+def lib():
+    return abi.load(abi.LIB_PATH)
+
+
+def has_device(lib) -> bool:
+    return lib.nc_device_count() > 0
+
+
+def test_exports_every_declared_symbol(lib):
+    names = declared(ROOT / "include" / "nc.h") | declared(ROOT / "include" / "nc_hip.h")
+    assert len(names) >= 150
+    missing = [n for n in sorted(names) if not hasattr(lib, n)]
+    assert not missing, missing
+
+
+def test_nc_h_declares_the_full_reference_api():
+    ours = declared(ROOT / "include" / "nc.h")
+    assert set(abi.NC_SIGNATURES) <= ours
+
+
+def test_reference_python_bindings_resolve(lib):
+    names = (GOLD / "lib_py_names.txt").read_text().split()
+    assert len(names) == 111
+    missing = [n for n in names if not hasattr(lib, n)]
+    assert not missing, missing
+
+
+def test_kernel_layer_binds(lib):
+    from newch_amd import hip
+    hip.bind(ctypes.CDLL(str(abi.LIB_PATH)))
+
+
+def test_index_divider_matches_integer_division(lib):
+    from newch_amd import hip
+    L = hip.bind(ctypes.CDLL(str(abi.LIB_PATH)))
+    rng = random.Random(5)
+    divs = list(range(1, 1025)) + [rng.randrange(1, 2 ** 32) for _ in range(2000)]
+    for k in range(1, 32):
+        divs += [2 ** k - 1, 2 ** k, 2 ** k + 1]
+    nums = list(range(0, 4097)) + [2 ** 32 - 1 - i for i in range(4096)] + [rng.randrange(0, 2 ** 32) for _ in range(20000)]
+    for k in range(1, 32):
+        nums += [2 ** k - 1, 2 ** k, 2 ** k + 1]
+    dv = (c_uint32 * len(divs))(*divs)
+    nv = (c_uint32 * len(nums))(*nums)
+    assert L.nc_hip_check_intdiv(dv, len(divs), nv, len(nums)) == 0
+    # edge numerators for each divisor: multiples and their neighbours
+    edge = []
+    for d in divs[:3000:7]:
+        for m in (1, 2, 3, (2 ** 32 - 1) // d):
+            for t in (d * m - 1, d * m, d * m + 1):
+                if 0 <= t < 2 ** 32:
+                    edge.append(t)
+    ev = (c_uint32 * len(edge))(*edge)
+    assert L.nc_hip_check_intdiv(dv, len(divs), ev, len(edge)) == 0
+
+
+# ------------------------------------------------------------------------------------------------
+# behaviour without a device (this container): host logic works, compute refuses
+# ------------------------------------------------------------------------------------------------
+@pytest.fixture
+def eng(lib):
+    if has_device(lib):
+        pytest.skip("a HIP device is visible: the no-device behaviour is not observable here")
+    e = Engine(lib=lib)
+    yield e
+    e.close()
+
+
+def test_no_device_compute_fails_loudly(eng):
+    L = eng.lib
+    assert L.nc_kernel_backend(eng.ctx) == b"hip:none"
+    a = eng.tensor(np.arange(6, dtype=np.float32).reshape(2, 3))
+    for fn in (lambda: L.nc_relu(a), lambda: L.nc_add(a, a), lambda: L.nc_sum(a, 0, 0),
+               lambda: L.nc_softmax(a), lambda: L.nc_gelu(a, 0)):
+        assert not fn()
+        assert L.nc_status_code(eng.ctx) == abi.ERR_STATE
+        assert b"no HIP device" in L.nc_error(eng.ctx)
+        L.nc_clear_error(eng.ctx)
+
+
+def test_off_path_ops_report_not_in_this_build(eng):
+    L = eng.lib
+    a = eng.tensor(np.ones((2, 2), np.float32))
+    assert not L.nc_matmul(a, a)
+    assert L.nc_status_code(eng.ctx) == abi.ERR_STATE and b"not in this build" in L.nc_error(eng.ctx)
+    L.nc_clear_error(eng.ctx)
+    assert not L.nc_sgd(eng.ctx, None, 0, abi.OptimOpts())
+    assert b"not in this build" in L.nc_error(eng.ctx)
+
+
+ref_only = pytest.mark.skipif(not O.REF_LIB.exists(), reason="oracle/_ref/libnc_ref.so not built")
+
+
+def _errors(e: Engine, calls):
+    """Runs each call on fresh inputs; returns [(status, message)] with the context cleared between."""
+    out = []
+    for make in calls:
+        r = make(e)
+        out.append((bool(r), e.lib.nc_status_code(e.ctx), e.lib.nc_error(e.ctx).decode()))
+        e.lib.nc_clear_error(e.ctx)
+        e.step_end()
+    return out
+
+
+SHAPE_ERRORS = [
+    lambda e: e.lib.nc_add(e.tensor(np.ones((2, 3), np.float32)), e.tensor(np.ones((4,), np.float32))),
+    lambda e: e.lib.nc_mul(e.tensor(np.ones((2, 3, 5), np.float32)), e.tensor(np.ones((3, 4), np.float32))),
+    lambda e: e.lib.nc_add(e.tensor(np.ones((2,), np.int32)), e.tensor(np.ones((2,), np.float32))),
+    lambda e: e.lib.nc_sum(e.tensor(np.ones((2, 3), np.float32)), 2, 0),
+    lambda e: e.lib.nc_max(e.tensor(np.ones((0, 3), np.float32)), 0, 0),
+    lambda e: e.lib.nc_argmax(e.tensor(np.ones((0,), np.float32)), abi.ALL_AXES),
+    lambda e: e.lib.nc_relu(e.tensor(np.ones((2,), np.int32))),
+    lambda e: e.lib.nc_softmax(e.tensor(np.ones((), np.float32))),
+    lambda e: e.lib.nc_layer_norm(e.tensor(np.ones((1, 4), np.float32)), 1, e.tensor(np.ones(3, np.float32)), None,
+                                  c_float(1e-5)),
+    lambda e: e.lib.nc_layer_norm(e.tensor(np.ones((1, 4), np.float32)), 3, None, None, c_float(1e-5)),
+    lambda e: e.lib.nc_reshape(e.tensor(np.ones((2, 3), np.float32)), *abi.shape_arg((4, 2))),
+    lambda e: e.lib.nc_reshape(e.tensor(np.ones((2, 3), np.float32)), *abi.shape_arg((-2, 3))),
+    lambda e: e.lib.nc_transpose(e.tensor(np.ones((2, 3), np.float32)), 0, 2),
+    lambda e: e.lib.nc_slice(e.tensor(np.ones((5, 3), np.float32)), 0, 2, 3, 2),
+    lambda e: e.lib.nc_slice(e.tensor(np.ones((5, 3), np.float32)), 1, 0, 1, 0),
+    lambda e: e.lib.nc_quantize_rows(e.tensor(np.ones((2, 3, 4), np.float32)), None),
+    lambda e: e.lib.nc_to_dtype(e.tensor(np.ones((2,), np.float32)), abi.F16),
+    lambda e: e.lib.nc_empty(e.ctx, abi.F32, 7, abi.shape_arg((1,) * 7)[1]),
+    lambda e: e.lib.nc_empty(e.ctx, abi.F32, 2, abi.shape_arg((2, -1))[1]),
+]
+
+
+@ref_only
+def test_shape_errors_match_reference(eng):
+    with Engine(O.REF_LIB) as ref:
+        want = _errors(ref, SHAPE_ERRORS)
+    got = _errors(eng, SHAPE_ERRORS)
+    for i, (w, g) in enumerate(zip(want, got)):
+        assert w == g, f"case {i}: reference {w}, this build {g}"
+
+
+def _views(e: Engine):
+    """View results observable without device compute: shapes, contiguity, aliasing, element reads."""
+    L = e.lib
+    t = e.tensor(np.arange(1, 25, dtype=np.float32).reshape(2, 3, 4))
+    out = []
+    r = L.nc_reshape(t, *abi.shape_arg((6, -1)))
+    out.append(("reshape", e.shape(r), L.nc_is_contiguous(r), L.nc_data_f32(r) == L.nc_data_f32(t)))
+    tt = L.nc_transpose(t, 0, 2)
+    out.append(("transpose", e.shape(tt), L.nc_is_contiguous(tt),
+                [L.nc_get(tt, abi.shape_arg(ix)[1]) for ix in ((3, 2, 1), (0, 1, 1), (2, 0, 0))]))
+    s = L.nc_slice(t, 2, 1, 2, 2)
+    out.append(("slice", e.shape(s), L.nc_is_contiguous(s),
+                [L.nc_get(s, abi.shape_arg(ix)[1]) for ix in ((1, 2, 1), (0, 0, 0))]))
+    v = L.nc_reshape(L.nc_transpose(t, 1, 2), *abi.shape_arg((2, 4, 3, 1)))  # viewable
+    out.append(("reshape_of_view", e.shape(v), bool(v) and L.nc_is_contiguous(v)))
+    d = L.nc_detach(t)
+    out.append(("detach", e.shape(d), L.nc_requires_grad(d)))
+    e.step_end()
+    return out
+
+
+@ref_only
+def test_views_match_reference(eng):
+    with Engine(O.REF_LIB) as ref:
+        want = _views(ref)
+    assert _views(eng) == want
+
+
+@ref_only
+def test_rng_matches_reference(eng):
+    """nc_randn / nc_rand_uniform draw the reference's xoshiro256** stream bit for bit."""
+    with Engine(O.REF_LIB, seed=77) as ref:
+        a = ref.read(ref.lib.nc_randn(ref.ctx, c_float(0.5), *abi.shape_arg((1000,))))
+        b = ref.read(ref.lib.nc_rand_uniform(ref.ctx, c_float(-1), c_float(2), *abi.shape_arg((333,))))
+    e = Engine(lib=eng.lib, seed=77)
+    try:
+        a2 = e.read(e.lib.nc_randn(e.ctx, c_float(0.5), *abi.shape_arg((1000,))))
+        b2 = e.read(e.lib.nc_rand_uniform(e.ctx, c_float(-1), c_float(2), *abi.shape_arg((333,))))
+    finally:
+        e.close()
+    assert a.tobytes() == a2.tobytes() and b.tobytes() == b2.tobytes()
+
+
+def test_mem_stats_layout(eng):
+    s = eng.lib.nc_get_mem_stats(eng.ctx)
+    assert ctypes.sizeof(s) == 4 * ctypes.sizeof(ctypes.c_size_t)
+    assert s.arena_bytes_in_use == 0
+
+
+def test_sticky_error_and_null_propagation(eng):
+    L = eng.lib
+    two = eng.tensor(np.ones(2, np.float32))
+    assert not L.nc_reshape(eng.tensor(np.ones(3, np.float32)), *abi.shape_arg((2,)))
+    msg = L.nc_error(eng.ctx)
+    assert b"reshape: cannot view [3] as [2]" == msg
+    assert not L.nc_relu(None)
+    assert not L.nc_add(two, None)
+    assert not L.nc_transpose(two, 0, 0)  # ops refuse to run while an error is pending
+    assert L.nc_error(eng.ctx) == msg  # first error sticks
+    L.nc_clear_error(eng.ctx)
+    assert L.nc_ok(eng.ctx)
