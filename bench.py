@@ -1,0 +1,311 @@
+"""Benchmark of the hot path on one MI355X: achieved HBM GB/s (and % of peak) per op class, and
+elements/s against the reference engine on the host CPU.
+
+    python bench.py [--steps K] [--warmup W] [--gpus 1] [--classes all|none] [--no-cpu]
+
+A step is one pass of the headline workload over its synthetic batch: the six activations (GELU
+(erf), SiLU, Sigmoid, Tanh, Hardswish, ReLU6) each forward y = f(x) and backward gi += f'(.) * g over
+2^28 fp32 elements resident in HBM.  `value` is the step's algorithmic bytes (forward 8 B/element:
+read x, write y; backward 16 B/element: read x or y, read g, read+write gi) over the timed wall
+time.  Every kernel launch is bracketed by HIP events on the launch stream; the per-kernel averages
+give `classes` (GB/s per op class, also for the broadcast / row-reduction / int8 / full-sum
+workloads unless --classes none) and the `roofline` of the dominant kernel.  `cpu_baseline` times
+the reference engine (oracle/_ref/libnc_ref.so, its own threaded AVX2 path) on a bounded sample of
+the same work.  Prints one JSON line.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+import numpy as np
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+PEAK_GBS = 8000.0  # MI355X HBM3E
+METRIC = "achieved HBM GB/s (% of MI355X peak) per op class; elements/s vs host CPU"
+ACTS = ["gelu", "silu", "sigmoid", "tanh", "hardswish", "relu6"]
+N_UNARY = 1 << 28
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+class Timeline:
+    """Per-launch HIP event pairs, grouped by kernel label."""
+
+    def __init__(self, hm):
+        self.hm = hm
+        self.pending = []
+        self.stats = {}
+
+    def run(self, label, nbytes, fn):
+        e0, e1 = self.hm.Event(), self.hm.Event()
+        e0.record()
+        fn()
+        e1.record()
+        self.pending.append((label, nbytes, e0, e1))
+
+    def collect(self):
+        for label, nbytes, e0, e1 in self.pending:
+            e1.synchronize()
+            ms = e0.elapsed_ms(e1)
+            s = self.stats.setdefault(label, {"bytes": nbytes, "ms": [], })
+            s["ms"].append(ms)
+        self.pending.clear()
+
+    def summary(self):
+        out = {}
+        for label, s in self.stats.items():
+            ms = float(np.median(s["ms"]))
+            gbs = s["bytes"] / (ms * 1e-3) / 1e9
+            out[label] = {"GB/s": round(gbs, 1), "frac": round(gbs / PEAK_GBS, 4), "us": round(ms * 1e3, 1),
+                          "bytes": s["bytes"], "launches": len(s["ms"])}
+        return out
+
+
+def unary_workload(K, hm, n):
+    rng = np.random.default_rng(1)
+    x = rng.standard_normal(n, dtype=np.float32)
+    g = np.random.default_rng(2).standard_normal(n, dtype=np.float32)
+    X, G = hm.DeviceBuffer.from_numpy(x), hm.DeviceBuffer.from_numpy(g)
+    del x, g
+    Y, GI = hm.DeviceBuffer(4 * n), hm.DeviceBuffer(4 * n)
+    GI.zero()
+    from newch_amd.hip import BWD_READS_Y
+
+    def step(tl):
+        for act in ACTS:
+            tl.run(f"{act}_fwd", 8 * n, lambda a=act: K.unary_fwd(a, X.ptr, Y.ptr, n))
+            reads_y = act in BWD_READS_Y
+            tl.run(f"{act}_bwd", 16 * n,
+                   lambda a=act, ry=reads_y: K.unary_bwd(a, 0 if ry else X.ptr, Y.ptr if ry else 0, G.ptr, GI.ptr, n,
+                                                         accumulate=True))
+
+    return step, 24 * n * len(ACTS), (X, G, Y, GI)
+
+
+def class_workloads(K, hm):
+    """Per-op-class workloads of the other configurations: (label, bytes, launcher) lists."""
+    work = []
+    keep = []
+    # broadcast binary: a[64,512,1,64] (one 2^30-output chunk of a[256,512,1,64]) op b[1,1,512,64]
+    blk = np.random.default_rng(3).standard_normal(1 << 21, dtype=np.float32)
+    A = hm.DeviceBuffer.from_numpy(blk)
+    Bv = hm.DeviceBuffer.from_numpy((0.5 + 1.5 * np.random.default_rng(4).random(512 * 64)).astype(np.float32))
+    n_out = 1 << 30
+    O = hm.DeviceBuffer(4 * n_out)
+    shape = (64, 512, 512, 64)
+    sa, sb, so = (32768, 64, 0, 1), (0, 0, 64, 1), (1 << 24, 1 << 15, 64, 1)
+    keep += [A, Bv, O]
+    fwd_bytes = 4 * n_out + 4 * (1 << 21) + 4 * 512 * 64
+    for op in ("add", "mul", "div"):
+        work.append((f"bcast_{op}_fwd", fwd_bytes,
+                     lambda op=op: K.binary_fwd(op, shape, A.ptr, sa, Bv.ptr, sb, O.ptr, so)))
+    # transposed view of a: storage [512(c),64(n),1,64] seen as [64,512,1,64] -> strides (64, 4096, 0, 1)
+    work.append(("bcast_add_fwd_transposed_a", fwd_bytes,
+                 lambda: K.binary_fwd("add", shape, A.ptr, (64, 4096, 0, 1), Bv.ptr, sb, O.ptr, so)))
+    # backward of add: grad_a (sum over h) and grad_b (sum over n, c) from g = O
+    GA, GB = hm.DeviceBuffer(4 * (1 << 21)), hm.DeviceBuffer(4 * 512 * 64)
+    GA.zero(), GB.zero()
+    sga, sgb = (32768, 64, 0, 1), (0, 0, 64, 1)
+    wsb = max(K.binary_bwd_workspace(shape, sga), K.binary_bwd_workspace(shape, sgb))
+    WS = hm.DeviceBuffer(max(wsb, 1))
+    keep += [GA, GB, WS]
+    work.append(("bcast_add_bwd_grad_a", 4 * n_out + 8 * (1 << 21),
+                 lambda: K.binary_bwd("add", 0, shape, O.ptr, so, A.ptr, sa, Bv.ptr, sb, GA.ptr, sga, WS.ptr, wsb)))
+    work.append(("bcast_add_bwd_grad_b", 4 * n_out + 8 * 512 * 64,
+                 lambda: K.binary_bwd("add", 1, shape, O.ptr, so, A.ptr, sa, Bv.ptr, sb, GB.ptr, sgb, WS.ptr, wsb)))
+    # row reductions X[65536, 1024]
+    rows, C = 65536, 1024
+    X = hm.DeviceBuffer.from_numpy((np.random.default_rng(7).standard_normal((rows, C), dtype=np.float32) * 2))
+    Y, G, GI = hm.DeviceBuffer(4 * rows * C), hm.DeviceBuffer(4 * rows * C), hm.DeviceBuffer(4 * rows * C)
+    G.upload(np.random.default_rng(9).standard_normal((rows, C), dtype=np.float32))
+    GI.zero()
+    W = hm.DeviceBuffer.from_numpy((1 + 0.1 * np.random.default_rng(8).standard_normal(C)).astype(np.float32))
+    Bb = hm.DeviceBuffer.from_numpy((0.1 * np.random.default_rng(8).standard_normal(C)).astype(np.float32))
+    S = hm.DeviceBuffer(8 * rows)
+    GW, GBb = hm.DeviceBuffer(4 * C), hm.DeviceBuffer(4 * C)
+    GW.zero(), GBb.zero()
+    lnws = K.layer_norm_bwd_workspace(rows, C)
+    LWS = hm.DeviceBuffer(max(lnws, 1))
+    M, AR = hm.DeviceBuffer(4 * rows), hm.DeviceBuffer(4 * rows)
+    keep += [X, Y, G, GI, W, Bb, S, GW, GBb, LWS, M, AR]
+    e = rows * C
+    work += [
+        ("softmax_fwd", 8 * e, lambda: K.softmax_fwd(False, rows, C, X.ptr, Y.ptr)),
+        ("softmax_bwd", 16 * e, lambda: K.softmax_bwd(False, rows, C, Y.ptr, G.ptr, GI.ptr)),
+        ("log_softmax_fwd", 8 * e, lambda: K.softmax_fwd(True, rows, C, X.ptr, Y.ptr)),
+        ("log_softmax_bwd", 16 * e, lambda: K.softmax_bwd(True, rows, C, Y.ptr, G.ptr, GI.ptr)),
+        ("layer_norm_fwd", 8 * e + 8 * rows, lambda: K.layer_norm_fwd(rows, C, X.ptr, W.ptr, Bb.ptr, 1e-5, Y.ptr, S.ptr)),
+        ("layer_norm_bwd", 16 * e + 8 * rows,
+         lambda: K.layer_norm_bwd(rows, C, X.ptr, W.ptr, S.ptr, G.ptr, GI.ptr, GW.ptr, GBb.ptr, LWS.ptr, lnws)),
+        ("max_argmax", 4 * e + 8 * rows, lambda: K.reduce_fwd("max", rows, C, 1, X.ptr, M.ptr, AR.ptr)),
+    ]
+    # int8: 48 x W[4096, 4096] quantize per row, dequantize back
+    qrows, qcols = 48 * 4096, 4096
+    blkw = (np.random.default_rng(11).standard_normal((4096, 4096), dtype=np.float32) * 0.02)
+    Wq = hm.DeviceBuffer(4 * qrows * qcols)
+    for m in range(48):
+        Wq.upload(blkw, offset=m * blkw.nbytes)
+    Q, SC, DQ = hm.DeviceBuffer(qrows * qcols), hm.DeviceBuffer(4 * qrows), hm.DeviceBuffer(4 * qrows * qcols)
+    keep += [Wq, Q, SC, DQ]
+    qe = qrows * qcols
+    work += [
+        ("quantize_rows", 5 * qe + 4 * qrows, lambda: K.quantize_rows(qrows, qcols, Wq.ptr, Q.ptr, SC.ptr)),
+        ("dequantize_rows", 5 * qe + 4 * qrows, lambda: K.dequantize_rows(qrows, qcols, Q.ptr, SC.ptr, DQ.ptr)),
+    ]
+    # full sum / mean over 2^30 fp32 (the bcast output buffer holds 2^30 values)
+    fws = K.reduce_workspace("sum", 1, n_out, 1)
+    FWS, FS = hm.DeviceBuffer(max(fws, 1)), hm.DeviceBuffer(4)
+    keep += [FWS, FS]
+    work += [
+        ("full_sum", 4 * n_out, lambda: K.reduce_fwd("sum", 1, n_out, 1, O.ptr, FS.ptr, 0, FWS.ptr, fws)),
+        ("full_mean", 4 * n_out, lambda: K.reduce_fwd("mean", 1, n_out, 1, O.ptr, FS.ptr, 0, FWS.ptr, fws)),
+    ]
+    return work, keep
+
+
+def cpu_baseline(budget_s: float = 20.0):
+    """The reference engine on host cores: y = f(x); y.sum().backward() per activation (the
+    reference's own activation benchmark, tools/bench_act.py:46-52) over a 2^22-element sample."""
+    import ctypes
+
+    from newch_amd import abi
+    from oracle import pyoracle
+
+    if not pyoracle.REF_LIB.exists():
+        return None
+    threads = int(os.environ.get("OMP_NUM_THREADS", "0")) or min(os.cpu_count() or 1, 64)
+    threads = min(threads, 64, os.cpu_count() or 1)
+    L = abi.load(pyoracle.REF_LIB)
+    cfg = abi.Config(0, 1, 0, threads)
+    ctx = L.nc_init(ctypes.byref(cfg))
+    n = 1 << 22
+    x = np.random.default_rng(1).standard_normal(n, dtype=np.float32)
+    nd, shp = abi.shape_arg((n,))
+    src = L.nc_from_data(ctx, abi.F32, x.ctypes.data_as(ctypes.c_void_p), nd, shp)
+    p = L.nc_parameter(ctx, src, nd, shp)
+    calls = {"gelu": lambda t: L.nc_gelu(t, 0), "silu": L.nc_silu, "sigmoid": L.nc_sigmoid, "tanh": L.nc_tanh,
+             "hardswish": L.nc_hardswish, "relu6": L.nc_relu6}
+    backend = L.nc_kernel_backend(ctx).decode()
+    t0 = time.perf_counter()
+    reps = 0
+    while True:
+        for act in ACTS:
+            y = calls[act](p)
+            L.nc_backward(L.nc_sum(y, abi.ALL_AXES, 0))
+            L.nc_step_end(ctx)
+        reps += 1
+        el = time.perf_counter() - t0
+        if el > budget_s or reps >= 50:
+            break
+    ok = L.nc_ok(ctx)
+    L.nc_free_ctx(ctx)
+    if not ok:
+        return None
+    el_per_s = reps * n * len(ACTS) / el
+    return {"value": round(el_per_s * 24 / 1e9, 2), "unit": "GB/s", "elements_per_s": round(el_per_s / 1e6, 1),
+            "elements_unit": "M el/s", "cores": threads, "kind": "reference",
+            "sample": f"2^22 fp32 elements, {reps} reps of y=f(x); y.sum().backward() for {', '.join(ACTS)} "
+                      f"on the reference engine ({backend} kernel tier), "
+                      f"{el:.1f} s; GB/s counts the same 24 B/element as the GPU value"}
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--classes", choices=["all", "none"], default="all")
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--elements", type=int, default=N_UNARY, help=argparse.SUPPRESS)
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(json.dumps({"error": "this build measures one GPU: every GPU box here has one MI355X; "
+                                   "the multi-GPU sharding is a design note (DESIGN.md), not a run"}))
+        sys.exit(2)
+
+    from newch_amd import hipmem as hm
+    from newch_amd.hip import Kernels
+
+    if hm.device_count() < 1:
+        sys.exit("bench.py: no HIP device visible")
+    K = Kernels()
+    n = args.elements
+    log(f"bench: unary workload, {n} elements x {len(ACTS)} activations, warmup {args.warmup}, steps {args.steps}")
+    step, step_bytes, _bufs = unary_workload(K, hm, n)
+    warm = Timeline(hm)
+    for _ in range(args.warmup):
+        step(warm)
+    warm.collect()
+    hm.synchronize()
+    tl = Timeline(hm)
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        step(tl)
+    hm.synchronize()
+    wall = time.perf_counter() - t0
+    tl.collect()
+    classes = tl.summary()
+    value = step_bytes * args.steps / wall / 1e9
+    dom = max((k for k in classes), key=lambda k: classes[k]["us"])
+    d = classes[dom]
+    log(f"bench: unary step {wall / args.steps * 1e3:.3f} ms, {value:.1f} GB/s; dominant {dom} {d['GB/s']} GB/s")
+
+    if args.classes == "all":
+        work, keep = class_workloads(K, hm)
+        for label, nbytes, fn in work:  # warm each once, then 5 timed launches
+            fn()
+        hm.synchronize()
+        ctl = Timeline(hm)
+        for _ in range(5):
+            for label, nbytes, fn in work:
+                ctl.run(label, nbytes, fn)
+        hm.synchronize()
+        ctl.collect()
+        extra = ctl.summary()
+        for k, v in extra.items():
+            log(f"bench: {k:28s} {v['GB/s']:8.1f} GB/s  {100 * v['frac']:5.1f}%  {v['us']:9.1f} us")
+        classes.update(extra)
+        del keep
+
+    cpu = None if args.no_cpu else cpu_baseline()
+    if cpu:
+        log(f"bench: cpu baseline {cpu['value']} GB/s ({cpu['elements_per_s']} M el/s) on {cpu['cores']} threads")
+    line = {
+        "metric": METRIC,
+        "value": round(value, 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(wall / args.steps * 1e3, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic",
+        "config": {"workload": "unary activations fwd+bwd over 2^28 fp32 elements (x~N(0,1) seed 1, "
+                               "g~N(0,1) seed 2): GELU(erf), SiLU, Sigmoid, Tanh, Hardswish, ReLU6",
+                   "elements": n, "bytes_per_step": step_bytes},
+        "hbm_frac": round(value / PEAK_GBS, 4),
+        "elements_per_s": round(n * len(ACTS) * args.steps / wall / 1e9, 3),
+        "elements_unit": "G el/s (fwd+bwd pairs)",
+        "roofline": {"bound": "hbm", "kernel": dom, "achieved": d["GB/s"], "peak": PEAK_GBS, "unit": "GB/s",
+                     "frac": d["frac"], "traffic": None},
+        "cpu_baseline": cpu,
+        "classes": classes,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

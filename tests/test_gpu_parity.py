@@ -328,28 +328,24 @@ def test_engine_views_and_residency(eng):
 # kernel layer on device buffers, against the oracle
 # ================================================================================================
 @pytest.fixture(scope="module")
-def torch():
-    import torch as _torch
-    assert _torch.cuda.is_available()
-    return _torch
-
-
-@pytest.fixture(scope="module")
 def K(lib):
     from newch_amd.hip import Kernels
     return Kernels()
 
 
-def dev(torch, a):
-    return torch.from_numpy(np.ascontiguousarray(a)).cuda()
+def dev(a, pad=0):
+    from newch_amd.hipmem import DeviceBuffer
+    return DeviceBuffer.from_numpy(np.asarray(a), pad)
 
 
-def sync(torch):
-    torch.cuda.synchronize()
+def empty(nbytes):
+    from newch_amd.hipmem import DeviceBuffer
+    return DeviceBuffer.empty(nbytes)
 
 
-def stream(torch):
-    return torch.cuda.current_stream().cuda_stream
+def sync():
+    from newch_amd.hipmem import synchronize
+    synchronize()
 
 
 SPECIAL = np.array([0.0, -0.0, np.inf, -np.inf, np.nan, 1e-40, -1e-40, -87.3365448, -87.34, 88.72, 88.8, 0.25,
@@ -361,30 +357,26 @@ KINDS = ["relu", "leaky_relu", "relu6", "hardsigmoid", "hardswish", "silu", "gel
 
 @pytest.mark.parametrize("kind", KINDS)
 @pytest.mark.parametrize("n,offset", [(1_000_003, 0), (4099, 1), (7, 0)])
-def test_kernel_unary(torch, K, kind, n, offset):
+def test_kernel_unary(K, kind, n, offset):
     rng = np.random.default_rng(n + len(kind))
     x = np.concatenate([SPECIAL, (rng.standard_normal(n) * 4).astype(np.float32)])[:n].astype(np.float32)
     g = rng.standard_normal(n).astype(np.float32)
     gi0 = rng.standard_normal(n).astype(np.float32)
     s = 0.3 if kind in ("leaky_relu", "scale", "add_scalar") else 0.0
-    okind = kind
-    y_ref = O.unary_fwd(okind, x, s)
-    # device buffers, optionally offset by one float so the 128-bit path cannot be used
-    X, Y, Gd, GI = (torch.zeros(n + 1, dtype=torch.float32, device="cuda") for _ in range(4))
-    X[offset:offset + n] = dev(torch, x)
-    Gd[offset:offset + n] = dev(torch, g)
-    GI[offset:offset + n] = dev(torch, gi0)
-    ptr = lambda t: t.data_ptr() + 4 * offset
-    K.unary_fwd(kind, ptr(X), ptr(Y), n, s, stream=stream(torch))
-    K.unary_bwd(kind, ptr(X), ptr(Y), ptr(Gd), ptr(GI), n, s, accumulate=True, stream=stream(torch))
-    sync(torch)
-    y = Y[offset:offset + n].cpu().numpy()
-    assert_bits(y, y_ref, f"{kind} fwd")
-    gi_ref = O.unary_bwd(okind, x, y_ref, g, gi0, s)
-    assert_bits(GI[offset:offset + n].cpu().numpy(), gi_ref, f"{kind} bwd accumulate")
-    K.unary_bwd(kind, ptr(X), ptr(Y), ptr(Gd), ptr(GI), n, s, accumulate=False, stream=stream(torch))
-    sync(torch)
-    assert_bits(GI[offset:offset + n].cpu().numpy(), O.unary_bwd(okind, x, y_ref, g, None, s), f"{kind} bwd store")
+    y_ref = O.unary_fwd(kind, x, s)
+    # buffers start `offset` floats into their allocation, so the 128-bit path cannot be used
+    pad = 4 * offset
+    X, Gd, GI = dev(x, pad), dev(g, pad), dev(gi0, pad)
+    Y = empty(4 * n + pad)
+    K.unary_fwd(kind, X.ptr + pad, Y.ptr + pad, n, s)
+    K.unary_bwd(kind, X.ptr + pad, Y.ptr + pad, Gd.ptr + pad, GI.ptr + pad, n, s, accumulate=True)
+    sync()
+    assert_bits(Y.to_numpy(np.float32, n, pad), y_ref, f"{kind} fwd")
+    gi_ref = O.unary_bwd(kind, x, y_ref, g, gi0, s)
+    assert_bits(GI.to_numpy(np.float32, n, pad), gi_ref, f"{kind} bwd accumulate")
+    K.unary_bwd(kind, X.ptr + pad, Y.ptr + pad, Gd.ptr + pad, GI.ptr + pad, n, s, accumulate=False)
+    sync()
+    assert_bits(GI.to_numpy(np.float32, n, pad), O.unary_bwd(kind, x, y_ref, g, None, s), f"{kind} bwd store")
 
 
 def strides_of(a):
@@ -415,34 +407,35 @@ BCAST = [
 
 @pytest.mark.parametrize("case,ash,aview,bsh", BCAST)
 @pytest.mark.parametrize("op", ["add", "sub", "mul", "div"])
-def test_kernel_binary(torch, K, case, ash, aview, bsh, op):
+def test_kernel_binary(K, case, ash, aview, bsh, op):
     rng = np.random.default_rng(zlib.crc32(f"{case}/{op}".encode()))
     A = rng.standard_normal(ash).astype(np.float32)
     B = (0.5 + 1.5 * rng.random(bsh)).astype(np.float32)
     a = np_view(A, aview)
     out_shape = O.broadcast_shape(a.shape, B.shape)
-    Ad, Bd = dev(torch, A), dev(torch, B)
-    Od = torch.empty(out_shape, dtype=torch.float32, device="cuda")
+    n_out = int(np.prod(out_shape))
+    Ad, Bd = dev(A), dev(B)
+    Od = empty(4 * n_out)
     sa = bcast_strides(a.shape, strides_of(a), out_shape)
     sb = bcast_strides(B.shape, strides_of(B), out_shape)
     so = [s // 4 for s in np.empty(out_shape, np.float32).strides]
-    K.binary_fwd(op, out_shape, Ad.data_ptr(), sa, Bd.data_ptr(), sb, Od.data_ptr(), so, stream=stream(torch))
-    sync(torch)
-    assert_bits(Od.cpu().numpy(), O.binary_fwd(op, a, B), f"{case} {op} fwd")
+    K.binary_fwd(op, out_shape, Ad.ptr, sa, Bd.ptr, sb, Od.ptr, so)
+    sync()
+    assert_bits(Od.to_numpy(np.float32, out_shape), O.binary_fwd(op, a, B), f"{case} {op} fwd")
     # gradients of both operands, accumulating onto random initial values
     G = rng.standard_normal(out_shape).astype(np.float32)
-    Gd = dev(torch, G)
+    Gd = dev(G)
     ta, tb = grad_terms64(op, a, B, G)
     for which, x, t in ((0, a, ta), (1, B, tb)):
         init = rng.standard_normal(x.shape).astype(np.float32)
-        GX = dev(torch, init)
+        GX = dev(init)
         sgx = bcast_strides(x.shape, [s // 4 for s in np.empty(x.shape, np.float32).strides], out_shape)
         wsb = K.binary_bwd_workspace(out_shape, sgx)
-        ws = torch.empty(max(wsb, 1), dtype=torch.uint8, device="cuda")
-        K.binary_bwd(op, which, out_shape, Gd.data_ptr(), so, Ad.data_ptr(), sa, Bd.data_ptr(), sb, GX.data_ptr(), sgx,
-                     ws.data_ptr(), wsb, accumulate=True, stream=stream(torch))
-        sync(torch)
-        got = GX.cpu().numpy()
+        ws = empty(max(wsb, 1))
+        K.binary_bwd(op, which, out_shape, Gd.ptr, so, Ad.ptr, sa, Bd.ptr, sb, GX.ptr, sgx, ws.ptr, wsb,
+                     accumulate=True)
+        sync()
+        got = GX.to_numpy(np.float32, x.shape)
         if tuple(x.shape) == tuple(out_shape):  # unreduced: the reference's fp32 expression, bit for bit
             want = O.binary_bwd(op, a, B, G, need_a=which == 0, need_b=which == 1,
                                 ga0=init if which == 0 else None, gb0=init if which == 1 else None)[which]
@@ -458,7 +451,7 @@ REDUCE_SHAPES = [((4096, 1024), 1), ((3, 1 << 20), 1), ((64, 1000, 33), 1), ((2,
 
 
 @pytest.mark.parametrize("shape,axis", REDUCE_SHAPES)
-def test_kernel_reduce(torch, K, shape, axis):
+def test_kernel_reduce(K, shape, axis):
     rng = np.random.default_rng(sum(shape))
     x = (rng.standard_normal(shape) * 2).astype(np.float32)
     if x.ndim >= 2 and axis == x.ndim - 1:  # ties and NaNs in some rows
@@ -471,62 +464,61 @@ def test_kernel_reduce(torch, K, shape, axis):
             rows[1, 0] = np.nan
             rows[2, rows.shape[1] // 2] = np.nan
     outer, R, inner = O.reduce_dims(x.shape, axis)
-    Xd = dev(torch, x)
+    Xd = dev(x)
     X64 = x.reshape(outer, R, inner).astype(np.float64)
     for kind in ("sum", "mean", "max", "argmax"):
-        Y = torch.empty(outer * inner, dtype=torch.float32, device="cuda")
-        A = torch.empty(outer * inner, dtype=torch.int32, device="cuda")
+        Y = empty(4 * outer * inner)
+        A = empty(4 * outer * inner)
         wsb = K.reduce_workspace(kind, outer, R, inner)
-        ws = torch.empty(max(wsb, 1), dtype=torch.uint8, device="cuda")
-        K.reduce_fwd(kind, outer, R, inner, Xd.data_ptr(), Y.data_ptr(), A.data_ptr(), ws.data_ptr(), wsb,
-                     stream=stream(torch))
-        sync(torch)
+        ws = empty(max(wsb, 1))
+        K.reduce_fwd(kind, outer, R, inner, Xd.ptr, Y.ptr, A.ptr, ws.ptr, wsb)
+        sync()
+        Yh = Y.to_numpy(np.float32, outer * inner)
+        Ah = A.to_numpy(np.int32, outer * inner)
         want, arg = O.reduce_fwd(kind, x, axis)
         if kind in ("sum", "mean"):
             good = ~np.isnan(X64).any(axis=1).ravel()
             ref64 = X64.sum(1).ravel() / (R if kind == "mean" else 1)
             scale = np.abs(X64).sum(1).ravel() / (R if kind == "mean" else 1) / np.sqrt(R)
-            assert_close64(Y.cpu().numpy()[good], ref64[good], scale[good], f"{shape} {kind}")
+            assert_close64(Yh[good], ref64[good], scale[good], f"{shape} {kind}")
         elif kind == "max":
-            assert_bits(Y.cpu().numpy(), want, f"{shape} max")
-            assert_bits(A.cpu().numpy(), arg, f"{shape} max arg")
+            assert_bits(Yh, want, f"{shape} max")
+            assert_bits(Ah, arg, f"{shape} max arg")
         else:
-            assert_bits(A.cpu().numpy(), want, f"{shape} argmax")
+            assert_bits(Ah, want, f"{shape} argmax")
     # backward: sum / mean broadcast back bit-exactly, max scatters to the argmax
     g = rng.standard_normal(outer * inner).astype(np.float32)
     gi0 = rng.standard_normal(x.size).astype(np.float32)
-    Gd = dev(torch, g)
+    Gd = dev(g)
     for kind in ("sum", "mean", "max"):
-        GI = dev(torch, gi0)
+        GI = dev(gi0)
         _, arg = O.reduce_fwd("max", x, axis)
-        Ad = dev(torch, arg)
-        K.reduce_bwd(kind, outer, R, inner, Gd.data_ptr(), Ad.data_ptr(), GI.data_ptr(), accumulate=True,
-                     stream=stream(torch))
-        sync(torch)
-        assert_bits(GI.cpu().numpy().reshape(x.shape), O.reduce_bwd(kind, x.shape, axis, g, arg, gi0.reshape(x.shape)),
+        Ad = dev(arg)
+        K.reduce_bwd(kind, outer, R, inner, Gd.ptr, Ad.ptr, GI.ptr, accumulate=True)
+        sync()
+        assert_bits(GI.to_numpy(np.float32, x.shape), O.reduce_bwd(kind, x.shape, axis, g, arg, gi0.reshape(x.shape)),
                     f"{shape} {kind} bwd")
 
 
 @pytest.mark.parametrize("rows,C", [(4096, 1024), (3, 1), (33, 7), (100, 64), (257, 100), (64, 4096), (5, 5000),
                                     (9, 4098)])
 @pytest.mark.parametrize("log_form", [False, True])
-def test_kernel_softmax(torch, K, rows, C, log_form):
+def test_kernel_softmax(K, rows, C, log_form):
     rng = np.random.default_rng(rows * C + log_form)
     x = (rng.standard_normal((rows, C)) * 2).astype(np.float32)
     if C > 5:
         x[0, 3] = -np.inf
     g = rng.standard_normal((rows, C)).astype(np.float32)
-    Xd, Yd, Gd = dev(torch, x), torch.empty((rows, C), device="cuda"), dev(torch, g)
-    K.softmax_fwd(log_form, rows, C, Xd.data_ptr(), Yd.data_ptr(), stream=stream(torch))
-    GI = torch.zeros((rows, C), device="cuda")
-    K.softmax_bwd(log_form, rows, C, Yd.data_ptr(), Gd.data_ptr(), GI.data_ptr(), accumulate=True,
-                  stream=stream(torch))
-    sync(torch)
+    Xd, Yd, Gd = dev(x), empty(x.nbytes), dev(g)
+    K.softmax_fwd(log_form, rows, C, Xd.ptr, Yd.ptr)
+    GI = dev(np.zeros((rows, C), np.float32))
+    K.softmax_bwd(log_form, rows, C, Yd.ptr, Gd.ptr, GI.ptr, accumulate=True)
+    sync()
     X = x.astype(np.float64)
     m = X.max(1, keepdims=True)
     e = np.exp(X - m)
     p = e / e.sum(1, keepdims=True)
-    y = Yd.cpu().numpy()
+    y = Yd.to_numpy(np.float32, (rows, C))
     if log_form:
         assert_close64(y, np.log(p), 1.0, "log_softmax fwd")
     else:
@@ -541,33 +533,31 @@ def test_kernel_softmax(torch, K, rows, C, log_form):
     else:
         gref = p * (G - (G * p).sum(1, keepdims=True))
         sc = p * (np.abs(G) + (np.abs(G) * p).sum(1, keepdims=True))
-    assert_close64(GI.cpu().numpy(), gref, sc, "softmax bwd")
+    assert_close64(GI.to_numpy(np.float32, (rows, C)), gref, sc, "softmax bwd")
 
 
 @pytest.mark.parametrize("rows,D", [(2048, 1024), (7, 10), (300, 64), (33, 4096), (5, 5000), (17, 333)])
-def test_kernel_layer_norm(torch, K, rows, D):
+def test_kernel_layer_norm(K, rows, D):
     rng = np.random.default_rng(rows + D)
     x = (rng.standard_normal((rows, D)) * 2 + 0.3).astype(np.float32)
     w = (1 + 0.1 * rng.standard_normal(D)).astype(np.float32)
     b = (0.1 * rng.standard_normal(D)).astype(np.float32)
     g = rng.standard_normal((rows, D)).astype(np.float32)
-    Xd, Wd, Bd, Gd = dev(torch, x), dev(torch, w), dev(torch, b), dev(torch, g)
-    Yd = torch.empty((rows, D), device="cuda")
-    Sd = torch.empty(2 * rows, device="cuda")
-    K.layer_norm_fwd(rows, D, Xd.data_ptr(), Wd.data_ptr(), Bd.data_ptr(), 1e-5, Yd.data_ptr(), Sd.data_ptr(),
-                     stream=stream(torch))
-    GX, GW, GB = torch.zeros((rows, D), device="cuda"), torch.zeros(D, device="cuda"), torch.zeros(D, device="cuda")
+    Xd, Wd, Bd, Gd = dev(x), dev(w), dev(b), dev(g)
+    Yd = empty(x.nbytes)
+    Sd = empty(8 * rows)
+    K.layer_norm_fwd(rows, D, Xd.ptr, Wd.ptr, Bd.ptr, 1e-5, Yd.ptr, Sd.ptr)
+    GX, GW, GB = dev(np.zeros((rows, D), np.float32)), dev(np.zeros(D, np.float32)), dev(np.zeros(D, np.float32))
     wsb = K.layer_norm_bwd_workspace(rows, D)
-    ws = torch.empty(max(wsb, 1), dtype=torch.uint8, device="cuda")
-    K.layer_norm_bwd(rows, D, Xd.data_ptr(), Wd.data_ptr(), Sd.data_ptr(), Gd.data_ptr(), GX.data_ptr(),
-                     GW.data_ptr(), GB.data_ptr(), ws.data_ptr(), wsb, accumulate=True, stream=stream(torch))
-    sync(torch)
+    ws = empty(max(wsb, 1))
+    K.layer_norm_bwd(rows, D, Xd.ptr, Wd.ptr, Sd.ptr, Gd.ptr, GX.ptr, GW.ptr, GB.ptr, ws.ptr, wsb, accumulate=True)
+    sync()
     y_o, st_o = O.layer_norm_fwd(x, D, w, b, 1e-5)
-    st = Sd.cpu().numpy()
+    st = Sd.to_numpy(np.float32, 2 * rows)
     # fp64 statistics rounded to fp32: equal to the reference's except at rare rounding ties
     assert (st == st_o).mean() > 0.999
     same = np.repeat((st.reshape(-1, 2) == st_o.reshape(-1, 2)).all(1), D).reshape(rows, D)
-    y = Yd.cpu().numpy()
+    y = Yd.to_numpy(np.float32, (rows, D))
     assert_bits(y[same], y_o[same], "layer_norm fwd rows with equal statistics")
     X = x.astype(np.float64)
     mu = X.mean(1, keepdims=True)
@@ -578,13 +568,13 @@ def test_kernel_layer_norm(torch, K, rows, D):
     gh = G * w
     gxr = rs * (gh - gh.mean(1, keepdims=True) - xh * (gh * xh).mean(1, keepdims=True))
     sc = rs * (np.abs(gh) + np.abs(gh).mean(1, keepdims=True) + np.abs(xh) * np.abs(gh * xh).mean(1, keepdims=True))
-    assert_close64(GX.cpu().numpy(), gxr, sc, "layer_norm dx")
-    assert_close64(GW.cpu().numpy(), (G * xh).sum(0), np.abs(G * xh).sum(0) / np.sqrt(rows), "layer_norm dw")
-    assert_close64(GB.cpu().numpy(), G.sum(0), np.abs(G).sum(0) / np.sqrt(rows), "layer_norm db")
+    assert_close64(GX.to_numpy(np.float32, (rows, D)), gxr, sc, "layer_norm dx")
+    assert_close64(GW.to_numpy(np.float32, D), (G * xh).sum(0), np.abs(G * xh).sum(0) / np.sqrt(rows), "layer_norm dw")
+    assert_close64(GB.to_numpy(np.float32, D), G.sum(0), np.abs(G).sum(0) / np.sqrt(rows), "layer_norm db")
 
 
 @pytest.mark.parametrize("rows,cols", [(512, 4096), (96, 70), (64, 8192), (33, 10000), (8, 16)])
-def test_kernel_quantize(torch, K, rows, cols):
+def test_kernel_quantize(K, rows, cols):
     rng = np.random.default_rng(rows * cols)
     w = (rng.standard_normal((rows, cols)) * 0.02).astype(np.float32)
     idx = rng.choice(w.size, max(1, w.size // 1000), replace=False)
@@ -595,14 +585,14 @@ def test_kernel_quantize(torch, K, rows, cols):
         w[1, 9:] = 0.25
         w[2, 1] = np.nan
         w[3, 2] = np.inf
-    Wd = dev(torch, w)
-    Q = torch.empty((rows, cols), dtype=torch.int8, device="cuda")
-    S = torch.empty(rows, dtype=torch.float32, device="cuda")
-    K.quantize_rows(rows, cols, Wd.data_ptr(), Q.data_ptr(), S.data_ptr(), stream=stream(torch))
-    D = torch.empty((rows, cols), dtype=torch.float32, device="cuda")
-    K.dequantize_rows(rows, cols, Q.data_ptr(), S.data_ptr(), D.data_ptr(), stream=stream(torch))
-    sync(torch)
+    Wd = dev(w)
+    Q = empty(rows * cols)
+    S = empty(4 * rows)
+    K.quantize_rows(rows, cols, Wd.ptr, Q.ptr, S.ptr)
+    D = empty(4 * rows * cols)
+    K.dequantize_rows(rows, cols, Q.ptr, S.ptr, D.ptr)
+    sync()
     q_ref, s_ref = O.quantize_rows(w)
-    assert_bits(Q.cpu().numpy(), q_ref, "q")
-    assert_bits(S.cpu().numpy(), s_ref, "scale")
-    assert_bits(D.cpu().numpy(), O.dequantize_rows(q_ref, s_ref), "dequant")
+    assert_bits(Q.to_numpy(np.int8, (rows, cols)), q_ref, "q")
+    assert_bits(S.to_numpy(np.float32, rows), s_ref, "scale")
+    assert_bits(D.to_numpy(np.float32, (rows, cols)), O.dequantize_rows(q_ref, s_ref), "dequant")
