@@ -173,7 +173,7 @@ def class_workloads(K, hm):
     return work, keep
 
 
-def cpu_baseline(budget_s: float = 20.0):
+def cpu_baseline(budget_s: float = 12.0):
     """The reference engine on host cores: y = f(x); y.sum().backward() per activation (the
     reference's own activation benchmark, tools/bench_act.py:46-52) over a 2^22-element sample."""
     import ctypes
@@ -205,7 +205,7 @@ def cpu_baseline(budget_s: float = 20.0):
             L.nc_step_end(ctx)
         reps += 1
         el = time.perf_counter() - t0
-        if el > budget_s or reps >= 50:
+        if el > budget_s or reps >= 2000:
             break
     ok = L.nc_ok(ctx)
     L.nc_free_ctx(ctx)
@@ -226,6 +226,9 @@ def main():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--classes", choices=["all", "none"], default="all")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--calibrate", action="store_true",
+                    help="also launch a plain copy kernel (y = -x over the same buffers, 8 B/element) so HBM "
+                         "counters can be scaled against known bytes")
     ap.add_argument("--elements", type=int, default=N_UNARY, help=argparse.SUPPRESS)
     args = ap.parse_args()
     if args.gpus != 1:
@@ -242,6 +245,14 @@ def main():
     n = args.elements
     log(f"bench: unary workload, {n} elements x {len(ACTS)} activations, warmup {args.warmup}, steps {args.steps}")
     step, step_bytes, _bufs = unary_workload(K, hm, n)
+    if args.calibrate:
+        X = _bufs[0]
+        Y = _bufs[2]
+        cal = Timeline(hm)
+        for _ in range(3):
+            cal.run("copy_calibration", 8 * n, lambda: K.unary_fwd("neg", X.ptr, Y.ptr, n))
+        cal.collect()
+        log(f"bench: copy calibration {cal.summary()['copy_calibration']}")
     warm = Timeline(hm)
     for _ in range(args.warmup):
         step(warm)
