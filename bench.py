@@ -173,6 +173,25 @@ def class_workloads(K, hm):
     return work, keep
 
 
+def measured_traffic(label: str):
+    """HBM bytes per launch of `label` from the committed rocprofv3 PMC summary (FETCH_SIZE and
+    WRITE_SIZE in KiB, scaled by what the same counters read for a plain copy of known size)."""
+    p = ROOT / "profiles" / "hbm_traffic_bench.txt"
+    if not p.exists():
+        return None
+    scale, rows = {}, {}
+    for line in p.read_text().splitlines():
+        parts = line.split()
+        if len(parts) == 2 and parts[0] in ("fetch_scale", "write_scale"):
+            scale[parts[0]] = float(parts[1])
+        elif len(parts) == 4 and not line.startswith("#") and parts[1].isdigit():
+            rows[parts[0]] = (float(parts[2]), float(parts[3]))
+    if label not in rows or len(scale) != 2:
+        return None
+    f, w = rows[label]
+    return int(round((f / scale["fetch_scale"] + w / scale["write_scale"]) * 1024))
+
+
 def cpu_baseline(budget_s: float = 12.0):
     """The reference engine on host cores: y = f(x); y.sum().backward() per activation (the
     reference's own activation benchmark, tools/bench_act.py:46-52) over a 2^22-element sample."""
@@ -311,7 +330,7 @@ def main():
         "elements_per_s": round(n * len(ACTS) * args.steps / wall / 1e9, 3),
         "elements_unit": "G el/s (fwd+bwd pairs)",
         "roofline": {"bound": "hbm", "kernel": dom, "achieved": d["GB/s"], "peak": PEAK_GBS, "unit": "GB/s",
-                     "frac": d["frac"], "traffic": None},
+                     "frac": d["frac"], "traffic": measured_traffic(dom), "algorithmic_bytes": d["bytes"]},
         "cpu_baseline": cpu,
         "classes": classes,
     }
