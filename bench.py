@@ -116,9 +116,18 @@ def class_workloads(K, hm):
     GA, GB = hm.DeviceBuffer(4 * (1 << 21)), hm.DeviceBuffer(4 * 512 * 64)
     GA.zero(), GB.zero()
     sga, sgb = (32768, 64, 0, 1), (0, 0, 64, 1)
-    wsb = max(K.binary_bwd_workspace(shape, sga), K.binary_bwd_workspace(shape, sgb))
+    wsb = max(K.binary_bwd_workspace(shape, sga), K.binary_bwd_workspace(shape, sgb),
+              K.binary_bwd2_workspace(shape, sga, sgb))
     WS = hm.DeviceBuffer(max(wsb, 1))
     keep += [GA, GB, WS]
+    # both gradients in one pass over g (g read, grad_a and grad_b read-modify-written, a and b read
+    # where the op needs them)
+    for op in ("add", "mul", "div"):
+        ab = 0 if op == "add" else 4 * (1 << 21) + 4 * 512 * 64
+        work.append((f"bcast_{op}_bwd", 4 * n_out + 8 * (1 << 21) + 8 * 512 * 64 + ab,
+                     lambda op=op: K.binary_bwd2(op, shape, O.ptr, so, A.ptr, sa, Bv.ptr, sb, GA.ptr, sga, GB.ptr,
+                                                 sgb, WS.ptr, wsb)))
+    # one operand at a time (the path when only one operand needs a gradient)
     work.append(("bcast_add_bwd_grad_a", 4 * n_out + 8 * (1 << 21),
                  lambda: K.binary_bwd("add", 0, shape, O.ptr, so, A.ptr, sa, Bv.ptr, sb, GA.ptr, sga, WS.ptr, wsb)))
     work.append(("bcast_add_bwd_grad_b", 4 * n_out + 8 * 512 * 64,
@@ -251,8 +260,8 @@ def main():
     ap.add_argument("--elements", type=int, default=N_UNARY, help=argparse.SUPPRESS)
     args = ap.parse_args()
     if args.gpus != 1:
-        print(json.dumps({"error": "this build measures one GPU: every GPU box here has one MI355X; "
-                                   "the multi-GPU sharding is a design note (DESIGN.md), not a run"}))
+        print(json.dumps({"error": "bench.py measures one MI355X: the kernels run on one GPU's share "
+                                   "and multi-GPU sharding is not implemented"}))
         sys.exit(2)
 
     from newch_amd import hipmem as hm

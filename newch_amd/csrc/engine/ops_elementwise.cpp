@@ -53,6 +53,31 @@ static void binary_bwd(nc_node *n) {
     bcast_strides(b, nd, o->shape, sb);
     float *g = fptr(o->grad), *pa = fptr(a), *pb = fptr(b);
     if (!g || !pa || !pb) return;
+    if (needs_grad(a) && needs_grad(b) && a != b && !same_shape(a, o) && !same_shape(b, o)) {
+        // both operands are reduced: one pass over g for both gradients (nc_hip_binary_bwd2)
+        if (!grad_buf(a) || !grad_buf(b)) return;
+        int64_t sga[NC_MAX_DIMS], sgb[NC_MAX_DIMS];
+        bcast_strides_shape(a->ndim, a->shape, nd, o->shape, sga);
+        bcast_strides_shape(b->ndim, b->shape, nd, o->shape, sgb);
+        const size_t ws_bytes = nc_hip_binary_bwd2_workspace(nd, o->shape, sga, sgb);
+        char *ws = ws_bytes ? arena_alloc(ctx, ws_bytes) : nullptr;
+        if (ws_bytes && !ws) return;
+        int acc_a = grad_acc(a), acc_b = grad_acc(b);
+        if (acc_a != acc_b) {  // one fresh buffer: give it its zeros so both accumulate
+            if (!fill_zero(acc_a ? b->grad : a->grad)) return;
+            acc_a = acc_b = 1;
+        }
+        float *ga = fptr(a->grad), *gb = fptr(b->grad);
+        if (!ga || !gb) return;
+        if (!hip_layer_ok(ctx,
+                          nc_hip_binary_bwd2(n->op->kind, nd, o->shape, g, o->stride, pa, sa, pb, sb, ga, sga, gb,
+                                             sgb, acc_a, ws, ws_bytes, stream(ctx)),
+                          n->op->name))
+            return;
+        wrote_dev(a->grad);
+        wrote_dev(b->grad);
+        return;
+    }
     for (int which = 0; which < 2; which++) {
         nc_tensor *x = n->in[which];
         if (!needs_grad(x)) continue;

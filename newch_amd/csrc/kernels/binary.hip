@@ -19,6 +19,8 @@
 
 #include <string.h>
 
+#include <algorithm>
+
 namespace nchip {
 
 constexpr int kB = 256;
@@ -74,24 +76,66 @@ struct VecModes {
     int64_t ia, ib;    // inner element strides (for gathers)
 };
 
+// NC_BIN_UNROLL work items per lane are decoded and loaded before any is computed and stored, so
+// several operand loads (mostly L2 hits on the broadcast operands) are in flight per lane.
+#ifndef NC_BIN_UNROLL
+#define NC_BIN_UNROLL 4
+#endif
+#ifndef NC_BIN_GRID_PER_CU
+#define NC_BIN_GRID_PER_CU 16
+#endif
+constexpr int kBU = NC_BIN_UNROLL;
+
 template <int OP, bool VEC>
 __global__ __launch_bounds__(kB) void k_binary_fwd(const float *__restrict__ a, const float *__restrict__ b,
                                                    float *__restrict__ o, IdxMap<3> m, VecModes vm, uint32_t nwork) {
-    const uint32_t step = gridDim.x * kB;
-    for (uint32_t w = blockIdx.x * kB + threadIdx.x; w < nwork; w += step) {
-        int64_t off[3];
-        offsets<3>(m, w, off);
+    const uint64_t step = (uint64_t)gridDim.x * kB * kBU;
+    for (uint64_t base = (uint64_t)blockIdx.x * kB * kBU + threadIdx.x; base < nwork; base += step) {
         if constexpr (VEC) {
-            const f4 x = load4(a + off[0], vm.ia, vm.a);
-            const f4 y = load4(b + off[1], vm.ib, vm.b);
-            f4 r;
-            r.x = bin<OP>(x.x, y.x);
-            r.y = bin<OP>(x.y, y.y);
-            r.z = bin<OP>(x.z, y.z);
-            r.w = bin<OP>(x.w, y.w);
-            __builtin_nontemporal_store(r, (f4 *)(o + off[2]));
+            f4 x[kBU], y[kBU];
+            int64_t oo[kBU];
+#pragma unroll
+            for (int u = 0; u < kBU; u++) {
+                const uint64_t w = base + (uint64_t)u * kB;
+                if (w < nwork) {
+                    int64_t off[3];
+                    offsets<3>(m, (uint32_t)w, off);
+                    x[u] = load4(a + off[0], vm.ia, vm.a);
+                    y[u] = load4(b + off[1], vm.ib, vm.b);
+                    oo[u] = off[2];
+                }
+            }
+#pragma unroll
+            for (int u = 0; u < kBU; u++) {
+                const uint64_t w = base + (uint64_t)u * kB;
+                if (w < nwork) {
+                    f4 r;
+                    r.x = bin<OP>(x[u].x, y[u].x);
+                    r.y = bin<OP>(x[u].y, y[u].y);
+                    r.z = bin<OP>(x[u].z, y[u].z);
+                    r.w = bin<OP>(x[u].w, y[u].w);
+                    __builtin_nontemporal_store(r, (f4 *)(o + oo[u]));
+                }
+            }
         } else {
-            o[off[2]] = bin<OP>(a[off[0]], b[off[1]]);
+            float x[kBU], y[kBU];
+            int64_t oo[kBU];
+#pragma unroll
+            for (int u = 0; u < kBU; u++) {
+                const uint64_t w = base + (uint64_t)u * kB;
+                if (w < nwork) {
+                    int64_t off[3];
+                    offsets<3>(m, (uint32_t)w, off);
+                    x[u] = a[off[0]];
+                    y[u] = b[off[1]];
+                    oo[u] = off[2];
+                }
+            }
+#pragma unroll
+            for (int u = 0; u < kBU; u++) {
+                const uint64_t w = base + (uint64_t)u * kB;
+                if (w < nwork) o[oo[u]] = bin<OP>(x[u], y[u]);
+            }
         }
     }
 }
@@ -117,7 +161,7 @@ __global__ __launch_bounds__(kB) void k_binary_fwd_big(const float *__restrict__
 struct Prepared {
     int nd;
     int64_t shape[NC_HIP_MAX_DIMS];
-    int64_t st[4][NC_HIP_MAX_DIMS];
+    int64_t st[5][NC_HIP_MAX_DIMS];
     int64_t numel;
 };
 
@@ -188,7 +232,7 @@ static int launch_fwd(const float *a, const float *b, float *o, const Prepared &
     }
     IdxMap<3> m;
     make_map<3>(p, unit, m);
-    const unsigned grid = stream_grid(nwork, kB, 16);
+    const unsigned grid = stream_grid((nwork + kBU - 1) / kBU, kB, NC_BIN_GRID_PER_CU);
     if (vec) {
         VecModes vm{ma, mb, p.st[0][inner], p.st[1][inner]};
         hipLaunchKernelGGL((k_binary_fwd<OP, true>), dim3(grid), dim3(kB), 0, st, a, b, o, m, vm, (uint32_t)nwork);
@@ -483,6 +527,189 @@ static int prepare_grad(int op, int which, int nd, const int64_t *shape, const i
     return prepare(nd, shape, 4, strides, p, "nc_hip_binary_bwd");
 }
 
+// ------------------------------------------------------------------------------------------------
+// Fused backward of both operands (one pass over g) for the pattern
+//     g[P..., H, W] (contiguous),  a[P..., 1, W] (broadcast over H),  b[H, W] (broadcast over P...)
+// i.e. grad_a = sum over H, grad_b = sum over the plane dims.  A 512-lane workgroup owns whole
+// [H, W] planes: lane t holds float4 columns q = t + 512 k (k < T, T = H*W/2048 <= 16), all in the
+// same column group w4 = t mod W4 (W4 = W/4 divides 64).  Per plane, grad_a[p, :] is reduced across
+// the lanes sharing w4 (wave shuffles, then LDS across the 8 waves, in a fixed order) and written;
+// grad_b accumulates in fp64 registers over the workgroup's planes and is written once as a
+// partial, combined by k_bwd2_gb_combine in workgroup order.  MODE: 0 add/sub, 1 mul, 3 div.
+// ------------------------------------------------------------------------------------------------
+constexpr int kB2 = 512;
+constexpr int kB2Waves = kB2 / kWave;
+constexpr int kB2MaxT = 16;
+
+struct Bwd2Plan {
+    uint32_t P, H, W4, T;
+    uint32_t planes_per_block;
+    IdxMap<1> amap;  // element offset of a[p, 0, 0] over the plane dims
+    int64_t ga_row;  // element offset step of grad_a per plane (its contiguous stride: W)
+};
+
+template <int MODE, bool ACC>
+__global__ __launch_bounds__(kB2) void k_bcast_bwd2(const float *__restrict__ g, const float *__restrict__ a,
+                                                    const float *__restrict__ b, float *__restrict__ ga,
+                                                    double *__restrict__ gb_part, Bwd2Plan pl, double alpha_b) {
+    __shared__ double sh[kB2Waves][64][4];
+    const int tid = threadIdx.x, lane = tid & (kWave - 1), wv = tid / kWave;
+    const uint32_t W4 = pl.W4, T = pl.T;
+    const uint32_t w4 = tid % W4;
+    const uint32_t plane4 = pl.H * W4;  // float4 per plane (= kB2 * T)
+    const uint32_t p0 = blockIdx.x * pl.planes_per_block;
+    const uint32_t p1 = min(pl.P, p0 + pl.planes_per_block);
+    double accb[kB2MaxT][4];
+#pragma unroll
+    for (int k = 0; k < kB2MaxT; k++) accb[k][0] = accb[k][1] = accb[k][2] = accb[k][3] = 0.0;
+    for (uint32_t p = p0; p < p1; p++) {
+        const f4 *gp = (const f4 *)(g + (size_t)p * plane4 * 4);
+        f4 av = f4{0.f, 0.f, 0.f, 0.f};
+        if constexpr (MODE == 1 || MODE == 3) {
+            int64_t off[1];
+            offsets<1>(pl.amap, p, off);
+            av = *(const f4 *)(a + off[0] + 4 * w4);
+        }
+        double sa[4] = {0.0, 0.0, 0.0, 0.0};
+#pragma unroll
+        for (int k = 0; k < kB2MaxT; k++) {
+            if ((uint32_t)k < T) {
+                const uint32_t q = tid + kB2 * k;
+                const f4 gv = __builtin_nontemporal_load(gp + q);
+                f4 bv = f4{1.f, 1.f, 1.f, 1.f};
+                if constexpr (MODE != 0) bv = ((const f4 *)b)[q];
+                const float gg[4] = {gv.x, gv.y, gv.z, gv.w};
+                const float bb[4] = {bv.x, bv.y, bv.z, bv.w};
+                const float aa[4] = {av.x, av.y, av.z, av.w};
+#pragma unroll
+                for (int c = 0; c < 4; c++) {
+                    const double gd = (double)gg[c];
+                    // grad_a term: g (add, sub), g*b (mul), g/b (div)
+                    sa[c] += MODE == 0 ? gd : MODE == 1 ? gd * (double)bb[c] : gd / (double)bb[c];
+                    // grad_b term before the per-column factor: g (add, sub), g*a (mul, div)
+                    accb[k][c] += (MODE == 1 || MODE == 3) ? gd * (double)aa[c] : gd;
+                }
+            }
+        }
+        // lanes sharing w4 inside the wave, then the 8 waves in order
+        for (uint32_t o = W4; o < (uint32_t)kWave; o <<= 1) {
+#pragma unroll
+            for (int c = 0; c < 4; c++) sa[c] += __shfl_xor(sa[c], (int)o, kWave);
+        }
+        if ((uint32_t)lane < W4) {
+#pragma unroll
+            for (int c = 0; c < 4; c++) sh[wv][lane][c] = sa[c];
+        }
+        __syncthreads();
+        if ((uint32_t)tid < W4 * 4) {
+            const uint32_t col = tid / 4, c = tid % 4;
+            double t = 0.0;
+            for (int w = 0; w < kB2Waves; w++) t += sh[w][col][c];
+            float *dst = ga + (size_t)p * pl.ga_row + 4 * col + c;
+            *dst = (float)((ACC ? (double)*dst : 0.0) + t);
+        }
+        __syncthreads();
+    }
+    double *out = gb_part + (size_t)blockIdx.x * plane4 * 4;
+#pragma unroll
+    for (int k = 0; k < kB2MaxT; k++) {
+        if ((uint32_t)k < T) {
+            const uint32_t q = tid + kB2 * k;
+#pragma unroll
+            for (int c = 0; c < 4; c++) out[4 * q + c] = accb[k][c] * alpha_b;
+        }
+    }
+}
+
+// grad_b[e] (+)= factor(e) * sum over workgroups of part[wg][e], workgroups in order (64 x 16 lanes)
+template <int MODE, bool ACC>
+__global__ __launch_bounds__(1024) void k_bwd2_gb_combine(const double *__restrict__ part, const float *__restrict__ b,
+                                                          float *__restrict__ gb, uint32_t n, uint32_t nparts) {
+    __shared__ double shc[16][64];
+    const int x = threadIdx.x % 64, y = threadIdx.x / 64;
+    const uint32_t e = blockIdx.x * 64 + x;
+    double t = 0.0;
+    if (e < n) {
+#pragma unroll 8
+        for (uint32_t q = y; q < nparts; q += 16) t += part[(size_t)q * n + e];
+    }
+    shc[y][x] = t;
+    __syncthreads();
+    if (y == 0 && e < n) {
+        double s = 0.0;
+#pragma unroll
+        for (int k = 0; k < 16; k++) s += shc[k][x];
+        if constexpr (MODE == 3) {  // d(a/b)/db = -(g a) / b^2: the b factor is the same for every term
+            const double bv = (double)b[e];
+            s = -s / (bv * bv);
+        }
+        gb[e] = (float)((ACC ? (double)gb[e] : 0.0) + s);
+    }
+}
+
+// Returns true (and the plan) when the fused kernel applies to the prepared operand strides
+// (order: g, a, b, ga, gb).
+static bool plan_bwd2(const Prepared &p, const float *g, const float *a, const float *b, const float *ga,
+                      const float *gb, Bwd2Plan &pl) {
+    if (p.nd < 3 || p.numel >= (int64_t)UINT32_MAX) return false;
+    const int h = p.nd - 2, w = p.nd - 1;
+    const int64_t H = p.shape[h], W = p.shape[w];
+    if (W % 4 || 64 % (W / 4) || (H * (W / 4)) % kB2 || H * (W / 4) / kB2 > kB2MaxT) return false;
+    // g contiguous; a: stride 0 over H, 1 over W; b: [H, W] contiguous, 0 over planes;
+    // ga: 0 over H, 1 over W, contiguous rows of W over planes; gb: [H, W] contiguous, 0 over planes
+    if (p.st[0][w] != 1 || p.st[0][h] != W) return false;
+    if (p.st[1][h] != 0 || p.st[1][w] != 1) return false;
+    if (p.st[2][h] != W || p.st[2][w] != 1) return false;
+    if (p.st[3][h] != 0 || p.st[3][w] != 1) return false;
+    if (p.st[4][h] != W || p.st[4][w] != 1) return false;
+    int64_t P = 1, rowg = H * W, rowa = W;
+    for (int d = h - 1; d >= 0; d--) {
+        if (p.st[0][d] != rowg || p.st[2][d] != 0 || p.st[4][d] != 0 || p.st[3][d] != rowa) return false;
+        rowg *= p.shape[d];
+        rowa *= p.shape[d];
+        P *= p.shape[d];
+    }
+    if (!aligned16(g) || !aligned16(b) || !aligned16(ga) || !aligned16(gb) || !aligned16(a)) return false;
+    for (int d = 0; d < h; d++)
+        if (p.st[1][d] % 4) return false;
+    Prepared ap{};
+    ap.nd = h;
+    for (int d = 0; d < h; d++) {
+        ap.shape[d] = p.shape[d];
+        ap.st[0][d] = p.st[1][d];
+    }
+    make_map<1>(ap, 1, pl.amap);
+    pl.P = (uint32_t)P;
+    pl.H = (uint32_t)H;
+    pl.W4 = (uint32_t)(W / 4);
+    pl.T = (uint32_t)(H * (W / 4) / kB2);
+    const uint32_t blocks = (uint32_t)std::min<int64_t>(P, num_cus());
+    pl.planes_per_block = (uint32_t)((P + blocks - 1) / blocks);
+    pl.ga_row = W;
+    return true;
+}
+
+static size_t bwd2_ws(const Bwd2Plan &pl) {
+    const uint32_t blocks = (pl.P + pl.planes_per_block - 1) / pl.planes_per_block;
+    return (size_t)blocks * pl.H * pl.W4 * 4 * sizeof(double);
+}
+
+template <int MODE>
+static int launch_bwd2(const float *g, const float *a, const float *b, float *ga, float *gb, const Bwd2Plan &pl,
+                       double alpha_b, int acc, void *ws, size_t ws_bytes, hipStream_t st) {
+    const size_t need = bwd2_ws(pl);
+    if (ws_bytes < need || !ws)
+        return set_error(NC_HIP_ERR_WORKSPACE, "binary_bwd2: workspace of %zu bytes needed, %zu given", need, ws_bytes);
+    const uint32_t blocks = (pl.P + pl.planes_per_block - 1) / pl.planes_per_block;
+    double *part = (double *)ws;
+    if (acc) hipLaunchKernelGGL((k_bcast_bwd2<MODE, true>), dim3(blocks), dim3(kB2), 0, st, g, a, b, ga, part, pl, alpha_b);
+    else hipLaunchKernelGGL((k_bcast_bwd2<MODE, false>), dim3(blocks), dim3(kB2), 0, st, g, a, b, ga, part, pl, alpha_b);
+    const uint32_t n = pl.H * pl.W4 * 4;
+    if (acc) hipLaunchKernelGGL((k_bwd2_gb_combine<MODE, true>), dim3((n + 63) / 64), dim3(1024), 0, st, part, b, gb, n, blocks);
+    else hipLaunchKernelGGL((k_bwd2_gb_combine<MODE, false>), dim3((n + 63) / 64), dim3(1024), 0, st, part, b, gb, n, blocks);
+    return check_launch("nc_hip_binary_bwd2");
+}
+
 }  // namespace nchip
 
 using namespace nchip;
@@ -544,11 +771,32 @@ extern "C" NC_HIP_API int nc_hip_binary_bwd(int op, int which, int nd, const int
     }
 }
 
+static int prepare_bwd2(int nd, const int64_t *shape, const int64_t *sg, const int64_t *sa, const int64_t *sb,
+                        const int64_t *sga, const int64_t *sgb, Prepared &p) {
+    const int64_t *strides[5] = {sg, sa, sb, sga, sgb};
+    return prepare(nd, shape, 5, strides, p, "nc_hip_binary_bwd2");
+}
+
 extern "C" NC_HIP_API size_t nc_hip_binary_bwd2_workspace(int nd, const int64_t *shape, const int64_t *sga,
                                                           const int64_t *sgb) {
     size_t wa = sga ? nc_hip_binary_bwd_workspace(nd, shape, sga) : 0;
     size_t wb = sgb ? nc_hip_binary_bwd_workspace(nd, shape, sgb) : 0;
-    return wa > wb ? wa : wb;
+    size_t need = wa > wb ? wa : wb;
+    if (sga && sgb && nd >= 2 && nd <= NC_HIP_MAX_DIMS) {
+        // the fused plan depends on shape and grad layouts; model g, b as contiguous, a as broadcast like ga
+        int64_t cs[NC_HIP_MAX_DIMS], s = 1;
+        for (int d = nd - 1; d >= 0; d--) {
+            cs[d] = s;
+            s *= shape[d];
+        }
+        Prepared p;
+        if (prepare_bwd2(nd, shape, cs, sga, sgb, sga, sgb, p) == NC_HIP_OK) {
+            Bwd2Plan pl;
+            const float *al = (const float *)(uintptr_t)256;  // any 16-byte aligned address: only the plan is needed
+            if (plan_bwd2(p, al, al, al, al, al, pl)) need = std::max(need, bwd2_ws(pl));
+        }
+    }
+    return need;
 }
 
 extern "C" NC_HIP_API int nc_hip_binary_bwd2(int op, int nd, const int64_t *shape, const float *g,
@@ -556,6 +804,23 @@ extern "C" NC_HIP_API int nc_hip_binary_bwd2(int op, int nd, const int64_t *shap
                                              const int64_t *sb, float *ga, const int64_t *sga, float *gb,
                                              const int64_t *sgb, int accumulate, void *ws, size_t ws_bytes,
                                              void *stream) {
+    if (op < 0 || op > 3) return set_error(NC_HIP_ERR_ARG, "nc_hip_binary_bwd2: bad op");
+    if (ga && gb) {
+        Prepared p;
+        int rc = prepare_bwd2(nd, shape, sg, sa, sb, sga, sgb, p);
+        if (rc) return rc;
+        Bwd2Plan pl;
+        if (p.numel > 0 && plan_bwd2(p, g, a, b, ga, gb, pl)) {
+            hipStream_t st = as_stream(stream);
+            const double alpha_b = op == NC_HIP_BIN_SUB ? -1.0 : 1.0;
+            switch (op) {
+            case NC_HIP_BIN_ADD: return launch_bwd2<0>(g, a, b, ga, gb, pl, alpha_b, accumulate, ws, ws_bytes, st);
+            case NC_HIP_BIN_SUB: return launch_bwd2<0>(g, a, b, ga, gb, pl, alpha_b, accumulate, ws, ws_bytes, st);
+            case NC_HIP_BIN_MUL: return launch_bwd2<1>(g, a, b, ga, gb, pl, alpha_b, accumulate, ws, ws_bytes, st);
+            default: return launch_bwd2<3>(g, a, b, ga, gb, pl, alpha_b, accumulate, ws, ws_bytes, st);
+            }
+        }
+    }
     int rc = NC_HIP_OK;
     if (ga) rc = nc_hip_binary_bwd(op, 0, nd, shape, g, sg, a, sa, b, sb, ga, sga, accumulate, ws, ws_bytes, stream);
     if (rc == NC_HIP_OK && gb)

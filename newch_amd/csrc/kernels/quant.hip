@@ -5,13 +5,14 @@
 // quantize: one wave64 per row; a row of up to 8192 floats stays in registers (VPL 128-bit vectors
 // per lane), so w is read once (4 B/el) and q written once (1 B/el, four int8 packed per 32-bit
 // store).  Rows are independent, so 48 stacked 4096x4096 matrices are a single launch.
-// dequantize: a streaming map reading 16 int8 per lane (one 128-bit load) and writing four
-// 128-bit float vectors.
+// dequantize: a streaming map, each lane reading 4 int8 (one 32-bit load) and writing one 128-bit
+// float vector, lane-contiguous so loads and stores coalesce.
 //
 // Arithmetic is the reference's exactly: amax = max |x| (fmaxf, NaN ignored, order-free),
 // s = amax / 127 (1 for a zero row), inv = 1 / s, q = clamp(rne(x * inv), -127, 127); the
 // float -> int8 conversion maps NaN to 0 as the reference's truncating conversion does.
 #include "common.hpp"
+#include "intdiv.hpp"
 
 namespace nchip {
 
@@ -85,24 +86,33 @@ __global__ __launch_bounds__(kQB) void k_quant_blk(const float *__restrict__ w, 
     }
 }
 
-// 16 int8 per lane-step when cols % 16 == 0 and everything is 16-byte aligned
-__global__ __launch_bounds__(kQB) void k_dequant16(const int4 *__restrict__ q, const float *__restrict__ scale,
-                                                   f4 *__restrict__ w, int64_t n16, uint32_t per_row16) {
-    const int64_t step = (int64_t)gridDim.x * kQB;
-    for (int64_t i = (int64_t)blockIdx.x * kQB + threadIdx.x; i < n16; i += step) {
-        const i4 b = __builtin_nontemporal_load((const i4 *)q + i);
-        const float s = scale[i / per_row16];
-        f4 *o = w + 4 * i;
-        const int words[4] = {b.x, b.y, b.z, b.w};
+// Lane-contiguous dequantization: lane j reads 4 int8 as one 32-bit word and writes one 128-bit
+// float vector, so a wave reads 256 contiguous bytes and writes 1 KiB contiguous; U words in
+// flight per lane.  Requires cols % 4 == 0, q 4-byte and w 16-byte aligned, rows * cols / 4 < 2^32.
+constexpr int kDqU = 4;
+__global__ __launch_bounds__(kQB) void k_dequant4(const uint32_t *__restrict__ q, const float *__restrict__ scale,
+                                                  f4 *__restrict__ w, uint32_t n4, IntDiv per_row4) {
+    const uint64_t step = (uint64_t)gridDim.x * kQB * kDqU;
+    for (uint64_t base = (uint64_t)blockIdx.x * kQB * kDqU + threadIdx.x; base < n4; base += step) {
+        uint32_t v[kDqU];
 #pragma unroll
-        for (int k = 0; k < 4; k++) {
-            const int u = words[k];
-            f4 r;
-            r.x = (float)(int8_t)(u & 0xff) * s;
-            r.y = (float)(int8_t)((u >> 8) & 0xff) * s;
-            r.z = (float)(int8_t)((u >> 16) & 0xff) * s;
-            r.w = (float)(int8_t)((u >> 24) & 0xff) * s;
-            __builtin_nontemporal_store(r, o + k);
+        for (int u = 0; u < kDqU; u++) {
+            const uint64_t j = base + (uint64_t)u * kQB;
+            if (j < n4) v[u] = __builtin_nontemporal_load(q + j);
+        }
+#pragma unroll
+        for (int u = 0; u < kDqU; u++) {
+            const uint64_t j = base + (uint64_t)u * kQB;
+            if (j < n4) {
+                const float s = scale[per_row4.div((uint32_t)j)];
+                const uint32_t x = v[u];
+                f4 r;
+                r.x = (float)(int8_t)(x & 0xffu) * s;
+                r.y = (float)(int8_t)((x >> 8) & 0xffu) * s;
+                r.z = (float)(int8_t)((x >> 16) & 0xffu) * s;
+                r.w = (float)(int8_t)(x >> 24) * s;
+                __builtin_nontemporal_store(r, w + j);
+            }
         }
     }
 }
@@ -153,10 +163,10 @@ extern "C" NC_HIP_API int nc_hip_dequantize_rows(int64_t rows, int64_t cols, con
     const int64_t n = rows * cols;
     if (n == 0) return NC_HIP_OK;
     hipStream_t st = as_stream(stream);
-    if (cols % 16 == 0 && aligned16(q) && aligned16(w) && cols / 16 < (int64_t)UINT32_MAX) {
-        const int64_t n16 = n / 16;
-        hipLaunchKernelGGL(k_dequant16, stream_grid(n16, kQB, 16), kQB, 0, st, (const int4 *)q, scale, (f4 *)w, n16,
-                           (uint32_t)(cols / 16));
+    if (cols % 4 == 0 && ((uintptr_t)q & 3u) == 0 && aligned16(w) && n / 4 < (int64_t)UINT32_MAX) {
+        const int64_t n4 = n / 4;
+        hipLaunchKernelGGL(k_dequant4, stream_grid((n4 + kDqU - 1) / kDqU, kQB, 16), kQB, 0, st, (const uint32_t *)q,
+                           scale, (f4 *)w, (uint32_t)n4, IntDiv((uint32_t)(cols / 4)));
     } else {
         hipLaunchKernelGGL(k_dequant1, stream_grid(n, kQB, 16), kQB, 0, st, q, scale, w, n, cols);
     }

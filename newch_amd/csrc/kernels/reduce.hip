@@ -100,13 +100,23 @@ __global__ __launch_bounds__(kRB) void k_rows_wave(const float *__restrict__ x, 
         Acc<KIND> acc;
         acc.init();
         if constexpr (VEC) {
+            // 4 vectors per lane in flight, pushed in increasing index order (argmax tie rule)
             const int64_t nv = R / 4;
-            for (int64_t v = lane; v < nv; v += kWave) {
-                const f4 q = __builtin_nontemporal_load((const f4 *)row + v);
-                acc.push(q.x, (int)(4 * v));
-                acc.push(q.y, (int)(4 * v + 1));
-                acc.push(q.z, (int)(4 * v + 2));
-                acc.push(q.w, (int)(4 * v + 3));
+            for (int64_t v0 = lane; v0 < nv; v0 += 4 * kWave) {
+                f4 q[4];
+#pragma unroll
+                for (int k = 0; k < 4; k++)
+                    if (v0 + k * kWave < nv) q[k] = __builtin_nontemporal_load((const f4 *)row + v0 + k * kWave);
+#pragma unroll
+                for (int k = 0; k < 4; k++) {
+                    const int64_t v = v0 + k * kWave;
+                    if (v < nv) {
+                        acc.push(q[k].x, (int)(4 * v));
+                        acc.push(q[k].y, (int)(4 * v + 1));
+                        acc.push(q[k].z, (int)(4 * v + 2));
+                        acc.push(q[k].w, (int)(4 * v + 3));
+                    }
+                }
             }
         } else {
             for (int64_t r = lane; r < R; r += kWave) acc.push(row[r], (int)r);

@@ -432,16 +432,36 @@ __global__ __launch_bounds__(kRowB) void k_ln_cols_part(const float *__restrict_
     }
 }
 
-__global__ __launch_bounds__(kRowB) void k_ln_cols_combine(const double *__restrict__ part, float *__restrict__ gw,
-                                                           float *__restrict__ gb, int64_t D, int P) {
-    for (int64_t i = (int64_t)blockIdx.x * kRowB + threadIdx.x; i < D; i += (int64_t)gridDim.x * kRowB) {
-        double sw = 0.0, sb = 0.0;
-        for (int p = 0; p < P; p++) {
+// gw[i] (+)= sum_p part[p][0][i], gb[i] (+)= sum_p part[p][1][i] in a fixed order: a 64 x 16 thread
+// block covers 64 columns; slice y sums partials y, y + 16, y + 32, ... in order, then slice 0 adds
+// the 16 slice sums in slice order.
+constexpr int kCombCols = 64, kCombSlices = 16;
+__global__ __launch_bounds__(kCombCols *kCombSlices) void k_ln_cols_combine(const double *__restrict__ part,
+                                                                            float *__restrict__ gw,
+                                                                            float *__restrict__ gb, int64_t D, int P) {
+    __shared__ double shw[kCombSlices][kCombCols], shb[kCombSlices][kCombCols];
+    const int x = threadIdx.x % kCombCols, y = threadIdx.x / kCombCols;
+    const int64_t i = (int64_t)blockIdx.x * kCombCols + x;
+    double sw = 0.0, sb = 0.0;
+    if (i < D) {
+#pragma unroll 8
+        for (int p = y; p < P; p += kCombSlices) {
             sw += part[(size_t)p * 2 * D + i];
             sb += part[(size_t)p * 2 * D + D + i];
         }
-        if (gw) gw[i] = (float)((double)gw[i] + sw);
-        if (gb) gb[i] = (float)((double)gb[i] + sb);
+    }
+    shw[y][x] = sw;
+    shb[y][x] = sb;
+    __syncthreads();
+    if (y == 0 && i < D) {
+        double tw = 0.0, tb = 0.0;
+#pragma unroll
+        for (int k = 0; k < kCombSlices; k++) {
+            tw += shw[k][x];
+            tb += shb[k][x];
+        }
+        if (gw) gw[i] = (float)((double)gw[i] + tw);
+        if (gb) gb[i] = (float)((double)gb[i] + tb);
     }
 }
 
@@ -588,7 +608,7 @@ extern "C" NC_HIP_API int nc_hip_layer_norm_bwd(int64_t rows, int64_t D, const f
         else
             NC_VPL_SWITCH(p.vpl, hipLaunchKernelGGL((k_ln_bwd_reg<VP, false>), dim3(p.blocks), kRowB, lds, st, x, w, stats, g, gx, part, rows, (int)D, p.rows_per_block))
         if (cols)
-            hipLaunchKernelGGL(k_ln_cols_combine, stream_grid(D, kRowB), kRowB, 0, st, part, gw, gb, D, (int)p.blocks);
+            hipLaunchKernelGGL(k_ln_cols_combine, dim3((D + kCombCols - 1) / kCombCols), kCombCols * kCombSlices, 0, st, part, gw, gb, D, (int)p.blocks);
     } else {
         const unsigned grid = (unsigned)(rows < num_cus() * 8 ? rows : num_cus() * 8);
         if (gx) {
@@ -598,7 +618,7 @@ extern "C" NC_HIP_API int nc_hip_layer_norm_bwd(int64_t rows, int64_t D, const f
         if (cols) {
             hipLaunchKernelGGL(k_ln_cols_part, stream_grid(D * p.P, kRowB), kRowB, 0, st, x, stats, g, part, rows, D,
                                p.chunk, p.P);
-            hipLaunchKernelGGL(k_ln_cols_combine, stream_grid(D, kRowB), kRowB, 0, st, part, gw, gb, D, p.P);
+            hipLaunchKernelGGL(k_ln_cols_combine, dim3((D + kCombCols - 1) / kCombCols), kCombCols * kCombSlices, 0, st, part, gw, gb, D, p.P);
         }
     }
     return check_launch("nc_hip_layer_norm_bwd");

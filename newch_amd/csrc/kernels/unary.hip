@@ -76,13 +76,35 @@ __device__ __forceinline__ float act_bwd(float gi, float v, float y, float g, fl
     }
 }
 
+// Launch shape: 256-lane workgroups, NC_UNARY_UNROLL independent 128-bit vectors in flight per lane,
+// NC_UNARY_GRID_PER_CU workgroups per CU (grid-stride beyond that); non-temporal hints on the
+// streamed loads / stores.  Defaults chosen by sweeping them on MI355X.
+#ifndef NC_UNARY_UNROLL
+#define NC_UNARY_UNROLL 4
+#endif
+#ifndef NC_UNARY_GRID_PER_CU
+#define NC_UNARY_GRID_PER_CU 8
+#endif
+#ifndef NC_UNARY_NT_LOAD
+#define NC_UNARY_NT_LOAD 1
+#endif
+#ifndef NC_UNARY_NT_STORE
+#define NC_UNARY_NT_STORE 1
+#endif
+
 constexpr int kBlock = 256;
-constexpr int kUnroll = 4;
+constexpr int kUnroll = NC_UNARY_UNROLL;
 
 template <typename T>
-__device__ __forceinline__ T ld_nt(const T *p) { return __builtin_nontemporal_load(p); }
+__device__ __forceinline__ T ld_nt(const T *p) {
+    if constexpr (NC_UNARY_NT_LOAD) return __builtin_nontemporal_load(p);
+    else return *p;
+}
 template <typename T>
-__device__ __forceinline__ void st_nt(T v, T *p) { __builtin_nontemporal_store(v, p); }
+__device__ __forceinline__ void st_nt(T v, T *p) {
+    if constexpr (NC_UNARY_NT_STORE) __builtin_nontemporal_store(v, p);
+    else *p = v;
+}
 
 template <int K>
 __global__ __launch_bounds__(kBlock) void k_unary_fwd(const f4 *__restrict__ x, f4 *__restrict__ y, int64_t nvec,
@@ -169,7 +191,7 @@ template <int K>
 static int launch_fwd(float s, const float *x, float *y, int64_t n, hipStream_t st) {
     const int64_t nvec = (aligned16(x) && aligned16(y)) ? n / 4 : 0;
     if (nvec > 0) {
-        hipLaunchKernelGGL(k_unary_fwd<K>, dim3(stream_grid((nvec + kUnroll - 1) / kUnroll, kBlock)), dim3(kBlock), 0,
+        hipLaunchKernelGGL(k_unary_fwd<K>, dim3(stream_grid((nvec + kUnroll - 1) / kUnroll, kBlock, NC_UNARY_GRID_PER_CU)), dim3(kBlock), 0,
                            st, (const f4 *)x, (f4 *)y, nvec, s);
     }
     const int64_t done = nvec * 4;
@@ -185,7 +207,7 @@ static int launch_bwd2(float s, const float *x, const float *y, const float *g, 
     const bool al = (!x || aligned16(x)) && (!y || aligned16(y)) && aligned16(g) && aligned16(gi);
     const int64_t nvec = al ? n / 4 : 0;
     if (nvec > 0) {
-        hipLaunchKernelGGL((k_unary_bwd<K, ACC>), dim3(stream_grid((nvec + kUnroll - 1) / kUnroll, kBlock)),
+        hipLaunchKernelGGL((k_unary_bwd<K, ACC>), dim3(stream_grid((nvec + kUnroll - 1) / kUnroll, kBlock, NC_UNARY_GRID_PER_CU)),
                            dim3(kBlock), 0, st, (const f4 *)x, (const f4 *)y, (const f4 *)g, (f4 *)gi, nvec, s);
     }
     const int64_t done = nvec * 4;

@@ -6,7 +6,7 @@ Two levels:
   * through the nc_hip.h kernel layer on device buffers at larger, ragged and misaligned sizes,
     against oracle/_build/liboracle.so on the same seeded inputs.
 
-Bars (BASELINE north star): bit-exact for IEEE elementwise arithmetic, activations (the AVX2 tier's
+Bars: bit-exact for IEEE elementwise arithmetic, activations (the AVX2 tier's
 transcendentals are replicated op for op, so 0 ulp rather than the allowed 2), argmax/max, int8
 quantize/dequantize and every gradient that is not a reduction; reductions, softmax, LayerNorm and
 sum-to-shape gradients within 1e-5 relative against fp64, measured as
@@ -446,6 +446,49 @@ def test_kernel_binary(K, case, ash, aview, bsh, op):
             red = sum_to(t, x.shape).reshape(x.shape)
             scale = sum_to(np.abs(t), x.shape).reshape(x.shape) / np.sqrt(max(t.size // max(red.size, 1), 1))
             assert_close64(got, init + red, scale + np.abs(init), f"{case} {op} grad {which}")
+
+
+BWD2 = [
+    ("cfg2_T2", (8, 32, 1, 64), None, (1, 1, 64, 64)),
+    ("cfg2_T16", (4, 5, 1, 64), None, (1, 1, 512, 64)),
+    ("w128", (3, 7, 1, 128), None, (1, 1, 64, 128)),
+    ("w8", (6, 1, 8), None, (1, 512, 8)),
+    ("batch_t", (8, 4, 1, 64), ("t", 0, 1), (1, 1, 64, 64)),
+    ("fallback_h48", (4, 8, 1, 64), None, (1, 1, 48, 64)),
+]
+
+
+@pytest.mark.parametrize("case,ash,aview,bsh", BWD2)
+@pytest.mark.parametrize("op", ["add", "sub", "mul", "div"])
+@pytest.mark.parametrize("accumulate", [True, False])
+def test_kernel_binary_bwd_fused(K, case, ash, aview, bsh, op, accumulate):
+    """Both operand gradients from one pass over g (the broadcast backward of a[..., 1, W] op b[H, W])."""
+    rng = np.random.default_rng(zlib.crc32(f"bwd2/{case}/{op}/{accumulate}".encode()))
+    A = rng.standard_normal(ash).astype(np.float32)
+    B = (0.5 + 1.5 * rng.random(bsh)).astype(np.float32)
+    a = np_view(A, aview)
+    out_shape = O.broadcast_shape(a.shape, B.shape)
+    G = rng.standard_normal(out_shape).astype(np.float32)
+    sa = bcast_strides(a.shape, strides_of(a), out_shape)
+    sb = bcast_strides(B.shape, strides_of(B), out_shape)
+    so = [s // 4 for s in np.empty(out_shape, np.float32).strides]
+    sga = bcast_strides(a.shape, [s // 4 for s in np.empty(a.shape, np.float32).strides], out_shape)
+    sgb = bcast_strides(B.shape, [s // 4 for s in np.empty(B.shape, np.float32).strides], out_shape)
+    ia = rng.standard_normal(a.shape).astype(np.float32)
+    ib = rng.standard_normal(B.shape).astype(np.float32)
+    Ad, Bd, Gd, GA, GB = dev(A), dev(B), dev(G), dev(ia), dev(ib)
+    wsb = K.binary_bwd2_workspace(out_shape, sga, sgb)
+    ws = empty(max(wsb, 1))
+    K.binary_bwd2(op, out_shape, Gd.ptr, so, Ad.ptr, sa, Bd.ptr, sb, GA.ptr, sga, GB.ptr, sgb, ws.ptr, wsb,
+                  accumulate=accumulate)
+    sync()
+    ta, tb = grad_terms64(op, a, B, G)
+    for name, got, t, init, x in (("a", GA.to_numpy(np.float32, a.shape), ta, ia, a),
+                                  ("b", GB.to_numpy(np.float32, B.shape), tb, ib, B)):
+        red = sum_to(t, x.shape).reshape(x.shape)
+        base = init.astype(np.float64) if accumulate else 0.0
+        scale = sum_to(np.abs(t), x.shape).reshape(x.shape) / np.sqrt(max(t.size // max(red.size, 1), 1))
+        assert_close64(got, base + red, scale + (np.abs(init) if accumulate else 0), f"{case} {op} grad {name}")
 
 
 REDUCE_SHAPES = [((4096, 1024), 1), ((3, 1 << 20), 1), ((64, 1000, 33), 1), ((2, 5000, 3), 1), ((1 << 22,), None),
