@@ -530,98 +530,155 @@ static int prepare_grad(int op, int which, int nd, const int64_t *shape, const i
 // ------------------------------------------------------------------------------------------------
 // Fused backward of both operands (one pass over g) for the pattern
 //     g[P..., H, W] (contiguous),  a[P..., 1, W] (broadcast over H),  b[H, W] (broadcast over P...)
-// i.e. grad_a = sum over H, grad_b = sum over the plane dims.  A 512-lane workgroup owns whole
-// [H, W] planes: lane t holds float4 columns q = t + 512 k (k < T, T = H*W/2048 <= 16), all in the
-// same column group w4 = t mod W4 (W4 = W/4 divides 64).  Per plane, grad_a[p, :] is reduced across
-// the lanes sharing w4 (wave shuffles, then LDS across the 8 waves, in a fixed order) and written;
-// grad_b accumulates in fp64 registers over the workgroup's planes and is written once as a
-// partial, combined by k_bwd2_gb_combine in workgroup order.  MODE: 0 add/sub, 1 mul, 3 div.
+// i.e. grad_a = sum over H, grad_b = sum over the plane dims.
+//   * A plane of H*W/4 float4 is cut into NBAND row bands of 512*T float4 (T <= NC_B2_TMAX); a
+//     512-lane workgroup owns one band of a range of planes.  Lane t holds float4 q = t + 512 k
+//     (k < T) of the band, all in column group w4 = t mod W4 (W4 = W/4 divides 64).
+//   * g: the T loads of the next plane are issued before the current plane is summed.
+//   * grad_b accumulates in fp64 registers (T x 4 per lane) over the workgroup's planes and is written
+//     once as a partial, combined by k_bwd2_gb_combine in plane-range order.
+//   * b (mul) or its fp32 reciprocal (div) stays in registers.  Each term is an fp32 product, as in
+//     the unreduced gradient (g*b, g*a; g*(1/b) is within 1 ulp of g/b), and the sums run in fp64.
+//   * grad_a: per plane, lanes sharing w4 are reduced by wave shuffles; the 8 wave partials of a
+//     group of NB = 64 / W4 planes wait in LDS, and after one barrier per group a lane per (plane,
+//     column) adds them in wave order.  With one band that sum completes grad_a; with several it is an
+//     fp64 partial that k_bwd2_ga_combine adds up in band order.
+// MODE: 0 add/sub, 1 mul, 3 div.
 // ------------------------------------------------------------------------------------------------
+#ifndef NC_B2_TMAX
+#define NC_B2_TMAX 4
+#endif
+#ifndef NC_B2_BLOCKS_PER_CU
+#define NC_B2_BLOCKS_PER_CU 2
+#endif
 constexpr int kB2 = 512;
 constexpr int kB2Waves = kB2 / kWave;
-constexpr int kB2MaxT = 16;
+constexpr int kB2MaxBand = 16;  // bands per plane: planes up to 16 * 512 * NC_B2_TMAX float4
+constexpr int kB2GroupDoubles = kB2Waves * 4 * 64;
 
 struct Bwd2Plan {
-    uint32_t P, H, W4, T;
-    uint32_t planes_per_block;
+    uint32_t P, H, W4, T, nband;
+    uint32_t ranges, planes_per_block;
     IdxMap<1> amap;  // element offset of a[p, 0, 0] over the plane dims
-    int64_t ga_row;  // element offset step of grad_a per plane (its contiguous stride: W)
 };
 
-template <int MODE, bool ACC>
-__global__ __launch_bounds__(kB2) void k_bcast_bwd2(const float *__restrict__ g, const float *__restrict__ a,
+// two resident workgroups per CU (4 waves per SIMD): at most 128 VGPRs
+template <int MODE, bool ACC, int T>
+__global__ __launch_bounds__(kB2, 4) void k_bcast_bwd2(const float *__restrict__ g, const float *__restrict__ a,
                                                     const float *__restrict__ b, float *__restrict__ ga,
-                                                    double *__restrict__ gb_part, Bwd2Plan pl, double alpha_b) {
-    __shared__ double sh[kB2Waves][64][4];
+                                                    double *__restrict__ ga_part, double *__restrict__ gb_part,
+                                                    Bwd2Plan pl, double alpha_b) {
+    constexpr uint32_t band4 = kB2 * T;  // float4 per band
+    __shared__ double sh[kB2GroupDoubles];  // [NB][8 waves][W4][4]
     const int tid = threadIdx.x, lane = tid & (kWave - 1), wv = tid / kWave;
-    const uint32_t W4 = pl.W4, T = pl.T;
+    const uint32_t W4 = pl.W4, nband = pl.nband;
+    const uint32_t NB = 64 / W4;
     const uint32_t w4 = tid % W4;
-    const uint32_t plane4 = pl.H * W4;  // float4 per plane (= kB2 * T)
-    const uint32_t p0 = blockIdx.x * pl.planes_per_block;
-    const uint32_t p1 = min(pl.P, p0 + pl.planes_per_block);
-    double accb[kB2MaxT][4];
+    const uint32_t band = blockIdx.x % nband, range = blockIdx.x / nband;
+    const uint32_t plane4 = band4 * nband;
+    const uint32_t p0 = range * pl.planes_per_block;
+    const uint32_t p1 = min(pl.P, p0 + pl.planes_per_block);  // the launch has p0 < P for every workgroup
+    const uint32_t qb = band * band4 + tid;                    // this lane's first float4 in a plane
+    f4 bv[T];
 #pragma unroll
-    for (int k = 0; k < kB2MaxT; k++) accb[k][0] = accb[k][1] = accb[k][2] = accb[k][3] = 0.0;
-    for (uint32_t p = p0; p < p1; p++) {
-        const f4 *gp = (const f4 *)(g + (size_t)p * plane4 * 4);
-        f4 av = f4{0.f, 0.f, 0.f, 0.f};
-        if constexpr (MODE == 1 || MODE == 3) {
-            int64_t off[1];
-            offsets<1>(pl.amap, p, off);
-            av = *(const f4 *)(a + off[0] + 4 * w4);
-        }
-        double sa[4] = {0.0, 0.0, 0.0, 0.0};
+    for (int k = 0; k < T; k++) {
+        bv[k] = f4{1.f, 1.f, 1.f, 1.f};
+        if constexpr (MODE != 0) bv[k] = ((const f4 *)b)[qb + kB2 * k];
+        if constexpr (MODE == 3) bv[k] = f4{1.0f / bv[k].x, 1.0f / bv[k].y, 1.0f / bv[k].z, 1.0f / bv[k].w};
+    }
+    double accb[T][4];
 #pragma unroll
-        for (int k = 0; k < kB2MaxT; k++) {
-            if ((uint32_t)k < T) {
-                const uint32_t q = tid + kB2 * k;
-                const f4 gv = __builtin_nontemporal_load(gp + q);
-                f4 bv = f4{1.f, 1.f, 1.f, 1.f};
-                if constexpr (MODE != 0) bv = ((const f4 *)b)[q];
-                const float gg[4] = {gv.x, gv.y, gv.z, gv.w};
-                const float bb[4] = {bv.x, bv.y, bv.z, bv.w};
+    for (int k = 0; k < T; k++) accb[k][0] = accb[k][1] = accb[k][2] = accb[k][3] = 0.0;
+    f4 cur[T];
+    {
+        const f4 *gp = (const f4 *)g + (size_t)p0 * plane4 + qb;
+#pragma unroll
+        for (int k = 0; k < T; k++) cur[k] = __builtin_nontemporal_load(gp + kB2 * k);
+    }
+    for (uint32_t pg = p0; pg < p1; pg += NB) {
+        const uint32_t nb = min(NB, p1 - pg);
+        for (uint32_t j = 0; j < nb; j++) {
+            const uint32_t p = pg + j;
+            // next plane's loads first (the last plane loads itself again: in bounds, unused)
+            f4 nxt[T];
+            {
+                const f4 *gn = (const f4 *)g + (size_t)min(p + 1, p1 - 1) * plane4 + qb;
+#pragma unroll
+                for (int k = 0; k < T; k++) nxt[k] = __builtin_nontemporal_load(gn + kB2 * k);
+            }
+            f4 av = f4{0.f, 0.f, 0.f, 0.f};
+            if constexpr (MODE == 1 || MODE == 3) {
+                int64_t off[1];
+                offsets<1>(pl.amap, p, off);
+                av = *(const f4 *)(a + off[0] + 4 * w4);
+            }
+            double sa[4] = {0.0, 0.0, 0.0, 0.0};
+#pragma unroll
+            for (int k = 0; k < T; k++) {
+                const float gg[4] = {cur[k].x, cur[k].y, cur[k].z, cur[k].w};
+                const float bb[4] = {bv[k].x, bv[k].y, bv[k].z, bv[k].w};
                 const float aa[4] = {av.x, av.y, av.z, av.w};
 #pragma unroll
                 for (int c = 0; c < 4; c++) {
-                    const double gd = (double)gg[c];
-                    // grad_a term: g (add, sub), g*b (mul), g/b (div)
-                    sa[c] += MODE == 0 ? gd : MODE == 1 ? gd * (double)bb[c] : gd / (double)bb[c];
+                    // terms are the fp32 products the unreduced gradient holds, summed in fp64
+                    // grad_a term: g (add, sub), g*b (mul), g*(1/b) (div)
+                    sa[c] += (double)(MODE == 0 ? gg[c] : gg[c] * bb[c]);
                     // grad_b term before the per-column factor: g (add, sub), g*a (mul, div)
-                    accb[k][c] += (MODE == 1 || MODE == 3) ? gd * (double)aa[c] : gd;
+                    accb[k][c] += (double)((MODE == 1 || MODE == 3) ? gg[c] * aa[c] : gg[c]);
                 }
             }
-        }
-        // lanes sharing w4 inside the wave, then the 8 waves in order
-        for (uint32_t o = W4; o < (uint32_t)kWave; o <<= 1) {
 #pragma unroll
-            for (int c = 0; c < 4; c++) sa[c] += __shfl_xor(sa[c], (int)o, kWave);
-        }
-        if ((uint32_t)lane < W4) {
+            for (int k = 0; k < T; k++) cur[k] = nxt[k];
+            // lanes sharing w4 inside the wave; the wave's partial goes to LDS slot (j, wv)
+            for (uint32_t o = W4; o < (uint32_t)kWave; o <<= 1) {
 #pragma unroll
-            for (int c = 0; c < 4; c++) sh[wv][lane][c] = sa[c];
+                for (int c = 0; c < 4; c++) sa[c] += __shfl_xor(sa[c], (int)o, kWave);
+            }
+            if ((uint32_t)lane < W4) {
+                double *d = sh + ((j * kB2Waves + wv) * W4 + lane) * 4;
+#pragma unroll
+                for (int c = 0; c < 4; c++) d[c] = sa[c];
+            }
         }
         __syncthreads();
-        if ((uint32_t)tid < W4 * 4) {
-            const uint32_t col = tid / 4, c = tid % 4;
-            double t = 0.0;
-            for (int w = 0; w < kB2Waves; w++) t += sh[w][col][c];
-            float *dst = ga + (size_t)p * pl.ga_row + 4 * col + c;
-            *dst = (float)((ACC ? (double)*dst : 0.0) + t);
+        {
+            // lane -> (plane j, column col, component c) of the group; the 8 waves added in order
+            const uint32_t c = tid % 4, col = (tid / 4) % W4, j = tid / (4 * W4);
+            if (j < nb) {
+                double t = 0.0;
+#pragma unroll
+                for (int w = 0; w < kB2Waves; w++) t += sh[((j * kB2Waves + w) * W4 + col) * 4 + c];
+                const size_t e = (size_t)(pg + j) * (4 * W4) + 4 * col + c;  // grad_a element
+                if (nband == 1) ga[e] = (float)((ACC ? (double)ga[e] : 0.0) + t);
+                else ga_part[(size_t)(pg + j) * nband * 4 * W4 + band * 4 * W4 + 4 * col + c] = t;
+            }
         }
         __syncthreads();
     }
-    double *out = gb_part + (size_t)blockIdx.x * plane4 * 4;
+    double *out = gb_part + (size_t)range * plane4 * 4;
 #pragma unroll
-    for (int k = 0; k < kB2MaxT; k++) {
-        if ((uint32_t)k < T) {
-            const uint32_t q = tid + kB2 * k;
+    for (int k = 0; k < T; k++) {
+        const uint32_t q = qb + kB2 * k;
 #pragma unroll
-            for (int c = 0; c < 4; c++) out[4 * q + c] = accb[k][c] * alpha_b;
-        }
+        for (int c = 0; c < 4; c++) out[4 * q + c] = accb[k][c] * alpha_b;
     }
 }
 
-// grad_b[e] (+)= factor(e) * sum over workgroups of part[wg][e], workgroups in order (64 x 16 lanes)
+// grad_a[e] (+)= sum over bands of part[p][band][w] (e = p * W + w), bands in order
+template <bool ACC>
+__global__ __launch_bounds__(kB) void k_bwd2_ga_combine(const double *__restrict__ part, float *__restrict__ ga,
+                                                        uint32_t n, uint32_t W, uint32_t nband) {
+    const uint32_t step = gridDim.x * kB;
+    for (uint32_t e = blockIdx.x * kB + threadIdx.x; e < n; e += step) {
+        const uint32_t p = e / W, w = e - p * W;
+        const double *src = part + (size_t)p * nband * W + w;
+        double t = 0.0;
+        for (uint32_t k = 0; k < nband; k++) t += src[(size_t)k * W];
+        ga[e] = (float)((ACC ? (double)ga[e] : 0.0) + t);
+    }
+}
+
+// grad_b[e] (+)= factor(e) * sum over plane ranges of part[r][e], ranges in order (64 x 16 lanes)
 template <int MODE, bool ACC>
 __global__ __launch_bounds__(1024) void k_bwd2_gb_combine(const double *__restrict__ part, const float *__restrict__ b,
                                                           float *__restrict__ gb, uint32_t n, uint32_t nparts) {
@@ -654,7 +711,14 @@ static bool plan_bwd2(const Prepared &p, const float *g, const float *a, const f
     if (p.nd < 3 || p.numel >= (int64_t)UINT32_MAX) return false;
     const int h = p.nd - 2, w = p.nd - 1;
     const int64_t H = p.shape[h], W = p.shape[w];
-    if (W % 4 || 64 % (W / 4) || (H * (W / 4)) % kB2 || H * (W / 4) / kB2 > kB2MaxT) return false;
+    if (W % 4 || 64 % (W / 4) || (H * (W / 4)) % kB2) return false;
+    int64_t T = H * (W / 4) / kB2, nband = 1;  // float4 per lane per plane
+    if (T & (T - 1)) return false;
+    while (T > NC_B2_TMAX) {
+        T /= 2;
+        nband *= 2;
+    }
+    if (nband > kB2MaxBand) return false;
     // g contiguous; a: stride 0 over H, 1 over W; b: [H, W] contiguous, 0 over planes;
     // ga: 0 over H, 1 over W, contiguous rows of W over planes; gb: [H, W] contiguous, 0 over planes
     if (p.st[0][w] != 1 || p.st[0][h] != W) return false;
@@ -682,16 +746,21 @@ static bool plan_bwd2(const Prepared &p, const float *g, const float *a, const f
     pl.P = (uint32_t)P;
     pl.H = (uint32_t)H;
     pl.W4 = (uint32_t)(W / 4);
-    pl.T = (uint32_t)(H * (W / 4) / kB2);
-    const uint32_t blocks = (uint32_t)std::min<int64_t>(P, num_cus());
-    pl.planes_per_block = (uint32_t)((P + blocks - 1) / blocks);
-    pl.ga_row = W;
+    pl.T = (uint32_t)T;
+    pl.nband = (uint32_t)nband;
+    const int64_t want = std::max<int64_t>(1, (int64_t)num_cus() * NC_B2_BLOCKS_PER_CU / nband);
+    const int64_t ranges = std::min<int64_t>(P, want);
+    pl.planes_per_block = (uint32_t)((P + ranges - 1) / ranges);
+    pl.ranges = (uint32_t)((P + pl.planes_per_block - 1) / pl.planes_per_block);
     return true;
 }
 
+// workspace: grad_b partials [ranges][H*W], then (several bands) grad_a partials [P][nband][W]
+static size_t bwd2_gb_bytes(const Bwd2Plan &pl) { return (size_t)pl.ranges * pl.H * pl.W4 * 4 * sizeof(double); }
 static size_t bwd2_ws(const Bwd2Plan &pl) {
-    const uint32_t blocks = (pl.P + pl.planes_per_block - 1) / pl.planes_per_block;
-    return (size_t)blocks * pl.H * pl.W4 * 4 * sizeof(double);
+    size_t n = bwd2_gb_bytes(pl);
+    if (pl.nband > 1) n += (size_t)pl.P * pl.nband * pl.W4 * 4 * sizeof(double);
+    return n;
 }
 
 template <int MODE>
@@ -700,13 +769,37 @@ static int launch_bwd2(const float *g, const float *a, const float *b, float *ga
     const size_t need = bwd2_ws(pl);
     if (ws_bytes < need || !ws)
         return set_error(NC_HIP_ERR_WORKSPACE, "binary_bwd2: workspace of %zu bytes needed, %zu given", need, ws_bytes);
-    const uint32_t blocks = (pl.P + pl.planes_per_block - 1) / pl.planes_per_block;
-    double *part = (double *)ws;
-    if (acc) hipLaunchKernelGGL((k_bcast_bwd2<MODE, true>), dim3(blocks), dim3(kB2), 0, st, g, a, b, ga, part, pl, alpha_b);
-    else hipLaunchKernelGGL((k_bcast_bwd2<MODE, false>), dim3(blocks), dim3(kB2), 0, st, g, a, b, ga, part, pl, alpha_b);
+    const uint32_t blocks = pl.ranges * pl.nband;
+    double *gb_part = (double *)ws;
+    double *ga_part = pl.nband > 1 ? (double *)((char *)ws + bwd2_gb_bytes(pl)) : nullptr;
+#define NC_B2_LAUNCH(TT)                                                                                          \
+    if (acc)                                                                                                      \
+        hipLaunchKernelGGL((k_bcast_bwd2<MODE, true, TT>), dim3(blocks), dim3(kB2), 0, st, g, a, b, ga, ga_part,  \
+                           gb_part, pl, alpha_b);                                                                 \
+    else                                                                                                          \
+        hipLaunchKernelGGL((k_bcast_bwd2<MODE, false, TT>), dim3(blocks), dim3(kB2), 0, st, g, a, b, ga, ga_part, \
+                           gb_part, pl, alpha_b)
+    switch (pl.T) {
+    case 1: NC_B2_LAUNCH(1); break;
+    case 2: NC_B2_LAUNCH(2); break;
+#if NC_B2_TMAX >= 4
+    case 4: NC_B2_LAUNCH(4); break;
+#endif
+#if NC_B2_TMAX >= 8
+    case 8: NC_B2_LAUNCH(8); break;
+#endif
+    default: return set_error(NC_HIP_ERR_ARG, "binary_bwd2: unsupported plan");
+    }
+#undef NC_B2_LAUNCH
+    if (pl.nband > 1) {
+        const uint32_t n = pl.P * pl.W4 * 4;
+        const unsigned grid = stream_grid(n, kB);
+        if (acc) hipLaunchKernelGGL((k_bwd2_ga_combine<true>), dim3(grid), dim3(kB), 0, st, ga_part, ga, n, pl.W4 * 4, pl.nband);
+        else hipLaunchKernelGGL((k_bwd2_ga_combine<false>), dim3(grid), dim3(kB), 0, st, ga_part, ga, n, pl.W4 * 4, pl.nband);
+    }
     const uint32_t n = pl.H * pl.W4 * 4;
-    if (acc) hipLaunchKernelGGL((k_bwd2_gb_combine<MODE, true>), dim3((n + 63) / 64), dim3(1024), 0, st, part, b, gb, n, blocks);
-    else hipLaunchKernelGGL((k_bwd2_gb_combine<MODE, false>), dim3((n + 63) / 64), dim3(1024), 0, st, part, b, gb, n, blocks);
+    if (acc) hipLaunchKernelGGL((k_bwd2_gb_combine<MODE, true>), dim3((n + 63) / 64), dim3(1024), 0, st, gb_part, b, gb, n, pl.ranges);
+    else hipLaunchKernelGGL((k_bwd2_gb_combine<MODE, false>), dim3((n + 63) / 64), dim3(1024), 0, st, gb_part, b, gb, n, pl.ranges);
     return check_launch("nc_hip_binary_bwd2");
 }
 

@@ -454,7 +454,9 @@ BWD2 = [
     ("w128", (3, 7, 1, 128), None, (1, 1, 64, 128)),
     ("w8", (6, 1, 8), None, (1, 512, 8)),
     ("batch_t", (8, 4, 1, 64), ("t", 0, 1), (1, 1, 64, 64)),
+    ("bands8", (3, 1, 64), None, (1, 1024, 64)),
     ("fallback_h48", (4, 8, 1, 64), None, (1, 1, 48, 64)),
+    ("fallback_bands32", (2, 1, 64), None, (1, 4096, 64)),
 ]
 
 
