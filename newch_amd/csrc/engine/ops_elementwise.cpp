@@ -29,13 +29,26 @@ static nc_status binary_infer(nc_node *n, nc_dtype *dt, int *nd, int64_t *shape)
     return NC_OK;
 }
 
+// Device address and broadcast strides of operand x of output o.  An operand that the output reuses
+// at least 4 times over but whose innermost stride is not 1 (a transposed view) is first gathered
+// into contiguous arena memory: the broadcast kernels then read it with 128-bit loads rather than
+// one cache line per element.
+static float *operand(nc_tensor *x, const nc_tensor *o, int64_t *sx) {
+    const bool strided_inner = x->ndim > 0 && x->shape[x->ndim - 1] > 1 && x->stride[x->ndim - 1] != 1;
+    if (strided_inner && 4 * nc_numel(x) <= nc_numel(o)) {
+        float *p = contig_f32(x);
+        if (p) bcast_strides_shape(x->ndim, x->shape, o->ndim, o->shape, sx);
+        return p;
+    }
+    bcast_strides(x, o->ndim, o->shape, sx);
+    return fptr(x);
+}
+
 static nc_status binary_fwd(nc_node *n) {
     nc_tensor *a = n->in[0], *b = n->in[1], *o = n->out;
     nc_ctx *ctx = o->ctx;
     int64_t sa[NC_MAX_DIMS], sb[NC_MAX_DIMS];
-    bcast_strides(a, o->ndim, o->shape, sa);
-    bcast_strides(b, o->ndim, o->shape, sb);
-    float *pa = fptr(a), *pb = fptr(b), *po = fptr(o);
+    float *pa = operand(a, o, sa), *pb = operand(b, o, sb), *po = fptr(o);
     if (!pa || !pb || !po) return NC_ERR_STATE;
     if (!hip_layer_ok(ctx, nc_hip_binary_fwd(n->op->kind, o->ndim, o->shape, pa, sa, pb, sb, po, o->stride, stream(ctx)),
                       n->op->name))
@@ -49,9 +62,7 @@ static void binary_bwd(nc_node *n) {
     nc_ctx *ctx = o->ctx;
     const int nd = o->ndim;
     int64_t sa[NC_MAX_DIMS], sb[NC_MAX_DIMS];
-    bcast_strides(a, nd, o->shape, sa);
-    bcast_strides(b, nd, o->shape, sb);
-    float *g = fptr(o->grad), *pa = fptr(a), *pb = fptr(b);
+    float *g = fptr(o->grad), *pa = operand(a, o, sa), *pb = operand(b, o, sb);
     if (!g || !pa || !pb) return;
     if (needs_grad(a) && needs_grad(b) && a != b && !same_shape(a, o) && !same_shape(b, o)) {
         // both operands are reduced: one pass over g for both gradients (nc_hip_binary_bwd2)

@@ -84,6 +84,9 @@ struct VecModes {
 #ifndef NC_BIN_GRID_PER_CU
 #define NC_BIN_GRID_PER_CU 16
 #endif
+#ifndef NC_BIN_NT_STORE
+#define NC_BIN_NT_STORE 1
+#endif
 constexpr int kBU = NC_BIN_UNROLL;
 
 template <int OP, bool VEC>
@@ -114,7 +117,8 @@ __global__ __launch_bounds__(kB) void k_binary_fwd(const float *__restrict__ a, 
                     r.y = bin<OP>(x[u].y, y[u].y);
                     r.z = bin<OP>(x[u].z, y[u].z);
                     r.w = bin<OP>(x[u].w, y[u].w);
-                    __builtin_nontemporal_store(r, (f4 *)(o + oo[u]));
+                    if constexpr (NC_BIN_NT_STORE) __builtin_nontemporal_store(r, (f4 *)(o + oo[u]));
+                    else *(f4 *)(o + oo[u]) = r;
                 }
             }
         } else {
@@ -899,11 +903,13 @@ extern "C" NC_HIP_API int nc_hip_binary_bwd2(int op, int nd, const int64_t *shap
                                              void *stream) {
     if (op < 0 || op > 3) return set_error(NC_HIP_ERR_ARG, "nc_hip_binary_bwd2: bad op");
     if (ga && gb) {
+        // add / sub read neither operand: plan with the gradients' layouts in their place
+        const bool reads_ab = op == NC_HIP_BIN_MUL || op == NC_HIP_BIN_DIV;
         Prepared p;
-        int rc = prepare_bwd2(nd, shape, sg, sa, sb, sga, sgb, p);
+        int rc = prepare_bwd2(nd, shape, sg, reads_ab ? sa : sga, reads_ab ? sb : sgb, sga, sgb, p);
         if (rc) return rc;
         Bwd2Plan pl;
-        if (p.numel > 0 && plan_bwd2(p, g, a, b, ga, gb, pl)) {
+        if (p.numel > 0 && plan_bwd2(p, g, reads_ab ? a : ga, reads_ab ? b : gb, ga, gb, pl)) {
             hipStream_t st = as_stream(stream);
             const double alpha_b = op == NC_HIP_BIN_SUB ? -1.0 : 1.0;
             switch (op) {

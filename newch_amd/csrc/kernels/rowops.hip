@@ -290,15 +290,20 @@ __global__ __launch_bounds__(kRowB) void k_ln_fwd_blk(const float *__restrict__ 
     }
 }
 
-// Backward, register rows.  Each workgroup owns a contiguous range of rows; its 4 waves take rows
-// round-robin, accumulate the gw / gb column partials of their rows in registers, combine them in
-// LDS in wave order and write one fp64 partial per workgroup; k_ln_cols_combine adds the workgroup
-// partials in workgroup order.
+// Backward, register rows.  Each workgroup (8 waves, two per CU) owns a contiguous range of rows;
+// its waves take rows round-robin, accumulate the gw / gb column partials of their rows in
+// registers, combine them in LDS in wave order and write one fp64 partial per workgroup;
+// k_ln_cols_combine adds the workgroup partials in workgroup order.  A row's x, g and (when
+// accumulating) gx are all requested before its first use.
+constexpr int kLnB = 512;
+constexpr int kLnWaves = kLnB / kWave;
+
+// rows up to 1024 floats: two workgroups per CU (at most 128 VGPRs); longer rows: one
 template <int VPL, bool ACC>
-__global__ __launch_bounds__(kRowB) void k_ln_bwd_reg(const float *__restrict__ x, const float *__restrict__ w,
-                                                      const float *__restrict__ stats, const float *__restrict__ g,
-                                                      float *__restrict__ gx, double *__restrict__ part, int64_t rows,
-                                                      int D, int64_t rows_per_block) {
+__global__ __launch_bounds__(kLnB, VPL <= 4 ? 4 : 2) void k_ln_bwd_reg(const float *__restrict__ x, const float *__restrict__ w,
+                                                     const float *__restrict__ stats, const float *__restrict__ g,
+                                                     float *__restrict__ gx, double *__restrict__ part, int64_t rows,
+                                                     int D, int64_t rows_per_block) {
     const int lane = threadIdx.x & (kWave - 1);
     const int wv = threadIdx.x / kWave;
     const int nv = D / 4;
@@ -307,50 +312,65 @@ __global__ __launch_bounds__(kRowB) void k_ln_bwd_reg(const float *__restrict__ 
     f4 aw[VPL], ab[VPL];
 #pragma unroll
     for (int k = 0; k < VPL; k++) aw[k] = ab[k] = f4{0.f, 0.f, 0.f, 0.f};
-    for (int64_t r = r0 + wv; r < r1; r += kWavesPerBlock) {
+    for (int64_t r = r0 + wv; r < r1; r += kLnWaves) {
         const f4 *xr = (const f4 *)(x + r * D), *gr = (const f4 *)(g + r * D);
+        f4 *dx = gx ? (f4 *)(gx + r * D) : nullptr;
+        f4 xv4[VPL], gg[VPL], go[VPL];
+#pragma unroll
+        for (int k = 0; k < VPL; k++) {
+            const int j = lane + k * kWave;
+            if (j < nv) {
+                xv4[k] = __builtin_nontemporal_load(xr + j);
+                gg[k] = __builtin_nontemporal_load(gr + j);
+                if (ACC && dx) go[k] = __builtin_nontemporal_load(dx + j);
+            }
+        }
         const float mean = stats[2 * r], rstd = stats[2 * r + 1];
-        f4 xh[VPL], gg[VPL], gw4[VPL];
+        // xhat = (x - mean) * rstd and gw = g * w, recomputed (same fp32 operations) in the second
+        // pass rather than held live across the row reductions
+        auto terms = [&](int k, int j, f4 &xh, f4 &gw) {
+            const f4 ww = w ? ((const f4 *)w)[j] : f4{1.f, 1.f, 1.f, 1.f};
+            xh.x = (xv4[k].x - mean) * rstd;
+            xh.y = (xv4[k].y - mean) * rstd;
+            xh.z = (xv4[k].z - mean) * rstd;
+            xh.w = (xv4[k].w - mean) * rstd;
+            gw.x = w ? gg[k].x * ww.x : gg[k].x;
+            gw.y = w ? gg[k].y * ww.y : gg[k].y;
+            gw.z = w ? gg[k].z * ww.z : gg[k].z;
+            gw.w = w ? gg[k].w * ww.w : gg[k].w;
+        };
         double sg = 0.0, sgx = 0.0;
 #pragma unroll
         for (int k = 0; k < VPL; k++) {
             const int j = lane + k * kWave;
             if (j < nv) {
-                const f4 xv = __builtin_nontemporal_load(xr + j);
-                gg[k] = __builtin_nontemporal_load(gr + j);
-                const f4 ww = w ? ((const f4 *)w)[j] : f4{1.f, 1.f, 1.f, 1.f};
-                xh[k].x = (xv.x - mean) * rstd;
-                xh[k].y = (xv.y - mean) * rstd;
-                xh[k].z = (xv.z - mean) * rstd;
-                xh[k].w = (xv.w - mean) * rstd;
-                gw4[k].x = w ? gg[k].x * ww.x : gg[k].x;
-                gw4[k].y = w ? gg[k].y * ww.y : gg[k].y;
-                gw4[k].z = w ? gg[k].z * ww.z : gg[k].z;
-                gw4[k].w = w ? gg[k].w * ww.w : gg[k].w;
-                sg += ((double)gw4[k].x + (double)gw4[k].y) + ((double)gw4[k].z + (double)gw4[k].w);
-                sgx += ((double)(gw4[k].x * xh[k].x) + (double)(gw4[k].y * xh[k].y)) +
-                       ((double)(gw4[k].z * xh[k].z) + (double)(gw4[k].w * xh[k].w));
-                aw[k].x += gg[k].x * xh[k].x;
-                aw[k].y += gg[k].y * xh[k].y;
-                aw[k].z += gg[k].z * xh[k].z;
-                aw[k].w += gg[k].w * xh[k].w;
+                f4 xh, gw4;
+                terms(k, j, xh, gw4);
+                sg += ((double)gw4.x + (double)gw4.y) + ((double)gw4.z + (double)gw4.w);
+                sgx += ((double)(gw4.x * xh.x) + (double)(gw4.y * xh.y)) +
+                       ((double)(gw4.z * xh.z) + (double)(gw4.w * xh.w));
+                aw[k].x += gg[k].x * xh.x;
+                aw[k].y += gg[k].y * xh.y;
+                aw[k].z += gg[k].z * xh.z;
+                aw[k].w += gg[k].w * xh.w;
                 ab[k] += gg[k];
             }
         }
-        if (gx) {
+        if (dx) {
             sg = wave_sum(sg);
             sgx = wave_sum(sgx);
             const float mg = (float)(sg / (double)D), mgx = (float)(sgx / (double)D);
-            f4 *dx = (f4 *)(gx + r * D);
 #pragma unroll
             for (int k = 0; k < VPL; k++) {
                 const int j = lane + k * kWave;
                 if (j < nv) {
-                    f4 o = ACC ? __builtin_nontemporal_load(dx + j) : f4{0.f, 0.f, 0.f, 0.f};
-                    o.x = o.x + rstd * ((gw4[k].x - mg) - xh[k].x * mgx);
-                    o.y = o.y + rstd * ((gw4[k].y - mg) - xh[k].y * mgx);
-                    o.z = o.z + rstd * ((gw4[k].z - mg) - xh[k].z * mgx);
-                    o.w = o.w + rstd * ((gw4[k].w - mg) - xh[k].w * mgx);
+                    f4 xh, gw4;
+                    terms(k, j, xh, gw4);
+                    f4 o = ACC ? go[k] : f4{0.f, 0.f, 0.f, 0.f};
+                    o.x = o.x + rstd * ((gw4.x - mg) - xh.x * mgx);
+                    o.y = o.y + rstd * ((gw4.y - mg) - xh.y * mgx);
+                    o.z = o.z + rstd * ((gw4.z - mg) - xh.z * mgx);
+                    o.w = o.w + rstd * ((gw4.w - mg) - xh.w * mgx);
                     __builtin_nontemporal_store(o, dx + j);
                 }
             }
@@ -359,9 +379,9 @@ __global__ __launch_bounds__(kRowB) void k_ln_bwd_reg(const float *__restrict__ 
     if (!part) return;
     // combine the 4 waves' column partials in LDS (wave order), write the workgroup partial
     extern __shared__ double lds[];  // [2][D]
-    for (int i = threadIdx.x; i < 2 * D; i += kRowB) lds[i] = 0.0;
+    for (int i = threadIdx.x; i < 2 * D; i += kLnB) lds[i] = 0.0;
     __syncthreads();
-    for (int wsel = 0; wsel < kWavesPerBlock; wsel++) {
+    for (int wsel = 0; wsel < kLnWaves; wsel++) {
         if (wv == wsel) {
 #pragma unroll
             for (int k = 0; k < VPL; k++) {
@@ -381,7 +401,7 @@ __global__ __launch_bounds__(kRowB) void k_ln_bwd_reg(const float *__restrict__ 
         __syncthreads();
     }
     double *out = part + (size_t)blockIdx.x * 2 * D;
-    for (int i = threadIdx.x; i < 2 * D; i += kRowB) out[i] = lds[i];
+    for (int i = threadIdx.x; i < 2 * D; i += kLnB) out[i] = lds[i];
 }
 
 // Generic backward: one workgroup per row for gx, and column partials for gw/gb.
@@ -490,6 +510,14 @@ static unsigned rows_grid(int64_t rows) {
     default: { constexpr int VP = 16; CALL; } break; \
     }
 
+#define NC_VPL_SWITCH8(V, CALL)                     \
+    switch (V) {                                    \
+    case 1: { constexpr int VP = 1; CALL; } break;  \
+    case 2: { constexpr int VP = 2; CALL; } break;  \
+    case 4: { constexpr int VP = 4; CALL; } break;  \
+    default: { constexpr int VP = 8; CALL; } break; \
+    }
+
 // LayerNorm backward plan (shared by the workspace query and the launch)
 struct LnPlan {
     bool reg;
@@ -503,11 +531,12 @@ struct LnPlan {
 static LnPlan ln_plan(int64_t rows, int64_t D, bool aligned) {
     LnPlan p{};
     p.vpl = (D % 4 == 0 && aligned) ? vpl_for(D) : 0;
+    if (p.vpl > 8) p.vpl = 0;  // rows beyond 2048 floats would spill registers: generic path
     p.reg = p.vpl != 0;
     if (p.reg) {
-        int64_t want = (int64_t)num_cus() * 2;
+        int64_t want = (int64_t)num_cus() * (p.vpl <= 4 ? 2 : 1);  // the resident workgroups
         int64_t rpb = (rows + want - 1) / want;
-        if (rpb < kWavesPerBlock) rpb = kWavesPerBlock;
+        if (rpb < kLnWaves) rpb = kLnWaves;
         p.rows_per_block = rpb;
         p.blocks = (rows + rpb - 1) / rpb;
         p.ws = (size_t)p.blocks * 2 * D * sizeof(double);
@@ -604,9 +633,9 @@ extern "C" NC_HIP_API int nc_hip_layer_norm_bwd(int64_t rows, int64_t D, const f
         const size_t lds = cols ? (size_t)2 * D * sizeof(double) : 0;
         if (lds > 65536) return set_error(NC_HIP_ERR_ARG, "nc_hip_layer_norm_bwd: D too large for LDS combine");
         if (accumulate)
-            NC_VPL_SWITCH(p.vpl, hipLaunchKernelGGL((k_ln_bwd_reg<VP, true>), dim3(p.blocks), kRowB, lds, st, x, w, stats, g, gx, part, rows, (int)D, p.rows_per_block))
+            NC_VPL_SWITCH8(p.vpl, hipLaunchKernelGGL((k_ln_bwd_reg<VP, true>), dim3(p.blocks), kLnB, lds, st, x, w, stats, g, gx, part, rows, (int)D, p.rows_per_block))
         else
-            NC_VPL_SWITCH(p.vpl, hipLaunchKernelGGL((k_ln_bwd_reg<VP, false>), dim3(p.blocks), kRowB, lds, st, x, w, stats, g, gx, part, rows, (int)D, p.rows_per_block))
+            NC_VPL_SWITCH8(p.vpl, hipLaunchKernelGGL((k_ln_bwd_reg<VP, false>), dim3(p.blocks), kLnB, lds, st, x, w, stats, g, gx, part, rows, (int)D, p.rows_per_block))
         if (cols)
             hipLaunchKernelGGL(k_ln_cols_combine, dim3((D + kCombCols - 1) / kCombCols), kCombCols * kCombSlices, 0, st, part, gw, gb, D, (int)p.blocks);
     } else {

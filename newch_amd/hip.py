@@ -1,10 +1,10 @@
 """ctypes binding of the nc_hip.h kernel layer (exported by newch_amd/libnc.so).
 
 The functions take raw device addresses, element counts/strides and a hipStream_t.  `Kernels`
-wraps them for callers that hold device buffers (PyTorch-ROCm tensors in the tests and the
-benchmark): pointers come from ``tensor.data_ptr()`` and the stream from
-``torch.cuda.current_stream().cuda_stream``.  Every wrapper raises ``HipLayerError`` with the
-library's message when a call returns an error code; nothing here falls back to the host.
+wraps them for callers that hold device buffers (``newch_amd.hipmem.DeviceBuffer`` in the tests and
+the benchmark; any device address on the same HIP runtime works): pointers are plain integers and
+``stream=None`` is the null stream.  Every wrapper raises ``HipLayerError`` with the library's
+message when a call returns an error code; nothing here falls back to the host.
 """
 
 from __future__ import annotations
@@ -111,6 +111,9 @@ class Kernels:
         self._ok(self.lib.nc_hip_binary_bwd2(BIN[op], len(shape), _i64(shape), g, _i64(sg), a, _i64(sa), b, _i64(sb),
                                              ga, _i64(sga), gb, _i64(sgb), int(accumulate), ws, ws_bytes, stream),
                  "binary_bwd2")
+
+    def fill(self, dst, elem_bytes, pattern, n, stream=None):
+        self._ok(self.lib.nc_hip_fill(dst, elem_bytes, pattern, n, stream), "fill")
 
     def copy_strided(self, elem_bytes, shape, src, ss, dst, stream=None):
         self._ok(self.lib.nc_hip_copy_strided(elem_bytes, len(shape), _i64(shape), src, _i64(ss), dst, stream),

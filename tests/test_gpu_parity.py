@@ -159,6 +159,39 @@ def test_engine_binary_golden(eng, case, aview, op):
     eng.step_end()
 
 
+STRIDED_OPERAND = [
+    # a: storage [4, 8, 32] .transpose(1, 2) .reshape(4, 32, 1, 8): innermost stride 32, reused 16x
+    ("inner_strided", (4, 8, 32), ("t_reshape", 1, 2, (4, 32, 1, 8)), (1, 1, 16, 8)),
+    # a: storage [32, 4, 1, 8] .transpose(0, 1): batch dims swapped, innermost stride 1
+    ("batch_t", (32, 4, 1, 8), ("t", 0, 1), (1, 1, 64, 8)),
+]
+
+
+@pytest.mark.parametrize("case,astore,aview,bsh", STRIDED_OPERAND)
+@pytest.mark.parametrize("op", ["add", "sub", "mul", "div"])
+def test_engine_binary_strided_operand(eng, case, astore, aview, bsh, op):
+    """Views of a broadcast operand (the transposed inputs of the broadcast benchmark), through the
+    engine: forward bit-exact against the oracle, both sum-to-shape grads within 1e-5 of fp64."""
+    rng = np.random.default_rng(zlib.crc32(f"strided/{case}/{op}".encode()))
+    A = rng.standard_normal(astore).astype(np.float32)
+    B = (0.5 + 1.5 * rng.random(bsh)).astype(np.float32)
+    L = eng.lib
+    pa, pb = eng.param(A), eng.param(B)
+    va = eng.view(pa, aview)
+    out = {"add": L.nc_add, "sub": L.nc_sub, "mul": L.nc_mul, "div": L.nc_div}[op](va, pb)
+    y = eng.read(out)
+    a = np_view(A, aview)
+    assert_bits(y, O.binary_fwd(op, a, B), f"{case} {op} fwd")
+    G = rng.standard_normal(y.shape).astype(np.float32)
+    eng.backward_with(out, G)
+    ta, tb = grad_terms64(op, a, B, G)
+    for name, got, t, shape in (("a", eng.grad(va), ta, a.shape), ("b", eng.grad(pb), tb, B.shape)):
+        ref64 = sum_to(t, shape).reshape(shape)
+        scale = sum_to(np.abs(t), shape).reshape(shape) / np.sqrt(max(t.size // max(ref64.size, 1), 1))
+        assert_close64(got, ref64, scale, f"{case} {op} grad {name}")
+    eng.step_end()
+
+
 @pytest.mark.parametrize("case", ["r2x3", "r4x5x6", "r3x1000", "r5x13x9", "special"])
 def test_engine_reduce_golden(eng, case):
     d = load("reduce")
