@@ -95,6 +95,41 @@ __global__ __launch_bounds__(kRB) void k_rows_wave(const float *__restrict__ x, 
     const int lane = threadIdx.x & (kWave - 1);
     const int64_t wave = ((int64_t)blockIdx.x * kRB + threadIdx.x) / kWave;
     const int64_t nwaves = (int64_t)gridDim.x * (kRB / kWave);
+    if constexpr (VEC) {
+        if (R <= 16 * kWave) {
+            // a row is at most 4 vectors per lane: the next row's loads are issued before the current
+            // row is reduced; lane 0 holds the row's first element (the NaN rule's x0) in q[0].x
+            const int64_t nv = R / 4;
+            auto load = [&](int64_t o, f4 *q) {
+                const f4 *row = (const f4 *)(x + o * R);
+#pragma unroll
+                for (int k = 0; k < 4; k++)
+                    if (lane + k * kWave < nv) q[k] = __builtin_nontemporal_load(row + lane + k * kWave);
+            };
+            f4 q[4], qn[4];
+            if (wave < outer) load(wave, q);
+            for (int64_t o = wave; o < outer; o += nwaves) {
+                if (o + nwaves < outer) load(o + nwaves, qn);
+                Acc<KIND> acc;
+                acc.init();
+#pragma unroll
+                for (int k = 0; k < 4; k++) {
+                    const int v = lane + k * kWave;
+                    if (v < nv) {
+                        acc.push(q[k].x, 4 * v);
+                        acc.push(q[k].y, 4 * v + 1);
+                        acc.push(q[k].z, 4 * v + 2);
+                        acc.push(q[k].w, 4 * v + 3);
+                    }
+                }
+                acc.wave();
+                if (lane == 0) emit<KIND>(acc, q[0].x, scale, y, arg, o);
+#pragma unroll
+                for (int k = 0; k < 4; k++) q[k] = qn[k];
+            }
+            return;
+        }
+    }
     for (int64_t o = wave; o < outer; o += nwaves) {
         const float *row = x + o * R;
         Acc<KIND> acc;

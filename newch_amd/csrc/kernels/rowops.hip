@@ -23,26 +23,32 @@ __device__ __forceinline__ float row_max_finish(float m_nonnan, float x0) { retu
 // ------------------------------------------------------------------------------------------------
 // softmax, register-resident rows
 // ------------------------------------------------------------------------------------------------
+// One wave per row; the next row's loads are issued before the current row is reduced.
 template <int VPL, bool LOG>
 __global__ __launch_bounds__(kRowB) void k_softmax_fwd_reg(const float *__restrict__ x, float *__restrict__ y,
                                                            int64_t rows, int C) {
     const int lane = threadIdx.x & (kWave - 1);
     const int nv = C / 4;
-    for (int64_t r = ((int64_t)blockIdx.x * kRowB + threadIdx.x) / kWave; r < rows;
-         r += (int64_t)gridDim.x * kWavesPerBlock) {
+    const int64_t stride = (int64_t)gridDim.x * kWavesPerBlock;
+    auto load = [&](int64_t r, f4 *v) {
         const f4 *xr = (const f4 *)(x + r * C);
-        f4 v[VPL];
+#pragma unroll
+        for (int k = 0; k < VPL; k++)
+            if (lane + k * kWave < nv) v[k] = __builtin_nontemporal_load(xr + lane + k * kWave);
+    };
+    const int64_t r0 = ((int64_t)blockIdx.x * kRowB + threadIdx.x) / kWave;
+    f4 v[VPL], vn[VPL];
+    if (r0 < rows) load(r0, v);
+    for (int64_t r = r0; r < rows; r += stride) {
+        if (r + stride < rows) load(r + stride, vn);
         float m = -__builtin_inff();
 #pragma unroll
         for (int k = 0; k < VPL; k++) {
-            const int j = lane + k * kWave;
-            if (j < nv) {
-                v[k] = __builtin_nontemporal_load(xr + j);
+            if (lane + k * kWave < nv)
                 m = __builtin_fmaxf(m, __builtin_fmaxf(__builtin_fmaxf(v[k].x, v[k].y), __builtin_fmaxf(v[k].z, v[k].w)));
-            }
         }
         m = wave_max_nan_skip(m);
-        m = row_max_finish(m, x[r * C]);
+        m = row_max_finish(m, __shfl(v[0].x, 0, kWave));  // lane 0 holds the row's first element
         double s = 0.0;
 #pragma unroll
         for (int k = 0; k < VPL; k++) {
@@ -88,26 +94,46 @@ __global__ __launch_bounds__(kRowB) void k_softmax_fwd_reg(const float *__restri
                 }
             }
         }
+#pragma unroll
+        for (int k = 0; k < VPL; k++) v[k] = vn[k];
     }
 }
 
+// One wave per row; the row's gi (when accumulating) and the next row's y, g are requested before
+// the current row is reduced.
 template <int VPL, bool LOG, bool ACC>
 __global__ __launch_bounds__(kRowB) void k_softmax_bwd_reg(const float *__restrict__ y, const float *__restrict__ g,
                                                            float *__restrict__ gi, int64_t rows, int C) {
     const int lane = threadIdx.x & (kWave - 1);
     const int nv = C / 4;
-    for (int64_t r = ((int64_t)blockIdx.x * kRowB + threadIdx.x) / kWave; r < rows;
-         r += (int64_t)gridDim.x * kWavesPerBlock) {
+    const int64_t stride = (int64_t)gridDim.x * kWavesPerBlock;
+    auto load = [&](int64_t r, f4 *vy, f4 *vg) {
         const f4 *yr = (const f4 *)(y + r * C), *gr = (const f4 *)(g + r * C);
-        f4 *orow = (f4 *)(gi + r * C);
-        f4 vy[VPL], vg[VPL];
-        double s = 0.0;
 #pragma unroll
         for (int k = 0; k < VPL; k++) {
             const int j = lane + k * kWave;
             if (j < nv) {
                 vy[k] = __builtin_nontemporal_load(yr + j);
                 vg[k] = __builtin_nontemporal_load(gr + j);
+            }
+        }
+    };
+    const int64_t r0 = ((int64_t)blockIdx.x * kRowB + threadIdx.x) / kWave;
+    f4 vy[VPL], vg[VPL], ny[VPL], ng[VPL];
+    if (r0 < rows) load(r0, vy, vg);
+    for (int64_t r = r0; r < rows; r += stride) {
+        f4 *orow = (f4 *)(gi + r * C);
+        f4 go[VPL];
+        if (ACC) {
+#pragma unroll
+            for (int k = 0; k < VPL; k++)
+                if (lane + k * kWave < nv) go[k] = __builtin_nontemporal_load(orow + lane + k * kWave);
+        }
+        if (r + stride < rows) load(r + stride, ny, ng);
+        double s = 0.0;
+#pragma unroll
+        for (int k = 0; k < VPL; k++) {
+            if (lane + k * kWave < nv) {
                 if (LOG) s += ((double)vg[k].x + (double)vg[k].y) + ((double)vg[k].z + (double)vg[k].w);
                 else
                     s += ((double)(vg[k].x * vy[k].x) + (double)(vg[k].y * vy[k].y)) +
@@ -119,7 +145,7 @@ __global__ __launch_bounds__(kRowB) void k_softmax_bwd_reg(const float *__restri
         for (int k = 0; k < VPL; k++) {
             const int j = lane + k * kWave;
             if (j < nv) {
-                f4 o = ACC ? __builtin_nontemporal_load(orow + j) : f4{0.f, 0.f, 0.f, 0.f};
+                f4 o = ACC ? go[k] : f4{0.f, 0.f, 0.f, 0.f};
                 if (LOG) {
                     o.x = o.x + (vg[k].x - expf(vy[k].x) * sf);
                     o.y = o.y + (vg[k].y - expf(vy[k].y) * sf);
@@ -133,6 +159,11 @@ __global__ __launch_bounds__(kRowB) void k_softmax_bwd_reg(const float *__restri
                 }
                 __builtin_nontemporal_store(o, orow + j);
             }
+        }
+#pragma unroll
+        for (int k = 0; k < VPL; k++) {
+            vy[k] = ny[k];
+            vg[k] = ng[k];
         }
     }
 }
@@ -205,31 +236,43 @@ __global__ __launch_bounds__(kRowB) void k_softmax_bwd_blk(const float *__restri
 // ------------------------------------------------------------------------------------------------
 // LayerNorm
 // ------------------------------------------------------------------------------------------------
+// One wave per row; gamma / beta are held in registers and the next row's loads are issued before
+// the current row is reduced.
 template <int VPL>
 __global__ __launch_bounds__(kRowB) void k_ln_fwd_reg(const float *__restrict__ x, const float *__restrict__ w,
                                                       const float *__restrict__ b, float eps, float *__restrict__ y,
                                                       float *__restrict__ stats, int64_t rows, int D) {
     const int lane = threadIdx.x & (kWave - 1);
     const int nv = D / 4;
-    for (int64_t r = ((int64_t)blockIdx.x * kRowB + threadIdx.x) / kWave; r < rows;
-         r += (int64_t)gridDim.x * kWavesPerBlock) {
+    const int64_t stride = (int64_t)gridDim.x * kWavesPerBlock;
+    f4 ww[VPL], bv[VPL];
+#pragma unroll
+    for (int k = 0; k < VPL; k++) {
+        const int j = lane + k * kWave;
+        ww[k] = (w && j < nv) ? ((const f4 *)w)[j] : f4{0.f, 0.f, 0.f, 0.f};
+        bv[k] = (b && j < nv) ? ((const f4 *)b)[j] : f4{0.f, 0.f, 0.f, 0.f};
+    }
+    auto load = [&](int64_t r, f4 *v) {
         const f4 *xr = (const f4 *)(x + r * D);
-        f4 v[VPL];
+#pragma unroll
+        for (int k = 0; k < VPL; k++)
+            if (lane + k * kWave < nv) v[k] = __builtin_nontemporal_load(xr + lane + k * kWave);
+    };
+    const int64_t r0 = ((int64_t)blockIdx.x * kRowB + threadIdx.x) / kWave;
+    f4 v[VPL], vn[VPL];
+    if (r0 < rows) load(r0, v);
+    for (int64_t r = r0; r < rows; r += stride) {
+        if (r + stride < rows) load(r + stride, vn);
         double s = 0.0;
 #pragma unroll
         for (int k = 0; k < VPL; k++) {
-            const int j = lane + k * kWave;
-            if (j < nv) {
-                v[k] = __builtin_nontemporal_load(xr + j);
-                s += ((double)v[k].x + (double)v[k].y) + ((double)v[k].z + (double)v[k].w);
-            }
+            if (lane + k * kWave < nv) s += ((double)v[k].x + (double)v[k].y) + ((double)v[k].z + (double)v[k].w);
         }
         const double mean = wave_sum(s) / (double)D;
         double ss = 0.0;
 #pragma unroll
         for (int k = 0; k < VPL; k++) {
-            const int j = lane + k * kWave;
-            if (j < nv) {
+            if (lane + k * kWave < nv) {
                 const double a = (double)v[k].x - mean, bb = (double)v[k].y - mean, c = (double)v[k].z - mean,
                              d = (double)v[k].w - mean;
                 ss += (a * a + bb * bb) + (c * c + d * d);
@@ -247,17 +290,17 @@ __global__ __launch_bounds__(kRowB) void k_ln_fwd_reg(const float *__restrict__ 
         for (int k = 0; k < VPL; k++) {
             const int j = lane + k * kWave;
             if (j < nv) {
-                const f4 ww = w ? ((const f4 *)w)[j] : f4{0.f, 0.f, 0.f, 0.f};
-                const f4 bv = b ? ((const f4 *)b)[j] : f4{0.f, 0.f, 0.f, 0.f};
                 f4 o;
                 float t;
-                t = (v[k].x - mf) * rstd; o.x = (w ? t * ww.x : t) + bv.x;
-                t = (v[k].y - mf) * rstd; o.y = (w ? t * ww.y : t) + bv.y;
-                t = (v[k].z - mf) * rstd; o.z = (w ? t * ww.z : t) + bv.z;
-                t = (v[k].w - mf) * rstd; o.w = (w ? t * ww.w : t) + bv.w;
+                t = (v[k].x - mf) * rstd; o.x = (w ? t * ww[k].x : t) + bv[k].x;
+                t = (v[k].y - mf) * rstd; o.y = (w ? t * ww[k].y : t) + bv[k].y;
+                t = (v[k].z - mf) * rstd; o.z = (w ? t * ww[k].z : t) + bv[k].z;
+                t = (v[k].w - mf) * rstd; o.w = (w ? t * ww[k].w : t) + bv[k].w;
                 __builtin_nontemporal_store(o, yr + j);
             }
         }
+#pragma unroll
+        for (int k = 0; k < VPL; k++) v[k] = vn[k];
     }
 }
 
