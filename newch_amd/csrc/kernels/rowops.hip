@@ -333,13 +333,23 @@ __global__ __launch_bounds__(kRowB) void k_ln_fwd_blk(const float *__restrict__ 
     }
 }
 
-// Backward, register rows.  Each workgroup (8 waves, two per CU) owns a contiguous range of rows;
-// its waves take rows round-robin, accumulate the gw / gb column partials of their rows in
-// registers, combine them in LDS in wave order and write one fp64 partial per workgroup;
-// k_ln_cols_combine adds the workgroup partials in workgroup order.  A row's x, g and (when
-// accumulating) gx are all requested before its first use.
+// Backward, register rows.  Each workgroup (8 waves) owns a contiguous range of rows; its waves take
+// rows round-robin.  Per row, the gx loads (when accumulating) and then the next row's x and g are
+// requested before the row is reduced.  The gw / gb column partials of a wave's rows accumulate in
+// fp32 in that wave's own LDS slice (rows up to 1024 floats; registers for longer rows), in row
+// order; at the end each column's 8 wave partials are added in wave order in fp64 and written as
+// the workgroup's partial, which k_ln_cols_combine adds up in workgroup order.
 constexpr int kLnB = 512;
 constexpr int kLnWaves = kLnB / kWave;
+
+template <int VPL>
+constexpr bool ln_cols_in_lds() { return VPL <= 4; }
+
+// bytes of dynamic LDS k_ln_bwd_reg needs for gw / gb
+static size_t ln_bwd_lds(int vpl, int64_t D, bool cols) {
+    if (!cols) return 0;
+    return vpl <= 4 ? (size_t)kLnWaves * 2 * D * sizeof(float) : (size_t)2 * D * sizeof(double);
+}
 
 // rows up to 1024 floats: two workgroups per CU (at most 128 VGPRs); longer rows: one
 template <int VPL, bool ACC>
@@ -347,32 +357,66 @@ __global__ __launch_bounds__(kLnB, VPL <= 4 ? 4 : 2) void k_ln_bwd_reg(const flo
                                                      const float *__restrict__ stats, const float *__restrict__ g,
                                                      float *__restrict__ gx, double *__restrict__ part, int64_t rows,
                                                      int D, int64_t rows_per_block) {
+    extern __shared__ char ln_lds[];
+    // gamma staged in LDS: its reads then wait on the LDS counter, not behind the prefetched row
+    __shared__ f4 wsh[VPL * kWave];
+    constexpr bool kLdsCols = ln_cols_in_lds<VPL>();
     const int lane = threadIdx.x & (kWave - 1);
     const int wv = threadIdx.x / kWave;
     const int nv = D / 4;
     const int64_t r0 = (int64_t)blockIdx.x * rows_per_block;
     const int64_t r1 = min(rows, r0 + rows_per_block);
-    f4 aw[VPL], ab[VPL];
+    const bool cols = part != nullptr;
+    if (w) {
+        for (int j = threadIdx.x; j < nv; j += kLnB) wsh[j] = ((const f4 *)w)[j];
+        __syncthreads();
+    }
+    // column accumulators: this wave's LDS slice [2][D] floats, or registers
+    f4 *accw = (f4 *)ln_lds + (size_t)wv * 2 * nv, *accb = accw + nv;
+    f4 aw[kLdsCols ? 1 : VPL], ab[kLdsCols ? 1 : VPL];
+    if constexpr (kLdsCols) {
+        if (cols) {
 #pragma unroll
-    for (int k = 0; k < VPL; k++) aw[k] = ab[k] = f4{0.f, 0.f, 0.f, 0.f};
-    for (int64_t r = r0 + wv; r < r1; r += kLnWaves) {
+            for (int k = 0; k < VPL; k++) {
+                const int j = lane + k * kWave;
+                if (j < nv) accw[j] = accb[j] = f4{0.f, 0.f, 0.f, 0.f};
+            }
+        }
+    } else {
+#pragma unroll
+        for (int k = 0; k < VPL; k++) aw[k] = ab[k] = f4{0.f, 0.f, 0.f, 0.f};
+    }
+    auto load = [&](int64_t r, f4 *xv, f4 *gv) {
         const f4 *xr = (const f4 *)(x + r * D), *gr = (const f4 *)(g + r * D);
-        f4 *dx = gx ? (f4 *)(gx + r * D) : nullptr;
-        f4 xv4[VPL], gg[VPL], go[VPL];
 #pragma unroll
         for (int k = 0; k < VPL; k++) {
             const int j = lane + k * kWave;
             if (j < nv) {
-                xv4[k] = __builtin_nontemporal_load(xr + j);
-                gg[k] = __builtin_nontemporal_load(gr + j);
-                if (ACC && dx) go[k] = __builtin_nontemporal_load(dx + j);
+                xv[k] = __builtin_nontemporal_load(xr + j);
+                gv[k] = __builtin_nontemporal_load(gr + j);
             }
         }
+    };
+    constexpr bool kPrefetch = VPL <= 4;  // longer rows have no registers for the next row
+    f4 xv4[VPL], gg[VPL], xn[kPrefetch ? VPL : 1], gn[kPrefetch ? VPL : 1];
+    if (kPrefetch && r0 + wv < r1) load(r0 + wv, xv4, gg);
+    for (int64_t r = r0 + wv; r < r1; r += kLnWaves) {
+        f4 *dx = gx ? (f4 *)(gx + r * D) : nullptr;
+        // the row's statistics, then its gx, then the next row: waits for the first two do not
+        // wait for the prefetch
         const float mean = stats[2 * r], rstd = stats[2 * r + 1];
+        if (!kPrefetch) load(r, xv4, gg);
+        f4 go[VPL];
+        if (ACC && dx) {
+#pragma unroll
+            for (int k = 0; k < VPL; k++)
+                if (lane + k * kWave < nv) go[k] = __builtin_nontemporal_load(dx + lane + k * kWave);
+        }
+        if (kPrefetch && r + kLnWaves < r1) load(r + kLnWaves, xn, gn);
         // xhat = (x - mean) * rstd and gw = g * w, recomputed (same fp32 operations) in the second
         // pass rather than held live across the row reductions
         auto terms = [&](int k, int j, f4 &xh, f4 &gw) {
-            const f4 ww = w ? ((const f4 *)w)[j] : f4{1.f, 1.f, 1.f, 1.f};
+            const f4 ww = w ? wsh[j] : f4{1.f, 1.f, 1.f, 1.f};
             xh.x = (xv4[k].x - mean) * rstd;
             xh.y = (xv4[k].y - mean) * rstd;
             xh.z = (xv4[k].z - mean) * rstd;
@@ -392,11 +436,21 @@ __global__ __launch_bounds__(kLnB, VPL <= 4 ? 4 : 2) void k_ln_bwd_reg(const flo
                 sg += ((double)gw4.x + (double)gw4.y) + ((double)gw4.z + (double)gw4.w);
                 sgx += ((double)(gw4.x * xh.x) + (double)(gw4.y * xh.y)) +
                        ((double)(gw4.z * xh.z) + (double)(gw4.w * xh.w));
-                aw[k].x += gg[k].x * xh.x;
-                aw[k].y += gg[k].y * xh.y;
-                aw[k].z += gg[k].z * xh.z;
-                aw[k].w += gg[k].w * xh.w;
-                ab[k] += gg[k];
+                if (cols) {
+                    f4 t = kLdsCols ? accw[j] : aw[k], u = kLdsCols ? accb[j] : ab[k];
+                    t.x += gg[k].x * xh.x;
+                    t.y += gg[k].y * xh.y;
+                    t.z += gg[k].z * xh.z;
+                    t.w += gg[k].w * xh.w;
+                    u += gg[k];
+                    if constexpr (kLdsCols) {
+                        accw[j] = t;
+                        accb[j] = u;
+                    } else {
+                        aw[k] = t;
+                        ab[k] = u;
+                    }
+                }
             }
         }
         if (dx) {
@@ -418,33 +472,52 @@ __global__ __launch_bounds__(kLnB, VPL <= 4 ? 4 : 2) void k_ln_bwd_reg(const flo
                 }
             }
         }
-    }
-    if (!part) return;
-    // combine the 4 waves' column partials in LDS (wave order), write the workgroup partial
-    extern __shared__ double lds[];  // [2][D]
-    for (int i = threadIdx.x; i < 2 * D; i += kLnB) lds[i] = 0.0;
-    __syncthreads();
-    for (int wsel = 0; wsel < kLnWaves; wsel++) {
-        if (wv == wsel) {
+        if constexpr (kPrefetch) {
 #pragma unroll
             for (int k = 0; k < VPL; k++) {
-                const int j = lane + k * kWave;
-                if (j < nv) {
-                    lds[4 * j + 0] += aw[k].x;
-                    lds[4 * j + 1] += aw[k].y;
-                    lds[4 * j + 2] += aw[k].z;
-                    lds[4 * j + 3] += aw[k].w;
-                    lds[D + 4 * j + 0] += ab[k].x;
-                    lds[D + 4 * j + 1] += ab[k].y;
-                    lds[D + 4 * j + 2] += ab[k].z;
-                    lds[D + 4 * j + 3] += ab[k].w;
-                }
+                xv4[k] = xn[k];
+                gg[k] = gn[k];
             }
         }
-        __syncthreads();
     }
+    if (!cols) return;
     double *out = part + (size_t)blockIdx.x * 2 * D;
-    for (int i = threadIdx.x; i < 2 * D; i += kLnB) out[i] = lds[i];
+    if constexpr (kLdsCols) {
+        // column i of [gw | gb]: the 8 wave slices added in wave order
+        __syncthreads();
+        const float *acc = (const float *)ln_lds;
+        for (int i = threadIdx.x; i < 2 * D; i += kLnB) {
+            double t = 0.0;
+#pragma unroll
+            for (int w8 = 0; w8 < kLnWaves; w8++) t += (double)acc[(size_t)w8 * 2 * D + i];
+            out[i] = t;
+        }
+    } else {
+        // combine the waves' register partials in LDS (wave order)
+        double *lds = (double *)ln_lds;  // [2][D]
+        for (int i = threadIdx.x; i < 2 * D; i += kLnB) lds[i] = 0.0;
+        __syncthreads();
+        for (int wsel = 0; wsel < kLnWaves; wsel++) {
+            if (wv == wsel) {
+#pragma unroll
+                for (int k = 0; k < VPL; k++) {
+                    const int j = lane + k * kWave;
+                    if (j < nv) {
+                        lds[4 * j + 0] += aw[k].x;
+                        lds[4 * j + 1] += aw[k].y;
+                        lds[4 * j + 2] += aw[k].z;
+                        lds[4 * j + 3] += aw[k].w;
+                        lds[D + 4 * j + 0] += ab[k].x;
+                        lds[D + 4 * j + 1] += ab[k].y;
+                        lds[D + 4 * j + 2] += ab[k].z;
+                        lds[D + 4 * j + 3] += ab[k].w;
+                    }
+                }
+            }
+            __syncthreads();
+        }
+        for (int i = threadIdx.x; i < 2 * D; i += kLnB) out[i] = lds[i];
+    }
 }
 
 // Generic backward: one workgroup per row for gx, and column partials for gw/gb.
@@ -673,7 +746,7 @@ extern "C" NC_HIP_API int nc_hip_layer_norm_bwd(int64_t rows, int64_t D, const f
         return set_error(NC_HIP_ERR_WORKSPACE, "nc_hip_layer_norm_bwd: workspace of %zu bytes needed", p.ws);
     double *part = cols ? (double *)ws : nullptr;
     if (p.reg) {
-        const size_t lds = cols ? (size_t)2 * D * sizeof(double) : 0;
+        const size_t lds = ln_bwd_lds(p.vpl, D, cols);
         if (lds > 65536) return set_error(NC_HIP_ERR_ARG, "nc_hip_layer_norm_bwd: D too large for LDS combine");
         if (accumulate)
             NC_VPL_SWITCH8(p.vpl, hipLaunchKernelGGL((k_ln_bwd_reg<VP, true>), dim3(p.blocks), kLnB, lds, st, x, w, stats, g, gx, part, rows, (int)D, p.rows_per_block))

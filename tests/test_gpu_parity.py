@@ -655,6 +655,48 @@ def test_kernel_layer_norm(K, rows, D):
     assert_close64(GB.to_numpy(np.float32, D), G.sum(0), np.abs(G).sum(0) / np.sqrt(rows), "layer_norm db")
 
 
+@pytest.mark.parametrize("rows,D", [(129, 512), (1031, 1024), (40, 2048), (9, 64)])
+@pytest.mark.parametrize("mode", ["store_all", "acc_gx_only", "cols_only"])
+def test_kernel_layer_norm_bwd_modes(K, rows, D, mode):
+    """Backward with a fresh (stored) gx, with gx alone accumulated onto nonzero values, and with
+    only the gw / gb column sums requested; row lengths covering every register layout."""
+    rng = np.random.default_rng(zlib.crc32(f"lnbwd/{rows}/{D}/{mode}".encode()))
+    x = (rng.standard_normal((rows, D)) * 2 + 0.3).astype(np.float32)
+    w = (1 + 0.1 * rng.standard_normal(D)).astype(np.float32)
+    g = rng.standard_normal((rows, D)).astype(np.float32)
+    gx0 = rng.standard_normal((rows, D)).astype(np.float32)
+    Xd, Wd, Gd = dev(x), dev(w), dev(g)
+    Sd = empty(8 * rows)
+    Yd = empty(x.nbytes)
+    K.layer_norm_fwd(rows, D, Xd.ptr, Wd.ptr, 0, 1e-5, Yd.ptr, Sd.ptr)
+    GX, GW, GB = dev(gx0), dev(np.zeros(D, np.float32)), dev(np.zeros(D, np.float32))
+    wsb = K.layer_norm_bwd_workspace(rows, D)
+    ws = empty(max(wsb, 1))
+    want_gx, want_cols, acc = mode != "cols_only", mode != "acc_gx_only", mode == "acc_gx_only"
+    K.layer_norm_bwd(rows, D, Xd.ptr, Wd.ptr, Sd.ptr, Gd.ptr, GX.ptr if want_gx else 0, GW.ptr if want_cols else 0,
+                     GB.ptr if want_cols else 0, ws.ptr, wsb, accumulate=acc)
+    sync()
+    X, G = x.astype(np.float64), g.astype(np.float64)
+    mu = X.mean(1, keepdims=True)
+    rs = 1 / np.sqrt(X.var(1, keepdims=True) + 1e-5)
+    xh = (X - mu) * rs
+    gh = G * w
+    gxr = rs * (gh - gh.mean(1, keepdims=True) - xh * (gh * xh).mean(1, keepdims=True))
+    sc = rs * (np.abs(gh) + np.abs(gh).mean(1, keepdims=True) + np.abs(xh) * np.abs(gh * xh).mean(1, keepdims=True))
+    got_gx = GX.to_numpy(np.float32, (rows, D))
+    if not want_gx:
+        assert_bits(got_gx, gx0, "gx untouched")
+    elif acc:
+        assert_close64(got_gx, gx0.astype(np.float64) + gxr, sc + np.abs(gx0), "layer_norm dx (accumulated)")
+    else:
+        assert_close64(got_gx, gxr, sc, "layer_norm dx (stored)")
+    if want_cols:
+        assert_close64(GW.to_numpy(np.float32, D), (G * xh).sum(0), np.abs(G * xh).sum(0) / np.sqrt(rows), "dw")
+        assert_close64(GB.to_numpy(np.float32, D), G.sum(0), np.abs(G).sum(0) / np.sqrt(rows), "db")
+    else:
+        assert (GW.to_numpy(np.float32, D) == 0).all() and (GB.to_numpy(np.float32, D) == 0).all()
+
+
 @pytest.mark.parametrize("rows,cols", [(512, 4096), (96, 70), (64, 8192), (33, 10000), (8, 16)])
 def test_kernel_quantize(K, rows, cols):
     rng = np.random.default_rng(rows * cols)
