@@ -566,8 +566,9 @@ struct Bwd2Plan {
     IdxMap<1> amap;  // element offset of a[p, 0, 0] over the plane dims
 };
 
+// OUT selects the gradients written: 1 grad_a, 2 grad_b, 3 both.
 // two resident workgroups per CU (4 waves per SIMD): at most 128 VGPRs
-template <int MODE, bool ACC, int T>
+template <int MODE, bool ACC, int T, int OUT>
 __global__ __launch_bounds__(kB2, 4) void k_bcast_bwd2(const float *__restrict__ g, const float *__restrict__ a,
                                                     const float *__restrict__ b, float *__restrict__ ga,
                                                     double *__restrict__ ga_part, double *__restrict__ gb_part,
@@ -583,12 +584,13 @@ __global__ __launch_bounds__(kB2, 4) void k_bcast_bwd2(const float *__restrict__
     const uint32_t p0 = range * pl.planes_per_block;
     const uint32_t p1 = min(pl.P, p0 + pl.planes_per_block);  // the launch has p0 < P for every workgroup
     const uint32_t qb = band * band4 + tid;                    // this lane's first float4 in a plane
+    constexpr bool WA = OUT & 1, WB = OUT & 2;
     f4 bv[T];
 #pragma unroll
     for (int k = 0; k < T; k++) {
         bv[k] = f4{1.f, 1.f, 1.f, 1.f};
-        if constexpr (MODE != 0) bv[k] = ((const f4 *)b)[qb + kB2 * k];
-        if constexpr (MODE == 3) bv[k] = f4{1.0f / bv[k].x, 1.0f / bv[k].y, 1.0f / bv[k].z, 1.0f / bv[k].w};
+        if constexpr (WA && MODE != 0) bv[k] = ((const f4 *)b)[qb + kB2 * k];
+        if constexpr (WA && MODE == 3) bv[k] = f4{1.0f / bv[k].x, 1.0f / bv[k].y, 1.0f / bv[k].z, 1.0f / bv[k].w};
     }
     double accb[T][4];
 #pragma unroll
@@ -611,12 +613,12 @@ __global__ __launch_bounds__(kB2, 4) void k_bcast_bwd2(const float *__restrict__
                 for (int k = 0; k < T; k++) nxt[k] = __builtin_nontemporal_load(gn + kB2 * k);
             }
             f4 av = f4{0.f, 0.f, 0.f, 0.f};
-            if constexpr (MODE == 1 || MODE == 3) {
+            if constexpr (WB && (MODE == 1 || MODE == 3)) {
                 int64_t off[1];
                 offsets<1>(pl.amap, p, off);
                 av = *(const f4 *)(a + off[0] + 4 * w4);
             }
-            double sa[4] = {0.0, 0.0, 0.0, 0.0};
+            double ta[T][4];  // grad_a terms of this lane's T float4, added as a pairwise tree
 #pragma unroll
             for (int k = 0; k < T; k++) {
                 const float gg[4] = {cur[k].x, cur[k].y, cur[k].z, cur[k].w};
@@ -626,13 +628,28 @@ __global__ __launch_bounds__(kB2, 4) void k_bcast_bwd2(const float *__restrict__
                 for (int c = 0; c < 4; c++) {
                     // terms are the fp32 products the unreduced gradient holds, summed in fp64
                     // grad_a term: g (add, sub), g*b (mul), g*(1/b) (div)
-                    sa[c] += (double)(MODE == 0 ? gg[c] : gg[c] * bb[c]);
+                    if constexpr (WA) ta[k][c] = (double)(MODE == 0 ? gg[c] : gg[c] * bb[c]);
                     // grad_b term before the per-column factor: g (add, sub), g*a (mul, div)
-                    accb[k][c] += (double)((MODE == 1 || MODE == 3) ? gg[c] * aa[c] : gg[c]);
+                    if constexpr (WB) accb[k][c] += (double)((MODE == 1 || MODE == 3) ? gg[c] * aa[c] : gg[c]);
+                }
+            }
+            double sa[4];
+#pragma unroll
+            for (int c = 0; c < 4; c++) {
+                if constexpr (!WA) {
+                    sa[c] = 0.0;
+                } else {
+#pragma unroll
+                    for (int h = T / 2; h >= 1; h /= 2) {
+#pragma unroll
+                        for (int k = 0; k < h; k++) ta[k][c] += ta[k + h][c];
+                    }
+                    sa[c] = ta[0][c];
                 }
             }
 #pragma unroll
             for (int k = 0; k < T; k++) cur[k] = nxt[k];
+            if constexpr (!WA) continue;
             // lanes sharing w4 inside the wave; the wave's partial goes to LDS slot (j, wv)
             for (uint32_t o = W4; o < (uint32_t)kWave; o <<= 1) {
 #pragma unroll
@@ -644,7 +661,8 @@ __global__ __launch_bounds__(kB2, 4) void k_bcast_bwd2(const float *__restrict__
                 for (int c = 0; c < 4; c++) d[c] = sa[c];
             }
         }
-        __syncthreads();
+        if constexpr (!WA) continue;
+        lds_barrier();
         {
             // lane -> (plane j, column col, component c) of the group; the 8 waves added in order
             const uint32_t c = tid % 4, col = (tid / 4) % W4, j = tid / (4 * W4);
@@ -657,14 +675,16 @@ __global__ __launch_bounds__(kB2, 4) void k_bcast_bwd2(const float *__restrict__
                 else ga_part[(size_t)(pg + j) * nband * 4 * W4 + band * 4 * W4 + 4 * col + c] = t;
             }
         }
-        __syncthreads();
+        lds_barrier();
     }
-    double *out = gb_part + (size_t)range * plane4 * 4;
+    if constexpr (WB) {
+        double *out = gb_part + (size_t)range * plane4 * 4;
 #pragma unroll
-    for (int k = 0; k < T; k++) {
-        const uint32_t q = qb + kB2 * k;
+        for (int k = 0; k < T; k++) {
+            const uint32_t q = qb + kB2 * k;
 #pragma unroll
-        for (int c = 0; c < 4; c++) out[4 * q + c] = accb[k][c] * alpha_b;
+            for (int c = 0; c < 4; c++) out[4 * q + c] = accb[k][c] * alpha_b;
+        }
     }
 }
 
@@ -759,30 +779,33 @@ static bool plan_bwd2(const Prepared &p, const float *g, const float *a, const f
     return true;
 }
 
-// workspace: grad_b partials [ranges][H*W], then (several bands) grad_a partials [P][nband][W]
-static size_t bwd2_gb_bytes(const Bwd2Plan &pl) { return (size_t)pl.ranges * pl.H * pl.W4 * 4 * sizeof(double); }
-static size_t bwd2_ws(const Bwd2Plan &pl) {
-    size_t n = bwd2_gb_bytes(pl);
-    if (pl.nband > 1) n += (size_t)pl.P * pl.nband * pl.W4 * 4 * sizeof(double);
+// workspace: grad_b partials [ranges][H*W] (when grad_b is written), then grad_a partials
+// [P][nband][W] (when grad_a is written and a plane has several bands)
+static size_t bwd2_gb_bytes(const Bwd2Plan &pl, int out) {
+    return (out & 2) ? (size_t)pl.ranges * pl.H * pl.W4 * 4 * sizeof(double) : 0;
+}
+static size_t bwd2_ws(const Bwd2Plan &pl, int out = 3) {
+    size_t n = bwd2_gb_bytes(pl, out);
+    if ((out & 1) && pl.nband > 1) n += (size_t)pl.P * pl.nband * pl.W4 * 4 * sizeof(double);
     return n;
 }
 
-template <int MODE>
+template <int MODE, int OUT>
 static int launch_bwd2(const float *g, const float *a, const float *b, float *ga, float *gb, const Bwd2Plan &pl,
                        double alpha_b, int acc, void *ws, size_t ws_bytes, hipStream_t st) {
-    const size_t need = bwd2_ws(pl);
-    if (ws_bytes < need || !ws)
+    const size_t need = bwd2_ws(pl, OUT);
+    if (ws_bytes < need || (need && !ws))
         return set_error(NC_HIP_ERR_WORKSPACE, "binary_bwd2: workspace of %zu bytes needed, %zu given", need, ws_bytes);
     const uint32_t blocks = pl.ranges * pl.nband;
-    double *gb_part = (double *)ws;
-    double *ga_part = pl.nband > 1 ? (double *)((char *)ws + bwd2_gb_bytes(pl)) : nullptr;
+    double *gb_part = (OUT & 2) ? (double *)ws : nullptr;
+    double *ga_part = ((OUT & 1) && pl.nband > 1) ? (double *)((char *)ws + bwd2_gb_bytes(pl, OUT)) : nullptr;
 #define NC_B2_LAUNCH(TT)                                                                                          \
     if (acc)                                                                                                      \
-        hipLaunchKernelGGL((k_bcast_bwd2<MODE, true, TT>), dim3(blocks), dim3(kB2), 0, st, g, a, b, ga, ga_part,  \
-                           gb_part, pl, alpha_b);                                                                 \
+        hipLaunchKernelGGL((k_bcast_bwd2<MODE, true, TT, OUT>), dim3(blocks), dim3(kB2), 0, st, g, a, b, ga,      \
+                           ga_part, gb_part, pl, alpha_b);                                                        \
     else                                                                                                          \
-        hipLaunchKernelGGL((k_bcast_bwd2<MODE, false, TT>), dim3(blocks), dim3(kB2), 0, st, g, a, b, ga, ga_part, \
-                           gb_part, pl, alpha_b)
+        hipLaunchKernelGGL((k_bcast_bwd2<MODE, false, TT, OUT>), dim3(blocks), dim3(kB2), 0, st, g, a, b, ga,     \
+                           ga_part, gb_part, pl, alpha_b)
     switch (pl.T) {
     case 1: NC_B2_LAUNCH(1); break;
     case 2: NC_B2_LAUNCH(2); break;
@@ -795,16 +818,76 @@ static int launch_bwd2(const float *g, const float *a, const float *b, float *ga
     default: return set_error(NC_HIP_ERR_ARG, "binary_bwd2: unsupported plan");
     }
 #undef NC_B2_LAUNCH
-    if (pl.nband > 1) {
+    if ((OUT & 1) && pl.nband > 1) {
         const uint32_t n = pl.P * pl.W4 * 4;
         const unsigned grid = stream_grid(n, kB);
         if (acc) hipLaunchKernelGGL((k_bwd2_ga_combine<true>), dim3(grid), dim3(kB), 0, st, ga_part, ga, n, pl.W4 * 4, pl.nband);
         else hipLaunchKernelGGL((k_bwd2_ga_combine<false>), dim3(grid), dim3(kB), 0, st, ga_part, ga, n, pl.W4 * 4, pl.nband);
     }
-    const uint32_t n = pl.H * pl.W4 * 4;
-    if (acc) hipLaunchKernelGGL((k_bwd2_gb_combine<MODE, true>), dim3((n + 63) / 64), dim3(1024), 0, st, gb_part, b, gb, n, pl.ranges);
-    else hipLaunchKernelGGL((k_bwd2_gb_combine<MODE, false>), dim3((n + 63) / 64), dim3(1024), 0, st, gb_part, b, gb, n, pl.ranges);
+    if (OUT & 2) {
+        const uint32_t n = pl.H * pl.W4 * 4;
+        if (acc) hipLaunchKernelGGL((k_bwd2_gb_combine<MODE, true>), dim3((n + 63) / 64), dim3(1024), 0, st, gb_part, b, gb, n, pl.ranges);
+        else hipLaunchKernelGGL((k_bwd2_gb_combine<MODE, false>), dim3((n + 63) / 64), dim3(1024), 0, st, gb_part, b, gb, n, pl.ranges);
+    }
     return check_launch("nc_hip_binary_bwd2");
+}
+
+// op -> kernel mode (add and sub share the kernel; sub scales grad_b by -1)
+template <int OUT>
+static int launch_bwd2_op(int op, const float *g, const float *a, const float *b, float *ga, float *gb,
+                          const Bwd2Plan &pl, int acc, void *ws, size_t ws_bytes, hipStream_t st) {
+    const double alpha_b = op == NC_HIP_BIN_SUB ? -1.0 : 1.0;
+    switch (op) {
+    case NC_HIP_BIN_ADD:
+    case NC_HIP_BIN_SUB: return launch_bwd2<0, OUT>(g, a, b, ga, gb, pl, alpha_b, acc, ws, ws_bytes, st);
+    case NC_HIP_BIN_MUL: return launch_bwd2<1, OUT>(g, a, b, ga, gb, pl, alpha_b, acc, ws, ws_bytes, st);
+    default: return launch_bwd2<3, OUT>(g, a, b, ga, gb, pl, alpha_b, acc, ws, ws_bytes, st);
+    }
+}
+
+// Layout of a contiguous gradient for an operand with broadcast strides sx over `shape`: stride 0
+// where the operand is broadcast, row-major over its own dims elsewhere.
+static void grad_layout(int nd, const int64_t *shape, const int64_t *sx, int64_t *out) {
+    int64_t run = 1;
+    for (int d = nd - 1; d >= 0; d--) {
+        if (sx[d] == 0 && shape[d] != 1) {
+            out[d] = 0;
+        } else {
+            out[d] = run;
+            run *= shape[d];
+        }
+    }
+}
+
+// Workspace bound of the fused path for one gradient whose layout is sgx: the plan built as if the
+// output were g[P, H, W] with H, W the last two dims (both operand layouts derived from sgx).
+static size_t bwd2_single_ws_bound(int nd, const int64_t *shape, const int64_t *sgx) {
+    if (nd < 3 || nd > NC_HIP_MAX_DIMS) return 0;
+    int64_t cs[NC_HIP_MAX_DIMS], s = 1;
+    for (int d = nd - 1; d >= 0; d--) {
+        cs[d] = s;
+        s *= shape[d];
+    }
+    // the two broadcast patterns of the fused kernel: a over [P, W] (0 over H), b over [H, W]
+    int64_t sa[NC_HIP_MAX_DIMS], sb[NC_HIP_MAX_DIMS], run = 1;
+    for (int d = nd - 1; d >= 0; d--) {
+        const bool is_h = d == nd - 2;
+        sa[d] = is_h ? 0 : run;
+        if (!is_h) run *= shape[d];
+    }
+    run = 1;
+    for (int d = nd - 1; d >= 0; d--) {
+        const bool plane = d < nd - 2;
+        sb[d] = plane ? 0 : run;
+        if (!plane) run *= shape[d];
+    }
+    (void)sgx;
+    const int64_t *strides[5] = {cs, sa, sb, sa, sb};
+    Prepared p;
+    if (prepare(nd, shape, 5, strides, p, "nc_hip_binary_bwd_workspace")) return 0;
+    Bwd2Plan pl;
+    const float *al = (const float *)(uintptr_t)256;
+    return plan_bwd2(p, al, al, al, al, al, pl) ? bwd2_ws(pl, 3) : 0;
 }
 
 }  // namespace nchip
@@ -842,7 +925,35 @@ extern "C" NC_HIP_API size_t nc_hip_binary_bwd_workspace(int nd, const int64_t *
     if (prepare(nd, shape, 4, strides, p, "nc_hip_binary_bwd_workspace") || p.numel == 0) return 0;
     RedPlan pl;
     size_t need = 0;
-    return plan_reduce(p, pl, &need) ? need : 0;
+    if (!plan_reduce(p, pl, &need)) need = 0;
+    bool reduces = false;
+    for (int d = 0; d < nd; d++) reduces |= sgx[d] == 0 && shape[d] != 1;
+    // room for the fused single-pass kernel when the broadcast has its pattern
+    if (reduces) need = std::max(need, bwd2_single_ws_bound(nd, shape, sgx));
+    return need;
+}
+
+static int prepare_bwd2(int nd, const int64_t *shape, const int64_t *sg, const int64_t *sa, const int64_t *sb,
+                        const int64_t *sga, const int64_t *sgb, Prepared &p);
+
+// One operand's gradient through the fused kernel (the other output switched off), when the
+// broadcast has its pattern and the workspace covers it.  Returns -1 when it does not apply.
+static int try_bwd_fused_single(int op, int which, int nd, const int64_t *shape, const float *g, const int64_t *sg,
+                                const float *a, const int64_t *sa, const float *b, const int64_t *sb, float *gx,
+                                const int64_t *sgx, int accumulate, void *ws, size_t ws_bytes, hipStream_t st) {
+    if (nd < 3 || nd > NC_HIP_MAX_DIMS) return -1;
+    int64_t sgo[NC_HIP_MAX_DIMS];  // layout of the other (unwritten) gradient
+    grad_layout(nd, shape, which == 0 ? sb : sa, sgo);
+    const int64_t *sga = which == 0 ? sgx : sgo, *sgb = which == 0 ? sgo : sgx;
+    const bool reads_ab = op == NC_HIP_BIN_MUL || op == NC_HIP_BIN_DIV;
+    Prepared p;
+    if (prepare_bwd2(nd, shape, sg, reads_ab ? sa : sga, reads_ab ? sb : sgb, sga, sgb, p) != NC_HIP_OK) return -1;
+    Bwd2Plan pl;
+    if (p.numel == 0 || !plan_bwd2(p, g, reads_ab ? a : gx, reads_ab ? b : gx, gx, gx, pl)) return -1;
+    const size_t need = bwd2_ws(pl, which == 0 ? 1 : 2);
+    if (ws_bytes < need || (need && !ws)) return -1;
+    if (which == 0) return launch_bwd2_op<1>(op, g, a, b, gx, nullptr, pl, accumulate, ws, ws_bytes, st);
+    return launch_bwd2_op<2>(op, g, a, b, nullptr, gx, pl, accumulate, ws, ws_bytes, st);
 }
 
 extern "C" NC_HIP_API int nc_hip_binary_bwd(int op, int which, int nd, const int64_t *shape, const float *g,
@@ -860,6 +971,10 @@ extern "C" NC_HIP_API int nc_hip_binary_bwd(int op, int which, int nd, const int
     const float *p1 = p1_is_a ? a : b;
     const float *p2 = b;
     hipStream_t st = as_stream(stream);
+    if (p.numel > 0) {
+        rc = try_bwd_fused_single(op, which, nd, shape, g, sg, a, sa, b, sb, gx, sgx, accumulate, ws, ws_bytes, st);
+        if (rc >= 0) return rc;
+    }
     switch (mode) {
     case 0: return launch_grad<0>(g, g, g, gx, p, alpha, accumulate, ws, ws_bytes, st);
     case 1: return launch_grad<1>(g, p1, g, gx, p, alpha, accumulate, ws, ws_bytes, st);
@@ -909,16 +1024,8 @@ extern "C" NC_HIP_API int nc_hip_binary_bwd2(int op, int nd, const int64_t *shap
         int rc = prepare_bwd2(nd, shape, sg, reads_ab ? sa : sga, reads_ab ? sb : sgb, sga, sgb, p);
         if (rc) return rc;
         Bwd2Plan pl;
-        if (p.numel > 0 && plan_bwd2(p, g, reads_ab ? a : ga, reads_ab ? b : gb, ga, gb, pl)) {
-            hipStream_t st = as_stream(stream);
-            const double alpha_b = op == NC_HIP_BIN_SUB ? -1.0 : 1.0;
-            switch (op) {
-            case NC_HIP_BIN_ADD: return launch_bwd2<0>(g, a, b, ga, gb, pl, alpha_b, accumulate, ws, ws_bytes, st);
-            case NC_HIP_BIN_SUB: return launch_bwd2<0>(g, a, b, ga, gb, pl, alpha_b, accumulate, ws, ws_bytes, st);
-            case NC_HIP_BIN_MUL: return launch_bwd2<1>(g, a, b, ga, gb, pl, alpha_b, accumulate, ws, ws_bytes, st);
-            default: return launch_bwd2<3>(g, a, b, ga, gb, pl, alpha_b, accumulate, ws, ws_bytes, st);
-            }
-        }
+        if (p.numel > 0 && plan_bwd2(p, g, reads_ab ? a : ga, reads_ab ? b : gb, ga, gb, pl))
+            return launch_bwd2_op<3>(op, g, a, b, ga, gb, pl, accumulate, ws, ws_bytes, as_stream(stream));
     }
     int rc = NC_HIP_OK;
     if (ga) rc = nc_hip_binary_bwd(op, 0, nd, shape, g, sg, a, sa, b, sb, ga, sga, accumulate, ws, ws_bytes, stream);

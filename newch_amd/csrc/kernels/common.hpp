@@ -118,6 +118,12 @@ __device__ __forceinline__ float ref_fminf(float a, float b) {
 // ------------------------------------------------------------------------------------------------
 // wave64 reductions (DPP/permute via __shfl_xor, which lowers to ds_swizzle / v_permlane on gfx950)
 // ------------------------------------------------------------------------------------------------
+// Workgroup barrier for LDS traffic only: waits for this wave's LDS operations, then meets the
+// other waves.  Unlike __syncthreads(), whose fence also waits for every outstanding global load,
+// it leaves prefetched global loads in flight.  The memory clobber keeps the compiler from moving
+// memory accesses across it.
+__device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
 __device__ __forceinline__ double wave_sum(double v) {
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, kWave);

@@ -526,6 +526,39 @@ def test_kernel_binary_bwd_fused(K, case, ash, aview, bsh, op, accumulate):
         assert_close64(got, base + red, scale + (np.abs(init) if accumulate else 0), f"{case} {op} grad {name}")
 
 
+@pytest.mark.parametrize("case,ash,aview,bsh", BWD2)
+@pytest.mark.parametrize("op", ["add", "sub", "mul", "div"])
+@pytest.mark.parametrize("accumulate", [True, False])
+def test_kernel_binary_bwd_single(K, case, ash, aview, bsh, op, accumulate):
+    """One operand's gradient at a time (the other needs none), on the broadcast patterns of the
+    one-pass kernel and on its fallbacks."""
+    rng = np.random.default_rng(zlib.crc32(f"single/{case}/{op}/{accumulate}".encode()))
+    A = rng.standard_normal(ash).astype(np.float32)
+    B = (0.5 + 1.5 * rng.random(bsh)).astype(np.float32)
+    a = np_view(A, aview)
+    out_shape = O.broadcast_shape(a.shape, B.shape)
+    G = rng.standard_normal(out_shape).astype(np.float32)
+    sa = bcast_strides(a.shape, strides_of(a), out_shape)
+    sb = bcast_strides(B.shape, strides_of(B), out_shape)
+    so = [s // 4 for s in np.empty(out_shape, np.float32).strides]
+    Ad, Bd, Gd = dev(A), dev(B), dev(G)
+    ta, tb = grad_terms64(op, a, B, G)
+    for which, x, t in ((0, a, ta), (1, B, tb)):
+        init = rng.standard_normal(x.shape).astype(np.float32)
+        GX = dev(init)
+        sgx = bcast_strides(x.shape, [s // 4 for s in np.empty(x.shape, np.float32).strides], out_shape)
+        wsb = K.binary_bwd_workspace(out_shape, sgx)
+        ws = empty(max(wsb, 1))
+        K.binary_bwd(op, which, out_shape, Gd.ptr, so, Ad.ptr, sa, Bd.ptr, sb, GX.ptr, sgx, ws.ptr, wsb,
+                     accumulate=accumulate)
+        sync()
+        red = sum_to(t, x.shape).reshape(x.shape)
+        scale = sum_to(np.abs(t), x.shape).reshape(x.shape) / np.sqrt(max(t.size // max(red.size, 1), 1))
+        base = init.astype(np.float64) if accumulate else 0.0
+        assert_close64(GX.to_numpy(np.float32, x.shape), base + red, scale + (np.abs(init) if accumulate else 0),
+                       f"{case} {op} grad {which}")
+
+
 REDUCE_SHAPES = [((4096, 1024), 1), ((3, 1 << 20), 1), ((64, 1000, 33), 1), ((2, 5000, 3), 1), ((1 << 22,), None),
                  ((7, 13), 0), ((1000, 3), 1), ((5, 4097), 1)]
 
