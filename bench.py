@@ -174,6 +174,20 @@ def class_workloads(K, hm):
          lambda: K.layer_norm_bwd(rows, C, X.ptr, W.ptr, S.ptr, G.ptr, GI.ptr, GW.ptr, GBb.ptr, LWS.ptr, lnws)),
         ("max_argmax", 4 * e + 8 * rows, lambda: K.reduce_fwd("max", rows, C, 1, X.ptr, M.ptr, AR.ptr)),
     ]
+    # cross entropy over the same rows with labels ~ U[0, 1024): fwd reads x, writes prob (8 B/el);
+    # bwd reads prob, read-modify-writes gi (12 B/el)
+    LAB = hm.DeviceBuffer.from_numpy(np.random.default_rng(10).integers(0, C, rows).astype(np.int32))
+    LS, BADF = hm.DeviceBuffer(4), hm.DeviceBuffer(8)
+    GO = hm.DeviceBuffer.from_numpy(np.array([1.0], np.float32))
+    lws = K.loss_workspace(rows, C)
+    LWS2 = hm.DeviceBuffer(max(lws, 8))
+    keep += [LAB, LS, BADF, GO, LWS2]
+    work += [
+        ("cross_entropy_fwd", 8 * e + 4 * rows,
+         lambda: K.cross_entropy_fwd(rows, C, X.ptr, LAB.ptr, Y.ptr, LS.ptr, BADF.ptr, LWS2.ptr, lws)),
+        ("cross_entropy_bwd", 12 * e + 4 * rows,
+         lambda: K.cross_entropy_bwd(rows, C, Y.ptr, LAB.ptr, GO.ptr, GI.ptr, accumulate=True)),
+    ]
     # int8: 48 x W[4096, 4096] quantize per row, dequantize back
     qrows, qcols = 48 * 4096, 4096
     blkw = (np.random.default_rng(11).standard_normal((4096, 4096), dtype=np.float32) * 0.02)

@@ -148,6 +148,27 @@ NC_HIP_API int nc_hip_quantize_rows(int64_t rows, int64_t cols, const float *w, 
 NC_HIP_API int nc_hip_dequantize_rows(int64_t rows, int64_t cols, const int8_t *q, const float *scale, float *w,
                                       void *stream);
 
+/* Losses over rows [N, C] (contiguous) with i32 labels [N].  `loss` and `gout` are one float in
+ * device memory.  `bad` (8 bytes, device) receives all ones, or the first row whose label is outside
+ * [0, C) as (row << 32) | (uint32)label — that row contributes nothing; the caller reads it back to
+ * raise the reference's "label %d at row %lld outside [0, %lld)" error.  Loss sums are fp64 in a
+ * fixed order.  Workspace of both forwards: nc_hip_loss_workspace(N, C) bytes. */
+NC_HIP_API size_t nc_hip_loss_workspace(int64_t N, int64_t C);
+/* Cross entropy (fused log-softmax + NLL, mean over rows; NaN for N = 0): ce_fwd, ops_nn.c:107-131.
+ * prob receives exp(log_softmax(x)) for the backward. */
+NC_HIP_API int nc_hip_cross_entropy_fwd(int64_t N, int64_t C, const float *x, const int32_t *lab, float *prob,
+                                        float *loss, uint64_t *bad, void *ws, size_t ws_bytes, void *stream);
+/* gi (+)= s * prob, then gi[i, lab_i] -= s, with s = gout / N: ce_bwd, ops_nn.c:133-147. */
+NC_HIP_API int nc_hip_cross_entropy_bwd(int64_t N, int64_t C, const float *prob, const int32_t *lab,
+                                        const float *gout, float *gi, int accumulate, void *stream);
+/* NLL over log-probabilities: loss = -sum_i x[i, lab_i] (sum != 0), or that / N (NaN for N = 0):
+ * nll_fwd, ops_nn.c:391-410. */
+NC_HIP_API int nc_hip_nll_loss_fwd(int64_t N, int64_t C, const float *x, const int32_t *lab, int sum,
+                                   float *loss, uint64_t *bad, void *ws, size_t ws_bytes, void *stream);
+/* gi[i, lab_i] -= s, s = gout (sum) or gout / N; gi is read and written: nll_bwd, ops_nn.c:412-420. */
+NC_HIP_API int nc_hip_nll_loss_bwd(int64_t N, int64_t C, const int32_t *lab, const float *gout, int sum,
+                                   float *gi, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

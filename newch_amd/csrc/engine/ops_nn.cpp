@@ -1,5 +1,6 @@
-// softmax / log_softmax over the last axis and LayerNorm over the last k axes.
-// Reference: engine/src/ops/ops_nn.c (:8-77 softmax, :434-538 layer_norm).
+// softmax / log_softmax over the last axis, LayerNorm over the last k axes, and the losses built on
+// the softmax rows.  Reference: engine/src/ops/ops_nn.c (:8-77 softmax, :83-162 cross_entropy and
+// mse_loss, :368-426 nll_loss, :434-538 layer_norm).
 #include "engine.hpp"
 
 namespace nce {
@@ -137,6 +138,99 @@ static void layer_norm_bwd(nc_node *n) {
 
 const OpDef op_layer_norm = {"layer_norm", 0, 0, layer_norm_infer, nullptr, layer_norm_fwd, layer_norm_bwd};
 
+// ---- losses ----------------------------------------------------------------------------------------
+// cross_entropy (ops_nn.c:83-156) and nll_loss (ops_nn.c:368-426): f32 rows [N, C], i32 labels [N],
+// a 0-d f32 loss.  The forward keeps a copy of the labels (and for cross entropy the probabilities)
+// for the backward, as the reference does, and reads the kernel's label check back before returning
+// so an out-of-range label fails the call the reference's way.
+enum { LOSS_CE = 0, LOSS_NLL = 1 };
+
+static nc_status loss_infer(nc_node *n, nc_dtype *dt, int *nd, int64_t *) {
+    nc_tensor *x = n->in[0], *y = n->in[1];
+    const bool ce = n->op->kind == LOSS_CE;
+    if (!expect_f32(n, 0)) return NC_ERR_DTYPE;
+    if (y->dtype != NC_I32) {
+        error(x->ctx, NC_ERR_DTYPE, "%s: labels must be i32", n->op->name);
+        return NC_ERR_DTYPE;
+    }
+    if (x->ndim != 2 || y->ndim != 1 || y->shape[0] != x->shape[0] || (ce && x->shape[1] < 1)) {
+        char sa[96], sb[96];
+        error(x->ctx, NC_ERR_SHAPE, "%s: expected %s [N, C] and labels [N], got %s and %s", n->op->name,
+              ce ? "logits" : "log-probabilities", shape_str(x->ndim, x->shape, sa, sizeof sa),
+              shape_str(y->ndim, y->shape, sb, sizeof sb));
+        return NC_ERR_SHAPE;
+    }
+    *dt = NC_F32;
+    *nd = 0;
+    return NC_OK;
+}
+
+static nc_status loss_fwd(nc_node *n) {
+    nc_tensor *xt = n->in[0], *yt = n->in[1];
+    nc_ctx *ctx = xt->ctx;
+    const bool ce = n->op->kind == LOSS_CE;
+    const int64_t N = xt->shape[0], C = xt->shape[1];
+    float *x = contig_f32(xt), *loss = fptr(n->out);
+    char *labels = dptr(yt);
+    if (!x || !loss || !labels) return NC_ERR_STATE;
+    // saved block: [prob N*C floats (cross entropy)][labels N int32]
+    const size_t pbytes = ce ? (size_t)(N * C) * sizeof(float) : 0;
+    const size_t sbytes = pbytes + (size_t)(N ? N : 1) * sizeof(int32_t);
+    char *saved = arena_alloc(ctx, sbytes);
+    const size_t ws_bytes = nc_hip_loss_workspace(N, C);
+    char *ws = arena_alloc(ctx, ws_bytes ? ws_bytes : 8);
+    uint64_t *bad = (uint64_t *)arena_alloc(ctx, sizeof(uint64_t));
+    if (!saved || !ws || !bad) return NC_ERR_STATE;
+    float *prob = ce ? (float *)saved : nullptr;
+    int32_t *lab = (int32_t *)(saved + pbytes);
+    if (N > 0 && !hip_layer_ok(ctx, nc_hip_copy_strided(4, 1, yt->shape, labels, yt->stride, lab, stream(ctx)),
+                               n->op->name))
+        return NC_ERR_STATE;
+    const int rc = ce ? nc_hip_cross_entropy_fwd(N, C, x, lab, prob, loss, bad, ws, ws_bytes, stream(ctx))
+                      : nc_hip_nll_loss_fwd(N, C, x, lab, (int)n->p.i[0], loss, bad, ws, ws_bytes, stream(ctx));
+    if (!hip_layer_ok(ctx, rc, n->op->name)) return NC_ERR_STATE;
+    uint64_t hb = 0;
+    if (!hip_ok(ctx, hipMemcpyAsync(&hb, bad, sizeof hb, hipMemcpyDeviceToHost, stream(ctx)), n->op->name) ||
+        !hip_ok(ctx, hipStreamSynchronize(stream(ctx)), n->op->name))
+        return NC_ERR_STATE;
+    if (hb != ~(uint64_t)0) {
+        error(ctx, NC_ERR_ARG, "%s: label %d at row %lld outside [0, %lld)", n->op->name, (int32_t)(uint32_t)hb,
+              (long long)(hb >> 32), (long long)C);
+        return NC_ERR_ARG;
+    }
+    n->saved = saved;
+    n->saved_bytes = sbytes;
+    wrote_dev(n->out);
+    return NC_OK;
+}
+
+static void loss_bwd(nc_node *n) {
+    nc_tensor *xt = n->in[0];
+    nc_ctx *ctx = xt->ctx;
+    const bool ce = n->op->kind == LOSS_CE;
+    const int64_t N = xt->shape[0], C = xt->shape[1];
+    if (!grad_buf(xt)) return;
+    float *g = fptr(n->out->grad);
+    if (!g) return;
+    const char *saved = (const char *)n->saved;
+    const size_t pbytes = ce ? (size_t)(N * C) * sizeof(float) : 0;
+    const int32_t *lab = (const int32_t *)(saved + pbytes);
+    int acc = grad_acc(xt);
+    if (!ce && !acc) {  // only the labels' entries change: the rest of a fresh buffer needs its zeros
+        if (!fill_zero(xt->grad)) return;
+        acc = 1;
+    }
+    float *gi = fptr(xt->grad);
+    if (!gi) return;
+    const int rc = ce ? nc_hip_cross_entropy_bwd(N, C, (const float *)saved, lab, g, gi, acc, stream(ctx))
+                      : nc_hip_nll_loss_bwd(N, C, lab, g, (int)n->p.i[0], gi, stream(ctx));
+    if (!hip_layer_ok(ctx, rc, n->op->name)) return;
+    wrote_dev(xt->grad);
+}
+
+const OpDef op_cross_entropy = {"cross_entropy", 0, LOSS_CE, loss_infer, nullptr, loss_fwd, loss_bwd};
+const OpDef op_nll_loss = {"nll_loss", 0, LOSS_NLL, loss_infer, nullptr, loss_fwd, loss_bwd};
+
 }  // namespace nce
 
 using namespace nce;
@@ -144,6 +238,24 @@ using namespace nce;
 extern "C" {
 nc_tensor *nc_log_softmax(nc_tensor *x) { return apply(&op_log_softmax, &x, 1, nullptr); }
 nc_tensor *nc_softmax(nc_tensor *x) { return apply(&op_softmax, &x, 1, nullptr); }
+
+nc_tensor *nc_cross_entropy(nc_tensor *logits, nc_tensor *labels) {
+    nc_tensor *in[2] = {logits, labels};
+    return apply(&op_cross_entropy, in, 2, nullptr);
+}
+
+nc_tensor *nc_nll_loss(nc_tensor *logp, nc_tensor *labels, int sum) {
+    nc_tensor *in[2] = {logp, labels};
+    Params p{};
+    p.i[0] = sum ? 1 : 0;
+    return apply(&op_nll_loss, in, 2, &p);
+}
+
+// composite, differentiable through the ops it is built from (ops_nn.c:158-162)
+nc_tensor *nc_mse_loss(nc_tensor *pred, nc_tensor *target) {
+    nc_tensor *d = nc_sub(pred, target);
+    return nc_mean(nc_mul(d, d), NC_ALL_AXES, 0);
+}
 
 nc_tensor *nc_layer_norm(nc_tensor *x, int normalized_ndim, nc_tensor *weight, nc_tensor *bias, float eps) {
     nc_tensor *in[3] = {x, nullptr, nullptr};

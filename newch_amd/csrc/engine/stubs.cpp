@@ -1,5 +1,5 @@
 // The rest of the reference ABI (engine/include/nc.h) outside this build's hot path: GEMM-based ops,
-// convolution, losses, masking, serialization, modules and optimizers.  Every symbol exists, so the
+// convolution, masking, serialization, modules and optimizers.  Every symbol exists, so the
 // reference's ctypes bindings resolve all their names at import (newch/_lib.py:174-177), and every
 // call fails cleanly the reference way -- a sticky NC_ERR_STATE in the context and a NULL / error
 // result -- instead of computing anything on the host.
@@ -9,7 +9,7 @@ using namespace nce;
 
 static nc_tensor *absent(nc_tensor *any, const char *name) {
     if (any) error(any->ctx, NC_ERR_STATE, "%s: not in this build (the MI355X engine runs the elementwise, "
-                                          "reduction, normalization and int8 hot path)", name);
+                                          "reduction, normalization, loss and int8 hot path)", name);
     return nullptr;
 }
 
@@ -33,9 +33,6 @@ nc_tensor *nc_batch_norm(nc_tensor *x, nc_tensor *, nc_tensor *, nc_tensor *, nc
     return absent(x, "batch_norm");
 }
 nc_tensor *nc_masked_fill(nc_tensor *x, nc_tensor *, float) { return absent(x, "masked_fill"); }
-nc_tensor *nc_cross_entropy(nc_tensor *logits, nc_tensor *) { return absent(logits, "cross_entropy"); }
-nc_tensor *nc_mse_loss(nc_tensor *pred, nc_tensor *) { return absent(pred, "mse_loss"); }
-nc_tensor *nc_nll_loss(nc_tensor *logp, nc_tensor *, int) { return absent(logp, "nll_loss"); }
 nc_tensor *nc_compare(nc_tensor *a, nc_tensor *b, nc_cmp) { return absent(a ? a : b, "compare"); }
 nc_tensor *nc_cat(int n, nc_tensor *const *xs, int) { return absent(n > 0 && xs ? xs[0] : nullptr, "cat"); }
 nc_tensor *nc_linear_int8(nc_tensor *x, nc_tensor *wq, nc_tensor *, nc_tensor *) {

@@ -116,8 +116,12 @@ __device__ __forceinline__ float ref_fminf(float a, float b) {
 }
 
 // ------------------------------------------------------------------------------------------------
-// wave64 reductions (DPP/permute via __shfl_xor, which lowers to ds_swizzle / v_permlane on gfx950)
+// wave64 reductions (__shfl_xor: ds_bpermute / DPP lane exchanges)
 // ------------------------------------------------------------------------------------------------
+// max of a row with the reference's scan semantics (ops_nn.c:23-25): NaN at index 0 wins, later
+// NaNs are skipped (fmaxf ignores them, order-free), otherwise the plain maximum.
+__device__ __forceinline__ float row_max_finish(float m_nonnan, float x0) { return x0 != x0 ? x0 : m_nonnan; }
+
 // Workgroup barrier for LDS traffic only: waits for this wave's LDS operations, then meets the
 // other waves.  Unlike __syncthreads(), whose fence also waits for every outstanding global load,
 // it leaves prefetched global loads in flight.  The memory clobber keeps the compiler from moving

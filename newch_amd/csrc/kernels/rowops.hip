@@ -16,9 +16,6 @@ namespace nchip {
 constexpr int kRowB = 256;             // 4 waves per workgroup, one row per wave
 constexpr int kWavesPerBlock = kRowB / kWave;
 
-// max of a row with the reference's scan semantics (ops_nn.c:23-25): NaN at index 0 wins, later
-// NaNs are skipped (fmaxf ignores them, order-free), otherwise the plain maximum.
-__device__ __forceinline__ float row_max_finish(float m_nonnan, float x0) { return x0 != x0 ? x0 : m_nonnan; }
 
 // ------------------------------------------------------------------------------------------------
 // softmax, register-resident rows

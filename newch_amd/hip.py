@@ -55,6 +55,11 @@ SIGNATURES = {
     "nc_hip_layer_norm_bwd": (c_int, [c_int64, c_int64, P, P, P, P, P, P, P, c_int, P, c_size_t, P]),
     "nc_hip_quantize_rows": (c_int, [c_int64, c_int64, P, P, P, P]),
     "nc_hip_dequantize_rows": (c_int, [c_int64, c_int64, P, P, P, P]),
+    "nc_hip_loss_workspace": (c_size_t, [c_int64, c_int64]),
+    "nc_hip_cross_entropy_fwd": (c_int, [c_int64, c_int64, P, P, P, P, P, P, c_size_t, P]),
+    "nc_hip_cross_entropy_bwd": (c_int, [c_int64, c_int64, P, P, P, P, c_int, P]),
+    "nc_hip_nll_loss_fwd": (c_int, [c_int64, c_int64, P, P, c_int, P, P, P, c_size_t, P]),
+    "nc_hip_nll_loss_bwd": (c_int, [c_int64, c_int64, P, P, c_int, P, P]),
 }
 
 
@@ -148,6 +153,24 @@ class Kernels:
 
     def quantize_rows(self, rows, cols, w, q, scale, stream=None):
         self._ok(self.lib.nc_hip_quantize_rows(rows, cols, w, q, scale, stream), "quantize_rows")
+
+    def loss_workspace(self, N, C):
+        return self.lib.nc_hip_loss_workspace(N, C)
+
+    def cross_entropy_fwd(self, N, C, x, lab, prob, loss, bad, ws, ws_bytes, stream=None):
+        self._ok(self.lib.nc_hip_cross_entropy_fwd(N, C, x, lab, prob, loss, bad, ws, ws_bytes, stream),
+                 "cross_entropy_fwd")
+
+    def cross_entropy_bwd(self, N, C, prob, lab, gout, gi, accumulate=True, stream=None):
+        self._ok(self.lib.nc_hip_cross_entropy_bwd(N, C, prob, lab, gout, gi, int(accumulate), stream),
+                 "cross_entropy_bwd")
+
+    def nll_loss_fwd(self, N, C, x, lab, sum, loss, bad, ws, ws_bytes, stream=None):
+        self._ok(self.lib.nc_hip_nll_loss_fwd(N, C, x, lab, int(sum), loss, bad, ws, ws_bytes, stream),
+                 "nll_loss_fwd")
+
+    def nll_loss_bwd(self, N, C, lab, gout, sum, gi, stream=None):
+        self._ok(self.lib.nc_hip_nll_loss_bwd(N, C, lab, gout, int(sum), gi, stream), "nll_loss_bwd")
 
     def dequantize_rows(self, rows, cols, q, scale, w, stream=None):
         self._ok(self.lib.nc_hip_dequantize_rows(rows, cols, q, scale, w, stream), "dequantize_rows")

@@ -560,3 +560,47 @@ void or_dequantize_rows(int64_t rows, int64_t cols, const int8_t *q, const float
     for (int64_t r = 0; r < rows; r++)
         for (int64_t i = 0; i < cols; i++) w[r * cols + i] = (float)(double)q[r * cols + i] * scale[r];
 }
+
+/* ---------------------------------------------------------------------------------------------- */
+/* cross entropy: ops_nn.c:107-147.  Per row the log-softmax of softmax_row (ops_nn.c:22-36), the  */
+/* loss accumulated in double by subtraction in row order, then the row turned into probabilities  */
+/* by the exp kernel (exp8 in the AVX2 tier); backward: gi += s * prob, gi[label] -= s.             */
+/* ---------------------------------------------------------------------------------------------- */
+int64_t or_cross_entropy_fwd(int64_t N, int64_t C, const float *x, const int32_t *lab, float *prob, float *loss) {
+    double l = 0.0;
+    for (int64_t i = 0; i < N; i++) {
+        if (lab[i] < 0 || lab[i] >= C) return i;
+        float *p = prob + i * C;
+        or_softmax_fwd(1, 1, C, x + i * C, p);
+        l -= p[lab[i]];
+        for (int64_t c = 0; c < C; c++) p[c] = or_exp(p[c]);
+    }
+    *loss = N ? (float)(l / (double)N) : NAN;
+    return -1;
+}
+
+void or_cross_entropy_bwd(int64_t N, int64_t C, const float *prob, const int32_t *lab, float gout, float *gi) {
+    const float s = gout / (float)(N ? N : 1);
+    for (int64_t i = 0; i < N; i++) {
+        for (int64_t c = 0; c < C; c++) gi[i * C + c] = gi[i * C + c] + s * prob[i * C + c];
+        gi[i * C + lab[i]] = gi[i * C + lab[i]] - s;
+    }
+}
+
+/* ---------------------------------------------------------------------------------------------- */
+/* nll loss: ops_nn.c:391-420 (double accumulation by subtraction in row order)                   */
+/* ---------------------------------------------------------------------------------------------- */
+int64_t or_nll_loss_fwd(int64_t N, int64_t C, const float *x, const int32_t *lab, int sum, float *loss) {
+    double l = 0.0;
+    for (int64_t i = 0; i < N; i++) {
+        if (lab[i] < 0 || lab[i] >= C) return i;
+        l -= x[i * C + lab[i]];
+    }
+    *loss = sum ? (float)l : N ? (float)(l / (double)N) : NAN;
+    return -1;
+}
+
+void or_nll_loss_bwd(int64_t N, int64_t C, const int32_t *lab, float gout, int sum, float *gi) {
+    const float s = sum ? gout : gout / (float)(N ? N : 1);
+    for (int64_t i = 0; i < N; i++) gi[i * C + lab[i]] = gi[i * C + lab[i]] - s;
+}

@@ -75,6 +75,16 @@ void or_layer_norm_bwd(int64_t rows, int64_t D, const float *x, const float *w, 
 void or_quantize_rows(int64_t rows, int64_t cols, const float *w, int8_t *q, float *scale);
 void or_dequantize_rows(int64_t rows, int64_t cols, const int8_t *q, const float *scale, float *w);
 
+/* cross entropy over logits [N, C] with labels [N] (mean over rows): prob [N, C] receives
+ * exp(log_softmax(x)), *loss the mean; returns -1, or the first row whose label is outside [0, C). */
+int64_t or_cross_entropy_fwd(int64_t N, int64_t C, const float *x, const int32_t *lab, float *prob, float *loss);
+/* gi (accumulated) += (gout / N) * prob; gi[i, lab_i] -= gout / N */
+void or_cross_entropy_bwd(int64_t N, int64_t C, const float *prob, const int32_t *lab, float gout, float *gi);
+/* nll loss over log-probabilities [N, C]: -sum of x[i, lab_i], or its mean (sum == 0); returns -1 or
+ * the first row with an out-of-range label */
+int64_t or_nll_loss_fwd(int64_t N, int64_t C, const float *x, const int32_t *lab, int sum, float *loss);
+void or_nll_loss_bwd(int64_t N, int64_t C, const int32_t *lab, float gout, int sum, float *gi);
+
 #ifdef __cplusplus
 }
 #endif

@@ -223,3 +223,48 @@ def dequantize_rows(q, scale):
     w = np.empty((rows, cols), np.float32)
     lib().or_dequantize_rows(c_int64(rows), c_int64(cols), _p(q), _p(_f32(scale)), _p(w))
     return w
+
+
+def cross_entropy_fwd(x, lab):
+    """(loss, prob) of cross_entropy(x [N, C], lab [N]); raises ValueError naming the first bad row."""
+    x = _f32(x)
+    lab = np.ascontiguousarray(lab, np.int32)
+    N, C = x.shape
+    prob = np.empty_like(x)
+    loss = c_float(0.0)
+    L = lib()
+    L.or_cross_entropy_fwd.restype = c_int64
+    bad = L.or_cross_entropy_fwd(c_int64(N), c_int64(C), _p(x), _p(lab), _p(prob), ctypes.byref(loss))
+    if bad >= 0:
+        raise ValueError(f"label {int(lab[bad])} at row {bad} outside [0, {C})")
+    return np.float32(loss.value), prob
+
+
+def cross_entropy_bwd(prob, lab, gout, gi=None):
+    prob = _f32(prob)
+    lab = np.ascontiguousarray(lab, np.int32)
+    N, C = prob.shape
+    gi = np.zeros_like(prob) if gi is None else _f32(gi).copy()
+    lib().or_cross_entropy_bwd(c_int64(N), c_int64(C), _p(prob), _p(lab), c_float(gout), _p(gi))
+    return gi
+
+
+def nll_loss_fwd(x, lab, sum=False):
+    x = _f32(x)
+    lab = np.ascontiguousarray(lab, np.int32)
+    N, C = x.shape
+    loss = c_float(0.0)
+    L = lib()
+    L.or_nll_loss_fwd.restype = c_int64
+    bad = L.or_nll_loss_fwd(c_int64(N), c_int64(C), _p(x), _p(lab), c_int(int(sum)), ctypes.byref(loss))
+    if bad >= 0:
+        raise ValueError(f"label {int(lab[bad])} at row {bad} outside [0, {C})")
+    return np.float32(loss.value)
+
+
+def nll_loss_bwd(shape, lab, gout, sum=False, gi=None):
+    N, C = shape
+    lab = np.ascontiguousarray(lab, np.int32)
+    gi = np.zeros((N, C), np.float32) if gi is None else _f32(gi).copy()
+    lib().or_nll_loss_bwd(c_int64(N), c_int64(C), _p(lab), c_float(gout), c_int(int(sum)), _p(gi))
+    return gi

@@ -341,26 +341,82 @@ def gen_chain(ref, rng):
     ref.step_end()
 
 
+def gen_loss(ref, rng):
+    """cross_entropy and nll_loss (mean and sum): loss, and the input gradient for an upstream grad
+    G (a scalar), from a retained backward; plus the reference's messages for out-of-range labels."""
+    res = {}
+    cases = [("3x5", 3, 5), ("8x10", 8, 10), ("4x1", 4, 1), ("6x64", 6, 64), ("5x1030", 5, 1030), ("0x7", 0, 7)]
+    for key, N, C in cases:
+        X = (rng.standard_normal((N, C)) * 3).astype(np.float32)
+        lab = rng.integers(0, C, N).astype(np.int32)
+        if N >= 4:
+            lab[0], lab[1] = 0, C - 1
+        if N >= 4 and C >= 7:
+            X[2, 3] = -np.inf
+            X[3, :] = 0.0  # a uniform row
+        res[f"{key}/x"] = X
+        res[f"{key}/lab"] = lab
+        G = np.float32(rng.standard_normal())
+        res[f"{key}/G"] = G
+        for form in ("ce", "nll_mean", "nll_sum"):
+            p = ref.param(X)
+            t = ref.tensor(lab, dtype=abi.I32)
+            if form == "ce":
+                out = ref.lib.nc_cross_entropy(p, t)
+            else:
+                out = ref.lib.nc_nll_loss(p, t, int(form == "nll_sum"))
+            res[f"{key}/{form}/loss"] = ref.read(out)
+            if N > 0:
+                ref.backward_with(out, np.asarray(G))
+                res[f"{key}/{form}/gx"] = ref.grad(p)
+            ref.step_end()
+    # out-of-range labels: the reference's error text
+    X = rng.standard_normal((4, 6)).astype(np.float32)
+    for name, lab in (("high", [0, 1, 6, 2]), ("negative", [0, -1, 2, 9])):
+        lab = np.array(lab, np.int32)
+        for form, fn in (("ce", lambda p, t: ref.lib.nc_cross_entropy(p, t)),
+                         ("nll", lambda p, t: ref.lib.nc_nll_loss(p, t, 0))):
+            out = fn(ref.tensor(X), ref.tensor(lab, dtype=abi.I32))
+            assert not out and not ref.lib.nc_ok(ref.ctx)
+            res[f"bad_{name}/{form}/message"] = np.array(ref.lib.nc_error(ref.ctx).decode())
+            res[f"bad_{name}/{form}/status"] = np.int32(ref.lib.nc_status_code(ref.ctx))
+            ref.lib.nc_clear_error(ref.ctx)
+        res[f"bad_{name}/x"] = X
+        res[f"bad_{name}/lab"] = lab
+    ref.step_end()
+    np.savez_compressed(OUT / "loss.npz", **res)
+
+
+GENERATORS = ["transcendentals", "unary", "binary", "reduce", "softmax", "layer_norm", "quant", "chain", "loss"]
+
+
 def main():
     lib = abi.load(REF_LIB)
     lib.ncref_backend.restype = ctypes.c_char_p
     backend = lib.ncref_backend().decode()
     if backend != "avx2":
         raise SystemExit(f"reference kernel tier is {backend!r}; fixtures must come from the avx2 tier")
-    rng = np.random.default_rng(20261201)
+    # every generator draws from its own seeded stream, so one fixture can be rewritten alone:
+    #   python tests/golden/gen_golden.py loss
+    only = sys.argv[1:] or GENERATORS
     ref = Ref(lib)
-    gen_transcendentals(lib, rng)
-    gen_unary(ref, rng)
-    gen_binary(ref, rng)
-    gen_reduce(ref, rng)
-    gen_softmax(ref, rng)
-    gen_layer_norm(ref, rng)
-    gen_quant(ref, rng)
-    gen_chain(ref, rng)
+    rng = np.random.default_rng(20261201)  # the first eight share one stream, in this order
+    if any(g in only for g in GENERATORS[:8]):
+        gen_transcendentals(lib, rng)
+        gen_unary(ref, rng)
+        gen_binary(ref, rng)
+        gen_reduce(ref, rng)
+        gen_softmax(ref, rng)
+        gen_layer_norm(ref, rng)
+        gen_quant(ref, rng)
+        gen_chain(ref, rng)
+    if "loss" in only:
+        gen_loss(ref, np.random.default_rng(20261202))
     (OUT / "PROVENANCE.txt").write_text(
         "Written by tests/golden/gen_golden.py from oracle/_ref/libnc_ref.so, which oracle/Makefile builds\n"
         "from the reference engine sources (engine/src/**/*.c) with gcc 11.4, -O2 -std=gnu11, x86-64\n"
-        f"baseline + AVX2/FMA target functions; kernel tier: {backend}; numpy seed 20261201.\n")
+        f"baseline + AVX2/FMA target functions; kernel tier: {backend}; numpy seeds 20261201 (one stream\n"
+        "for transcendentals .. chain, in that order) and 20261202 (loss).\n")
     for f in sorted(OUT.glob("*.npz")):
         print(f"{f.name}: {f.stat().st_size / 1024:.0f} KiB")
 

@@ -730,6 +730,204 @@ def test_kernel_layer_norm_bwd_modes(K, rows, D, mode):
         assert (GW.to_numpy(np.float32, D) == 0).all() and (GB.to_numpy(np.float32, D) == 0).all()
 
 
+# ------------------------------------------------------------------------------------------------
+# losses
+# ------------------------------------------------------------------------------------------------
+LOSS_KEYS = ["3x5", "8x10", "4x1", "6x64", "5x1030", "0x7"]
+
+
+def loss_ref64(x, lab, form):
+    """fp64 loss and the per-row scale of its terms (the bar's 'scale')."""
+    X = np.asarray(x, np.float64)
+    N = X.shape[0]
+    if N == 0:
+        return (np.nan if form != "nll_sum" else 0.0), 0.0
+    if form == "ce":
+        m = X.max(1, keepdims=True)
+        with np.errstate(invalid="ignore", divide="ignore"):
+            lse = m[:, 0] + np.log(np.exp(X - m).sum(1))
+            terms = lse - X[np.arange(N), lab]
+    else:
+        terms = -X[np.arange(N), lab]
+    total = terms.sum()
+    scale = np.abs(terms).sum() / np.sqrt(N)
+    return (total / N if form != "nll_sum" else total), (scale / N if form != "nll_sum" else scale)
+
+
+@pytest.mark.parametrize("key", LOSS_KEYS)
+def test_engine_loss_golden(eng, key):
+    """cross_entropy / nll_loss through nc.h against the reference's fixtures: nll gradients bit for
+    bit, losses and cross-entropy gradients within the reductions' 1e-5 bar."""
+    d = load("loss")
+    x, lab, G = d[f"{key}/x"], d[f"{key}/lab"], d[f"{key}/G"]
+    N, C = x.shape
+    L = eng.lib
+    for form in ("ce", "nll_mean", "nll_sum"):
+        p = eng.param(x)
+        t = eng.tensor(lab)
+        out = L.nc_cross_entropy(p, t) if form == "ce" else L.nc_nll_loss(p, t, int(form == "nll_sum"))
+        got = eng.read(out)
+        want = d[f"{key}/{form}/loss"]
+        ref64, scale = loss_ref64(x, lab, form)
+        assert_close64(got, ref64, scale, f"{key} {form} loss")
+        assert_close64(want, ref64, scale, f"{key} {form} reference loss (sanity)")
+        if N:
+            eng.backward_with(out, np.asarray(G))
+            gx = eng.grad(p)
+            if form == "ce":
+                P = np.exp(np.asarray(O.softmax_fwd(x, log_form=True), np.float64))
+                onehot = np.zeros_like(P)
+                onehot[np.arange(N), lab] = 1.0
+                g64 = (P - onehot) * (float(G) / N)
+                assert_close64(gx, g64, np.abs(float(G) / N) * (P + onehot), f"{key} ce grad")
+                assert_close64(d[f"{key}/ce/gx"], g64, np.abs(float(G) / N) * (P + onehot), f"{key} ref grad")
+            else:
+                assert_bits(gx, d[f"{key}/{form}/gx"], f"{key} {form} grad")
+        eng.step_end()
+
+
+@pytest.mark.parametrize("which", ["high", "negative"])
+def test_engine_loss_bad_label(eng, which):
+    """An out-of-range label fails the call with the reference's status and message."""
+    d = load("loss")
+    L = eng.lib
+    for form, fn in (("ce", lambda p, t: L.nc_cross_entropy(p, t)), ("nll", lambda p, t: L.nc_nll_loss(p, t, 0))):
+        out = fn(eng.tensor(d[f"bad_{which}/x"]), eng.tensor(d[f"bad_{which}/lab"]))
+        assert not out
+        assert L.nc_status_code(eng.ctx) == int(d[f"bad_{which}/{form}/status"])
+        assert L.nc_error(eng.ctx).decode() == str(d[f"bad_{which}/{form}/message"])
+        L.nc_clear_error(eng.ctx)
+        eng.step_end()
+    # the context keeps working
+    assert eng.read(L.nc_nll_loss(eng.tensor(np.ones((2, 3), np.float32)), eng.tensor(np.array([0, 2], np.int32)),
+                                  1)) == -2.0
+    eng.step_end()
+
+
+def test_engine_mse_loss(eng):
+    L = eng.lib
+    rng = np.random.default_rng(11)
+    a, b = rng.standard_normal((7, 9)).astype(np.float32), rng.standard_normal((7, 9)).astype(np.float32)
+    pa = eng.param(a)
+    out = L.nc_mse_loss(pa, eng.tensor(b))
+    d64 = a.astype(np.float64) - b
+    assert_close64(eng.read(out), (d64 * d64).mean(), (d64 * d64).mean(), "mse")
+    eng.backward_with(out, np.asarray(np.float32(1.5)))
+    assert_close64(eng.grad(pa), 1.5 * 2 * d64 / d64.size, np.abs(1.5 * 2 * d64 / d64.size), "mse grad")
+    eng.step_end()
+
+
+LOSS_SHAPES = [(2048, 1024), (1000, 32), (64, 4096), (300, 100), (17, 8192), (5, 1), (129, 260)]
+
+
+@pytest.mark.parametrize("N,C", LOSS_SHAPES)
+def test_kernel_cross_entropy(K, N, C):
+    """Register rows (C % 4 == 0, C <= 4096) and the generic path; loss within the bar, prob within a
+    few ulp of the oracle's, the backward bit for bit given the kernel's own prob."""
+    rng = np.random.default_rng(N * 10007 + C)
+    x = (rng.standard_normal((N, C)) * 3).astype(np.float32)
+    if C >= 8:
+        x[1, 5] = -np.inf  # a zero probability
+    lab = rng.integers(0, C, N).astype(np.int32)
+    Xd, Ld = dev(x), dev(lab)
+    P, LS, BAD = empty(4 * N * C), empty(4), empty(8)
+    wsb = K.loss_workspace(N, C)
+    ws = empty(max(wsb, 8))
+    K.cross_entropy_fwd(N, C, Xd.ptr, Ld.ptr, P.ptr, LS.ptr, BAD.ptr, ws.ptr, wsb)
+    sync()
+    assert BAD.to_numpy(np.uint64, 1)[0] == np.uint64(0xFFFFFFFFFFFFFFFF)
+    loss_o, prob_o = O.cross_entropy_fwd(x, lab)
+    prob = P.to_numpy(np.float32, (N, C))
+    fin = np.isfinite(prob_o)
+    assert (np.isnan(prob) == np.isnan(prob_o)).all()
+    # exp of a log-probability whose log-sum-exp is rounded from an fp64 row sum (the reference: fp32)
+    assert np.allclose(prob[fin], prob_o[fin], rtol=1e-5, atol=1e-30), "prob"
+    got = LS.to_numpy(np.float32, 1)[0]
+    ref64, scale = loss_ref64(x, lab, "ce")
+    assert_close64(got, ref64, scale, "cross_entropy loss")
+    assert abs(float(got) - float(loss_o)) <= 1e-5 * abs(float(loss_o)), (got, loss_o)
+    gout = np.float32(rng.standard_normal())
+    GO = dev(np.array([gout], np.float32))
+    for acc in (True, False):
+        gi0 = rng.standard_normal((N, C)).astype(np.float32)
+        GI = dev(gi0)
+        K.cross_entropy_bwd(N, C, P.ptr, Ld.ptr, GO.ptr, GI.ptr, accumulate=acc)
+        sync()
+        want = O.cross_entropy_bwd(prob, lab, float(gout), gi0 if acc else None)
+        assert_bits(GI.to_numpy(np.float32, (N, C)), want, f"ce bwd acc={acc}")
+
+
+@pytest.mark.parametrize("N,C", [(65536, 1024), (1000, 7), (3, 1), (0, 5)])
+@pytest.mark.parametrize("sum_", [False, True])
+def test_kernel_nll_loss(K, N, C, sum_):
+    rng = np.random.default_rng(N + C + int(sum_))
+    x = rng.standard_normal((N, C)).astype(np.float32)
+    lab = rng.integers(0, C, N).astype(np.int32)
+    Xd, Ld = dev(x), dev(lab)
+    LS, BAD = empty(4), empty(8)
+    wsb = K.loss_workspace(N, C)
+    ws = empty(max(wsb, 8))
+    K.nll_loss_fwd(N, C, Xd.ptr, Ld.ptr, sum_, LS.ptr, BAD.ptr, ws.ptr, wsb)
+    sync()
+    assert BAD.to_numpy(np.uint64, 1)[0] == np.uint64(0xFFFFFFFFFFFFFFFF)
+    got = LS.to_numpy(np.float32, 1)[0]
+    want = O.nll_loss_fwd(x, lab, sum_)
+    if N == 0:
+        assert (np.isnan(got) and np.isnan(want)) or got == want
+        return
+    ref64, scale = loss_ref64(x, lab, "nll_sum" if sum_ else "nll_mean")
+    assert_close64(got, ref64, scale, "nll loss")
+    gout = np.float32(0.75)
+    GO = dev(np.array([gout], np.float32))
+    gi0 = rng.standard_normal((N, C)).astype(np.float32)
+    GI = dev(gi0)
+    K.nll_loss_bwd(N, C, Ld.ptr, GO.ptr, sum_, GI.ptr)
+    sync()
+    assert_bits(GI.to_numpy(np.float32, (N, C)), O.nll_loss_bwd((N, C), lab, float(gout), sum_, gi0), "nll bwd")
+
+
+def test_kernel_cross_entropy_nan_rows(K):
+    """NaN logits: at index 0 the row maximum is NaN (the reference's scan keeps it), later ones make
+    the exp sum NaN; either way the row's probabilities and the loss are NaN, other rows unaffected."""
+    N, C = 6, 8
+    rng = np.random.default_rng(8)
+    x = rng.standard_normal((N, C)).astype(np.float32)
+    x[1, 0] = np.nan
+    x[3, 5] = np.nan
+    lab = np.arange(N, dtype=np.int32) % C
+    Xd, Ld = dev(x), dev(lab)
+    P, LS, BAD = empty(4 * N * C), empty(4), empty(8)
+    wsb = K.loss_workspace(N, C)
+    ws = empty(max(wsb, 8))
+    K.cross_entropy_fwd(N, C, Xd.ptr, Ld.ptr, P.ptr, LS.ptr, BAD.ptr, ws.ptr, wsb)
+    sync()
+    loss_o, prob_o = O.cross_entropy_fwd(x, lab)
+    prob = P.to_numpy(np.float32, (N, C))
+    assert (np.isnan(prob) == np.isnan(prob_o)).all() and np.isnan(prob[[1, 3]]).all()
+    assert np.allclose(prob[[0, 2, 4, 5]], prob_o[[0, 2, 4, 5]], rtol=1e-5)
+    assert np.isnan(LS.to_numpy(np.float32, 1)[0]) and np.isnan(loss_o)
+
+
+def test_kernel_loss_bad_labels(K):
+    """The first row with an out-of-range label, packed (row << 32) | label, whatever the launch order."""
+    N, C = 5000, 64
+    rng = np.random.default_rng(3)
+    x = rng.standard_normal((N, C)).astype(np.float32)
+    lab = rng.integers(0, C, N).astype(np.int32)
+    lab[[4321, 777, 4999]] = [C, -3, 1000]
+    Xd, Ld = dev(x), dev(lab)
+    P, LS, BAD = empty(4 * N * C), empty(4), empty(8)
+    wsb = K.loss_workspace(N, C)
+    ws = empty(max(wsb, 8))
+    want = np.uint64((777 << 32) | (-3 & 0xFFFFFFFF))
+    K.cross_entropy_fwd(N, C, Xd.ptr, Ld.ptr, P.ptr, LS.ptr, BAD.ptr, ws.ptr, wsb)
+    sync()
+    assert BAD.to_numpy(np.uint64, 1)[0] == want
+    K.nll_loss_fwd(N, C, Xd.ptr, Ld.ptr, False, LS.ptr, BAD.ptr, ws.ptr, wsb)
+    sync()
+    assert BAD.to_numpy(np.uint64, 1)[0] == want
+
+
 @pytest.mark.parametrize("rows,cols", [(512, 4096), (96, 70), (64, 8192), (33, 10000), (8, 16)])
 def test_kernel_quantize(K, rows, cols):
     rng = np.random.default_rng(rows * cols)

@@ -151,6 +151,16 @@ SHAPE_ERRORS = [
     lambda e: e.lib.nc_to_dtype(e.tensor(np.ones((2,), np.float32)), abi.F16),
     lambda e: e.lib.nc_empty(e.ctx, abi.F32, 7, abi.shape_arg((1,) * 7)[1]),
     lambda e: e.lib.nc_empty(e.ctx, abi.F32, 2, abi.shape_arg((2, -1))[1]),
+    # losses: label dtype, logits / labels shapes, empty classes
+    lambda e: e.lib.nc_cross_entropy(e.tensor(np.ones((2, 3), np.float32)), e.tensor(np.zeros(2, np.float32))),
+    lambda e: e.lib.nc_cross_entropy(e.tensor(np.ones((2, 3, 1), np.float32)), e.tensor(np.zeros(2, np.int32))),
+    lambda e: e.lib.nc_cross_entropy(e.tensor(np.ones((2, 3), np.float32)), e.tensor(np.zeros(3, np.int32))),
+    lambda e: e.lib.nc_cross_entropy(e.tensor(np.ones((2, 0), np.float32)), e.tensor(np.zeros(2, np.int32))),
+    lambda e: e.lib.nc_cross_entropy(e.tensor(np.ones((2, 3), np.int32)), e.tensor(np.zeros(2, np.int32))),
+    lambda e: e.lib.nc_nll_loss(e.tensor(np.ones((4,), np.float32)), e.tensor(np.zeros(4, np.int32)), 0),
+    lambda e: e.lib.nc_nll_loss(e.tensor(np.ones((2, 3), np.float32)), e.tensor(np.zeros((2, 1), np.int32)), 1),
+    lambda e: e.lib.nc_nll_loss(e.tensor(np.ones((2, 3), np.float32)), e.tensor(np.zeros(2, np.int8)), 0),
+    lambda e: e.lib.nc_mse_loss(e.tensor(np.ones((2, 3), np.float32)), e.tensor(np.ones((4,), np.float32))),
 ]
 
 

@@ -186,6 +186,35 @@ def test_chain_golden():
     assert_bits(gb, d["gbias"], "chain grad bias")
 
 
+LOSS_CASES = ["3x5", "8x10", "4x1", "6x64", "5x1030", "0x7"]
+
+
+@pytest.mark.parametrize("key", LOSS_CASES)
+def test_loss_golden(key):
+    d = load("loss")
+    x, lab, G = d[f"{key}/x"], d[f"{key}/lab"], float(d[f"{key}/G"])
+    N = x.shape[0]
+    loss, prob = O.cross_entropy_fwd(x, lab)
+    assert_bits(loss, d[f"{key}/ce/loss"], f"{key} cross_entropy")
+    if N:
+        assert_bits(O.cross_entropy_bwd(prob, lab, G), d[f"{key}/ce/gx"], f"{key} cross_entropy bwd")
+    for form, sm in (("nll_mean", False), ("nll_sum", True)):
+        assert_bits(O.nll_loss_fwd(x, lab, sm), d[f"{key}/{form}/loss"], f"{key} {form}")
+        if N:
+            assert_bits(O.nll_loss_bwd(x.shape, lab, G, sm), d[f"{key}/{form}/gx"], f"{key} {form} bwd")
+
+
+@pytest.mark.parametrize("which", ["high", "negative"])
+def test_loss_bad_label_golden(which):
+    d = load("loss")
+    x, lab = d[f"bad_{which}/x"], d[f"bad_{which}/lab"]
+    for form, fn in (("ce", lambda: O.cross_entropy_fwd(x, lab)), ("nll", lambda: O.nll_loss_fwd(x, lab))):
+        with pytest.raises(ValueError) as e:
+            fn()
+        msg = str(d[f"bad_{which}/{form}/message"])
+        assert msg.endswith(str(e.value)), (msg, str(e.value))
+
+
 # ------------------------------------------------------------------------------------------------
 # the live reference (only where oracle/_ref was built: this container, or a box it travelled to)
 # ------------------------------------------------------------------------------------------------
@@ -220,9 +249,65 @@ def test_unary_vs_live_reference(name, kind, s):
     assert_bits(O.unary_bwd(kind, x, y, g, s=s), gx_ref, name + " bwd")
 
 
+@ref_only
+@pytest.mark.parametrize("N,C", [(33, 257), (64, 1024), (7, 3)])
+def test_loss_vs_live_reference(N, C):
+    from tests.ncdrive import Engine
+    rng = np.random.default_rng(N * 1000 + C)
+    x = (rng.standard_normal((N, C)) * 4).astype(np.float32)
+    lab = rng.integers(0, C, N).astype(np.int32)
+    G = np.float32(rng.standard_normal())
+    loss, prob = O.cross_entropy_fwd(x, lab)
+    with Engine(O.REF_LIB) as ref:
+        L = ref.lib
+        for form in ("ce", "mean", "sum"):
+            p = ref.param(x)
+            t = ref.tensor(lab)
+            out = L.nc_cross_entropy(p, t) if form == "ce" else L.nc_nll_loss(p, t, int(form == "sum"))
+            got = ref.read(out)
+            ref.backward_with(out, np.asarray(G))
+            gx = ref.grad(p)
+            if form == "ce":
+                assert_bits(loss, got, "cross_entropy")
+                assert_bits(O.cross_entropy_bwd(prob, lab, float(G)), gx, "cross_entropy bwd")
+            else:
+                assert_bits(O.nll_loss_fwd(x, lab, form == "sum"), got, f"nll {form}")
+                assert_bits(O.nll_loss_bwd(x.shape, lab, float(G), form == "sum"), gx, f"nll {form} bwd")
+            ref.step_end()
+
+
 # ------------------------------------------------------------------------------------------------
 # closed forms, invariants and the reference's own known answers
 # ------------------------------------------------------------------------------------------------
+def test_loss_closed_forms():
+    rng = np.random.default_rng(5)
+    # uniform logits: every row's loss is log(C), every probability 1/C
+    for C in (1, 2, 7, 1000):
+        loss, prob = O.cross_entropy_fwd(np.full((3, C), 2.5, np.float32), np.zeros(3, np.int32))
+        assert abs(float(loss) - math.log(C)) <= 4e-7 * max(1.0, math.log(C))
+        assert np.allclose(prob, 1.0 / C, rtol=2e-7)
+    x = (rng.standard_normal((50, 40)) * 3).astype(np.float32)
+    lab = rng.integers(0, 40, 50).astype(np.int32)
+    loss, prob = O.cross_entropy_fwd(x, lab)
+    X = x.astype(np.float64)
+    lse = X.max(1) + np.log(np.exp(X - X.max(1, keepdims=True)).sum(1))
+    want = float(np.mean(lse - X[np.arange(50), lab]))
+    assert abs(float(loss) - want) <= 1e-5 * abs(want)
+    # cross entropy = nll of the log-softmax (same arithmetic, same rows)
+    assert O.nll_loss_fwd(O.softmax_fwd(x, log_form=True), lab) == loss
+    # gradient of the mean loss: (prob - onehot) / N; each row sums to ~0
+    gx = O.cross_entropy_bwd(prob, lab, 1.0)
+    onehot = np.zeros_like(X)
+    onehot[np.arange(50), lab] = 1.0
+    assert np.allclose(gx, (prob - onehot) / 50, atol=1e-7)
+    assert np.abs(gx.sum(1)).max() < 1e-7
+    # nll: mean = sum / N; gradient -G at the label only, scaled by 1/N for the mean
+    assert O.nll_loss_fwd(x, lab, True) == np.float32(-np.float64(x[np.arange(50), lab]).sum())
+    g = O.nll_loss_bwd(x.shape, lab, 2.0, sum=False)
+    assert (g[np.arange(50), lab] == np.float32(-2.0 / 50)).all() and np.count_nonzero(g) == 50
+    # rows sharing a label accumulate
+    g2 = O.nll_loss_bwd((2, 3), np.array([1, 1], np.int32), 1.0, sum=True)
+    assert g2.tolist() == [[0, -1, 0], [0, -1, 0]]
 def test_known_answers_from_reference_tests():
     # engine/tests/test_main.c:335-341
     t = np.array([-1.0, 0.5, 4.0], np.float32)
