@@ -169,6 +169,20 @@ NC_HIP_API int nc_hip_nll_loss_fwd(int64_t N, int64_t C, const float *x, const i
 NC_HIP_API int nc_hip_nll_loss_bwd(int64_t N, int64_t C, const int32_t *lab, const float *gout, int sum,
                                    float *gi, void *stream);
 
+/* One optimizer update of a parameter w [n] with gradient g (optim.c:161-216): the reference's fp32
+ * expression per element, in its order, without fused multiply-adds.  kind: NC_HIP_OPT_*.  s1 is
+ * the momentum buffer (SGD, RMSprop; NULL without momentum) or Adam's m, s2 Adam's v or RMSprop's
+ * square average.  gs = 1 / accumulation steps; bc1, bc2 = Adam's 1 - beta^t (1 otherwise). */
+enum { NC_HIP_OPT_SGD = 0, NC_HIP_OPT_ADAM = 1, NC_HIP_OPT_ADAMW = 2, NC_HIP_OPT_RMSPROP = 3 };
+NC_HIP_API int nc_hip_optim_step(int kind, int64_t n, float *w, const float *g, float *s1, float *s2, float lr,
+                                 float momentum, float weight_decay, float beta1, float beta2, float eps, float gs,
+                                 float bc1, float bc2, int eps_inside_sqrt, void *stream);
+/* ss (+)= sum of x[i]^2 in fp64 (one double in device memory), clip_grad_norm's sum
+ * (optim.c:219-225); fixed order.  Workspace: nc_hip_sumsq_workspace(n). */
+NC_HIP_API size_t nc_hip_sumsq_workspace(int64_t n);
+NC_HIP_API int nc_hip_sumsq(int64_t n, const float *x, double *ss, int accumulate, void *ws, size_t ws_bytes,
+                            void *stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -368,6 +368,7 @@ void nc_free_ctx(nc_ctx *ctx) {
         (void)hipStreamSynchronize(ctx->stream);
     }
     nc_step_end(ctx);
+    while (!ctx->optims.empty()) nc_optim_free(ctx->optims.back());
     for (nc_tensor *t : ctx->persistent) {
         if (t->dev && (t->flags & TF_OWNS_DATA)) (void)hipFree(t->dev);
         free(t->host);

@@ -154,6 +154,8 @@ struct nc_ctx {
     nc_cpu_info cpu{};
     int n_threads = 1;
 
+    std::vector<nc_optim *> optims;  // live optimizers, freed at nc_free_ctx
+
     int device = -1;  // -1: no HIP device
     hipStream_t stream = nullptr;
     bool own_stream = false;

@@ -1,5 +1,5 @@
 // The rest of the reference ABI (engine/include/nc.h) outside this build's hot path: GEMM-based ops,
-// convolution, masking, serialization, modules and optimizers.  Every symbol exists, so the
+// convolution, masking, serialization and modules.  Every symbol exists, so the
 // reference's ctypes bindings resolve all their names at import (newch/_lib.py:174-177), and every
 // call fails cleanly the reference way -- a sticky NC_ERR_STATE in the context and a NULL / error
 // result -- instead of computing anything on the host.
@@ -64,28 +64,5 @@ nc_tensor *nc_forward(nc_module *, nc_tensor *x) { return absent(x, "nc_forward"
 int nc_parameters(nc_module *, nc_tensor **, int) { return 0; }
 const char *nc_module_name(const nc_module *) { return ""; }
 void nc_set_training(nc_module *, int) {}
-
-static nc_optim *no_optim(nc_ctx *ctx, const char *name) {
-    absent_ctx(ctx, name);
-    return nullptr;
-}
-nc_optim *nc_sgd(nc_ctx *ctx, nc_tensor **, int, nc_optim_opts) { return no_optim(ctx, "nc_sgd"); }
-nc_optim *nc_adam(nc_ctx *ctx, nc_tensor **, int, nc_optim_opts) { return no_optim(ctx, "nc_adam"); }
-nc_optim *nc_adamw(nc_ctx *ctx, nc_tensor **, int, nc_optim_opts) { return no_optim(ctx, "nc_adamw"); }
-nc_optim *nc_rmsprop(nc_ctx *ctx, nc_tensor **, int, nc_optim_opts, int) { return no_optim(ctx, "nc_rmsprop"); }
-void nc_optim_zero_grad(nc_optim *) {}
-void nc_optim_clear_grad(nc_optim *) {}
-void nc_optim_step(nc_optim *) {}
-void nc_optim_free(nc_optim *) {}
-void nc_optim_set_lr(nc_optim *, float) {}
-float *nc_optim_state(nc_optim *, int, int) { return nullptr; }
-int64_t nc_optim_get_step(const nc_optim *) { return 0; }
-void nc_optim_set_step(nc_optim *, int64_t) {}
-void nc_optim_set_opts(nc_optim *, nc_optim_opts) {}
-void nc_optim_set_accumulation(nc_optim *, int) {}
-float nc_clip_grad_norm(nc_tensor **params, int n, float) {
-    absent(n > 0 && params ? params[0] : nullptr, "nc_clip_grad_norm");
-    return 0.0f;
-}
 
 }  // extern "C"

@@ -1,0 +1,220 @@
+// Optimizer updates and the gradient norm (optim.c:161-233).
+//
+// k_optim<KIND, ...>: one streaming pass over a parameter: w, g and the state the optimizer keeps
+// read once, w and the state written once, 128-bit accesses (4 items in flight per lane) when every
+// array is 16-byte aligned, one float per lane for the rest.  Per element the reference's scalar
+// expression is evaluated in fp32, left to right, without fused multiply-adds (this file is compiled
+// with -ffp-contract=off), with correctly rounded division and square root: updates are
+// bit-identical to the reference's.  Constants the reference recomputes per element (1 - beta,
+// AdamW's 1 - lr * wd) are computed once on the host with the same fp32 operations.
+//
+// k_sumsq + k_sumsq_finish: fp64 sum of squares (each square exact in fp64), workgroup partials in
+// order and one ordered combine into a double that several tensors accumulate into.
+#include "common.hpp"
+
+#include <math.h>
+
+#include <algorithm>
+
+namespace nchip {
+
+constexpr int kOB = 256;
+constexpr int kOU = 4;
+
+struct OptArgs {
+    float lr, momentum, wd, b1, b2, eps, gs, bc1, bc2;
+    float one_m_b1, one_m_b2;  // 1 - beta1, 1 - beta2 (RMSprop: 1 - alpha)
+    float decay, l2;           // AdamW: w *= 1 - lr * wd; Adam: L2 term wd
+    int inside;                // RMSprop: sqrt(v + eps) instead of sqrt(v) + eps
+};
+
+enum { K_SGD = 0, K_ADAM = 1, K_RMS = 3 };
+
+template <int KIND, bool S1>
+__device__ __forceinline__ void opt1(float &w, float g, float &s1, float &s2, const OptArgs &a) {
+    if constexpr (KIND == K_SGD) {
+        float gj = a.gs * g + a.wd * w;
+        if constexpr (S1) {
+            s1 = a.momentum * s1 + gj;
+            gj = s1;
+        }
+        w = w - a.lr * gj;
+    } else if constexpr (KIND == K_RMS) {
+        const float gj = a.gs * g + a.wd * w;
+        s2 = a.b2 * s2 + a.one_m_b2 * gj * gj;
+        const float den = a.inside ? sqrtf(s2 + a.eps) : sqrtf(s2) + a.eps;
+        float step = gj / den;
+        if constexpr (S1) {
+            s1 = a.momentum * s1 + step;
+            step = s1;
+        }
+        w = w - a.lr * step;
+    } else {
+        w = w * a.decay;
+        const float gj = a.gs * g + a.l2 * w;
+        s1 = a.b1 * s1 + a.one_m_b1 * gj;
+        s2 = a.b2 * s2 + a.one_m_b2 * gj * gj;
+        w = w - a.lr * (s1 / a.bc1) / (sqrtf(s2 / a.bc2) + a.eps);
+    }
+}
+
+template <int KIND, bool S1, bool S2>
+__global__ __launch_bounds__(kOB) void k_optim4(f4 *__restrict__ w, const f4 *__restrict__ g, f4 *__restrict__ s1,
+                                                f4 *__restrict__ s2, int64_t n4, OptArgs a) {
+    const int64_t step = (int64_t)gridDim.x * kOB * kOU;
+    for (int64_t base = (int64_t)blockIdx.x * kOB * kOU + threadIdx.x; base < n4; base += step) {
+        f4 W[kOU], G[kOU], A[kOU], B[kOU];
+#pragma unroll
+        for (int u = 0; u < kOU; u++) {
+            const int64_t e = base + (int64_t)u * kOB;
+            if (e < n4) {
+                W[u] = w[e];
+                G[u] = __builtin_nontemporal_load(g + e);
+                A[u] = S1 ? s1[e] : f4{0.f, 0.f, 0.f, 0.f};
+                B[u] = S2 ? s2[e] : f4{0.f, 0.f, 0.f, 0.f};
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < kOU; u++) {
+            const int64_t e = base + (int64_t)u * kOB;
+            if (e < n4) {
+                float wv[4] = {W[u].x, W[u].y, W[u].z, W[u].w}, av[4] = {A[u].x, A[u].y, A[u].z, A[u].w},
+                      bv[4] = {B[u].x, B[u].y, B[u].z, B[u].w};
+                const float gv[4] = {G[u].x, G[u].y, G[u].z, G[u].w};
+#pragma unroll
+                for (int c = 0; c < 4; c++) opt1<KIND, S1>(wv[c], gv[c], av[c], bv[c], a);
+                w[e] = f4{wv[0], wv[1], wv[2], wv[3]};
+                if (S1) s1[e] = f4{av[0], av[1], av[2], av[3]};
+                if (S2) s2[e] = f4{bv[0], bv[1], bv[2], bv[3]};
+            }
+        }
+    }
+}
+
+template <int KIND, bool S1, bool S2>
+__global__ __launch_bounds__(kOB) void k_optim1(float *__restrict__ w, const float *__restrict__ g,
+                                                float *__restrict__ s1, float *__restrict__ s2, int64_t n, OptArgs a) {
+    for (int64_t e = (int64_t)blockIdx.x * kOB + threadIdx.x; e < n; e += (int64_t)gridDim.x * kOB) {
+        float W = w[e], A = S1 ? s1[e] : 0.0f, B = S2 ? s2[e] : 0.0f;
+        opt1<KIND, S1>(W, g[e], A, B, a);
+        w[e] = W;
+        if (S1) s1[e] = A;
+        if (S2) s2[e] = B;
+    }
+}
+
+template <int KIND, bool S1, bool S2>
+static void launch_opt(float *w, const float *g, float *s1, float *s2, int64_t n, const OptArgs &a, hipStream_t st) {
+    const bool vec = aligned16(w) && aligned16(g) && (!S1 || aligned16(s1)) && (!S2 || aligned16(s2));
+    const int64_t n4 = vec ? n / 4 : 0;
+    if (n4 > 0)
+        hipLaunchKernelGGL((k_optim4<KIND, S1, S2>), dim3(stream_grid((n4 + kOU - 1) / kOU, kOB)), dim3(kOB), 0, st,
+                           (f4 *)w, (const f4 *)g, (f4 *)s1, (f4 *)s2, n4, a);
+    const int64_t done = n4 * 4;
+    if (done < n)
+        hipLaunchKernelGGL((k_optim1<KIND, S1, S2>), dim3(stream_grid(n - done, kOB)), dim3(kOB), 0, st, w + done,
+                           g + done, S1 ? s1 + done : nullptr, S2 ? s2 + done : nullptr, n - done, a);
+}
+
+// sum of squares: fp64 per thread, workgroup partials in wave order, then an ordered combine
+__device__ __forceinline__ double block_sum_waves(double v) {
+    __shared__ double sh[kOB / kWave];
+    v = wave_sum(v);
+    if ((threadIdx.x & (kWave - 1)) == 0) sh[threadIdx.x / kWave] = v;
+    __syncthreads();
+    double t = 0.0;
+    if (threadIdx.x == 0)
+        for (int i = 0; i < kOB / kWave; i++) t += sh[i];
+    return t;
+}
+
+__global__ __launch_bounds__(kOB) void k_sumsq(const float *__restrict__ x, int64_t n, double *__restrict__ part) {
+    double acc = 0.0;
+    for (int64_t e = (int64_t)blockIdx.x * kOB + threadIdx.x; e < n; e += (int64_t)gridDim.x * kOB) {
+        const double v = (double)x[e];
+        acc += v * v;
+    }
+    const double t = block_sum_waves(acc);
+    if (threadIdx.x == 0) part[blockIdx.x] = t;
+}
+
+__global__ __launch_bounds__(kOB) void k_sumsq_finish(const double *__restrict__ part, int nparts, double *ss,
+                                                      int accumulate) {
+    double t = 0.0;
+    for (int i = threadIdx.x; i < nparts; i += kOB) t += part[i];
+    const double s = block_sum_waves(t);
+    if (threadIdx.x == 0) *ss = (accumulate ? *ss : 0.0) + s;
+}
+
+static unsigned sumsq_grid(int64_t n) {
+    const int64_t blocks = (n + kOB - 1) / kOB, cap = (int64_t)num_cus() * 8;
+    return (unsigned)std::max<int64_t>(1, std::min(blocks, cap));
+}
+
+}  // namespace nchip
+
+using namespace nchip;
+
+extern "C" NC_HIP_API int nc_hip_optim_step(int kind, int64_t n, float *w, const float *g, float *s1, float *s2,
+                                            float lr, float momentum, float weight_decay, float beta1, float beta2,
+                                            float eps, float gs, float bc1, float bc2, int eps_inside_sqrt,
+                                            void *stream) {
+    if (n < 0) return set_error(NC_HIP_ERR_ARG, "nc_hip_optim_step: negative size");
+    if (n == 0) return NC_HIP_OK;
+    if (!w || !g) return set_error(NC_HIP_ERR_ARG, "nc_hip_optim_step: NULL parameter or gradient");
+    OptArgs a{};
+    a.lr = lr;
+    a.momentum = momentum;
+    a.wd = weight_decay;
+    a.b1 = beta1;
+    a.b2 = beta2;
+    a.eps = eps;
+    a.gs = gs;
+    a.bc1 = bc1;
+    a.bc2 = bc2;
+    a.one_m_b1 = 1.0f - beta1;
+    a.one_m_b2 = 1.0f - beta2;
+    a.inside = eps_inside_sqrt ? 1 : 0;
+    hipStream_t st = as_stream(stream);
+    switch (kind) {
+    case NC_HIP_OPT_SGD:
+        if (s1) launch_opt<K_SGD, true, false>(w, g, s1, nullptr, n, a, st);
+        else launch_opt<K_SGD, false, false>(w, g, nullptr, nullptr, n, a, st);
+        break;
+    case NC_HIP_OPT_ADAM:
+    case NC_HIP_OPT_ADAMW:
+        if (!s1 || !s2) return set_error(NC_HIP_ERR_ARG, "nc_hip_optim_step: Adam needs both state buffers");
+        a.l2 = kind == NC_HIP_OPT_ADAM ? weight_decay : 0.0f;
+        a.decay = kind == NC_HIP_OPT_ADAMW ? 1.0f - lr * weight_decay : 1.0f;
+        launch_opt<K_ADAM, true, true>(w, g, s1, s2, n, a, st);
+        break;
+    case NC_HIP_OPT_RMSPROP:
+        if (!s2) return set_error(NC_HIP_ERR_ARG, "nc_hip_optim_step: RMSprop needs its square average");
+        if (s1) launch_opt<K_RMS, true, true>(w, g, s1, s2, n, a, st);
+        else launch_opt<K_RMS, false, true>(w, g, nullptr, s2, n, a, st);
+        break;
+    default: return set_error(NC_HIP_ERR_ARG, "nc_hip_optim_step: unknown optimizer %d", kind);
+    }
+    return check_launch("nc_hip_optim_step");
+}
+
+extern "C" NC_HIP_API size_t nc_hip_sumsq_workspace(int64_t n) {
+    return n > 0 ? (size_t)sumsq_grid(n) * sizeof(double) : 0;
+}
+
+extern "C" NC_HIP_API int nc_hip_sumsq(int64_t n, const float *x, double *ss, int accumulate, void *ws,
+                                       size_t ws_bytes, void *stream) {
+    if (n < 0 || !ss) return set_error(NC_HIP_ERR_ARG, "nc_hip_sumsq: bad arguments");
+    hipStream_t st = as_stream(stream);
+    int nparts = 0;
+    if (n > 0) {
+        if (!x || !ws || ws_bytes < nc_hip_sumsq_workspace(n))
+            return set_error(NC_HIP_ERR_WORKSPACE, "nc_hip_sumsq: workspace of %zu bytes needed",
+                             nc_hip_sumsq_workspace(n));
+        const unsigned grid = sumsq_grid(n);
+        hipLaunchKernelGGL(k_sumsq, grid, kOB, 0, st, x, n, (double *)ws);
+        nparts = (int)grid;
+    }
+    hipLaunchKernelGGL(k_sumsq_finish, 1, kOB, 0, st, (const double *)ws, nparts, ss, accumulate ? 1 : 0);
+    return check_launch("nc_hip_sumsq");
+}

@@ -19,6 +19,7 @@ UN = {"relu": 0, "leaky_relu": 1, "relu6": 2, "hardsigmoid": 3, "hardswish": 4, 
       "sqrt": 15, "pow": 16}
 BIN = {"add": 0, "sub": 1, "mul": 2, "div": 3}
 RED = {"sum": 0, "mean": 1, "max": 2, "argmax": 3}
+OPT = {"sgd": 0, "adam": 1, "adamw": 2, "rmsprop": 3}
 # which tensor an activation's backward reads besides g
 BWD_READS_Y = {"sigmoid", "tanh", "exp", "sqrt"}
 BWD_READS_NONE = {"neg", "scale", "add_scalar"}
@@ -55,6 +56,10 @@ SIGNATURES = {
     "nc_hip_layer_norm_bwd": (c_int, [c_int64, c_int64, P, P, P, P, P, P, P, c_int, P, c_size_t, P]),
     "nc_hip_quantize_rows": (c_int, [c_int64, c_int64, P, P, P, P]),
     "nc_hip_dequantize_rows": (c_int, [c_int64, c_int64, P, P, P, P]),
+    "nc_hip_optim_step": (c_int, [c_int, c_int64, P, P, P, P, c_float, c_float, c_float, c_float, c_float, c_float,
+                                  c_float, c_float, c_float, c_int, P]),
+    "nc_hip_sumsq_workspace": (c_size_t, [c_int64]),
+    "nc_hip_sumsq": (c_int, [c_int64, P, P, c_int, P, c_size_t, P]),
     "nc_hip_loss_workspace": (c_size_t, [c_int64, c_int64]),
     "nc_hip_cross_entropy_fwd": (c_int, [c_int64, c_int64, P, P, P, P, P, P, c_size_t, P]),
     "nc_hip_cross_entropy_bwd": (c_int, [c_int64, c_int64, P, P, P, P, c_int, P]),
@@ -153,6 +158,17 @@ class Kernels:
 
     def quantize_rows(self, rows, cols, w, q, scale, stream=None):
         self._ok(self.lib.nc_hip_quantize_rows(rows, cols, w, q, scale, stream), "quantize_rows")
+
+    def optim_step(self, kind, n, w, g, s1, s2, lr, momentum=0.0, weight_decay=0.0, beta1=0.0, beta2=0.0, eps=0.0,
+                   gs=1.0, bc1=1.0, bc2=1.0, eps_inside_sqrt=False, stream=None):
+        self._ok(self.lib.nc_hip_optim_step(OPT[kind], n, w, g, s1, s2, lr, momentum, weight_decay, beta1, beta2, eps,
+                                            gs, bc1, bc2, int(eps_inside_sqrt), stream), "optim_step")
+
+    def sumsq_workspace(self, n):
+        return self.lib.nc_hip_sumsq_workspace(n)
+
+    def sumsq(self, n, x, ss, accumulate, ws, ws_bytes, stream=None):
+        self._ok(self.lib.nc_hip_sumsq(n, x, ss, int(accumulate), ws, ws_bytes, stream), "sumsq")
 
     def loss_workspace(self, N, C):
         return self.lib.nc_hip_loss_workspace(N, C)

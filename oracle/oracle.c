@@ -604,3 +604,44 @@ void or_nll_loss_bwd(int64_t N, int64_t C, const int32_t *lab, float gout, int s
     const float s = sum ? gout : gout / (float)(N ? N : 1);
     for (int64_t i = 0; i < N; i++) gi[i * C + lab[i]] = gi[i * C + lab[i]] - s;
 }
+
+/* ---------------------------------------------------------------------------------------------- */
+/* optimizers: optim.c:161-216 (scalar glue: fp32, left to right, no contraction); clip: :219-233  */
+/* ---------------------------------------------------------------------------------------------- */
+void or_optim_step(int kind, int64_t n, float *w, const float *g, float *s1, float *s2, float lr, float momentum,
+                   float weight_decay, float beta1, float beta2, float eps, float gs, float bc1, float bc2,
+                   int eps_inside_sqrt) {
+    if (kind == OR_OPT_SGD) {
+        for (int64_t j = 0; j < n; j++) {
+            float gj = gs * g[j] + weight_decay * w[j];
+            if (s1) gj = s1[j] = momentum * s1[j] + gj;
+            w[j] -= lr * gj;
+        }
+    } else if (kind == OR_OPT_RMSPROP) {
+        const float a = beta2;
+        for (int64_t j = 0; j < n; j++) {
+            float gj = gs * g[j] + weight_decay * w[j];
+            s2[j] = a * s2[j] + (1.0f - a) * gj * gj;
+            float den = eps_inside_sqrt ? sqrtf(s2[j] + eps) : sqrtf(s2[j]) + eps;
+            float step = gj / den;
+            if (s1) step = s1[j] = momentum * s1[j] + step;
+            w[j] -= lr * step;
+        }
+    } else {
+        const float l2 = kind == OR_OPT_ADAM ? weight_decay : 0.0f;
+        const float decay = kind == OR_OPT_ADAMW ? 1.0f - lr * weight_decay : 1.0f;
+        for (int64_t j = 0; j < n; j++) {
+            w[j] *= decay;
+            float gj = gs * g[j] + l2 * w[j];
+            s1[j] = beta1 * s1[j] + (1.0f - beta1) * gj;
+            s2[j] = beta2 * s2[j] + (1.0f - beta2) * gj * gj;
+            w[j] -= lr * (s1[j] / bc1) / (sqrtf(s2[j] / bc2) + eps);
+        }
+    }
+}
+
+double or_sumsq(int64_t n, const float *x) {
+    double ss = 0.0;
+    for (int64_t j = 0; j < n; j++) ss += (double)x[j] * x[j];
+    return ss;
+}

@@ -85,6 +85,17 @@ void or_cross_entropy_bwd(int64_t N, int64_t C, const float *prob, const int32_t
 int64_t or_nll_loss_fwd(int64_t N, int64_t C, const float *x, const int32_t *lab, int sum, float *loss);
 void or_nll_loss_bwd(int64_t N, int64_t C, const int32_t *lab, float gout, int sum, float *gi);
 
+/* One optimizer update of one parameter (optim.c:161-216), the reference's fp32 expressions in its
+ * order without fused multiply-adds.  kind: 0 SGD, 1 Adam, 2 AdamW, 3 RMSprop (OR_OPT_*); s1 / s2
+ * may be NULL when that state does not exist; gs = 1 / accumulation steps; bc1 / bc2 = Adam's
+ * 1 - beta^t. */
+enum { OR_OPT_SGD = 0, OR_OPT_ADAM = 1, OR_OPT_ADAMW = 2, OR_OPT_RMSPROP = 3 };
+void or_optim_step(int kind, int64_t n, float *w, const float *g, float *s1, float *s2, float lr, float momentum,
+                   float weight_decay, float beta1, float beta2, float eps, float gs, float bc1, float bc2,
+                   int eps_inside_sqrt);
+/* sum of squares in double, as clip_grad_norm accumulates it (optim.c:219-225) */
+double or_sumsq(int64_t n, const float *x);
+
 #ifdef __cplusplus
 }
 #endif

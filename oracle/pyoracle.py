@@ -268,3 +268,100 @@ def nll_loss_bwd(shape, lab, gout, sum=False, gi=None):
     gi = np.zeros((N, C), np.float32) if gi is None else _f32(gi).copy()
     lib().or_nll_loss_bwd(c_int64(N), c_int64(C), _p(lab), c_float(gout), c_int(int(sum)), _p(gi))
     return gi
+
+
+OPT = {"sgd": 0, "adam": 1, "adamw": 2, "rmsprop": 3}
+
+
+def optim_step(kind, w, g, s1, s2, lr, momentum=0.0, weight_decay=0.0, beta1=0.0, beta2=0.0, eps=0.0, gs=1.0,
+               bc1=1.0, bc2=1.0, eps_inside_sqrt=False):
+    """One update in place on float32 arrays w, s1, s2 (s1 / s2 may be None); returns (w, s1, s2)."""
+    from ctypes import c_double  # noqa: F401
+    for a in (w, s1, s2):
+        assert a is None or (a.dtype == np.float32 and a.flags.c_contiguous)
+    g = _f32(g)
+    lib().or_optim_step(c_int(OPT[kind]), c_int64(w.size), _p(w), _p(g), _p(s1), _p(s2), c_float(lr),
+                        c_float(momentum), c_float(weight_decay), c_float(beta1), c_float(beta2), c_float(eps),
+                        c_float(gs), c_float(bc1), c_float(bc2), c_int(int(eps_inside_sqrt)))
+    return w, s1, s2
+
+
+def sumsq(x):
+    from ctypes import c_double
+    L = lib()
+    L.or_sumsq.restype = c_double
+    x = _f32(x)
+    return L.or_sumsq(c_int64(x.size), _p(x))
+
+
+_libm = None
+
+
+def powf(x, y):
+    """glibc powf, as the reference computes Adam's bias corrections (optim.c:167-168)."""
+    global _libm
+    if _libm is None:
+        _libm = ctypes.CDLL("libm.so.6")
+        _libm.powf.restype = c_float
+        _libm.powf.argtypes = [c_float, c_float]
+    return np.float32(_libm.powf(float(x), float(y)))
+
+
+def optim_defaults(ctor, opts, inside=None):
+    """The constructors' defaults for zero hyperparameters (optim.c:101-124)."""
+    lr, mom, wd, b1, b2, eps = (np.float32(v) for v in opts)
+    if ctor in ("nc_adam", "nc_adamw"):
+        b1 = b1 or np.float32(0.9)
+        b2 = b2 or np.float32(0.999)
+        eps = eps or np.float32(1e-8)
+    elif ctor == "nc_rmsprop":
+        b2 = b2 or np.float32(0.99)
+        eps = eps or np.float32(1e-8)
+    return lr, mom, wd, b1, b2, eps
+
+
+def optim_replay(cfg, W, Gs):
+    """The optimizer scenario of tests/golden/gen_golden.py on the oracle: per step, grads accumulate
+    (zero_grad is skipped mid-accumulation), every accum-th call updates.  Returns the same keys."""
+    name, ctor, opts, inside, accum, steps = cfg
+    kind = {"nc_sgd": "sgd", "nc_adam": "adam", "nc_adamw": "adamw", "nc_rmsprop": "rmsprop"}[ctor]
+    lr, mom, wd, b1, b2, eps = optim_defaults(ctor, opts, inside)
+    w = [np.array(x, np.float32, copy=True) for x in W]
+    adam = kind in ("adam", "adamw")
+    s1 = [np.zeros_like(x) for x in w] if (adam or mom != 0) else [None] * len(w)
+    s2 = [np.zeros_like(x) for x in w] if (adam or kind == "rmsprop") else [None] * len(w)
+    grads = [np.zeros_like(x) for x in w]
+    t, count, out = 0, 0, {}
+    for k in range(steps):
+        if count == 0:
+            grads = [np.zeros_like(x) for x in w]
+        grads = [g + np.asarray(G, np.float32) for g, G in zip(grads, Gs[k])]  # fp32 accumulation
+        count += 1
+        if not (accum > 1 and count < accum):
+            count = 0
+            t += 1
+            gs = np.float32(1.0) / np.float32(accum)
+            bc1 = np.float32(1.0) - powf(b1, np.float32(t)) if adam else np.float32(1.0)
+            bc2 = np.float32(1.0) - powf(b2, np.float32(t)) if adam else np.float32(1.0)
+            for i in range(len(w)):
+                optim_step(kind, w[i], grads[i], s1[i], s2[i], lr, mom, wd, b1, b2, eps, gs, bc1, bc2,
+                           bool(inside))
+        for i in range(len(w)):
+            out[f"{name}/step{k}/w{i}"] = w[i].copy()
+            for slot, s in ((0, s1[i]), (1, s2[i])):
+                if s is not None:
+                    out[f"{name}/step{k}/s{slot}_{i}"] = s.copy()
+    out[f"{name}/t"] = np.int64(t)
+    return out
+
+
+def clip_grad_norm(grads, max_norm):
+    """(total, scaled grads) as nc_clip_grad_norm (optim.c:219-233): fp64 sum of squares in order."""
+    ss = 0.0
+    for g in grads:
+        ss += sumsq(g)
+    total = np.float32(np.sqrt(ss))
+    coef = np.float32(max_norm) / (total + np.float32(1e-6))
+    if coef < np.float32(1.0):
+        grads = [(np.asarray(g, np.float32) * coef).astype(np.float32) for g in grads]
+    return total, grads

@@ -387,7 +387,95 @@ def gen_loss(ref, rng):
     np.savez_compressed(OUT / "loss.npz", **res)
 
 
-GENERATORS = ["transcendentals", "unary", "binary", "reduce", "softmax", "layer_norm", "quant", "chain", "loss"]
+OPTIM_CONFIGS = [
+    # name, constructor, opts (lr, momentum, weight_decay, beta1, beta2, eps), rmsprop eps_inside_sqrt,
+    # accumulation steps, micro-steps
+    ("sgd", "nc_sgd", (0.1, 0, 0, 0, 0, 0), None, 1, 3),
+    ("sgd_mom_wd", "nc_sgd", (0.05, 0.9, 0.01, 0, 0, 0), None, 1, 3),
+    ("adam", "nc_adam", (0.01, 0, 0.01, 0, 0, 0), None, 1, 3),
+    ("adamw", "nc_adamw", (0.01, 0, 0.1, 0.8, 0.99, 1e-6), None, 1, 3),
+    ("rmsprop", "nc_rmsprop", (0.01, 0, 0, 0, 0, 0), 0, 1, 3),
+    ("rmsprop_keras_mom", "nc_rmsprop", (0.01, 0.5, 0.001, 0, 0.9, 1e-7), 1, 1, 3),
+    ("adam_accum2", "nc_adam", (0.01, 0, 0, 0, 0, 0), None, 2, 4),
+]
+OPTIM_SHAPES = [(7,), (3, 5)]
+
+
+def optim_scenario(e, lib, cfg, W, Gs):
+    """Runs one optimizer configuration on params initialised to W with upstream grads Gs[step][param]
+    (loss = sum_i sum(p_i * G_i), so each step's grads are exactly G); returns per-step weights and
+    state.  `e` is any context wrapper with tensor / param / read (the reference's or this build's)."""
+    name, ctor, opts, inside, accum, steps = cfg
+    params = [e.param(w) for w in W]
+    arr = (ctypes.c_void_p * len(params))(*params)
+    o_opts = abi.OptimOpts(*[float(v) for v in opts])
+    o = getattr(lib, ctor)(e.ctx, arr, len(params), o_opts) if inside is None else \
+        lib.nc_rmsprop(e.ctx, arr, len(params), o_opts, inside)
+    assert o, lib.nc_error(e.ctx)
+    if accum > 1:
+        lib.nc_optim_set_accumulation(o, accum)
+    out = {}
+    for k in range(steps):
+        lib.nc_optim_zero_grad(o)
+        loss = None
+        for p, G in zip(params, Gs[k]):
+            term = lib.nc_sum(lib.nc_mul(p, e.tensor(G)), abi.ALL_AXES, 0)
+            loss = term if loss is None else lib.nc_add(loss, term)
+        assert lib.nc_backward_ex(loss, 0, None, 0) == 0, lib.nc_error(e.ctx)
+        lib.nc_optim_step(o)
+        for i, p in enumerate(params):
+            out[f"{name}/step{k}/w{i}"] = e.read(p)
+            for slot in (0, 1):
+                ptr = lib.nc_optim_state(o, i, slot)
+                if ptr:
+                    n = W[i].size
+                    out[f"{name}/step{k}/s{slot}_{i}"] = np.ctypeslib.as_array(
+                        (ctypes.c_float * n).from_address(ptr)).reshape(W[i].shape).copy()
+        e.step_end()
+    out[f"{name}/t"] = np.int64(lib.nc_optim_get_step(o))
+    lib.nc_optim_free(o)
+    return out
+
+
+def gen_optim(ref, rng):
+    """Every optimizer kind through the reference's nc.h, a few steps each, plus clip_grad_norm."""
+    res = {}
+    lib = ref.lib
+    for cfg in OPTIM_CONFIGS:
+        name, steps = cfg[0], cfg[5]
+        W = [rng.standard_normal(sh).astype(np.float32) for sh in OPTIM_SHAPES]
+        Gs = [[rng.standard_normal(sh).astype(np.float32) for sh in OPTIM_SHAPES] for _ in range(steps)]
+        for i, w in enumerate(W):
+            res[f"{name}/w_init{i}"] = w
+        for k in range(steps):
+            for i, G in enumerate(Gs[k]):
+                res[f"{name}/G{k}_{i}"] = G
+        res.update(optim_scenario(ref, lib, cfg, W, Gs))
+    # clip_grad_norm: one case that clips, one that does not
+    for case, factor in (("clip", 0.5), ("noclip", 10.0)):
+        W = [rng.standard_normal(sh).astype(np.float32) for sh in OPTIM_SHAPES]
+        G = [rng.standard_normal(sh).astype(np.float32) * 3 for sh in OPTIM_SHAPES]
+        params = [ref.param(w) for w in W]
+        loss = None
+        for p, g in zip(params, G):
+            term = lib.nc_sum(lib.nc_mul(p, ref.tensor(g)), abi.ALL_AXES, 0)
+            loss = term if loss is None else lib.nc_add(loss, term)
+        assert lib.nc_backward_ex(loss, 0, None, 0) == 0
+        norm = float(np.sqrt(sum((g.astype(np.float64) ** 2).sum() for g in G)))
+        max_norm = np.float32(norm * factor)
+        arr = (ctypes.c_void_p * len(params))(*params)
+        total = lib.nc_clip_grad_norm(arr, len(params), max_norm)
+        res[f"{case}/max_norm"] = max_norm
+        res[f"{case}/total"] = np.float32(total)
+        for i in range(len(params)):
+            res[f"{case}/G{i}"] = G[i]
+            res[f"{case}/g{i}"] = ref.grad(params[i])
+        ref.step_end()
+    np.savez_compressed(OUT / "optim.npz", **res)
+
+
+GENERATORS = ["transcendentals", "unary", "binary", "reduce", "softmax", "layer_norm", "quant", "chain", "loss",
+              "optim"]
 
 
 def main():
@@ -412,11 +500,13 @@ def main():
         gen_chain(ref, rng)
     if "loss" in only:
         gen_loss(ref, np.random.default_rng(20261202))
+    if "optim" in only:
+        gen_optim(ref, np.random.default_rng(20261203))
     (OUT / "PROVENANCE.txt").write_text(
         "Written by tests/golden/gen_golden.py from oracle/_ref/libnc_ref.so, which oracle/Makefile builds\n"
         "from the reference engine sources (engine/src/**/*.c) with gcc 11.4, -O2 -std=gnu11, x86-64\n"
         f"baseline + AVX2/FMA target functions; kernel tier: {backend}; numpy seeds 20261201 (one stream\n"
-        "for transcendentals .. chain, in that order) and 20261202 (loss).\n")
+        "for transcendentals .. chain, in that order), 20261202 (loss) and 20261203 (optim).\n")
     for f in sorted(OUT.glob("*.npz")):
         print(f"{f.name}: {f.stat().st_size / 1024:.0f} KiB")
 

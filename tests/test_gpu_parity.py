@@ -928,6 +928,157 @@ def test_kernel_loss_bad_labels(K):
     assert BAD.to_numpy(np.uint64, 1)[0] == want
 
 
+# ------------------------------------------------------------------------------------------------
+# optimizers and gradient clipping
+# ------------------------------------------------------------------------------------------------
+def _optim_configs():
+    from tests.golden.gen_golden import OPTIM_CONFIGS
+    return OPTIM_CONFIGS
+
+
+@pytest.mark.parametrize("cfg", _optim_configs(), ids=[c[0] for c in _optim_configs()])
+def test_engine_optim_golden(eng, cfg):
+    """Every optimizer kind through nc.h, step by step against the reference's weights and state,
+    bit for bit (the state read back through nc_optim_state)."""
+    from tests.golden.gen_golden import optim_scenario
+    d = load("optim")
+    name, steps = cfg[0], cfg[5]
+    W = [d[f"{name}/w_init{i}"] for i in range(2)]
+    Gs = [[d[f"{name}/G{k}_{i}"] for i in range(2)] for k in range(steps)]
+    got = optim_scenario(eng, eng.lib, cfg, W, Gs)
+    for k, v in got.items():
+        assert_bits(v, d[k], k)
+
+
+@pytest.mark.parametrize("case", ["clip", "noclip"])
+def test_engine_clip_grad_norm_golden(eng, case):
+    d = load("optim")
+    L = eng.lib
+    params = [eng.param(np.zeros_like(d[f"{case}/G{i}"])) for i in range(2)]
+    loss = None
+    for i, p in enumerate(params):
+        term = L.nc_sum(L.nc_mul(p, eng.tensor(d[f"{case}/G{i}"])), abi.ALL_AXES, 0)
+        loss = term if loss is None else L.nc_add(loss, term)
+    assert L.nc_backward_ex(loss, 0, None, 0) == 0
+    arr = (c_void_p * 2)(*params)
+    total = np.float32(L.nc_clip_grad_norm(arr, 2, c_float(float(d[f"{case}/max_norm"]))))
+    want = d[f"{case}/total"]
+    assert abs(float(total) - float(want)) <= 1e-6 * float(want), (total, want)
+    coef = np.float32(d[f"{case}/max_norm"]) / (total + np.float32(1e-6))
+    for i, p in enumerate(params):
+        G = d[f"{case}/G{i}"]
+        exp = (G * coef).astype(np.float32) if coef < 1 else G
+        assert_bits(eng.grad(p), exp, f"grad {i}")
+        if total == want:
+            assert_bits(eng.grad(p), d[f"{case}/g{i}"], f"grad {i} vs reference")
+    eng.step_end()
+
+
+def test_engine_optim_state_roundtrip(eng):
+    """nc_optim_state's host copy is authoritative until the next step: a value written there is
+    what the step uses (checkpoint restore)."""
+    L = eng.lib
+    w0 = np.array([1.0, -2.0, 3.0, 0.5], np.float32)
+    p = eng.param(w0)
+    arr = (c_void_p * 1)(p)
+    o = L.nc_sgd(eng.ctx, arr, 1, abi.OptimOpts(0.1, 0.9, 0, 0, 0, 0))
+    assert o
+    ptr = L.nc_optim_state(o, 0, 0)
+    buf = np.ctypeslib.as_array((ctypes.c_float * 4).from_address(ptr))
+    assert (buf == 0).all()
+    buf[:] = [1.0, 1.0, 1.0, 1.0]  # restore a momentum buffer
+    G = np.array([0.5, 0.5, 0.5, 0.5], np.float32)
+    L.nc_optim_zero_grad(o)
+    assert L.nc_backward_ex(L.nc_sum(L.nc_mul(p, eng.tensor(G)), abi.ALL_AXES, 0), 0, None, 0) == 0
+    L.nc_optim_step(o)
+    v = np.float32(0.9) * np.float32(1.0) + G
+    assert_bits(eng.read(p), (w0 - np.float32(0.1) * v).astype(np.float32), "weights")
+    buf2 = np.ctypeslib.as_array((ctypes.c_float * 4).from_address(L.nc_optim_state(o, 0, 0)))
+    assert_bits(buf2.copy(), v.astype(np.float32), "momentum")
+    assert L.nc_optim_state(o, 0, 1) is None and L.nc_optim_get_step(o) == 1
+    L.nc_optim_free(o)
+    eng.step_end()
+
+
+def test_engine_optim_errors_match_reference(eng):
+    if not O.REF_LIB.exists():
+        pytest.skip("oracle/_ref/libnc_ref.so not built")
+
+    def calls(e):
+        L = e.lib
+        p = e.param(np.ones(3, np.float32))
+        arr = (c_void_p * 1)(p)
+        out = []
+        o = L.nc_sgd(e.ctx, arr, 1, abi.OptimOpts(0.1, 0.0, 0, 0, 0, 0))
+        for fn in (lambda: L.nc_optim_set_accumulation(o, 0), lambda: L.nc_optim_set_step(o, -2),
+                   lambda: L.nc_optim_set_opts(o, abi.OptimOpts(0.1, 0.5, 0, 0, 0, 0))):
+            fn()
+            out.append((L.nc_status_code(e.ctx), L.nc_error(e.ctx).decode()))
+            L.nc_clear_error(e.ctx)
+        L.nc_optim_free(o)
+        e.step_end()
+        return out
+    with Engine(O.REF_LIB) as ref:
+        want = calls(ref)
+    assert calls(eng) == want
+
+
+OPT_KERNEL_CASES = [("sgd", False, False), ("sgd", True, False), ("adam", True, True), ("adamw", True, True),
+                    ("rmsprop", False, True), ("rmsprop", True, True)]
+
+
+@pytest.mark.parametrize("kind,s1,s2", OPT_KERNEL_CASES)
+@pytest.mark.parametrize("n,offset", [(1_000_003, 0), (4097, 1)])
+@pytest.mark.parametrize("inside", [False, True])
+def test_kernel_optim_step(K, kind, s1, s2, n, offset, inside):
+    """Three updates at a large and a misaligned size, bit for bit against the oracle."""
+    if inside and kind != "rmsprop":
+        pytest.skip("eps_inside_sqrt is RMSprop's")
+    rng = np.random.default_rng(zlib.crc32(f"opt/{kind}/{s1}/{s2}/{n}".encode()))
+    w = rng.standard_normal(n).astype(np.float32)
+    m = np.zeros(n, np.float32) if s1 else None
+    v = np.zeros(n, np.float32) if s2 else None
+    pad = 4 * offset
+    Wd = dev(w, pad)
+    M = dev(m, pad) if s1 else None
+    V = dev(v, pad) if s2 else None
+    hp = dict(lr=np.float32(0.01), momentum=np.float32(0.9 if s1 and kind != "adam" and kind != "adamw" else 0.0),
+              weight_decay=np.float32(0.01), beta1=np.float32(0.9), beta2=np.float32(0.999 if "adam" in kind else 0.99),
+              eps=np.float32(1e-8), gs=np.float32(0.5))
+    for t in range(1, 4):
+        g = (rng.standard_normal(n) * (10.0 ** rng.integers(-3, 3, n))).astype(np.float32)
+        Gd = dev(g, pad)
+        adam = kind in ("adam", "adamw")
+        bc1 = np.float32(1) - O.powf(hp["beta1"], t) if adam else np.float32(1)
+        bc2 = np.float32(1) - O.powf(hp["beta2"], t) if adam else np.float32(1)
+        K.optim_step(kind, n, Wd.ptr + pad, Gd.ptr + pad, M.ptr + pad if s1 else None, V.ptr + pad if s2 else None,
+                     bc1=bc1, bc2=bc2, eps_inside_sqrt=inside, **hp)
+        O.optim_step(kind, w, g, m, v, bc1=bc1, bc2=bc2, eps_inside_sqrt=inside, **hp)
+    sync()
+    assert_bits(Wd.to_numpy(np.float32, n, pad), w, f"{kind} w")
+    if s1:
+        assert_bits(M.to_numpy(np.float32, n, pad), m, f"{kind} s1")
+    if s2:
+        assert_bits(V.to_numpy(np.float32, n, pad), v, f"{kind} s2")
+
+
+@pytest.mark.parametrize("sizes", [(1_000_003, 7, 65536), (0, 5), (1 << 22,)])
+def test_kernel_sumsq(K, sizes):
+    rng = np.random.default_rng(len(sizes))
+    xs = [(rng.standard_normal(n) * 3).astype(np.float32) for n in sizes]
+    SS = dev(np.array([123.0], np.float64))
+    for i, x in enumerate(xs):
+        X = dev(x)
+        wsb = K.sumsq_workspace(x.size)
+        ws = empty(max(wsb, 8))
+        K.sumsq(x.size, X.ptr, SS.ptr, i > 0, ws.ptr, wsb)
+    sync()
+    got = SS.to_numpy(np.float64, 1)[0]
+    want = sum(O.sumsq(x) for x in xs)
+    exact = sum(float(np.sum(x.astype(np.float64) ** 2)) for x in xs)
+    assert abs(got - want) <= 1e-12 * max(want, 1.0) and abs(got - exact) <= 1e-12 * max(exact, 1.0)
+
+
 @pytest.mark.parametrize("rows,cols", [(512, 4096), (96, 70), (64, 8192), (33, 10000), (8, 16)])
 def test_kernel_quantize(K, rows, cols):
     rng = np.random.default_rng(rows * cols)

@@ -112,8 +112,30 @@ def test_off_path_ops_report_not_in_this_build(eng):
     assert not L.nc_matmul(a, a)
     assert L.nc_status_code(eng.ctx) == abi.ERR_STATE and b"not in this build" in L.nc_error(eng.ctx)
     L.nc_clear_error(eng.ctx)
-    assert not L.nc_sgd(eng.ctx, None, 0, abi.OptimOpts())
+    assert not L.nc_conv2d(a, a, None, 1, 1, 0, 0)
     assert b"not in this build" in L.nc_error(eng.ctx)
+
+
+def test_optimizer_argument_errors_match_reference(eng):
+    """Parameter validation happens before any device work: same status and message as the reference."""
+    def calls(e):
+        L = e.lib
+        t = e.tensor(np.ones(3, np.float32))            # not a parameter
+        p = e.param(np.ones((2, 2), np.float32))
+        pt = L.nc_transpose(p, 0, 1)                    # not contiguous (and not persistent)
+        out = []
+        for params in ([t], [p, t], [pt]):
+            arr = (ctypes.c_void_p * len(params))(*params)
+            o = L.nc_adam(e.ctx, arr, len(params), abi.OptimOpts(0.1, 0, 0, 0, 0, 0))
+            out.append((bool(o), L.nc_status_code(e.ctx), L.nc_error(e.ctx).decode()))
+            L.nc_clear_error(e.ctx)
+        e.step_end()
+        return out
+    if not O.REF_LIB.exists():
+        pytest.skip("oracle/_ref/libnc_ref.so not built")
+    with Engine(O.REF_LIB) as ref:
+        want = calls(ref)
+    assert calls(eng) == want
 
 
 ref_only = pytest.mark.skipif(not O.REF_LIB.exists(), reason="oracle/_ref/libnc_ref.so not built")

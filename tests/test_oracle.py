@@ -215,6 +215,32 @@ def test_loss_bad_label_golden(which):
         assert msg.endswith(str(e.value)), (msg, str(e.value))
 
 
+def optim_configs():
+    from tests.golden.gen_golden import OPTIM_CONFIGS
+    return OPTIM_CONFIGS
+
+
+@pytest.mark.parametrize("cfg", optim_configs(), ids=[c[0] for c in optim_configs()])
+def test_optim_golden(cfg):
+    d = load("optim")
+    name, steps = cfg[0], cfg[5]
+    W = [d[f"{name}/w_init{i}"] for i in range(2)]
+    Gs = [[d[f"{name}/G{k}_{i}"] for i in range(2)] for k in range(steps)]
+    got = O.optim_replay(cfg, W, Gs)
+    assert set(got) == {k for k in d.files if k.startswith(name + "/") and "/step" in k or k == f"{name}/t"}
+    for k, v in got.items():
+        assert_bits(v, d[k], k)
+
+
+@pytest.mark.parametrize("case", ["clip", "noclip"])
+def test_clip_grad_norm_golden(case):
+    d = load("optim")
+    total, g = O.clip_grad_norm([d[f"{case}/G{i}"] for i in range(2)], d[f"{case}/max_norm"])
+    assert_bits(total, d[f"{case}/total"], "total")
+    for i in range(2):
+        assert_bits(g[i], d[f"{case}/g{i}"], f"grad {i}")
+
+
 # ------------------------------------------------------------------------------------------------
 # the live reference (only where oracle/_ref was built: this container, or a box it travelled to)
 # ------------------------------------------------------------------------------------------------
@@ -279,6 +305,35 @@ def test_loss_vs_live_reference(N, C):
 # ------------------------------------------------------------------------------------------------
 # closed forms, invariants and the reference's own known answers
 # ------------------------------------------------------------------------------------------------
+def test_optim_closed_forms():
+    rng = np.random.default_rng(4)
+    w0 = rng.standard_normal(1000).astype(np.float32)
+    g = rng.standard_normal(1000).astype(np.float32)
+    # plain SGD: w - lr * g in fp32
+    w, _, _ = O.optim_step("sgd", w0.copy(), g, None, None, lr=0.1)
+    assert_bits(w, (w0 - np.float32(0.1) * g).astype(np.float32), "sgd")
+    # Adam's first step moves each weight by ~lr in the direction of -g (bias-corrected m / sqrt(v) = sign)
+    m, v = np.zeros_like(w0), np.zeros_like(w0)
+    b1, b2 = np.float32(0.9), np.float32(0.999)
+    w, m, v = O.optim_step("adam", w0.copy(), g, m, v, lr=0.01, beta1=b1, beta2=b2, eps=1e-8,
+                           bc1=np.float32(1) - O.powf(b1, 1), bc2=np.float32(1) - O.powf(b2, 1))
+    big = np.abs(g) > 1e-2
+    assert np.allclose((w0 - w)[big], 0.01 * np.sign(g[big]), rtol=1e-3)
+    one_m_b1, one_m_b2 = np.float64(np.float32(1) - b1), np.float64(np.float32(1) - b2)  # fp32 constants
+    assert np.allclose(m, one_m_b1 * g, rtol=1e-6) and np.allclose(v, one_m_b2 * g * g, rtol=1e-6)
+    # AdamW's decay multiplies the weights before the Adam update; with g = 0 only the decay acts
+    z = np.zeros_like(g)
+    w, _, _ = O.optim_step("adamw", w0.copy(), z, np.zeros_like(w0), np.zeros_like(w0), lr=0.1, weight_decay=0.5,
+                           beta1=b1, beta2=b2, eps=1e-8, bc1=np.float32(0.1), bc2=np.float32(0.001))
+    assert_bits(w, (w0 * (np.float32(1) - np.float32(0.1) * np.float32(0.5))).astype(np.float32), "adamw decay")
+    # clip: the clipped grads' norm is max_norm; below the threshold nothing changes
+    total, gc = O.clip_grad_norm([g, 2 * g], 1.0)
+    assert abs(float(total) - float(np.sqrt(5 * (g.astype(np.float64) ** 2).sum()))) <= 1e-6 * float(total)
+    assert abs(np.sqrt(sum((x.astype(np.float64) ** 2).sum() for x in gc)) - 1.0) < 1e-5
+    total, gc = O.clip_grad_norm([g], 1e9)
+    assert_bits(gc[0], g, "no clip")
+
+
 def test_loss_closed_forms():
     rng = np.random.default_rng(5)
     # uniform logits: every row's loss is log(C), every probability 1/C
