@@ -201,8 +201,9 @@ def class_workloads(K, hm):
         ("quantize_rows", 5 * qe + 4 * qrows, lambda: K.quantize_rows(qrows, qcols, Wq.ptr, Q.ptr, SC.ptr)),
         ("dequantize_rows", 5 * qe + 4 * qrows, lambda: K.dequantize_rows(qrows, qcols, Q.ptr, SC.ptr, DQ.ptr)),
     ]
-    # optimizer step over 2^26 parameters: Adam reads w, g, m, v and writes w, m, v (28 B/param);
-    # clip_grad_norm's fp64 sum of squares reads g (4 B/param)
+    # optimizer step over 2^26 parameters: Adam reads w, g, m, v and writes w, m, v (28 B/param), SGD
+    # with momentum reads w, g, v and writes w, v (20 B/param); clip_grad_norm's fp64 sum of squares
+    # reads g (4 B/param)
     npar = 1 << 26
     PW = hm.DeviceBuffer.from_numpy(np.random.default_rng(12).standard_normal(npar, dtype=np.float32))
     PG = hm.DeviceBuffer.from_numpy(np.random.default_rng(13).standard_normal(npar, dtype=np.float32))
@@ -216,7 +217,7 @@ def class_workloads(K, hm):
         ("adam_step", 28 * npar,
          lambda: K.optim_step("adam", npar, PW.ptr, PG.ptr, PM.ptr, PV.ptr, 1e-3, 0.0, 0.0, 0.9, 0.999, 1e-8, 1.0,
                               0.1, 0.001)),
-        ("sgd_momentum_step", 16 * npar,
+        ("sgd_momentum_step", 20 * npar,
          lambda: K.optim_step("sgd", npar, PW.ptr, PG.ptr, PM.ptr, None, 1e-3, 0.9, 0.0)),
         ("grad_sumsq", 4 * npar, lambda: K.sumsq(npar, PG.ptr, SSD.ptr, False, SWS.ptr, sws)),
     ]

@@ -128,13 +128,31 @@ __device__ __forceinline__ double block_sum_waves(double v) {
     return t;
 }
 
-__global__ __launch_bounds__(kOB) void k_sumsq(const float *__restrict__ x, int64_t n, double *__restrict__ part) {
-    double acc = 0.0;
-    for (int64_t e = (int64_t)blockIdx.x * kOB + threadIdx.x; e < n; e += (int64_t)gridDim.x * kOB) {
-        const double v = (double)x[e];
-        acc += v * v;
+// float4 items (kOU per lane in flight) into four fp64 accumulators per lane, one per item slot,
+// added in slot order at the end; the scalar tail (n % 4, or an unaligned x) goes to slot 0
+__global__ __launch_bounds__(kOB) void k_sumsq(const float *__restrict__ x, int64_t n, int64_t n4,
+                                               double *__restrict__ part) {
+    double acc[kOU] = {0.0, 0.0, 0.0, 0.0};
+    const f4 *x4 = (const f4 *)x;
+    const int64_t step = (int64_t)gridDim.x * kOB * kOU;
+    for (int64_t base = (int64_t)blockIdx.x * kOB * kOU + threadIdx.x; base < n4; base += step) {
+        f4 v[kOU];
+#pragma unroll
+        for (int u = 0; u < kOU; u++)
+            if (base + (int64_t)u * kOB < n4) v[u] = __builtin_nontemporal_load(x4 + base + (int64_t)u * kOB);
+#pragma unroll
+        for (int u = 0; u < kOU; u++) {
+            if (base + (int64_t)u * kOB < n4) {
+                const double a = v[u].x, b = v[u].y, c = v[u].z, d = v[u].w;
+                acc[u] += (a * a + b * b) + (c * c + d * d);
+            }
+        }
     }
-    const double t = block_sum_waves(acc);
+    for (int64_t e = n4 * 4 + (int64_t)blockIdx.x * kOB + threadIdx.x; e < n; e += (int64_t)gridDim.x * kOB) {
+        const double v = (double)x[e];
+        acc[0] += v * v;
+    }
+    const double t = block_sum_waves((acc[0] + acc[1]) + (acc[2] + acc[3]));
     if (threadIdx.x == 0) part[blockIdx.x] = t;
 }
 
@@ -147,7 +165,7 @@ __global__ __launch_bounds__(kOB) void k_sumsq_finish(const double *__restrict__
 }
 
 static unsigned sumsq_grid(int64_t n) {
-    const int64_t blocks = (n + kOB - 1) / kOB, cap = (int64_t)num_cus() * 8;
+    const int64_t blocks = (n + 4 * kOB * kOU - 1) / (4 * kOB * kOU), cap = (int64_t)num_cus() * 8;
     return (unsigned)std::max<int64_t>(1, std::min(blocks, cap));
 }
 
@@ -212,7 +230,8 @@ extern "C" NC_HIP_API int nc_hip_sumsq(int64_t n, const float *x, double *ss, in
             return set_error(NC_HIP_ERR_WORKSPACE, "nc_hip_sumsq: workspace of %zu bytes needed",
                              nc_hip_sumsq_workspace(n));
         const unsigned grid = sumsq_grid(n);
-        hipLaunchKernelGGL(k_sumsq, grid, kOB, 0, st, x, n, (double *)ws);
+        const int64_t n4 = aligned16(x) ? n / 4 : 0;  // float4 items; the rest one float per lane
+        hipLaunchKernelGGL(k_sumsq, grid, kOB, 0, st, x, n, n4, (double *)ws);
         nparts = (int)grid;
     }
     hipLaunchKernelGGL(k_sumsq_finish, 1, kOB, 0, st, (const double *)ws, nparts, ss, accumulate ? 1 : 0);
