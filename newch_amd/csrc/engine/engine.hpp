@@ -155,6 +155,7 @@ struct nc_ctx {
     int n_threads = 1;
 
     std::vector<nc_optim *> optims;  // live optimizers, freed at nc_free_ctx
+    char *io_stage = nullptr;        // pinned staging for NCW1 file I/O (two halves), allocated on first use
 
     int device = -1;  // -1: no HIP device
     hipStream_t stream = nullptr;

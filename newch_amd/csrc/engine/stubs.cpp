@@ -1,5 +1,5 @@
 // The rest of the reference ABI (engine/include/nc.h) outside this build's hot path: GEMM-based ops,
-// convolution, masking, serialization and modules.  Every symbol exists, so the
+// convolution, masking and modules.  Every symbol exists, so the
 // reference's ctypes bindings resolve all their names at import (newch/_lib.py:174-177), and every
 // call fails cleanly the reference way -- a sticky NC_ERR_STATE in the context and a NULL / error
 // result -- instead of computing anything on the host.
@@ -39,14 +39,6 @@ nc_tensor *nc_linear_int8(nc_tensor *x, nc_tensor *wq, nc_tensor *, nc_tensor *)
     return absent(x ? x : wq, "linear_int8");
 }
 
-nc_status nc_save(nc_ctx *ctx, const char *, int, const char *const *, nc_tensor *const *) {
-    absent_ctx(ctx, "nc_save");
-    return NC_ERR_STATE;
-}
-nc_status nc_load(nc_ctx *ctx, const char *, int, const char *const *, nc_tensor *const *) {
-    absent_ctx(ctx, "nc_load");
-    return NC_ERR_STATE;
-}
 
 nc_module *nc_linear(nc_ctx *ctx, int64_t, int64_t, int) {
     absent_ctx(ctx, "nc_linear");

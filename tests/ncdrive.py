@@ -6,7 +6,7 @@ for both."""
 from __future__ import annotations
 
 import ctypes
-from ctypes import c_float, c_void_p
+from ctypes import c_char_p, c_float, c_void_p
 
 import numpy as np
 
@@ -134,3 +134,52 @@ class Engine:
         gx = self.grad(p)
         self.step_end()
         return yv, gx
+
+
+# ---- NCW1 files --------------------------------------------------------------------------------------
+def io_tensors(e: "Engine", rng_seed: int = 0, big: int = 0):
+    """A fixed set of named tensors built in engine `e`: f32 / i32 / i8 / u8, a 0-d scalar, an empty
+    tensor, a transposed (strided) view, a parameter, and optionally one f32 tensor of `big` floats.
+    Returns (names, tensors, numpy values in file order)."""
+    rng = np.random.default_rng(rng_seed)
+    L = e.lib
+    vals = {
+        "w": rng.standard_normal((3, 4)).astype(np.float32),
+        "idx": np.arange(-2, 3, dtype=np.int32),
+        "q": rng.integers(-127, 128, (2, 3)).astype(np.int8),
+        "mask": rng.integers(0, 256, 7).astype(np.uint8),
+        "scalar": np.array(2.5, np.float32),
+        "empty": np.zeros((0, 3), np.float32),
+    }
+    names, tensors, arrays = [], [], []
+    for k, v in vals.items():
+        names.append(k)
+        tensors.append(e.tensor(v))
+        arrays.append(v)
+    base = rng.standard_normal((4, 5)).astype(np.float32)
+    names.append("w_t")
+    tensors.append(L.nc_transpose(e.tensor(base), 0, 1))
+    arrays.append(np.ascontiguousarray(base.T))
+    p = rng.standard_normal(6).astype(np.float32)
+    names.append("0.weight")
+    tensors.append(e.param(p))
+    arrays.append(p)
+    if big:
+        b = rng.standard_normal(big).astype(np.float32)
+        names.append("big")
+        tensors.append(e.tensor(b))
+        arrays.append(b)
+    e.check()
+    return names, tensors, arrays
+
+
+def io_save(e: "Engine", path, names, tensors):
+    arr_n = (c_char_p * len(names))(*[n.encode() for n in names])
+    arr_t = (c_void_p * len(tensors))(*tensors)
+    return e.lib.nc_save(e.ctx, str(path).encode(), len(names), arr_n, arr_t)
+
+
+def io_load(e: "Engine", path, names, tensors):
+    arr_n = (c_char_p * len(names))(*[n.encode() for n in names])
+    arr_t = (c_void_p * len(tensors))(*tensors)
+    return e.lib.nc_load(e.ctx, str(path).encode(), len(names), arr_n, arr_t)

@@ -1079,6 +1079,58 @@ def test_kernel_sumsq(K, sizes):
     assert abs(got - want) <= 1e-12 * max(want, 1.0) and abs(got - exact) <= 1e-12 * max(exact, 1.0)
 
 
+# ------------------------------------------------------------------------------------------------
+# NCW1 files from and to device memory
+# ------------------------------------------------------------------------------------------------
+BIG_IO = 10_000_003  # 40 MB of f32: three staging chunks, the last one partial
+
+
+def test_engine_ncw1_device_roundtrip(eng, tmp_path):
+    """Device tensors (a strided view, a parameter, int8 / uint8 / i32, 0-d, empty and a 40 MB one)
+    saved and loaded back into fresh device tensors, values and dtypes intact; the file is the
+    reference's byte for byte when the reference library is present."""
+    from tests.ncdrive import io_load, io_save, io_tensors
+    names, ts, arrays = io_tensors(eng, rng_seed=9, big=BIG_IO)
+    # a kernel writes the big tensor's storage, so its data is device-resident when saved
+    big = ts[-1]
+    ts[-1] = eng.lib.nc_scale(big, c_float(1.0))
+    assert io_save(eng, tmp_path / "dev.ncw", names, ts) == 0, eng.lib.nc_error(eng.ctx)
+    targets = [eng.tensor(np.zeros_like(a)) for a in arrays]
+    assert io_load(eng, tmp_path / "dev.ncw", names[::-1], targets[::-1]) == 0, eng.lib.nc_error(eng.ctx)
+    for n, t, a in zip(names, targets, arrays):
+        got = eng.read(t)
+        assert got.dtype == a.dtype and got.shape == a.shape and (got == a).all(), n
+    # loaded data is device-resident: an op reads it without a host round trip
+    s = eng.read(eng.lib.nc_sum(targets[-1], abi.ALL_AXES, 0))
+    assert abs(float(s) - float(arrays[-1].astype(np.float64).sum())) <= 1e-3 * float(np.abs(arrays[-1]).sum())
+    eng.step_end()
+    if O.REF_LIB.exists():
+        with Engine(O.REF_LIB) as ref:
+            rn, rt, _ = io_tensors(ref, rng_seed=9, big=BIG_IO)
+            assert io_save(ref, tmp_path / "ref.ncw", rn, rt) == 0
+        assert (tmp_path / "dev.ncw").read_bytes() == (tmp_path / "ref.ncw").read_bytes()
+
+
+def test_engine_ncw1_load_into_parameters(eng, tmp_path):
+    """A checkpoint restored into parameters that kernels already wrote (host copies stale)."""
+    from tests.ncdrive import io_load, io_save
+    L = eng.lib
+    rng = np.random.default_rng(2)
+    w = rng.standard_normal((64, 33)).astype(np.float32)
+    src = eng.tensor(w)
+    assert io_save(eng, tmp_path / "p.ncw", ["layer.weight"], [src]) == 0
+    p = eng.param(np.zeros_like(w))
+    _ = eng.read(p)  # host copy exists
+    arr = (c_void_p * 1)(p)
+    o = L.nc_sgd(eng.ctx, arr, 1, abi.OptimOpts(0.5, 0, 0, 0, 0, 0))
+    assert L.nc_backward_ex(L.nc_sum(p, abi.ALL_AXES, 0), 0, None, 0) == 0
+    L.nc_optim_step(o)  # device copy now newer than the host copy
+    assert io_load(eng, tmp_path / "p.ncw", ["layer.weight"], [p]) == 0, L.nc_error(eng.ctx)
+    assert_bits(eng.read(p), w, "restored weights")
+    L.nc_optim_free(o)
+    eng.step_end()
+
+
 @pytest.mark.parametrize("rows,cols", [(512, 4096), (96, 70), (64, 8192), (33, 10000), (8, 16)])
 def test_kernel_quantize(K, rows, cols):
     rng = np.random.default_rng(rows * cols)

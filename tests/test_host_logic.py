@@ -6,7 +6,7 @@ HIP device instead of falling back to the host."""
 import ctypes
 import random
 import re
-from ctypes import c_float, c_uint32, c_void_p
+from ctypes import c_char_p, c_float, c_uint32, c_void_p
 from pathlib import Path
 
 import numpy as np
@@ -256,3 +256,81 @@ def test_sticky_error_and_null_propagation(eng):
     assert L.nc_error(eng.ctx) == msg  # first error sticks
     L.nc_clear_error(eng.ctx)
     assert L.nc_ok(eng.ctx)
+
+
+# ------------------------------------------------------------------------------------------------
+# NCW1 files: the reference's bytes and messages (host storage: no device needed)
+# ------------------------------------------------------------------------------------------------
+@ref_only
+def test_ncw1_bytes_match_reference(eng, tmp_path):
+    from tests.ncdrive import io_save, io_tensors
+    with Engine(O.REF_LIB) as ref:
+        names, ts, _ = io_tensors(ref)
+        assert io_save(ref, tmp_path / "ref.ncw", names, ts) == 0
+    names, ts, _ = io_tensors(eng)
+    assert io_save(eng, tmp_path / "ours.ncw", names, ts) == 0
+    assert (tmp_path / "ours.ncw").read_bytes() == (tmp_path / "ref.ncw").read_bytes()
+    eng.step_end()
+
+
+@ref_only
+def test_ncw1_load_reference_file(eng, tmp_path):
+    from tests.ncdrive import io_load, io_save, io_tensors
+    with Engine(O.REF_LIB) as ref:
+        names, ts, arrays = io_tensors(ref, rng_seed=5)
+        assert io_save(ref, tmp_path / "ref.ncw", names, ts) == 0
+    # fresh contiguous targets of the same dtypes / shapes; ask for a subset in another order
+    L = eng.lib
+    want = {n: a for n, a in zip(names, arrays)}
+    pick = ["0.weight", "q", "w_t", "scalar", "empty", "mask"]
+    targets = [eng.tensor(np.zeros_like(want[n])) for n in pick]
+    assert io_load(eng, tmp_path / "ref.ncw", pick, targets) == 0, L.nc_error(eng.ctx)
+    for n, t in zip(pick, targets):
+        got = eng.read(t)
+        assert got.dtype == want[n].dtype and got.shape == want[n].shape and (got == want[n]).all(), n
+    eng.step_end()
+
+
+def _io_errors(e, tmp_path):
+    from tests.ncdrive import io_load, io_save
+    L = e.lib
+    good = tmp_path / "good.ncw"
+    t = e.tensor(np.ones((2, 3), np.float32))
+    assert io_save(e, good, ["a"], [t]) == 0
+    raw = good.read_bytes()
+    (tmp_path / "magic.ncw").write_bytes(b"XXXX" + raw[4:])
+    (tmp_path / "version.ncw").write_bytes(raw[:4] + (2).to_bytes(4, "little") + raw[8:])
+    (tmp_path / "trunc.ncw").write_bytes(raw[:-5])
+    (tmp_path / "header.ncw").write_bytes(raw[:20])
+    nb = raw.index((24).to_bytes(8, "little"))
+    (tmp_path / "bytes.ncw").write_bytes(raw[:nb] + (28).to_bytes(8, "little") + raw[nb + 8:] + b"\0" * 4)
+    out = []
+
+    def record(rc):
+        out.append((rc, L.nc_status_code(e.ctx), L.nc_error(e.ctx).decode().replace(str(tmp_path), "<dir>")))
+        L.nc_clear_error(e.ctx)
+
+    record(io_load(e, tmp_path / "missing.ncw", ["a"], [t]))
+    for f in ("magic", "version", "trunc", "header", "bytes"):
+        record(io_load(e, tmp_path / f"{f}.ncw", ["a"], [e.tensor(np.zeros((2, 3), np.float32))]))
+    record(io_load(e, good, ["b"], [e.tensor(np.zeros((2, 3), np.float32))]))               # not found
+    record(io_load(e, good, ["a"], [e.tensor(np.zeros((3, 2), np.float32))]))               # shape
+    record(io_load(e, good, ["a"], [e.tensor(np.zeros((2, 3), np.int32))]))                 # dtype
+    record(io_load(e, good, ["a"], [L.nc_transpose(e.tensor(np.zeros((3, 2), np.float32)), 0, 1)]))  # view
+    record(io_save(e, tmp_path / "nope" / "x.ncw", ["a"], [t]))                              # unopenable
+    arr_n = (c_char_p * 2)(b"a", None)
+    arr_t = (c_void_p * 2)(t, t)
+    record(L.nc_save(e.ctx, str(tmp_path / "n.ncw").encode(), 2, arr_n, arr_t))              # NULL name
+    e.step_end()
+    return out
+
+
+@ref_only
+def test_ncw1_errors_match_reference(eng, tmp_path):
+    (tmp_path / "r").mkdir()
+    (tmp_path / "o").mkdir()
+    with Engine(O.REF_LIB) as ref:
+        want = _io_errors(ref, tmp_path / "r")
+    got = _io_errors(eng, tmp_path / "o")
+    for i, (w, g) in enumerate(zip(want, got)):
+        assert w == g, f"case {i}: reference {w}, this build {g}"
