@@ -9,7 +9,8 @@ A step is one pass of the headline workload over its synthetic batch: the six ac
 read x, write y; backward 16 B/element: read x or y, read g, read+write gi) over the timed wall
 time.  Every kernel launch is bracketed by HIP events on the launch stream; the per-kernel averages
 give `classes` (GB/s per op class, also for the broadcast / row-reduction / int8 / full-sum
-workloads unless --classes none) and the `roofline` of the dominant kernel.  `cpu_baseline` times
+workloads unless --classes none; `gemm`: TFLOP/s against the matrix-core peaks for the fp32 and int8
+linear / batched-matmul contractions) and the `roofline` of the dominant kernel.  `cpu_baseline` times
 the reference engine (oracle/_ref/libnc_ref.so, its own threaded AVX2 path) on a bounded sample of
 the same work.  Prints one JSON line.
 """
@@ -232,6 +233,53 @@ def class_workloads(K, hm):
     return work, keep
 
 
+PEAK_F32_TFLOPS = 157.3   # MI355X dense fp32 matrix
+PEAK_I8_TOPS = 5000.0     # MI355X dense int8 matrix
+
+
+def gemm_workloads(K, hm):
+    """Dense contractions at a transformer-linear shape: x [8192, 4096] through a [4096, 4096] weight
+    (forward NT, the two backward GEMMs NN and TN), the int8 linear (row quantization + int8 MFMA GEMM
+    + fused dequant/bias epilogue) and its bare int8 GEMM, and an attention-shaped batched product
+    (64 x [1024, 128] @ [128, 1024], B a transposed view).  Items: label, ops per launch, peak, fn."""
+    rng = np.random.default_rng(21)
+    M, Kd, N = 8192, 4096, 4096
+    X = hm.DeviceBuffer.from_numpy(rng.standard_normal((M, Kd), dtype=np.float32))
+    W = hm.DeviceBuffer.from_numpy((rng.standard_normal((N, Kd), dtype=np.float32) * 0.02).astype(np.float32))
+    G = hm.DeviceBuffer.from_numpy(rng.standard_normal((M, N), dtype=np.float32))
+    Y, GX, GW = hm.DeviceBuffer(4 * M * N), hm.DeviceBuffer(4 * M * Kd), hm.DeviceBuffer(4 * N * Kd)
+    WQ, WS = hm.DeviceBuffer(N * Kd), hm.DeviceBuffer(4 * N)
+    K.quantize_rows(N, Kd, W.ptr, WQ.ptr, WS.ptr)
+    BIAS = hm.DeviceBuffer.from_numpy(rng.standard_normal(N, dtype=np.float32))
+    XQ, XS = hm.DeviceBuffer(M * Kd), hm.DeviceBuffer(4 * M)
+    K.quantize_rows(M, Kd, X.ptr, XQ.ptr, XS.ptr)
+    C32 = hm.DeviceBuffer(4 * M * N)
+    qws = K.linear_int8_workspace(M, Kd)
+    QWS = hm.DeviceBuffer(qws)
+    Bh, S, D = 64, 1024, 128
+    QA = hm.DeviceBuffer.from_numpy(rng.standard_normal((Bh, S, D), dtype=np.float32))
+    KB = hm.DeviceBuffer.from_numpy(rng.standard_normal((Bh, S, D), dtype=np.float32))
+    SC = hm.DeviceBuffer(4 * Bh * S * S)
+    keep = [X, W, G, Y, GX, GW, WQ, WS, BIAS, XQ, XS, C32, QWS, QA, KB, SC]
+    f = 2.0 * M * N * Kd
+    work = [
+        ("linear_fwd_sgemm_nt", f, PEAK_F32_TFLOPS,
+         lambda: K.gemm_f32(0, 1, M, N, Kd, 1.0, X.ptr, Kd, W.ptr, Kd, 0.0, Y.ptr, N)),
+        ("linear_bwd_dx_sgemm_nn", f, PEAK_F32_TFLOPS,
+         lambda: K.gemm_f32(0, 0, M, Kd, N, 1.0, G.ptr, N, W.ptr, Kd, 0.0, GX.ptr, Kd)),
+        ("linear_bwd_dw_sgemm_tn", f, PEAK_F32_TFLOPS,
+         lambda: K.gemm_f32(1, 0, N, Kd, M, 1.0, G.ptr, N, X.ptr, Kd, 0.0, GW.ptr, Kd)),
+        ("bmm_qk_t_sgemm", 2.0 * Bh * S * S * D, PEAK_F32_TFLOPS,
+         lambda: K.gemm_f32_bmm(0, 1, S, S, D, QA.ptr, D, KB.ptr, D, 0.0, SC.ptr, S, [Bh], [S * D], [S * D],
+                                [S * S])),
+        ("gemm_s8_nt", f, PEAK_I8_TOPS,
+         lambda: K.gemm_s8_nt(M, N, Kd, XQ.ptr, Kd, WQ.ptr, Kd, C32.ptr, N)),
+        ("linear_int8", f, PEAK_I8_TOPS,
+         lambda: K.linear_int8(M, Kd, N, X.ptr, WQ.ptr, WS.ptr, BIAS.ptr, Y.ptr, QWS.ptr, qws)),
+    ]
+    return work, keep
+
+
 def measured_traffic(label: str):
     """HBM bytes per launch of `label` from the committed rocprofv3 PMC summary (FETCH_SIZE and
     WRITE_SIZE in KiB, scaled by what the same counters read for a plain copy of known size)."""
@@ -349,6 +397,7 @@ def main():
     d = classes[dom]
     log(f"bench: unary step {wall / args.steps * 1e3:.3f} ms, {value:.1f} GB/s; dominant {dom} {d['GB/s']} GB/s")
 
+    gemm = {}
     if args.classes == "all":
         work, keep = class_workloads(K, hm)
         for label, nbytes, fn in work:  # warm each once, then 5 timed launches
@@ -369,6 +418,24 @@ def main():
             log(f"bench: {k:28s} {v['GB/s']:8.1f} GB/s  {100 * v['frac']:5.1f}%  {v['us']:9.1f} us")
         classes.update(extra)
         del keep
+        gwork, gkeep = gemm_workloads(K, hm)
+        for label, ops, peak, fn in gwork:
+            fn()
+        hm.synchronize()
+        gtl = Timeline(hm)
+        for _ in range(5):
+            for label, ops, peak, fn in gwork:
+                gtl.run(label, ops, fn)
+        hm.synchronize()
+        gtl.collect()
+        for label, ops, peak, fn in gwork:
+            ms = float(np.median(gtl.stats[label]["ms"]))
+            rate = ops / (ms * 1e-3) / 1e12
+            gemm[label] = {"TFLOP/s" if peak == PEAK_F32_TFLOPS else "TOP/s": round(rate, 1), "peak": peak,
+                           "frac": round(rate / peak, 4), "us": round(ms * 1e3, 1), "ops": ops,
+                           "launches": len(gtl.stats[label]["ms"])}
+            log(f"bench: {label:28s} {rate:8.1f} T/s  {100 * rate / peak:5.1f}% of {peak}  {ms * 1e3:9.1f} us")
+        del gkeep
 
     cpu = None if args.no_cpu else cpu_baseline()
     if cpu:
@@ -396,6 +463,7 @@ def main():
                      "frac": d["frac"], "traffic": measured_traffic(dom), "algorithmic_bytes": d["bytes"]},
         "cpu_baseline": cpu,
         "classes": classes,
+        "gemm": gemm,
     }
     print(json.dumps(line), flush=True)
 

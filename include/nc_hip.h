@@ -183,6 +183,42 @@ NC_HIP_API size_t nc_hip_sumsq_workspace(int64_t n);
 NC_HIP_API int nc_hip_sumsq(int64_t n, const float *x, double *ss, int accumulate, void *ws, size_t ws_bytes,
                             void *stream);
 
+/* Row-major fp32 GEMM: C = alpha * op(A) op(B) + beta * C, op(X) = X^T when its flag is set; op(A) is
+ * M x K, op(B) K x N, leading dims in elements.  The reference's gemm_f32 (kernels.h:36-41) as used by
+ * matmul / linear (ops_linalg.c:64-99,296-330); dense GEMM on the matrix cores through rocBLAS,
+ * deterministic.  The batched form takes device arrays of `count` matrix pointers. */
+NC_HIP_API int nc_hip_gemm_f32(int ta, int tb, int64_t M, int64_t N, int64_t K, float alpha, const float *A,
+                               int64_t lda, const float *B, int64_t ldb, float beta, float *C, int64_t ldc,
+                               void *stream);
+NC_HIP_API int nc_hip_gemm_f32_batched(int ta, int tb, int64_t M, int64_t N, int64_t K, float alpha,
+                                       const float *const *A, int64_t lda, const float *const *B, int64_t ldb,
+                                       float beta, float *const *C, int64_t ldc, int64_t count, void *stream);
+/* Batched matmul with broadcast batch dims (the reference's bmm, ops_linalg.c:89-252): for every index
+ * of the batch shape bshape[nb], C_i = op(A_i) op(B_i) + beta C_i with A_i = A + sum_d idx_d sa[d]
+ * (likewise B, C; stride 0 = broadcast).  When several batch indices share one C block (sc has a 0 on
+ * a dim > 1, a broadcast operand's gradient) they run in batch order, each adding into the block; the
+ * others run as one batched rocBLAS call.  Workspace: device pointer arrays (0 bytes when the batch
+ * dims collapse to one uniform stride). */
+NC_HIP_API size_t nc_hip_gemm_f32_bmm_workspace(int64_t count);
+NC_HIP_API int nc_hip_gemm_f32_bmm(int ta, int tb, int64_t M, int64_t N, int64_t K, const float *A, int64_t lda,
+                                   const float *B, int64_t ldb, float beta, float *C, int64_t ldc, int nb,
+                                   const int64_t *bshape, const int64_t *sa, const int64_t *sb, const int64_t *sc,
+                                   void *ws, size_t ws_bytes, void *stream);
+
+/* int8 GEMM, C[m][n] = sum_k A[m][k] B[n][k] in int32 (A [M, K], B [N, K], both K-contiguous with
+ * leading dims lda / ldb; C leading dim ldc).  Exact, so bit-identical to the reference's gemm_s8_nt
+ * (kernels.h:42-43, kernels_ref.c:117-128) for K <= 133143.  Matrix cores (MFMA int8). */
+NC_HIP_API int nc_hip_gemm_s8_nt(int64_t M, int64_t N, int64_t K, const int8_t *A, int64_t lda, const int8_t *B,
+                                 int64_t ldb, int32_t *C, int64_t ldc, void *stream);
+/* linear_int8 forward (ops_quant.c:41-113): rows of x [M, K] quantized as quantize_rows does, the
+ * int8 product with wq [N, K] on the matrix cores, and the epilogue
+ * y = (float)acc * xs[m] * wscale[n] + (bias ? bias[n] : 0) fused into it; bit-identical to the
+ * reference.  Workspace: the quantized rows and their scales. */
+NC_HIP_API size_t nc_hip_linear_int8_workspace(int64_t M, int64_t K);
+NC_HIP_API int nc_hip_linear_int8(int64_t M, int64_t K, int64_t N, const float *x, const int8_t *wq,
+                                  const float *wscale, const float *bias, float *y, void *ws, size_t ws_bytes,
+                                  void *stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -1,5 +1,5 @@
-// The rest of the reference ABI (engine/include/nc.h) outside this build's hot path: GEMM-based ops,
-// convolution, masking and modules.  Every symbol exists, so the
+// The rest of the reference ABI (engine/include/nc.h) outside this build's hot path: convolution,
+// pooling, masking and modules.  Every symbol exists, so the
 // reference's ctypes bindings resolve all their names at import (newch/_lib.py:174-177), and every
 // call fails cleanly the reference way -- a sticky NC_ERR_STATE in the context and a NULL / error
 // result -- instead of computing anything on the host.
@@ -19,8 +19,6 @@ static void absent_ctx(nc_ctx *ctx, const char *name) {
 
 extern "C" {
 
-nc_tensor *nc_matmul(nc_tensor *a, nc_tensor *b) { return absent(a ? a : b, "matmul"); }
-nc_tensor *nc_linear_fn(nc_tensor *x, nc_tensor *weight, nc_tensor *) { return absent(x ? x : weight, "linear"); }
 nc_tensor *nc_index_select(nc_tensor *x, nc_tensor *) { return absent(x, "index_select"); }
 nc_tensor *nc_conv2d(nc_tensor *x, nc_tensor *, nc_tensor *, int, int, int, int) { return absent(x, "conv2d"); }
 nc_tensor *nc_conv2d_ex(nc_tensor *x, nc_tensor *, nc_tensor *, int, int, int, int, int, int, int) {
@@ -35,9 +33,6 @@ nc_tensor *nc_batch_norm(nc_tensor *x, nc_tensor *, nc_tensor *, nc_tensor *, nc
 nc_tensor *nc_masked_fill(nc_tensor *x, nc_tensor *, float) { return absent(x, "masked_fill"); }
 nc_tensor *nc_compare(nc_tensor *a, nc_tensor *b, nc_cmp) { return absent(a ? a : b, "compare"); }
 nc_tensor *nc_cat(int n, nc_tensor *const *xs, int) { return absent(n > 0 && xs ? xs[0] : nullptr, "cat"); }
-nc_tensor *nc_linear_int8(nc_tensor *x, nc_tensor *wq, nc_tensor *, nc_tensor *) {
-    return absent(x ? x : wq, "linear_int8");
-}
 
 
 nc_module *nc_linear(nc_ctx *ctx, int64_t, int64_t, int) {

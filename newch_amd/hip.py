@@ -65,6 +65,16 @@ SIGNATURES = {
     "nc_hip_cross_entropy_bwd": (c_int, [c_int64, c_int64, P, P, P, P, c_int, P]),
     "nc_hip_nll_loss_fwd": (c_int, [c_int64, c_int64, P, P, c_int, P, P, P, c_size_t, P]),
     "nc_hip_nll_loss_bwd": (c_int, [c_int64, c_int64, P, P, c_int, P, P]),
+    "nc_hip_gemm_f32": (c_int, [c_int, c_int, c_int64, c_int64, c_int64, c_float, P, c_int64, P, c_int64, c_float, P,
+                                c_int64, P]),
+    "nc_hip_gemm_f32_batched": (c_int, [c_int, c_int, c_int64, c_int64, c_int64, c_float, P, c_int64, P, c_int64,
+                                        c_float, P, c_int64, c_int64, P]),
+    "nc_hip_gemm_f32_bmm_workspace": (c_size_t, [c_int64]),
+    "nc_hip_gemm_f32_bmm": (c_int, [c_int, c_int, c_int64, c_int64, c_int64, P, c_int64, P, c_int64, c_float, P,
+                                    c_int64, c_int, I64P, I64P, I64P, I64P, P, c_size_t, P]),
+    "nc_hip_gemm_s8_nt": (c_int, [c_int64, c_int64, c_int64, P, c_int64, P, c_int64, P, c_int64, P]),
+    "nc_hip_linear_int8_workspace": (c_size_t, [c_int64, c_int64]),
+    "nc_hip_linear_int8": (c_int, [c_int64, c_int64, c_int64, P, P, P, P, P, P, c_size_t, P]),
 }
 
 
@@ -190,3 +200,29 @@ class Kernels:
 
     def dequantize_rows(self, rows, cols, q, scale, w, stream=None):
         self._ok(self.lib.nc_hip_dequantize_rows(rows, cols, q, scale, w, stream), "dequantize_rows")
+
+    def gemm_f32(self, ta, tb, M, N, K, alpha, A, lda, B, ldb, beta, C, ldc, stream=None):
+        self._ok(self.lib.nc_hip_gemm_f32(int(ta), int(tb), M, N, K, alpha, A, lda, B, ldb, beta, C, ldc, stream),
+                 "gemm_f32")
+
+    def gemm_f32_batched(self, ta, tb, M, N, K, alpha, A, lda, B, ldb, beta, C, ldc, count, stream=None):
+        self._ok(self.lib.nc_hip_gemm_f32_batched(int(ta), int(tb), M, N, K, alpha, A, lda, B, ldb, beta, C, ldc, count,
+                                                  stream), "gemm_f32_batched")
+
+    def gemm_f32_bmm_workspace(self, count):
+        return self.lib.nc_hip_gemm_f32_bmm_workspace(count)
+
+    def gemm_f32_bmm(self, ta, tb, M, N, K, A, lda, B, ldb, beta, C, ldc, bshape, sa, sb, sc, ws=None, ws_bytes=0,
+                     stream=None):
+        self._ok(self.lib.nc_hip_gemm_f32_bmm(int(ta), int(tb), M, N, K, A, lda, B, ldb, beta, C, ldc, len(bshape),
+                                              _i64(bshape), _i64(sa), _i64(sb), _i64(sc), ws, ws_bytes, stream),
+                 "gemm_f32_bmm")
+
+    def gemm_s8_nt(self, M, N, K, A, lda, B, ldb, C, ldc, stream=None):
+        self._ok(self.lib.nc_hip_gemm_s8_nt(M, N, K, A, lda, B, ldb, C, ldc, stream), "gemm_s8_nt")
+
+    def linear_int8_workspace(self, M, K):
+        return self.lib.nc_hip_linear_int8_workspace(M, K)
+
+    def linear_int8(self, M, K, N, x, wq, wscale, bias, y, ws, ws_bytes, stream=None):
+        self._ok(self.lib.nc_hip_linear_int8(M, K, N, x, wq, wscale, bias, y, ws, ws_bytes, stream), "linear_int8")

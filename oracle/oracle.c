@@ -9,6 +9,7 @@
 #include "oracle.h"
 
 #include <math.h>
+#include <stdlib.h>
 #include <stdint.h>
 #include <string.h>
 
@@ -559,6 +560,39 @@ void or_quantize_rows(int64_t rows, int64_t cols, const float *w, int8_t *q, flo
 void or_dequantize_rows(int64_t rows, int64_t cols, const int8_t *q, const float *scale, float *w) {
     for (int64_t r = 0; r < rows; r++)
         for (int64_t i = 0; i < cols; i++) w[r * cols + i] = (float)(double)q[r * cols + i] * scale[r];
+}
+
+/* gemm_s8_nt (kernels_ref.c:117-128; the AVX2 tier kernels_avx2.c:314-340 sums the same products
+ * in another order, exact either way): integer products summed in int64, stored as int32 (exact for
+ * K <= 133143, where |C| <= K * 127 * 127 < 2^31). */
+void or_gemm_s8_nt(int64_t M, int64_t N, int64_t K, const int8_t *A, int64_t lda, const int8_t *B, int64_t ldb,
+                   int32_t *C, int64_t ldc) {
+    for (int64_t i = 0; i < M; i++)
+        for (int64_t j = 0; j < N; j++) {
+            int64_t s = 0;
+            for (int64_t k = 0; k < K; k++) s += (int32_t)A[i * lda + k] * (int32_t)B[j * ldb + k];
+            C[i * ldc + j] = (int32_t)s;
+        }
+}
+
+/* linear_int8 forward (ops_quant.c:72-113): each row of x quantized by quantize_row (:11-21), the
+ * int8 product with wq, then the epilogue y = (float)acc * xs * ws + (bias or 0) of :75-79,
+ * left to right, uncontracted. */
+void or_linear_int8(int64_t M, int64_t K, int64_t N, const float *x, const int8_t *wq, const float *ws,
+                    const float *bias, float *y) {
+    int8_t *xq = (int8_t *)malloc((size_t)(M * K) + 1);
+    float *xs = (float *)malloc((size_t)(M ? M : 1) * sizeof(float));
+    int32_t *acc = (int32_t *)malloc((size_t)(M * N + 1) * sizeof(int32_t));
+    or_quantize_rows(M, K, x, xq, xs);
+    or_gemm_s8_nt(M, N, K, xq, K, wq, K, acc, N);
+    for (int64_t r = 0; r < M; r++)
+        for (int64_t o = 0; o < N; o++) {
+            const float prod = (float)acc[r * N + o] * xs[r];
+            y[r * N + o] = prod * ws[o] + (bias ? bias[o] : 0.0f);
+        }
+    free(xq);
+    free(xs);
+    free(acc);
 }
 
 /* ---------------------------------------------------------------------------------------------- */

@@ -75,6 +75,13 @@ void or_layer_norm_bwd(int64_t rows, int64_t D, const float *x, const float *w, 
 void or_quantize_rows(int64_t rows, int64_t cols, const float *w, int8_t *q, float *scale);
 void or_dequantize_rows(int64_t rows, int64_t cols, const int8_t *q, const float *scale, float *w);
 
+/* int8 GEMM C[m][n] = sum_k A[m][k] B[n][k] in int32 (A [M, K] lda, B [N, K] ldb, C ldc) */
+void or_gemm_s8_nt(int64_t M, int64_t N, int64_t K, const int8_t *A, int64_t lda, const int8_t *B, int64_t ldb,
+                   int32_t *C, int64_t ldc);
+/* linear_int8 forward: x [M, K] f32, wq [N, K] i8, ws [N], bias [N] or NULL -> y [M, N] */
+void or_linear_int8(int64_t M, int64_t K, int64_t N, const float *x, const int8_t *wq, const float *ws,
+                    const float *bias, float *y);
+
 /* cross entropy over logits [N, C] with labels [N] (mean over rows): prob [N, C] receives
  * exp(log_softmax(x)), *loss the mean; returns -1, or the first row whose label is outside [0, C). */
 int64_t or_cross_entropy_fwd(int64_t N, int64_t C, const float *x, const int32_t *lab, float *prob, float *loss);

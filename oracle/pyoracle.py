@@ -365,3 +365,103 @@ def clip_grad_norm(grads, max_norm):
     if coef < np.float32(1.0):
         grads = [(np.asarray(g, np.float32) * coef).astype(np.float32) for g in grads]
     return total, grads
+
+
+# ---- int8 GEMM and linear_int8 (exact; C restatement) ------------------------------------------
+def gemm_s8_nt(A, B):
+    """C = A @ B^T in int32 for A [M, K], B [N, K] int8 (kernels_ref.c:117-128)."""
+    A = np.ascontiguousarray(A, np.int8)
+    B = np.ascontiguousarray(B, np.int8)
+    (M, K), N = A.shape, B.shape[0]
+    C = np.empty((M, N), np.int32)
+    lib().or_gemm_s8_nt(c_int64(M), c_int64(N), c_int64(K), _p(A), c_int64(K), _p(B), c_int64(K), _p(C),
+                        c_int64(N))
+    return C
+
+
+def linear_int8(x, wq, ws, bias=None):
+    """linear_int8 forward (ops_quant.c:72-113) for x [..., K]; returns y [..., N]."""
+    x = _f32(x)
+    wq = np.ascontiguousarray(wq, np.int8)
+    N, K = wq.shape
+    M = int(np.prod(x.shape[:-1]))
+    y = np.empty(x.shape[:-1] + (N,), np.float32)
+    lib().or_linear_int8(c_int64(M), c_int64(K), c_int64(N), _p(x), _p(wq), _p(_f32(ws)),
+                         _p(None if bias is None else _f32(bias)), _p(y))
+    return y
+
+
+# ---- fp32 GEMM ops: fp64 truth ------------------------------------------------------------------
+# The reference's fp32 GEMMs (kernels_avx2.c:182-303, split over threads by nc__gemm,
+# threadpool.c:243-265) sum in an order that is theirs alone; the truth here is the exact product in
+# fp64, and results (the reference's and the HIP path's) are held to
+#     |y - y64| <= rtol * max(|y64|, T / sqrt(K)),   T = sum_k |a_k b_k|  (|A| @ |B| in fp64),
+# the reductions' tolerance applied to a K-term dot product.
+def sum_to_shape(x, shape):
+    """Sums a broadcast result back to `shape` (numpy broadcasting rules)."""
+    x = np.asarray(x)
+    lead = x.ndim - len(shape)
+    if lead:
+        x = x.sum(axis=tuple(range(lead)))
+    axes = tuple(i for i, s in enumerate(shape) if s == 1 and x.shape[i] != 1)
+    if axes:
+        x = x.sum(axis=axes, keepdims=True)
+    return x.reshape(shape)
+
+
+def matmul64(a, b):
+    """Forward truth and term bound of matmul / bmm (ops_linalg.c:58-66, :220-234): numpy's
+    broadcasting matmul has the reference's semantics ([..., M, K] @ [K, N] folds a's leading dims;
+    3-D+ operands broadcast their batch dims)."""
+    a64, b64 = np.asarray(a, np.float64), np.asarray(b, np.float64)
+    return np.matmul(a64, b64), np.matmul(np.abs(a64), np.abs(b64))
+
+
+def matmul_grads64(a, b, G):
+    """(ga, gb, ta, tb): gradients of sum(matmul(a, b) * G) (ops_linalg.c:68-85, :236-262) summed to
+    the operands' shapes, and their term bounds."""
+    a64, b64, G64 = (np.asarray(v, np.float64) for v in (a, b, G))
+    bt, at = np.swapaxes(b64, -1, -2), np.swapaxes(a64, -1, -2)
+    if b64.ndim == 2 and a64.ndim > 2:  # folded: a [..., M, K]
+        M = a64.size // a64.shape[-1]
+        a2, G2 = a64.reshape(M, -1), G64.reshape(M, -1)
+        ga = (G2 @ b64.T).reshape(a64.shape)
+        ta = (np.abs(G2) @ np.abs(b64.T)).reshape(a64.shape)
+        gb, tb = a2.T @ G2, np.abs(a2.T) @ np.abs(G2)
+        return ga, gb, ta, tb
+    ga = sum_to_shape(np.matmul(G64, bt), a64.shape)
+    ta = sum_to_shape(np.matmul(np.abs(G64), np.abs(bt)), a64.shape)
+    gb = sum_to_shape(np.matmul(at, G64), b64.shape)
+    tb = sum_to_shape(np.matmul(np.abs(at), np.abs(G64)), b64.shape)
+    return ga, gb, ta, tb
+
+
+def linear64(x, W, bias=None):
+    """(y, t): y = x @ W^T + b (ops_linalg.c:296-306) in fp64 and its term bound."""
+    x64, W64 = np.asarray(x, np.float64), np.asarray(W, np.float64)
+    y, t = x64 @ W64.T, np.abs(x64) @ np.abs(W64.T)
+    if bias is not None:
+        y = y + np.asarray(bias, np.float64)
+        t = t + np.abs(np.asarray(bias, np.float64))
+    return y, t
+
+
+def linear_grads64(x, W, G):
+    """(gx, gW, gb, tx, tW, tb): gradients of sum(linear(x, W, b) * G) (ops_linalg.c:308-330)."""
+    x64, W64, G64 = (np.asarray(v, np.float64) for v in (x, W, G))
+    N, K = W64.shape
+    x2, G2 = x64.reshape(-1, K), G64.reshape(-1, N)
+    gx = (G2 @ W64).reshape(x64.shape)
+    tx = (np.abs(G2) @ np.abs(W64)).reshape(x64.shape)
+    return gx, G2.T @ x2, G2.sum(0), tx, np.abs(G2.T) @ np.abs(x2), np.abs(G2).sum(0)
+
+
+def gemm_excess(got, truth, terms, K, rtol=1e-5):
+    """max over elements of |got - truth| / (rtol * max(|truth|, terms / sqrt(K))); <= 1 passes."""
+    got = np.asarray(got, np.float64)
+    bound = rtol * np.maximum(np.abs(truth), np.asarray(terms) / np.sqrt(max(K, 1)))
+    err = np.abs(got - truth)
+    with np.errstate(divide="ignore", invalid="ignore"):
+        r = np.where(err == 0, 0.0, err / bound)  # a nonzero error on a zero bound is inf; NaN stays NaN
+    r = np.where(np.isnan(r), np.inf, r)
+    return float(r.max()) if r.size else 0.0

@@ -7,7 +7,8 @@
  * Reference interfaces used (read-only, compiled in place):
  *   engine/src/kernels/kernels.h:9-44      nc_kernels table
  *   engine/src/kernels/dispatch.c:35-47    nc__select_kernels (avx2 tier on x86 with AVX2+FMA)
- *   engine/src/kernels/x86/kernels_avx2.c  exp8/sigmoid8/tanh8/erf8/sum_f32/axpy_f32
+ *   engine/src/kernels/x86/kernels_avx2.c  exp8/sigmoid8/tanh8/erf8/sum_f32/axpy_f32,
+ *                                          gemm_f32 (:298-303), gemm_s8_nt (:314-340)
  */
 #include "kernels.h"
 #include "../core/nc_internal.h"
@@ -31,3 +32,11 @@ void ncref_tanh_f32(int64_t n, const float *x, float *y) { probe_table()->tanh_f
 void ncref_erf_f32(int64_t n, const float *x, float *y) { probe_table()->erf_f32(n, x, y); }
 float ncref_sum_f32(int64_t n, const float *x) { return probe_table()->sum_f32(n, x); }
 void ncref_axpy_f32(int64_t n, float alpha, const float *x, float *y) { probe_table()->axpy_f32(n, alpha, x, y); }
+void ncref_gemm_f32(int ta, int tb, int64_t M, int64_t N, int64_t K, float alpha, const float *A, int64_t lda,
+                    const float *B, int64_t ldb, float beta, float *C, int64_t ldc) {
+    probe_table()->gemm_f32(ta, tb, M, N, K, alpha, A, lda, B, ldb, beta, C, ldc);
+}
+void ncref_gemm_s8_nt(int64_t M, int64_t N, int64_t K, const int8_t *A, int64_t lda, const int8_t *B, int64_t ldb,
+                      int32_t *C, int64_t ldc) {
+    probe_table()->gemm_s8_nt(M, N, K, A, lda, B, ldb, C, ldc);
+}

@@ -474,8 +474,109 @@ def gen_optim(ref, rng):
     np.savez_compressed(OUT / "optim.npz", **res)
 
 
+MATMUL_CASES = [
+    # name, a storage shape, a view, b storage shape, b view  (nc_matmul: b 2-D -> matmul, else bmm)
+    ("mm_2d", (33, 70), None, (70, 45), None),
+    ("mm_fold3d", (3, 17, 40), None, (40, 29), None),
+    ("mm_a_t", (70, 33), ("t", 0, 1), (70, 45), None),
+    ("mm_b_t", (33, 70), None, (45, 70), ("t", 0, 1)),
+    ("mm_both_t", (70, 33), ("t", 0, 1), (45, 70), ("t", 0, 1)),
+    ("mm_outer", (8, 1), None, (1, 9), None),
+    ("mm_fold_t", (3, 40, 17), ("t", 1, 2), (40, 29), None),
+    ("bmm_same", (4, 9, 20), None, (4, 20, 11), None),
+    ("bmm_bcast_a2d", (9, 20), None, (4, 20, 11), None),
+    ("bmm_bcast_4d", (2, 1, 9, 20), None, (1, 3, 20, 11), None),
+    ("bmm_b_t", (2, 3, 9, 20), None, (2, 3, 11, 20), ("t", 2, 3)),
+    ("bmm_rank", (5, 9, 20), None, (2, 1, 20, 11), None),
+    ("bmm_batch_t", (9, 4, 20), ("t", 0, 1), (4, 20, 11), None),
+]
+
+LINEAR_CASES = [  # name, x storage shape, x view, W shape, bias
+    ("lin_bias", (6, 70), None, (13, 70), True),
+    ("lin_nobias_3d", (2, 5, 33), None, (17, 33), False),
+    ("lin_x_t", (70, 6), ("t", 0, 1), (13, 70), True),
+    ("lin_wide", (20, 160), None, (130, 160), True),
+]
+
+QLINEAR_CASES = [  # name, x shape, W shape, bias
+    ("q_ref_test", (7, 70), (13, 70), True),          # the reference's own int8 test sizes (test_main.c:1046)
+    ("q_aligned", (37, 128), (70, 128), False),
+    ("q_3d", (2, 3, 64), (5, 64), True),
+    ("q_tiles", (131, 80), (130, 80), True),          # four 128 x 128 tiles, K % 64 = 16
+    ("q_odd_k", (9, 37), (11, 37), True),
+]
+
+
+def gen_linalg(ref, rng):
+    """matmul / bmm / linear forward and grads, linear_int8 outputs, and the int8 GEMM kernel
+    (ops_linalg.c, ops_quant.c:41-113, kernels_avx2.c:314-340)."""
+    res = {}
+    for name, ash, aview, bsh, bview in MATMUL_CASES:
+        A = rng.standard_normal(ash).astype(np.float32)
+        B = rng.standard_normal(bsh).astype(np.float32)
+        pa, va = make_view(ref, A, aview)
+        pb, vb = make_view(ref, B, bview)
+        out = ref.lib.nc_matmul(va, vb)
+        y = ref.read(out)
+        G = rng.standard_normal(y.shape).astype(np.float32)
+        ref.backward_with(out, G)
+        res.update({f"{name}/a_storage": A, f"{name}/b_storage": B, f"{name}/out": y, f"{name}/G": G,
+                    f"{name}/ga": ref.grad(va), f"{name}/gb": ref.grad(vb)})
+        ref.step_end()
+    for name, xsh, xview, wsh, has_b in LINEAR_CASES:
+        X = rng.standard_normal(xsh).astype(np.float32)
+        W = (rng.standard_normal(wsh) * 0.2).astype(np.float32)
+        Bv = rng.standard_normal(wsh[0]).astype(np.float32)
+        px, vx = make_view(ref, X, xview)
+        pw = ref.param(W)
+        pbias = ref.param(Bv) if has_b else None
+        out = ref.lib.nc_linear_fn(vx, pw, pbias)
+        y = ref.read(out)
+        G = rng.standard_normal(y.shape).astype(np.float32)
+        ref.backward_with(out, G)
+        res.update({f"{name}/x_storage": X, f"{name}/w": W, f"{name}/out": y, f"{name}/G": G,
+                    f"{name}/gx": ref.grad(vx), f"{name}/gw": ref.grad(pw)})
+        if has_b:
+            res[f"{name}/bias"] = Bv
+            res[f"{name}/gbias"] = ref.grad(pbias)
+        ref.step_end()
+    for name, xsh, wsh, has_b in QLINEAR_CASES:
+        X = rng.standard_normal(xsh).astype(np.float32)
+        if name == "q_tiles":
+            X[3] = 0.0                      # zero row: scale 1
+            X[5, 7] = 40.0                  # one large value dominates its row's scale
+        W = (rng.standard_normal(wsh) * 0.2).astype(np.float32)
+        Bv = rng.standard_normal(wsh[0]).astype(np.float32)
+        pw = ref.tensor(W)
+        sc = c_void_p()
+        q = ref.lib.nc_quantize_rows(pw, ctypes.byref(sc))
+        out = ref.lib.nc_linear_int8(ref.tensor(X), q, sc.value, ref.tensor(Bv) if has_b else None)
+        res.update({f"{name}/x": X, f"{name}/w": W, f"{name}/q": ref.read(q, np.int8),
+                    f"{name}/scale": ref.read(sc.value), f"{name}/out": ref.read(out),
+                    f"{name}/fp32_out": ref.read(ref.lib.nc_linear_fn(ref.tensor(X), pw,
+                                                                      ref.tensor(Bv) if has_b else None))})
+        if has_b:
+            res[f"{name}/bias"] = Bv
+        ref.step_end()
+    # the int8 GEMM of the kernel table on the reference's own known-answer inputs (test_main.c:1062-1073)
+    # and on random ones; kernel-table entries are reached through oracle/ref_probe.c
+    P = c_void_p
+    kat_a = np.array([(i * 37) % 255 - 127 for i in range(5 * 37)], np.int8).reshape(5, 37)
+    kat_b = np.array([(i * 91) % 255 - 127 for i in range(6 * 37)], np.int8).reshape(6, 37)
+    for name, A, B in (("s8_kat", kat_a, kat_b),
+                       ("s8_rand", rng.integers(-127, 128, (19, 131)).astype(np.int8),
+                        rng.integers(-127, 128, (23, 131)).astype(np.int8)),
+                       ("s8_extreme", np.full((4, 300), -127, np.int8), np.full((3, 300), -127, np.int8))):
+        C = np.empty((A.shape[0], B.shape[0]), np.int32)
+        ref.lib.ncref_gemm_s8_nt(c_int64(A.shape[0]), c_int64(B.shape[0]), c_int64(A.shape[1]), A.ctypes.data_as(P),
+                                 c_int64(A.shape[1]), B.ctypes.data_as(P), c_int64(B.shape[1]), C.ctypes.data_as(P),
+                                 c_int64(B.shape[0]))
+        res.update({f"{name}/a": A, f"{name}/b": B, f"{name}/c": C})
+    np.savez_compressed(OUT / "linalg.npz", **res)
+
+
 GENERATORS = ["transcendentals", "unary", "binary", "reduce", "softmax", "layer_norm", "quant", "chain", "loss",
-              "optim"]
+              "optim", "linalg"]
 
 
 def main():
@@ -502,11 +603,14 @@ def main():
         gen_loss(ref, np.random.default_rng(20261202))
     if "optim" in only:
         gen_optim(ref, np.random.default_rng(20261203))
+    if "linalg" in only:
+        gen_linalg(ref, np.random.default_rng(20261204))
     (OUT / "PROVENANCE.txt").write_text(
         "Written by tests/golden/gen_golden.py from oracle/_ref/libnc_ref.so, which oracle/Makefile builds\n"
         "from the reference engine sources (engine/src/**/*.c) with gcc 11.4, -O2 -std=gnu11, x86-64\n"
         f"baseline + AVX2/FMA target functions; kernel tier: {backend}; numpy seeds 20261201 (one stream\n"
-        "for transcendentals .. chain, in that order), 20261202 (loss) and 20261203 (optim).\n")
+        "for transcendentals .. chain, in that order), 20261202 (loss), 20261203 (optim) and\n"
+        "20261204 (linalg).\n")
     for f in sorted(OUT.glob("*.npz")):
         print(f"{f.name}: {f.stat().st_size / 1024:.0f} KiB")
 

@@ -1154,3 +1154,260 @@ def test_kernel_quantize(K, rows, cols):
     assert_bits(Q.to_numpy(np.int8, (rows, cols)), q_ref, "q")
     assert_bits(S.to_numpy(np.float32, rows), s_ref, "scale")
     assert_bits(D.to_numpy(np.float32, (rows, cols)), O.dequantize_rows(q_ref, s_ref), "dequant")
+
+
+# ================================================================================================
+# dense linear algebra: matmul / bmm / linear (fp32 GEMM) and linear_int8 (int8 MFMA)
+# ================================================================================================
+# fp32 GEMM results are held to the tolerance of a K-term reduction against the fp64 truth,
+# |y - y64| <= 1e-5 * max(|y64|, T / sqrt(K)) with T = |A| @ |B| (oracle.pyoracle.gemm_excess <= 1);
+# int8 results are exact, so bit for bit.
+MATMUL_CASES = [
+    ("mm_2d", None, None), ("mm_fold3d", None, None), ("mm_a_t", ("t", 0, 1), None),
+    ("mm_b_t", None, ("t", 0, 1)), ("mm_both_t", ("t", 0, 1), ("t", 0, 1)), ("mm_outer", None, None),
+    ("mm_fold_t", ("t", 1, 2), None), ("bmm_same", None, None), ("bmm_bcast_a2d", None, None),
+    ("bmm_bcast_4d", None, None), ("bmm_b_t", None, ("t", 2, 3)), ("bmm_rank", None, None),
+    ("bmm_batch_t", ("t", 0, 1), None)]
+
+
+def _mm_term_counts(a, b, y):
+    N = y.shape[-1]
+    if b.ndim == 2:
+        return N, y.size // N
+    M = y.shape[-2]
+    Bo = y.size // (M * N)
+    return N * Bo // (a.size // (a.shape[-2] * a.shape[-1])), M * Bo // (b.size // (b.shape[-2] * b.shape[-1]))
+
+
+@pytest.mark.parametrize("case,aview,bview", MATMUL_CASES, ids=[c[0] for c in MATMUL_CASES])
+def test_engine_matmul_golden(eng, case, aview, bview):
+    """The reference's matmul / bmm calls replayed (transposed views as GEMM flags, folded leading
+    dims, broadcast batch dims with their grads summed): forward and both grads within the GEMM
+    tolerance of fp64, as the reference's own outputs are."""
+    d = load("linalg")
+    A, B = d[f"{case}/a_storage"], d[f"{case}/b_storage"]
+    pa, pb = eng.param(A), eng.param(B)
+    va, vb = eng.view(pa, aview), eng.view(pb, bview)
+    out = eng.lib.nc_matmul(va, vb)
+    y = eng.read(out)
+    a, b = np_view(A, aview), np_view(B, bview)
+    y64, ty = O.matmul64(a, b)
+    assert y.shape == y64.shape
+    assert O.gemm_excess(y, y64, ty, a.shape[-1]) <= 1.0, "forward"
+    G = d[f"{case}/G"]
+    eng.backward_with(out, G)
+    ga64, gb64, ta, tb = O.matmul_grads64(a, b, G)
+    na, nb = _mm_term_counts(a, b, y64)
+    assert O.gemm_excess(eng.grad(va), ga64, ta, na) <= 1.0, "grad a"
+    assert O.gemm_excess(eng.grad(vb), gb64, tb, nb) <= 1.0, "grad b"
+    eng.step_end()
+
+
+def test_engine_matmul_grad_accumulates(eng):
+    """A parameter used by two products: the second GEMM adds into the grad the first one wrote
+    (beta 1 after a fresh buffer's beta 0), also through the ordered broadcast-grad path of bmm."""
+    rng = np.random.default_rng(11)
+    A = rng.standard_normal((24, 40)).astype(np.float32)
+    B1 = rng.standard_normal((40, 17)).astype(np.float32)
+    B3 = rng.standard_normal((3, 40, 17)).astype(np.float32)
+    L = eng.lib
+    pa, pb1, pb3 = eng.param(A), eng.param(B1), eng.param(B3)
+    y1, y3 = L.nc_matmul(pa, pb1), L.nc_matmul(pa, pb3)  # [24, 17] and [3, 24, 17]
+    G1 = rng.standard_normal((24, 17)).astype(np.float32)
+    G3 = rng.standard_normal((3, 24, 17)).astype(np.float32)
+    loss = L.nc_add(L.nc_sum(L.nc_mul(y1, eng.tensor(G1)), abi.ALL_AXES, 0),
+                    L.nc_sum(L.nc_mul(y3, eng.tensor(G3)), abi.ALL_AXES, 0))
+    assert L.nc_backward(loss) == 0, L.nc_error(eng.ctx)
+    ga64 = G1.astype(np.float64) @ B1.T.astype(np.float64) + sum(
+        G3[i].astype(np.float64) @ B3[i].T.astype(np.float64) for i in range(3))
+    ta = np.abs(G1) @ np.abs(B1.T) + sum(np.abs(G3[i]) @ np.abs(B3[i].T) for i in range(3))
+    assert O.gemm_excess(eng.grad(pa), ga64, ta, 17 * 4) <= 1.0
+    eng.step_end()
+
+
+LINEAR_CASES = [("lin_bias", None, True), ("lin_nobias_3d", None, False), ("lin_x_t", ("t", 0, 1), True),
+                ("lin_wide", None, True)]
+
+
+@pytest.mark.parametrize("case,xview,has_b", LINEAR_CASES, ids=[c[0] for c in LINEAR_CASES])
+def test_engine_linear_golden(eng, case, xview, has_b):
+    d = load("linalg")
+    X, W = d[f"{case}/x_storage"], d[f"{case}/w"]
+    bias = d[f"{case}/bias"] if has_b else None
+    px, pw = eng.param(X), eng.param(W)
+    pbias = eng.param(bias) if has_b else None
+    vx = eng.view(px, xview)
+    out = eng.lib.nc_linear_fn(vx, pw, pbias)
+    y = eng.read(out)
+    x = np_view(X, xview)
+    y64, ty = O.linear64(x, W, bias)
+    assert O.gemm_excess(y, y64, ty, W.shape[1]) <= 1.0, "forward"
+    G = d[f"{case}/G"]
+    eng.backward_with(out, G)
+    gx, gw, gb, tx, tw, tb = O.linear_grads64(x, W, G)
+    M = x.size // W.shape[1]
+    assert O.gemm_excess(eng.grad(vx), gx, tx, W.shape[0]) <= 1.0, "grad x"
+    assert O.gemm_excess(eng.grad(pw), gw, tw, M) <= 1.0, "grad w"
+    if has_b:
+        assert O.gemm_excess(eng.grad(pbias), gb, tb, M) <= 1.0, "grad bias"
+    eng.step_end()
+
+
+@pytest.mark.parametrize("case", ["q_ref_test", "q_aligned", "q_3d", "q_tiles", "q_odd_k"])
+def test_engine_linear_int8_golden(eng, case):
+    """quantize_rows then linear_int8 through the engine: bit-identical to the reference."""
+    d = load("linalg")
+    L = eng.lib
+    w = eng.tensor(d[f"{case}/w"])
+    sc = c_void_p()
+    q = L.nc_quantize_rows(w, ctypes.byref(sc))
+    has_b = f"{case}/bias" in d.files
+    out = L.nc_linear_int8(eng.tensor(d[f"{case}/x"]), q, sc.value, eng.tensor(d[f"{case}/bias"]) if has_b else None)
+    assert_bits(eng.read(out), d[f"{case}/out"], f"{case} linear_int8")
+    assert L.nc_requires_grad(out) == 0
+    eng.step_end()
+
+
+def test_engine_linear_int8_errors(eng):
+    """A transposed (non-contiguous) int8 weight fails the reference's way: NC_ERR_ARG and its
+    message (ops_quant.c:96-99)."""
+    L = eng.lib
+    wq = eng.tensor(np.ones((5, 4), np.int8))
+    x = eng.tensor(np.ones((2, 5), np.float32))
+    assert not L.nc_linear_int8(x, L.nc_transpose(wq, 0, 1), eng.tensor(np.ones(4, np.float32)), None)
+    assert L.nc_status_code(eng.ctx) == abi.ERR_ARG
+    assert L.nc_error(eng.ctx) == b"linear_int8: weight must be contiguous"
+    L.nc_clear_error(eng.ctx)
+    eng.step_end()
+
+
+S8_SIZES = [(1, 1, 16), (5, 6, 37), (128, 128, 64), (300, 260, 1040), (257, 129, 1000), (33, 517, 80), (7, 3, 0),
+            (2048, 1024, 4096)]
+
+
+def _rows_sample(M, n=48, seed=0):
+    if M <= n:
+        return np.arange(M)
+    rng = np.random.default_rng(seed)
+    return np.unique(np.concatenate([[0, M - 1], rng.choice(M, n - 2, replace=False)]))
+
+
+@pytest.mark.parametrize("M,N,Kd", S8_SIZES)
+def test_kernel_gemm_s8(K, M, N, Kd):
+    """int8 GEMM bit-exact against the oracle (rows sampled at the largest size: rows are
+    independent), on aligned (16-byte k chunks) and unaligned (byte path) shapes, partial tiles."""
+    rng = np.random.default_rng(M * 7919 + N * 31 + Kd)
+    A = rng.integers(-127, 128, (M, Kd)).astype(np.int8)
+    B = rng.integers(-127, 128, (N, Kd)).astype(np.int8)
+    if M > 3 and Kd:
+        A[1] = -127
+        B[0] = -127
+    Ad, Bd = dev(A), dev(B)
+    C = empty(4 * M * N)
+    K.gemm_s8_nt(M, N, Kd, Ad.ptr, Kd, Bd.ptr, Kd, C.ptr, N)
+    sync()
+    got = C.to_numpy(np.int32, (M, N))
+    rows = _rows_sample(M)
+    assert_bits(got[rows], O.gemm_s8_nt(A[rows], B), f"gemm_s8 {M}x{N}x{Kd}")
+
+
+def test_kernel_gemm_s8_leading_dims(K):
+    """Submatrices of wider buffers: lda, ldb, ldc larger than K and N."""
+    rng = np.random.default_rng(5)
+    M, N, Kd, lda, ldb, ldc = 150, 70, 96, 128, 112, 80
+    A = rng.integers(-127, 128, (M, lda)).astype(np.int8)
+    B = rng.integers(-127, 128, (N, ldb)).astype(np.int8)
+    Ad, Bd = dev(A), dev(B)
+    C0 = np.full((M, ldc), 12345, np.int32)
+    Cd = dev(C0)
+    K.gemm_s8_nt(M, N, Kd, Ad.ptr, lda, Bd.ptr, ldb, Cd.ptr, ldc)
+    sync()
+    got = Cd.to_numpy(np.int32, (M, ldc))
+    assert_bits(got[:, :N], O.gemm_s8_nt(A[:, :Kd], B[:, :Kd]), "C")
+    assert (got[:, N:] == 12345).all(), "wrote past N"
+
+
+QLIN_SIZES = [(7, 70, 13, True), (37, 128, 70, False), (300, 1024, 520, True), (129, 4000, 257, True),
+              (8192, 4096, 4096, True), (1, 64, 1, False), (5, 0, 3, True)]
+
+
+@pytest.mark.parametrize("M,Kd,N,has_b", QLIN_SIZES)
+def test_kernel_linear_int8(K, M, Kd, N, has_b):
+    """Fused quantize + int8 MFMA GEMM + epilogue, bit-exact against the oracle (rows sampled at the
+    benchmark size [8192, 4096] x [4096, 4096]^T)."""
+    rng = np.random.default_rng(M + 3 * Kd + 7 * N)
+    x = rng.standard_normal((M, Kd)).astype(np.float32)
+    if M > 4 and Kd:
+        x[2] = 0.0
+        x[3, 0] = 60.0
+    wq = rng.integers(-127, 128, (N, Kd)).astype(np.int8)
+    ws = (rng.random(N) * 0.01).astype(np.float32)
+    bias = rng.standard_normal(N).astype(np.float32) if has_b else None
+    xd, wqd, wsd = dev(x), dev(wq), dev(ws)
+    bd = dev(bias) if has_b else None
+    y = empty(4 * M * N)
+    nws = K.linear_int8_workspace(M, Kd)
+    ws_buf = empty(max(nws, 1))
+    K.linear_int8(M, Kd, N, xd.ptr, wqd.ptr, wsd.ptr, bd.ptr if has_b else None, y.ptr, ws_buf.ptr, nws)
+    sync()
+    got = y.to_numpy(np.float32, (M, N))
+    rows = _rows_sample(M)
+    assert_bits(got[rows], O.linear_int8(x[rows], wq, ws, bias), f"linear_int8 {M}x{Kd}x{N}")
+
+
+GEMM_F32 = [(0, 0, 1000, 500, 300), (1, 0, 257, 129, 1000), (0, 1, 64, 4096, 512), (1, 1, 33, 65, 17),
+            (0, 1, 4096, 4096, 4096), (0, 0, 5, 7, 0)]
+
+
+@pytest.mark.parametrize("ta,tb,M,N,Kd", GEMM_F32)
+def test_kernel_gemm_f32(K, ta, tb, M, N, Kd):
+    rng = np.random.default_rng(M + N + Kd + ta + 2 * tb)
+    A = rng.standard_normal((Kd, M) if ta else (M, Kd)).astype(np.float32)
+    B = rng.standard_normal((N, Kd) if tb else (Kd, N)).astype(np.float32)
+    C0 = rng.standard_normal((M, N)).astype(np.float32)
+    beta = 0.0 if Kd == 0 else 1.0  # K = 0 with beta 0: C is cleared (the engine's fresh-output call)
+    Ad, Bd, Cd = dev(A), dev(B), dev(C0)
+    K.gemm_f32(ta, tb, M, N, Kd, 0.5, Ad.ptr, A.shape[1], Bd.ptr, B.shape[1], beta, Cd.ptr, N)
+    sync()
+    got = Cd.to_numpy(np.float32, (M, N))
+    rows = _rows_sample(M, 64)
+    opA = (A.T if ta else A).astype(np.float64)[rows]
+    opB = (B.T if tb else B).astype(np.float64)
+    want = 0.5 * (opA @ opB) + beta * C0[rows]
+    terms = 0.5 * (np.abs(opA) @ np.abs(opB)) + beta * np.abs(C0[rows])
+    assert O.gemm_excess(got[rows], want, terms, Kd + 1) <= 1.0
+
+
+BMM_LAYOUTS = [
+    # name, batch shape, a batch strides (in matrices), b batch strides, c batch strides
+    ("strided", (6,), (1,), (1,), (1,)),
+    ("bcast_a", (4,), (0,), (1,), (1,)),
+    ("two_dims", (3, 4), (4, 1), (1, 3), (4, 1)),         # b's batch dims swapped: pointer arrays
+    ("shared_c", (2, 3), (3, 1), (3, 1), (1, 0)),          # C shared along dim 1: ordered GEMMs
+]
+
+
+@pytest.mark.parametrize("name,bshape,sa,sb,sc", BMM_LAYOUTS)
+def test_kernel_gemm_f32_bmm(K, name, bshape, sa, sb, sc):
+    rng = np.random.default_rng(len(name))
+    M, N, Kd = 33, 20, 47
+    count = int(np.prod(bshape))
+    na, nb_, nc_ = (max(1, 1 + sum((s_ - 1) * st for s_, st in zip(bshape, st_))) for st_ in (sa, sb, sc))
+    A = rng.standard_normal((na, M, Kd)).astype(np.float32)
+    B = rng.standard_normal((nb_, Kd, N)).astype(np.float32)
+    C0 = rng.standard_normal((nc_, M, N)).astype(np.float32)
+    Ad, Bd, Cd = dev(A), dev(B), dev(C0)
+    nws = K.gemm_f32_bmm_workspace(count)
+    wsb = empty(max(nws, 8))
+    K.gemm_f32_bmm(0, 0, M, N, Kd, Ad.ptr, Kd, Bd.ptr, N, 1.0, Cd.ptr, N, bshape, [s * M * Kd for s in sa],
+                   [s * Kd * N for s in sb], [s * M * N for s in sc], wsb.ptr, nws)
+    sync()
+    want = C0.astype(np.float64)
+    terms = np.abs(C0).astype(np.float64)
+    for idx in np.ndindex(*bshape):
+        ia = sum(i * s for i, s in zip(idx, sa))
+        ib = sum(i * s for i, s in zip(idx, sb))
+        ic = sum(i * s for i, s in zip(idx, sc))
+        want[ic] += A[ia].astype(np.float64) @ B[ib].astype(np.float64)
+        terms[ic] += np.abs(A[ia]) @ np.abs(B[ib])
+    assert O.gemm_excess(Cd.to_numpy(np.float32, C0.shape), want, terms, Kd * 3) <= 1.0

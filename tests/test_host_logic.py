@@ -108,11 +108,11 @@ def test_no_device_compute_fails_loudly(eng):
 
 def test_off_path_ops_report_not_in_this_build(eng):
     L = eng.lib
-    a = eng.tensor(np.ones((2, 2), np.float32))
-    assert not L.nc_matmul(a, a)
+    a = eng.tensor(np.ones((1, 1, 2, 2), np.float32))
+    assert not L.nc_conv2d(a, a, None, 1, 1, 0, 0)
     assert L.nc_status_code(eng.ctx) == abi.ERR_STATE and b"not in this build" in L.nc_error(eng.ctx)
     L.nc_clear_error(eng.ctx)
-    assert not L.nc_conv2d(a, a, None, 1, 1, 0, 0)
+    assert not L.nc_dropout(a, c_float(0.5))
     assert b"not in this build" in L.nc_error(eng.ctx)
 
 
@@ -183,6 +183,23 @@ SHAPE_ERRORS = [
     lambda e: e.lib.nc_nll_loss(e.tensor(np.ones((2, 3), np.float32)), e.tensor(np.zeros((2, 1), np.int32)), 1),
     lambda e: e.lib.nc_nll_loss(e.tensor(np.ones((2, 3), np.float32)), e.tensor(np.zeros(2, np.int8)), 0),
     lambda e: e.lib.nc_mse_loss(e.tensor(np.ones((2, 3), np.float32)), e.tensor(np.ones((4,), np.float32))),
+    # matmul / bmm / linear / linear_int8: ranks, inner dims, batch broadcast, dtypes
+    lambda e: e.lib.nc_matmul(e.tensor(np.ones((3,), np.float32)), e.tensor(np.ones((3, 4), np.float32))),
+    lambda e: e.lib.nc_matmul(e.tensor(np.ones((2, 3), np.float32)), e.tensor(np.ones((4, 5), np.float32))),
+    lambda e: e.lib.nc_matmul(e.tensor(np.ones((2, 3, 4), np.float32)), e.tensor(np.ones((3, 4, 6), np.float32))),
+    lambda e: e.lib.nc_matmul(e.tensor(np.ones((2, 3), np.float32)), e.tensor(np.ones((2, 4, 5), np.float32))),
+    lambda e: e.lib.nc_matmul(e.tensor(np.ones((2, 3), np.int32)), e.tensor(np.ones((3, 5), np.float32))),
+    lambda e: e.lib.nc_linear_fn(e.tensor(np.ones((2, 3), np.float32)), e.tensor(np.ones((4, 5), np.float32)), None),
+    lambda e: e.lib.nc_linear_fn(e.tensor(np.ones((2, 5), np.float32)), e.tensor(np.ones((4, 5), np.float32)),
+                                 e.tensor(np.ones((3,), np.float32))),
+    lambda e: e.lib.nc_linear_fn(e.tensor(np.ones((2, 5), np.float32)), e.tensor(np.ones((5,), np.float32)), None),
+    lambda e: e.lib.nc_linear_fn(e.tensor(np.ones((2, 5), np.float32)), e.tensor(np.ones((4, 5), np.int32)), None),
+    lambda e: e.lib.nc_linear_int8(e.tensor(np.ones((2, 5), np.float32)), e.tensor(np.ones((4, 5), np.float32)),
+                                   e.tensor(np.ones((4,), np.float32)), None),
+    lambda e: e.lib.nc_linear_int8(e.tensor(np.ones((2, 5), np.float32)), e.tensor(np.ones((4, 5), np.int8), abi.I8),
+                                   e.tensor(np.ones((3,), np.float32)), None),
+    lambda e: e.lib.nc_linear_int8(e.tensor(np.ones((2, 6), np.float32)), e.tensor(np.ones((4, 5), np.int8), abi.I8),
+                                   e.tensor(np.ones((4,), np.float32)), e.tensor(np.ones((4,), np.float32))),
 ]
 
 

@@ -241,6 +241,110 @@ def test_clip_grad_norm_golden(case):
         assert_bits(g[i], d[f"{case}/g{i}"], f"grad {i}")
 
 
+MATMUL_CASES = [
+    ("mm_2d", None, None), ("mm_fold3d", None, None), ("mm_a_t", ("t", 0, 1), None),
+    ("mm_b_t", None, ("t", 0, 1)), ("mm_both_t", ("t", 0, 1), ("t", 0, 1)), ("mm_outer", None, None),
+    ("mm_fold_t", ("t", 1, 2), None), ("bmm_same", None, None), ("bmm_bcast_a2d", None, None),
+    ("bmm_bcast_4d", None, None), ("bmm_b_t", None, ("t", 2, 3)), ("bmm_rank", None, None),
+    ("bmm_batch_t", ("t", 0, 1), None)]
+LINEAR_CASES = [("lin_bias", None, True), ("lin_nobias_3d", None, False), ("lin_x_t", ("t", 0, 1), True),
+                ("lin_wide", None, True)]
+QLINEAR_CASES = ["q_ref_test", "q_aligned", "q_3d", "q_tiles", "q_odd_k"]
+
+
+def _grad_term_counts(a, b, y):
+    """Terms summed per element of ga and gb: N (times the batches a matrix of a is broadcast over)
+    and M (likewise for b); a folded matmul sums gb over every row of a."""
+    N = y.shape[-1]
+    if b.ndim == 2:
+        return N, y.size // N
+    M = y.shape[-2]
+    Bo = y.size // (M * N)
+    Ba = a.size // (a.shape[-2] * a.shape[-1])
+    Bb = b.size // (b.shape[-2] * b.shape[-1])
+    return N * Bo // Ba, M * Bo // Bb
+
+
+@pytest.mark.parametrize("case,aview,bview", MATMUL_CASES, ids=[c[0] for c in MATMUL_CASES])
+def test_matmul_golden(case, aview, bview):
+    """The reference's fp32 matmul / bmm and their grads lie within the GEMM tolerance of the fp64
+    truth; a transposed operand, a wrong fold or a broadcast grad not summed would miss by O(1)."""
+    d = load("linalg")
+    a = make_view(d[f"{case}/a_storage"], aview)
+    b = make_view(d[f"{case}/b_storage"], bview)
+    y64, ty = O.matmul64(a, b)
+    ga, gb, ta, tb = O.matmul_grads64(a, b, d[f"{case}/G"])
+    assert d[f"{case}/out"].shape == y64.shape
+    assert d[f"{case}/ga"].shape == a.shape and d[f"{case}/gb"].shape == b.shape
+    na, nb = _grad_term_counts(a, b, y64)
+    assert O.gemm_excess(d[f"{case}/out"], y64, ty, a.shape[-1]) <= 1.0
+    assert O.gemm_excess(d[f"{case}/ga"], ga, ta, na) <= 1.0
+    assert O.gemm_excess(d[f"{case}/gb"], gb, tb, nb) <= 1.0
+
+
+@pytest.mark.parametrize("case,xview,has_b", LINEAR_CASES, ids=[c[0] for c in LINEAR_CASES])
+def test_linear_golden(case, xview, has_b):
+    d = load("linalg")
+    x = make_view(d[f"{case}/x_storage"], xview)
+    W = d[f"{case}/w"]
+    bias = d[f"{case}/bias"] if has_b else None
+    y64, ty = O.linear64(x, W, bias)
+    assert O.gemm_excess(d[f"{case}/out"], y64, ty, W.shape[1]) <= 1.0
+    gx, gw, gb, tx, tw, tb = O.linear_grads64(x, W, d[f"{case}/G"])
+    M = x.size // W.shape[1]
+    assert O.gemm_excess(d[f"{case}/gx"], gx, tx, W.shape[0]) <= 1.0
+    assert O.gemm_excess(d[f"{case}/gw"], gw, tw, M) <= 1.0
+    if has_b:
+        assert O.gemm_excess(d[f"{case}/gbias"], gb, tb, M) <= 1.0
+
+
+@pytest.mark.parametrize("case", QLINEAR_CASES)
+def test_linear_int8_golden(case):
+    d = load("linalg")
+    q, scale = O.quantize_rows(d[f"{case}/w"])
+    assert_bits(q, d[f"{case}/q"], "weight q")
+    assert_bits(scale, d[f"{case}/scale"], "weight scale")
+    bias = d[f"{case}/bias"] if f"{case}/bias" in d.files else None
+    y = O.linear_int8(d[f"{case}/x"], q, scale, bias)
+    assert_bits(y, d[f"{case}/out"], "linear_int8")
+    # the reference's own acceptance bound against the fp32 linear (test_main.c:1046-1060)
+    ref32 = d[f"{case}/fp32_out"].astype(np.float64)
+    rel = np.sqrt(((y - ref32) ** 2).sum() / (ref32 ** 2).sum())
+    assert rel < 0.02, rel
+
+
+@pytest.mark.parametrize("case", ["s8_kat", "s8_rand", "s8_extreme"])
+def test_gemm_s8_golden(case):
+    d = load("linalg")
+    A, B = d[f"{case}/a"], d[f"{case}/b"]
+    C = O.gemm_s8_nt(A, B)
+    assert_bits(C, d[f"{case}/c"], case)
+    assert (C == A.astype(np.int64) @ B.astype(np.int64).T).all()  # exact integer product
+
+
+def test_linear_int8_epilogue_order():
+    """The epilogue is ((float)acc * xs) * ws + b, each step rounded to fp32: the oracle matches that
+    form on every element, and on these inputs the reassociated product (xs * ws first) and the
+    contracted fma(prod, ws, b) each differ from it somewhere, so either mistake would be caught."""
+    rng = np.random.default_rng(7)
+    x = rng.standard_normal((200, 48)).astype(np.float32)
+    wq = rng.integers(-127, 128, (24, 48)).astype(np.int8)
+    ws = (rng.random(24) * 0.02).astype(np.float32)
+    bias = rng.standard_normal(24).astype(np.float32)
+    y = O.linear_int8(x, wq, ws, bias)
+    xq, xs = O.quantize_rows(x)
+    accf = (xq.astype(np.int64) @ wq.astype(np.int64).T).astype(np.float32)
+    prod = (accf * xs[:, None]).astype(np.float32)
+    want = ((prod * ws).astype(np.float32) + bias).astype(np.float32)
+    assert_bits(y, want, "left-to-right epilogue")
+    reassoc = ((accf * (xs[:, None] * ws).astype(np.float32)).astype(np.float32) + bias).astype(np.float32)
+    fused = (prod.astype(np.float64) * ws + bias).astype(np.float32)
+    assert not bits_equal(reassoc, y)[0] and not bits_equal(fused, y)[0]
+    y0 = O.linear_int8(x, wq, ws, None)  # no bias: the + 0.0f still applies (-0 becomes +0)
+    assert_bits(y0, ((prod * ws).astype(np.float32) + np.float32(0)).astype(np.float32), "no bias")
+    assert not np.signbit(y0[y0 == 0]).any()
+
+
 # ------------------------------------------------------------------------------------------------
 # the live reference (only where oracle/_ref was built: this container, or a box it travelled to)
 # ------------------------------------------------------------------------------------------------
