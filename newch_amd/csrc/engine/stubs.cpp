@@ -9,7 +9,7 @@ using namespace nce;
 
 static nc_tensor *absent(nc_tensor *any, const char *name) {
     if (any) error(any->ctx, NC_ERR_STATE, "%s: not in this build (the MI355X engine runs the elementwise, "
-                                          "reduction, normalization, loss and int8 hot path)", name);
+                                          "reduction, normalization, loss, optimizer, linear-algebra and int8 ops)", name);
     return nullptr;
 }
 

@@ -6,14 +6,16 @@
 // accumulation is exact in).  Integer sums do not depend on order, so every tiling gives the
 // reference's bits.
 //
-// Tiling: a 256-thread workgroup (4 wave64, 2 x 2) owns a 128 x 128 tile of C; each wave a 64 x 64
-// quarter as 2 x 2 v_mfma_i32_32x32x32_i8 accumulators (16 int32 per lane each).  K advances 64 bytes
-// at a time: the workgroup stages the A and B panels (128 x 64 bytes each) in LDS with rows padded to
-// 80 bytes (16-byte reads of 16 consecutive rows then hit distinct banks), and loads the next panels
-// into registers while the matrix cores work on the current one.  Each lane feeds the MFMA 16
-// consecutive k bytes of its row (lanes 0-31 rows 0-31 with k 0-15, lanes 32-63 the same rows with
-// k 16-31) for A and for B alike, so whatever order the instruction sums a lane's bytes in, A and B
-// pair the same k.
+// Tiling: a workgroup owns a BM x BN tile of C, each of its waves a (32 TM) x (32 TN) block of it as
+// TM x TN v_mfma_i32_32x32x32_i8 accumulators (16 int32 per lane each).  K advances BK bytes per
+// step through two LDS stages: the A and B panels (BM and BN rows of BK bytes, rows padded by 16 bytes
+// so 16-byte reads of 16 consecutive rows hit distinct banks) of step k+1 are loaded into registers
+// while the matrix cores work on step k, stored into the other stage, and one barrier per step
+// separates the two.  Each lane feeds the MFMA 16 consecutive k bytes of its row (lanes 0-31 rows
+// 0-31 with k 0-15, lanes 32-63 the same rows with k 16-31) for A and for B alike, so whatever order
+// the instruction sums a lane's bytes in, A and B pair the same k.  Large problems run 256 x 256
+// tiles (8 waves of 4 x 2 MFMA tiles, BK 128, 147 KiB of LDS), smaller ones 128 x 128 (4 waves of
+// 2 x 2, BK 64).
 // Blocks are remapped so each XCD (blocks b with b % 8 equal) works a contiguous run of tiles, and
 // tiles run in groups of 8 tile-rows so neighbouring blocks share panels in L2.
 //
@@ -26,10 +28,25 @@ namespace nchip {
 
 typedef int i16v __attribute__((ext_vector_type(16)));
 
-constexpr int kQgB = 256;
-constexpr int kQgBM = 128, kQgBN = 128, kQgBK = 64;
-constexpr int kQgPitch = kQgBK + 16;
 constexpr int kQgGroupM = 8;
+
+// Tile configurations: TM x TN MFMA tiles (32 x 32) per wave, WGM x WGN waves per workgroup, BK
+// k-bytes per stage, two LDS stages.  Large problems use a 256 x 256 tile (8 waves, 147 KiB of LDS,
+// one workgroup per CU); problems with fewer such tiles than CUs use 128 x 128 (4 waves, 40 KiB).
+template <int TM_, int TN_, int WGM_, int WGN_, int BK_, int OCC_>
+struct QgCfg {
+    static constexpr int TM = TM_, TN = TN_, WGM = WGM_, WGN = WGN_, BK = BK_, OCC = OCC_;
+    static constexpr int NT = 64 * WGM * WGN;
+    static constexpr int BM = 32 * TM * WGM, BN = 32 * TN * WGN;
+    static constexpr int PITCH = BK + 16;  // 16-byte reads of 16 consecutive rows land on distinct banks
+    static constexpr int CHUNK_ROW = BK / 16;  // 16-byte chunks per staged row
+    static constexpr int CHUNKS = (BM + BN) * CHUNK_ROW / NT;
+    static constexpr int STAGE = (BM + BN) * PITCH;  // bytes of one LDS stage (A rows, then B rows)
+    static constexpr size_t LDS = 2 * (size_t)STAGE;
+    static_assert((BM + BN) * CHUNK_ROW % NT == 0, "staging chunks must divide over the workgroup");
+};
+using QgBig = QgCfg<4, 2, 2, 4, 128, 1>;
+using QgSmall = QgCfg<2, 2, 2, 2, 64, 2>;
 
 struct QgArgs {
     const int8_t *A;
@@ -62,10 +79,12 @@ __device__ __forceinline__ i4 load16(const int8_t *p, int64_t ld, int row, int r
     return v;
 }
 
-template <bool ALIGNED, bool OUT_F32>
-__global__ __launch_bounds__(kQgB, 2) void k_qgemm(QgArgs p) {
-    __shared__ __attribute__((aligned(16))) int8_t sa[kQgBM * kQgPitch];
-    __shared__ __attribute__((aligned(16))) int8_t sb[kQgBN * kQgPitch];
+template <class C, bool ALIGNED, bool OUT_F32>
+__global__ __launch_bounds__(C::NT, C::OCC) void k_qgemm(QgArgs p) {
+    extern __shared__ __attribute__((aligned(16))) int8_t smem[];
+    constexpr int kTM = C::TM, kTN = C::TN, kWGN = C::WGN, kBK = C::BK, kQgB = C::NT;
+    constexpr int kQgBM = C::BM, kQgBN = C::BN, kQgPitch = C::PITCH, kChunkRow = C::CHUNK_ROW;
+    constexpr int kChunks = C::CHUNKS, kStage = C::STAGE;
 
     int id = blockIdx.x;
     const int nblk = gridDim.x;
@@ -78,58 +97,70 @@ __global__ __launch_bounds__(kQgB, 2) void k_qgemm(QgArgs p) {
     const int m0 = tm * kQgBM, n0 = tn * kQgBN;
 
     const int t = threadIdx.x, lane = t & (kWave - 1), wid = t / kWave;
-    const int wm = wid >> 1, wn = wid & 1;
+    const int wm = wid / kWGN, wn = wid % kWGN;
 
-    // staging: thread t moves 16-byte chunks c = t and t + 256 of each panel (row c / 4, chunk c % 4)
-    const int r0 = t >> 2, r1 = r0 + kQgB / 4, kc = (t & 3) * 16;
-    i4 ra0, ra1, rb0, rb1;
+    // staging: thread t moves chunks c = t + i * kQgB; chunk c is row c / kChunkRow of the stacked
+    // [A rows; B rows] panel, k offset (c % kChunkRow) * 16
+    i4 reg[kChunks];
     auto gload = [&](int k0) {
-        ra0 = load16<ALIGNED>(p.A, p.lda, m0 + r0, p.M, k0 + kc, p.K);
-        ra1 = load16<ALIGNED>(p.A, p.lda, m0 + r1, p.M, k0 + kc, p.K);
-        rb0 = load16<ALIGNED>(p.B, p.ldb, n0 + r0, p.N, k0 + kc, p.K);
-        rb1 = load16<ALIGNED>(p.B, p.ldb, n0 + r1, p.N, k0 + kc, p.K);
+#pragma unroll
+        for (int i = 0; i < kChunks; i++) {
+            const int c = t + i * kQgB, row = c / kChunkRow, kc = (c % kChunkRow) * 16;
+            reg[i] = row < kQgBM ? load16<ALIGNED>(p.A, p.lda, m0 + row, p.M, k0 + kc, p.K)
+                                 : load16<ALIGNED>(p.B, p.ldb, n0 + row - kQgBM, p.N, k0 + kc, p.K);
+        }
+    };
+    auto sstore = [&](int8_t *stage) {
+#pragma unroll
+        for (int i = 0; i < kChunks; i++) {
+            const int c = t + i * kQgB, row = c / kChunkRow, kc = (c % kChunkRow) * 16;
+            *(i4 *)(stage + row * kQgPitch + kc) = reg[i];
+        }
     };
 
-    i16v acc[2][2];
+    i16v acc[kTM][kTN];
 #pragma unroll
-    for (int i = 0; i < 2; i++)
+    for (int i = 0; i < kTM; i++)
 #pragma unroll
-        for (int j = 0; j < 2; j++) acc[i][j] = i16v{};
+        for (int j = 0; j < kTN; j++) acc[i][j] = i16v{};
 
     const int frow = lane & 31, fk = (lane >> 5) * 16;
-    gload(0);
-    for (int k0 = 0; k0 < p.K; k0 += kQgBK) {
-        *(i4 *)(sa + r0 * kQgPitch + kc) = ra0;
-        *(i4 *)(sa + r1 * kQgPitch + kc) = ra1;
-        *(i4 *)(sb + r0 * kQgPitch + kc) = rb0;
-        *(i4 *)(sb + r1 * kQgPitch + kc) = rb1;
+    const int nk = (p.K + kBK - 1) / kBK;
+    if (nk > 0) {
+        gload(0);
+        sstore(smem);
         __syncthreads();
-        if (k0 + kQgBK < p.K) gload(k0 + kQgBK);
+    }
+    for (int kt = 0; kt < nk; kt++) {
+        const int8_t *cur = smem + (kt & 1) * kStage;
+        if (kt + 1 < nk) gload((kt + 1) * kBK);
 #pragma unroll
-        for (int s = 0; s < kQgBK / 32; s++) {
-            i4 fa[2], fb[2];
+        for (int s = 0; s < kBK / 32; s++) {
+            i4 fa[kTM], fb[kTN];
 #pragma unroll
-            for (int i = 0; i < 2; i++)
-                fa[i] = *(const i4 *)(sa + (wm * 64 + i * 32 + frow) * kQgPitch + s * 32 + fk);
+            for (int i = 0; i < kTM; i++)
+                fa[i] = *(const i4 *)(cur + ((wm * kTM + i) * 32 + frow) * kQgPitch + s * 32 + fk);
 #pragma unroll
-            for (int j = 0; j < 2; j++)
-                fb[j] = *(const i4 *)(sb + (wn * 64 + j * 32 + frow) * kQgPitch + s * 32 + fk);
+            for (int j = 0; j < kTN; j++)
+                fb[j] = *(const i4 *)(cur + (kQgBM + (wn * kTN + j) * 32 + frow) * kQgPitch + s * 32 + fk);
 #pragma unroll
-            for (int i = 0; i < 2; i++)
+            for (int i = 0; i < kTM; i++)
 #pragma unroll
-                for (int j = 0; j < 2; j++)
+                for (int j = 0; j < kTN; j++)
                     acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fa[i], fb[j], acc[i][j], 0, 0, 0);
         }
+        // the other stage was last read before the previous barrier, so it can be refilled now
+        if (kt + 1 < nk) sstore(smem + ((kt + 1) & 1) * kStage);
         __syncthreads();
     }
 
     // accumulator layout of a 32 x 32 MFMA tile: lane l, element v holds row 8*(v/4) + 4*(l/32) + v%4,
     // column l % 32
 #pragma unroll
-    for (int i = 0; i < 2; i++) {
+    for (int i = 0; i < kTM; i++) {
 #pragma unroll
-        for (int j = 0; j < 2; j++) {
-            const int n = n0 + wn * 64 + j * 32 + (lane & 31);
+        for (int j = 0; j < kTN; j++) {
+            const int n = n0 + (wn * kTN + j) * 32 + (lane & 31);
             if (n >= p.N) continue;
             float wsn = 0.0f, bn = 0.0f;
             if (OUT_F32) {
@@ -138,7 +169,7 @@ __global__ __launch_bounds__(kQgB, 2) void k_qgemm(QgArgs p) {
             }
 #pragma unroll
             for (int v = 0; v < 16; v++) {
-                const int m = m0 + wm * 64 + i * 32 + 8 * (v >> 2) + 4 * (lane >> 5) + (v & 3);
+                const int m = m0 + (wm * kTM + i) * 32 + 8 * (v >> 2) + 4 * (lane >> 5) + (v & 3);
                 if (m >= p.M) continue;
                 if (OUT_F32)
                     p.Y[(int64_t)m * p.ldc + n] = (float)acc[i][j][v] * p.xs[m] * wsn + bn;
@@ -149,18 +180,40 @@ __global__ __launch_bounds__(kQgB, 2) void k_qgemm(QgArgs p) {
     }
 }
 
-static int launch_qgemm(QgArgs p, bool out_f32, hipStream_t st, const char *what) {
-    p.tiles_m = (p.M + kQgBM - 1) / kQgBM;
-    p.tiles_n = (p.N + kQgBN - 1) / kQgBN;
+template <class C>
+static void qgemm_lds_attr() {
+    // dynamic LDS above 64 KiB has to be allowed per kernel, once per device
+    static bool done[64] = {};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64 || done[dev]) return;
+    const int lds = (int)C::LDS;
+    (void)hipFuncSetAttribute((const void *)k_qgemm<C, true, true>, hipFuncAttributeMaxDynamicSharedMemorySize, lds);
+    (void)hipFuncSetAttribute((const void *)k_qgemm<C, true, false>, hipFuncAttributeMaxDynamicSharedMemorySize, lds);
+    (void)hipFuncSetAttribute((const void *)k_qgemm<C, false, true>, hipFuncAttributeMaxDynamicSharedMemorySize, lds);
+    (void)hipFuncSetAttribute((const void *)k_qgemm<C, false, false>, hipFuncAttributeMaxDynamicSharedMemorySize, lds);
+    done[dev] = true;
+}
+
+template <class C>
+static int launch_qgemm_cfg(QgArgs p, bool out_f32, hipStream_t st, const char *what) {
+    p.tiles_m = (p.M + C::BM - 1) / C::BM;
+    p.tiles_n = (p.N + C::BN - 1) / C::BN;
     const int64_t blocks = (int64_t)p.tiles_m * p.tiles_n;
     if (blocks > INT32_MAX) return set_error(NC_HIP_ERR_ARG, "%s: %lld tiles exceed one launch", what, (long long)blocks);
     const bool aligned = p.K % 16 == 0 && p.lda % 16 == 0 && p.ldb % 16 == 0 && aligned16(p.A) && aligned16(p.B);
-    const dim3 grid((unsigned)blocks), block(kQgB);
-    if (aligned && out_f32) hipLaunchKernelGGL((k_qgemm<true, true>), grid, block, 0, st, p);
-    else if (aligned) hipLaunchKernelGGL((k_qgemm<true, false>), grid, block, 0, st, p);
-    else if (out_f32) hipLaunchKernelGGL((k_qgemm<false, true>), grid, block, 0, st, p);
-    else hipLaunchKernelGGL((k_qgemm<false, false>), grid, block, 0, st, p);
+    const dim3 grid((unsigned)blocks), block(C::NT);
+    qgemm_lds_attr<C>();
+    if (aligned && out_f32) hipLaunchKernelGGL((k_qgemm<C, true, true>), grid, block, C::LDS, st, p);
+    else if (aligned) hipLaunchKernelGGL((k_qgemm<C, true, false>), grid, block, C::LDS, st, p);
+    else if (out_f32) hipLaunchKernelGGL((k_qgemm<C, false, true>), grid, block, C::LDS, st, p);
+    else hipLaunchKernelGGL((k_qgemm<C, false, false>), grid, block, C::LDS, st, p);
     return check_launch(what);
+}
+
+static int launch_qgemm(QgArgs p, bool out_f32, hipStream_t st, const char *what) {
+    const int64_t big_tiles = (int64_t)((p.M + QgBig::BM - 1) / QgBig::BM) * ((p.N + QgBig::BN - 1) / QgBig::BN);
+    if (big_tiles >= num_cus()) return launch_qgemm_cfg<QgBig>(p, out_f32, st, what);
+    return launch_qgemm_cfg<QgSmall>(p, out_f32, st, what);
 }
 
 static bool fits_int(int64_t v) { return v >= 0 && v <= INT32_MAX; }
