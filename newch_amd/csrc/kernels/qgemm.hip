@@ -15,7 +15,8 @@
 // 0-31 with k 0-15, lanes 32-63 the same rows with k 16-31) for A and for B alike, so whatever order
 // the instruction sums a lane's bytes in, A and B pair the same k.  Large problems run 256 x 256
 // tiles (8 waves of 4 x 2 MFMA tiles, BK 128, 147 KiB of LDS), smaller ones 128 x 128 (4 waves of
-// 2 x 2, BK 64).
+// 2 x 2, BK 64).  Large problems with K a multiple of 64 and 16-byte aligned rows take k_qgemm_dma
+// instead: the same tile, its panels loaded straight into LDS three k steps ahead.
 // Blocks are remapped so each XCD (blocks b with b % 8 equal) works a contiguous run of tiles, and
 // tiles run in groups of 8 tile-rows so neighbouring blocks share panels in L2.
 //
@@ -180,6 +181,153 @@ __global__ __launch_bounds__(C::NT, C::OCC) void k_qgemm(QgArgs p) {
     }
 }
 
+// ------------------------------------------------------------------------------------------------
+// Deep-prefetch variant for large aligned problems (K a multiple of 64, 16-byte aligned rows): the
+// same 256 x 256 tile and 8 waves of 4 x 2 MFMA tiles, but the A and B panels go straight from global
+// memory into LDS (global_load_lds_dwordx4: lane i's 16 bytes land at M0 + 16 i) three k steps ahead,
+// through four 32 KiB stages.  No staging registers and no LDS write instructions; one barrier per k
+// step.  Rows are 64 bytes without padding; logical 16-byte chunk c of row r sits at chunk
+// c ^ ((r >> 2) & 3), so the fragment reads of 16 consecutive rows hit distinct banks and every load
+// instruction still fills 1 KiB of consecutive LDS (16 rows).  Rows past M or N load row M-1 / N-1
+// (in bounds; those accumulators are never stored).  The loads are issued from inline assembly so
+// the compiler does not wait for them before every LDS read; the waits are explicit vmcnt counts.
+constexpr int kDmaBK = 64, kDmaRows = 256, kDmaNT = 512;
+constexpr int kDmaStage = 2 * kDmaRows * kDmaBK;  // A rows, then B rows
+constexpr size_t kDmaLds = 4 * (size_t)kDmaStage;
+
+__device__ __forceinline__ int dma_swz(int row, int c) { return (c ^ ((row >> 2) & 3)) * 16; }
+
+// M0 holds the wave's LDS destination; one wait state separates its write from the load.  The
+// compiler treats M0 as reserved and does not honour the clobber: the kernels using this were checked
+// in their compiled code to touch M0 nowhere else.
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+__device__ __forceinline__ void dma16(const void *g, uint32_t lds) {
+    asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off" ::"s"(lds), "v"(g) : "memory", "m0");
+}
+#pragma clang diagnostic pop
+
+template <bool OUT_F32>
+__global__ __launch_bounds__(kDmaNT, 1) void k_qgemm_dma(QgArgs p) {
+    extern __shared__ __attribute__((aligned(16))) int8_t smem[];
+    constexpr int kTM = 4, kTN = 2, kWGN = 4;
+    constexpr int kLoads = 32 / (kDmaNT / kWave);  // 1 KiB load instructions per wave per k step (32 per stage)
+
+    int id = blockIdx.x;
+    const int nblk = gridDim.x;
+    if ((nblk & 7) == 0) id = (id & 7) * (nblk >> 3) + (id >> 3);
+    const int per_group = kQgGroupM * p.tiles_n;
+    const int first_m = (id / per_group) * kQgGroupM;
+    const int gsize = min(p.tiles_m - first_m, kQgGroupM);
+    const int tm = first_m + (id % per_group) % gsize;
+    const int tn = (id % per_group) / gsize;
+    const int m0 = tm * kDmaRows, n0 = tn * kDmaRows;
+
+    const int t = threadIdx.x, lane = t & (kWave - 1), wid = t / kWave;
+    const int wm = wid / kWGN, wn = wid % kWGN;
+
+    // the stage holds 32 blocks of 16 rows (A rows 0-255, then B rows 0-255); wave wid loads blocks
+    // wid * kLoads .. wid * kLoads + kLoads - 1
+    const int8_t *src[kLoads];
+    uint32_t loff[kLoads];
+#pragma unroll
+    for (int q = 0; q < kLoads; q++) {
+        const int blk = wid * kLoads + q, panel = blk >> 4, r16 = (blk & 15) * 16, row = r16 + (lane >> 2);
+        const int c = (lane & 3) ^ ((row >> 2) & 3);
+        const int64_t grow = panel == 0 ? min(m0 + row, p.M - 1) : min(n0 + row, p.N - 1);
+        src[q] = (panel == 0 ? p.A + grow * p.lda : p.B + grow * p.ldb) + c * 16;
+        loff[q] = (uint32_t)(panel * kDmaRows * kDmaBK + r16 * kDmaBK);
+    }
+    const uint32_t sbase = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) int8_t *)smem;
+    auto issue = [&](int kt) {
+        const uint32_t st = sbase + (uint32_t)(kt & 3) * kDmaStage;
+#pragma unroll
+        for (int q = 0; q < kLoads; q++)
+            dma16(src[q] + (int64_t)kt * kDmaBK, __builtin_amdgcn_readfirstlane(st + loff[q]));
+    };
+
+    i16v acc[kTM][kTN];
+#pragma unroll
+    for (int i = 0; i < kTM; i++)
+#pragma unroll
+        for (int j = 0; j < kTN; j++) acc[i][j] = i16v{};
+
+    const int nk = p.K / kDmaBK;
+    for (int kt = 0; kt < 3 && kt < nk; kt++) issue(kt);
+    const int frow = lane & 31, fhalf = lane >> 5;
+    for (int kt = 0; kt < nk; kt++) {
+        // this wave's loads of step kt are done once at most 4 per later step in flight remain
+        const int ahead = min(nk - 1 - kt, 2);
+        if (ahead == 2) asm volatile("s_waitcnt vmcnt(%0)" ::"n"(2 * kLoads) : "memory");
+        else if (ahead == 1) asm volatile("s_waitcnt vmcnt(%0)" ::"n"(kLoads) : "memory");
+        else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        __builtin_amdgcn_s_barrier();  // every wave's loads of step kt have landed; step kt-1's reads are done
+        asm volatile("" ::: "memory");
+        if (kt + 3 < nk) issue(kt + 3);  // into the stage step kt-1 used
+        const int8_t *cur = smem + (kt & 3) * kDmaStage;
+#pragma unroll
+        for (int s = 0; s < kDmaBK / 32; s++) {
+            const int c = s * 2 + fhalf;
+            i4 fa[kTM], fb[kTN];
+#pragma unroll
+            for (int i = 0; i < kTM; i++) {
+                const int r = (wm * kTM + i) * 32 + frow;
+                fa[i] = *(const i4 *)(cur + r * kDmaBK + dma_swz(r, c));
+            }
+#pragma unroll
+            for (int j = 0; j < kTN; j++) {
+                const int r = (wn * kTN + j) * 32 + frow;
+                fb[j] = *(const i4 *)(cur + kDmaRows * kDmaBK + r * kDmaBK + dma_swz(r, c));
+            }
+#pragma unroll
+            for (int i = 0; i < kTM; i++)
+#pragma unroll
+                for (int j = 0; j < kTN; j++)
+                    acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fa[i], fb[j], acc[i][j], 0, 0, 0);
+        }
+    }
+
+#pragma unroll
+    for (int i = 0; i < kTM; i++) {
+#pragma unroll
+        for (int j = 0; j < kTN; j++) {
+            const int n = n0 + (wn * kTN + j) * 32 + (lane & 31);
+            if (n >= p.N) continue;
+            float wsn = 0.0f, bn = 0.0f;
+            if (OUT_F32) {
+                wsn = p.ws[n];
+                bn = p.bias ? p.bias[n] : 0.0f;
+            }
+#pragma unroll
+            for (int v = 0; v < 16; v++) {
+                const int m = m0 + (wm * kTM + i) * 32 + 8 * (v >> 2) + 4 * (lane >> 5) + (v & 3);
+                if (m >= p.M) continue;
+                if (OUT_F32)
+                    p.Y[(int64_t)m * p.ldc + n] = (float)acc[i][j][v] * p.xs[m] * wsn + bn;
+                else
+                    p.C[(int64_t)m * p.ldc + n] = acc[i][j][v];
+            }
+        }
+    }
+}
+
+static int launch_qgemm_dma(QgArgs p, bool out_f32, hipStream_t st, const char *what) {
+    p.tiles_m = (p.M + kDmaRows - 1) / kDmaRows;
+    p.tiles_n = (p.N + kDmaRows - 1) / kDmaRows;
+    const int64_t blocks = (int64_t)p.tiles_m * p.tiles_n;
+    if (blocks > INT32_MAX) return set_error(NC_HIP_ERR_ARG, "%s: %lld tiles exceed one launch", what, (long long)blocks);
+    static bool done[64] = {};
+    int dev = 0;
+    if (hipGetDevice(&dev) == hipSuccess && dev >= 0 && dev < 64 && !done[dev]) {
+        (void)hipFuncSetAttribute((const void *)k_qgemm_dma<true>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)kDmaLds);
+        (void)hipFuncSetAttribute((const void *)k_qgemm_dma<false>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)kDmaLds);
+        done[dev] = true;
+    }
+    if (out_f32) hipLaunchKernelGGL(k_qgemm_dma<true>, dim3((unsigned)blocks), dim3(kDmaNT), kDmaLds, st, p);
+    else hipLaunchKernelGGL(k_qgemm_dma<false>, dim3((unsigned)blocks), dim3(kDmaNT), kDmaLds, st, p);
+    return check_launch(what);
+}
+
 template <class C>
 static void qgemm_lds_attr() {
     // dynamic LDS above 64 KiB has to be allowed per kernel, once per device
@@ -212,6 +360,9 @@ static int launch_qgemm_cfg(QgArgs p, bool out_f32, hipStream_t st, const char *
 
 static int launch_qgemm(QgArgs p, bool out_f32, hipStream_t st, const char *what) {
     const int64_t big_tiles = (int64_t)((p.M + QgBig::BM - 1) / QgBig::BM) * ((p.N + QgBig::BN - 1) / QgBig::BN);
+    const bool dma_ok = p.K > 0 && p.K % kDmaBK == 0 && p.lda % 16 == 0 && p.ldb % 16 == 0 && aligned16(p.A) &&
+                        aligned16(p.B);
+    if (big_tiles >= num_cus() && dma_ok) return launch_qgemm_dma(p, out_f32, st, what);
     if (big_tiles >= num_cus()) return launch_qgemm_cfg<QgBig>(p, out_f32, st, what);
     return launch_qgemm_cfg<QgSmall>(p, out_f32, st, what);
 }

@@ -1282,7 +1282,10 @@ def test_engine_linear_int8_errors(eng):
 
 
 S8_SIZES = [(1, 1, 16), (5, 6, 37), (128, 128, 64), (300, 260, 1040), (257, 129, 1000), (33, 517, 80), (7, 3, 0),
-            (2048, 1024, 4096)]
+            (2048, 1024, 4096),
+            # >= 256 tiles of 256 x 256: the deep-prefetch kernel (K % 64 == 0; partial edge tiles) and,
+            # with K % 64 != 0, the register-staged 256 x 256 kernel
+            (4100, 4000, 512), (4096, 4352, 1040)]
 
 
 def _rows_sample(M, n=48, seed=0):
