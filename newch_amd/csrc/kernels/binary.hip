@@ -87,19 +87,23 @@ struct VecModes {
 #ifndef NC_BIN_NT_STORE
 #define NC_BIN_NT_STORE 1
 #endif
+#ifndef NC_BIN_BLOCK
+#define NC_BIN_BLOCK 256
+#endif
 constexpr int kBU = NC_BIN_UNROLL;
+constexpr int kBF = NC_BIN_BLOCK;  // forward workgroup size
 
 template <int OP, bool VEC>
-__global__ __launch_bounds__(kB) void k_binary_fwd(const float *__restrict__ a, const float *__restrict__ b,
-                                                   float *__restrict__ o, IdxMap<3> m, VecModes vm, uint32_t nwork) {
-    const uint64_t step = (uint64_t)gridDim.x * kB * kBU;
-    for (uint64_t base = (uint64_t)blockIdx.x * kB * kBU + threadIdx.x; base < nwork; base += step) {
+__global__ __launch_bounds__(kBF) void k_binary_fwd(const float *__restrict__ a, const float *__restrict__ b,
+                                                    float *__restrict__ o, IdxMap<3> m, VecModes vm, uint32_t nwork) {
+    const uint64_t step = (uint64_t)gridDim.x * kBF * kBU;
+    for (uint64_t base = (uint64_t)blockIdx.x * kBF * kBU + threadIdx.x; base < nwork; base += step) {
         if constexpr (VEC) {
             f4 x[kBU], y[kBU];
             int64_t oo[kBU];
 #pragma unroll
             for (int u = 0; u < kBU; u++) {
-                const uint64_t w = base + (uint64_t)u * kB;
+                const uint64_t w = base + (uint64_t)u * kBF;
                 if (w < nwork) {
                     int64_t off[3];
                     offsets<3>(m, (uint32_t)w, off);
@@ -110,7 +114,7 @@ __global__ __launch_bounds__(kB) void k_binary_fwd(const float *__restrict__ a, 
             }
 #pragma unroll
             for (int u = 0; u < kBU; u++) {
-                const uint64_t w = base + (uint64_t)u * kB;
+                const uint64_t w = base + (uint64_t)u * kBF;
                 if (w < nwork) {
                     f4 r;
                     r.x = bin<OP>(x[u].x, y[u].x);
@@ -126,7 +130,7 @@ __global__ __launch_bounds__(kB) void k_binary_fwd(const float *__restrict__ a, 
             int64_t oo[kBU];
 #pragma unroll
             for (int u = 0; u < kBU; u++) {
-                const uint64_t w = base + (uint64_t)u * kB;
+                const uint64_t w = base + (uint64_t)u * kBF;
                 if (w < nwork) {
                     int64_t off[3];
                     offsets<3>(m, (uint32_t)w, off);
@@ -137,7 +141,7 @@ __global__ __launch_bounds__(kB) void k_binary_fwd(const float *__restrict__ a, 
             }
 #pragma unroll
             for (int u = 0; u < kBU; u++) {
-                const uint64_t w = base + (uint64_t)u * kB;
+                const uint64_t w = base + (uint64_t)u * kBF;
                 if (w < nwork) o[oo[u]] = bin<OP>(x[u], y[u]);
             }
         }
@@ -219,7 +223,7 @@ static int launch_fwd(const float *a, const float *b, float *o, const Prepared &
         q.shape[0] = 1;
         q.st[0][0] = q.st[1][0] = q.st[2][0] = 0;
         make_map<3>(q, 1, m);
-        hipLaunchKernelGGL((k_binary_fwd<OP, false>), dim3(1), dim3(kB), 0, st, a, b, o, m, VecModes{}, 1u);
+        hipLaunchKernelGGL((k_binary_fwd<OP, false>), dim3(1), dim3(kBF), 0, st, a, b, o, m, VecModes{}, 1u);
         return check_launch("nc_hip_binary_fwd");
     }
     const int inner = p.nd - 1;
@@ -236,12 +240,12 @@ static int launch_fwd(const float *a, const float *b, float *o, const Prepared &
     }
     IdxMap<3> m;
     make_map<3>(p, unit, m);
-    const unsigned grid = stream_grid((nwork + kBU - 1) / kBU, kB, NC_BIN_GRID_PER_CU);
+    const unsigned grid = stream_grid((nwork + kBU - 1) / kBU, kBF, NC_BIN_GRID_PER_CU);
     if (vec) {
         VecModes vm{ma, mb, p.st[0][inner], p.st[1][inner]};
-        hipLaunchKernelGGL((k_binary_fwd<OP, true>), dim3(grid), dim3(kB), 0, st, a, b, o, m, vm, (uint32_t)nwork);
+        hipLaunchKernelGGL((k_binary_fwd<OP, true>), dim3(grid), dim3(kBF), 0, st, a, b, o, m, vm, (uint32_t)nwork);
     } else {
-        hipLaunchKernelGGL((k_binary_fwd<OP, false>), dim3(grid), dim3(kB), 0, st, a, b, o, m, VecModes{},
+        hipLaunchKernelGGL((k_binary_fwd<OP, false>), dim3(grid), dim3(kBF), 0, st, a, b, o, m, VecModes{},
                            (uint32_t)nwork);
     }
     return check_launch("nc_hip_binary_fwd");
@@ -559,6 +563,7 @@ constexpr int kB2 = 512;
 constexpr int kB2Waves = kB2 / kWave;
 constexpr int kB2MaxBand = 16;  // bands per plane: planes up to 16 * 512 * NC_B2_TMAX float4
 constexpr int kB2GroupDoubles = kB2Waves * 4 * 64;
+constexpr int kB2ResGroups = 16;  // groups of grad_a held in LDS between stores
 
 struct Bwd2Plan {
     uint32_t P, H, W4, T, nband;
@@ -574,7 +579,8 @@ __global__ __launch_bounds__(kB2, 4) void k_bcast_bwd2(const float *__restrict__
                                                     double *__restrict__ ga_part, double *__restrict__ gb_part,
                                                     Bwd2Plan pl, double alpha_b) {
     constexpr uint32_t band4 = kB2 * T;  // float4 per band
-    __shared__ double sh[kB2GroupDoubles];  // [NB][8 waves][W4][4]
+    __shared__ double sh[2][kB2GroupDoubles];  // two group slot sets, each [NB][8 waves][W4][4]
+    __shared__ double res[kB2ResGroups * 4 * 64];  // grad_a of the last kB2ResGroups groups, [plane][W]
     const int tid = threadIdx.x, lane = tid & (kWave - 1), wv = tid / kWave;
     const uint32_t W4 = pl.W4, nband = pl.nband;
     const uint32_t NB = 64 / W4;
@@ -601,7 +607,38 @@ __global__ __launch_bounds__(kB2, 4) void k_bcast_bwd2(const float *__restrict__
 #pragma unroll
         for (int k = 0; k < T; k++) cur[k] = __builtin_nontemporal_load(gp + kB2 * k);
     }
-    for (uint32_t pg = p0; pg < p1; pg += NB) {
+    // grad_a of the nb planes of group gi: lane -> (plane j, column col, component c), the 8 wave
+    // partials added in wave order, into the group's slot of res
+    const uint32_t WE = 4 * W4;  // grad_a elements per plane
+    auto flush = [&](uint32_t gi, uint32_t nb) {
+        const double *set = sh[gi & 1];
+        double *dst = res + (gi % kB2ResGroups) * NB * WE;
+        for (uint32_t idx = tid; idx < WE * nb; idx += kB2) {
+            const uint32_t c = idx % 4, col = (idx / 4) % W4, j = idx / WE;
+            double t = 0.0;
+#pragma unroll
+            for (int w = 0; w < kB2Waves; w++) t += set[((j * kB2Waves + w) * W4 + col) * 4 + c];
+            dst[j * WE + 4 * col + c] = t;
+        }
+    };
+    // res -> grad_a (one band) or this band's fp64 partials, for the np planes from `first` (the
+    // first plane of a res-aligned run of groups).  Stores are few and bunched: a store waits in the
+    // same in-order counter as the plane loads, so each one issued inside the plane loop would make
+    // the next wait for data wait for it too.
+    auto drain = [&](uint32_t first, uint32_t np) {
+        for (uint32_t idx = tid; idx < WE * np; idx += kB2) {
+            const uint32_t pl_ = first + idx / WE, e = idx % WE;
+            const double t = res[idx];
+            if (nband == 1) {
+                const size_t ge = (size_t)pl_ * WE + e;
+                ga[ge] = (float)((ACC ? (double)ga[ge] : 0.0) + t);
+            } else {
+                ga_part[((size_t)pl_ * nband + band) * WE + e] = t;
+            }
+        }
+    };
+    uint32_t gi = 0;
+    for (uint32_t pg = p0; pg < p1; pg += NB, gi++) {
         const uint32_t nb = min(NB, p1 - pg);
         for (uint32_t j = 0; j < nb; j++) {
             const uint32_t p = pg + j;
@@ -611,6 +648,16 @@ __global__ __launch_bounds__(kB2, 4) void k_bcast_bwd2(const float *__restrict__
                 const f4 *gn = (const f4 *)g + (size_t)min(p + 1, p1 - 1) * plane4 + qb;
 #pragma unroll
                 for (int k = 0; k < T; k++) nxt[k] = __builtin_nontemporal_load(gn + kB2 * k);
+            }
+            if constexpr (WA) {
+                if (j == 0 && gi > 0) {
+                    lds_barrier();  // every wave has written the previous group's slots
+                    flush(gi - 1, NB);
+                    if (gi % kB2ResGroups == 0) {  // res holds groups gi - kB2ResGroups .. gi - 1
+                        lds_barrier();
+                        drain(pg - kB2ResGroups * NB, kB2ResGroups * NB);
+                    }
+                }
             }
             f4 av = f4{0.f, 0.f, 0.f, 0.f};
             if constexpr (WB && (MODE == 1 || MODE == 3)) {
@@ -656,26 +703,20 @@ __global__ __launch_bounds__(kB2, 4) void k_bcast_bwd2(const float *__restrict__
                 for (int c = 0; c < 4; c++) sa[c] += __shfl_xor(sa[c], (int)o, kWave);
             }
             if ((uint32_t)lane < W4) {
-                double *d = sh + ((j * kB2Waves + wv) * W4 + lane) * 4;
+                double *d = sh[gi & 1] + ((j * kB2Waves + wv) * W4 + lane) * 4;
 #pragma unroll
                 for (int c = 0; c < 4; c++) d[c] = sa[c];
             }
         }
-        if constexpr (!WA) continue;
+    }
+    if constexpr (WA) {
+        // the last group and the rest of res.  Slot sets and res slots are rewritten only after a
+        // barrier that every wave reaches after it has finished reading them.
         lds_barrier();
-        {
-            // lane -> (plane j, column col, component c) of the group; the 8 waves added in order
-            const uint32_t c = tid % 4, col = (tid / 4) % W4, j = tid / (4 * W4);
-            if (j < nb) {
-                double t = 0.0;
-#pragma unroll
-                for (int w = 0; w < kB2Waves; w++) t += sh[((j * kB2Waves + w) * W4 + col) * 4 + c];
-                const size_t e = (size_t)(pg + j) * (4 * W4) + 4 * col + c;  // grad_a element
-                if (nband == 1) ga[e] = (float)((ACC ? (double)ga[e] : 0.0) + t);
-                else ga_part[(size_t)(pg + j) * nband * 4 * W4 + band * 4 * W4 + 4 * col + c] = t;
-            }
-        }
+        const uint32_t last = gi - 1, first = p0 + (last / kB2ResGroups) * kB2ResGroups * NB;
+        flush(last, p1 - (p0 + last * NB));
         lds_barrier();
+        drain(first, p1 - first);
     }
     if constexpr (WB) {
         double *out = gb_part + (size_t)range * plane4 * 4;

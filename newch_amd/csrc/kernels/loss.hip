@@ -131,20 +131,30 @@ __global__ __launch_bounds__(kLB) void k_loss_finish(const double *__restrict__ 
 
 // gi (+)= s * prob; gi[i, lab_i] -= s, s = gout / N.  A lane owns float4 items (four consecutive
 // floats of a row), kCeU of them loaded before any is stored.
-constexpr int kCeU = 4;
+#ifndef NC_CEB_UNROLL
+#define NC_CEB_UNROLL 1
+#endif
+#ifndef NC_CEB_BLOCK
+#define NC_CEB_BLOCK 64
+#endif
+#ifndef NC_CEB_GRID_PER_CU
+#define NC_CEB_GRID_PER_CU 65536
+#endif
+constexpr int kCeU = NC_CEB_UNROLL;
+constexpr int kCeB = NC_CEB_BLOCK;
 template <bool ACC>
-__global__ __launch_bounds__(kLB) void k_ce_bwd4(const f4 *__restrict__ prob, const int32_t *__restrict__ lab,
+__global__ __launch_bounds__(kCeB) void k_ce_bwd4(const f4 *__restrict__ prob, const int32_t *__restrict__ lab,
                                                  const float *__restrict__ gout, f4 *__restrict__ gi, int64_t N,
                                                  uint32_t n4, IntDiv row4) {
     const float s = gout[0] / (float)(N ? N : 1);
     const uint32_t per_row = row4.d;
-    const uint64_t step = (uint64_t)gridDim.x * kLB * kCeU;
-    for (uint64_t base = (uint64_t)blockIdx.x * kLB * kCeU + threadIdx.x; base < n4; base += step) {
+    const uint64_t step = (uint64_t)gridDim.x * kCeB * kCeU;
+    for (uint64_t base = (uint64_t)blockIdx.x * kCeB * kCeU + threadIdx.x; base < n4; base += step) {
         f4 p[kCeU], o[kCeU];
         int32_t rel[kCeU];  // label column relative to the item's first column
 #pragma unroll
         for (int u = 0; u < kCeU; u++) {
-            const uint64_t e = base + (uint64_t)u * kLB;
+            const uint64_t e = base + (uint64_t)u * kCeB;
             if (e < n4) {
                 const uint32_t r = row4.div((uint32_t)e);
                 rel[u] = lab[r] - 4 * (int32_t)((uint32_t)e - r * per_row);
@@ -154,7 +164,7 @@ __global__ __launch_bounds__(kLB) void k_ce_bwd4(const f4 *__restrict__ prob, co
         }
 #pragma unroll
         for (int u = 0; u < kCeU; u++) {
-            const uint64_t e = base + (uint64_t)u * kLB;
+            const uint64_t e = base + (uint64_t)u * kCeB;
             if (e < n4) {
                 f4 v = o[u];
                 v.x = v.x + s * p[u].x;
@@ -200,8 +210,11 @@ static int vpl_for_row(int64_t C) {
     return nv <= 64 ? 1 : nv <= 128 ? 2 : nv <= 256 ? 4 : nv <= 512 ? 8 : nv <= 1024 ? 16 : 0;
 }
 
+#ifndef NC_CE_GRID_PER_CU
+#define NC_CE_GRID_PER_CU 16
+#endif
 static unsigned ce_grid(int64_t N) {
-    const int64_t blocks = (N + kLWaves - 1) / kLWaves, cap = (int64_t)num_cus() * 16;
+    const int64_t blocks = (N + kLWaves - 1) / kLWaves, cap = (int64_t)num_cus() * NC_CE_GRID_PER_CU;
     return (unsigned)std::max<int64_t>(1, std::min(blocks, cap));
 }
 
@@ -271,12 +284,12 @@ extern "C" NC_HIP_API int nc_hip_cross_entropy_bwd(int64_t N, int64_t C, const f
     hipStream_t st = as_stream(stream);
     if (C % 4 == 0 && aligned16(prob) && aligned16(gi) && n / 4 < (int64_t)UINT32_MAX) {
         const uint32_t n4 = (uint32_t)(n / 4);
-        const unsigned grid = stream_grid((n4 + kCeU - 1) / kCeU, kLB);
+        const unsigned grid = stream_grid((n4 + kCeU - 1) / kCeU, kCeB, NC_CEB_GRID_PER_CU);
         const IntDiv row4((uint32_t)(C / 4));
         if (accumulate)
-            hipLaunchKernelGGL(k_ce_bwd4<true>, grid, kLB, 0, st, (const f4 *)prob, lab, gout, (f4 *)gi, N, n4, row4);
+            hipLaunchKernelGGL(k_ce_bwd4<true>, grid, kCeB, 0, st, (const f4 *)prob, lab, gout, (f4 *)gi, N, n4, row4);
         else
-            hipLaunchKernelGGL(k_ce_bwd4<false>, grid, kLB, 0, st, (const f4 *)prob, lab, gout, (f4 *)gi, N, n4, row4);
+            hipLaunchKernelGGL(k_ce_bwd4<false>, grid, kCeB, 0, st, (const f4 *)prob, lab, gout, (f4 *)gi, N, n4, row4);
     } else {
         const unsigned grid = stream_grid(n, kLB);
         if (accumulate) hipLaunchKernelGGL(k_ce_bwd1<true>, grid, kLB, 0, st, prob, lab, gout, gi, N, C);

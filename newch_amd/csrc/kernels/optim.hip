@@ -18,8 +18,17 @@
 
 namespace nchip {
 
-constexpr int kOB = 256;
-constexpr int kOU = 4;
+#ifndef NC_OPT_BLOCK
+#define NC_OPT_BLOCK 64
+#endif
+#ifndef NC_OPT_UNROLL
+#define NC_OPT_UNROLL 1
+#endif
+#ifndef NC_OPT_GRID_PER_CU
+#define NC_OPT_GRID_PER_CU 65536
+#endif
+constexpr int kOB = NC_OPT_BLOCK;
+constexpr int kOU = NC_OPT_UNROLL;
 
 struct OptArgs {
     float lr, momentum, wd, b1, b2, eps, gs, bc1, bc2;
@@ -108,7 +117,7 @@ static void launch_opt(float *w, const float *g, float *s1, float *s2, int64_t n
     const bool vec = aligned16(w) && aligned16(g) && (!S1 || aligned16(s1)) && (!S2 || aligned16(s2));
     const int64_t n4 = vec ? n / 4 : 0;
     if (n4 > 0)
-        hipLaunchKernelGGL((k_optim4<KIND, S1, S2>), dim3(stream_grid((n4 + kOU - 1) / kOU, kOB)), dim3(kOB), 0, st,
+        hipLaunchKernelGGL((k_optim4<KIND, S1, S2>), dim3(stream_grid((n4 + kOU - 1) / kOU, kOB, NC_OPT_GRID_PER_CU)), dim3(kOB), 0, st,
                            (f4 *)w, (const f4 *)g, (f4 *)s1, (f4 *)s2, n4, a);
     const int64_t done = n4 * 4;
     if (done < n)
@@ -116,39 +125,42 @@ static void launch_opt(float *w, const float *g, float *s1, float *s2, int64_t n
                            g + done, S1 ? s1 + done : nullptr, S2 ? s2 + done : nullptr, n - done, a);
 }
 
+constexpr int kSB = 256;  // sum of squares: workgroup size
+constexpr int kSU = 4;    // float4 items per lane in flight (and fp64 accumulators per lane)
+
 // sum of squares: fp64 per thread, workgroup partials in wave order, then an ordered combine
 __device__ __forceinline__ double block_sum_waves(double v) {
-    __shared__ double sh[kOB / kWave];
+    __shared__ double sh[kSB / kWave];
     v = wave_sum(v);
     if ((threadIdx.x & (kWave - 1)) == 0) sh[threadIdx.x / kWave] = v;
     __syncthreads();
     double t = 0.0;
     if (threadIdx.x == 0)
-        for (int i = 0; i < kOB / kWave; i++) t += sh[i];
+        for (int i = 0; i < kSB / kWave; i++) t += sh[i];
     return t;
 }
 
-// float4 items (kOU per lane in flight) into four fp64 accumulators per lane, one per item slot,
+// float4 items (kSU per lane in flight) into four fp64 accumulators per lane, one per item slot,
 // added in slot order at the end; the scalar tail (n % 4, or an unaligned x) goes to slot 0
-__global__ __launch_bounds__(kOB) void k_sumsq(const float *__restrict__ x, int64_t n, int64_t n4,
+__global__ __launch_bounds__(kSB) void k_sumsq(const float *__restrict__ x, int64_t n, int64_t n4,
                                                double *__restrict__ part) {
-    double acc[kOU] = {0.0, 0.0, 0.0, 0.0};
+    double acc[kSU] = {0.0, 0.0, 0.0, 0.0};
     const f4 *x4 = (const f4 *)x;
-    const int64_t step = (int64_t)gridDim.x * kOB * kOU;
-    for (int64_t base = (int64_t)blockIdx.x * kOB * kOU + threadIdx.x; base < n4; base += step) {
-        f4 v[kOU];
+    const int64_t step = (int64_t)gridDim.x * kSB * kSU;
+    for (int64_t base = (int64_t)blockIdx.x * kSB * kSU + threadIdx.x; base < n4; base += step) {
+        f4 v[kSU];
 #pragma unroll
-        for (int u = 0; u < kOU; u++)
-            if (base + (int64_t)u * kOB < n4) v[u] = __builtin_nontemporal_load(x4 + base + (int64_t)u * kOB);
+        for (int u = 0; u < kSU; u++)
+            if (base + (int64_t)u * kSB < n4) v[u] = __builtin_nontemporal_load(x4 + base + (int64_t)u * kSB);
 #pragma unroll
-        for (int u = 0; u < kOU; u++) {
-            if (base + (int64_t)u * kOB < n4) {
+        for (int u = 0; u < kSU; u++) {
+            if (base + (int64_t)u * kSB < n4) {
                 const double a = v[u].x, b = v[u].y, c = v[u].z, d = v[u].w;
                 acc[u] += (a * a + b * b) + (c * c + d * d);
             }
         }
     }
-    for (int64_t e = n4 * 4 + (int64_t)blockIdx.x * kOB + threadIdx.x; e < n; e += (int64_t)gridDim.x * kOB) {
+    for (int64_t e = n4 * 4 + (int64_t)blockIdx.x * kSB + threadIdx.x; e < n; e += (int64_t)gridDim.x * kSB) {
         const double v = (double)x[e];
         acc[0] += v * v;
     }
@@ -156,16 +168,16 @@ __global__ __launch_bounds__(kOB) void k_sumsq(const float *__restrict__ x, int6
     if (threadIdx.x == 0) part[blockIdx.x] = t;
 }
 
-__global__ __launch_bounds__(kOB) void k_sumsq_finish(const double *__restrict__ part, int nparts, double *ss,
+__global__ __launch_bounds__(kSB) void k_sumsq_finish(const double *__restrict__ part, int nparts, double *ss,
                                                       int accumulate) {
     double t = 0.0;
-    for (int i = threadIdx.x; i < nparts; i += kOB) t += part[i];
+    for (int i = threadIdx.x; i < nparts; i += kSB) t += part[i];
     const double s = block_sum_waves(t);
     if (threadIdx.x == 0) *ss = (accumulate ? *ss : 0.0) + s;
 }
 
 static unsigned sumsq_grid(int64_t n) {
-    const int64_t blocks = (n + 4 * kOB * kOU - 1) / (4 * kOB * kOU), cap = (int64_t)num_cus() * 8;
+    const int64_t blocks = (n + 4 * kSB * kSU - 1) / (4 * kSB * kSU), cap = (int64_t)num_cus() * 8;
     return (unsigned)std::max<int64_t>(1, std::min(blocks, cap));
 }
 
@@ -231,9 +243,9 @@ extern "C" NC_HIP_API int nc_hip_sumsq(int64_t n, const float *x, double *ss, in
                              nc_hip_sumsq_workspace(n));
         const unsigned grid = sumsq_grid(n);
         const int64_t n4 = aligned16(x) ? n / 4 : 0;  // float4 items; the rest one float per lane
-        hipLaunchKernelGGL(k_sumsq, grid, kOB, 0, st, x, n, n4, (double *)ws);
+        hipLaunchKernelGGL(k_sumsq, grid, kSB, 0, st, x, n, n4, (double *)ws);
         nparts = (int)grid;
     }
-    hipLaunchKernelGGL(k_sumsq_finish, 1, kOB, 0, st, (const double *)ws, nparts, ss, accumulate ? 1 : 0);
+    hipLaunchKernelGGL(k_sumsq_finish, 1, kSB, 0, st, (const double *)ws, nparts, ss, accumulate ? 1 : 0);
     return check_launch("nc_hip_sumsq");
 }

@@ -89,20 +89,30 @@ __global__ __launch_bounds__(kQB) void k_quant_blk(const float *__restrict__ w, 
 // Lane-contiguous dequantization: lane j reads 4 int8 as one 32-bit word and writes one 128-bit
 // float vector, so a wave reads 256 contiguous bytes and writes 1 KiB contiguous; U words in
 // flight per lane.  Requires cols % 4 == 0, q 4-byte and w 16-byte aligned, rows * cols / 4 < 2^32.
-constexpr int kDqU = 4;
-__global__ __launch_bounds__(kQB) void k_dequant4(const uint32_t *__restrict__ q, const float *__restrict__ scale,
+#ifndef NC_DQ_UNROLL
+#define NC_DQ_UNROLL 2
+#endif
+#ifndef NC_DQ_BLOCK
+#define NC_DQ_BLOCK 128
+#endif
+#ifndef NC_DQ_GRID_PER_CU
+#define NC_DQ_GRID_PER_CU 65536
+#endif
+constexpr int kDqU = NC_DQ_UNROLL;
+constexpr int kDqB = NC_DQ_BLOCK;
+__global__ __launch_bounds__(kDqB) void k_dequant4(const uint32_t *__restrict__ q, const float *__restrict__ scale,
                                                   f4 *__restrict__ w, uint32_t n4, IntDiv per_row4) {
-    const uint64_t step = (uint64_t)gridDim.x * kQB * kDqU;
-    for (uint64_t base = (uint64_t)blockIdx.x * kQB * kDqU + threadIdx.x; base < n4; base += step) {
+    const uint64_t step = (uint64_t)gridDim.x * kDqB * kDqU;
+    for (uint64_t base = (uint64_t)blockIdx.x * kDqB * kDqU + threadIdx.x; base < n4; base += step) {
         uint32_t v[kDqU];
 #pragma unroll
         for (int u = 0; u < kDqU; u++) {
-            const uint64_t j = base + (uint64_t)u * kQB;
+            const uint64_t j = base + (uint64_t)u * kDqB;
             if (j < n4) v[u] = __builtin_nontemporal_load(q + j);
         }
 #pragma unroll
         for (int u = 0; u < kDqU; u++) {
-            const uint64_t j = base + (uint64_t)u * kQB;
+            const uint64_t j = base + (uint64_t)u * kDqB;
             if (j < n4) {
                 const float s = scale[per_row4.div((uint32_t)j)];
                 const uint32_t x = v[u];
@@ -165,7 +175,7 @@ extern "C" NC_HIP_API int nc_hip_dequantize_rows(int64_t rows, int64_t cols, con
     hipStream_t st = as_stream(stream);
     if (cols % 4 == 0 && ((uintptr_t)q & 3u) == 0 && aligned16(w) && n / 4 < (int64_t)UINT32_MAX) {
         const int64_t n4 = n / 4;
-        hipLaunchKernelGGL(k_dequant4, stream_grid((n4 + kDqU - 1) / kDqU, kQB, 16), kQB, 0, st, (const uint32_t *)q,
+        hipLaunchKernelGGL(k_dequant4, stream_grid((n4 + kDqU - 1) / kDqU, kDqB, NC_DQ_GRID_PER_CU), kDqB, 0, st, (const uint32_t *)q,
                            scale, (f4 *)w, (uint32_t)n4, IntDiv((uint32_t)(cols / 4)));
     } else {
         hipLaunchKernelGGL(k_dequant1, stream_grid(n, kQB, 16), kQB, 0, st, q, scale, w, n, cols);

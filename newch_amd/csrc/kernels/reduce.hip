@@ -15,6 +15,10 @@
 
 #include <float.h>
 
+#ifndef NC_RED_ROWS_GRID_PER_CU
+#define NC_RED_ROWS_GRID_PER_CU 65536
+#endif
+
 namespace nchip {
 
 constexpr int kRB = 256;
@@ -335,7 +339,8 @@ static int launch(int64_t outer, int64_t R, int64_t inner, const float *x, float
         const bool vec = R % 4 == 0 && aligned16(x);
         const int64_t waves = outer;
         const int64_t blocks64 = (waves + (kRB / kWave) - 1) / (kRB / kWave);
-        const unsigned grid = (unsigned)(blocks64 < num_cus() * 32 ? blocks64 : num_cus() * 32);
+        const int64_t cap = (int64_t)num_cus() * NC_RED_ROWS_GRID_PER_CU;
+        const unsigned grid = (unsigned)(blocks64 < cap ? blocks64 : cap);
         if (vec)
             hipLaunchKernelGGL((k_rows_wave<KIND, true>), grid, kRB, 0, st, x, y, arg, outer, R, scale);
         else

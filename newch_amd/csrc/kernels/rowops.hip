@@ -608,9 +608,12 @@ static int vpl_for(int64_t C) {
     return 0;
 }
 
+#ifndef NC_ROWS_GRID_PER_CU
+#define NC_ROWS_GRID_PER_CU 65536
+#endif
 static unsigned rows_grid(int64_t rows) {
     const int64_t blocks = (rows + kWavesPerBlock - 1) / kWavesPerBlock;
-    const int64_t cap = (int64_t)num_cus() * 16;
+    const int64_t cap = (int64_t)num_cus() * NC_ROWS_GRID_PER_CU;
     return (unsigned)(blocks < cap ? blocks : cap);
 }
 
