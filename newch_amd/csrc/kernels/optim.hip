@@ -176,8 +176,11 @@ __global__ __launch_bounds__(kSB) void k_sumsq_finish(const double *__restrict__
     if (threadIdx.x == 0) *ss = (accumulate ? *ss : 0.0) + s;
 }
 
+#ifndef NC_SUMSQ_GRID_PER_CU
+#define NC_SUMSQ_GRID_PER_CU 8
+#endif
 static unsigned sumsq_grid(int64_t n) {
-    const int64_t blocks = (n + 4 * kSB * kSU - 1) / (4 * kSB * kSU), cap = (int64_t)num_cus() * 8;
+    const int64_t blocks = (n + 4 * kSB * kSU - 1) / (4 * kSB * kSU), cap = (int64_t)num_cus() * NC_SUMSQ_GRID_PER_CU;
     return (unsigned)std::max<int64_t>(1, std::min(blocks, cap));
 }
 

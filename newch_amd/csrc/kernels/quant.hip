@@ -14,6 +14,10 @@
 #include "common.hpp"
 #include "intdiv.hpp"
 
+#ifndef NC_QUANT_GRID_PER_CU
+#define NC_QUANT_GRID_PER_CU 16
+#endif
+
 namespace nchip {
 
 constexpr int kQB = 256;
@@ -151,7 +155,8 @@ extern "C" NC_HIP_API int nc_hip_quantize_rows(int64_t rows, int64_t cols, const
     int vpl = 0;
     if (cols % 4 == 0 && al) vpl = nv <= 64 ? 1 : nv <= 128 ? 2 : nv <= 256 ? 4 : nv <= 512 ? 8 : nv <= 1024 ? 16 : nv <= 2048 ? 32 : 0;
     const int64_t blocks = (rows + (kQB / kWave) - 1) / (kQB / kWave);
-    const unsigned grid = (unsigned)(blocks < num_cus() * 16 ? blocks : num_cus() * 16);
+    const int64_t cap = (int64_t)num_cus() * NC_QUANT_GRID_PER_CU;
+    const unsigned grid = (unsigned)(blocks < cap ? blocks : cap);
     switch (vpl) {
     case 1: hipLaunchKernelGGL(k_quant_reg<1>, grid, kQB, 0, st, w, q, scale, rows, (int)cols); break;
     case 2: hipLaunchKernelGGL(k_quant_reg<2>, grid, kQB, 0, st, w, q, scale, rows, (int)cols); break;

@@ -517,6 +517,128 @@ __global__ __launch_bounds__(kLnB, VPL <= 4 ? 4 : 2) void k_ln_bwd_reg(const flo
     }
 }
 
+// Backward for full rows (D = 256 VPL floats, VPL <= 4) that write gx: the same arithmetic and
+// column partials as k_ln_bwd_reg, with the rows streamed through two register bundles (x, g and
+// the old gx of a row) in turn: the loads of row r + 8 are issued, then row r is reduced and
+// stored, then row r + 16 is loaded into the first bundle and row r + 8 reduced.  Every load in the
+// steady-state loop is unconditional, so the compiler's in-order memory-counter waits for a row's
+// bundle never cover the other bundle's loads (a single prefetch buffer copied forward at the end
+// of each row makes it wait for the prefetched row before moving on).
+template <int VPL, bool ACC>
+__global__ __launch_bounds__(kLnB, 2) void k_ln_bwd_pp(const float *__restrict__ x, const float *__restrict__ w,
+                                                      const float *__restrict__ stats, const float *__restrict__ g,
+                                                      float *__restrict__ gx, double *__restrict__ part,
+                                                      int64_t rows, int D, int64_t rows_per_block) {
+    extern __shared__ char ln_lds[];
+    __shared__ f4 wsh[VPL * kWave];
+    constexpr int nv = VPL * kWave;
+    const int lane = threadIdx.x & (kWave - 1);
+    const int wv = threadIdx.x / kWave;
+    const int64_t r0 = (int64_t)blockIdx.x * rows_per_block;
+    const int64_t r1 = min(rows, r0 + rows_per_block);
+    const bool cols = part != nullptr;
+    if (w) {
+        for (int j = threadIdx.x; j < nv; j += kLnB) wsh[j] = ((const f4 *)w)[j];
+        __syncthreads();
+    }
+    f4 *accw = (f4 *)ln_lds + (size_t)wv * 2 * nv, *accb = accw + nv;
+    if (cols) {
+#pragma unroll
+        for (int k = 0; k < VPL; k++) accw[lane + k * kWave] = accb[lane + k * kWave] = f4{0.f, 0.f, 0.f, 0.f};
+    }
+    struct Bundle {
+        f4 x[VPL], g[VPL], o[VPL];
+        f2 st;  // mean, rstd
+    };
+    auto load = [&](int64_t r, Bundle &b) {
+        const f4 *xr = (const f4 *)(x + r * D), *gr = (const f4 *)(g + r * D), *orow = (const f4 *)(gx + r * D);
+#pragma unroll
+        for (int k = 0; k < VPL; k++) {
+            const int j = lane + k * kWave;
+            b.x[k] = __builtin_nontemporal_load(xr + j);
+            b.g[k] = __builtin_nontemporal_load(gr + j);
+            if (ACC) b.o[k] = __builtin_nontemporal_load(orow + j);
+        }
+        b.st = *(const f2 *)(stats + 2 * r);  // with the row: a later load would be waited for with the other bundle
+    };
+    auto process = [&](int64_t r, const Bundle &b) {
+        const float mean = b.st.x, rstd = b.st.y;
+        auto terms = [&](int k, f4 &xh, f4 &gw) {
+            const f4 ww = w ? wsh[lane + k * kWave] : f4{1.f, 1.f, 1.f, 1.f};
+            xh.x = (b.x[k].x - mean) * rstd;
+            xh.y = (b.x[k].y - mean) * rstd;
+            xh.z = (b.x[k].z - mean) * rstd;
+            xh.w = (b.x[k].w - mean) * rstd;
+            gw.x = w ? b.g[k].x * ww.x : b.g[k].x;
+            gw.y = w ? b.g[k].y * ww.y : b.g[k].y;
+            gw.z = w ? b.g[k].z * ww.z : b.g[k].z;
+            gw.w = w ? b.g[k].w * ww.w : b.g[k].w;
+        };
+        double sg = 0.0, sgx = 0.0;
+#pragma unroll
+        for (int k = 0; k < VPL; k++) {
+            const int j = lane + k * kWave;
+            f4 xh, gw4;
+            terms(k, xh, gw4);
+            sg += ((double)gw4.x + (double)gw4.y) + ((double)gw4.z + (double)gw4.w);
+            sgx += ((double)(gw4.x * xh.x) + (double)(gw4.y * xh.y)) + ((double)(gw4.z * xh.z) + (double)(gw4.w * xh.w));
+            if (cols) {
+                f4 t = accw[j], u = accb[j];
+                t.x += b.g[k].x * xh.x;
+                t.y += b.g[k].y * xh.y;
+                t.z += b.g[k].z * xh.z;
+                t.w += b.g[k].w * xh.w;
+                u += b.g[k];
+                accw[j] = t;
+                accb[j] = u;
+            }
+        }
+        sg = wave_sum(sg);
+        sgx = wave_sum(sgx);
+        const float mg = (float)(sg / (double)D), mgx = (float)(sgx / (double)D);
+        f4 *dx = (f4 *)(gx + r * D);
+#pragma unroll
+        for (int k = 0; k < VPL; k++) {
+            f4 xh, gw4;
+            terms(k, xh, gw4);
+            f4 o = ACC ? b.o[k] : f4{0.f, 0.f, 0.f, 0.f};
+            o.x = o.x + rstd * ((gw4.x - mg) - xh.x * mgx);
+            o.y = o.y + rstd * ((gw4.y - mg) - xh.y * mgx);
+            o.z = o.z + rstd * ((gw4.z - mg) - xh.z * mgx);
+            o.w = o.w + rstd * ((gw4.w - mg) - xh.w * mgx);
+            __builtin_nontemporal_store(o, dx + lane + k * kWave);
+        }
+    };
+    int64_t r = r0 + wv;
+    Bundle A, B;
+    if (r < r1) load(r, A);
+    // steady state: rows r and r + 8 exist, and row r + 16 too for the next first bundle
+    while (r + 2 * kLnWaves < r1) {
+        load(r + kLnWaves, B);
+        process(r, A);
+        load(r + 2 * kLnWaves, A);
+        process(r + kLnWaves, B);
+        r += 2 * kLnWaves;
+    }
+    if (r < r1) {
+        const bool hb = r + kLnWaves < r1;
+        if (hb) load(r + kLnWaves, B);
+        process(r, A);
+        if (hb) process(r + kLnWaves, B);
+    }
+    if (!cols) return;
+    // column i of [gw | gb]: the 8 wave slices added in wave order
+    __syncthreads();
+    double *out = part + (size_t)blockIdx.x * 2 * D;
+    const float *acc = (const float *)ln_lds;
+    for (int i = threadIdx.x; i < 2 * D; i += kLnB) {
+        double t = 0.0;
+#pragma unroll
+        for (int w8 = 0; w8 < kLnWaves; w8++) t += (double)acc[(size_t)w8 * 2 * D + i];
+        out[i] = t;
+    }
+}
+
 // Generic backward: one workgroup per row for gx, and column partials for gw/gb.
 template <bool ACC>
 __global__ __launch_bounds__(kRowB) void k_ln_bwd_blk(const float *__restrict__ x, const float *__restrict__ w,
@@ -608,6 +730,9 @@ static int vpl_for(int64_t C) {
     return 0;
 }
 
+#ifndef NC_LN_BWD_BLOCKS_PER_CU
+#define NC_LN_BWD_BLOCKS_PER_CU 2
+#endif
 #ifndef NC_ROWS_GRID_PER_CU
 #define NC_ROWS_GRID_PER_CU 65536
 #endif
@@ -624,6 +749,13 @@ static unsigned rows_grid(int64_t rows) {
     case 4: { constexpr int VP = 4; CALL; } break;  \
     case 8: { constexpr int VP = 8; CALL; } break;  \
     default: { constexpr int VP = 16; CALL; } break; \
+    }
+
+#define NC_VPL_SWITCH4(V, CALL)                     \
+    switch (V) {                                    \
+    case 1: { constexpr int VP = 1; CALL; } break;  \
+    case 2: { constexpr int VP = 2; CALL; } break;  \
+    default: { constexpr int VP = 4; CALL; } break; \
     }
 
 #define NC_VPL_SWITCH8(V, CALL)                     \
@@ -650,7 +782,7 @@ static LnPlan ln_plan(int64_t rows, int64_t D, bool aligned) {
     if (p.vpl > 8) p.vpl = 0;  // rows beyond 2048 floats would spill registers: generic path
     p.reg = p.vpl != 0;
     if (p.reg) {
-        int64_t want = (int64_t)num_cus() * (p.vpl <= 4 ? 2 : 1);  // the resident workgroups
+        int64_t want = (int64_t)num_cus() * (p.vpl <= 4 ? NC_LN_BWD_BLOCKS_PER_CU : 1);  // the resident workgroups
         int64_t rpb = (rows + want - 1) / want;
         if (rpb < kLnWaves) rpb = kLnWaves;
         p.rows_per_block = rpb;
@@ -748,7 +880,12 @@ extern "C" NC_HIP_API int nc_hip_layer_norm_bwd(int64_t rows, int64_t D, const f
     if (p.reg) {
         const size_t lds = ln_bwd_lds(p.vpl, D, cols);
         if (lds > 65536) return set_error(NC_HIP_ERR_ARG, "nc_hip_layer_norm_bwd: D too large for LDS combine");
-        if (accumulate)
+        const bool full = gx && p.vpl <= 4 && D == (int64_t)p.vpl * 4 * kWave;
+        if (full && accumulate)
+            NC_VPL_SWITCH4(p.vpl, hipLaunchKernelGGL((k_ln_bwd_pp<VP, true>), dim3(p.blocks), kLnB, lds, st, x, w, stats, g, gx, part, rows, (int)D, p.rows_per_block))
+        else if (full)
+            NC_VPL_SWITCH4(p.vpl, hipLaunchKernelGGL((k_ln_bwd_pp<VP, false>), dim3(p.blocks), kLnB, lds, st, x, w, stats, g, gx, part, rows, (int)D, p.rows_per_block))
+        else if (accumulate)
             NC_VPL_SWITCH8(p.vpl, hipLaunchKernelGGL((k_ln_bwd_reg<VP, true>), dim3(p.blocks), kLnB, lds, st, x, w, stats, g, gx, part, rows, (int)D, p.rows_per_block))
         else
             NC_VPL_SWITCH8(p.vpl, hipLaunchKernelGGL((k_ln_bwd_reg<VP, false>), dim3(p.blocks), kLnB, lds, st, x, w, stats, g, gx, part, rows, (int)D, p.rows_per_block))
