@@ -541,11 +541,11 @@ __global__ __launch_bounds__(kLnB, 2) void k_ln_bwd_pp(const float *__restrict__
         for (int j = threadIdx.x; j < nv; j += kLnB) wsh[j] = ((const f4 *)w)[j];
         __syncthreads();
     }
-    f4 *accw = (f4 *)ln_lds + (size_t)wv * 2 * nv, *accb = accw + nv;
-    if (cols) {
+    // column partials of this wave's rows, fp32 in row order, in registers (the LDS slice layout of
+    // k_ln_bwd_reg is filled once at the end, so the sums are the same)
+    f4 aw[VPL], ab[VPL];
 #pragma unroll
-        for (int k = 0; k < VPL; k++) accw[lane + k * kWave] = accb[lane + k * kWave] = f4{0.f, 0.f, 0.f, 0.f};
-    }
+    for (int k = 0; k < VPL; k++) aw[k] = ab[k] = f4{0.f, 0.f, 0.f, 0.f};
     struct Bundle {
         f4 x[VPL], g[VPL], o[VPL];
         f2 st;  // mean, rstd
@@ -577,20 +577,16 @@ __global__ __launch_bounds__(kLnB, 2) void k_ln_bwd_pp(const float *__restrict__
         double sg = 0.0, sgx = 0.0;
 #pragma unroll
         for (int k = 0; k < VPL; k++) {
-            const int j = lane + k * kWave;
             f4 xh, gw4;
             terms(k, xh, gw4);
             sg += ((double)gw4.x + (double)gw4.y) + ((double)gw4.z + (double)gw4.w);
             sgx += ((double)(gw4.x * xh.x) + (double)(gw4.y * xh.y)) + ((double)(gw4.z * xh.z) + (double)(gw4.w * xh.w));
             if (cols) {
-                f4 t = accw[j], u = accb[j];
-                t.x += b.g[k].x * xh.x;
-                t.y += b.g[k].y * xh.y;
-                t.z += b.g[k].z * xh.z;
-                t.w += b.g[k].w * xh.w;
-                u += b.g[k];
-                accw[j] = t;
-                accb[j] = u;
+                aw[k].x += b.g[k].x * xh.x;
+                aw[k].y += b.g[k].y * xh.y;
+                aw[k].z += b.g[k].z * xh.z;
+                aw[k].w += b.g[k].w * xh.w;
+                ab[k] += b.g[k];
             }
         }
         sg = wave_sum(sg);
@@ -628,6 +624,12 @@ __global__ __launch_bounds__(kLnB, 2) void k_ln_bwd_pp(const float *__restrict__
     }
     if (!cols) return;
     // column i of [gw | gb]: the 8 wave slices added in wave order
+    f4 *accw = (f4 *)ln_lds + (size_t)wv * 2 * nv, *accb = accw + nv;
+#pragma unroll
+    for (int k = 0; k < VPL; k++) {
+        accw[lane + k * kWave] = aw[k];
+        accb[lane + k * kWave] = ab[k];
+    }
     __syncthreads();
     double *out = part + (size_t)blockIdx.x * 2 * D;
     const float *acc = (const float *)ln_lds;
