@@ -1,15 +1,20 @@
 // fp32 GEMM entry points (the reference's gemm_f32 kernel-table entry, kernels.h:36-41): dense GEMMs
-// on the matrix cores through rocBLAS, row-major interface.
+// on the matrix cores through hipBLASLt (rocBLAS for the cases it does not take), row-major interface.
 //
 // Row-major C (M x N) = op(A) op(B) is column-major C^T = op(B)^T op(A)^T, so the operands are passed
-// to rocBLAS swapped, each with its own transpose flag.  One rocBLAS handle per device, created on
-// first use, atomics disabled so results do not depend on scheduling (deterministic), host pointer
-// mode for alpha / beta.
+// to the library swapped, each with its own transpose flag.  hipBLASLt runs with no workspace (no
+// split-k partial buffers; the same inputs give the same bits run after run) and its first heuristic
+// choice, planned once per shape and cached; measured on MI355X it reaches 148-154 TFLOP/s on
+// [8192,4096] x [4096,4096] and ~100 on 64 x [1024,128] x [128,1024], where rocBLAS ran 134-139 and
+// 46.  rocBLAS (one handle per device, atomics off, host pointer mode) covers K = 0, unaligned
+// operands, broadcast batch strides and pointer-array batches.
 #include "common.hpp"
 
+#include <hipblaslt/hipblaslt.h>
 #include <rocblas/rocblas.h>
 
 #include <mutex>
+#include <unordered_map>
 
 namespace nchip {
 
@@ -35,6 +40,102 @@ static int blas_error(rocblas_status s, const char *what) {
 
 static rocblas_operation op_of(int t) { return t ? rocblas_operation_transpose : rocblas_operation_none; }
 
+// ---- hipBLASLt plans ----------------------------------------------------------------------------
+struct LtKey {
+    int dev, ta, tb;
+    int64_t M, N, K, lda, ldb, ldc, count, sa, sb, sc;
+    bool operator==(const LtKey &o) const {
+        return dev == o.dev && ta == o.ta && tb == o.tb && M == o.M && N == o.N && K == o.K && lda == o.lda &&
+               ldb == o.ldb && ldc == o.ldc && count == o.count && sa == o.sa && sb == o.sb && sc == o.sc;
+    }
+};
+struct LtKeyHash {
+    size_t operator()(const LtKey &k) const {
+        const int64_t v[] = {k.dev, k.ta, k.tb, k.M, k.N, k.K, k.lda, k.ldb, k.ldc, k.count, k.sa, k.sb, k.sc};
+        size_t h = 1469598103934665603ull;
+        for (int64_t x : v) h = (h ^ (size_t)x) * 1099511628211ull;
+        return h;
+    }
+};
+struct LtPlan {
+    bool ok = false;
+    hipblasLtMatmulDesc_t desc{};
+    hipblasLtMatrixLayout_t la{}, lb{}, lc{};
+    hipblasLtMatmulAlgo_t algo{};
+};
+
+static std::mutex lt_mu;
+static hipblasLtHandle_t lt_handles[64];
+static std::unordered_map<LtKey, LtPlan, LtKeyHash> lt_plans;
+
+// The plan for a key (created on first use; ok == false when hipBLASLt offers no algorithm).
+static const LtPlan *lt_plan(const LtKey &k) {
+    std::lock_guard<std::mutex> lock(lt_mu);
+    auto it = lt_plans.find(k);
+    if (it != lt_plans.end()) return &it->second;
+    LtPlan &p = lt_plans[k];
+    if (!lt_handles[k.dev] && hipblasLtCreate(&lt_handles[k.dev]) != HIPBLAS_STATUS_SUCCESS) {
+        lt_handles[k.dev] = nullptr;
+        return &p;
+    }
+    hipblasLtHandle_t h = lt_handles[k.dev];
+    // column-major D (N x M) = op(B) (N x K) op(A) (K x M)
+    const hipblasOperation_t oa = k.tb ? HIPBLAS_OP_T : HIPBLAS_OP_N, ob = k.ta ? HIPBLAS_OP_T : HIPBLAS_OP_N;
+    bool ok = hipblasLtMatmulDescCreate(&p.desc, HIPBLAS_COMPUTE_32F, HIP_R_32F) == HIPBLAS_STATUS_SUCCESS;
+    ok = ok && hipblasLtMatmulDescSetAttribute(p.desc, HIPBLASLT_MATMUL_DESC_TRANSA, &oa, sizeof oa) == HIPBLAS_STATUS_SUCCESS;
+    ok = ok && hipblasLtMatmulDescSetAttribute(p.desc, HIPBLASLT_MATMUL_DESC_TRANSB, &ob, sizeof ob) == HIPBLAS_STATUS_SUCCESS;
+    ok = ok && hipblasLtMatrixLayoutCreate(&p.la, HIP_R_32F, k.tb ? k.K : k.N, k.tb ? k.N : k.K, k.ldb) == HIPBLAS_STATUS_SUCCESS;
+    ok = ok && hipblasLtMatrixLayoutCreate(&p.lb, HIP_R_32F, k.ta ? k.M : k.K, k.ta ? k.K : k.M, k.lda) == HIPBLAS_STATUS_SUCCESS;
+    ok = ok && hipblasLtMatrixLayoutCreate(&p.lc, HIP_R_32F, k.N, k.M, k.ldc) == HIPBLAS_STATUS_SUCCESS;
+    if (ok && k.count > 1) {
+        const int32_t cnt = (int32_t)k.count;
+        const int64_t st[3] = {k.sb, k.sa, k.sc};
+        hipblasLtMatrixLayout_t ls[3] = {p.la, p.lb, p.lc};
+        for (int i = 0; i < 3 && ok; i++) {
+            ok = hipblasLtMatrixLayoutSetAttribute(ls[i], HIPBLASLT_MATRIX_LAYOUT_BATCH_COUNT, &cnt, sizeof cnt) ==
+                     HIPBLAS_STATUS_SUCCESS &&
+                 hipblasLtMatrixLayoutSetAttribute(ls[i], HIPBLASLT_MATRIX_LAYOUT_STRIDED_BATCH_OFFSET, &st[i],
+                                                   sizeof st[i]) == HIPBLAS_STATUS_SUCCESS;
+        }
+    }
+    hipblasLtMatmulPreference_t pref{};
+    ok = ok && hipblasLtMatmulPreferenceCreate(&pref) == HIPBLAS_STATUS_SUCCESS;
+    const uint64_t no_ws = 0;
+    ok = ok && hipblasLtMatmulPreferenceSetAttribute(pref, HIPBLASLT_MATMUL_PREF_MAX_WORKSPACE_BYTES, &no_ws,
+                                                     sizeof no_ws) == HIPBLAS_STATUS_SUCCESS;
+    hipblasLtMatmulHeuristicResult_t res{};
+    int nres = 0;
+    ok = ok && hipblasLtMatmulAlgoGetHeuristic(h, p.desc, p.la, p.lb, p.lc, p.lc, pref, 1, &res, &nres) ==
+                   HIPBLAS_STATUS_SUCCESS &&
+         nres > 0 && res.workspaceSize == 0;
+    if (pref) hipblasLtMatmulPreferenceDestroy(pref);
+    if (ok) p.algo = res.algo;
+    p.ok = ok;
+    return &p;
+}
+
+// C = alpha op(A) op(B) + beta C through hipBLASLt (count > 1: strided batch).  Returns false when
+// the case is left to rocBLAS: K = 0, a zero or negative batch stride, operands not 16-byte aligned or
+// leading dims not multiples of 4, or no algorithm.
+static bool lt_gemm(int ta, int tb, int64_t M, int64_t N, int64_t K, float alpha, const float *A, int64_t lda,
+                    const float *B, int64_t ldb, float beta, float *C, int64_t ldc, int64_t count, int64_t sa,
+                    int64_t sb, int64_t sc, hipStream_t st, int *rc) {
+    if (K == 0 || count > INT32_MAX || !aligned16(A) || !aligned16(B) || !aligned16(C) || lda % 4 || ldb % 4 || ldc % 4)
+        return false;
+    if (count > 1 && (sa <= 0 || sb <= 0 || sc <= 0 || sa % 4 || sb % 4 || sc % 4)) return false;
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return false;
+    const LtKey key{dev, ta ? 1 : 0, tb ? 1 : 0, M, N, K, lda, ldb, ldc, count, count > 1 ? sa : 0,
+                    count > 1 ? sb : 0, count > 1 ? sc : 0};
+    const LtPlan *p = lt_plan(key);
+    if (!p->ok) return false;
+    const hipblasStatus_t s = hipblasLtMatmul(lt_handles[dev], p->desc, &alpha, B, p->la, A, p->lb, &beta, C, p->lc,
+                                              C, p->lc, &p->algo, nullptr, 0, st);
+    *rc = s == HIPBLAS_STATUS_SUCCESS ? NC_HIP_OK
+                                      : set_error(NC_HIP_ERR_DEVICE, "hipBLASLt matmul failed (status %d)", (int)s);
+    return true;
+}
+
 // With K = 0 no element of A or B is read, but rocBLAS still checks their leading dims against the
 // stored shapes (row-major A: M x K, or K x M when transposed); a [M, 0] tensor has leading dim 0.
 static void k0_leading_dims(int ta, int tb, int64_t M, int64_t N, int64_t K, int64_t *lda, int64_t *ldb) {
@@ -53,6 +154,8 @@ extern "C" NC_HIP_API int nc_hip_gemm_f32(int ta, int tb, int64_t M, int64_t N, 
                                           void *stream) {
     if (M < 0 || N < 0 || K < 0) return set_error(NC_HIP_ERR_ARG, "nc_hip_gemm_f32: negative size");
     if (M == 0 || N == 0) return NC_HIP_OK;
+    int rc = NC_HIP_OK;
+    if (lt_gemm(ta, tb, M, N, K, alpha, A, lda, B, ldb, beta, C, ldc, 1, 0, 0, 0, as_stream(stream), &rc)) return rc;
     rocblas_handle h = blas_handle();
     if (!h) return set_error(NC_HIP_ERR_DEVICE, "nc_hip_gemm_f32: no rocBLAS handle");
     k0_leading_dims(ta, tb, M, N, K, &lda, &ldb);
@@ -187,6 +290,12 @@ extern "C" NC_HIP_API int nc_hip_gemm_f32_bmm(int ta, int tb, int64_t M, int64_t
         return NC_HIP_OK;
     }
     k0_leading_dims(ta, tb, M, N, K, &lda, &ldb);
+    if (bd.nb == 1) {
+        int rc = NC_HIP_OK;
+        if (lt_gemm(ta, tb, M, N, K, one, A, lda, B, ldb, beta, C, ldc, count, bd.st[0][0], bd.st[1][0], bd.st[2][0],
+                    as_stream(stream), &rc))
+            return rc;
+    }
     rocblas_handle h = blas_handle();
     if (!h) return set_error(NC_HIP_ERR_DEVICE, "nc_hip_gemm_f32_bmm: no rocBLAS handle");
     rocblas_status s = rocblas_set_stream(h, as_stream(stream));

@@ -1381,6 +1381,26 @@ def test_kernel_gemm_f32(K, ta, tb, M, N, Kd):
     assert O.gemm_excess(got[rows], want, terms, Kd + 1) <= 1.0
 
 
+def test_kernel_gemm_f32_strided_batch_aligned_and_deterministic(K):
+    """A strided batch with 16-byte aligned rows (the hipBLASLt path, B a transposed view as in
+    attention scores): within the GEMM tolerance of fp64, and bit-identical when run again."""
+    rng = np.random.default_rng(17)
+    Bc, M, N, Kd = 6, 64, 96, 128
+    A = rng.standard_normal((Bc, M, Kd)).astype(np.float32)
+    Bm = rng.standard_normal((Bc, N, Kd)).astype(np.float32)  # used transposed
+    Ad, Bd = dev(A), dev(Bm)
+    outs = []
+    for _ in range(2):
+        C = empty(4 * Bc * M * N)
+        K.gemm_f32_bmm(0, 1, M, N, Kd, Ad.ptr, Kd, Bd.ptr, Kd, 0.0, C.ptr, N, (Bc,), (M * Kd,), (N * Kd,), (M * N,))
+        sync()
+        outs.append(C.to_numpy(np.float32, (Bc, M, N)))
+    want = A.astype(np.float64) @ np.swapaxes(Bm, 1, 2).astype(np.float64)
+    terms = np.abs(A).astype(np.float64) @ np.abs(np.swapaxes(Bm, 1, 2)).astype(np.float64)
+    assert O.gemm_excess(outs[0], want, terms, Kd) <= 1.0
+    assert_bits(outs[1], outs[0], "second run")
+
+
 BMM_LAYOUTS = [
     # name, batch shape, a batch strides (in matrices), b batch strides, c batch strides
     ("strided", (6,), (1,), (1,), (1,)),
