@@ -67,6 +67,19 @@ __device__ __forceinline__ void opt1(float &w, float g, float &s1, float &s2, co
     }
 }
 
+#ifndef NC_OPT_NT
+#define NC_OPT_NT 1
+#endif
+// the parameter and state streams: plain or non-temporal accesses
+__device__ __forceinline__ f4 opt_ld(const f4 *p) {
+    if constexpr (NC_OPT_NT) return __builtin_nontemporal_load(p);
+    else return *p;
+}
+__device__ __forceinline__ void opt_st(f4 v, f4 *p) {
+    if constexpr (NC_OPT_NT) __builtin_nontemporal_store(v, p);
+    else *p = v;
+}
+
 template <int KIND, bool S1, bool S2>
 __global__ __launch_bounds__(kOB) void k_optim4(f4 *__restrict__ w, const f4 *__restrict__ g, f4 *__restrict__ s1,
                                                 f4 *__restrict__ s2, int64_t n4, OptArgs a) {
@@ -77,10 +90,10 @@ __global__ __launch_bounds__(kOB) void k_optim4(f4 *__restrict__ w, const f4 *__
         for (int u = 0; u < kOU; u++) {
             const int64_t e = base + (int64_t)u * kOB;
             if (e < n4) {
-                W[u] = w[e];
+                W[u] = opt_ld(w + e);
                 G[u] = __builtin_nontemporal_load(g + e);
-                A[u] = S1 ? s1[e] : f4{0.f, 0.f, 0.f, 0.f};
-                B[u] = S2 ? s2[e] : f4{0.f, 0.f, 0.f, 0.f};
+                A[u] = S1 ? opt_ld(s1 + e) : f4{0.f, 0.f, 0.f, 0.f};
+                B[u] = S2 ? opt_ld(s2 + e) : f4{0.f, 0.f, 0.f, 0.f};
             }
         }
 #pragma unroll
@@ -92,9 +105,9 @@ __global__ __launch_bounds__(kOB) void k_optim4(f4 *__restrict__ w, const f4 *__
                 const float gv[4] = {G[u].x, G[u].y, G[u].z, G[u].w};
 #pragma unroll
                 for (int c = 0; c < 4; c++) opt1<KIND, S1>(wv[c], gv[c], av[c], bv[c], a);
-                w[e] = f4{wv[0], wv[1], wv[2], wv[3]};
-                if (S1) s1[e] = f4{av[0], av[1], av[2], av[3]};
-                if (S2) s2[e] = f4{bv[0], bv[1], bv[2], bv[3]};
+                opt_st(f4{wv[0], wv[1], wv[2], wv[3]}, w + e);
+                if (S1) opt_st(f4{av[0], av[1], av[2], av[3]}, s1 + e);
+                if (S2) opt_st(f4{bv[0], bv[1], bv[2], bv[3]}, s2 + e);
             }
         }
     }
