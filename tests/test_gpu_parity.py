@@ -688,7 +688,7 @@ def test_kernel_layer_norm(K, rows, D):
     assert_close64(GB.to_numpy(np.float32, D), G.sum(0), np.abs(G).sum(0) / np.sqrt(rows), "layer_norm db")
 
 
-@pytest.mark.parametrize("rows,D", [(129, 512), (1031, 1024), (40, 2048), (9, 64)])
+@pytest.mark.parametrize("rows,D", [(129, 512), (1031, 1024), (40, 2048), (9, 64), (300, 256), (7, 1024), (17, 1024)])
 @pytest.mark.parametrize("mode", ["store_all", "acc_gx_only", "cols_only"])
 def test_kernel_layer_norm_bwd_modes(K, rows, D, mode):
     """Backward with a fresh (stored) gx, with gx alone accumulated onto nonzero values, and with
