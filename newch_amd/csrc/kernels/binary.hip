@@ -95,6 +95,9 @@ struct VecModes {
 #ifndef NC_BIN_BLOCK
 #define NC_BIN_BLOCK 64
 #endif
+#ifndef NC_BIN_SMALL_INDEX
+#define NC_BIN_SMALL_INDEX 1  // 32-bit index kernel where offsets allow it
+#endif
 constexpr int kBU = NC_BIN_UNROLL;
 constexpr int kBF = NC_BIN_BLOCK;  // forward workgroup size
 
@@ -148,6 +151,90 @@ __global__ __launch_bounds__(kBF) void k_binary_fwd(const float *__restrict__ a,
             for (int u = 0; u < kBU; u++) {
                 const uint64_t w = base + (uint64_t)u * kBF;
                 if (w < nwork) o[oo[u]] = bin<OP>(x[u], y[u]);
+            }
+        }
+    }
+}
+
+// 32-bit index path: fewer than 2^31 work items, at most 4 dims after coalescing, non-negative
+// strides and every operand's largest element offset below 2^31.  The multiply-high division then
+// needs no 64-bit add (quotient estimate + dividend < 2^32), the outermost index needs no division,
+// offsets are 32-bit sums, and when every size, stride and quotient fits in 24 bits the products are
+// full-rate 24-bit multiplies.  Only the uniform kernel arguments that ND dims use are passed, so the
+// decode stays in scalar registers instead of spilling them.
+template <int ND>
+struct SmallMap {
+    uint32_t size[ND];
+    uint32_t mul[ND];
+    uint32_t shift[ND];
+    uint32_t st[3][ND];  // element strides; innermost already multiplied by the unit
+};
+
+struct SmallModes {
+    int a, b;        // 0 splat, 1 vector, 2 gather
+    uint32_t ia, ib; // inner element strides (for gathers)
+};
+
+template <bool U24>
+__device__ __forceinline__ uint32_t umul(uint32_t x, uint32_t y) {
+    if constexpr (U24) return __umul24(x, y);
+    else return x * y;
+}
+
+template <int ND, bool U24>
+__device__ __forceinline__ void offsets_small(const SmallMap<ND> &m, uint32_t w, uint32_t *off) {
+    off[0] = off[1] = off[2] = 0;
+#pragma unroll
+    for (int d = ND - 1; d >= 1; d--) {
+        const uint32_t q = IntDiv::div31(w, m.mul[d], m.shift[d]);
+        const uint32_t i = w - umul<U24>(q, m.size[d]);
+        w = q;
+#pragma unroll
+        for (int o = 0; o < 3; o++) off[o] += umul<U24>(i, m.st[o][d]);
+    }
+#pragma unroll
+    for (int o = 0; o < 3; o++) off[o] += umul<U24>(w, m.st[o][0]);
+}
+
+__device__ __forceinline__ f4 load4s(const float *p, uint32_t is, int mode) {
+    if (mode == 1) return *(const f4 *)p;
+    if (mode == 0) {
+        const float v = *p;
+        return f4{v, v, v, v};
+    }
+    return f4{p[0], p[is], p[2 * is], p[3 * is]};
+}
+
+template <int OP, int ND, bool U24>
+__global__ __launch_bounds__(kBF) void k_binary_fwd_s(const float *__restrict__ a, const float *__restrict__ b,
+                                                      float *__restrict__ o, SmallMap<ND> m, SmallModes vm,
+                                                      uint32_t nwork) {
+    const uint32_t step = gridDim.x * kBF * kBU;
+    for (uint32_t base = blockIdx.x * kBF * kBU + threadIdx.x; base < nwork; base += step) {
+        f4 x[kBU], y[kBU];
+        uint32_t oo[kBU];
+#pragma unroll
+        for (int u = 0; u < kBU; u++) {
+            const uint32_t w = base + u * kBF;
+            if (w < nwork) {
+                uint32_t off[3];
+                offsets_small<ND, U24>(m, w, off);
+                x[u] = load4s(a + off[0], vm.ia, vm.a);
+                y[u] = load4s(b + off[1], vm.ib, vm.b);
+                oo[u] = off[2];
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < kBU; u++) {
+            const uint32_t w = base + u * kBF;
+            if (w < nwork) {
+                f4 r;
+                r.x = bin<OP>(x[u].x, y[u].x);
+                r.y = bin<OP>(x[u].y, y[u].y);
+                r.z = bin<OP>(x[u].z, y[u].z);
+                r.w = bin<OP>(x[u].w, y[u].w);
+                if constexpr (NC_BIN_NT_STORE) __builtin_nontemporal_store(r, (f4 *)(o + oo[u]));
+                else *(f4 *)(o + oo[u]) = r;
             }
         }
     }
@@ -246,6 +333,42 @@ static void warm_operand(const float *x, const Prepared &p, int k, hipStream_t s
     hipLaunchKernelGGL(k_touch, dim3((unsigned)((lines + 63) / 64)), dim3(64), 0, st, x, lines);
 }
 
+// 0: the 64-bit index kernel; 1: the 32-bit index kernel; 2: the same with 24-bit products
+static int small_kind(const Prepared &p, int unit, int64_t nwork) {
+    if (p.nd < 1 || p.nd > 4 || nwork >= (int64_t(1) << 31)) return 0;
+    bool u24 = true;
+    int64_t outer = 1;  // the quotient formed at dim d is below the product of the outer sizes
+    for (int d = 0; d < p.nd; d++) {
+        const int64_t sz = d == p.nd - 1 ? p.shape[d] / unit : p.shape[d];
+        if (sz >= (1 << 24) || (d > 0 && outer > (1 << 24))) u24 = false;
+        outer *= sz;
+    }
+    for (int o = 0; o < 3; o++) {
+        int64_t hi = 0;
+        for (int d = 0; d < p.nd; d++) {
+            const int64_t s = p.st[o][d];
+            if (s < 0) return 0;
+            hi += (p.shape[d] - 1) * s;
+            if ((d == p.nd - 1 ? s * unit : s) >= (1 << 24)) u24 = false;
+        }
+        if (hi >= (int64_t(1) << 31)) return 0;
+    }
+    return u24 ? 2 : 1;
+}
+
+template <int OP, int ND, bool U24>
+static void launch_small(const float *a, const float *b, float *o, const IdxMap<3> &full, SmallModes vm,
+                         uint32_t nwork, unsigned grid, hipStream_t st) {
+    SmallMap<ND> m;
+    for (int d = 0; d < ND; d++) {
+        m.size[d] = full.size[d];
+        m.mul[d] = full.div[d].m;
+        m.shift[d] = full.div[d].s;
+        for (int k = 0; k < 3; k++) m.st[k][d] = (uint32_t)full.st[k][d];
+    }
+    hipLaunchKernelGGL((k_binary_fwd_s<OP, ND, U24>), dim3(grid), dim3(kBF), 0, st, a, b, o, m, vm, nwork);
+}
+
 template <int OP>
 static int launch_fwd(const float *a, const float *b, float *o, const Prepared &p, hipStream_t st) {
     if (p.numel == 0) return NC_HIP_OK;
@@ -278,7 +401,20 @@ static int launch_fwd(const float *a, const float *b, float *o, const Prepared &
         warm_operand(b, p, 1, st);
     }
     const unsigned grid = stream_grid((nwork + kBU - 1) / kBU, kBF, NC_BIN_GRID_PER_CU);
-    if (vec) {
+    const int kind = vec && NC_BIN_SMALL_INDEX ? small_kind(p, unit, nwork) : 0;
+    if (kind) {
+        SmallModes vm{ma, mb, (uint32_t)p.st[0][inner], (uint32_t)p.st[1][inner]};
+        switch (p.nd * 2 + (kind == 2)) {
+#define NC_BIN_SMALL(ND)                                                                                        \
+    case 2 * ND: launch_small<OP, ND, false>(a, b, o, m, vm, (uint32_t)nwork, grid, st); break;                 \
+    case 2 * ND + 1: launch_small<OP, ND, true>(a, b, o, m, vm, (uint32_t)nwork, grid, st); break;
+            NC_BIN_SMALL(1)
+            NC_BIN_SMALL(2)
+            NC_BIN_SMALL(3)
+            NC_BIN_SMALL(4)
+#undef NC_BIN_SMALL
+        }
+    } else if (vec) {
         VecModes vm{ma, mb, p.st[0][inner], p.st[1][inner]};
         hipLaunchKernelGGL((k_binary_fwd<OP, true>), dim3(grid), dim3(kBF), 0, st, a, b, o, m, vm, (uint32_t)nwork);
     } else {

@@ -81,7 +81,10 @@ extern "C" NC_HIP_API uint64_t nc_hip_check_intdiv(const uint32_t *divs, int ndi
     for (int i = 0; i < ndivs; i++) {
         if (divs[i] == 0) continue;
         const nchip::IntDiv d(divs[i]);
-        for (int j = 0; j < nnums; j++) bad += d.div(nums[j]) != nums[j] / divs[i];
+        for (int j = 0; j < nnums; j++) {
+            bad += d.div(nums[j]) != nums[j] / divs[i];
+            if (nums[j] < (1u << 31) && divs[i] <= (1u << 31)) bad += d.div31(nums[j]) != nums[j] / divs[i];
+        }
     }
     return bad;
 }

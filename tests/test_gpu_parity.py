@@ -481,6 +481,40 @@ def test_kernel_binary(K, case, ash, aview, bsh, op):
             assert_close64(got, init + red, scale + np.abs(init), f"{case} {op} grad {which}")
 
 
+FWD_INDEX = [
+    # (case, a shape, a element strides (None: contiguous), b shape)
+    ("nd1_same", (64, 128), None, (64, 128)),                    # one dim after coalescing
+    ("nd2_row", (1000, 36), None, (36,)),
+    ("nd3_gather", (6, 5, 8), (1, 6, 30), (5, 8)),               # innermost stride 30
+    ("nd4", (2, 1, 3, 8), None, (1, 5, 1, 8)),
+    ("nd5_generic", (2, 1, 3, 1, 8), None, (1, 5, 1, 7, 8)),     # more dims than the 32-bit kernel
+    ("stride_2p24", (3, 64), ((1 << 24) + 4, 1), (64,)),         # stride beyond 24 bits
+    ("quotient_2p24", ((1 << 24) + 8, 4), None, (4,)),           # quotient beyond 24 bits
+]
+
+
+@pytest.mark.parametrize("case,ash,ast,bsh", FWD_INDEX)
+@pytest.mark.parametrize("op", ["add", "div"])
+def test_kernel_binary_fwd_index_paths(K, case, ash, ast, bsh, op):
+    """Broadcast forward through each index path (32-bit offsets with 24- or 32-bit products for up
+    to 4 coalesced dims, 64-bit offsets beyond): bit-exact against the oracle."""
+    rng = np.random.default_rng(zlib.crc32(f"fwdidx/{case}/{op}".encode()))
+    st = ast if ast is not None else [int(np.prod(ash[i + 1:])) for i in range(len(ash))]
+    n_store = 1 + sum((s - 1) * t for s, t in zip(ash, st))  # one past the view's largest offset
+    A = rng.standard_normal(n_store).astype(np.float32)
+    a = np.lib.stride_tricks.as_strided(A, ash, [4 * t for t in st])
+    B = (0.5 + 1.5 * rng.random(bsh)).astype(np.float32)
+    out_shape = O.broadcast_shape(a.shape, B.shape)
+    Ad, Bd = dev(A), dev(B)
+    Od = empty(4 * int(np.prod(out_shape)))
+    sa = bcast_strides(a.shape, list(st), out_shape)
+    sb = bcast_strides(B.shape, strides_of(B), out_shape)
+    so = [s // 4 for s in np.empty(out_shape, np.float32).strides]
+    K.binary_fwd(op, out_shape, Ad.ptr, sa, Bd.ptr, sb, Od.ptr, so)
+    sync()
+    assert_bits(Od.to_numpy(np.float32, out_shape), O.binary_fwd(op, a, B), f"{case} {op} fwd")
+
+
 BWD2 = [
     ("cfg2_T2", (8, 32, 1, 64), None, (1, 1, 64, 64)),
     ("cfg2_T16", (4, 5, 1, 64), None, (1, 1, 512, 64)),
