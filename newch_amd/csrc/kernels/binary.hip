@@ -17,6 +17,7 @@
 #include "common.hpp"
 #include "intdiv.hpp"
 
+#include <stdlib.h>
 #include <string.h>
 
 #include <algorithm>
@@ -736,7 +737,16 @@ constexpr int kB2 = 512;
 constexpr int kB2Waves = kB2 / kWave;
 constexpr int kB2MaxBand = 16;  // bands per plane: planes up to 16 * 512 * NC_B2_TMAX float4
 constexpr int kB2GroupDoubles = kB2Waves * 4 * 64;
-constexpr int kB2ResGroups = 16;  // groups of grad_a held in LDS between stores
+#ifndef NC_B2_RES_GROUPS
+#define NC_B2_RES_GROUPS 16
+#endif
+#ifndef NC_B2_GB_BLOCKS_PER_CU
+#define NC_B2_GB_BLOCKS_PER_CU 1
+#endif
+#ifndef NC_B2_NB_SHIFT
+#define NC_B2_NB_SHIFT 0
+#endif
+constexpr int kB2ResGroups = NC_B2_RES_GROUPS;  // groups of grad_a held in LDS between stores
 
 struct Bwd2Plan {
     uint32_t P, H, W4, T, nband;
@@ -756,7 +766,7 @@ __global__ __launch_bounds__(kB2, 4) void k_bcast_bwd2(const float *__restrict__
     __shared__ double res[kB2ResGroups * 4 * 64];  // grad_a of the last kB2ResGroups groups, [plane][W]
     const int tid = threadIdx.x, lane = tid & (kWave - 1), wv = tid / kWave;
     const uint32_t W4 = pl.W4, nband = pl.nband;
-    const uint32_t NB = 64 / W4;
+    const uint32_t NB = max(1u, (64 / W4) >> NC_B2_NB_SHIFT);
     const uint32_t w4 = tid % W4;
     const uint32_t band = blockIdx.x % nband, range = blockIdx.x / nband;
     const uint32_t plane4 = band4 * nband;
@@ -780,6 +790,15 @@ __global__ __launch_bounds__(kB2, 4) void k_bcast_bwd2(const float *__restrict__
 #pragma unroll
         for (int k = 0; k < T; k++) cur[k] = __builtin_nontemporal_load(gp + kB2 * k);
     }
+    // a[p, this lane's 4 columns] (grad_b terms of mul and div), loaded one plane ahead with g
+    constexpr bool RA = WB && (MODE == 1 || MODE == 3);
+    auto load_a = [&](uint32_t p) {
+        int64_t off[1];
+        offsets<1>(pl.amap, p, off);
+        return *(const f4 *)(a + off[0] + 4 * w4);
+    };
+    f4 av = f4{0.f, 0.f, 0.f, 0.f};
+    if constexpr (RA) av = load_a(p0);
     // grad_a of the nb planes of group gi: lane -> (plane j, column col, component c), the 8 wave
     // partials added in wave order, into the group's slot of res
     const uint32_t WE = 4 * W4;  // grad_a elements per plane
@@ -798,10 +817,12 @@ __global__ __launch_bounds__(kB2, 4) void k_bcast_bwd2(const float *__restrict__
     // first plane of a res-aligned run of groups).  Stores are few and bunched: a store waits in the
     // same in-order counter as the plane loads, so each one issued inside the plane loop would make
     // the next wait for data wait for it too.
-    auto drain = [&](uint32_t first, uint32_t np) {
+    auto drain = [&](uint32_t g0, uint32_t np) {
+        const uint32_t first = p0 + g0 * NB;
+        const double *src = res + (g0 % kB2ResGroups) * NB * WE;
         for (uint32_t idx = tid; idx < WE * np; idx += kB2) {
             const uint32_t pl_ = first + idx / WE, e = idx % WE;
-            const double t = res[idx];
+            const double t = src[idx];
             if (nband == 1) {
                 const size_t ge = (size_t)pl_ * WE + e;
                 ga[ge] = (float)((ACC ? (double)ga[ge] : 0.0) + t);
@@ -810,7 +831,7 @@ __global__ __launch_bounds__(kB2, 4) void k_bcast_bwd2(const float *__restrict__
             }
         }
     };
-    uint32_t gi = 0;
+    uint32_t gi = 0, dg = 0;  // dg: the first group not yet drained
     for (uint32_t pg = p0; pg < p1; pg += NB, gi++) {
         const uint32_t nb = min(NB, p1 - pg);
         for (uint32_t j = 0; j < nb; j++) {
@@ -822,53 +843,46 @@ __global__ __launch_bounds__(kB2, 4) void k_bcast_bwd2(const float *__restrict__
 #pragma unroll
                 for (int k = 0; k < T; k++) nxt[k] = __builtin_nontemporal_load(gn + kB2 * k);
             }
+            f4 avn = av;
+            if constexpr (RA) avn = load_a(min(p + 1, p1 - 1));
             if constexpr (WA) {
                 if (j == 0 && gi > 0) {
                     lds_barrier();  // every wave has written the previous group's slots
                     flush(gi - 1, NB);
-                    if (gi % kB2ResGroups == 0) {  // res holds groups gi - kB2ResGroups .. gi - 1
+                    if (gi % kB2ResGroups == 0) {  // res holds groups dg = gi - kB2ResGroups .. gi - 1
                         lds_barrier();
-                        drain(pg - kB2ResGroups * NB, kB2ResGroups * NB);
+                        drain(dg, (gi - dg) * NB);
+                        dg = gi;
                     }
                 }
             }
-            f4 av = f4{0.f, 0.f, 0.f, 0.f};
-            if constexpr (WB && (MODE == 1 || MODE == 3)) {
-                int64_t off[1];
-                offsets<1>(pl.amap, p, off);
-                av = *(const f4 *)(a + off[0] + 4 * w4);
-            }
-            double ta[T][4];  // grad_a terms of this lane's T float4, added as a pairwise tree
-#pragma unroll
-            for (int k = 0; k < T; k++) {
-                const float gg[4] = {cur[k].x, cur[k].y, cur[k].z, cur[k].w};
-                const float bb[4] = {bv[k].x, bv[k].y, bv[k].z, bv[k].w};
-                const float aa[4] = {av.x, av.y, av.z, av.w};
-#pragma unroll
-                for (int c = 0; c < 4; c++) {
-                    // terms are the fp32 products the unreduced gradient holds, summed in fp64
-                    // grad_a term: g (add, sub), g*b (mul), g*(1/b) (div)
-                    if constexpr (WA) ta[k][c] = (double)(MODE == 0 ? gg[c] : gg[c] * bb[c]);
-                    // grad_b term before the per-column factor: g (add, sub), g*a (mul, div)
-                    if constexpr (WB) accb[k][c] += (double)((MODE == 1 || MODE == 3) ? gg[c] * aa[c] : gg[c]);
-                }
-            }
+            // one component at a time, so that only T grad_a terms are live: terms are the fp32
+            // products the unreduced gradient holds, summed in fp64 (grad_a: g for add and sub, g*b
+            // for mul, g*(1/b) for div, added as a pairwise tree over the lane's T float4; grad_b
+            // before its per-column factor: g for add and sub, g*a for mul and div)
             double sa[4];
 #pragma unroll
             for (int c = 0; c < 4; c++) {
-                if constexpr (!WA) {
-                    sa[c] = 0.0;
-                } else {
+                double ta[T];
+#pragma unroll
+                for (int k = 0; k < T; k++) {
+                    const float gg = cur[k][c];
+                    if constexpr (WA) ta[k] = (double)(MODE == 0 ? gg : gg * bv[k][c]);
+                    if constexpr (WB) accb[k][c] += (double)((MODE == 1 || MODE == 3) ? gg * av[c] : gg);
+                }
+                sa[c] = 0.0;
+                if constexpr (WA) {
 #pragma unroll
                     for (int h = T / 2; h >= 1; h /= 2) {
 #pragma unroll
-                        for (int k = 0; k < h; k++) ta[k][c] += ta[k + h][c];
+                        for (int k = 0; k < h; k++) ta[k] += ta[k + h];
                     }
-                    sa[c] = ta[0][c];
+                    sa[c] = ta[0];
                 }
             }
 #pragma unroll
             for (int k = 0; k < T; k++) cur[k] = nxt[k];
+            av = avn;
             if constexpr (!WA) continue;
             // lanes sharing w4 inside the wave; the wave's partial goes to LDS slot (j, wv)
             for (uint32_t o = W4; o < (uint32_t)kWave; o <<= 1) {
@@ -886,10 +900,10 @@ __global__ __launch_bounds__(kB2, 4) void k_bcast_bwd2(const float *__restrict__
         // the last group and the rest of res.  Slot sets and res slots are rewritten only after a
         // barrier that every wave reaches after it has finished reading them.
         lds_barrier();
-        const uint32_t last = gi - 1, first = p0 + (last / kB2ResGroups) * kB2ResGroups * NB;
+        const uint32_t last = gi - 1;
         flush(last, p1 - (p0 + last * NB));
         lds_barrier();
-        drain(first, p1 - first);
+        drain(dg, p1 - (p0 + dg * NB));
     }
     if constexpr (WB) {
         double *out = gb_part + (size_t)range * plane4 * 4;
@@ -945,7 +959,7 @@ __global__ __launch_bounds__(1024) void k_bwd2_gb_combine(const double *__restri
 // Returns true (and the plan) when the fused kernel applies to the prepared operand strides
 // (order: g, a, b, ga, gb).
 static bool plan_bwd2(const Prepared &p, const float *g, const float *a, const float *b, const float *ga,
-                      const float *gb, Bwd2Plan &pl) {
+                      const float *gb, Bwd2Plan &pl, int blocks_per_cu = NC_B2_BLOCKS_PER_CU) {
     if (p.nd < 3 || p.numel >= (int64_t)UINT32_MAX) return false;
     const int h = p.nd - 2, w = p.nd - 1;
     const int64_t H = p.shape[h], W = p.shape[w];
@@ -986,8 +1000,12 @@ static bool plan_bwd2(const Prepared &p, const float *g, const float *a, const f
     pl.W4 = (uint32_t)(W / 4);
     pl.T = (uint32_t)T;
     pl.nband = (uint32_t)nband;
-    const int64_t want = std::max<int64_t>(1, (int64_t)num_cus() * NC_B2_BLOCKS_PER_CU / nband);
-    const int64_t ranges = std::min<int64_t>(P, want);
+    const int64_t want = std::max<int64_t>(1, (int64_t)num_cus() * blocks_per_cu / nband);
+    int64_t ranges = std::min<int64_t>(P, want);
+    // NC_HIP_BWD2_MAX_RANGES caps the plane ranges (more planes per workgroup): lets a small test
+    // problem run the long-range paths (several wraps of the grad_a ring) that only large inputs reach
+    if (const char *cap = getenv("NC_HIP_BWD2_MAX_RANGES"))
+        if (atoll(cap) > 0) ranges = std::min<int64_t>(ranges, atoll(cap));
     pl.planes_per_block = (uint32_t)((P + ranges - 1) / ranges);
     pl.ranges = (uint32_t)((P + pl.planes_per_block - 1) / pl.planes_per_block);
     return true;
@@ -1163,7 +1181,10 @@ static int try_bwd_fused_single(int op, int which, int nd, const int64_t *shape,
     Prepared p;
     if (prepare_bwd2(nd, shape, sg, reads_ab ? sa : sga, reads_ab ? sb : sgb, sga, sgb, p) != NC_HIP_OK) return -1;
     Bwd2Plan pl;
-    if (p.numel == 0 || !plan_bwd2(p, g, reads_ab ? a : gx, reads_ab ? b : gx, gx, gx, pl)) return -1;
+    // grad_b alone has no LDS exchange between waves: one workgroup per CU streams faster (fewer
+    // ranges also means a smaller workspace than the one the query reports)
+    const int bpc = which == 0 ? NC_B2_BLOCKS_PER_CU : NC_B2_GB_BLOCKS_PER_CU;
+    if (p.numel == 0 || !plan_bwd2(p, g, reads_ab ? a : gx, reads_ab ? b : gx, gx, gx, pl, bpc)) return -1;
     const size_t need = bwd2_ws(pl, which == 0 ? 1 : 2);
     if (ws_bytes < need || (need && !ws)) return -1;
     if (which == 0) return launch_bwd2_op<1>(op, g, a, b, gx, nullptr, pl, accumulate, ws, ws_bytes, st);

@@ -560,6 +560,23 @@ def test_kernel_binary_bwd_fused(K, case, ash, aview, bsh, op, accumulate):
         assert_close64(got, base + red, scale + (np.abs(init) if accumulate else 0), f"{case} {op} grad {name}")
 
 
+# Many planes per workgroup (plane ranges capped through NC_HIP_BWD2_MAX_RANGES): the grad_a ring of
+# group partials wraps several times, from a different starting slot in each workgroup.
+BWD2_LONG = [
+    ("ring_T1", (2048, 1, 64), None, (1, 32, 64), 4),
+    ("ring_T4_4bands", (256, 1, 64), None, (1, 512, 64), 2),
+    ("ring_w32", (1024, 1, 32), None, (1, 128, 32), 2),
+]
+
+
+@pytest.mark.parametrize("case,ash,aview,bsh,cap", BWD2_LONG)
+@pytest.mark.parametrize("op", ["add", "mul", "div"])
+def test_kernel_binary_bwd_fused_long_ranges(K, monkeypatch, case, ash, aview, bsh, cap, op):
+    monkeypatch.setenv("NC_HIP_BWD2_MAX_RANGES", str(cap))
+    test_kernel_binary_bwd_fused(K, case, ash, aview, bsh, op, True)
+    test_kernel_binary_bwd_single(K, case, ash, aview, bsh, op, False)
+
+
 @pytest.mark.parametrize("case,ash,aview,bsh", BWD2)
 @pytest.mark.parametrize("op", ["add", "sub", "mul", "div"])
 @pytest.mark.parametrize("accumulate", [True, False])
