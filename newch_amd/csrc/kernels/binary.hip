@@ -717,6 +717,11 @@ static int prepare_grad(int op, int which, int nd, const int64_t *shape, const i
 //     512-lane workgroup owns one band of a range of planes.  Lane t holds float4 q = t + 512 k
 //     (k < T) of the band, all in column group w4 = t mod W4 (W4 = W/4 divides 64).
 //   * g: the T loads of the next plane are issued before the current plane is summed.
+//   * Launch shape: when grad_a is written, T = 8 where the plane allows it, with one workgroup
+//     per CU (256 VGPRs per lane): twice the bytes per lane per plane of T = 4 at two workgroups
+//     per CU, so the per-plane grad_a exchange (shuffles, LDS slots, group sums, partial stores)
+//     is paid per twice the data (2^30-output backward: 775 -> 732 us).  grad_b alone has no
+//     exchange and runs T <= 4 with one workgroup per CU.
 //   * grad_b accumulates in fp64 registers (T x 4 per lane) over the workgroup's planes and is written
 //     once as a partial, combined by k_bwd2_gb_combine in plane-range order.
 //   * b (mul) or its fp32 reciprocal (div) stays in registers.  Each term is an fp32 product, as in
@@ -728,20 +733,17 @@ static int prepare_grad(int op, int which, int nd, const int64_t *shape, const i
 // MODE: 0 add/sub, 1 mul, 3 div.
 // ------------------------------------------------------------------------------------------------
 #ifndef NC_B2_TMAX
-#define NC_B2_TMAX 4
+#define NC_B2_TMAX 8  // T when grad_a is written
 #endif
-#ifndef NC_B2_BLOCKS_PER_CU
-#define NC_B2_BLOCKS_PER_CU 2
+#ifndef NC_B2_GB_TMAX
+#define NC_B2_GB_TMAX 4  // T for grad_b alone
 #endif
 constexpr int kB2 = 512;
 constexpr int kB2Waves = kB2 / kWave;
-constexpr int kB2MaxBand = 16;  // bands per plane: planes up to 16 * 512 * NC_B2_TMAX float4
+constexpr int kB2MaxBand = 16;  // bands per plane: planes up to 16 * 512 * T float4
 constexpr int kB2GroupDoubles = kB2Waves * 4 * 64;
 #ifndef NC_B2_RES_GROUPS
 #define NC_B2_RES_GROUPS 16
-#endif
-#ifndef NC_B2_GB_BLOCKS_PER_CU
-#define NC_B2_GB_BLOCKS_PER_CU 1
 #endif
 #ifndef NC_B2_NB_SHIFT
 #define NC_B2_NB_SHIFT 0
@@ -757,7 +759,7 @@ struct Bwd2Plan {
 // OUT selects the gradients written: 1 grad_a, 2 grad_b, 3 both.
 // two resident workgroups per CU (4 waves per SIMD): at most 128 VGPRs
 template <int MODE, bool ACC, int T, int OUT>
-__global__ __launch_bounds__(kB2, 4) void k_bcast_bwd2(const float *__restrict__ g, const float *__restrict__ a,
+__global__ __launch_bounds__(kB2, T >= 8 ? 2 : 4) void k_bcast_bwd2(const float *__restrict__ g, const float *__restrict__ a,
                                                     const float *__restrict__ b, float *__restrict__ ga,
                                                     double *__restrict__ ga_part, double *__restrict__ gb_part,
                                                     Bwd2Plan pl, double alpha_b) {
@@ -958,15 +960,18 @@ __global__ __launch_bounds__(1024) void k_bwd2_gb_combine(const double *__restri
 
 // Returns true (and the plan) when the fused kernel applies to the prepared operand strides
 // (order: g, a, b, ga, gb).
+// out: the gradients written (1 grad_a, 2 grad_b, 3 both).  The workspace of a plan for 3 covers the
+// plans for 1 and 2 of the same problem (the same or fewer plane ranges, the same grad_a bands).
 static bool plan_bwd2(const Prepared &p, const float *g, const float *a, const float *b, const float *ga,
-                      const float *gb, Bwd2Plan &pl, int blocks_per_cu = NC_B2_BLOCKS_PER_CU) {
+                      const float *gb, Bwd2Plan &pl, int out) {
+    const int64_t tmax = out == 2 ? NC_B2_GB_TMAX : NC_B2_TMAX;
     if (p.nd < 3 || p.numel >= (int64_t)UINT32_MAX) return false;
     const int h = p.nd - 2, w = p.nd - 1;
     const int64_t H = p.shape[h], W = p.shape[w];
     if (W % 4 || 64 % (W / 4) || (H * (W / 4)) % kB2) return false;
     int64_t T = H * (W / 4) / kB2, nband = 1;  // float4 per lane per plane
     if (T & (T - 1)) return false;
-    while (T > NC_B2_TMAX) {
+    while (T > tmax) {
         T /= 2;
         nband *= 2;
     }
@@ -1000,6 +1005,7 @@ static bool plan_bwd2(const Prepared &p, const float *g, const float *a, const f
     pl.W4 = (uint32_t)(W / 4);
     pl.T = (uint32_t)T;
     pl.nband = (uint32_t)nband;
+    const int64_t blocks_per_cu = out == 2 || T >= 8 ? 1 : 2;
     const int64_t want = std::max<int64_t>(1, (int64_t)num_cus() * blocks_per_cu / nband);
     int64_t ranges = std::min<int64_t>(P, want);
     // NC_HIP_BWD2_MAX_RANGES caps the plane ranges (more planes per workgroup): lets a small test
@@ -1119,7 +1125,7 @@ static size_t bwd2_single_ws_bound(int nd, const int64_t *shape, const int64_t *
     if (prepare(nd, shape, 5, strides, p, "nc_hip_binary_bwd_workspace")) return 0;
     Bwd2Plan pl;
     const float *al = (const float *)(uintptr_t)256;
-    return plan_bwd2(p, al, al, al, al, al, pl) ? bwd2_ws(pl, 3) : 0;
+    return plan_bwd2(p, al, al, al, al, al, pl, 3) ? bwd2_ws(pl, 3) : 0;
 }
 
 }  // namespace nchip
@@ -1181,10 +1187,8 @@ static int try_bwd_fused_single(int op, int which, int nd, const int64_t *shape,
     Prepared p;
     if (prepare_bwd2(nd, shape, sg, reads_ab ? sa : sga, reads_ab ? sb : sgb, sga, sgb, p) != NC_HIP_OK) return -1;
     Bwd2Plan pl;
-    // grad_b alone has no LDS exchange between waves: one workgroup per CU streams faster (fewer
-    // ranges also means a smaller workspace than the one the query reports)
-    const int bpc = which == 0 ? NC_B2_BLOCKS_PER_CU : NC_B2_GB_BLOCKS_PER_CU;
-    if (p.numel == 0 || !plan_bwd2(p, g, reads_ab ? a : gx, reads_ab ? b : gx, gx, gx, pl, bpc)) return -1;
+    if (p.numel == 0 || !plan_bwd2(p, g, reads_ab ? a : gx, reads_ab ? b : gx, gx, gx, pl, which == 0 ? 1 : 2))
+        return -1;
     const size_t need = bwd2_ws(pl, which == 0 ? 1 : 2);
     if (ws_bytes < need || (need && !ws)) return -1;
     if (which == 0) return launch_bwd2_op<1>(op, g, a, b, gx, nullptr, pl, accumulate, ws, ws_bytes, st);
@@ -1241,7 +1245,7 @@ extern "C" NC_HIP_API size_t nc_hip_binary_bwd2_workspace(int nd, const int64_t 
         if (prepare_bwd2(nd, shape, cs, sga, sgb, sga, sgb, p) == NC_HIP_OK) {
             Bwd2Plan pl;
             const float *al = (const float *)(uintptr_t)256;  // any 16-byte aligned address: only the plan is needed
-            if (plan_bwd2(p, al, al, al, al, al, pl)) need = std::max(need, bwd2_ws(pl));
+            if (plan_bwd2(p, al, al, al, al, al, pl, 3)) need = std::max(need, bwd2_ws(pl));
         }
     }
     return need;
@@ -1260,7 +1264,7 @@ extern "C" NC_HIP_API int nc_hip_binary_bwd2(int op, int nd, const int64_t *shap
         int rc = prepare_bwd2(nd, shape, sg, reads_ab ? sa : sga, reads_ab ? sb : sgb, sga, sgb, p);
         if (rc) return rc;
         Bwd2Plan pl;
-        if (p.numel > 0 && plan_bwd2(p, g, reads_ab ? a : ga, reads_ab ? b : gb, ga, gb, pl)) {
+        if (p.numel > 0 && plan_bwd2(p, g, reads_ab ? a : ga, reads_ab ? b : gb, ga, gb, pl, 3)) {
             if (reads_ab && NC_BIN_WARM) warm_operand(a, p, 1, as_stream(stream));  // grad_b's terms read a
             return launch_bwd2_op<3>(op, g, a, b, ga, gb, pl, accumulate, ws, ws_bytes, as_stream(stream));
         }

@@ -523,7 +523,8 @@ BWD2 = [
     ("batch_t", (8, 4, 1, 64), ("t", 0, 1), (1, 1, 64, 64)),
     ("bands8", (3, 1, 64), None, (1, 1024, 64)),
     ("fallback_h48", (4, 8, 1, 64), None, (1, 1, 48, 64)),
-    ("fallback_bands32", (2, 1, 64), None, (1, 4096, 64)),
+    ("bands16", (2, 1, 64), None, (1, 4096, 64)),
+    ("fallback_bands32", (2, 1, 64), None, (1, 8192, 64)),
 ]
 
 
@@ -564,7 +565,7 @@ def test_kernel_binary_bwd_fused(K, case, ash, aview, bsh, op, accumulate):
 # group partials wraps several times, from a different starting slot in each workgroup.
 BWD2_LONG = [
     ("ring_T1", (2048, 1, 64), None, (1, 32, 64), 4),
-    ("ring_T4_4bands", (256, 1, 64), None, (1, 512, 64), 2),
+    ("ring_T8_2bands", (256, 1, 64), None, (1, 512, 64), 2),
     ("ring_w32", (1024, 1, 32), None, (1, 128, 32), 2),
 ]
 
