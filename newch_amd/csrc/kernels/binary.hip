@@ -742,13 +742,12 @@ constexpr int kB2 = 512;
 constexpr int kB2Waves = kB2 / kWave;
 constexpr int kB2MaxBand = 16;  // bands per plane: planes up to 16 * 512 * T float4
 constexpr int kB2GroupDoubles = kB2Waves * 4 * 64;
-#ifndef NC_B2_RES_GROUPS
-#define NC_B2_RES_GROUPS 16
-#endif
-#ifndef NC_B2_NB_SHIFT
-#define NC_B2_NB_SHIFT 0
-#endif
-constexpr int kB2ResGroups = NC_B2_RES_GROUPS;  // groups of grad_a held in LDS between stores
+// Groups of grad_a held in LDS between stores, sized so that the slot sets and res fill the CU's
+// 160 KiB of LDS at the launch's workgroups per CU.  A drain of res is a burst of stores that the
+// next plane loads wait behind (one in-order memory counter): at one drain per 64 planes the
+// 2^30-output backward took 728 us, with none before the end 648 us, so the plan gives each
+// workgroup no more planes than res holds where the problem allows.
+constexpr uint32_t b2_res_groups(int64_t T) { return T >= 8 ? 64 : 24; }
 
 struct Bwd2Plan {
     uint32_t P, H, W4, T, nband;
@@ -765,10 +764,11 @@ __global__ __launch_bounds__(kB2, T >= 8 ? 2 : 4) void k_bcast_bwd2(const float 
                                                     Bwd2Plan pl, double alpha_b) {
     constexpr uint32_t band4 = kB2 * T;  // float4 per band
     __shared__ double sh[2][kB2GroupDoubles];  // two group slot sets, each [NB][8 waves][W4][4]
+    constexpr uint32_t kB2ResGroups = b2_res_groups(T);
     __shared__ double res[kB2ResGroups * 4 * 64];  // grad_a of the last kB2ResGroups groups, [plane][W]
     const int tid = threadIdx.x, lane = tid & (kWave - 1), wv = tid / kWave;
     const uint32_t W4 = pl.W4, nband = pl.nband;
-    const uint32_t NB = max(1u, (64 / W4) >> NC_B2_NB_SHIFT);
+    const uint32_t NB = 64 / W4;
     const uint32_t w4 = tid % W4;
     const uint32_t band = blockIdx.x % nband, range = blockIdx.x / nband;
     const uint32_t plane4 = band4 * nband;
@@ -1008,6 +1008,11 @@ static bool plan_bwd2(const Prepared &p, const float *g, const float *a, const f
     const int64_t blocks_per_cu = out == 2 || T >= 8 ? 1 : 2;
     const int64_t want = std::max<int64_t>(1, (int64_t)num_cus() * blocks_per_cu / nband);
     int64_t ranges = std::min<int64_t>(P, want);
+    if (out & 1) {  // whole multiples of the resident workgroups until each range fits in res
+        const int64_t fit = (int64_t)b2_res_groups(T) * (64 / (W / 4));
+        const int64_t rounds = ((P + fit - 1) / fit + want - 1) / want;
+        ranges = std::min<int64_t>(P, want * rounds);
+    }
     // NC_HIP_BWD2_MAX_RANGES caps the plane ranges (more planes per workgroup): lets a small test
     // problem run the long-range paths (several wraps of the grad_a ring) that only large inputs reach
     if (const char *cap = getenv("NC_HIP_BWD2_MAX_RANGES"))

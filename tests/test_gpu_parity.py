@@ -565,7 +565,7 @@ def test_kernel_binary_bwd_fused(K, case, ash, aview, bsh, op, accumulate):
 # group partials wraps several times, from a different starting slot in each workgroup.
 BWD2_LONG = [
     ("ring_T1", (2048, 1, 64), None, (1, 32, 64), 4),
-    ("ring_T8_2bands", (256, 1, 64), None, (1, 512, 64), 2),
+    ("ring_T8_2bands", (640, 1, 64), None, (1, 512, 64), 1),
     ("ring_w32", (1024, 1, 32), None, (1, 128, 32), 2),
 ]
 
