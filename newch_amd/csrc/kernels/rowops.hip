@@ -335,7 +335,7 @@ __global__ __launch_bounds__(kRowB) void k_ln_fwd_blk(const float *__restrict__ 
 // requested before the row is reduced.  The gw / gb column partials of a wave's rows accumulate in
 // fp32 in that wave's own LDS slice (rows up to 1024 floats; registers for longer rows), in row
 // order; at the end each column's 8 wave partials are added in wave order in fp64 and written as
-// the workgroup's partial, which k_ln_cols_combine adds up in workgroup order.
+// the workgroup's partial, which k_ln_cols_combine adds up in a fixed order.
 constexpr int kLnB = 512;
 constexpr int kLnWaves = kLnB / kWave;
 
@@ -523,9 +523,18 @@ __global__ __launch_bounds__(kLnB, VPL <= 4 ? 4 : 2) void k_ln_bwd_reg(const flo
 // stored, then row r + 16 is loaded into the first bundle and row r + 8 reduced.  Every load in the
 // steady-state loop is unconditional, so the compiler's in-order memory-counter waits for a row's
 // bundle never cover the other bundle's loads (a single prefetch buffer copied forward at the end
-// of each row makes it wait for the prefetched row before moving on).
+// of each row makes it wait for the prefetched row before moving on).  Rows are dealt to the
+// waves of the whole grid in turn (wave w of workgroup b takes rows 8 b + w, 8 b + w + 8 G, ...),
+// so the chip sweeps the four row streams together instead of one contiguous range per workgroup
+// (65536 x 1024: 197 -> 190 us).  At 160-210 VGPRs one workgroup is resident per CU.
+#ifndef NC_LN_BWD_INTERLEAVE
+#define NC_LN_BWD_INTERLEAVE 1
+#endif
+#ifndef NC_LN_BWD_WAVES_PER_EU
+#define NC_LN_BWD_WAVES_PER_EU 2
+#endif
 template <int VPL, bool ACC>
-__global__ __launch_bounds__(kLnB, 2) void k_ln_bwd_pp(const float *__restrict__ x, const float *__restrict__ w,
+__global__ __launch_bounds__(kLnB, NC_LN_BWD_WAVES_PER_EU) void k_ln_bwd_pp(const float *__restrict__ x, const float *__restrict__ w,
                                                       const float *__restrict__ stats, const float *__restrict__ g,
                                                       float *__restrict__ gx, double *__restrict__ part,
                                                       int64_t rows, int D, int64_t rows_per_block) {
@@ -605,22 +614,25 @@ __global__ __launch_bounds__(kLnB, 2) void k_ln_bwd_pp(const float *__restrict__
             __builtin_nontemporal_store(o, dx + lane + k * kWave);
         }
     };
-    int64_t r = r0 + wv;
+    // rows of this wave: r, r + step, r + 2 step, ...
+    int64_t r = NC_LN_BWD_INTERLEAVE ? (int64_t)blockIdx.x * kLnWaves + wv : r0 + wv;
+    const int64_t step = NC_LN_BWD_INTERLEAVE ? (int64_t)gridDim.x * kLnWaves : kLnWaves;
+    const int64_t rend = NC_LN_BWD_INTERLEAVE ? rows : r1;
     Bundle A, B;
-    if (r < r1) load(r, A);
-    // steady state: rows r and r + 8 exist, and row r + 16 too for the next first bundle
-    while (r + 2 * kLnWaves < r1) {
-        load(r + kLnWaves, B);
+    if (r < rend) load(r, A);
+    // steady state: rows r and r + step exist, and row r + 2 step too for the next first bundle
+    while (r + 2 * step < rend) {
+        load(r + step, B);
         process(r, A);
-        load(r + 2 * kLnWaves, A);
-        process(r + kLnWaves, B);
-        r += 2 * kLnWaves;
+        load(r + 2 * step, A);
+        process(r + step, B);
+        r += 2 * step;
     }
-    if (r < r1) {
-        const bool hb = r + kLnWaves < r1;
-        if (hb) load(r + kLnWaves, B);
+    if (r < rend) {
+        const bool hb = r + step < rend;
+        if (hb) load(r + step, B);
         process(r, A);
-        if (hb) process(r + kLnWaves, B);
+        if (hb) process(r + step, B);
     }
     if (!cols) return;
     // column i of [gw | gb]: the 8 wave slices added in wave order
@@ -689,36 +701,34 @@ __global__ __launch_bounds__(kRowB) void k_ln_cols_part(const float *__restrict_
     }
 }
 
-// gw[i] (+)= sum_p part[p][0][i], gb[i] (+)= sum_p part[p][1][i] in a fixed order: a 64 x 16 thread
-// block covers 64 columns; slice y sums partials y, y + 16, y + 32, ... in order, then slice 0 adds
-// the 16 slice sums in slice order.
-constexpr int kCombCols = 64, kCombSlices = 16;
+// gw[i] (+)= sum_p part[p][0][i], gb[i] (+)= sum_p part[p][1][i] in a fixed order: a 16 x 64 thread
+// block covers 16 columns of one of the two (blockIdx.y: 0 gw, 1 gb); slice y sums partials y,
+// y + 64, y + 128, ... in order, then slice 0 adds the 64 slice sums in slice order.  Narrow column
+// tiles give D/16 x 2 workgroups, so the few MiB of partials are read by many CUs at once (64 x 16
+// tiles over both outputs: 16 workgroups at D = 1024, 10 us for 512 partials).
+constexpr int kCombCols = 16, kCombSlices = 64;
 __global__ __launch_bounds__(kCombCols *kCombSlices) void k_ln_cols_combine(const double *__restrict__ part,
                                                                             float *__restrict__ gw,
                                                                             float *__restrict__ gb, int64_t D, int P) {
-    __shared__ double shw[kCombSlices][kCombCols], shb[kCombSlices][kCombCols];
+    __shared__ double sh[kCombSlices][kCombCols];
     const int x = threadIdx.x % kCombCols, y = threadIdx.x / kCombCols;
     const int64_t i = (int64_t)blockIdx.x * kCombCols + x;
-    double sw = 0.0, sb = 0.0;
+    const int which = blockIdx.y;
+    float *out = which == 0 ? gw : gb;
+    if (!out) return;  // uniform over the workgroup
+    const double *src = part + (size_t)which * D;
+    double t = 0.0;
     if (i < D) {
-#pragma unroll 8
-        for (int p = y; p < P; p += kCombSlices) {
-            sw += part[(size_t)p * 2 * D + i];
-            sb += part[(size_t)p * 2 * D + D + i];
-        }
+#pragma unroll 4
+        for (int p = y; p < P; p += kCombSlices) t += src[(size_t)p * 2 * D + i];
     }
-    shw[y][x] = sw;
-    shb[y][x] = sb;
+    sh[y][x] = t;
     __syncthreads();
     if (y == 0 && i < D) {
-        double tw = 0.0, tb = 0.0;
+        double s = 0.0;
 #pragma unroll
-        for (int k = 0; k < kCombSlices; k++) {
-            tw += shw[k][x];
-            tb += shb[k][x];
-        }
-        if (gw) gw[i] = (float)((double)gw[i] + tw);
-        if (gb) gb[i] = (float)((double)gb[i] + tb);
+        for (int k = 0; k < kCombSlices; k++) s += sh[k][x];
+        out[i] = (float)((double)out[i] + s);
     }
 }
 
@@ -733,7 +743,10 @@ static int vpl_for(int64_t C) {
 }
 
 #ifndef NC_LN_BWD_BLOCKS_PER_CU
-#define NC_LN_BWD_BLOCKS_PER_CU 2
+#define NC_LN_BWD_BLOCKS_PER_CU 2  // k_ln_bwd_reg, rows up to 1024 floats
+#endif
+#ifndef NC_LN_BWD_PP_BLOCKS_PER_CU
+#define NC_LN_BWD_PP_BLOCKS_PER_CU 1  // k_ln_bwd_pp
 #endif
 #ifndef NC_ROWS_GRID_PER_CU
 #define NC_ROWS_GRID_PER_CU 65536
@@ -772,19 +785,22 @@ static unsigned rows_grid(int64_t rows) {
 struct LnPlan {
     bool reg;
     int vpl;
+    bool full;                       // k_ln_bwd_pp (full rows of up to 1024 floats, gx written)
     int64_t blocks, rows_per_block;  // register path
     int64_t chunk;
     int P;                           // generic path
     size_t ws;
 };
 
-static LnPlan ln_plan(int64_t rows, int64_t D, bool aligned) {
+static LnPlan ln_plan(int64_t rows, int64_t D, bool aligned, bool has_gx) {
     LnPlan p{};
     p.vpl = (D % 4 == 0 && aligned) ? vpl_for(D) : 0;
     if (p.vpl > 8) p.vpl = 0;  // rows beyond 2048 floats would spill registers: generic path
     p.reg = p.vpl != 0;
     if (p.reg) {
-        int64_t want = (int64_t)num_cus() * (p.vpl <= 4 ? NC_LN_BWD_BLOCKS_PER_CU : 1);  // the resident workgroups
+        p.full = has_gx && p.vpl <= 4 && D == (int64_t)p.vpl * 4 * kWave;
+        const int per_cu = p.full ? NC_LN_BWD_PP_BLOCKS_PER_CU : p.vpl <= 4 ? NC_LN_BWD_BLOCKS_PER_CU : 1;
+        int64_t want = (int64_t)num_cus() * per_cu;  // the resident workgroups
         int64_t rpb = (rows + want - 1) / want;
         if (rpb < kLnWaves) rpb = kLnWaves;
         p.rows_per_block = rpb;
@@ -863,8 +879,9 @@ extern "C" NC_HIP_API int nc_hip_layer_norm_fwd(int64_t rows, int64_t D, const f
 
 extern "C" NC_HIP_API size_t nc_hip_layer_norm_bwd_workspace(int64_t rows, int64_t D) {
     if (rows <= 0 || D <= 0) return 0;
-    return ln_plan(rows, D, true).ws > ln_plan(rows, D, false).ws ? ln_plan(rows, D, true).ws
-                                                                    : ln_plan(rows, D, false).ws;
+    // the plans without gx have at least as many workgroups (partials) as those with it
+    const size_t a = ln_plan(rows, D, true, false).ws, b = ln_plan(rows, D, false, false).ws;
+    return a > b ? a : b;
 }
 
 extern "C" NC_HIP_API int nc_hip_layer_norm_bwd(int64_t rows, int64_t D, const float *x, const float *w,
@@ -874,7 +891,7 @@ extern "C" NC_HIP_API int nc_hip_layer_norm_bwd(int64_t rows, int64_t D, const f
     if (rows == 0) return NC_HIP_OK;
     hipStream_t st = as_stream(stream);
     const bool al = aligned16(x) && aligned16(g) && (!gx || aligned16(gx)) && (!w || aligned16(w));
-    const LnPlan p = ln_plan(rows, D, al);
+    const LnPlan p = ln_plan(rows, D, al, gx != nullptr);
     const bool cols = gw || gb;
     if (cols && (ws_bytes < p.ws || !ws))
         return set_error(NC_HIP_ERR_WORKSPACE, "nc_hip_layer_norm_bwd: workspace of %zu bytes needed", p.ws);
@@ -882,7 +899,7 @@ extern "C" NC_HIP_API int nc_hip_layer_norm_bwd(int64_t rows, int64_t D, const f
     if (p.reg) {
         const size_t lds = ln_bwd_lds(p.vpl, D, cols);
         if (lds > 65536) return set_error(NC_HIP_ERR_ARG, "nc_hip_layer_norm_bwd: D too large for LDS combine");
-        const bool full = gx && p.vpl <= 4 && D == (int64_t)p.vpl * 4 * kWave;
+        const bool full = p.full;
         if (full && accumulate)
             NC_VPL_SWITCH4(p.vpl, hipLaunchKernelGGL((k_ln_bwd_pp<VP, true>), dim3(p.blocks), kLnB, lds, st, x, w, stats, g, gx, part, rows, (int)D, p.rows_per_block))
         else if (full)
@@ -892,7 +909,7 @@ extern "C" NC_HIP_API int nc_hip_layer_norm_bwd(int64_t rows, int64_t D, const f
         else
             NC_VPL_SWITCH8(p.vpl, hipLaunchKernelGGL((k_ln_bwd_reg<VP, false>), dim3(p.blocks), kLnB, lds, st, x, w, stats, g, gx, part, rows, (int)D, p.rows_per_block))
         if (cols)
-            hipLaunchKernelGGL(k_ln_cols_combine, dim3((D + kCombCols - 1) / kCombCols), kCombCols * kCombSlices, 0, st, part, gw, gb, D, (int)p.blocks);
+            hipLaunchKernelGGL(k_ln_cols_combine, dim3((unsigned)((D + kCombCols - 1) / kCombCols), 2), kCombCols * kCombSlices, 0, st, part, gw, gb, D, (int)p.blocks);
     } else {
         const unsigned grid = (unsigned)(rows < num_cus() * 8 ? rows : num_cus() * 8);
         if (gx) {
@@ -902,7 +919,7 @@ extern "C" NC_HIP_API int nc_hip_layer_norm_bwd(int64_t rows, int64_t D, const f
         if (cols) {
             hipLaunchKernelGGL(k_ln_cols_part, stream_grid(D * p.P, kRowB), kRowB, 0, st, x, stats, g, part, rows, D,
                                p.chunk, p.P);
-            hipLaunchKernelGGL(k_ln_cols_combine, dim3((D + kCombCols - 1) / kCombCols), kCombCols * kCombSlices, 0, st, part, gw, gb, D, p.P);
+            hipLaunchKernelGGL(k_ln_cols_combine, dim3((unsigned)((D + kCombCols - 1) / kCombCols), 2), kCombCols * kCombSlices, 0, st, part, gw, gb, D, p.P);
         }
     }
     return check_launch("nc_hip_layer_norm_bwd");
