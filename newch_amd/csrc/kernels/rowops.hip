@@ -533,7 +533,7 @@ __global__ __launch_bounds__(kLnB, VPL <= 4 ? 4 : 2) void k_ln_bwd_reg(const flo
 #ifndef NC_LN_BWD_WAVES_PER_EU
 #define NC_LN_BWD_WAVES_PER_EU 2
 #endif
-template <int VPL, bool ACC>
+template <int VPL, bool ACC, bool HW>
 __global__ __launch_bounds__(kLnB, NC_LN_BWD_WAVES_PER_EU) void k_ln_bwd_pp(const float *__restrict__ x, const float *__restrict__ w,
                                                       const float *__restrict__ stats, const float *__restrict__ g,
                                                       float *__restrict__ gx, double *__restrict__ part,
@@ -546,7 +546,7 @@ __global__ __launch_bounds__(kLnB, NC_LN_BWD_WAVES_PER_EU) void k_ln_bwd_pp(cons
     const int64_t r0 = (int64_t)blockIdx.x * rows_per_block;
     const int64_t r1 = min(rows, r0 + rows_per_block);
     const bool cols = part != nullptr;
-    if (w) {
+    if constexpr (HW) {  // HW: w is given (the kernel is specialised so no per-element test remains)
         for (int j = threadIdx.x; j < nv; j += kLnB) wsh[j] = ((const f4 *)w)[j];
         __syncthreads();
     }
@@ -573,15 +573,15 @@ __global__ __launch_bounds__(kLnB, NC_LN_BWD_WAVES_PER_EU) void k_ln_bwd_pp(cons
     auto process = [&](int64_t r, const Bundle &b) {
         const float mean = b.st.x, rstd = b.st.y;
         auto terms = [&](int k, f4 &xh, f4 &gw) {
-            const f4 ww = w ? wsh[lane + k * kWave] : f4{1.f, 1.f, 1.f, 1.f};
+            const f4 ww = HW ? wsh[lane + k * kWave] : f4{1.f, 1.f, 1.f, 1.f};
             xh.x = (b.x[k].x - mean) * rstd;
             xh.y = (b.x[k].y - mean) * rstd;
             xh.z = (b.x[k].z - mean) * rstd;
             xh.w = (b.x[k].w - mean) * rstd;
-            gw.x = w ? b.g[k].x * ww.x : b.g[k].x;
-            gw.y = w ? b.g[k].y * ww.y : b.g[k].y;
-            gw.z = w ? b.g[k].z * ww.z : b.g[k].z;
-            gw.w = w ? b.g[k].w * ww.w : b.g[k].w;
+            gw.x = HW ? b.g[k].x * ww.x : b.g[k].x;
+            gw.y = HW ? b.g[k].y * ww.y : b.g[k].y;
+            gw.z = HW ? b.g[k].z * ww.z : b.g[k].z;
+            gw.w = HW ? b.g[k].w * ww.w : b.g[k].w;
         };
         double sg = 0.0, sgx = 0.0;
 #pragma unroll
@@ -901,9 +901,9 @@ extern "C" NC_HIP_API int nc_hip_layer_norm_bwd(int64_t rows, int64_t D, const f
         if (lds > 65536) return set_error(NC_HIP_ERR_ARG, "nc_hip_layer_norm_bwd: D too large for LDS combine");
         const bool full = p.full;
         if (full && accumulate)
-            NC_VPL_SWITCH4(p.vpl, hipLaunchKernelGGL((k_ln_bwd_pp<VP, true>), dim3(p.blocks), kLnB, lds, st, x, w, stats, g, gx, part, rows, (int)D, p.rows_per_block))
+            NC_VPL_SWITCH4(p.vpl, if (w) hipLaunchKernelGGL((k_ln_bwd_pp<VP, true, true>), dim3(p.blocks), kLnB, lds, st, x, w, stats, g, gx, part, rows, (int)D, p.rows_per_block); else hipLaunchKernelGGL((k_ln_bwd_pp<VP, true, false>), dim3(p.blocks), kLnB, lds, st, x, w, stats, g, gx, part, rows, (int)D, p.rows_per_block))
         else if (full)
-            NC_VPL_SWITCH4(p.vpl, hipLaunchKernelGGL((k_ln_bwd_pp<VP, false>), dim3(p.blocks), kLnB, lds, st, x, w, stats, g, gx, part, rows, (int)D, p.rows_per_block))
+            NC_VPL_SWITCH4(p.vpl, if (w) hipLaunchKernelGGL((k_ln_bwd_pp<VP, false, true>), dim3(p.blocks), kLnB, lds, st, x, w, stats, g, gx, part, rows, (int)D, p.rows_per_block); else hipLaunchKernelGGL((k_ln_bwd_pp<VP, false, false>), dim3(p.blocks), kLnB, lds, st, x, w, stats, g, gx, part, rows, (int)D, p.rows_per_block))
         else if (accumulate)
             NC_VPL_SWITCH8(p.vpl, hipLaunchKernelGGL((k_ln_bwd_reg<VP, true>), dim3(p.blocks), kLnB, lds, st, x, w, stats, g, gx, part, rows, (int)D, p.rows_per_block))
         else

@@ -741,24 +741,28 @@ def test_kernel_layer_norm(K, rows, D):
 
 
 @pytest.mark.parametrize("rows,D", [(129, 512), (1031, 1024), (40, 2048), (9, 64), (300, 256), (7, 1024), (17, 1024)])
-@pytest.mark.parametrize("mode", ["store_all", "acc_gx_only", "cols_only"])
+@pytest.mark.parametrize("mode", ["store_all", "acc_gx_only", "cols_only", "no_weight"])
 def test_kernel_layer_norm_bwd_modes(K, rows, D, mode):
-    """Backward with a fresh (stored) gx, with gx alone accumulated onto nonzero values, and with
-    only the gw / gb column sums requested; row lengths covering every register layout."""
+    """Backward with a fresh (stored) gx, with gx alone accumulated onto nonzero values, with only
+    the gw / gb column sums requested, and without a weight (all outputs, gx accumulated); row
+    lengths covering every register layout."""
     rng = np.random.default_rng(zlib.crc32(f"lnbwd/{rows}/{D}/{mode}".encode()))
     x = (rng.standard_normal((rows, D)) * 2 + 0.3).astype(np.float32)
     w = (1 + 0.1 * rng.standard_normal(D)).astype(np.float32)
     g = rng.standard_normal((rows, D)).astype(np.float32)
     gx0 = rng.standard_normal((rows, D)).astype(np.float32)
     Xd, Wd, Gd = dev(x), dev(w), dev(g)
+    wp = 0 if mode == "no_weight" else Wd.ptr
+    if mode == "no_weight":
+        w = np.ones(D, np.float32)
     Sd = empty(8 * rows)
     Yd = empty(x.nbytes)
-    K.layer_norm_fwd(rows, D, Xd.ptr, Wd.ptr, 0, 1e-5, Yd.ptr, Sd.ptr)
+    K.layer_norm_fwd(rows, D, Xd.ptr, wp, 0, 1e-5, Yd.ptr, Sd.ptr)
     GX, GW, GB = dev(gx0), dev(np.zeros(D, np.float32)), dev(np.zeros(D, np.float32))
     wsb = K.layer_norm_bwd_workspace(rows, D)
     ws = empty(max(wsb, 1))
-    want_gx, want_cols, acc = mode != "cols_only", mode != "acc_gx_only", mode == "acc_gx_only"
-    K.layer_norm_bwd(rows, D, Xd.ptr, Wd.ptr, Sd.ptr, Gd.ptr, GX.ptr if want_gx else 0, GW.ptr if want_cols else 0,
+    want_gx, want_cols, acc = mode != "cols_only", mode != "acc_gx_only", mode in ("acc_gx_only", "no_weight")
+    K.layer_norm_bwd(rows, D, Xd.ptr, wp, Sd.ptr, Gd.ptr, GX.ptr if want_gx else 0, GW.ptr if want_cols else 0,
                      GB.ptr if want_cols else 0, ws.ptr, wsb, accumulate=acc)
     sync()
     X, G = x.astype(np.float64), g.astype(np.float64)
