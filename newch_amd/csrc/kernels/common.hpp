@@ -50,10 +50,7 @@ __device__ __forceinline__ float fma_(float a, float b, float c) { return __buil
 // exp8: clamp (NaN -> LO through the compare-select), n = floor(x log2e + 1/2), r = x - n ln2 in two
 // fused steps, degree-6 polynomial, 2^n assembled in the exponent field (n = 128 as 2^127 * 2),
 // zero below LO, NaN passed through.
-__device__ __forceinline__ float exp8(float x) {
-    const float x0 = x;
-    float xc = x > NC_K_EXP_LO ? x : NC_K_EXP_LO;
-    xc = xc < NC_K_EXP_HI ? xc : NC_K_EXP_HI;
+__device__ __forceinline__ float exp8_poly(float xc, int &n) {  // p(r) for a clamped argument; n
     const float fx = __builtin_floorf(fma_(xc, NC_K_LOG2E, 0.5f));
     float r = fma_(-fx, NC_K_LN2_HI, xc);
     r = fma_(-fx, NC_K_LN2_LO, r);
@@ -64,11 +61,33 @@ __device__ __forceinline__ float exp8(float x) {
     y = fma_(y, r, 1.6666665459e-1f);
     y = fma_(y, r, 5.0000001201e-1f);
     y = fma_(y, r * r, r + 1.0f);
-    int n = (int)fx;
+    n = (int)fx;
+    return y;
+}
+
+__device__ __forceinline__ float exp8(float x) {
+    const float x0 = x;
+    float xc = x > NC_K_EXP_LO ? x : NC_K_EXP_LO;
+    xc = xc < NC_K_EXP_HI ? xc : NC_K_EXP_HI;
+    int n;
+    const float y = exp8_poly(xc, n);
     const int big = n > 127;
     n -= big;
     float res = y * __int_as_float((n + 127) << 23);
     res = res * (big ? 2.0f : 1.0f);
+    res = x0 < NC_K_EXP_LO ? 0.0f : res;
+    return x0 != x0 ? x0 : res;
+}
+
+// exp8 for arguments that are <= 0 or NaN (x minus its row maximum, log-probabilities): there the
+// upper clamp is inactive and n <= 0, so the 2^128 split multiplies by 1; both are dropped, and the
+// result is bit-identical to exp8 on that domain.
+__device__ __forceinline__ float exp8_nonpos(float x) {
+    const float x0 = x;
+    const float xc = x > NC_K_EXP_LO ? x : NC_K_EXP_LO;
+    int n;
+    const float y = exp8_poly(xc, n);
+    float res = y * __int_as_float((n + 127) << 23);
     res = x0 < NC_K_EXP_LO ? 0.0f : res;
     return x0 != x0 ? x0 : res;
 }

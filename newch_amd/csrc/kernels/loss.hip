@@ -84,8 +84,8 @@ __global__ __launch_bounds__(kLB) void k_ce_fwd_reg(const float *__restrict__ x,
 #pragma unroll
         for (int k = 0; k < VPL; k++) {
             if (lane + k * kWave < nv)
-                s += ((double)exp8(v[k].x - m) + (double)exp8(v[k].y - m)) +
-                     ((double)exp8(v[k].z - m) + (double)exp8(v[k].w - m));
+                s += ((double)exp8_nonpos(v[k].x - m) + (double)exp8_nonpos(v[k].y - m)) +
+                     ((double)exp8_nonpos(v[k].z - m) + (double)exp8_nonpos(v[k].w - m));
         }
         const float ls = logf((float)wave_sum(s));
         f4 *pr = (f4 *)(prob + r * C);
@@ -95,7 +95,7 @@ __global__ __launch_bounds__(kLB) void k_ce_fwd_reg(const float *__restrict__ x,
             if (j < nv) {
                 const float lp[4] = {(v[k].x - m) - ls, (v[k].y - m) - ls, (v[k].z - m) - ls, (v[k].w - m) - ls};
                 if (ok && (L >> 2) == j) acc -= (double)lp[L & 3];
-                __builtin_nontemporal_store(f4{exp8(lp[0]), exp8(lp[1]), exp8(lp[2]), exp8(lp[3])}, pr + j);
+                __builtin_nontemporal_store(f4{exp8_nonpos(lp[0]), exp8_nonpos(lp[1]), exp8_nonpos(lp[2]), exp8_nonpos(lp[3])}, pr + j);
             }
         }
 #pragma unroll

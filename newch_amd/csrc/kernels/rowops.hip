@@ -52,10 +52,10 @@ __global__ __launch_bounds__(kRowB) void k_softmax_fwd_reg(const float *__restri
             const int j = lane + k * kWave;
             if (j < nv) {
                 f4 e;
-                e.x = exp8(v[k].x - m);
-                e.y = exp8(v[k].y - m);
-                e.z = exp8(v[k].z - m);
-                e.w = exp8(v[k].w - m);
+                e.x = exp8_nonpos(v[k].x - m);
+                e.y = exp8_nonpos(v[k].y - m);
+                e.z = exp8_nonpos(v[k].z - m);
+                e.w = exp8_nonpos(v[k].w - m);
                 s += ((double)e.x + (double)e.y) + ((double)e.z + (double)e.w);
                 if (!LOG) v[k] = e;
             }
@@ -199,14 +199,14 @@ __global__ __launch_bounds__(kRowB) void k_softmax_fwd_blk(const float *__restri
         for (int64_t c = threadIdx.x; c < C; c += kRowB) m = __builtin_fmaxf(m, xr[c]);
         m = row_max_finish(block_max(m, shf), xr[0]);
         double s = 0.0;
-        for (int64_t c = threadIdx.x; c < C; c += kRowB) s += (double)exp8(xr[c] - m);
+        for (int64_t c = threadIdx.x; c < C; c += kRowB) s += (double)exp8_nonpos(xr[c] - m);
         const float sf = (float)block_sum(s, shd);
         if (LOG) {
             const float ls = logf(sf);
             for (int64_t c = threadIdx.x; c < C; c += kRowB) yr[c] = (xr[c] - m) - ls;
         } else {
             const float inv = 1.0f / sf;
-            for (int64_t c = threadIdx.x; c < C; c += kRowB) yr[c] = inv * exp8(xr[c] - m);
+            for (int64_t c = threadIdx.x; c < C; c += kRowB) yr[c] = inv * exp8_nonpos(xr[c] - m);
         }
         __syncthreads();
     }
