@@ -206,17 +206,40 @@ __device__ __forceinline__ f4 load4s(const float *p, uint32_t is, int mode) {
     return f4{p[0], p[is], p[2 * is], p[3 * is]};
 }
 
+// Launch shape of the 32-bit index kernel per op (a[64,512,1,64] op b[512,64] into 2^30 outputs):
+// add, sub and mul run two work items per lane in 128-lane workgroups (685 -> 640 us against four
+// in 64-lane ones); divide, with ten times the arithmetic per element, keeps four in 64-lane ones
+// (660 us; 740 us with two in 128).
+#ifndef NC_BIN_S_UNROLL
+#define NC_BIN_S_UNROLL 2
+#endif
+#ifndef NC_BIN_S_BLOCK
+#define NC_BIN_S_BLOCK 128
+#endif
+#ifndef NC_BIN_S_DIV_UNROLL
+#define NC_BIN_S_DIV_UNROLL 4
+#endif
+#ifndef NC_BIN_S_DIV_BLOCK
+#define NC_BIN_S_DIV_BLOCK 64
+#endif
+template <int OP>
+constexpr int small_unroll() { return OP == NC_HIP_BIN_DIV ? NC_BIN_S_DIV_UNROLL : NC_BIN_S_UNROLL; }
+template <int OP>
+constexpr int small_block() { return OP == NC_HIP_BIN_DIV ? NC_BIN_S_DIV_BLOCK : NC_BIN_S_BLOCK; }
+
 template <int OP, int ND, bool U24>
-__global__ __launch_bounds__(kBF) void k_binary_fwd_s(const float *__restrict__ a, const float *__restrict__ b,
-                                                      float *__restrict__ o, SmallMap<ND> m, SmallModes vm,
-                                                      uint32_t nwork) {
-    const uint32_t step = gridDim.x * kBF * kBU;
-    for (uint32_t base = blockIdx.x * kBF * kBU + threadIdx.x; base < nwork; base += step) {
-        f4 x[kBU], y[kBU];
-        uint32_t oo[kBU];
+__global__ __launch_bounds__(small_block<OP>()) void k_binary_fwd_s(const float *__restrict__ a,
+                                                                    const float *__restrict__ b,
+                                                                    float *__restrict__ o, SmallMap<ND> m,
+                                                                    SmallModes vm, uint32_t nwork) {
+    constexpr int kU = small_unroll<OP>(), kBk = small_block<OP>();
+    const uint32_t step = gridDim.x * kBk * kU;
+    for (uint32_t base = blockIdx.x * kBk * kU + threadIdx.x; base < nwork; base += step) {
+        f4 x[kU], y[kU];
+        uint32_t oo[kU];
 #pragma unroll
-        for (int u = 0; u < kBU; u++) {
-            const uint32_t w = base + u * kBF;
+        for (int u = 0; u < kU; u++) {
+            const uint32_t w = base + u * kBk;
             if (w < nwork) {
                 uint32_t off[3];
                 offsets_small<ND, U24>(m, w, off);
@@ -226,8 +249,8 @@ __global__ __launch_bounds__(kBF) void k_binary_fwd_s(const float *__restrict__ 
             }
         }
 #pragma unroll
-        for (int u = 0; u < kBU; u++) {
-            const uint32_t w = base + u * kBF;
+        for (int u = 0; u < kU; u++) {
+            const uint32_t w = base + u * kBk;
             if (w < nwork) {
                 f4 r;
                 r.x = bin<OP>(x[u].x, y[u].x);
@@ -359,7 +382,7 @@ static int small_kind(const Prepared &p, int unit, int64_t nwork) {
 
 template <int OP, int ND, bool U24>
 static void launch_small(const float *a, const float *b, float *o, const IdxMap<3> &full, SmallModes vm,
-                         uint32_t nwork, unsigned grid, hipStream_t st) {
+                         uint32_t nwork, hipStream_t st) {
     SmallMap<ND> m;
     for (int d = 0; d < ND; d++) {
         m.size[d] = full.size[d];
@@ -367,7 +390,9 @@ static void launch_small(const float *a, const float *b, float *o, const IdxMap<
         m.shift[d] = full.div[d].s;
         for (int k = 0; k < 3; k++) m.st[k][d] = (uint32_t)full.st[k][d];
     }
-    hipLaunchKernelGGL((k_binary_fwd_s<OP, ND, U24>), dim3(grid), dim3(kBF), 0, st, a, b, o, m, vm, nwork);
+    constexpr int kU = small_unroll<OP>(), kBk = small_block<OP>();
+    const unsigned grid = stream_grid(((int64_t)nwork + kU - 1) / kU, kBk, NC_BIN_GRID_PER_CU);
+    hipLaunchKernelGGL((k_binary_fwd_s<OP, ND, U24>), dim3(grid), dim3(kBk), 0, st, a, b, o, m, vm, nwork);
 }
 
 template <int OP>
@@ -407,8 +432,8 @@ static int launch_fwd(const float *a, const float *b, float *o, const Prepared &
         SmallModes vm{ma, mb, (uint32_t)p.st[0][inner], (uint32_t)p.st[1][inner]};
         switch (p.nd * 2 + (kind == 2)) {
 #define NC_BIN_SMALL(ND)                                                                                        \
-    case 2 * ND: launch_small<OP, ND, false>(a, b, o, m, vm, (uint32_t)nwork, grid, st); break;                 \
-    case 2 * ND + 1: launch_small<OP, ND, true>(a, b, o, m, vm, (uint32_t)nwork, grid, st); break;
+    case 2 * ND: launch_small<OP, ND, false>(a, b, o, m, vm, (uint32_t)nwork, st); break;                 \
+    case 2 * ND + 1: launch_small<OP, ND, true>(a, b, o, m, vm, (uint32_t)nwork, st); break;
             NC_BIN_SMALL(1)
             NC_BIN_SMALL(2)
             NC_BIN_SMALL(3)
