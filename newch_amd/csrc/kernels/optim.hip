@@ -21,14 +21,10 @@ namespace nchip {
 #ifndef NC_OPT_BLOCK
 #define NC_OPT_BLOCK 64
 #endif
-#ifndef NC_OPT_UNROLL
-#define NC_OPT_UNROLL 1
-#endif
 #ifndef NC_OPT_GRID_PER_CU
 #define NC_OPT_GRID_PER_CU 65536
 #endif
 constexpr int kOB = NC_OPT_BLOCK;
-constexpr int kOU = NC_OPT_UNROLL;
 
 struct OptArgs {
     float lr, momentum, wd, b1, b2, eps, gs, bc1, bc2;
@@ -80,36 +76,24 @@ __device__ __forceinline__ void opt_st(f4 v, f4 *p) {
     else *p = v;
 }
 
+// One float4 of every stream per lane and iteration.  Written as a single load-compute-store body:
+// with the loads and the stores in two separate unrolled loops, the optimizer rebuilt the stores
+// and dropped their non-temporal hint (plain stores: 18% slower at 2^26 parameters).
 template <int KIND, bool S1, bool S2>
 __global__ __launch_bounds__(kOB) void k_optim4(f4 *__restrict__ w, const f4 *__restrict__ g, f4 *__restrict__ s1,
                                                 f4 *__restrict__ s2, int64_t n4, OptArgs a) {
-    const int64_t step = (int64_t)gridDim.x * kOB * kOU;
-    for (int64_t base = (int64_t)blockIdx.x * kOB * kOU + threadIdx.x; base < n4; base += step) {
-        f4 W[kOU], G[kOU], A[kOU], B[kOU];
+    const int64_t step = (int64_t)gridDim.x * kOB;
+    for (int64_t e = (int64_t)blockIdx.x * kOB + threadIdx.x; e < n4; e += step) {
+        const f4 W = opt_ld(w + e), G = __builtin_nontemporal_load(g + e);
+        const f4 A = S1 ? opt_ld(s1 + e) : f4{0.f, 0.f, 0.f, 0.f};
+        const f4 B = S2 ? opt_ld(s2 + e) : f4{0.f, 0.f, 0.f, 0.f};
+        float wv[4] = {W.x, W.y, W.z, W.w}, av[4] = {A.x, A.y, A.z, A.w}, bv[4] = {B.x, B.y, B.z, B.w};
+        const float gv[4] = {G.x, G.y, G.z, G.w};
 #pragma unroll
-        for (int u = 0; u < kOU; u++) {
-            const int64_t e = base + (int64_t)u * kOB;
-            if (e < n4) {
-                W[u] = opt_ld(w + e);
-                G[u] = __builtin_nontemporal_load(g + e);
-                A[u] = S1 ? opt_ld(s1 + e) : f4{0.f, 0.f, 0.f, 0.f};
-                B[u] = S2 ? opt_ld(s2 + e) : f4{0.f, 0.f, 0.f, 0.f};
-            }
-        }
-#pragma unroll
-        for (int u = 0; u < kOU; u++) {
-            const int64_t e = base + (int64_t)u * kOB;
-            if (e < n4) {
-                float wv[4] = {W[u].x, W[u].y, W[u].z, W[u].w}, av[4] = {A[u].x, A[u].y, A[u].z, A[u].w},
-                      bv[4] = {B[u].x, B[u].y, B[u].z, B[u].w};
-                const float gv[4] = {G[u].x, G[u].y, G[u].z, G[u].w};
-#pragma unroll
-                for (int c = 0; c < 4; c++) opt1<KIND, S1>(wv[c], gv[c], av[c], bv[c], a);
-                opt_st(f4{wv[0], wv[1], wv[2], wv[3]}, w + e);
-                if (S1) opt_st(f4{av[0], av[1], av[2], av[3]}, s1 + e);
-                if (S2) opt_st(f4{bv[0], bv[1], bv[2], bv[3]}, s2 + e);
-            }
-        }
+        for (int c = 0; c < 4; c++) opt1<KIND, S1>(wv[c], gv[c], av[c], bv[c], a);
+        opt_st(f4{wv[0], wv[1], wv[2], wv[3]}, w + e);
+        if constexpr (S1) opt_st(f4{av[0], av[1], av[2], av[3]}, s1 + e);
+        if constexpr (S2) opt_st(f4{bv[0], bv[1], bv[2], bv[3]}, s2 + e);
     }
 }
 
@@ -130,7 +114,7 @@ static void launch_opt(float *w, const float *g, float *s1, float *s2, int64_t n
     const bool vec = aligned16(w) && aligned16(g) && (!S1 || aligned16(s1)) && (!S2 || aligned16(s2));
     const int64_t n4 = vec ? n / 4 : 0;
     if (n4 > 0)
-        hipLaunchKernelGGL((k_optim4<KIND, S1, S2>), dim3(stream_grid((n4 + kOU - 1) / kOU, kOB, NC_OPT_GRID_PER_CU)), dim3(kOB), 0, st,
+        hipLaunchKernelGGL((k_optim4<KIND, S1, S2>), dim3(stream_grid(n4, kOB, NC_OPT_GRID_PER_CU)), dim3(kOB), 0, st,
                            (f4 *)w, (const f4 *)g, (f4 *)s1, (f4 *)s2, n4, a);
     const int64_t done = n4 * 4;
     if (done < n)
