@@ -1079,17 +1079,16 @@ def test_engine_optim_errors_match_reference(eng):
     assert calls(eng) == want
 
 
-OPT_KERNEL_CASES = [("sgd", False, False), ("sgd", True, False), ("adam", True, True), ("adamw", True, True),
-                    ("rmsprop", False, True), ("rmsprop", True, True)]
+# (kind, momentum/first-moment state, second state, RMSprop's eps inside the square root)
+OPT_KERNEL_CASES = [("sgd", False, False, False), ("sgd", True, False, False), ("adam", True, True, False),
+                    ("adamw", True, True, False), ("rmsprop", False, True, False), ("rmsprop", True, True, False),
+                    ("rmsprop", False, True, True), ("rmsprop", True, True, True)]
 
 
-@pytest.mark.parametrize("kind,s1,s2", OPT_KERNEL_CASES)
+@pytest.mark.parametrize("kind,s1,s2,inside", OPT_KERNEL_CASES)
 @pytest.mark.parametrize("n,offset", [(1_000_003, 0), (4097, 1)])
-@pytest.mark.parametrize("inside", [False, True])
 def test_kernel_optim_step(K, kind, s1, s2, n, offset, inside):
     """Three updates at a large and a misaligned size, bit for bit against the oracle."""
-    if inside and kind != "rmsprop":
-        pytest.skip("eps_inside_sqrt is RMSprop's")
     rng = np.random.default_rng(zlib.crc32(f"opt/{kind}/{s1}/{s2}/{n}".encode()))
     w = rng.standard_normal(n).astype(np.float32)
     m = np.zeros(n, np.float32) if s1 else None
