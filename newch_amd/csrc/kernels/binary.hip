@@ -946,10 +946,10 @@ __global__ __launch_bounds__(kB2, T >= 8 ? 2 : 4) void k_bcast_bwd2(const float 
 // grad_a[e] (+)= sum over bands of part[p][band][w] (e = p * W + w), bands in order
 template <bool ACC>
 __global__ __launch_bounds__(kB) void k_bwd2_ga_combine(const double *__restrict__ part, float *__restrict__ ga,
-                                                        uint32_t n, uint32_t W, uint32_t nband) {
+                                                        uint32_t n, uint32_t W, IntDiv divW, uint32_t nband) {
     const uint32_t step = gridDim.x * kB;
     for (uint32_t e = blockIdx.x * kB + threadIdx.x; e < n; e += step) {
-        const uint32_t p = e / W, w = e - p * W;
+        const uint32_t p = divW.div(e), w = e - p * W;
         const double *src = part + (size_t)p * nband * W + w;
         double t = 0.0;
         for (uint32_t k = 0; k < nband; k++) t += src[(size_t)k * W];
@@ -1088,9 +1088,10 @@ static int launch_bwd2(const float *g, const float *a, const float *b, float *ga
 #undef NC_B2_LAUNCH
     if ((OUT & 1) && pl.nband > 1) {
         const uint32_t n = pl.P * pl.W4 * 4;
-        const unsigned grid = stream_grid(n, kB);
-        if (acc) hipLaunchKernelGGL((k_bwd2_ga_combine<true>), dim3(grid), dim3(kB), 0, st, ga_part, ga, n, pl.W4 * 4, pl.nband);
-        else hipLaunchKernelGGL((k_bwd2_ga_combine<false>), dim3(grid), dim3(kB), 0, st, ga_part, ga, n, pl.W4 * 4, pl.nband);
+        const unsigned grid = stream_grid(n, kB, 65536);  // one element per lane
+        const IntDiv divW(pl.W4 * 4);
+        if (acc) hipLaunchKernelGGL((k_bwd2_ga_combine<true>), dim3(grid), dim3(kB), 0, st, ga_part, ga, n, pl.W4 * 4, divW, pl.nband);
+        else hipLaunchKernelGGL((k_bwd2_ga_combine<false>), dim3(grid), dim3(kB), 0, st, ga_part, ga, n, pl.W4 * 4, divW, pl.nband);
     }
     if (OUT & 2) {
         const uint32_t n = pl.H * pl.W4 * 4;
