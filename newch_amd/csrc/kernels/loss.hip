@@ -159,7 +159,7 @@ __global__ __launch_bounds__(kCeB) void k_ce_bwd4(const f4 *__restrict__ prob, c
                 const uint32_t r = row4.div((uint32_t)e);
                 rel[u] = lab[r] - 4 * (int32_t)((uint32_t)e - r * per_row);
                 p[u] = __builtin_nontemporal_load(prob + e);
-                o[u] = ACC ? gi[e] : f4{0.f, 0.f, 0.f, 0.f};
+                o[u] = ACC ? __builtin_nontemporal_load(gi + e) : f4{0.f, 0.f, 0.f, 0.f};
             }
         }
 #pragma unroll
@@ -175,7 +175,7 @@ __global__ __launch_bounds__(kCeB) void k_ce_bwd4(const f4 *__restrict__ prob, c
                 if (rel[u] == 1) v.y = v.y - s;
                 if (rel[u] == 2) v.z = v.z - s;
                 if (rel[u] == 3) v.w = v.w - s;
-                gi[e] = v;
+                __builtin_nontemporal_store(v, gi + e);
             }
         }
     }
