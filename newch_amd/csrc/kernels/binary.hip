@@ -1344,6 +1344,14 @@ __global__ __launch_bounds__(kB) void k_fill(T *__restrict__ dst, T v, int64_t n
     for (int64_t i = (int64_t)blockIdx.x * kB + threadIdx.x; i < n; i += step) dst[i] = v;
 }
 
+// 16-byte pattern fill: one non-temporal 128-bit store per lane, 64-lane workgroups over the whole
+// range (the streaming shape that reaches the write ceiling)
+typedef uint32_t u4v __attribute__((ext_vector_type(4)));
+__global__ __launch_bounds__(64) void k_fill16(u4v *__restrict__ dst, u4v v, int64_t n16) {
+    const int64_t i = (int64_t)blockIdx.x * 64 + threadIdx.x;
+    if (i < n16) __builtin_nontemporal_store(v, dst + i);
+}
+
 __global__ void k_add_at(float *p, float v) { p[0] = p[0] + v; }
 
 template <typename S>
@@ -1427,6 +1435,26 @@ extern "C" NC_HIP_API int nc_hip_axpy(int64_t n, float alpha, const float *x, fl
 extern "C" NC_HIP_API int nc_hip_fill(void *dst, int elem_bytes, uint64_t pattern, int64_t n, void *stream) {
     if (n <= 0) return NC_HIP_OK;
     hipStream_t st = as_stream(stream);
+    if ((elem_bytes == 1 || elem_bytes == 2 || elem_bytes == 4 || elem_bytes == 8) && aligned16(dst) &&
+        n * elem_bytes >= 16) {
+        // whole 16-byte blocks with the pattern repeated, then the tail elements below
+        uint64_t w = pattern;
+        if (elem_bytes == 1) w = (w & 0xffu) * 0x0101010101010101ull;
+        else if (elem_bytes == 2) w = (w & 0xffffu) * 0x0001000100010001ull;
+        else if (elem_bytes == 4) w = (w & 0xffffffffu) * 0x0000000100000001ull;
+        const u4v v{(uint32_t)w, (uint32_t)(w >> 32), (uint32_t)w, (uint32_t)(w >> 32)};
+        const int64_t n16 = n * elem_bytes / 16;
+        const int64_t blocks = (n16 + 63) / 64;
+        for (int64_t b0 = 0; b0 < blocks; b0 += INT32_MAX / 2) {  // launches of < 2^30 workgroups
+            const int64_t nb = std::min<int64_t>(blocks - b0, INT32_MAX / 2);
+            hipLaunchKernelGGL(k_fill16, dim3((unsigned)nb), dim3(64), 0, st, (u4v *)dst + b0 * 64,
+                               v, std::min<int64_t>(n16 - b0 * 64, nb * 64));
+        }
+        const int64_t done = n16 * 16 / elem_bytes;
+        if (done == n) return check_launch("nc_hip_fill");
+        dst = (char *)dst + done * elem_bytes;
+        n -= done;
+    }
     const unsigned grid = stream_grid(n, kB, 16);
     switch (elem_bytes) {
     case 1: hipLaunchKernelGGL(k_fill<uint8_t>, grid, kB, 0, st, (uint8_t *)dst, (uint8_t)pattern, n); break;

@@ -1489,3 +1489,23 @@ def test_kernel_gemm_f32_bmm(K, name, bshape, sa, sb, sc):
         want[ic] += A[ia].astype(np.float64) @ B[ib].astype(np.float64)
         terms[ic] += np.abs(A[ia]) @ np.abs(B[ib])
     assert O.gemm_excess(Cd.to_numpy(np.float32, C0.shape), want, terms, Kd * 3) <= 1.0
+
+
+@pytest.mark.parametrize("elem", [1, 2, 4, 8])
+@pytest.mark.parametrize("n,offset", [(1, 0), (3, 1), (17, 0), (17, 3), (4096, 0), (1_000_003, 0), (1_000_003, 5)])
+def test_kernel_fill(K, elem, n, offset):
+    """Pattern fill (the zero-gradient and cache-flush fill): 16-byte vector blocks plus a scalar
+    tail, or the scalar kernel when the start is not 16-byte aligned; bytes around the range keep
+    their values."""
+    dt = {1: np.uint8, 2: np.uint16, 4: np.uint32, 8: np.uint64}[elem]
+    rng = np.random.default_rng(zlib.crc32(f"fill/{elem}/{n}/{offset}".encode()))
+    guard = 64
+    buf = rng.integers(0, np.iinfo(dt).max, size=offset + n + guard, dtype=dt)
+    pattern = int(rng.integers(1, np.iinfo(dt).max, dtype=dt))
+    D = dev(buf)
+    K.fill(D.ptr + offset * elem, elem, pattern, n)
+    sync()
+    got = D.to_numpy(dt, buf.size)
+    want = buf.copy()
+    want[offset:offset + n] = pattern
+    assert_bits(got, want, f"fill elem={elem} n={n} offset={offset}")
