@@ -488,6 +488,27 @@ __global__ __launch_bounds__(kB) void k_grad_elementwise(const float *__restrict
     }
 }
 
+// The same for contiguous, 16-byte aligned operands of one shape (residual and elementwise-product
+// backward): one float4 of each stream per lane, non-temporal, a grid over the whole range.
+template <int MODE, bool ACC>
+__global__ __launch_bounds__(64) void k_grad_elementwise4(const f4 *__restrict__ g, const f4 *__restrict__ p1,
+                                                          const f4 *__restrict__ p2, f4 *__restrict__ gx, int64_t n4,
+                                                          float alpha) {
+    const int64_t i = (int64_t)blockIdx.x * 64 + threadIdx.x;
+    if (i >= n4) return;
+    const f4 z = f4{0.f, 0.f, 0.f, 0.f};
+    const f4 gg = __builtin_nontemporal_load(g + i);
+    const f4 a = MODE == 1 || MODE == 2 || MODE == 3 ? __builtin_nontemporal_load(p1 + i) : z;
+    const f4 b = MODE == 3 ? __builtin_nontemporal_load(p2 + i) : z;
+    const f4 o = ACC ? __builtin_nontemporal_load(gx + i) : z;
+    f4 r;
+    r.x = grad_f<MODE>(o.x, gg.x, a.x, b.x, alpha);
+    r.y = grad_f<MODE>(o.y, gg.y, a.y, b.y, alpha);
+    r.z = grad_f<MODE>(o.z, gg.z, a.z, b.z, alpha);
+    r.w = grad_f<MODE>(o.w, gg.w, a.w, b.w, alpha);
+    __builtin_nontemporal_store(r, gx + i);
+}
+
 // Reduced grads.  The coalesced dims split into kept dims (gx stride != 0) and reduced dims.
 struct RedPlan {
     IdxMap<4> kept;      // over the M kept indices (gx offsets in operand 3)
@@ -684,6 +705,20 @@ static int launch_grad(const float *g, const float *p1, const float *p2, float *
             q.nd = 1;
             q.shape[0] = 1;
             for (int o = 0; o < 4; o++) q.st[o][0] = 0;
+        }
+        constexpr bool R1 = MODE == 1 || MODE == 2 || MODE == 3, R2 = MODE == 3;
+        if (q.nd == 1 && q.numel % 4 == 0 && q.st[0][0] == 1 && q.st[3][0] == 1 && (!R1 || q.st[1][0] == 1) &&
+            (!R2 || q.st[2][0] == 1) && aligned16(g) && aligned16(gx) && (!R1 || aligned16(p1)) &&
+            (!R2 || aligned16(p2))) {
+            const int64_t n4 = q.numel / 4;
+            const dim3 grid4((unsigned)((n4 + 63) / 64));
+            if (acc)
+                hipLaunchKernelGGL((k_grad_elementwise4<MODE, true>), grid4, dim3(64), 0, st, (const f4 *)g,
+                                   (const f4 *)p1, (const f4 *)p2, (f4 *)gx, n4, alpha);
+            else
+                hipLaunchKernelGGL((k_grad_elementwise4<MODE, false>), grid4, dim3(64), 0, st, (const f4 *)g,
+                                   (const f4 *)p1, (const f4 *)p2, (f4 *)gx, n4, alpha);
+            return check_launch("nc_hip_binary_bwd");
         }
         IdxMap<4> m;
         make_map<4>(q, 1, m);

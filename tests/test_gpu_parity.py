@@ -435,6 +435,7 @@ BCAST = [
     ("row", (1000, 37), None, (37,)),
     ("col", (513, 1), None, (513, 7)),
     ("same", (123, 457), None, (123, 457)),
+    ("same_vec", (96, 256), None, (96, 256)),  # same-shape grads through the 128-bit kernel
     ("same_t", (457, 123), ("t", 0, 1), (123, 457)),
     ("scalar", (), None, (5, 6)),
 ]
