@@ -172,7 +172,7 @@ struct SmallMap {
 };
 
 struct SmallModes {
-    int a, b;        // 0 splat, 1 vector, 2 gather
+    int a, b;        // 0 splat, 1 vector, 2 gather, 3 vector read once (no broadcast dim)
     uint32_t ia, ib; // inner element strides (for gathers)
 };
 
@@ -198,6 +198,7 @@ __device__ __forceinline__ void offsets_small(const SmallMap<ND> &m, uint32_t w,
 }
 
 __device__ __forceinline__ f4 load4s(const float *p, uint32_t is, int mode) {
+    if (mode == 3) return __builtin_nontemporal_load((const f4 *)p);  // read once: streamed past the caches
     if (mode == 1) return *(const f4 *)p;
     if (mode == 0) {
         const float v = *p;
@@ -429,7 +430,14 @@ static int launch_fwd(const float *a, const float *b, float *o, const Prepared &
     const unsigned grid = stream_grid((nwork + kBU - 1) / kBU, kBF, NC_BIN_GRID_PER_CU);
     const int kind = vec && NC_BIN_SMALL_INDEX ? small_kind(p, unit, nwork) : 0;
     if (kind) {
-        SmallModes vm{ma, mb, (uint32_t)p.st[0][inner], (uint32_t)p.st[1][inner]};
+        // an operand with no broadcast dim is read once: non-temporal loads
+        auto once = [&](int k) {
+            for (int d = 0; d < p.nd; d++)
+                if (p.st[k][d] == 0 && p.shape[d] > 1) return false;
+            return true;
+        };
+        SmallModes vm{ma == 1 && once(0) ? 3 : ma, mb == 1 && once(1) ? 3 : mb, (uint32_t)p.st[0][inner],
+                      (uint32_t)p.st[1][inner]};
         switch (p.nd * 2 + (kind == 2)) {
 #define NC_BIN_SMALL(ND)                                                                                        \
     case 2 * ND: launch_small<OP, ND, false>(a, b, o, m, vm, (uint32_t)nwork, st); break;                 \
