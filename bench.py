@@ -10,9 +10,11 @@ read x, write y; backward 16 B/element: read x or y, read g, read+write gi) over
 time.  Every kernel launch is bracketed by HIP events on the launch stream; the per-kernel averages
 give `classes` (GB/s per op class, also for the broadcast / row-reduction / int8 / full-sum
 workloads unless --classes none; `gemm`: TFLOP/s against the matrix-core peaks for the fp32 and int8
-linear / batched-matmul contractions) and the `roofline` of the dominant kernel.  `cpu_baseline` times
-the reference engine (oracle/_ref/libnc_ref.so, its own threaded AVX2 path) on a bounded sample of
-the same work.  Prints one JSON line.
+linear / batched-matmul contractions) and the `roofline` of the dominant kernel; `chain` is the
+launch-bound MNIST-CNN chain (add-bias, ReLU, two sums, backward) through the engine's nc.h API, in
+microseconds per iteration.  `cpu_baseline` times the reference engine (oracle/_ref/libnc_ref.so, its
+own threaded AVX2 path) on a bounded sample of the same work, and the same chain.  Prints one JSON
+line.
 """
 
 from __future__ import annotations
@@ -306,6 +308,51 @@ def measured_traffic(label: str):
     return int(round((f / scale["fetch_scale"] + w / scale["write_scale"]) * 1024))
 
 
+def chain_latency(lib_path=None, iters: int = 200, warmup: int = 10, threads: int = 0):
+    """The chain of the MNIST-CNN configuration through an nc.h engine, as the reference's Python
+    layer drives it: h = relu(x + bias) for x[64,16,28,28]~U(-1,1) (seed 0) and bias[1,16,1,1]~U(-0.1,
+    0.1) (the same stream, next), s = h.sum(3).sum(2), s.sum().backward(), zero_grad, step_end.
+    Returns microseconds per iteration (host wall time, the device synchronised every iteration)."""
+    import ctypes
+
+    from newch_amd import abi
+
+    L = abi.load(lib_path)
+    cfg = abi.Config(0, 0, 0, threads)
+    ctx = L.nc_init(ctypes.byref(cfg))
+    rng = np.random.default_rng(0)
+    x = rng.uniform(-1, 1, (64, 16, 28, 28)).astype(np.float32)
+    b = rng.uniform(-0.1, 0.1, (1, 16, 1, 1)).astype(np.float32)
+
+    def param(arr):
+        nd, shp = abi.shape_arg(arr.shape)
+        src = L.nc_from_data(ctx, abi.F32, arr.ctypes.data_as(ctypes.c_void_p), nd, shp)
+        return L.nc_parameter(ctx, src, nd, shp)
+
+    px, pb = param(x), param(b)
+    sync = getattr(L, "nc_synchronize", None)
+
+    def one():
+        h = L.nc_relu(L.nc_add(px, pb))
+        s = L.nc_sum(L.nc_sum(h, 3, 1), 2, 1)
+        L.nc_backward(L.nc_sum(s, abi.ALL_AXES, 0))
+        if sync is not None:
+            sync(ctx)
+        L.nc_zero_grad(px)
+        L.nc_zero_grad(pb)
+        L.nc_step_end(ctx)
+
+    for _ in range(warmup):
+        one()
+    t0 = time.perf_counter()
+    for _ in range(iters):
+        one()
+    el = time.perf_counter() - t0
+    ok = L.nc_ok(ctx)
+    L.nc_free_ctx(ctx)
+    return round(el / iters * 1e6, 1) if ok else None
+
+
 def cpu_baseline(budget_s: float = 12.0):
     """The reference engine on host cores: y = f(x); y.sum().backward() per activation (the
     reference's own activation benchmark, tools/bench_act.py:46-52) over a 2^22-element sample."""
@@ -344,12 +391,15 @@ def cpu_baseline(budget_s: float = 12.0):
     L.nc_free_ctx(ctx)
     if not ok:
         return None
+    chain_us = chain_latency(pyoracle.REF_LIB, iters=50, warmup=3, threads=threads)
     el_per_s = reps * n * len(ACTS) / el
     return {"value": round(el_per_s * 24 / 1e9, 2), "unit": "GB/s", "elements_per_s": round(el_per_s / 1e6, 1),
             "elements_unit": "M el/s", "cores": threads, "kind": "reference",
             "sample": f"2^22 fp32 elements, {reps} reps of y=f(x); y.sum().backward() for {', '.join(ACTS)} "
                       f"on the reference engine ({backend} kernel tier), "
-                      f"{el:.1f} s; GB/s counts the same 24 B/element as the GPU value"}
+                      f"{el:.1f} s; GB/s counts the same 24 B/element as the GPU value",
+            "chain_us": chain_us,
+            "chain_sample": "the MNIST-CNN chain (as `chain`), 50 iterations on the reference engine"}
 
 
 def main():
@@ -444,6 +494,8 @@ def main():
             log(f"bench: {label:28s} {rate:8.1f} T/s  {100 * rate / peak:5.1f}% of {peak}  {ms * 1e3:9.1f} us")
         del gkeep
 
+    chain_us = chain_latency()
+    log(f"bench: MNIST-CNN chain fwd+bwd through the engine {chain_us} us per iteration")
     cpu = None if args.no_cpu else cpu_baseline()
     if cpu:
         log(f"bench: cpu baseline {cpu['value']} GB/s ({cpu['elements_per_s']} M el/s) on {cpu['cores']} threads")
@@ -471,6 +523,9 @@ def main():
         "cpu_baseline": cpu,
         "classes": classes,
         "gemm": gemm,
+        "chain": {"workload": "MNIST-CNN chain through nc.h: relu(x[64,16,28,28] + bias[1,16,1,1]), sum over "
+                              "dims 3 then 2, sum().backward(), zero_grad, step_end (802,816 elements; "
+                              "launch-bound)", "us_per_iter": chain_us},
     }
     print(json.dumps(line), flush=True)
 
