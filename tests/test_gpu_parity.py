@@ -953,6 +953,10 @@ def test_kernel_cross_entropy_nan_rows(K):
     x = rng.standard_normal((N, C)).astype(np.float32)
     x[1, 0] = np.nan
     x[3, 5] = np.nan
+    # row 4: a logit 87 below the maximum (x - max stays above exp8's lower clamp, its log-probability
+    # falls below it); row 5: one 200 below (x - max itself under the clamp)
+    x[4, 2] = x[4].max() - 87.0
+    x[5, 6] = np.float32(-200.0)
     lab = np.arange(N, dtype=np.int32) % C
     Xd, Ld = dev(x), dev(lab)
     P, LS, BAD = empty(4 * N * C), empty(4), empty(8)
