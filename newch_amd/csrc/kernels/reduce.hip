@@ -110,10 +110,7 @@ __global__ __launch_bounds__(kRB) void k_rows_wave(const float *__restrict__ x, 
                 for (int k = 0; k < 4; k++)
                     if (lane + k * kWave < nv) q[k] = __builtin_nontemporal_load(row + lane + k * kWave);
             };
-            f4 q[4], qn[4];
-            if (wave < outer) load(wave, q);
-            for (int64_t o = wave; o < outer; o += nwaves) {
-                if (o + nwaves < outer) load(o + nwaves, qn);
+            auto process = [&](int64_t o, const f4 *q) {
                 Acc<KIND> acc;
                 acc.init();
 #pragma unroll
@@ -128,8 +125,23 @@ __global__ __launch_bounds__(kRB) void k_rows_wave(const float *__restrict__ x, 
                 }
                 acc.wave();
                 if (lane == 0) emit<KIND>(acc, q[0].x, scale, y, arg, o);
-#pragma unroll
-                for (int k = 0; k < 4; k++) q[k] = qn[k];
+            };
+            // two register bundles in turn, every steady-state load unconditional
+            int64_t o = wave;
+            f4 A[4], B[4];
+            if (o < outer) load(o, A);
+            while (o + 2 * nwaves < outer) {
+                load(o + nwaves, B);
+                process(o, A);
+                load(o + 2 * nwaves, A);
+                process(o + nwaves, B);
+                o += 2 * nwaves;
+            }
+            if (o < outer) {
+                const bool hb = o + nwaves < outer;
+                if (hb) load(o + nwaves, B);
+                process(o, A);
+                if (hb) process(o + nwaves, B);
             }
             return;
         }

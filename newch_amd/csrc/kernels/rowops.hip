@@ -268,11 +268,9 @@ __global__ __launch_bounds__(kRowB) void k_ln_fwd_reg(const float *__restrict__ 
         for (int k = 0; k < VPL; k++)
             if (lane + k * kWave < nv) v[k] = __builtin_nontemporal_load(xr + lane + k * kWave);
     };
-    const int64_t r0 = ((int64_t)blockIdx.x * kRowB + threadIdx.x) / kWave;
-    f4 v[VPL], vn[VPL];
-    if (r0 < rows) load(r0, v);
-    for (int64_t r = r0; r < rows; r += stride) {
-        if (r + stride < rows) load(r + stride, vn);
+    // rows of this wave: r0, r0 + stride, ...; two register bundles in turn, every steady-state load
+    // unconditional
+    auto process = [&](int64_t r, const f4 *v) {
         double s = 0.0;
 #pragma unroll
         for (int k = 0; k < VPL; k++) {
@@ -309,8 +307,22 @@ __global__ __launch_bounds__(kRowB) void k_ln_fwd_reg(const float *__restrict__ 
                 __builtin_nontemporal_store(o, yr + j);
             }
         }
-#pragma unroll
-        for (int k = 0; k < VPL; k++) v[k] = vn[k];
+    };
+    int64_t r = ((int64_t)blockIdx.x * kRowB + threadIdx.x) / kWave;
+    f4 A[VPL], B[VPL];
+    if (r < rows) load(r, A);
+    while (r + 2 * stride < rows) {
+        load(r + stride, B);
+        process(r, A);
+        load(r + 2 * stride, A);
+        process(r + stride, B);
+        r += 2 * stride;
+    }
+    if (r < rows) {
+        const bool hb = r + stride < rows;
+        if (hb) load(r + stride, B);
+        process(r, A);
+        if (hb) process(r + stride, B);
     }
 }
 
