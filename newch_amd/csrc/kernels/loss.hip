@@ -58,9 +58,18 @@ __global__ __launch_bounds__(kLB) void k_ce_fwd_reg(const float *__restrict__ x,
             if (lane + k * kWave < nv) v[k] = __builtin_nontemporal_load(xr + lane + k * kWave);
     };
     double acc = 0.0;  // log-probabilities of the labels this lane holds
-    // rows of this wave: r0, r0 + stride, ...; two register bundles (row and label) in turn, every
-    // steady-state load unconditional
-    auto process = [&](int64_t r, f4 *v, int32_t L) {
+    const int64_t r0 = ((int64_t)blockIdx.x * kLB + threadIdx.x) / kWave;
+    f4 v[VPL], vn[VPL];
+    int32_t L = 0, Ln = 0;
+    if (r0 < N) {
+        load(r0, v);
+        L = lab[r0];
+    }
+    for (int64_t r = r0; r < N; r += stride) {
+        if (r + stride < N) {
+            load(r + stride, vn);
+            Ln = lab[r + stride];
+        }
         const bool ok = L >= 0 && L < C;
         if (!ok && lane == 0) flag_bad(bad, r, L);
         float m = -__builtin_inff();
@@ -89,31 +98,9 @@ __global__ __launch_bounds__(kLB) void k_ce_fwd_reg(const float *__restrict__ x,
                 __builtin_nontemporal_store(f4{exp8_nonpos(lp[0]), exp8_nonpos(lp[1]), exp8_nonpos(lp[2]), exp8_nonpos(lp[3])}, pr + j);
             }
         }
-    };
-    int64_t r = ((int64_t)blockIdx.x * kLB + threadIdx.x) / kWave;
-    f4 A[VPL], B[VPL];
-    int32_t LA = 0, LB = 0;
-    if (r < N) {
-        load(r, A);
-        LA = lab[r];
-    }
-    while (r + 2 * stride < N) {
-        load(r + stride, B);
-        LB = lab[r + stride];
-        process(r, A, LA);
-        load(r + 2 * stride, A);
-        LA = lab[r + 2 * stride];
-        process(r + stride, B, LB);
-        r += 2 * stride;
-    }
-    if (r < N) {
-        const bool hb = r + stride < N;
-        if (hb) {
-            load(r + stride, B);
-            LB = lab[r + stride];
-        }
-        process(r, A, LA);
-        if (hb) process(r + stride, B, LB);
+#pragma unroll
+        for (int k = 0; k < VPL; k++) v[k] = vn[k];
+        L = Ln;
     }
     const double t = block_sum_ordered(acc);
     if (threadIdx.x == 0) part[blockIdx.x] = t;

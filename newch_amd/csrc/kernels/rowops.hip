@@ -33,10 +33,11 @@ __global__ __launch_bounds__(kRowB) void k_softmax_fwd_reg(const float *__restri
         for (int k = 0; k < VPL; k++)
             if (lane + k * kWave < nv) v[k] = __builtin_nontemporal_load(xr + lane + k * kWave);
     };
-    // rows of this wave: r0, r0 + stride, ...; two register bundles in turn, every steady-state load
-    // unconditional (a prefetch buffer copied forward at each row end made the compiler wait for the
-    // prefetched row before going on)
-    auto process = [&](int64_t r, f4 *v) {
+    const int64_t r0 = ((int64_t)blockIdx.x * kRowB + threadIdx.x) / kWave;
+    f4 v[VPL], vn[VPL];
+    if (r0 < rows) load(r0, v);
+    for (int64_t r = r0; r < rows; r += stride) {
+        if (r + stride < rows) load(r + stride, vn);
         float m = -__builtin_inff();
 #pragma unroll
         for (int k = 0; k < VPL; k++) {
@@ -90,22 +91,8 @@ __global__ __launch_bounds__(kRowB) void k_softmax_fwd_reg(const float *__restri
                 }
             }
         }
-    };
-    int64_t r = ((int64_t)blockIdx.x * kRowB + threadIdx.x) / kWave;
-    f4 A[VPL], B[VPL];
-    if (r < rows) load(r, A);
-    while (r + 2 * stride < rows) {
-        load(r + stride, B);
-        process(r, A);
-        load(r + 2 * stride, A);
-        process(r + stride, B);
-        r += 2 * stride;
-    }
-    if (r < rows) {
-        const bool hb = r + stride < rows;
-        if (hb) load(r + stride, B);
-        process(r, A);
-        if (hb) process(r + stride, B);
+#pragma unroll
+        for (int k = 0; k < VPL; k++) v[k] = vn[k];
     }
 }
 
@@ -268,9 +255,11 @@ __global__ __launch_bounds__(kRowB) void k_ln_fwd_reg(const float *__restrict__ 
         for (int k = 0; k < VPL; k++)
             if (lane + k * kWave < nv) v[k] = __builtin_nontemporal_load(xr + lane + k * kWave);
     };
-    // rows of this wave: r0, r0 + stride, ...; two register bundles in turn, every steady-state load
-    // unconditional
-    auto process = [&](int64_t r, const f4 *v) {
+    const int64_t r0 = ((int64_t)blockIdx.x * kRowB + threadIdx.x) / kWave;
+    f4 v[VPL], vn[VPL];
+    if (r0 < rows) load(r0, v);
+    for (int64_t r = r0; r < rows; r += stride) {
+        if (r + stride < rows) load(r + stride, vn);
         double s = 0.0;
 #pragma unroll
         for (int k = 0; k < VPL; k++) {
@@ -307,22 +296,8 @@ __global__ __launch_bounds__(kRowB) void k_ln_fwd_reg(const float *__restrict__ 
                 __builtin_nontemporal_store(o, yr + j);
             }
         }
-    };
-    int64_t r = ((int64_t)blockIdx.x * kRowB + threadIdx.x) / kWave;
-    f4 A[VPL], B[VPL];
-    if (r < rows) load(r, A);
-    while (r + 2 * stride < rows) {
-        load(r + stride, B);
-        process(r, A);
-        load(r + 2 * stride, A);
-        process(r + stride, B);
-        r += 2 * stride;
-    }
-    if (r < rows) {
-        const bool hb = r + stride < rows;
-        if (hb) load(r + stride, B);
-        process(r, A);
-        if (hb) process(r + stride, B);
+#pragma unroll
+        for (int k = 0; k < VPL; k++) v[k] = vn[k];
     }
 }
 
@@ -776,12 +751,9 @@ static int vpl_for(int64_t C) {
 #ifndef NC_ROWS_GRID_PER_CU
 #define NC_ROWS_GRID_PER_CU 65536
 #endif
-#ifndef NC_SOFTMAX_GRID_PER_CU
-#define NC_SOFTMAX_GRID_PER_CU 65536  // a grid over all rows (one per wave) measured best
-#endif
-static unsigned rows_grid(int64_t rows, int64_t per_cu = NC_ROWS_GRID_PER_CU) {
+static unsigned rows_grid(int64_t rows) {
     const int64_t blocks = (rows + kWavesPerBlock - 1) / kWavesPerBlock;
-    const int64_t cap = (int64_t)num_cus() * per_cu;
+    const int64_t cap = (int64_t)num_cus() * NC_ROWS_GRID_PER_CU;
     return (unsigned)(blocks < cap ? blocks : cap);
 }
 
@@ -857,8 +829,8 @@ extern "C" NC_HIP_API int nc_hip_softmax_fwd(int log_form, int64_t rows, int64_t
     hipStream_t st = as_stream(stream);
     const int v = (C % 4 == 0 && aligned16(x) && aligned16(y)) ? vpl_for(C) : 0;
     if (v) {
-        if (log_form) NC_VPL_SWITCH(v, hipLaunchKernelGGL((k_softmax_fwd_reg<VP, true>), rows_grid(rows, NC_SOFTMAX_GRID_PER_CU), kRowB, 0, st, x, y, rows, (int)C))
-        else NC_VPL_SWITCH(v, hipLaunchKernelGGL((k_softmax_fwd_reg<VP, false>), rows_grid(rows, NC_SOFTMAX_GRID_PER_CU), kRowB, 0, st, x, y, rows, (int)C))
+        if (log_form) NC_VPL_SWITCH(v, hipLaunchKernelGGL((k_softmax_fwd_reg<VP, true>), rows_grid(rows), kRowB, 0, st, x, y, rows, (int)C))
+        else NC_VPL_SWITCH(v, hipLaunchKernelGGL((k_softmax_fwd_reg<VP, false>), rows_grid(rows), kRowB, 0, st, x, y, rows, (int)C))
     } else {
         const unsigned grid = (unsigned)(rows < num_cus() * 8 ? rows : num_cus() * 8);
         if (log_form) hipLaunchKernelGGL(k_softmax_fwd_blk<true>, grid, kRowB, 0, st, x, y, rows, C);
