@@ -1,7 +1,7 @@
 /* CPU oracle for the newch hot path -- TEST INFRASTRUCTURE ONLY.
  *
  * A from-scratch C restatement of the reference engine's arithmetic on this path, used by tests/,
- * __graft_entry__.smoke() and bench.py's cpu_baseline leg as the checker.  The product library
+ * __graft_entry__.smoke() and bench.py's cpu_baseline leg to check results against.  The product library
  * (newch_amd/libnc.so) never links or calls it.
  *
  * Every function follows the reference's evaluation order op for op (file:line cited at each

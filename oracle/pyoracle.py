@@ -1,7 +1,7 @@
 """numpy wrappers over the C oracle (oracle/_build/liboracle.so) -- TEST INFRASTRUCTURE ONLY.
 
-Imported by tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg, as the checker / CPU
-baseline.  The product library never uses it.  Function semantics: see oracle.h.
+Imported by tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg, to check results
+against and as the CPU baseline.  The product library never uses it.  Function semantics: see oracle.h.
 """
 
 from __future__ import annotations
