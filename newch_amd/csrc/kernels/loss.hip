@@ -11,7 +11,8 @@
 // Loss sums: fp64 per lane (or per thread), wave sums, workgroup partials added in wave order, and
 // one ordered combine (k_loss_finish): loss = -S / N (mean; NaN for N = 0, 0/0 as the reference) or
 // -S (sum).  A label outside [0, C) contributes nothing; the first such row is reported in *bad as
-// (row << 32) | (uint32)label through a 64-bit atomic minimum (all ones when every label is valid),
+// (row << 32) | (uint32)label, each workgroup's minimum key written beside its loss partial and the
+// minimum taken in the final combine (all ones when every label is valid: no separate initialising launch),
 // for the caller to raise the reference's error.
 #include "common.hpp"
 #include "intdiv.hpp"
@@ -24,8 +25,24 @@ constexpr int kLB = 256;  // 4 waves
 constexpr int kLWaves = kLB / kWave;
 constexpr unsigned long long kNoBad = ~0ull;
 
-__device__ __forceinline__ void flag_bad(unsigned long long *bad, int64_t row, int32_t lab) {
-    atomicMin(bad, ((unsigned long long)row << 32) | (uint32_t)lab);
+__device__ __forceinline__ unsigned long long bad_key(int64_t row, int32_t lab) {
+    return ((unsigned long long)row << 32) | (uint32_t)lab;
+}
+
+// minimum over the workgroup of the lanes' first-bad-row keys; thread 0 returns it
+__device__ __forceinline__ unsigned long long block_min_key(unsigned long long v) {
+    __shared__ unsigned long long shk[kLWaves];
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+        const unsigned long long u = __shfl_xor(v, o, kWave);
+        v = u < v ? u : v;
+    }
+    if ((threadIdx.x & (kWave - 1)) == 0) shk[threadIdx.x / kWave] = v;
+    __syncthreads();
+    unsigned long long t = kNoBad;
+    if (threadIdx.x == 0)
+        for (int i = 0; i < kLWaves; i++) t = shk[i] < t ? shk[i] : t;
+    return t;
 }
 
 // sum of this workgroup's per-thread fp64 values, waves added in order; thread 0 returns it
@@ -40,14 +57,10 @@ __device__ __forceinline__ double block_sum_ordered(double v) {
     return t;
 }
 
-__global__ void k_init_bad(unsigned long long *bad) {
-    if (threadIdx.x == 0 && blockIdx.x == 0) *bad = kNoBad;
-}
-
 template <int VPL>
 __global__ __launch_bounds__(kLB) void k_ce_fwd_reg(const float *__restrict__ x, const int32_t *__restrict__ lab,
                                                     float *__restrict__ prob, double *__restrict__ part,
-                                                    unsigned long long *__restrict__ bad, int64_t N, int C) {
+                                                    unsigned long long *__restrict__ badpart, int64_t N, int C) {
     const int lane = threadIdx.x & (kWave - 1);
     const int nv = C / 4;
     const int64_t stride = (int64_t)gridDim.x * kLWaves;
@@ -58,6 +71,7 @@ __global__ __launch_bounds__(kLB) void k_ce_fwd_reg(const float *__restrict__ x,
             if (lane + k * kWave < nv) v[k] = __builtin_nontemporal_load(xr + lane + k * kWave);
     };
     double acc = 0.0;  // log-probabilities of the labels this lane holds
+    unsigned long long mybad = kNoBad;  // first row with an out-of-range label among this wave's
     const int64_t r0 = ((int64_t)blockIdx.x * kLB + threadIdx.x) / kWave;
     f4 v[VPL], vn[VPL];
     int32_t L = 0, Ln = 0;
@@ -71,7 +85,7 @@ __global__ __launch_bounds__(kLB) void k_ce_fwd_reg(const float *__restrict__ x,
             Ln = lab[r + stride];
         }
         const bool ok = L >= 0 && L < C;
-        if (!ok && lane == 0) flag_bad(bad, r, L);
+        if (!ok) mybad = bad_key(r, L) < mybad ? bad_key(r, L) : mybad;
         float m = -__builtin_inff();
 #pragma unroll
         for (int k = 0; k < VPL; k++) {
@@ -103,30 +117,49 @@ __global__ __launch_bounds__(kLB) void k_ce_fwd_reg(const float *__restrict__ x,
         L = Ln;
     }
     const double t = block_sum_ordered(acc);
-    if (threadIdx.x == 0) part[blockIdx.x] = t;
+    const unsigned long long kb = block_min_key(mybad);
+    if (threadIdx.x == 0) {
+        part[blockIdx.x] = t;
+        badpart[blockIdx.x] = kb;
+    }
 }
 
 // one thread per row: -x[i, lab_i] into fp64 per-thread sums, workgroup partials
 __global__ __launch_bounds__(kLB) void k_label_gather(const float *__restrict__ x, const int32_t *__restrict__ lab,
-                                                      double *__restrict__ part, unsigned long long *__restrict__ bad,
+                                                      double *__restrict__ part, unsigned long long *__restrict__ badpart,
                                                       int64_t N, int64_t C) {
     double acc = 0.0;
+    unsigned long long mybad = kNoBad;
     for (int64_t r = (int64_t)blockIdx.x * kLB + threadIdx.x; r < N; r += (int64_t)gridDim.x * kLB) {
         const int32_t L = lab[r];
         if (L >= 0 && L < C) acc -= (double)x[r * C + L];
-        else flag_bad(bad, r, L);
+        else mybad = bad_key(r, L) < mybad ? bad_key(r, L) : mybad;
     }
     const double t = block_sum_ordered(acc);
-    if (threadIdx.x == 0) part[blockIdx.x] = t;
+    const unsigned long long kb = block_min_key(mybad);
+    if (threadIdx.x == 0) {
+        part[blockIdx.x] = t;
+        badpart[blockIdx.x] = kb;
+    }
 }
 
 // loss from the ordered partials: S = sum (already negated terms); mean -> S / N (NaN for N = 0)
-__global__ __launch_bounds__(kLB) void k_loss_finish(const double *__restrict__ part, int nparts, int64_t N, int sum,
-                                                     float *__restrict__ loss) {
+__global__ __launch_bounds__(kLB) void k_loss_finish(const double *__restrict__ part,
+                                                     const unsigned long long *__restrict__ badpart, int nparts,
+                                                     int64_t N, int sum, float *__restrict__ loss,
+                                                     unsigned long long *__restrict__ bad) {
     double t = 0.0;
-    for (int i = threadIdx.x; i < nparts; i += kLB) t += part[i];
+    unsigned long long kb = kNoBad;
+    for (int i = threadIdx.x; i < nparts; i += kLB) {
+        t += part[i];
+        kb = badpart[i] < kb ? badpart[i] : kb;
+    }
     const double S = block_sum_ordered(t);
-    if (threadIdx.x == 0) *loss = sum ? (float)S : N ? (float)(S / (double)N) : __builtin_nanf("");
+    kb = block_min_key(kb);
+    if (threadIdx.x == 0) {
+        *loss = sum ? (float)S : N ? (float)(S / (double)N) : __builtin_nanf("");
+        *bad = kb;
+    }
 }
 
 // gi (+)= s * prob; gi[i, lab_i] -= s, s = gout / N.  A lane owns float4 items (four consecutive
@@ -223,6 +256,9 @@ static unsigned gather_grid(int64_t N) {
     return (unsigned)std::max<int64_t>(1, std::min(blocks, cap));
 }
 
+// workgroup partials of either forward: fp64 loss sums, then first-bad-row keys
+static int64_t loss_parts(int64_t N) { return std::max(ce_grid(N), gather_grid(N)); }
+
 }  // namespace nchip
 
 using namespace nchip;
@@ -230,7 +266,7 @@ using namespace nchip;
 extern "C" NC_HIP_API size_t nc_hip_loss_workspace(int64_t N, int64_t C) {
     (void)C;
     if (N < 0) return 0;
-    return (size_t)std::max(ce_grid(N), gather_grid(N)) * sizeof(double);
+    return (size_t)loss_parts(N) * (sizeof(double) + sizeof(unsigned long long));
 }
 
 extern "C" NC_HIP_API int nc_hip_cross_entropy_fwd(int64_t N, int64_t C, const float *x, const int32_t *lab,
@@ -246,18 +282,18 @@ extern "C" NC_HIP_API int nc_hip_cross_entropy_fwd(int64_t N, int64_t C, const f
     hipStream_t st = as_stream(stream);
     unsigned long long *b = (unsigned long long *)bad;
     double *part = (double *)ws;
-    hipLaunchKernelGGL(k_init_bad, 1, 1, 0, st, b);
+    unsigned long long *bp = (unsigned long long *)(part + loss_parts(N));
     int nparts = 0;
     if (N > 0) {
         const int vpl = (C % 4 == 0 && aligned16(x) && aligned16(prob)) ? vpl_for_row(C) : 0;
         if (vpl) {
             const unsigned grid = ce_grid(N);
             switch (vpl) {
-            case 1: hipLaunchKernelGGL(k_ce_fwd_reg<1>, grid, kLB, 0, st, x, lab, prob, part, b, N, (int)C); break;
-            case 2: hipLaunchKernelGGL(k_ce_fwd_reg<2>, grid, kLB, 0, st, x, lab, prob, part, b, N, (int)C); break;
-            case 4: hipLaunchKernelGGL(k_ce_fwd_reg<4>, grid, kLB, 0, st, x, lab, prob, part, b, N, (int)C); break;
-            case 8: hipLaunchKernelGGL(k_ce_fwd_reg<8>, grid, kLB, 0, st, x, lab, prob, part, b, N, (int)C); break;
-            default: hipLaunchKernelGGL(k_ce_fwd_reg<16>, grid, kLB, 0, st, x, lab, prob, part, b, N, (int)C); break;
+            case 1: hipLaunchKernelGGL(k_ce_fwd_reg<1>, grid, kLB, 0, st, x, lab, prob, part, bp, N, (int)C); break;
+            case 2: hipLaunchKernelGGL(k_ce_fwd_reg<2>, grid, kLB, 0, st, x, lab, prob, part, bp, N, (int)C); break;
+            case 4: hipLaunchKernelGGL(k_ce_fwd_reg<4>, grid, kLB, 0, st, x, lab, prob, part, bp, N, (int)C); break;
+            case 8: hipLaunchKernelGGL(k_ce_fwd_reg<8>, grid, kLB, 0, st, x, lab, prob, part, bp, N, (int)C); break;
+            default: hipLaunchKernelGGL(k_ce_fwd_reg<16>, grid, kLB, 0, st, x, lab, prob, part, bp, N, (int)C); break;
             }
             nparts = (int)grid;
         } else {
@@ -265,13 +301,13 @@ extern "C" NC_HIP_API int nc_hip_cross_entropy_fwd(int64_t N, int64_t C, const f
             int rc = nc_hip_softmax_fwd(1, N, C, x, prob, stream);
             if (rc) return rc;
             const unsigned grid = gather_grid(N);
-            hipLaunchKernelGGL(k_label_gather, grid, kLB, 0, st, prob, lab, part, b, N, C);
+            hipLaunchKernelGGL(k_label_gather, grid, kLB, 0, st, prob, lab, part, bp, N, C);
             nparts = (int)grid;
             rc = nc_hip_unary_fwd(NC_HIP_UN_EXP, 0.0f, prob, prob, N * C, stream);
             if (rc) return rc;
         }
     }
-    hipLaunchKernelGGL(k_loss_finish, 1, kLB, 0, st, part, nparts, N, 0, loss);
+    hipLaunchKernelGGL(k_loss_finish, 1, kLB, 0, st, part, bp, nparts, N, 0, loss, b);
     return check_launch("nc_hip_cross_entropy_fwd");
 }
 
@@ -309,14 +345,14 @@ extern "C" NC_HIP_API int nc_hip_nll_loss_fwd(int64_t N, int64_t C, const float 
     hipStream_t st = as_stream(stream);
     unsigned long long *b = (unsigned long long *)bad;
     double *part = (double *)ws;
-    hipLaunchKernelGGL(k_init_bad, 1, 1, 0, st, b);
+    unsigned long long *bp = (unsigned long long *)(part + loss_parts(N));
     int nparts = 0;
     if (N > 0) {
         const unsigned grid = gather_grid(N);
-        hipLaunchKernelGGL(k_label_gather, grid, kLB, 0, st, x, lab, part, b, N, C);
+        hipLaunchKernelGGL(k_label_gather, grid, kLB, 0, st, x, lab, part, bp, N, C);
         nparts = (int)grid;
     }
-    hipLaunchKernelGGL(k_loss_finish, 1, kLB, 0, st, part, nparts, N, sum ? 1 : 0, loss);
+    hipLaunchKernelGGL(k_loss_finish, 1, kLB, 0, st, part, bp, nparts, N, sum ? 1 : 0, loss, b);
     return check_launch("nc_hip_nll_loss_fwd");
 }
 
