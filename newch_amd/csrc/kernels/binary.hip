@@ -784,7 +784,8 @@ static int prepare_grad(int op, int which, int nd, const int64_t *shape, const i
 //   * A plane of H*W/4 float4 is cut into NBAND row bands of 512*T float4 (T <= NC_B2_TMAX); a
 //     512-lane workgroup owns one band of a range of planes.  Lane t holds float4 q = t + 512 k
 //     (k < T) of the band, all in column group w4 = t mod W4 (W4 = W/4 divides 64).
-//   * g: the T loads of the next plane are issued before the current plane is summed.
+//   * g: the T loads of the next plane (and, for mul and div, a's row of it) are issued before the
+//     current plane is summed.
 //   * Launch shape: when grad_a is written, T = 8 where the plane allows it, with one workgroup
 //     per CU (256 VGPRs per lane): twice the bytes per lane per plane of T = 4 at two workgroups
 //     per CU, so the per-plane grad_a exchange (shuffles, LDS slots, group sums, partial stores)
