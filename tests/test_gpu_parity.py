@@ -562,6 +562,50 @@ def test_kernel_binary_bwd_fused(K, case, ash, aview, bsh, op, accumulate):
         assert_close64(got, base + red, scale + (np.abs(init) if accumulate else 0), f"{case} {op} grad {name}")
 
 
+def test_reductions_deterministic(K):
+    """Every fp64 partial is combined in a fixed order: the fused broadcast backward and the LayerNorm
+    backward give the same bits on a repeated call."""
+    rng = np.random.default_rng(77)
+    # fused backward of a[P,1,W] + b[H,W]: T = 8 and two bands per plane, several planes per workgroup
+    A = rng.standard_normal((300, 1, 64)).astype(np.float32)
+    B = (0.5 + rng.random((1, 512, 64))).astype(np.float32)
+    shape = (300, 512, 64)
+    G = rng.standard_normal(shape).astype(np.float32)
+    sa, sb = bcast_strides(A.shape, strides_of(A), shape), bcast_strides(B.shape, strides_of(B), shape)
+    so = [s // 4 for s in np.empty(shape, np.float32).strides]
+    Ad, Bd, Gd = dev(A), dev(B), dev(G)
+    wsb = K.binary_bwd2_workspace(shape, sa, sb)
+    ws = empty(max(wsb, 1))
+    outs = []
+    for _ in range(2):
+        GA, GB = dev(np.zeros(A.shape, np.float32)), dev(np.zeros(B.shape, np.float32))
+        K.binary_bwd2("mul", shape, Gd.ptr, so, Ad.ptr, sa, Bd.ptr, sb, GA.ptr, sa, GB.ptr, sb, ws.ptr, wsb,
+                      accumulate=False)
+        sync()
+        outs.append((GA.to_numpy(np.float32, A.shape), GB.to_numpy(np.float32, B.shape)))
+    assert_bits(outs[1][0], outs[0][0], "bwd2 grad_a repeat")
+    assert_bits(outs[1][1], outs[0][1], "bwd2 grad_b repeat")
+    # LayerNorm backward column sums
+    rows, D = 4099, 1024
+    x = rng.standard_normal((rows, D)).astype(np.float32)
+    g = rng.standard_normal((rows, D)).astype(np.float32)
+    w = (1 + 0.1 * rng.standard_normal(D)).astype(np.float32)
+    Xd, Wd, Gd2 = dev(x), dev(w), dev(g)
+    Sd, Yd = empty(8 * rows), empty(x.nbytes)
+    K.layer_norm_fwd(rows, D, Xd.ptr, Wd.ptr, 0, 1e-5, Yd.ptr, Sd.ptr)
+    wsl = K.layer_norm_bwd_workspace(rows, D)
+    wsL = empty(max(wsl, 1))
+    cols = []
+    for _ in range(2):
+        GX, GW, GB2 = empty(x.nbytes), dev(np.zeros(D, np.float32)), dev(np.zeros(D, np.float32))
+        K.layer_norm_bwd(rows, D, Xd.ptr, Wd.ptr, Sd.ptr, Gd2.ptr, GX.ptr, GW.ptr, GB2.ptr, wsL.ptr, wsl,
+                         accumulate=False)
+        sync()
+        cols.append((GX.to_numpy(np.float32, (rows, D)), GW.to_numpy(np.float32, D), GB2.to_numpy(np.float32, D)))
+    for k, name in enumerate(("gx", "gw", "gb")):
+        assert_bits(cols[1][k], cols[0][k], f"layer_norm bwd {name} repeat")
+
+
 # Many planes per workgroup (plane ranges capped through NC_HIP_BWD2_MAX_RANGES): the grad_a ring of
 # group partials wraps several times, from a different starting slot in each workgroup.
 BWD2_LONG = [
