@@ -252,6 +252,9 @@ NC_API nc_status nc_synchronize(nc_ctx *ctx);
 NC_API void *nc_device_ptr(nc_tensor *t);
 /* A new tensor copied from device memory (device-to-device). */
 NC_API nc_tensor *nc_from_device(nc_ctx *ctx, nc_dtype dt, const void *device_data, int ndim, const int64_t *shape);
+/* Device allocations (hipMalloc calls) the context has made so far: arena chunks, large arena blocks
+ * and persistent tensors.  Constant across steady-state steps, whose temporaries come from the arena. */
+NC_API uint64_t nc_device_alloc_count(const nc_ctx *ctx);
 
 #ifdef __cplusplus
 }

@@ -48,6 +48,12 @@ NC_HIP_API int nc_hip_device_count(void);
 /* Test hook (host only, no device work): how many (d, n) pairs the kernels' multiply-high index
  * divider gets wrong against n / d, over every d in divs and n in nums. */
 NC_HIP_API uint64_t nc_hip_check_intdiv(const uint32_t *divs, int ndivs, const uint32_t *nums, int nnums);
+/* Test hook: size the grids of grid-stride kernels for n compute units instead of the device's own
+ * count (n <= 0 restores it; the NC_HIP_CUS environment variable sets the same at start-up).  Every
+ * split of a reduction into partials depends on the problem shape only, so results are bit-identical
+ * for any n: the GPU counterpart of the reference's thread-count determinism (threadpool.c:182-186,
+ * engine/tests/test_main.c:1169-1246). */
+NC_HIP_API void nc_hip_set_grid_cus(int n);
 
 /* Activation forward over n contiguous floats: y = f(x).  `s` is the leaky_relu slope / scale
  * factor / added scalar / exponent.  Replaces unary_fwd_span, ops_elementwise.c:229-266 (with the

@@ -171,6 +171,7 @@ NC_DEVICE_SIGNATURES: dict[str, tuple] = {
     "nc_synchronize": (c_int, [P]),
     "nc_device_ptr": (c_void_p, [P]),
     "nc_from_device": (P, [P, c_int, c_void_p, c_int, I64P]),
+    "nc_device_alloc_count": (c_uint64, [P]),
 }
 
 

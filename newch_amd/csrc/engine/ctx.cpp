@@ -82,6 +82,26 @@ void *host_alloc(nc_ctx *ctx, size_t bytes, bool persistent) {
 void host_free(nc_ctx *, void *p) { free(p); }
 
 // ---- device arena ------------------------------------------------------------------------------------
+// NC_DEBUG_POISON=1 at nc_init (the reference's debug switch, ctx.c:41-56): every device block the
+// context gives back -- a step-arena block on free, a persistent tensor before hipFree -- is filled
+// with 0xCD bytes on the context's stream, so a kernel that reads released memory sees garbage
+// instead of stale values.
+static bool poison_env() {
+    const char *v = getenv("NC_DEBUG_POISON");
+    return v && v[0] && v[0] != '0';
+}
+
+static void poison(nc_ctx *ctx, char *p, size_t bytes) {
+    if (ctx->poison && p && bytes && ctx->device >= 0) (void)nc_hip_fill(p, 1, 0xCD, (int64_t)bytes, ctx->stream);
+}
+
+// every device allocation the context makes goes through here (counted for nc_device_alloc_count)
+static hipError_t device_malloc(nc_ctx *ctx, char **p, size_t bytes) {
+    const hipError_t e = hipMalloc((void **)p, bytes);
+    if (e == hipSuccess) ctx->device_allocs++;
+    return e;
+}
+
 static void large_trim(nc_ctx *ctx) {
     DevArena &a = ctx->darena;
     const size_t budget = std::max(a.large_peak, a.large_prev_peak);
@@ -116,13 +136,13 @@ char *arena_alloc(nc_ctx *ctx, size_t bytes) {
             a.large_live_bytes += sz;
             note_use(a, sz);
         } else {
-            hipError_t e = hipMalloc(&p, need);
+            hipError_t e = device_malloc(ctx, &p, need);
             if (e == hipErrorOutOfMemory && !a.large_cache.empty()) {  // give cached blocks back, retry
                 for (auto &kv : a.large_cache) (void)hipFree(kv.second), a.reserved -= kv.first;
                 a.large_cache.clear();
                 a.large_cache_bytes = 0;
                 (void)hipGetLastError();
-                e = hipMalloc(&p, need);
+                e = device_malloc(ctx, &p, need);
             }
             if (!hip_ok(ctx, e, "device arena (large block)")) return nullptr;
             a.reserved += need;
@@ -151,7 +171,7 @@ char *arena_alloc(nc_ctx *ctx, size_t bytes) {
             while (a.cur < a.chunks.size() && a.chunks[a.cur].cap - a.chunks[a.cur].used < need) a.cur++;
             if (a.cur == a.chunks.size()) {
                 char *base = nullptr;
-                if (!hip_ok(ctx, hipMalloc(&base, a.chunk_bytes), "device arena (chunk)")) return nullptr;
+                if (!hip_ok(ctx, device_malloc(ctx, &base, a.chunk_bytes), "device arena (chunk)")) return nullptr;
                 a.chunks.push_back({base, a.chunk_bytes, 0});
                 a.reserved += a.chunk_bytes;
             }
@@ -171,6 +191,7 @@ void arena_free(nc_ctx *ctx, char *p, size_t bytes) {
     auto it = a.large_live.find(p);
     if (it != a.large_live.end()) {
         const size_t sz = it->second;
+        poison(ctx, p, sz);
         a.large_live.erase(it);
         a.large_live_bytes -= sz;
         a.large_cache.insert({sz, p});
@@ -180,6 +201,7 @@ void arena_free(nc_ctx *ctx, char *p, size_t bytes) {
         return;
     }
     const size_t need = align_up(bytes ? bytes : 1, kDevAlign);
+    poison(ctx, p, need);
     a.free_small.push_back({p, need});
     a.in_use -= need;
 }
@@ -188,7 +210,7 @@ char *dev_alloc(nc_ctx *ctx, size_t bytes, bool persistent) {
     if (!persistent) return arena_alloc(ctx, bytes);
     if (!need_device(ctx, "allocation")) return nullptr;
     char *p = nullptr;
-    if (!hip_ok(ctx, hipMalloc(&p, align_up(bytes ? bytes : 1, kDevAlign)), "device allocation (persistent)"))
+    if (!hip_ok(ctx, device_malloc(ctx, &p, align_up(bytes ? bytes : 1, kDevAlign)), "device allocation (persistent)"))
         return nullptr;
     ctx->persistent_bytes += bytes;
     return p;
@@ -197,6 +219,10 @@ char *dev_alloc(nc_ctx *ctx, size_t bytes, bool persistent) {
 void dev_free(nc_ctx *ctx, char *p, size_t bytes, bool persistent) {
     if (!p) return;
     if (persistent) {
+        if (ctx->poison) {
+            poison(ctx, p, bytes);
+            (void)hipStreamSynchronize(ctx->stream);
+        }
         (void)hipFree(p);
         ctx->persistent_bytes -= bytes;
     } else {
@@ -302,6 +328,7 @@ nc_ctx *nc_init(const nc_config *cfg) {
     if (cfg) c = *cfg;
     if (c.arena_chunk_bytes) ctx->darena.chunk_bytes = align_up(c.arena_chunk_bytes, kDevAlign);
     nc_manual_seed(ctx, c.seed);
+    ctx->poison = poison_env();
     detect_cpu(&ctx->cpu);
     ctx->n_threads = c.threads > 0 ? c.threads : ctx->cpu.n_cores;
     ctx->n_threads = std::min(std::max(ctx->n_threads, 1), 64);
@@ -434,6 +461,8 @@ int nc_set_device(nc_ctx *ctx, int device) {
 }
 
 int nc_get_device(const nc_ctx *ctx) { return ctx ? ctx->device : -1; }
+
+uint64_t nc_device_alloc_count(const nc_ctx *ctx) { return ctx ? ctx->device_allocs : 0; }
 
 void nc_set_stream(nc_ctx *ctx, void *stream) {
     if (!ctx || ctx->device < 0) return;

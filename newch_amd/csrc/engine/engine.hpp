@@ -157,6 +157,8 @@ struct nc_ctx {
     std::vector<nc_optim *> optims;  // live optimizers, freed at nc_free_ctx
     char *io_stage = nullptr;        // pinned staging for NCW1 file I/O (two halves), allocated on first use
 
+    uint64_t device_allocs = 0;  // hipMalloc calls made for this context (arena chunks, large blocks, persistent)
+    bool poison = false;         // NC_DEBUG_POISON: released device blocks are filled with 0xCD
     int device = -1;  // -1: no HIP device
     hipStream_t stream = nullptr;
     bool own_stream = false;
@@ -196,6 +198,9 @@ inline nc_tensor *owner_of(const nc_tensor *t) { return t->owner ? t->owner : co
 // device address of element 0, uploading a host-authoritative copy first (NULL + error on failure)
 char *dptr(nc_tensor *t);
 inline float *fptr(nc_tensor *t) { return (float *)dptr(t); }
+// device address of element 0 for a caller that overwrites every element of t (the rest of the
+// owner's storage made current first when t does not cover it)
+char *dptr_overwrite(nc_tensor *t);
 // marks a tensor's storage as written on the device (host mirror stale)
 void wrote_dev(nc_tensor *t);
 // host address of element 0 with the host copy current; write = the caller may write through it

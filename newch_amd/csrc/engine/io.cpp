@@ -121,7 +121,7 @@ static bool write_tensor(nc_ctx *ctx, FILE *f, nc_tensor *t, size_t bytes) {
     if (bytes == 0) return true;
     nc_tensor *o = owner_of(t);
     const bool on_device = ctx->device >= 0 && o->dev && (o->res & RES_DEV) && !(o->res & RES_MAPPED) &&
-                           !(t->flags & TF_GRAD_FRESH);
+                           !(o->flags & TF_GRAD_FRESH);
     if (on_device) {
         const char *src = dptr(t);
         if (!src) return false;
@@ -239,9 +239,8 @@ nc_status nc_load(nc_ctx *ctx, const char *path, int n, const char *const *names
         bool ok = nc_is_contiguous(t);
         if (ok && bytes) {
             if (ctx->device >= 0) {
-                t->flags &= ~TF_GRAD_FRESH;  // every byte is about to be written
-                nc_tensor *o = owner_of(t);
-                char *dst = o->dev ? o->dev + t->offset * (int64_t)dtype_size(t->dtype) : nullptr;
+                // every byte of t is about to be written; the rest of its owner is made current first
+                char *dst = dptr_overwrite(t);
                 const int rc = dst ? read_device(ctx, f, dst, (size_t)bytes) : 0;
                 if (rc < 0) break;
                 ok = rc == 1;

@@ -164,11 +164,27 @@ nc_tensor *tensor_alias(const nc_tensor *src, bool persistent) {
 }
 
 // ---- residency -------------------------------------------------------------------------------------
-// A grad buffer still marked fresh holds no data yet: give it its zeros before anyone reads it.
+// A grad buffer still marked fresh holds no data yet: give it its zeros before anyone reads it.  The
+// mark lives on the storage owner, so a view of a lazily zeroed grad (reshape, transpose, slice of
+// nc_grad(p) after nc_zero_grad) reads zeros too.
 static bool materialize(nc_tensor *t) {
-    if (!(t->flags & TF_GRAD_FRESH)) return true;
-    t->flags &= ~TF_GRAD_FRESH;
-    return fill_zero(t);
+    nc_tensor *o = owner_of(t);
+    if (!(o->flags & TF_GRAD_FRESH)) return true;
+    return fill_zero(o);
+}
+
+// Device address of t's element 0 for a caller about to overwrite every element of t: a write that
+// covers the owner's whole storage needs neither the lazy zeros nor the host copy; a partial one
+// first makes the rest of the storage current on the device.
+char *dptr_overwrite(nc_tensor *t) {
+    nc_tensor *o = owner_of(t);
+    if (!need_device(t->ctx, "op")) return nullptr;
+    const size_t span = (size_t)shape_numel(t->ndim, t->shape) * dtype_size(t->dtype);
+    if (t->offset == 0 && span == o->bytes && nc_is_contiguous(t) && o->dev) {
+        o->flags &= ~TF_GRAD_FRESH;
+        return o->dev;
+    }
+    return dptr(t);
 }
 
 char *dptr(nc_tensor *t) {
@@ -448,7 +464,7 @@ void *nc_device_ptr(nc_tensor *t) {
 float nc_get(const nc_tensor *t, const int64_t *index) {
     if (!t) return NAN;
     nc_tensor *tt = const_cast<nc_tensor *>(t);
-    if ((tt->flags & TF_GRAD_FRESH) && !fill_zero(tt)) return NAN;
+    if (!materialize(tt)) return NAN;
     nc_tensor *o = owner_of(tt);
     int64_t off = 0;
     for (int i = 0; i < t->ndim; i++) off += index[i] * t->stride[i];
@@ -492,7 +508,7 @@ int nc_copy_to(const nc_tensor *t, void *dst, size_t dst_bytes) {
         return 0;
     }
     if (n == 0) return 1;
-    if ((tt->flags & TF_GRAD_FRESH) && !fill_zero(tt)) return 0;
+    if (!materialize(tt)) return 0;
     nc_tensor *o = owner_of(tt);
     if ((o->res & RES_HOST) && o->host) {
         // gather from the host copy
@@ -545,9 +561,8 @@ int nc_copy_from(nc_tensor *t, const void *src, size_t src_bytes) {
         memcpy(hptr(t, true), src, need);
         return 1;
     }
-    nc_tensor *o = owner_of(t);
-    if (!(o->res & RES_DEV) && !dptr(t)) return 0;  // partial overwrite of a host-authoritative view
-    char *d = o->dev + t->offset * (int64_t)dtype_size(t->dtype);
+    char *d = dptr_overwrite(t);
+    if (!d) return 0;
     if (!hip_ok(ctx, hipMemcpyAsync(d, src, need, hipMemcpyHostToDevice, ctx->stream), "nc_copy_from") ||
         !hip_ok(ctx, hipStreamSynchronize(ctx->stream), "nc_copy_from"))
         return 0;

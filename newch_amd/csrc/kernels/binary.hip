@@ -265,10 +265,18 @@ __global__ __launch_bounds__(small_block<OP>()) void k_binary_fwd_s(const float 
     }
 }
 
-// 64-bit fallback for outputs with 2^32 or more work items
+// 64-bit fallback, one element per work item, for outputs that cannot be cut into launches of the
+// 32-bit kernels (a single coalesced dim of 2^30 or more elements under a dim that is not merged
+// with it): sizes and offsets in int64
+struct BigMap {
+    int nd;
+    int64_t size[NC_HIP_MAX_DIMS];
+    int64_t st[3][NC_HIP_MAX_DIMS];
+};
+
 template <int OP>
 __global__ __launch_bounds__(kB) void k_binary_fwd_big(const float *__restrict__ a, const float *__restrict__ b,
-                                                       float *__restrict__ o, IdxMap<3> m, int64_t n) {
+                                                       float *__restrict__ o, BigMap m, int64_t n) {
     const int64_t step = (int64_t)gridDim.x * kB;
     for (int64_t w = (int64_t)blockIdx.x * kB + threadIdx.x; w < n; w += step) {
         int64_t rem = w, oa = 0, ob = 0, oo = 0;
@@ -414,9 +422,45 @@ static int launch_fwd(const float *a, const float *b, float *o, const Prepared &
     const bool vec = p.st[2][inner] == 1 && p.shape[inner] % 4 == 0 && vec_mode(o, p, 2) == 1 && ma >= 0 && mb >= 0;
     const int unit = vec ? 4 : 1;
     const int64_t nwork = p.numel / unit;
+    // Outputs past the 32-bit kernels' reach (2^31 work items, or an operand offset of 2^31 elements
+    // or more) are cut along the outermost coalesced dim into runs of at most 2^30 outputs, each a
+    // launch of its own with the operand bases advanced: the full [256,512,512,64] broadcast runs as
+    // the same 2^30-output launches as its chunks.
+    int64_t hi = 0;
+    for (int k = 0; k < 3; k++) {
+        int64_t h = 0;
+        for (int d = 0; d < p.nd; d++) h += (p.shape[d] - 1) * (p.st[k][d] < 0 ? -p.st[k][d] : p.st[k][d]);
+        hi = std::max(hi, h);
+    }
+    if (nwork >= (int64_t(1) << 31) || hi >= (int64_t(1) << 31)) {
+        const int64_t S0 = p.shape[0], per = p.numel / S0;  // outputs per index of the outer dim
+        int64_t run = (int64_t(1) << 30) / per;
+        for (int k = 0; k < 3 && run > 0; k++) {  // keep every operand's offsets of a run below 2^31
+            const int64_t s0 = p.st[k][0] < 0 ? -p.st[k][0] : p.st[k][0];
+            int64_t rest = 0;
+            for (int d = 1; d < p.nd; d++) rest += (p.shape[d] - 1) * (p.st[k][d] < 0 ? -p.st[k][d] : p.st[k][d]);
+            if (s0 > 0) run = std::min(run, ((int64_t(1) << 31) - 1 - rest) / s0 + 1);
+            if (rest >= (int64_t(1) << 31)) run = 0;
+        }
+        if (p.nd == 1) run -= run % 4;  // keep 16-byte alignment of every piece but the last
+        if (run >= 1 && run < S0) {
+            for (int64_t r0 = 0; r0 < S0; r0 += run) {
+                Prepared q = p;
+                q.shape[0] = std::min(run, S0 - r0);
+                q.numel = q.shape[0] * per;
+                const int rc = launch_fwd<OP>(a + r0 * p.st[0][0], b + r0 * p.st[1][0], o + r0 * p.st[2][0], q, st);
+                if (rc != NC_HIP_OK) return rc;
+            }
+            return NC_HIP_OK;
+        }
+    }
     if (nwork >= (int64_t)UINT32_MAX) {
-        IdxMap<3> m;
-        make_map<3>(p, 1, m);
+        BigMap m{};
+        m.nd = p.nd;
+        for (int d = 0; d < p.nd; d++) {
+            m.size[d] = p.shape[d];
+            for (int k = 0; k < 3; k++) m.st[k][d] = p.st[k][d];
+        }
         hipLaunchKernelGGL(k_binary_fwd_big<OP>, dim3(stream_grid(p.numel, kB)), dim3(kB), 0, st, a, b, o, m,
                            p.numel);
         return check_launch("nc_hip_binary_fwd");
@@ -680,7 +724,7 @@ static bool plan_reduce(const Prepared &p, RedPlan &pl, size_t *ws_need) {
     pl.M = (uint32_t)M;
     pl.K = (uint32_t)K;
     pl.inner_kept = p.nd > 0 && p.st[3][p.nd - 1] != 0;
-    const uint64_t target = (uint64_t)num_cus() * 2048;  // lanes to keep every CU busy
+    const uint64_t target = (uint64_t)kPlanCUs * 2048;  // lanes to keep every CU busy (shape-only plan)
     if (pl.inner_kept) {
         uint64_t P = (target + M - 1) / M;
         uint64_t maxP = (K + 63) / 64;  // at least 64 terms per lane
@@ -689,7 +733,7 @@ static bool plan_reduce(const Prepared &p, RedPlan &pl, size_t *ws_need) {
         pl.chunk = (uint32_t)((K + P - 1) / P);
         pl.P = (uint32_t)((K + pl.chunk - 1) / pl.chunk);
     } else {
-        uint64_t blocks_target = (uint64_t)num_cus() * 8;
+        uint64_t blocks_target = (uint64_t)kPlanCUs * 8;
         uint64_t P = (blocks_target + M - 1) / M;
         uint64_t maxP = (K + 4 * kB - 1) / (4 * kB);  // at least 4 terms per lane
         if (P > maxP) P = maxP;
@@ -795,6 +839,7 @@ static int prepare_grad(int op, int which, int nd, const int64_t *shape, const i
 //     once as a partial, combined by k_bwd2_gb_combine in plane-range order.
 //   * b (mul) or its fp32 reciprocal (div) stays in registers.  Each term is an fp32 product, as in
 //     the unreduced gradient (g*b, g*a; g*(1/b) is within 1 ulp of g/b), and the sums run in fp64.
+//     A wave whose b includes a nonzero subnormal (1/b overflows there) divides g / b instead.
 //   * grad_a: per plane, lanes sharing w4 are reduced by wave shuffles; the 8 wave partials of a
 //     group of NB = 64 / W4 planes wait in LDS, and after one barrier per group a lane per (plane,
 //     column) adds them in wave order.  With one band that sum completes grad_a; with several it is an
@@ -846,12 +891,23 @@ __global__ __launch_bounds__(kB2, T >= 8 ? 2 : 4) void k_bcast_bwd2(const float 
     const uint32_t qb = band * band4 + tid;                    // this lane's first float4 in a plane
     constexpr bool WA = OUT & 1, WB = OUT & 2;
     f4 bv[T];
+    bool tiny = false;  // a nonzero subnormal b, whose reciprocal overflows
 #pragma unroll
     for (int k = 0; k < T; k++) {
         bv[k] = f4{1.f, 1.f, 1.f, 1.f};
         if constexpr (WA && MODE != 0) bv[k] = ((const f4 *)b)[qb + kB2 * k];
-        if constexpr (WA && MODE == 3) bv[k] = f4{1.0f / bv[k].x, 1.0f / bv[k].y, 1.0f / bv[k].z, 1.0f / bv[k].w};
+        if constexpr (WA && MODE == 3) {
+#pragma unroll
+            for (int c = 0; c < 4; c++) {
+                const float m = __builtin_fabsf(bv[k][c]);
+                tiny |= m != 0.0f && m < 0x1p-126f;
+            }
+            bv[k] = f4{1.0f / bv[k].x, 1.0f / bv[k].y, 1.0f / bv[k].z, 1.0f / bv[k].w};
+        }
     }
+    // wave-uniform: a wave holding such a b divides (g / b, reloading b) instead of multiplying by
+    // the reciprocal, so grad_a stays finite where the reference's g / b is
+    const bool exact_div = WA && MODE == 3 && __ballot(tiny) != 0;
     double accb[T][4];
 #pragma unroll
     for (int k = 0; k < T; k++) accb[k][0] = accb[k][1] = accb[k][2] = accb[k][3] = 0.0;
@@ -938,7 +994,13 @@ __global__ __launch_bounds__(kB2, T >= 8 ? 2 : 4) void k_bcast_bwd2(const float 
 #pragma unroll
                 for (int k = 0; k < T; k++) {
                     const float gg = cur[k][c];
-                    if constexpr (WA) ta[k] = (double)(MODE == 0 ? gg : gg * bv[k][c]);
+                    if constexpr (WA) {
+                        float t = gg;
+                        if constexpr (MODE == 1) t = gg * bv[k][c];
+                        if constexpr (MODE == 3)
+                            t = exact_div ? gg / ((const f4 *)b)[qb + kB2 * k][c] : gg * bv[k][c];
+                        ta[k] = (double)t;
+                    }
                     if constexpr (WB) accb[k][c] += (double)((MODE == 1 || MODE == 3) ? gg * av[c] : gg);
                 }
                 sa[c] = 0.0;
@@ -1075,7 +1137,7 @@ static bool plan_bwd2(const Prepared &p, const float *g, const float *a, const f
     pl.T = (uint32_t)T;
     pl.nband = (uint32_t)nband;
     const int64_t blocks_per_cu = out == 2 || T >= 8 ? 1 : 2;
-    const int64_t want = std::max<int64_t>(1, (int64_t)num_cus() * blocks_per_cu / nband);
+    const int64_t want = std::max<int64_t>(1, (int64_t)kPlanCUs * blocks_per_cu / nband);
     int64_t ranges = std::min<int64_t>(P, want);
     if (out & 1) {  // whole multiples of the resident workgroups until each range fits in res
         const int64_t fit = (int64_t)b2_res_groups(T) * (64 / (W / 4));

@@ -21,12 +21,22 @@ typedef int i4 __attribute__((ext_vector_type(4)));
 
 constexpr int kWave = 64;
 
+// Every split of a reduction into partial sums -- and so every rounding of its result -- is a
+// function of the problem shape alone, planned for the 256 CUs of an MI355X whatever device runs
+// it: the same inputs give the same bits on a part with another CU count or partition mode.  The
+// device's own count (num_cus) sizes only the grids of grid-stride kernels whose partials do not
+// depend on the grid.
+constexpr int kPlanCUs = 256;
+
 // ------------------------------------------------------------------------------------------------
 // errors (thread-local detail string, nc_hip_last_error)
 // ------------------------------------------------------------------------------------------------
 int set_error(int code, const char *fmt, ...);
 int check_launch(const char *what);
-int num_cus();            // compute units of the current device (cached per device)
+// Compute units that grids are sized for: the current device's count (cached per device), or the
+// override set by nc_hip_set_grid_cus / the NC_HIP_CUS environment variable.  Grid size only:
+// nothing that fixes a summation order may depend on it (see kPlanCUs).
+int num_cus();
 hipStream_t as_stream(void *s);
 
 // ------------------------------------------------------------------------------------------------

@@ -246,13 +246,15 @@ static int vpl_for_row(int64_t C) {
 #ifndef NC_CE_GRID_PER_CU
 #define NC_CE_GRID_PER_CU 16
 #endif
+// Both forwards write one fp64 loss partial per workgroup, so their grids are part of the summation
+// order: planned from the shape alone (kPlanCUs), never from the device's CU count.
 static unsigned ce_grid(int64_t N) {
-    const int64_t blocks = (N + kLWaves - 1) / kLWaves, cap = (int64_t)num_cus() * NC_CE_GRID_PER_CU;
+    const int64_t blocks = (N + kLWaves - 1) / kLWaves, cap = (int64_t)kPlanCUs * NC_CE_GRID_PER_CU;
     return (unsigned)std::max<int64_t>(1, std::min(blocks, cap));
 }
 
 static unsigned gather_grid(int64_t N) {
-    const int64_t blocks = (N + kLB - 1) / kLB, cap = (int64_t)num_cus() * 4;
+    const int64_t blocks = (N + kLB - 1) / kLB, cap = (int64_t)kPlanCUs * 4;
     return (unsigned)std::max<int64_t>(1, std::min(blocks, cap));
 }
 

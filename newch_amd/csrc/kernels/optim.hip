@@ -176,8 +176,10 @@ __global__ __launch_bounds__(kSB) void k_sumsq_finish(const double *__restrict__
 #ifndef NC_SUMSQ_GRID_PER_CU
 #define NC_SUMSQ_GRID_PER_CU 8
 #endif
+// one fp64 partial per workgroup: the grid is part of the summation order, so it is planned from the
+// shape alone (kPlanCUs), never from the device's CU count
 static unsigned sumsq_grid(int64_t n) {
-    const int64_t blocks = (n + 4 * kSB * kSU - 1) / (4 * kSB * kSU), cap = (int64_t)num_cus() * NC_SUMSQ_GRID_PER_CU;
+    const int64_t blocks = (n + 4 * kSB * kSU - 1) / (4 * kSB * kSU), cap = (int64_t)kPlanCUs * NC_SUMSQ_GRID_PER_CU;
     return (unsigned)std::max<int64_t>(1, std::min(blocks, cap));
 }
 

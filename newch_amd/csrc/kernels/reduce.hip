@@ -305,7 +305,7 @@ struct RedShape {
 
 static RedShape plan(int kind, int64_t outer, int64_t R, int64_t inner) {
     RedShape s{0, R, 1, 0};
-    const int64_t cus = num_cus();
+    const int64_t cus = kPlanCUs;  // the partition depends on the shape only
     const size_t elt = (kind == NC_HIP_RED_SUM || kind == NC_HIP_RED_MEAN) ? sizeof(double) : sizeof(ArgState);
     if (inner == 1) {
         if (outer >= cus * 16 || R <= 4096) {

@@ -800,14 +800,16 @@ static LnPlan ln_plan(int64_t rows, int64_t D, bool aligned, bool has_gx) {
     if (p.reg) {
         p.full = has_gx && p.vpl <= 4 && D == (int64_t)p.vpl * 4 * kWave;
         const int per_cu = p.full ? NC_LN_BWD_PP_BLOCKS_PER_CU : p.vpl <= 4 ? NC_LN_BWD_BLOCKS_PER_CU : 1;
-        int64_t want = (int64_t)num_cus() * per_cu;  // the resident workgroups
+        // the resident workgroups of a 256-CU part: rows_per_block fixes which rows each gw/gb
+        // partial holds, so it depends on the shape only
+        int64_t want = (int64_t)kPlanCUs * per_cu;
         int64_t rpb = (rows + want - 1) / want;
         if (rpb < kLnWaves) rpb = kLnWaves;
         p.rows_per_block = rpb;
         p.blocks = (rows + rpb - 1) / rpb;
         p.ws = (size_t)p.blocks * 2 * D * sizeof(double);
     } else {
-        const int64_t target = (int64_t)num_cus() * 1024;
+        const int64_t target = (int64_t)kPlanCUs * 1024;  // shape-only partition
         int64_t P = (target + D - 1) / D;
         if (P > rows) P = rows;
         if (P < 1) P = 1;

@@ -4,6 +4,7 @@
 
 #include <stdarg.h>
 #include <stdio.h>
+#include <stdlib.h>
 #include <string.h>
 
 namespace nchip {
@@ -24,13 +25,22 @@ int check_launch(const char *what) {
     return NC_HIP_OK;
 }
 
+static int g_grid_cus = -1;  // -1: not read from the environment yet; 0: the device's own count
+
 int num_cus() {
+    if (g_grid_cus < 0) {
+        const char *env = getenv("NC_HIP_CUS");
+        const int v = env ? atoi(env) : 0;
+        g_grid_cus = v > 0 ? v : 0;
+    }
+    if (g_grid_cus > 0) return g_grid_cus;
     static int cache[64];
     int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return kPlanCUs;
     if (!cache[dev]) {
         int n = 0;
-        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
+            n = kPlanCUs;
         cache[dev] = n;
     }
     return cache[dev];
@@ -75,6 +85,8 @@ extern "C" NC_HIP_API int nc_hip_device_count(void) {
     if (hipGetDeviceCount(&n) != hipSuccess) return 0;
     return n;
 }
+
+extern "C" NC_HIP_API void nc_hip_set_grid_cus(int n) { nchip::g_grid_cus = n > 0 ? n : 0; }
 
 extern "C" NC_HIP_API uint64_t nc_hip_check_intdiv(const uint32_t *divs, int ndivs, const uint32_t *nums, int nnums) {
     uint64_t bad = 0;

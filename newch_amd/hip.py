@@ -31,6 +31,7 @@ SIGNATURES = {
     "nc_hip_last_error": (c_char_p, []),
     "nc_hip_device_count": (c_int, []),
     "nc_hip_check_intdiv": (c_uint64, [POINTER(c_uint32), c_int, POINTER(c_uint32), c_int]),
+    "nc_hip_set_grid_cus": (None, [c_int]),
     "nc_hip_unary_fwd": (c_int, [c_int, c_float, P, P, c_int64, P]),
     "nc_hip_unary_bwd": (c_int, [c_int, c_float, P, P, P, P, c_int64, c_int, P]),
     "nc_hip_binary_fwd": (c_int, [c_int, c_int, I64P, P, I64P, P, I64P, P, I64P, P]),
@@ -103,6 +104,11 @@ class Kernels:
     def _ok(self, rc: int, what: str):
         if rc != 0:
             raise HipLayerError(f"{what}: {self.lib.nc_hip_last_error().decode()} (code {rc})")
+
+    def set_grid_cus(self, n):
+        """Grids of grid-stride kernels sized for n CUs (0: the device's own count); results must not
+        change."""
+        self.lib.nc_hip_set_grid_cus(int(n))
 
     def unary_fwd(self, kind, x, y, n, s=0.0, stream=None):
         self._ok(self.lib.nc_hip_unary_fwd(UN[kind], s, x, y, n, stream), "unary_fwd")
