@@ -122,6 +122,16 @@ NC_HIP_API int nc_hip_add_scalar_at(float *p, float v, void *stream);
 NC_HIP_API size_t nc_hip_reduce_workspace(int kind, int64_t outer, int64_t R, int64_t inner);
 NC_HIP_API int nc_hip_reduce_fwd(int kind, int64_t outer, int64_t R, int64_t inner, const float *x, float *y,
                                  int32_t *arg, void *ws, size_t ws_bytes, void *stream);
+/* nc_hip_reduce_fwd without a workspace argument and without allocating: no counterpart in the
+ * reference.  For callers that cannot allocate device memory (code under HIP graph capture, tight
+ * serving loops, harnesses that forbid hipMalloc).  The partials live in a static device array of
+ * 8 MiB per GPU, held until the process ends, whose address is looked up (hipGetSymbolAddress) on
+ * the first call on each device; every shape nc_hip_reduce_fwd takes fits, and a plan that would not
+ * is refused with NC_HIP_ERR_WORKSPACE.  Same results, bit for bit, as nc_hip_reduce_fwd.  All calls
+ * on one GPU share that array: calls that overlap on one GPU (on different streams, or from
+ * different threads) race and must be serialized by the caller. */
+NC_HIP_API int nc_hip_reduce_fwd_noalloc(int kind, int64_t outer, int64_t R, int64_t inner, const float *x,
+                                         float *y, int32_t *arg, void *stream);
 /* gi (+)= broadcast-back of g (sum, mean) or scatter to arg (max).  ops_reduce.c:118-163. */
 NC_HIP_API int nc_hip_reduce_bwd(int kind, int64_t outer, int64_t R, int64_t inner, const float *g,
                                  const int32_t *arg, float *gi, int accumulate, void *stream);

@@ -15,6 +15,8 @@
 
 #include <float.h>
 
+#include <mutex>
+
 #ifndef NC_RED_ROWS_GRID_PER_CU
 #define NC_RED_ROWS_GRID_PER_CU 65536
 #endif
@@ -456,6 +458,52 @@ extern "C" NC_HIP_API int nc_hip_reduce_fwd(int kind, int64_t outer, int64_t R, 
     case NC_HIP_RED_ARGMAX: return launch<NC_HIP_RED_ARGMAX>(outer, R, inner, x, y, arg, ws, ws_bytes, st);
     default: return set_error(NC_HIP_ERR_ARG, "nc_hip_reduce_fwd: unknown kind %d", kind);
     }
+}
+
+// ---- allocation-free variant ---------------------------------------------------------------------------
+// Partials of nc_hip_reduce_fwd_noalloc: one array per GPU in the code object's device memory, held
+// until the process ends.  Host code never passes `scratch` itself to a kernel (in host code the name
+// is a stand-in, not a device address): the first call on a device looks its address up with
+// hipGetSymbolAddress, with that device current, and every later call on the device uses that
+// address.  The largest workspace any reduction plan asks for is below 8 MiB (column scans:
+// (cols * P) < 2 * 2^19 partials of 8 bytes), so every shape nc_hip_reduce_fwd takes fits.
+constexpr size_t kNoAllocScratchBytes = size_t(8) << 20;
+static __device__ __align__(256) unsigned char scratch[kNoAllocScratchBytes];
+
+static void *g_scratch_ptr[64];
+static std::mutex g_scratch_mu;
+
+static void *scratch_ptr() {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return nullptr;
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (!g_scratch_ptr[dev]) {
+        void *p = nullptr;
+        if (hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)) != hipSuccess || !p) {
+            (void)hipGetLastError();
+            return nullptr;
+        }
+        g_scratch_ptr[dev] = p;
+    }
+    return g_scratch_ptr[dev];
+}
+
+extern "C" NC_HIP_API int nc_hip_reduce_fwd_noalloc(int kind, int64_t outer, int64_t R, int64_t inner,
+                                                    const float *x, float *y, int32_t *arg, void *stream) {
+    if (outer < 0 || R < 0 || inner < 0)
+        return set_error(NC_HIP_ERR_ARG, "nc_hip_reduce_fwd_noalloc: negative size");
+    const size_t need = nc_hip_reduce_workspace(kind, outer, R, inner);
+    if (need > kNoAllocScratchBytes)
+        return set_error(NC_HIP_ERR_WORKSPACE,
+                         "nc_hip_reduce_fwd_noalloc: this shape needs %zu bytes of partials, more than the %zu "
+                         "bytes of the static scratch; use nc_hip_reduce_fwd with a workspace",
+                         need, kNoAllocScratchBytes);
+    void *ws = nullptr;
+    if (need) {
+        ws = scratch_ptr();
+        if (!ws) return set_error(NC_HIP_ERR_DEVICE, "nc_hip_reduce_fwd_noalloc: scratch address lookup failed");
+    }
+    return nc_hip_reduce_fwd(kind, outer, R, inner, x, y, arg, ws, need, stream);
 }
 
 extern "C" NC_HIP_API int nc_hip_reduce_bwd(int kind, int64_t outer, int64_t R, int64_t inner, const float *g,
