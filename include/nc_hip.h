@@ -171,12 +171,15 @@ NC_HIP_API int nc_hip_dequantize_rows(int64_t rows, int64_t cols, const int8_t *
  * fixed order.  Workspace of both forwards: nc_hip_loss_workspace(N, C) bytes. */
 NC_HIP_API size_t nc_hip_loss_workspace(int64_t N, int64_t C);
 /* Cross entropy (fused log-softmax + NLL, mean over rows; NaN for N = 0): ce_fwd, ops_nn.c:107-131.
- * prob receives exp(log_softmax(x)) for the backward. */
-NC_HIP_API int nc_hip_cross_entropy_fwd(int64_t N, int64_t C, const float *x, const int32_t *lab, float *prob,
+ * stats (8-byte aligned, [N][2] floats) receives each row's {max m, ls = logf(sum exp8(x - m))}: the
+ * reference's saved probabilities are exp8((x - m) - ls), which the backward recomputes from x. */
+NC_HIP_API int nc_hip_cross_entropy_fwd(int64_t N, int64_t C, const float *x, const int32_t *lab, float *stats,
                                         float *loss, uint64_t *bad, void *ws, size_t ws_bytes, void *stream);
-/* gi (+)= s * prob, then gi[i, lab_i] -= s, with s = gout / N: ce_bwd, ops_nn.c:133-147. */
-NC_HIP_API int nc_hip_cross_entropy_bwd(int64_t N, int64_t C, const float *prob, const int32_t *lab,
-                                        const float *gout, float *gi, int accumulate, void *stream);
+/* gi (+)= s * prob, then gi[i, lab_i] -= s, with s = gout / N and prob = exp8((x - m) - ls) from the
+ * forward's stats: ce_bwd, ops_nn.c:133-147, bit for bit. */
+NC_HIP_API int nc_hip_cross_entropy_bwd(int64_t N, int64_t C, const float *x, const float *stats,
+                                        const int32_t *lab, const float *gout, float *gi, int accumulate,
+                                        void *stream);
 /* NLL over log-probabilities: loss = -sum_i x[i, lab_i] (sum != 0), or that / N (NaN for N = 0):
  * nll_fwd, ops_nn.c:391-410. */
 NC_HIP_API int nc_hip_nll_loss_fwd(int64_t N, int64_t C, const float *x, const int32_t *lab, int sum,

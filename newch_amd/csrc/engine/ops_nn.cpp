@@ -140,9 +140,11 @@ const OpDef op_layer_norm = {"layer_norm", 0, 0, layer_norm_infer, nullptr, laye
 
 // ---- losses ----------------------------------------------------------------------------------------
 // cross_entropy (ops_nn.c:83-156) and nll_loss (ops_nn.c:368-426): f32 rows [N, C], i32 labels [N],
-// a 0-d f32 loss.  The forward keeps a copy of the labels (and for cross entropy the probabilities)
-// for the backward, as the reference does, and reads the kernel's label check back before returning
-// so an out-of-range label fails the call the reference's way.
+// a 0-d f32 loss.  The forward keeps a copy of the labels for the backward, as the reference does,
+// and for cross entropy each row's maximum and log-sum-exp (8 bytes per row, where the reference keeps
+// the [N, C] probabilities: the backward recomputes them from the logits with the same fp32
+// operations); it reads the kernel's label check back before returning so an out-of-range label
+// fails the call the reference's way.
 enum { LOSS_CE = 0, LOSS_NLL = 1 };
 
 static nc_status loss_infer(nc_node *n, nc_dtype *dt, int *nd, int64_t *) {
@@ -173,20 +175,20 @@ static nc_status loss_fwd(nc_node *n) {
     float *x = contig_f32(xt), *loss = fptr(n->out);
     char *labels = dptr(yt);
     if (!x || !loss || !labels) return NC_ERR_STATE;
-    // saved block: [prob N*C floats (cross entropy)][labels N int32]
-    const size_t pbytes = ce ? (size_t)(N * C) * sizeof(float) : 0;
+    // saved block: [row statistics N x {max, log-sum-exp} floats (cross entropy)][labels N int32]
+    const size_t pbytes = ce ? (size_t)N * 2 * sizeof(float) : 0;
     const size_t sbytes = pbytes + (size_t)(N ? N : 1) * sizeof(int32_t);
     char *saved = arena_alloc(ctx, sbytes);
     const size_t ws_bytes = nc_hip_loss_workspace(N, C);
     char *ws = arena_alloc(ctx, ws_bytes ? ws_bytes : 8);
     uint64_t *bad = (uint64_t *)arena_alloc(ctx, sizeof(uint64_t));
     if (!saved || !ws || !bad) return NC_ERR_STATE;
-    float *prob = ce ? (float *)saved : nullptr;
+    float *stats = ce ? (float *)saved : nullptr;
     int32_t *lab = (int32_t *)(saved + pbytes);
     if (N > 0 && !hip_layer_ok(ctx, nc_hip_copy_strided(4, 1, yt->shape, labels, yt->stride, lab, stream(ctx)),
                                n->op->name))
         return NC_ERR_STATE;
-    const int rc = ce ? nc_hip_cross_entropy_fwd(N, C, x, lab, prob, loss, bad, ws, ws_bytes, stream(ctx))
+    const int rc = ce ? nc_hip_cross_entropy_fwd(N, C, x, lab, stats, loss, bad, ws, ws_bytes, stream(ctx))
                       : nc_hip_nll_loss_fwd(N, C, x, lab, (int)n->p.i[0], loss, bad, ws, ws_bytes, stream(ctx));
     if (!hip_layer_ok(ctx, rc, n->op->name)) return NC_ERR_STATE;
     uint64_t hb = 0;
@@ -213,7 +215,7 @@ static void loss_bwd(nc_node *n) {
     float *g = fptr(n->out->grad);
     if (!g) return;
     const char *saved = (const char *)n->saved;
-    const size_t pbytes = ce ? (size_t)(N * C) * sizeof(float) : 0;
+    const size_t pbytes = ce ? (size_t)N * 2 * sizeof(float) : 0;
     const int32_t *lab = (const int32_t *)(saved + pbytes);
     int acc = grad_acc(xt);
     if (!ce && !acc) {  // only the labels' entries change: the rest of a fresh buffer needs its zeros
@@ -221,8 +223,9 @@ static void loss_bwd(nc_node *n) {
         acc = 1;
     }
     float *gi = fptr(xt->grad);
-    if (!gi) return;
-    const int rc = ce ? nc_hip_cross_entropy_bwd(N, C, (const float *)saved, lab, g, gi, acc, stream(ctx))
+    const float *x = ce ? contig_f32(xt) : nullptr;  // the logits the probabilities are recomputed from
+    if (!gi || (ce && !x)) return;
+    const int rc = ce ? nc_hip_cross_entropy_bwd(N, C, x, (const float *)saved, lab, g, gi, acc, stream(ctx))
                       : nc_hip_nll_loss_bwd(N, C, lab, g, (int)n->p.i[0], gi, stream(ctx));
     if (!hip_layer_ok(ctx, rc, n->op->name)) return;
     wrote_dev(xt->grad);

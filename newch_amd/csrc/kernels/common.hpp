@@ -104,6 +104,12 @@ __device__ __forceinline__ float exp8_nonpos(float x) {
 
 __device__ __forceinline__ float sigmoid8(float x) { return 1.0f / (1.0f + exp8(0.0f - x)); }
 
+// exp(x) for x <= 0 (or NaN) through the hardware base-2 exponential: within a few ulp of exp8 on
+// that domain, at a fraction of its instructions.  Only for terms of a row sum whose total is
+// compared at the reductions' tolerance (the log-sum-exp of log_softmax and cross entropy); every
+// value that is an output, or is recomputed bit for bit later, uses exp8.
+__device__ __forceinline__ float exp_sum_term(float x) { return __builtin_amdgcn_exp2f(x * NC_K_LOG2E); }
+
 __device__ __forceinline__ float tanh8(float x) {
     const unsigned sign = __float_as_uint(x) & 0x80000000u;
     const float ax = __uint_as_float(__float_as_uint(x) & 0x7fffffffu);
@@ -145,7 +151,7 @@ __device__ __forceinline__ float ref_fminf(float a, float b) {
 }
 
 // ------------------------------------------------------------------------------------------------
-// wave64 reductions (__shfl_xor: ds_bpermute / DPP lane exchanges)
+// wave64 reductions
 // ------------------------------------------------------------------------------------------------
 // max of a row with the reference's scan semantics (ops_nn.c:23-25): NaN at index 0 wins, later
 // NaNs are skipped (fmaxf ignores them, order-free), otherwise the plain maximum.
@@ -157,21 +163,71 @@ __device__ __forceinline__ float row_max_finish(float m_nonnan, float x0) { retu
 // memory accesses across it.
 __device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 
+// Reductions over all 64 lanes by DPP lane moves, with no LDS crossbar (ds_bpermute) round trips:
+// pairs (lane xor 1, xor 2) within quads, the half-row and row mirrors leave every lane of a 16-lane
+// row with the row's result, then row 15 -> rows 1, 3 and lane 31 -> rows 2, 3 leave the wave's
+// result in lane 63, which is broadcast (readlane) to every lane.  A fixed order, so deterministic.
+// Every lane of the wave must be active (the kernels call these in wave-uniform control flow).
+template <int CTRL, int ROWMASK = 0xf>
+__device__ __forceinline__ int dpp_i32(int v, int old) {
+    return __builtin_amdgcn_update_dpp(old, v, CTRL, ROWMASK, 0xf, false);
+}
+template <int CTRL, int ROWMASK = 0xf>
+__device__ __forceinline__ float dpp_f32(float v, float old) {
+    return __int_as_float(dpp_i32<CTRL, ROWMASK>(__float_as_int(v), __float_as_int(old)));
+}
+template <int CTRL, int ROWMASK = 0xf>
+__device__ __forceinline__ double dpp_f64(double v, double old) {
+    union { double d; int i[2]; } a, o, r;
+    a.d = v;
+    o.d = old;
+    r.i[0] = dpp_i32<CTRL, ROWMASK>(a.i[0], o.i[0]);
+    r.i[1] = dpp_i32<CTRL, ROWMASK>(a.i[1], o.i[1]);
+    return r.d;
+}
+__device__ __forceinline__ int lane63_i32(int v) { return __builtin_amdgcn_readlane(v, 63); }
+__device__ __forceinline__ float lane63_f32(float v) { return __int_as_float(lane63_i32(__float_as_int(v))); }
+__device__ __forceinline__ double lane63_f64(double v) {
+    union { double d; int i[2]; } a;
+    a.d = v;
+    a.i[0] = lane63_i32(a.i[0]);
+    a.i[1] = lane63_i32(a.i[1]);
+    return a.d;
+}
+// DPP steps: quad_perm [1,0,3,2], quad_perm [2,3,0,1], row_half_mirror, row_mirror, then
+// row_bcast:15 into rows 1 and 3 and row_bcast:31 into rows 2 and 3
+enum : int { kDppXor1 = 0xB1, kDppXor2 = 0x4E, kDppHalfMirror = 0x141, kDppMirror = 0x140, kDppBcast15 = 0x142,
+             kDppBcast31 = 0x143 };
+
 __device__ __forceinline__ double wave_sum(double v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, kWave);
-    return v;
+    v += dpp_f64<kDppXor1>(v, 0.0);
+    v += dpp_f64<kDppXor2>(v, 0.0);
+    v += dpp_f64<kDppHalfMirror>(v, 0.0);
+    v += dpp_f64<kDppMirror>(v, 0.0);
+    v += dpp_f64<kDppBcast15, 0xa>(v, 0.0);
+    v += dpp_f64<kDppBcast31, 0xc>(v, 0.0);
+    return lane63_f64(v);
 }
 __device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, kWave);
-    return v;
+    v += dpp_f32<kDppXor1>(v, 0.0f);
+    v += dpp_f32<kDppXor2>(v, 0.0f);
+    v += dpp_f32<kDppHalfMirror>(v, 0.0f);
+    v += dpp_f32<kDppMirror>(v, 0.0f);
+    v += dpp_f32<kDppBcast15, 0xa>(v, 0.0f);
+    v += dpp_f32<kDppBcast31, 0xc>(v, 0.0f);
+    return lane63_f32(v);
 }
 __device__ __forceinline__ float wave_max_nan_skip(float v) {  // fmaxf semantics, order-free
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v = __builtin_fmaxf(v, __shfl_xor(v, o, kWave));
-    return v;
+    v = __builtin_fmaxf(v, dpp_f32<kDppXor1>(v, v));
+    v = __builtin_fmaxf(v, dpp_f32<kDppXor2>(v, v));
+    v = __builtin_fmaxf(v, dpp_f32<kDppHalfMirror>(v, v));
+    v = __builtin_fmaxf(v, dpp_f32<kDppMirror>(v, v));
+    v = __builtin_fmaxf(v, dpp_f32<kDppBcast15, 0xa>(v, v));
+    v = __builtin_fmaxf(v, dpp_f32<kDppBcast31, 0xc>(v, v));
+    return lane63_f32(v);
 }
+// lane 0's value in every lane (the row's first element for the reference's NaN rule)
+__device__ __forceinline__ float lane0_f32(float v) { return __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(v))); }
 
 // ------------------------------------------------------------------------------------------------
 // 64-bit strided index decomposition for up to 6 dims (row-major, last dim fastest)

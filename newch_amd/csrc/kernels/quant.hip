@@ -2,9 +2,10 @@
 // dequantize = to_dtype i8 -> f32 then a row-broadcast multiply, ops_shape.c:491-504 and
 // ops_elementwise.c:22).
 //
-// quantize: one wave64 per row; a row of up to 8192 floats stays in registers (VPL 128-bit vectors
-// per lane), so w is read once (4 B/el) and q written once (1 B/el, four int8 packed per 32-bit
-// store).  Rows are independent, so 48 stacked 4096x4096 matrices are a single launch.
+// quantize: a row of up to 8192 floats stays in registers -- spread over a workgroup of 4 waves when
+// its length is a multiple of 1024, else in one wave64 (VPL 128-bit vectors per lane) -- so w is read
+// once (4 B/el) and q written once (1 B/el, four int8 packed per 32-bit store).  Rows are
+// independent, so 48 stacked 4096x4096 matrices are a single launch.
 // dequantize: a streaming map, each lane reading 4 int8 (one 32-bit load) and writing one 128-bit
 // float vector, lane-contiguous so loads and stores coalesce.
 //
@@ -66,6 +67,41 @@ __global__ __launch_bounds__(kQB) void k_quant_reg(const float *__restrict__ w, 
         }
         if (lane == 0) scale[r] = s;
     }
+}
+
+// Rows of VPLW * 1024 floats (1024 .. 8192): a workgroup of 4 waves per row, each lane holding VPLW
+// float4 of it, the waves' maxima meeting in LDS, and a grid with a workgroup for every row.  A wave
+// then has a quarter of a row in flight and many rows are resident at once: the 48 x 4096 x 4096
+// quantization runs at 665-673 us where one wave per 16 KiB row (k_quant_reg) took 712-723, and the
+// same workgroups looping over rows took 790-804.
+template <int VPLW>
+__global__ __launch_bounds__(kQB) void k_quant_wg(const float *__restrict__ w, int8_t *__restrict__ q,
+                                                  float *__restrict__ scale, int cols) {
+    __shared__ float sh[kQB / kWave];
+    const int tid = threadIdx.x;
+    const int64_t r = blockIdx.x;
+    const f4 *wr = (const f4 *)(w + r * cols);
+    f4 v[VPLW];
+    float amax = 0.0f;
+#pragma unroll
+    for (int k = 0; k < VPLW; k++) {
+        v[k] = __builtin_nontemporal_load(wr + tid + k * kQB);
+        amax = __builtin_fmaxf(amax, __builtin_fmaxf(__builtin_fmaxf(__builtin_fabsf(v[k].x), __builtin_fabsf(v[k].y)),
+                                                     __builtin_fmaxf(__builtin_fabsf(v[k].z), __builtin_fabsf(v[k].w))));
+    }
+    amax = wave_max_nan_skip(amax);
+    if ((tid & (kWave - 1)) == 0) sh[tid / kWave] = amax;
+    __syncthreads();
+    amax = __builtin_fmaxf(__builtin_fmaxf(sh[0], sh[1]), __builtin_fmaxf(sh[2], sh[3]));
+    const float s = amax > 0.0f ? amax / 127.0f : 1.0f;
+    const float inv = 1.0f / s;
+    uint32_t *qr = (uint32_t *)(q + r * cols);
+#pragma unroll
+    for (int k = 0; k < VPLW; k++)
+        __builtin_nontemporal_store(pack4(quant1(v[k].x, inv), quant1(v[k].y, inv), quant1(v[k].z, inv),
+                                          quant1(v[k].w, inv)),
+                                    qr + tid + k * kQB);
+    if (tid == 0) scale[r] = s;
 }
 
 // any row length / alignment: one workgroup per row, two passes over the (L2-resident) row
@@ -154,6 +190,20 @@ extern "C" NC_HIP_API int nc_hip_quantize_rows(int64_t rows, int64_t cols, const
     const int64_t nv = cols / 4;
     int vpl = 0;
     if (cols % 4 == 0 && al) vpl = nv <= 64 ? 1 : nv <= 128 ? 2 : nv <= 256 ? 4 : nv <= 512 ? 8 : nv <= 1024 ? 16 : nv <= 2048 ? 32 : 0;
+    if (cols % 4 == 0 && al && cols % (4 * kQB) == 0 && cols <= 8 * 4 * kQB && rows <= INT32_MAX) {
+        const unsigned g = (unsigned)rows;
+        switch (cols / (4 * kQB)) {
+        case 1: hipLaunchKernelGGL(k_quant_wg<1>, g, kQB, 0, st, w, q, scale, (int)cols); break;
+        case 2: hipLaunchKernelGGL(k_quant_wg<2>, g, kQB, 0, st, w, q, scale, (int)cols); break;
+        case 3: hipLaunchKernelGGL(k_quant_wg<3>, g, kQB, 0, st, w, q, scale, (int)cols); break;
+        case 4: hipLaunchKernelGGL(k_quant_wg<4>, g, kQB, 0, st, w, q, scale, (int)cols); break;
+        case 5: hipLaunchKernelGGL(k_quant_wg<5>, g, kQB, 0, st, w, q, scale, (int)cols); break;
+        case 6: hipLaunchKernelGGL(k_quant_wg<6>, g, kQB, 0, st, w, q, scale, (int)cols); break;
+        case 7: hipLaunchKernelGGL(k_quant_wg<7>, g, kQB, 0, st, w, q, scale, (int)cols); break;
+        default: hipLaunchKernelGGL(k_quant_wg<8>, g, kQB, 0, st, w, q, scale, (int)cols); break;
+        }
+        return check_launch("nc_hip_quantize_rows");
+    }
     const int64_t blocks = (rows + (kQB / kWave) - 1) / (kQB / kWave);
     const int64_t cap = (int64_t)num_cus() * NC_QUANT_GRID_PER_CU;
     const unsigned grid = (unsigned)(blocks < cap ? blocks : cap);

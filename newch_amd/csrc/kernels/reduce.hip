@@ -49,13 +49,20 @@ __device__ __forceinline__ ArgState arg_combine(ArgState a, ArgState b) {
     return a.i <= b.i ? a : b;  // equal (including -0 == +0): first index
 }
 
+// arg_combine is a total order (larger value, then smaller index), so any combine order gives the
+// same state: the DPP steps of wave_sum, each moving the value and the index
+template <int CTRL, int ROWMASK = 0xf>
+__device__ __forceinline__ ArgState dpp_arg(ArgState s) {
+    return ArgState{dpp_f32<CTRL, ROWMASK>(s.v, s.v), dpp_i32<CTRL, ROWMASK>(s.i, s.i)};
+}
 __device__ __forceinline__ ArgState wave_arg(ArgState s) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) {
-        ArgState t{__shfl_xor(s.v, o, kWave), __shfl_xor(s.i, o, kWave)};
-        s = arg_combine(s, t);
-    }
-    return s;
+    s = arg_combine(s, dpp_arg<kDppXor1>(s));
+    s = arg_combine(s, dpp_arg<kDppXor2>(s));
+    s = arg_combine(s, dpp_arg<kDppHalfMirror>(s));
+    s = arg_combine(s, dpp_arg<kDppMirror>(s));
+    s = arg_combine(s, dpp_arg<kDppBcast15, 0xa>(s));
+    s = arg_combine(s, dpp_arg<kDppBcast31, 0xc>(s));
+    return ArgState{lane63_f32(s.v), lane63_i32(s.i)};
 }
 
 template <int KIND>

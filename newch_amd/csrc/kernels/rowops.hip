@@ -45,19 +45,28 @@ __global__ __launch_bounds__(kRowB) void k_softmax_fwd_reg(const float *__restri
                 m = __builtin_fmaxf(m, __builtin_fmaxf(__builtin_fmaxf(v[k].x, v[k].y), __builtin_fmaxf(v[k].z, v[k].w)));
         }
         m = wave_max_nan_skip(m);
-        m = row_max_finish(m, __shfl(v[0].x, 0, kWave));  // lane 0 holds the row's first element
+        m = row_max_finish(m, lane0_f32(v[0].x));  // lane 0 holds the row's first element
+        // the row sum: plain softmax needs exp8's values themselves (outputs); log_softmax only their
+        // sum, whose terms come from the hardware exponential (exp_sum_term)
         double s = 0.0;
 #pragma unroll
         for (int k = 0; k < VPL; k++) {
             const int j = lane + k * kWave;
             if (j < nv) {
                 f4 e;
-                e.x = exp8_nonpos(v[k].x - m);
-                e.y = exp8_nonpos(v[k].y - m);
-                e.z = exp8_nonpos(v[k].z - m);
-                e.w = exp8_nonpos(v[k].w - m);
+                if (LOG) {
+                    e.x = exp_sum_term(v[k].x - m);
+                    e.y = exp_sum_term(v[k].y - m);
+                    e.z = exp_sum_term(v[k].z - m);
+                    e.w = exp_sum_term(v[k].w - m);
+                } else {
+                    e.x = exp8_nonpos(v[k].x - m);
+                    e.y = exp8_nonpos(v[k].y - m);
+                    e.z = exp8_nonpos(v[k].z - m);
+                    e.w = exp8_nonpos(v[k].w - m);
+                    v[k] = e;
+                }
                 s += ((double)e.x + (double)e.y) + ((double)e.z + (double)e.w);
-                if (!LOG) v[k] = e;
             }
         }
         const float sf = (float)wave_sum(s);

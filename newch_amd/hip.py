@@ -63,7 +63,7 @@ SIGNATURES = {
     "nc_hip_sumsq": (c_int, [c_int64, P, P, c_int, P, c_size_t, P]),
     "nc_hip_loss_workspace": (c_size_t, [c_int64, c_int64]),
     "nc_hip_cross_entropy_fwd": (c_int, [c_int64, c_int64, P, P, P, P, P, P, c_size_t, P]),
-    "nc_hip_cross_entropy_bwd": (c_int, [c_int64, c_int64, P, P, P, P, c_int, P]),
+    "nc_hip_cross_entropy_bwd": (c_int, [c_int64, c_int64, P, P, P, P, P, c_int, P]),
     "nc_hip_nll_loss_fwd": (c_int, [c_int64, c_int64, P, P, c_int, P, P, P, c_size_t, P]),
     "nc_hip_nll_loss_bwd": (c_int, [c_int64, c_int64, P, P, c_int, P, P]),
     "nc_hip_gemm_f32": (c_int, [c_int, c_int, c_int64, c_int64, c_int64, c_float, P, c_int64, P, c_int64, c_float, P,
@@ -189,12 +189,13 @@ class Kernels:
     def loss_workspace(self, N, C):
         return self.lib.nc_hip_loss_workspace(N, C)
 
-    def cross_entropy_fwd(self, N, C, x, lab, prob, loss, bad, ws, ws_bytes, stream=None):
-        self._ok(self.lib.nc_hip_cross_entropy_fwd(N, C, x, lab, prob, loss, bad, ws, ws_bytes, stream),
+    def cross_entropy_fwd(self, N, C, x, lab, stats, loss, bad, ws, ws_bytes, stream=None):
+        """stats: [N][2] floats {row max, log-sum-exp} for the backward."""
+        self._ok(self.lib.nc_hip_cross_entropy_fwd(N, C, x, lab, stats, loss, bad, ws, ws_bytes, stream),
                  "cross_entropy_fwd")
 
-    def cross_entropy_bwd(self, N, C, prob, lab, gout, gi, accumulate=True, stream=None):
-        self._ok(self.lib.nc_hip_cross_entropy_bwd(N, C, prob, lab, gout, gi, int(accumulate), stream),
+    def cross_entropy_bwd(self, N, C, x, stats, lab, gout, gi, accumulate=True, stream=None):
+        self._ok(self.lib.nc_hip_cross_entropy_bwd(N, C, x, stats, lab, gout, gi, int(accumulate), stream),
                  "cross_entropy_bwd")
 
     def nll_loss_fwd(self, N, C, x, lab, sum, loss, bad, ws, ws_bytes, stream=None):

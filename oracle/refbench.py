@@ -1,0 +1,283 @@
+"""Test infrastructure: the CPU baseline of bench.py -- the reference engine timed per op class.
+
+The reference engine is oracle/_ref/libnc_ref.so, compiled in place from the reference's C sources by
+oracle/Makefile (its AVX2 kernel tier and its own thread pool, threads capped as its
+engine/src/core/ctx.c:289-291 does).  Every op class of the benchmark's GPU workloads is timed here on
+the reference's own code path, through the probe's ncref_time_forward / ncref_time_backward
+(oracle/ref_probe.c): the forward or backward function of the op that produced a tensor, re-run on
+buffers that already exist, so the time is the op's work (engine/src/ops/*.c) without dispatch or the
+first touch of a fresh output.  Ops that are not autograd ops (quantize, the dequantize pair) are
+timed through the public API after a warm call, when the arena reuses its large blocks.
+
+Which reference paths run, as the reference is written:
+  * activations: threaded, 16-aligned chunks (ops_elementwise.c:229-365, threadpool.c:182-205);
+  * broadcast forward and sum-to-shape backward: the serial strided odometer
+    (ops_elementwise.c:108-186, tensor.c:313-345);
+  * softmax / log_softmax, LayerNorm, max/argmax, cross entropy: serial over rows (ops_nn.c:22-147,
+    463-522; ops_reduce.c:60-116);
+  * quantize: serial rows (ops_quant.c:23-39); dequantize = to_dtype then a broadcast mul
+    (ops_shape.c:491-504); full sum: one sum_f32 call (ops_reduce.c:87-89).
+
+Samples are bounded so the whole baseline takes tens of seconds: they are stated per class.
+Only bench.py's cpu_baseline leg calls this module.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+import time
+from ctypes import c_double, c_float, c_int, c_void_p
+
+import numpy as np
+
+from newch_amd import abi
+
+from .pyoracle import REF_LIB
+
+ACTS = ["gelu", "silu", "sigmoid", "tanh", "hardswish", "relu6"]
+
+
+class RefEngine:
+    def __init__(self, threads: int, seed: int = 1):
+        L = abi.load(REF_LIB)
+        L.ncref_time_forward.restype = c_double
+        L.ncref_time_forward.argtypes = [c_void_p, c_int]
+        L.ncref_time_backward.restype = c_double
+        L.ncref_time_backward.argtypes = [c_void_p, c_void_p, c_int]
+        self.L = L
+        self.ctx = L.nc_init(ctypes.byref(abi.Config(0, seed, 0, threads)))
+        self.threads = L.nc_num_threads(self.ctx)
+        self.backend = L.nc_kernel_backend(self.ctx).decode()
+
+    def close(self):
+        self.L.nc_free_ctx(self.ctx)
+
+    def check(self):
+        if not self.L.nc_ok(self.ctx):
+            raise RuntimeError(self.L.nc_error(self.ctx).decode())
+
+    def tensor(self, a, dt=abi.F32):
+        a = np.ascontiguousarray(a)
+        nd, shp = abi.shape_arg(a.shape)
+        t = self.L.nc_from_data(self.ctx, dt, a.ctypes.data_as(c_void_p), nd, shp)
+        self.check()
+        return t
+
+    def param(self, a):
+        a = np.ascontiguousarray(a, np.float32)
+        nd, shp = abi.shape_arg(a.shape)
+        p = self.L.nc_parameter(self.ctx, self.tensor(a), nd, shp)
+        self.check()
+        self.L.nc_step_end(self.ctx)  # the staging copy goes back to the arena
+        return p
+
+    def persistent(self, a, dt=abi.F32):
+        self.L.nc_persistent_begin(self.ctx)
+        try:
+            return self.tensor(a, dt)
+        finally:
+            self.L.nc_persistent_end(self.ctx)
+
+    def fwd(self, out, reps=1):
+        self.check()
+        s = self.L.ncref_time_forward(out, reps)
+        if s < 0:
+            raise RuntimeError("ncref_time_forward failed")
+        return s
+
+    def bwd(self, out, g, reps=1):
+        g = np.ascontiguousarray(g, np.float32)
+        s = self.L.ncref_time_backward(out, g.ctypes.data_as(c_void_p), reps)
+        self.check()
+        if s < 0:
+            raise RuntimeError("ncref_time_backward failed")
+        return s
+
+    def wall(self, fn, reps=1):
+        fn()  # warm: the arena keeps the large blocks for the timed calls
+        self.L.nc_step_end(self.ctx)
+        t = 0.0
+        for _ in range(reps):
+            t0 = time.perf_counter()
+            fn()
+            t += time.perf_counter() - t0
+            self.check()
+            self.L.nc_step_end(self.ctx)
+        return t / reps
+
+    def step_end(self):
+        self.L.nc_step_end(self.ctx)
+
+
+def _unary(e: RefEngine, out: dict, n: int):
+    L = e.L
+    calls = {"gelu": lambda t: L.nc_gelu(t, 0), "silu": L.nc_silu, "sigmoid": L.nc_sigmoid, "tanh": L.nc_tanh,
+             "hardswish": L.nc_hardswish, "relu6": L.nc_relu6}
+    x, g = _pattern(n, 1), _pattern(n, 2)
+    p = e.param(x)
+    what = f"2^{n.bit_length() - 1} fp32 elements (tensors of {4 * n >> 20} MiB, past the host caches)"
+    for act in ACTS:
+        y = calls[act](p)
+        e.fwd(y)  # warm
+        out[f"{act}_fwd"] = (e.fwd(y, 3), n, what)
+        out[f"{act}_bwd"] = (e.bwd(y, g, 3), n, what)
+        e.step_end()
+    e.L.nc_release(p)
+
+
+def _pattern(n: int, seed: int) -> np.ndarray:
+    """n float32 values ~N(0,1): a 2^20 + 7 random block repeated (cheap to build at 2^30)."""
+    blk = np.random.default_rng(seed).standard_normal((1 << 20) + 7, dtype=np.float32)
+    return np.resize(blk, n)
+
+
+def _broadcast(e: RefEngine, out: dict, lead: int, labels):
+    """a[lead,512,1,64] op b[1,1,512,64] -> lead * 2^24 outputs: lead 64 is one 2^30-output chunk of
+    the configuration's a[256,512,1,64] (4 chunks: x4 time at the same rate)."""
+    L = e.L
+    a = np.random.default_rng(3).standard_normal((lead, 512, 1, 64), dtype=np.float32)
+    b = (0.5 + 1.5 * np.random.default_rng(4).random((1, 1, 512, 64))).astype(np.float32)
+    n_out = lead << 24
+    what = (f"a[{lead},512,1,64] op b[1,1,512,64] = 2^{n_out.bit_length() - 1} outputs "
+            + ("(one of the configuration's 4 chunks: x4 time)" if lead == 64 else
+               f"({n_out >> 20} Mi of the configuration's 4 Gi outputs)"))
+    pa, pb = e.param(a), e.param(b)
+    ta, tb = e.persistent(a), e.persistent(b)
+    g = _pattern(n_out, 6)
+    want = lambda *ls: any(x in labels for x in ls)  # noqa: E731
+    for op, fn in (("add", L.nc_add), ("mul", L.nc_mul), ("div", L.nc_div)):
+        if want(f"bcast_{op}_fwd", f"bcast_{op}_bwd"):
+            y = fn(pa, pb)
+            if want(f"bcast_{op}_fwd"):
+                out[f"bcast_{op}_fwd"] = (e.fwd(y), n_out, what)
+            if want(f"bcast_{op}_bwd"):
+                out[f"bcast_{op}_bwd"] = (e.bwd(y, g), n_out, what + "; both gradients")
+            e.step_end()
+    if want("bcast_add_fwd_transposed_a"):  # storage [512,lead,1,64] seen through transpose(0, 1)
+        pt = e.param(a.transpose(1, 0, 2, 3).copy())
+        y = L.nc_add(L.nc_transpose(pt, 0, 1), pb)
+        out["bcast_add_fwd_transposed_a"] = (e.fwd(y), n_out, what + "; a is a transposed view")
+        e.step_end()
+        L.nc_release(pt)
+    if want("bcast_add_fwd_inner_strided_a"):
+        # storage [lead,64,512] .transpose(1, 2) .reshape(lead,512,1,64): the reshape of a
+        # non-contiguous view copies (ops_shape.c:73-106), then the add reads the copy
+        ps = e.param(a.reshape(lead, 512, 64).transpose(0, 2, 1).copy())
+        nd, shp = abi.shape_arg((lead, 512, 1, 64))
+        r = L.nc_reshape(L.nc_transpose(ps, 1, 2), nd, shp)
+        y = L.nc_add(r, pb)
+        out["bcast_add_fwd_inner_strided_a"] = (e.fwd(r) + e.fwd(y), n_out,
+                                                what + "; a gathered from an innermost-strided view, then added")
+        e.step_end()
+        L.nc_release(ps)
+    if want("bcast_add_bwd_grad_a"):
+        y = L.nc_add(pa, tb)
+        out["bcast_add_bwd_grad_a"] = (e.bwd(y, g), n_out, what + "; grad_a only")
+        e.step_end()
+    if want("bcast_add_bwd_grad_b"):
+        y = L.nc_add(ta, pb)
+        out["bcast_add_bwd_grad_b"] = (e.bwd(y, g), n_out, what + "; grad_b only")
+        e.step_end()
+    for p in (pa, pb, ta, tb):
+        L.nc_release(p)
+
+
+def _rows(e: RefEngine, out: dict):
+    L = e.L
+    rows, C = 65536, 1024
+    e_ = rows * C
+    x = np.random.default_rng(7).standard_normal((rows, C), dtype=np.float32) * 2
+    g = np.random.default_rng(9).standard_normal((rows, C), dtype=np.float32)
+    w = (1 + 0.1 * np.random.default_rng(8).standard_normal(C)).astype(np.float32)
+    bb = (0.1 * np.random.default_rng(8).standard_normal(C)).astype(np.float32)
+    what = "X[65536,1024], the whole configuration"
+    px, pw, pbb = e.param(x), e.param(w), e.param(bb)
+    for label, fn in (("softmax", L.nc_softmax), ("log_softmax", L.nc_log_softmax)):
+        y = fn(px)
+        out[f"{label}_fwd"] = (e.fwd(y), e_, what)
+        out[f"{label}_bwd"] = (e.bwd(y, g), e_, what)
+        e.step_end()
+    y = L.nc_layer_norm(px, 1, pw, pbb, c_float(1e-5))
+    out["layer_norm_fwd"] = (e.fwd(y), e_, what)
+    out["layer_norm_bwd"] = (e.bwd(y, g), e_, what + "; gx, gw, gb")
+    e.step_end()
+    y = L.nc_max(px, -1, 0)
+    out["max_argmax"] = (e.fwd(y), e_, what + "; nc_max computes the value and the index")
+    e.step_end()
+    lab = e.persistent(np.random.default_rng(10).integers(0, C, rows).astype(np.int32), abi.I32)
+    y = L.nc_cross_entropy(px, lab)
+    out["cross_entropy_fwd"] = (e.fwd(y), e_, what)
+    out["cross_entropy_bwd"] = (e.bwd(y, np.ones(1, np.float32)), e_, what)
+    e.step_end()
+    for p in (px, pw, pbb, lab):
+        L.nc_release(p)
+
+
+def _int8_and_sums(e: RefEngine, out: dict, mats: int, sum_n: int):
+    L = e.L
+    blk = np.random.default_rng(11).standard_normal((4096, 4096), dtype=np.float32) * 0.02
+    w = np.concatenate([blk] * mats)
+    qrows, qcols = w.shape
+    what = f"{mats} of the 48 W[4096,4096] matrices stacked ({qrows} rows)"
+    tw_p = e.persistent(w)
+    del w
+    sc = c_void_p()
+    out["quantize_rows"] = (e.wall(lambda: L.nc_quantize_rows(tw_p, ctypes.byref(sc))), qrows * qcols, what)
+    L.nc_persistent_begin(e.ctx)
+    q = L.nc_quantize_rows(tw_p, ctypes.byref(sc))
+    L.nc_persistent_end(e.ctx)
+    scale = sc.value
+    nd, shp = abi.shape_arg((qrows, 1))
+
+    def dequant():
+        L.nc_mul(L.nc_to_dtype(q, abi.F32), L.nc_reshape(scale, nd, shp))
+    out["dequantize_rows"] = (e.wall(dequant), qrows * qcols, what + "; to_dtype then the row-broadcast mul")
+    for t in (tw_p, q, scale):
+        L.nc_release(t)
+    e.step_end()
+    x = _pattern(sum_n, 12)
+    px = e.param(x)
+    del x
+    what = f"2^{sum_n.bit_length() - 1} fp32 elements"
+    for label, fn in (("full_sum", L.nc_sum), ("full_mean", L.nc_mean)):
+        y = fn(px, abi.ALL_AXES, 0)
+        out[label] = (e.fwd(y), sum_n, what + " (one sum_f32 call on one core)")
+        e.step_end()
+    L.nc_release(px)
+
+
+def reference_classes(threads: int, unary_n: int = 1 << 26, quant_mats: int = 8, sum_n: int = 1 << 28,
+                      groups=("unary", "broadcast", "rows", "int8")) -> dict:
+    """{label: (seconds per launch, elements, sample description)} plus '_meta'."""
+    e = RefEngine(threads)
+    out: dict = {}
+    t0 = time.perf_counter()
+    try:
+        if "unary" in groups:
+            _unary(e, out, unary_n)
+        if "broadcast" in groups:
+            # add forward and backward over a whole 2^30-output chunk; the other variants on 2^28
+            _broadcast(e, out, 64, {"bcast_add_fwd", "bcast_add_bwd"})
+            _broadcast(e, out, 16, {"bcast_mul_fwd", "bcast_mul_bwd", "bcast_div_fwd", "bcast_div_bwd",
+                                    "bcast_add_fwd_transposed_a", "bcast_add_fwd_inner_strided_a",
+                                    "bcast_add_bwd_grad_a", "bcast_add_bwd_grad_b"})
+        if "rows" in groups:
+            _rows(e, out)
+        if "int8" in groups:
+            _int8_and_sums(e, out, quant_mats, sum_n)
+    finally:
+        e.close()
+    out["_meta"] = {"threads": e.threads, "backend": e.backend, "seconds": round(time.perf_counter() - t0, 1),
+                    "cpu": _cpu_model(), "nproc": os.cpu_count()}
+    return out
+
+
+def _cpu_model() -> str:
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"

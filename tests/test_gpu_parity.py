@@ -923,24 +923,33 @@ def test_engine_mse_loss(eng):
 LOSS_SHAPES = [(2048, 1024), (1000, 32), (64, 4096), (300, 100), (17, 8192), (5, 1), (129, 260)]
 
 
+def ce_prob(x, stats):
+    """The probabilities the reference stores, from the forward's row statistics {m, ls}:
+    exp8((x - m) - ls) in fp32 (the oracle's exp8 restatement)."""
+    st = np.asarray(stats, np.float32).reshape(-1, 2)
+    lp = (np.asarray(x, np.float32) - st[:, :1]) - st[:, 1:]
+    return O.unary_fwd("exp", lp).reshape(np.shape(x))
+
+
 @pytest.mark.parametrize("N,C", LOSS_SHAPES)
 def test_kernel_cross_entropy(K, N, C):
-    """Register rows (C % 4 == 0, C <= 4096) and the generic path; loss within the bar, prob within a
-    few ulp of the oracle's, the backward bit for bit given the kernel's own prob."""
+    """Register rows (C % 4 == 0, C <= 4096) and the generic path; loss within the bar; the
+    probabilities implied by the row statistics within a few ulp of the oracle's; the backward bit for
+    bit given them."""
     rng = np.random.default_rng(N * 10007 + C)
     x = (rng.standard_normal((N, C)) * 3).astype(np.float32)
     if C >= 8:
         x[1, 5] = -np.inf  # a zero probability
     lab = rng.integers(0, C, N).astype(np.int32)
     Xd, Ld = dev(x), dev(lab)
-    P, LS, BAD = empty(4 * N * C), empty(4), empty(8)
+    S, LS, BAD = empty(8 * N), empty(4), empty(8)
     wsb = K.loss_workspace(N, C)
     ws = empty(max(wsb, 8))
-    K.cross_entropy_fwd(N, C, Xd.ptr, Ld.ptr, P.ptr, LS.ptr, BAD.ptr, ws.ptr, wsb)
+    K.cross_entropy_fwd(N, C, Xd.ptr, Ld.ptr, S.ptr, LS.ptr, BAD.ptr, ws.ptr, wsb)
     sync()
     assert BAD.to_numpy(np.uint64, 1)[0] == np.uint64(0xFFFFFFFFFFFFFFFF)
     loss_o, prob_o = O.cross_entropy_fwd(x, lab)
-    prob = P.to_numpy(np.float32, (N, C))
+    prob = ce_prob(x, S.to_numpy(np.float32, (N, 2)))
     fin = np.isfinite(prob_o)
     assert (np.isnan(prob) == np.isnan(prob_o)).all()
     # exp of a log-probability whose log-sum-exp is rounded from an fp64 row sum (the reference: fp32)
@@ -954,7 +963,7 @@ def test_kernel_cross_entropy(K, N, C):
     for acc in (True, False):
         gi0 = rng.standard_normal((N, C)).astype(np.float32)
         GI = dev(gi0)
-        K.cross_entropy_bwd(N, C, P.ptr, Ld.ptr, GO.ptr, GI.ptr, accumulate=acc)
+        K.cross_entropy_bwd(N, C, Xd.ptr, S.ptr, Ld.ptr, GO.ptr, GI.ptr, accumulate=acc)
         sync()
         want = O.cross_entropy_bwd(prob, lab, float(gout), gi0 if acc else None)
         assert_bits(GI.to_numpy(np.float32, (N, C)), want, f"ce bwd acc={acc}")
@@ -1003,13 +1012,13 @@ def test_kernel_cross_entropy_nan_rows(K):
     x[5, 6] = np.float32(-200.0)
     lab = np.arange(N, dtype=np.int32) % C
     Xd, Ld = dev(x), dev(lab)
-    P, LS, BAD = empty(4 * N * C), empty(4), empty(8)
+    S, LS, BAD = empty(8 * N), empty(4), empty(8)
     wsb = K.loss_workspace(N, C)
     ws = empty(max(wsb, 8))
-    K.cross_entropy_fwd(N, C, Xd.ptr, Ld.ptr, P.ptr, LS.ptr, BAD.ptr, ws.ptr, wsb)
+    K.cross_entropy_fwd(N, C, Xd.ptr, Ld.ptr, S.ptr, LS.ptr, BAD.ptr, ws.ptr, wsb)
     sync()
     loss_o, prob_o = O.cross_entropy_fwd(x, lab)
-    prob = P.to_numpy(np.float32, (N, C))
+    prob = ce_prob(x, S.to_numpy(np.float32, (N, 2)))
     assert (np.isnan(prob) == np.isnan(prob_o)).all() and np.isnan(prob[[1, 3]]).all()
     assert np.allclose(prob[[0, 2, 4, 5]], prob_o[[0, 2, 4, 5]], rtol=1e-5)
     assert np.isnan(LS.to_numpy(np.float32, 1)[0]) and np.isnan(loss_o)
@@ -1023,11 +1032,11 @@ def test_kernel_loss_bad_labels(K):
     lab = rng.integers(0, C, N).astype(np.int32)
     lab[[4321, 777, 4999]] = [C, -3, 1000]
     Xd, Ld = dev(x), dev(lab)
-    P, LS, BAD = empty(4 * N * C), empty(4), empty(8)
+    S, LS, BAD = empty(8 * N), empty(4), empty(8)
     wsb = K.loss_workspace(N, C)
     ws = empty(max(wsb, 8))
     want = np.uint64((777 << 32) | (-3 & 0xFFFFFFFF))
-    K.cross_entropy_fwd(N, C, Xd.ptr, Ld.ptr, P.ptr, LS.ptr, BAD.ptr, ws.ptr, wsb)
+    K.cross_entropy_fwd(N, C, Xd.ptr, Ld.ptr, S.ptr, LS.ptr, BAD.ptr, ws.ptr, wsb)
     sync()
     assert BAD.to_numpy(np.uint64, 1)[0] == want
     K.nll_loss_fwd(N, C, Xd.ptr, Ld.ptr, False, LS.ptr, BAD.ptr, ws.ptr, wsb)
@@ -1237,7 +1246,8 @@ def test_engine_ncw1_load_into_parameters(eng, tmp_path):
     eng.step_end()
 
 
-@pytest.mark.parametrize("rows,cols", [(512, 4096), (96, 70), (64, 8192), (33, 10000), (8, 16)])
+@pytest.mark.parametrize("rows,cols", [(512, 4096), (96, 70), (64, 8192), (33, 10000), (8, 16), (17, 1024), (9, 3072),
+                                       (3, 5120), (40, 256)])
 def test_kernel_quantize(K, rows, cols):
     rng = np.random.default_rng(rows * cols)
     w = (rng.standard_normal((rows, cols)) * 0.02).astype(np.float32)

@@ -1,0 +1,131 @@
+"""The reference's own error beside this build's, on the reductions whose fp32 accumulation order
+decides the result.
+
+For each case the same inputs go through the nc.h API of both engines (tests/ncdrive.Engine): this
+build on the GPU and the reference engine compiled from its sources (oracle/_ref/libnc_ref.so) on the
+CPU.  Both are measured against an fp64 truth with the bar of the parity tests,
+|x - ref64| <= 1e-5 * max(|ref64|, scale), scale = sum|terms| / sqrt(terms).  The GPU must meet it
+everywhere; the reference's own result is reported beside it and flagged where it misses:
+  * the full sum / mean of 2^30 fp32 values: the reference sums them in 16 fp32 lanes
+    (engine/src/kernels/x86/kernels_avx2.c:61-71, 2^26 sequential terms per lane);
+  * a sum-to-shape gradient of 131,072 terms per element (grad_b of a[131072,1,64] + b[1,32,64], the
+    term count of the configuration's grad_b[512,64]): the reference's row_acc adds them one by one in
+    fp32 (engine/src/ops/ops_elementwise.c:33-36, 166-168);
+  * LayerNorm gw / gb over 65,536 rows: fp32 sums across rows (engine/src/ops/ops_nn.c:511-512).
+The table is printed (pytest -s) and written to $NC_REFERR_OUT when that is set.
+"""
+
+import os
+
+import numpy as np
+import pytest
+
+from oracle import pyoracle as O
+from tests.ncdrive import Engine
+from tests.test_gpu_parity import assert_close64
+
+pytestmark = pytest.mark.gpu
+TOL = 1e-5
+ROWS = []
+
+
+@pytest.fixture(scope="module")
+def engines():
+    if not O.REF_LIB.exists():
+        pytest.skip("oracle/_ref/libnc_ref.so is not built (make -C oracle ref)")
+    gpu, cpu = Engine(), Engine(O.REF_LIB)
+    yield gpu, cpu
+    gpu.close()
+    cpu.close()
+    out = os.environ.get("NC_REFERR_OUT")
+    text = table()
+    print("\n" + text)
+    if out:
+        with open(out, "w") as f:
+            f.write(text)
+
+
+def table():
+    head = (f"{'case':34s} {'terms':>9s} {'max err / bound: GPU':>22s} {'reference CPU':>14s}  "
+            f"reference misses 1e-5")
+    return "\n".join([head] + [f"{c:34s} {n:9d} {g:22.3g} {r:14.3g}  {'YES' if r > 1 else 'no'}"
+                               for c, n, g, r in ROWS]) + "\n"
+
+
+def record(case, nterms, gpu, cpu, ref64, scale):
+    ref64 = np.asarray(ref64, np.float64)
+    bound = TOL * np.maximum(np.abs(ref64), np.broadcast_to(np.asarray(scale, np.float64), ref64.shape))
+    worst = lambda x: float(np.max(np.abs(np.asarray(x, np.float64) - ref64) / bound))  # noqa: E731
+    ROWS.append((case, nterms, worst(gpu), worst(cpu)))
+    assert_close64(gpu, ref64, scale, f"{case} (GPU)")
+
+
+def run_both(engines, fn):
+    """fn(engine) -> numpy results, on the GPU engine and on the reference engine."""
+    outs = []
+    for e in engines:
+        outs.append(fn(e))
+        e.step_end()
+    return outs
+
+
+def test_full_sum_and_mean_2_30(engines):
+    n = 1 << 30
+    x = np.random.default_rng(12).standard_normal(n, dtype=np.float32) * np.float32(0.02)
+    ref64 = float(x.sum(dtype=np.float64))
+    scale = float(np.abs(x).sum(dtype=np.float64)) / np.sqrt(n)
+    L_all = -128
+
+    def fn(e):
+        t = e.tensor(x)
+        return e.read(e.lib.nc_sum(t, L_all, 0)), e.read(e.lib.nc_mean(t, L_all, 0))
+
+    (gs, gm), (cs, cm) = run_both(engines, fn)
+    record("full sum, 2^30 x N(0,0.02)", n, gs, cs, ref64, scale)
+    record("full mean, 2^30 x N(0,0.02)", n, gm, cm, ref64 / n, scale / n)
+
+
+def test_sum_to_shape_131072_terms(engines):
+    P, H, W = 131072, 32, 64
+    rng = np.random.default_rng(6)
+    a = rng.standard_normal((P, 1, W), dtype=np.float32)
+    b = (0.5 + 1.5 * rng.random((1, H, W))).astype(np.float32)
+    G = rng.standard_normal((P, H, W), dtype=np.float32)
+
+    def fn(e):
+        pa, pb = e.param(a), e.param(b)
+        e.backward_with(e.lib.nc_add(pa, pb), G)
+        return e.grad(pa), e.grad(pb)
+
+    (ga, gb), (ca, cb) = run_both(engines, fn)
+    gb64 = G.sum(axis=0, dtype=np.float64, keepdims=True)
+    gb_scale = np.abs(G).sum(axis=0, dtype=np.float64, keepdims=True) / np.sqrt(P)
+    record("sum-to-shape grad_b [32,64]", P, gb, cb, gb64, gb_scale)
+    ga64 = G.sum(axis=1, dtype=np.float64, keepdims=True)
+    ga_scale = np.abs(G).sum(axis=1, dtype=np.float64, keepdims=True) / np.sqrt(H)
+    record("sum-to-shape grad_a [131072,1,64]", H, ga, ca, ga64, ga_scale)
+
+
+def test_layer_norm_column_sums_65536_rows(engines):
+    rows, D = 65536, 1024
+    rng = np.random.default_rng(7)
+    x = rng.standard_normal((rows, D), dtype=np.float32) * np.float32(2)
+    w = (1 + 0.1 * rng.standard_normal(D)).astype(np.float32)
+    bb = (0.1 * rng.standard_normal(D)).astype(np.float32)
+    G = rng.standard_normal((rows, D), dtype=np.float32)
+
+    def fn(e):
+        px, pw, pb = e.param(x), e.param(w), e.param(bb)
+        from ctypes import c_float
+        y = e.lib.nc_layer_norm(px, 1, pw, pb, c_float(1e-5))
+        e.backward_with(y, G)
+        return e.grad(pw), e.grad(pb)
+
+    (gw, gbv), (cw, cbv) = run_both(engines, fn)
+    X = x.astype(np.float64)
+    mean = X.mean(1, keepdims=True)
+    rstd = 1 / np.sqrt(((X - mean) ** 2).mean(1, keepdims=True) + 1e-5)
+    terms = G.astype(np.float64) * ((X - mean) * rstd)
+    record("LayerNorm gw over 65536 rows", rows, gw, cw, terms.sum(0), np.abs(terms).sum(0) / np.sqrt(rows))
+    record("LayerNorm gb over 65536 rows", rows, gbv, cbv, G.sum(0, dtype=np.float64),
+           np.abs(G).sum(0, dtype=np.float64) / np.sqrt(rows))
