@@ -181,7 +181,7 @@ char *arena_alloc(nc_ctx *ctx, size_t bytes) {
             note_use(a, need);
         }
     }
-    if (ctx->bwd_logging && !ctx->grad_alloc) ctx->bwd_tmp.push_back({p, need});
+    if (ctx->scratch && !ctx->storage_alloc) ctx->scratch->add(p, need);
     return p;
 }
 
@@ -363,8 +363,7 @@ void nc_step_end(nc_ctx *ctx) {
     a.large_prev_peak = a.large_peak;
     a.large_peak = 0;
     large_trim(ctx);
-    ctx->tape = nullptr;
-    ctx->bwd_tmp.clear();
+    ctx->tape.clear();
 }
 
 void nc_arena_trim(nc_ctx *ctx) {

@@ -1,15 +1,18 @@
 // Internal definitions of the MI355X newch engine (not installed).
 //
-// Structure follows the reference engine's layers (engine/src/core/nc_internal.h): tensors with
-// shape/stride views, an op registry of {infer, view, forward, backward}, one eager dispatch point
-// (apply) with a tape for reverse-mode autograd, a persistent pool and a per-step arena.  What
-// changes for the GPU:
-//   * a tensor's storage is device memory (HBM) with a lazily created host mirror and residency
-//     bits, so host-visible accessors copy on demand and host writes are uploaded before device use;
-//   * the step arena is a device bump arena (DevArena) freed in O(1) by nc_step_end, with a
-//     size-keyed cache of large blocks so steady-state steps never call hipMalloc;
-//   * the context owns a device and a HIP stream; op forward/backward functions enqueue kernels of
-//     the nc_hip_* layer (include/nc_hip.h) on that stream and never touch element data on the host.
+// The engine behind the reference's C API (include/nc.h): tensors whose storage is device memory
+// (HBM), ops that enqueue nc_hip_* kernels (include/nc_hip.h) on the context's HIP stream, and
+// reverse-mode autograd over a tape of recorded calls.  The pieces:
+//   * nc_tensor: shape / element strides / offset over an owner's storage; the storage is device
+//     memory with a lazily created host mirror and residency bits, so host-visible accessors copy
+//     on demand and host writes are uploaded before device use;
+//   * OpDef: an op's shape rule (validate the inputs, describe the output as an OutSpec), an
+//     optional alias rule (the output as a view of the input), and forward / backward launchers;
+//   * Scratch: the arena blocks one op call allocates for itself (workspaces, gathered operands),
+//     returned when the call ends; only state an op declares saved outlives its forward;
+//   * the tape: the recorded nodes in call order, walked newest to oldest by the backward pass;
+//   * DevArena: a device bump arena freed in O(1) by nc_step_end, with a size-keyed cache of large
+//     blocks so steady-state steps never call hipMalloc.
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -79,12 +82,35 @@ struct Params {
     float f[4];
 };
 
+// A shape as a value: rank and extents (the right-aligned view of numpy broadcasting is `back`).
+struct Dims {
+    int rank = 0;
+    int64_t e[NC_MAX_DIMS] = {};
+
+    static Dims of(const nc_tensor *t);
+    int64_t numel() const {
+        int64_t n = 1;
+        for (int i = 0; i < rank; i++) n *= e[i];
+        return n;
+    }
+    int64_t back(int k) const { return e[rank - 1 - k]; }  // k-th extent from the last
+    void push(int64_t v) { e[rank++] = v; }
+    // the reference's text for a shape, "[2, 3]"
+    const char *text(char *buf, size_t size) const;
+};
+
+// Output description produced by an op's shape rule.
+struct OutSpec {
+    nc_dtype dtype = NC_F32;
+    Dims dims;
+};
+
 struct OpDef {
     const char *name;
     uint32_t flags;
     int kind;
-    nc_status (*infer)(nc_node *n, nc_dtype *dt, int *nd, int64_t *shape);
-    int (*view)(nc_node *n, int nd, const int64_t *shape);  // may be NULL
+    nc_status (*shape)(nc_node *n, OutSpec &out);          // validate the inputs, describe the output
+    bool (*alias)(nc_node *n, const OutSpec &out);         // set n->out to a view of in[0]; may be NULL
     nc_status (*forward)(nc_node *n);
     void (*backward)(nc_node *n);  // NULL = not differentiable
 };
@@ -97,11 +123,10 @@ struct nc_node {
     int n_in;
     nc_tensor *out;
     nce::Params p;
-    void *saved;  // device memory from the arena (op private)
+    void *saved;  // state the backward needs (declared by the forward with save_state)
     size_t saved_bytes;
-    nc_node *prev;
-    uint32_t mark;
-    int released;
+    uint32_t seq;   // position on the context's tape
+    bool released;  // a FREE_GRAPH backward freed its activation
 };
 
 namespace nce {
@@ -130,6 +155,27 @@ struct HostArena {
     std::vector<char *> big;  // oversize requests, freed at step end
 };
 
+// The arena blocks one op call allocates for itself (workspaces, gathered operands): every raw
+// arena_alloc made while the scope is open is recorded and handed back when it closes.  The return
+// is stream-ordered -- the kernels that use a block are already queued on the context's stream -- so
+// the next op may reuse it at once.  Blocks that must outlive the call (a forward's saved state)
+// are claimed with keep(); tensor storage never counts as scratch.  Scopes nest (an op calling
+// another op's entry point): each closes its own blocks.
+class Scratch {
+  public:
+    explicit Scratch(nc_ctx *ctx);
+    ~Scratch();
+    Scratch(const Scratch &) = delete;
+    Scratch &operator=(const Scratch &) = delete;
+    void add(char *p, size_t bytes) { blocks_.push_back({p, bytes}); }
+    void keep(const void *p);
+
+  private:
+    nc_ctx *ctx_;
+    Scratch *outer_;
+    std::vector<std::pair<char *, size_t>> blocks_;
+};
+
 }  // namespace nce
 
 struct nc_ctx {
@@ -141,11 +187,9 @@ struct nc_ctx {
 
     int persistent_depth = 0;
     int grad_enabled = 1;
-    nc_node *tape = nullptr;
-    bool bwd_logging = false;
-    bool grad_alloc = false;
-    std::vector<std::pair<void *, size_t>> bwd_tmp;  // arena blocks a node's backward allocated
-    uint32_t mark_epoch = 0;
+    std::vector<nc_node *> tape;      // recorded nodes in call order, cleared by nc_step_end
+    nce::Scratch *scratch = nullptr;  // the innermost open op call's scratch
+    bool storage_alloc = false;       // tensor storage is being allocated: never scratch
 
     nc_status status = NC_OK;
     char err[256] = {0};
@@ -176,7 +220,7 @@ void *host_alloc(nc_ctx *ctx, size_t bytes, bool persistent);  // tensor headers
 void host_free(nc_ctx *ctx, void *p);
 char *dev_alloc(nc_ctx *ctx, size_t bytes, bool persistent);
 void dev_free(nc_ctx *ctx, char *p, size_t bytes, bool persistent);
-char *arena_alloc(nc_ctx *ctx, size_t bytes);  // logged as a backward temporary when logging
+char *arena_alloc(nc_ctx *ctx, size_t bytes);  // recorded as scratch while a Scratch scope is open
 void arena_free(nc_ctx *ctx, char *p, size_t bytes);
 bool persistent_mode(const nc_ctx *ctx);
 float rand_uniform01(nc_ctx *ctx);
@@ -191,7 +235,10 @@ void contig_strides(int nd, const int64_t *shape, int64_t *st);
 int norm_axis(int axis, int nd);
 bool same_shape(const nc_tensor *a, const nc_tensor *b);
 const char *shape_str(int nd, const int64_t *shape, char *buf, size_t size);
-bool expect_f32(const nc_node *n, int i);
+// Records an op's failure on its context (the first error sticks) and returns the code.
+nc_status reject(const nc_node *n, nc_status code, const char *fmt, ...);
+// Every listed input is f32, else the reference's dtype error for the first that is not.
+bool inputs_f32(const nc_node *n, int first, int count);
 nc_tensor *tensor_new(nc_ctx *ctx, nc_dtype dt, int nd, const int64_t *shape, bool persistent);
 nc_tensor *tensor_alias(const nc_tensor *src, bool persistent);
 inline nc_tensor *owner_of(const nc_tensor *t) { return t->owner ? t->owner : const_cast<nc_tensor *>(t); }
@@ -215,8 +262,11 @@ nc_tensor *grad_buf(nc_tensor *t);
 int grad_acc(nc_tensor *x);
 bool fill_zero(nc_tensor *t);
 
-// ---- autograd (autograd.cpp) -----------------------------------------------------------------------
+// ---- dispatch and autograd (dispatch.cpp) ----------------------------------------------------------
 nc_tensor *apply(const OpDef *op, nc_tensor **in, int n_in, const Params *p);
+// Device memory for state a node's backward reads, held with the node: released with the node's
+// activation by a FREE_GRAPH backward, at once when the call is not recorded, else at step end.
+void *save_state(nc_node *n, size_t bytes);
 
 inline bool needs_grad(const nc_tensor *t) { return (t->flags & TF_REQUIRES_GRAD) != 0; }
 inline hipStream_t stream(const nc_ctx *ctx) { return ctx->stream; }

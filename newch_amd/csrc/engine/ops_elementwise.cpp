@@ -1,7 +1,8 @@
 // Elementwise ops: broadcasting binary arithmetic and unary math / activations.
 // Reference: engine/src/ops/ops_elementwise.c (binary :60-204, unary :210-411).
-// Shape inference and error messages follow the reference; the arithmetic runs in the nc_hip_*
-// kernels (include/nc_hip.h) on the context's stream.
+// The shape rules keep the reference's error messages; the arithmetic runs in the nc_hip_* kernels
+// (include/nc_hip.h) on the context's stream, and op temporaries (gathered operands, reduction
+// workspaces) are scratch of the call.
 #include <stdio.h>
 
 #include "engine.hpp"
@@ -9,23 +10,20 @@
 namespace nce {
 
 // ---- binary ----------------------------------------------------------------------------------------
-static nc_status binary_infer(nc_node *n, nc_dtype *dt, int *nd, int64_t *shape) {
-    nc_tensor *a = n->in[0], *b = n->in[1];
-    if (!expect_f32(n, 0) || !expect_f32(n, 1)) return NC_ERR_DTYPE;
-    const int r = a->ndim > b->ndim ? a->ndim : b->ndim;
-    for (int i = 0; i < r; i++) {
-        const int ia = i - (r - a->ndim), ib = i - (r - b->ndim);
-        const int64_t da = ia < 0 ? 1 : a->shape[ia], db = ib < 0 ? 1 : b->shape[ib];
-        if (da != db && da != 1 && db != 1) {
-            char sa[96], sb[96];
-            error(a->ctx, NC_ERR_SHAPE, "%s: shapes %s and %s are not broadcastable", n->op->name,
-                  shape_str(a->ndim, a->shape, sa, sizeof sa), shape_str(b->ndim, b->shape, sb, sizeof sb));
-            return NC_ERR_SHAPE;
+// numpy broadcasting: extents are matched from the last axis back; a pair must agree or one be 1
+static nc_status broadcast_shape(nc_node *n, OutSpec &out) {
+    if (!inputs_f32(n, 0, 2)) return NC_ERR_DTYPE;
+    const Dims a = Dims::of(n->in[0]), b = Dims::of(n->in[1]);
+    out.dims.rank = a.rank > b.rank ? a.rank : b.rank;
+    for (int k = 0; k < out.dims.rank; k++) {
+        const int64_t ea = k < a.rank ? a.back(k) : 1, eb = k < b.rank ? b.back(k) : 1;
+        if (ea != eb && ea != 1 && eb != 1) {
+            char ta[96], tb[96];
+            return reject(n, NC_ERR_SHAPE, "%s: shapes %s and %s are not broadcastable", n->op->name,
+                          a.text(ta, sizeof ta), b.text(tb, sizeof tb));
         }
-        shape[i] = da == 1 ? db : da;
+        out.dims.e[out.dims.rank - 1 - k] = ea == 1 ? eb : ea;
     }
-    *dt = NC_F32;
-    *nd = r;
     return NC_OK;
 }
 
@@ -114,10 +112,10 @@ static void binary_bwd(nc_node *n) {
     }
 }
 
-const OpDef op_add = {"add", OPF_ELEMENTWISE, NC_HIP_BIN_ADD, binary_infer, nullptr, binary_fwd, binary_bwd};
-const OpDef op_sub = {"sub", OPF_ELEMENTWISE, NC_HIP_BIN_SUB, binary_infer, nullptr, binary_fwd, binary_bwd};
-const OpDef op_mul = {"mul", OPF_ELEMENTWISE, NC_HIP_BIN_MUL, binary_infer, nullptr, binary_fwd, binary_bwd};
-const OpDef op_div = {"div", OPF_ELEMENTWISE, NC_HIP_BIN_DIV, binary_infer, nullptr, binary_fwd, binary_bwd};
+const OpDef op_add = {"add", OPF_ELEMENTWISE, NC_HIP_BIN_ADD, broadcast_shape, nullptr, binary_fwd, binary_bwd};
+const OpDef op_sub = {"sub", OPF_ELEMENTWISE, NC_HIP_BIN_SUB, broadcast_shape, nullptr, binary_fwd, binary_bwd};
+const OpDef op_mul = {"mul", OPF_ELEMENTWISE, NC_HIP_BIN_MUL, broadcast_shape, nullptr, binary_fwd, binary_bwd};
+const OpDef op_div = {"div", OPF_ELEMENTWISE, NC_HIP_BIN_DIV, broadcast_shape, nullptr, binary_fwd, binary_bwd};
 
 static nc_tensor *binary(const OpDef *op, nc_tensor *a, nc_tensor *b) {
     nc_tensor *in[2] = {a, b};
@@ -125,11 +123,9 @@ static nc_tensor *binary(const OpDef *op, nc_tensor *a, nc_tensor *b) {
 }
 
 // ---- unary -----------------------------------------------------------------------------------------
-static nc_status unary_infer(nc_node *n, nc_dtype *dt, int *nd, int64_t *shape) {
-    if (!expect_f32(n, 0)) return NC_ERR_DTYPE;
-    *dt = NC_F32;
-    *nd = n->in[0]->ndim;
-    memcpy(shape, n->in[0]->shape, sizeof(int64_t) * (size_t)*nd);
+static nc_status unary_shape(nc_node *n, OutSpec &out) {
+    if (!inputs_f32(n, 0, 1)) return NC_ERR_DTYPE;
+    out.dims = Dims::of(n->in[0]);
     return NC_OK;
 }
 
@@ -169,7 +165,7 @@ static void unary_bwd(nc_node *n) {
 }
 
 #define NC_UNARY_DEF(nm, KIND) \
-    const OpDef op_##nm = {#nm, OPF_ELEMENTWISE, KIND, unary_infer, nullptr, unary_fwd, unary_bwd};
+    const OpDef op_##nm = {#nm, OPF_ELEMENTWISE, KIND, unary_shape, nullptr, unary_fwd, unary_bwd};
 NC_UNARY_DEF(neg, NC_HIP_UN_NEG)
 NC_UNARY_DEF(exp, NC_HIP_UN_EXP)
 NC_UNARY_DEF(log, NC_HIP_UN_LOG)

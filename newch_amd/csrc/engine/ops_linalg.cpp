@@ -1,273 +1,306 @@
-// Dense linear algebra: matmul, batched matmul with broadcast batch dims, linear.  Reference:
-// engine/src/ops/ops_linalg.c.  Every contraction is an fp32 GEMM on the matrix cores
-// (nc_hip_gemm_f32 / nc_hip_gemm_f32_bmm); 2-D operands that are transposed views go to the GEMM as
-// transpose flags with their own leading dim instead of being gathered (ops_linalg.c:17-27), anything
-// else is gathered once into a contiguous arena copy.  Gradients accumulate through the GEMM's beta
-// (0 while a grad buffer is fresh, 1 after), so no zero pass precedes them.
+// Dense linear algebra: matmul (2-D right operand), batched matmul with broadcast batch axes, and
+// linear.  Reference: engine/src/ops/ops_linalg.c (matmul :40-88, batched :89-252, linear :255-338);
+// output shapes and error messages are the reference's.
+//
+// All three ops, forward and backward, are one thing here: a Product C = A @ B over optional batch
+// axes, run as an fp32 GEMM on the device (nc_hip_gemm_f32, or nc_hip_gemm_f32_bmm with per-axis
+// batch strides).  Operands go to the GEMM in place whenever their strides allow it -- a transposed
+// view is a transpose flag, evenly spaced rows a leading dimension, a broadcast batch axis a zero batch
+// stride -- and are packed once into a scratch copy otherwise.  A gradient product is the forward
+// product with one operand replaced by the output gradient and the other transposed (its flag flipped,
+// no copy); it accumulates through the GEMM's beta (0 while the gradient buffer is fresh, 1 after).
 #include "engine.hpp"
 
-using namespace nce;
-
+namespace nce {
 namespace {
 
-struct GemmOperand {
-    const float *p;
-    int trans;
-    int64_t ld;
+// A matrix as the GEMM reads it: element (r, c) at p[r * ld + c], or at p[c * ld + r] when trans.
+struct Mat {
+    const float *p = nullptr;
+    int trans = 0;
+    int64_t ld = 0;
+    Mat t() const { return {p, trans ^ 1, ld}; }  // the transpose: same memory, other order
 };
 
-// rows x cols logical matrix held by a 2-D t (ops_linalg.c:17-27)
-bool as_gemm(nc_tensor *t, int64_t rows, int64_t cols, GemmOperand *g) {
-    if (t->ndim == 2 && t->stride[1] == 1 && t->stride[0] >= cols) {
-        *g = {fptr(t), 0, t->stride[0]};
-    } else if (t->ndim == 2 && t->stride[0] == 1 && t->stride[1] >= rows) {
-        *g = {fptr(t), 1, t->stride[1]};
+// One operand of a batched product: its matrix and, per output batch axis, the element step from one
+// batch matrix to the next (0 where the operand is broadcast).
+struct Operand {
+    Mat m;
+    int64_t bst[NC_MAX_DIMS] = {};
+    Operand transposed() const {
+        Operand o = *this;
+        o.m = m.t();
+        return o;
+    }
+};
+
+// t's last two axes [rows, cols] in place when one of them is unit-stride and the other steps over
+// at least a whole line; packed row-major otherwise.  *strides: the strides the matrix was taken with.
+bool last_two(nc_tensor *t, Mat &m, const int64_t **strides, int64_t *packed) {
+    const int nd = t->ndim;
+    const int64_t rows = t->shape[nd - 2], cols = t->shape[nd - 1];
+    const int64_t sr = t->stride[nd - 2], sc = t->stride[nd - 1];
+    *strides = t->stride;
+    if (sc == 1 && sr >= cols) {
+        m = {fptr(t), 0, sr};
+    } else if (sr == 1 && sc >= rows) {
+        m = {fptr(t), 1, sc};
     } else {
-        *g = {contig_f32(t), 0, cols};
+        contig_strides(nd, t->shape, packed);
+        *strides = packed;
+        m = {contig_f32(t), 0, cols};
     }
-    return g->p != nullptr;
+    return m.p != nullptr;
 }
 
-// a [..., M, K]: 2-D through as_gemm, otherwise leading dims folded into M (ops_linalg.c:52-56)
-bool a_operand(nc_tensor *a, int64_t M, int64_t K, GemmOperand *g) {
-    if (a->ndim == 2) return as_gemm(a, M, K, g);
-    *g = {contig_f32(a), 0, K};
-    return g->p != nullptr;
-}
-
-bool gemm(nc_ctx *ctx, int ta, int tb, int64_t M, int64_t N, int64_t K, const float *A, int64_t lda,
-          const float *B, int64_t ldb, float beta, float *C, int64_t ldc, const char *what) {
-    return hip_layer_ok(ctx, nc_hip_gemm_f32(ta, tb, M, N, K, 1.0f, A, lda, B, ldb, beta, C, ldc, stream(ctx)), what);
-}
-
-// ---- matmul: a [..., M, K] @ b [K, N] ------------------------------------------------------------
-nc_status matmul_infer(nc_node *n, nc_dtype *dt, int *nd, int64_t *shape) {
-    nc_tensor *a = n->in[0], *b = n->in[1];
-    if (!expect_f32(n, 0) || !expect_f32(n, 1)) return NC_ERR_DTYPE;
-    if (a->ndim < 2 || b->ndim != 2 || a->shape[a->ndim - 1] != b->shape[0]) {
-        char sa[96], sb[96];
-        error(a->ctx, NC_ERR_SHAPE, "matmul: cannot multiply %s by %s (expected [..., M, K] @ [K, N])",
-              shape_str(a->ndim, a->shape, sa, sizeof sa), shape_str(b->ndim, b->shape, sb, sizeof sb));
-        return NC_ERR_SHAPE;
+// t [..., M, K] as one [rows, K] matrix: in place when it is unit-stride along K and each leading axis
+// steps over whole blocks of evenly spaced rows, packed otherwise (a 2-D t may be a transposed view).
+bool as_rows(nc_tensor *t, Mat &m) {
+    const int nd = t->ndim;
+    const int64_t K = t->shape[nd - 1];
+    if (nd == 1) {
+        m = {contig_f32(t), 0, K};
+        return m.p != nullptr;
     }
-    *dt = NC_F32;
-    *nd = a->ndim;
-    memcpy(shape, a->shape, sizeof(int64_t) * (size_t)a->ndim);
-    shape[a->ndim - 1] = b->shape[1];
+    int64_t packed[NC_MAX_DIMS];
+    const int64_t *unused;
+    if (nd == 2) return last_two(t, m, &unused, packed);
+    const int64_t step = t->stride[nd - 2];
+    bool even = (t->stride[nd - 1] == 1 || K <= 1) && step >= K;
+    int64_t rows = t->shape[nd - 2];
+    for (int i = nd - 3; even && i >= 0; i--) {
+        if (t->shape[i] == 1) continue;
+        even = t->stride[i] == rows * step;
+        rows *= t->shape[i];
+    }
+    m = even ? Mat{fptr(t), 0, step} : Mat{contig_f32(t), 0, K};
+    return m.p != nullptr;
+}
+
+// the batch step of a tensor with `strides` along each axis of `batch` (its leading axes aligned at the
+// right; an axis of extent 1 against a larger batch axis is broadcast)
+void batch_steps(const nc_tensor *t, const int64_t *strides, const Dims &batch, int64_t *out) {
+    const int lead = t->ndim - 2;
+    for (int i = 0; i < batch.rank; i++) {
+        const int j = i - (batch.rank - lead);
+        out[i] = (j < 0 || t->shape[j] == 1) ? 0 : strides[j];
+    }
+}
+
+// a batched-product operand: last two axes as a Mat, leading axes as batch steps
+bool batch_operand(nc_tensor *t, const Dims &batch, Operand &o) {
+    int64_t packed[NC_MAX_DIMS];
+    const int64_t *strides;
+    if (!last_two(t, o.m, &strides, packed)) return false;
+    batch_steps(t, strides, batch, o.bst);
+    return true;
+}
+
+// the batch steps of t's (contiguous) gradient buffer: a broadcast axis steps 0, so the GEMM layer
+// adds every batch's product into the same gradient matrix
+void grad_steps(const nc_tensor *t, const Dims &batch, int64_t *out) {
+    int64_t cs[NC_MAX_DIMS];
+    contig_strides(t->ndim, t->shape, cs);
+    batch_steps(t, cs, batch, out);
+}
+
+// C (+)= A @ B, A [M, K], B [K, N], C [M, N] with leading dim ldc; batched when batch has axes
+bool product(nc_ctx *ctx, const Dims &batch, int64_t M, int64_t N, int64_t K, const Operand &a, const Operand &b,
+             float beta, float *C, int64_t ldc, const int64_t *cst, const char *what) {
+    if (batch.rank == 0)
+        return hip_layer_ok(ctx,
+                            nc_hip_gemm_f32(a.m.trans, b.m.trans, M, N, K, 1.0f, a.m.p, a.m.ld, b.m.p, b.m.ld, beta, C,
+                                            ldc, stream(ctx)),
+                            what);
+    const size_t ws_bytes = nc_hip_gemm_f32_bmm_workspace(batch.numel());
+    char *ws = ws_bytes ? arena_alloc(ctx, ws_bytes) : nullptr;
+    if (ws_bytes && !ws) return false;
+    return hip_layer_ok(ctx,
+                        nc_hip_gemm_f32_bmm(a.m.trans, b.m.trans, M, N, K, a.m.p, a.m.ld, b.m.p, b.m.ld, beta, C, ldc,
+                                            batch.rank, batch.e, a.bst, b.bst, cst, ws, ws_bytes, stream(ctx)),
+                        what);
+}
+
+// the product of all but the last axis
+int64_t leading_rows(const nc_tensor *t) {
+    int64_t r = 1;
+    for (int i = 0; i + 1 < t->ndim; i++) r *= t->shape[i];
+    return r;
+}
+
+// gradient buffer of x for a product about to write it: its address and the GEMM beta
+float *grad_target(nc_tensor *x, float *beta) {
+    if (!grad_buf(x)) return nullptr;
+    *beta = grad_acc(x) ? 1.0f : 0.0f;
+    return fptr(x->grad);
+}
+
+// a dense row-major [rows, cols] matrix (an output gradient)
+Operand dense(const float *p, int64_t cols) {
+    Operand o;
+    o.m = {p, 0, cols};
+    return o;
+}
+
+// ---- matmul: a [..., M, K] @ b [K, N]; a's leading axes fold into M -------------------------------
+nc_status matmul_shape(nc_node *n, OutSpec &out) {
+    if (!inputs_f32(n, 0, 2)) return NC_ERR_DTYPE;
+    const Dims a = Dims::of(n->in[0]), b = Dims::of(n->in[1]);
+    if (a.rank < 2 || b.rank != 2 || a.back(0) != b.e[0]) {
+        char ta[96], tb[96];
+        return reject(n, NC_ERR_SHAPE, "matmul: cannot multiply %s by %s (expected [..., M, K] @ [K, N])",
+                      a.text(ta, sizeof ta), b.text(tb, sizeof tb));
+    }
+    out.dims = a;
+    out.dims.e[a.rank - 1] = b.e[1];
     return NC_OK;
 }
 
-void mm_dims(const nc_node *n, int64_t *M, int64_t *K, int64_t *N) {
-    *K = n->in[1]->shape[0];
-    *N = n->in[1]->shape[1];
-    *M = nc_numel(n->in[0]) / (*K ? *K : 1);
-}
+struct Mnk {
+    int64_t M, N, K;
+};
+
+Mnk matmul_mnk(const nc_node *n) { return {leading_rows(n->in[0]), n->in[1]->shape[1], n->in[1]->shape[0]}; }
 
 nc_status matmul_fwd(nc_node *n) {
-    nc_ctx *ctx = n->out->ctx;
-    int64_t M, K, N;
-    mm_dims(n, &M, &K, &N);
-    GemmOperand A, B;
+    const Mnk d = matmul_mnk(n);
+    Operand a, b;
+    const int64_t *unused;
+    int64_t packed[NC_MAX_DIMS];
     float *C = fptr(n->out);
-    if (!a_operand(n->in[0], M, K, &A) || !as_gemm(n->in[1], K, N, &B) || !C) return NC_ERR_STATE;
-    if (!gemm(ctx, A.trans, B.trans, M, N, K, A.p, A.ld, B.p, B.ld, 0.0f, C, N, "matmul")) return NC_ERR_STATE;
+    if (!as_rows(n->in[0], a.m) || !last_two(n->in[1], b.m, &unused, packed) || !C) return NC_ERR_STATE;
+    if (!product(n->out->ctx, Dims{}, d.M, d.N, d.K, a, b, 0.0f, C, d.N, nullptr, "matmul")) return NC_ERR_STATE;
     wrote_dev(n->out);
     return NC_OK;
 }
 
 void matmul_bwd(nc_node *n) {
-    nc_tensor *a = n->in[0], *b = n->in[1];
-    nc_ctx *ctx = a->ctx;
-    int64_t M, K, N;
-    mm_dims(n, &M, &K, &N);
-    const float *g = fptr(n->out->grad);  // M x N
+    nc_tensor *at = n->in[0], *bt = n->in[1];
+    nc_ctx *ctx = at->ctx;
+    const Mnk d = matmul_mnk(n);
+    const float *g = fptr(n->out->grad);  // [M, N]
     if (!g) return;
-    if (needs_grad(a) && grad_buf(a)) {  // dA (M x K) (+)= dC @ B^T
-        GemmOperand B;
-        const float beta = grad_acc(a) ? 1.0f : 0.0f;
-        float *ga = fptr(a->grad);
-        if (ga && as_gemm(b, K, N, &B) && gemm(ctx, 0, !B.trans, M, K, N, g, N, B.p, B.ld, beta, ga, K, "matmul"))
-            wrote_dev(a->grad);
+    float beta;
+    const int64_t *unused;
+    int64_t packed[NC_MAX_DIMS];
+    if (needs_grad(at)) {  // dA [M, K] (+)= G @ B^T
+        Operand b;
+        float *ga = grad_target(at, &beta);
+        if (ga && last_two(bt, b.m, &unused, packed) &&
+            product(ctx, Dims{}, d.M, d.K, d.N, dense(g, d.N), b.transposed(), beta, ga, d.K, nullptr, "matmul"))
+            wrote_dev(at->grad);
     }
-    if (needs_grad(b) && grad_buf(b)) {  // dB (K x N) (+)= A^T @ dC
-        GemmOperand A;
-        const float beta = grad_acc(b) ? 1.0f : 0.0f;
-        float *gb = fptr(b->grad);
-        if (gb && a_operand(a, M, K, &A) && gemm(ctx, !A.trans, 0, K, N, M, A.p, A.ld, g, N, beta, gb, N, "matmul"))
-            wrote_dev(b->grad);
+    if (needs_grad(bt)) {  // dB [K, N] (+)= A^T @ G
+        Operand a;
+        float *gb = grad_target(bt, &beta);
+        if (gb && as_rows(at, a.m) &&
+            product(ctx, Dims{}, d.K, d.N, d.M, a.transposed(), dense(g, d.N), beta, gb, d.N, nullptr, "matmul"))
+            wrote_dev(bt->grad);
     }
 }
 
-const OpDef op_matmul = {"matmul", 0, 0, matmul_infer, nullptr, matmul_fwd, matmul_bwd};
+const OpDef op_matmul = {"matmul", 0, 0, matmul_shape, nullptr, matmul_fwd, matmul_bwd};
 
-// ---- batched matmul: a [..., M, K] @ b [..., K, N], broadcast batch dims (ops_linalg.c:89-252) ----
-struct BatchDims {
-    int nb;
-    int64_t shape[NC_MAX_DIMS];
-    int64_t count;
-};
-
-bool batch_shape(const nc_tensor *a, const nc_tensor *b, BatchDims *bd) {
-    const int na = a->ndim - 2, nb = b->ndim - 2;
-    bd->nb = na > nb ? na : nb;
-    bd->count = 1;
-    for (int i = 0; i < bd->nb; i++) {
-        const int ia = i - (bd->nb - na), ib = i - (bd->nb - nb);
-        const int64_t da = ia < 0 ? 1 : a->shape[ia], db = ib < 0 ? 1 : b->shape[ib];
-        if (da != db && da != 1 && db != 1) return false;
-        bd->shape[i] = da == 1 ? db : da;
-        bd->count *= bd->shape[i];
+// ---- batched matmul: a [..., M, K] @ b [..., K, N], batch axes broadcast ----------------------------
+// the broadcast of a's and b's leading axes, false when they do not broadcast
+bool batch_of(const nc_tensor *a, const nc_tensor *b, Dims &batch) {
+    const int la = a->ndim - 2, lb = b->ndim - 2;
+    batch.rank = la > lb ? la : lb;
+    for (int k = 0; k < batch.rank; k++) {  // k-th batch axis from the last
+        const int64_t ea = k < la ? a->shape[la - 1 - k] : 1, eb = k < lb ? b->shape[lb - 1 - k] : 1;
+        if (ea != eb && ea != 1 && eb != 1) return false;
+        batch.e[batch.rank - 1 - k] = ea == 1 ? eb : ea;
     }
     return true;
 }
 
-// element stride of t's batch matrices along each output batch dim (0 = broadcast)
-void batch_strides(const nc_tensor *t, const int64_t *st, const BatchDims &bd, int64_t *out) {
-    const int tb = t->ndim - 2;
-    for (int i = 0; i < bd.nb; i++) {
-        const int j = i - (bd.nb - tb);
-        out[i] = (j < 0 || t->shape[j] == 1) ? 0 : st[j];
+nc_status bmm_shape(nc_node *n, OutSpec &out) {
+    if (!inputs_f32(n, 0, 2)) return NC_ERR_DTYPE;
+    const Dims a = Dims::of(n->in[0]), b = Dims::of(n->in[1]);
+    if (a.rank < 2 || b.rank < 2 || a.back(0) != b.back(1) || !batch_of(n->in[0], n->in[1], out.dims)) {
+        char ta[96], tb[96];
+        return reject(n, NC_ERR_SHAPE, "matmul: cannot multiply %s by %s (expected [..., M, K] @ [..., K, N])",
+                      a.text(ta, sizeof ta), b.text(tb, sizeof tb));
     }
-}
-
-struct BmmOperand {
-    const float *p;
-    int trans;
-    int64_t ld;
-    int64_t bst[NC_MAX_DIMS];
-};
-
-bool bmm_operand(nc_tensor *t, const BatchDims &bd, BmmOperand *o) {
-    const int nd = t->ndim;
-    const int64_t rows = t->shape[nd - 2], cols = t->shape[nd - 1];
-    const int64_t *st = t->stride;
-    int64_t cs[NC_MAX_DIMS];
-    if (t->stride[nd - 1] == 1 && t->stride[nd - 2] >= cols) {
-        o->p = fptr(t), o->trans = 0, o->ld = t->stride[nd - 2];
-    } else if (t->stride[nd - 2] == 1 && t->stride[nd - 1] >= rows) {
-        o->p = fptr(t), o->trans = 1, o->ld = t->stride[nd - 1];
-    } else {
-        o->p = contig_f32(t), o->trans = 0, o->ld = cols;
-        contig_strides(nd, t->shape, cs);
-        st = cs;
-    }
-    batch_strides(t, st, bd, o->bst);
-    return o->p != nullptr;
-}
-
-nc_status bmm_infer(nc_node *n, nc_dtype *dt, int *nd, int64_t *shape) {
-    nc_tensor *a = n->in[0], *b = n->in[1];
-    BatchDims bd;
-    if (!expect_f32(n, 0) || !expect_f32(n, 1)) return NC_ERR_DTYPE;
-    if (a->ndim < 2 || b->ndim < 2 || a->shape[a->ndim - 1] != b->shape[b->ndim - 2] || !batch_shape(a, b, &bd)) {
-        char sa[96], sb[96];
-        error(a->ctx, NC_ERR_SHAPE, "matmul: cannot multiply %s by %s (expected [..., M, K] @ [..., K, N])",
-              shape_str(a->ndim, a->shape, sa, sizeof sa), shape_str(b->ndim, b->shape, sb, sizeof sb));
-        return NC_ERR_SHAPE;
-    }
-    *dt = NC_F32;
-    *nd = bd.nb + 2;
-    memcpy(shape, bd.shape, sizeof(int64_t) * (size_t)bd.nb);
-    shape[bd.nb] = a->shape[a->ndim - 2];
-    shape[bd.nb + 1] = b->shape[b->ndim - 1];
+    out.dims.push(a.back(1));
+    out.dims.push(b.back(0));
     return NC_OK;
 }
 
-bool bmm_run(nc_ctx *ctx, const BatchDims &bd, int ta, int tb, int64_t M, int64_t N, int64_t K, const float *A,
-             int64_t lda, const int64_t *sa, const float *B, int64_t ldb, const int64_t *sb, float beta, float *C,
-             int64_t ldc, const int64_t *sc) {
-    const size_t ws_bytes = nc_hip_gemm_f32_bmm_workspace(bd.count);
-    char *ws = ws_bytes ? arena_alloc(ctx, ws_bytes) : nullptr;
-    if (ws_bytes && !ws) return false;
-    return hip_layer_ok(ctx,
-                        nc_hip_gemm_f32_bmm(ta, tb, M, N, K, A, lda, B, ldb, beta, C, ldc, bd.nb, bd.shape, sa, sb,
-                                            sc, ws, ws_bytes, stream(ctx)),
-                        "matmul");
-}
-
 nc_status bmm_fwd(nc_node *n) {
-    nc_tensor *a = n->in[0], *b = n->in[1], *o = n->out;
-    BatchDims bd;
-    batch_shape(a, b, &bd);
-    BmmOperand A, B;
+    nc_tensor *at = n->in[0], *bt = n->in[1], *o = n->out;
+    Dims batch;
+    batch_of(at, bt, batch);
+    const int64_t M = at->shape[at->ndim - 2], K = at->shape[at->ndim - 1], N = bt->shape[bt->ndim - 1];
+    Operand a, b;
+    int64_t cst[NC_MAX_DIMS];
+    batch_steps(o, o->stride, batch, cst);
     float *C = fptr(o);
-    if (!bmm_operand(a, bd, &A) || !bmm_operand(b, bd, &B) || !C) return NC_ERR_STATE;
-    const int64_t M = o->shape[bd.nb], N = o->shape[bd.nb + 1], K = a->shape[a->ndim - 1];
-    int64_t sc[NC_MAX_DIMS];
-    batch_strides(o, o->stride, bd, sc);
-    if (!bmm_run(o->ctx, bd, A.trans, B.trans, M, N, K, A.p, A.ld, A.bst, B.p, B.ld, B.bst, 0.0f, C, N, sc))
-        return NC_ERR_STATE;
+    if (!batch_operand(at, batch, a) || !batch_operand(bt, batch, b) || !C) return NC_ERR_STATE;
+    if (!product(o->ctx, batch, M, N, K, a, b, 0.0f, C, N, cst, "matmul")) return NC_ERR_STATE;
     wrote_dev(o);
     return NC_OK;
 }
 
 void bmm_bwd(nc_node *n) {
-    nc_tensor *a = n->in[0], *b = n->in[1], *o = n->out;
+    nc_tensor *at = n->in[0], *bt = n->in[1], *o = n->out;
     nc_ctx *ctx = o->ctx;
-    BatchDims bd;
-    batch_shape(a, b, &bd);
-    const int64_t M = o->shape[bd.nb], N = o->shape[bd.nb + 1], K = a->shape[a->ndim - 1];
-    const float *g = fptr(o->grad);
-    if (!g) return;
-    int64_t cs[NC_MAX_DIMS], sg[NC_MAX_DIMS], sgrad[NC_MAX_DIMS];
-    contig_strides(o->ndim, o->shape, cs);
-    batch_strides(o, cs, bd, sg);
-    if (needs_grad(a) && grad_buf(a)) {  // dA_i (M x K) (+)= dC_i @ B_i^T
-        BmmOperand B;
-        const float beta = grad_acc(a) ? 1.0f : 0.0f;
-        float *ga = fptr(a->grad);
-        contig_strides(a->ndim, a->shape, cs);
-        batch_strides(a, cs, bd, sgrad);
-        if (ga && bmm_operand(b, bd, &B) &&
-            bmm_run(ctx, bd, 0, !B.trans, M, K, N, g, N, sg, B.p, B.ld, B.bst, beta, ga, K, sgrad))
-            wrote_dev(a->grad);
+    Dims batch;
+    batch_of(at, bt, batch);
+    const int64_t M = at->shape[at->ndim - 2], K = at->shape[at->ndim - 1], N = bt->shape[bt->ndim - 1];
+    Operand g = dense(fptr(o->grad), N);
+    if (!g.m.p) return;
+    grad_steps(o, batch, g.bst);
+    float beta;
+    int64_t gst[NC_MAX_DIMS];
+    if (needs_grad(at)) {  // dA_i [M, K] (+)= G_i @ B_i^T
+        Operand b;
+        float *ga = grad_target(at, &beta);
+        grad_steps(at, batch, gst);
+        if (ga && batch_operand(bt, batch, b) && product(ctx, batch, M, K, N, g, b.transposed(), beta, ga, K, gst, "matmul"))
+            wrote_dev(at->grad);
     }
-    if (needs_grad(b) && grad_buf(b)) {  // dB_i (K x N) (+)= A_i^T @ dC_i
-        BmmOperand A;
-        const float beta = grad_acc(b) ? 1.0f : 0.0f;
-        float *gb = fptr(b->grad);
-        contig_strides(b->ndim, b->shape, cs);
-        batch_strides(b, cs, bd, sgrad);
-        if (gb && bmm_operand(a, bd, &A) &&
-            bmm_run(ctx, bd, !A.trans, 0, K, N, M, A.p, A.ld, A.bst, g, N, sg, beta, gb, N, sgrad))
-            wrote_dev(b->grad);
+    if (needs_grad(bt)) {  // dB_i [K, N] (+)= A_i^T @ G_i
+        Operand a;
+        float *gb = grad_target(bt, &beta);
+        grad_steps(bt, batch, gst);
+        if (gb && batch_operand(at, batch, a) && product(ctx, batch, K, N, M, a.transposed(), g, beta, gb, N, gst, "matmul"))
+            wrote_dev(bt->grad);
     }
 }
 
-const OpDef op_bmm = {"bmm", 0, 0, bmm_infer, nullptr, bmm_fwd, bmm_bwd};
+const OpDef op_bmm = {"bmm", 0, 0, bmm_shape, nullptr, bmm_fwd, bmm_bwd};
 
-// ---- linear: y = x @ W^T + b, W [out, in] (ops_linalg.c:255-338) ---------------------------------
-nc_status linear_infer(nc_node *n, nc_dtype *dt, int *nd, int64_t *shape) {
-    nc_tensor *x = n->in[0], *w = n->in[1], *b = n->n_in > 2 ? n->in[2] : nullptr;
-    for (int i = 0; i < n->n_in; i++)
-        if (!expect_f32(n, i)) return NC_ERR_DTYPE;
-    if (x->ndim < 1 || w->ndim != 2 || x->shape[x->ndim - 1] != w->shape[1] ||
-        (b && (b->ndim != 1 || b->shape[0] != w->shape[0]))) {
-        char sx[96], sw[96], sb[96] = "none";
-        if (b) shape_str(b->ndim, b->shape, sb, sizeof sb);
-        error(x->ctx, NC_ERR_SHAPE, "linear: expected x [..., in], weight [out, in], bias [out]; got %s, %s, %s",
-              shape_str(x->ndim, x->shape, sx, sizeof sx), shape_str(w->ndim, w->shape, sw, sizeof sw), sb);
-        return NC_ERR_SHAPE;
+// ---- linear: y = x @ W^T + b, x [..., in], W [out, in], b [out] -----------------------------------------
+nc_status linear_shape(nc_node *n, OutSpec &out) {
+    if (!inputs_f32(n, 0, n->n_in)) return NC_ERR_DTYPE;
+    const bool has_b = n->n_in > 2;
+    const Dims x = Dims::of(n->in[0]), w = Dims::of(n->in[1]), b = has_b ? Dims::of(n->in[2]) : Dims{};
+    if (x.rank < 1 || w.rank != 2 || x.back(0) != w.e[1] || (has_b && (b.rank != 1 || b.e[0] != w.e[0]))) {
+        char tx[96], tw[96], tb[96] = "none";
+        if (has_b) b.text(tb, sizeof tb);
+        return reject(n, NC_ERR_SHAPE, "linear: expected x [..., in], weight [out, in], bias [out]; got %s, %s, %s",
+                      x.text(tx, sizeof tx), w.text(tw, sizeof tw), tb);
     }
-    *dt = NC_F32;
-    *nd = x->ndim;
-    memcpy(shape, x->shape, sizeof(int64_t) * (size_t)x->ndim);
-    shape[x->ndim - 1] = w->shape[0];
+    out.dims = x;
+    out.dims.e[x.rank - 1] = w.e[0];
     return NC_OK;
 }
 
 nc_status linear_fwd(nc_node *n) {
-    nc_tensor *x = n->in[0], *w = n->in[1], *b = n->n_in > 2 ? n->in[2] : nullptr;
+    nc_tensor *x = n->in[0], *w = n->in[1], *bias = n->n_in > 2 ? n->in[2] : nullptr;
     nc_ctx *ctx = x->ctx;
-    const int64_t in = w->shape[1], out = w->shape[0], M = in ? nc_numel(x) / in : 0;
-    const float *X = contig_f32(x), *W = contig_f32(w), *B = b ? contig_f32(b) : nullptr;
+    const int64_t M = leading_rows(x), in = w->shape[1], out = w->shape[0];
+    Operand a, wt;
+    const int64_t *unused;
+    int64_t packed[NC_MAX_DIMS];
+    const float *B = bias ? contig_f32(bias) : nullptr;
     float *Y = fptr(n->out);
-    if (!X || !W || (b && !B) || !Y) return NC_ERR_STATE;
-    if (!gemm(ctx, 0, 1, M, out, in, X, in, W, in, 0.0f, Y, out, "linear")) return NC_ERR_STATE;
-    if (B && M > 0 && out > 0) {  // y = (x W^T) + b, one rounding of the sum as the reference's beta = 1 pass
-        const int64_t shape[2] = {M, out}, sy[2] = {out, 1}, sbias[2] = {0, 1};
-        if (!hip_layer_ok(ctx, nc_hip_binary_fwd(NC_HIP_BIN_ADD, 2, shape, Y, sy, B, sbias, Y, sy, stream(ctx)),
-                          "linear"))
+    if (!as_rows(x, a.m) || !last_two(w, wt.m, &unused, packed) || (bias && !B) || !Y) return NC_ERR_STATE;
+    if (!product(ctx, Dims{}, M, out, in, a, wt.transposed(), 0.0f, Y, out, nullptr, "linear")) return NC_ERR_STATE;
+    if (B && M > 0 && out > 0) {  // y = (x W^T) + b: the sum rounded once, as a beta = 1 GEMM over b rows would
+        const int64_t shape[2] = {M, out}, sy[2] = {out, 1}, sb[2] = {0, 1};
+        if (!hip_layer_ok(ctx, nc_hip_binary_fwd(NC_HIP_BIN_ADD, 2, shape, Y, sy, B, sb, Y, sy, stream(ctx)), "linear"))
             return NC_ERR_STATE;
     }
     wrote_dev(n->out);
@@ -275,42 +308,49 @@ nc_status linear_fwd(nc_node *n) {
 }
 
 void linear_bwd(nc_node *n) {
-    nc_tensor *x = n->in[0], *w = n->in[1], *b = n->n_in > 2 ? n->in[2] : nullptr;
+    nc_tensor *x = n->in[0], *w = n->in[1], *bias = n->n_in > 2 ? n->in[2] : nullptr;
     nc_ctx *ctx = x->ctx;
-    const int64_t in = w->shape[1], out = w->shape[0], M = in ? nc_numel(x) / in : 0;
-    const float *g = fptr(n->out->grad);  // M x out
+    const int64_t M = leading_rows(x), in = w->shape[1], out = w->shape[0];
+    const float *g = fptr(n->out->grad);  // [M, out]
     if (!g) return;
-    if (needs_grad(x) && grad_buf(x)) {  // dX (M x in) (+)= dY @ W
-        const float beta = grad_acc(x) ? 1.0f : 0.0f;
-        const float *W = contig_f32(w);
-        float *gx = fptr(x->grad);
-        if (W && gx && gemm(ctx, 0, 0, M, in, out, g, out, W, in, beta, gx, in, "linear")) wrote_dev(x->grad);
+    float beta;
+    const int64_t *unused;
+    int64_t packed[NC_MAX_DIMS];
+    if (needs_grad(x)) {  // dX [M, in] (+)= G @ W
+        Operand wm;
+        float *gx = grad_target(x, &beta);
+        if (gx && last_two(w, wm.m, &unused, packed) &&
+            product(ctx, Dims{}, M, in, out, dense(g, out), wm, beta, gx, in, nullptr, "linear"))
+            wrote_dev(x->grad);
     }
-    if (needs_grad(w) && grad_buf(w)) {  // dW (out x in) (+)= dY^T @ X
-        const float beta = grad_acc(w) ? 1.0f : 0.0f;
-        const float *X = contig_f32(x);
-        float *gw = fptr(w->grad);
-        if (X && gw && gemm(ctx, 1, 0, out, in, M, g, out, X, in, beta, gw, in, "linear")) wrote_dev(w->grad);
+    if (needs_grad(w)) {  // dW [out, in] (+)= G^T @ X
+        Operand xm;
+        float *gw = grad_target(w, &beta);
+        if (gw && as_rows(x, xm.m) &&
+            product(ctx, Dims{}, out, in, M, dense(g, out).transposed(), xm, beta, gw, in, nullptr, "linear"))
+            wrote_dev(w->grad);
     }
-    if (b && needs_grad(b) && grad_buf(b)) {  // db (+)= column sums of dY, fp64 in a fixed order
-        const int acc = grad_acc(b);
-        float *gb = fptr(b->grad);
-        if (!gb) return;
+    if (bias && needs_grad(bias) && grad_buf(bias)) {  // db (+)= column sums of G, fp64 in a fixed order
+        const int acc = grad_acc(bias);
+        float *gb = fptr(bias->grad);
         const int64_t shape[2] = {M, out}, sg[2] = {out, 1}, sgb[2] = {0, 1};
         const size_t ws_bytes = nc_hip_binary_bwd_workspace(2, shape, sgb);
         char *ws = ws_bytes ? arena_alloc(ctx, ws_bytes) : nullptr;
-        if (ws_bytes && !ws) return;
+        if (!gb || (ws_bytes && !ws)) return;
         if (hip_layer_ok(ctx,
                          nc_hip_binary_bwd(NC_HIP_BIN_ADD, 1, 2, shape, g, sg, g, sg, gb, sgb, gb, sgb, acc, ws,
                                            ws_bytes, stream(ctx)),
                          "linear"))
-            wrote_dev(b->grad);
+            wrote_dev(bias->grad);
     }
 }
 
-const OpDef op_linear = {"linear", 0, 0, linear_infer, nullptr, linear_fwd, linear_bwd};
+const OpDef op_linear = {"linear", 0, 0, linear_shape, nullptr, linear_fwd, linear_bwd};
 
 }  // namespace
+}  // namespace nce
+
+using namespace nce;
 
 extern "C" {
 

@@ -7,16 +7,11 @@ namespace nce {
 
 enum { SM_LOG = 0, SM_PLAIN = 1 };
 
-static nc_status softmax_infer(nc_node *n, nc_dtype *dt, int *nd, int64_t *shape) {
-    nc_tensor *x = n->in[0];
-    if (!expect_f32(n, 0)) return NC_ERR_DTYPE;
-    if (x->ndim < 1) {
-        error(x->ctx, NC_ERR_SHAPE, "%s: input must have at least 1 dimension", n->op->name);
-        return NC_ERR_SHAPE;
-    }
-    *dt = NC_F32;
-    *nd = x->ndim;
-    memcpy(shape, x->shape, sizeof(int64_t) * (size_t)x->ndim);
+// softmax rows are the last axis
+static nc_status softmax_shape(nc_node *n, OutSpec &out) {
+    if (!inputs_f32(n, 0, 1)) return NC_ERR_DTYPE;
+    out.dims = Dims::of(n->in[0]);
+    if (out.dims.rank == 0) return reject(n, NC_ERR_SHAPE, "%s: input must have at least 1 dimension", n->op->name);
     return NC_OK;
 }
 
@@ -54,31 +49,24 @@ static void softmax_bwd(nc_node *n) {
     wrote_dev(in->grad);
 }
 
-const OpDef op_log_softmax = {"log_softmax", 0, SM_LOG, softmax_infer, nullptr, softmax_fwd, softmax_bwd};
-const OpDef op_softmax = {"softmax", 0, SM_PLAIN, softmax_infer, nullptr, softmax_fwd, softmax_bwd};
+const OpDef op_log_softmax = {"log_softmax", 0, SM_LOG, softmax_shape, nullptr, softmax_fwd, softmax_bwd};
+const OpDef op_softmax = {"softmax", 0, SM_PLAIN, softmax_shape, nullptr, softmax_fwd, softmax_bwd};
 
 // ---- layer norm ------------------------------------------------------------------------------------
-// inputs: x, then weight and bias [D] when present (p.i[1], p.i[2]); p.i[0] = normalized ndim
-static nc_status layer_norm_infer(nc_node *n, nc_dtype *dt, int *nd, int64_t *shape) {
-    nc_tensor *x = n->in[0];
+// inputs: x, then weight and bias when present (p.i[1], p.i[2]).  The rows are x's last k axes
+// flattened (k = p.i[0]); weight and bias hold one value per row element.
+static nc_status layer_norm_shape(nc_node *n, OutSpec &out) {
+    if (!inputs_f32(n, 0, n->n_in)) return NC_ERR_DTYPE;
+    out.dims = Dims::of(n->in[0]);
     const int k = (int)n->p.i[0];
-    for (int i = 0; i < n->n_in; i++)
-        if (!expect_f32(n, i)) return NC_ERR_DTYPE;
-    if (k < 1 || k > x->ndim) {
-        error(x->ctx, NC_ERR_SHAPE, "layer_norm: normalized_shape has %d dims, input only %d", k, x->ndim);
-        return NC_ERR_SHAPE;
-    }
-    const int64_t D = shape_numel(k, x->shape + x->ndim - k);
-    for (int i = 1; i < n->n_in; i++) {
-        if (nc_numel(n->in[i]) != D) {
-            error(x->ctx, NC_ERR_SHAPE, "layer_norm: weight/bias need %lld elements, got %lld", (long long)D,
-                  (long long)nc_numel(n->in[i]));
-            return NC_ERR_SHAPE;
-        }
-    }
-    *dt = NC_F32;
-    *nd = x->ndim;
-    memcpy(shape, x->shape, sizeof(int64_t) * (size_t)x->ndim);
+    if (k < 1 || k > out.dims.rank)
+        return reject(n, NC_ERR_SHAPE, "layer_norm: normalized_shape has %d dims, input only %d", k, out.dims.rank);
+    int64_t row = 1;
+    for (int j = 0; j < k; j++) row *= out.dims.back(j);
+    for (int i = 1; i < n->n_in; i++)
+        if (nc_numel(n->in[i]) != row)
+            return reject(n, NC_ERR_SHAPE, "layer_norm: weight/bias need %lld elements, got %lld", (long long)row,
+                          (long long)nc_numel(n->in[i]));
     return NC_OK;
 }
 
@@ -96,13 +84,11 @@ static nc_status layer_norm_fwd(nc_node *n) {
     float *b = has_b ? contig_f32(n->in[1 + has_w]) : nullptr;
     float *X = contig_f32(x), *Y = fptr(n->out);
     const int64_t D = ln_dim(n), R = D ? nc_numel(x) / D : 0;
-    const size_t sbytes = (size_t)(2 * R + 1) * sizeof(float);
-    float *stats = (float *)arena_alloc(ctx, sbytes);
+    // per-row {mean, rstd}, read again by the backward
+    float *stats = (float *)save_state(n, (size_t)(2 * R + 1) * sizeof(float));
     if (!X || !Y || !stats || (has_w && !w) || (has_b && !b)) return NC_ERR_STATE;
     if (!hip_layer_ok(ctx, nc_hip_layer_norm_fwd(R, D, X, w, b, n->p.f[0], Y, stats, stream(ctx)), "layer_norm"))
         return NC_ERR_STATE;
-    n->saved = stats;
-    n->saved_bytes = sbytes;
     wrote_dev(n->out);
     return NC_OK;
 }
@@ -136,7 +122,7 @@ static void layer_norm_bwd(nc_node *n) {
     if (gb) wrote_dev(bt->grad);
 }
 
-const OpDef op_layer_norm = {"layer_norm", 0, 0, layer_norm_infer, nullptr, layer_norm_fwd, layer_norm_bwd};
+const OpDef op_layer_norm = {"layer_norm", 0, 0, layer_norm_shape, nullptr, layer_norm_fwd, layer_norm_bwd};
 
 // ---- losses ----------------------------------------------------------------------------------------
 // cross_entropy (ops_nn.c:83-156) and nll_loss (ops_nn.c:368-426): f32 rows [N, C], i32 labels [N],
@@ -147,23 +133,18 @@ const OpDef op_layer_norm = {"layer_norm", 0, 0, layer_norm_infer, nullptr, laye
 // fails the call the reference's way.
 enum { LOSS_CE = 0, LOSS_NLL = 1 };
 
-static nc_status loss_infer(nc_node *n, nc_dtype *dt, int *nd, int64_t *) {
-    nc_tensor *x = n->in[0], *y = n->in[1];
+static nc_status loss_shape(nc_node *n, OutSpec &out) {
     const bool ce = n->op->kind == LOSS_CE;
-    if (!expect_f32(n, 0)) return NC_ERR_DTYPE;
-    if (y->dtype != NC_I32) {
-        error(x->ctx, NC_ERR_DTYPE, "%s: labels must be i32", n->op->name);
-        return NC_ERR_DTYPE;
+    if (!inputs_f32(n, 0, 1)) return NC_ERR_DTYPE;
+    if (n->in[1]->dtype != NC_I32) return reject(n, NC_ERR_DTYPE, "%s: labels must be i32", n->op->name);
+    const Dims x = Dims::of(n->in[0]), y = Dims::of(n->in[1]);
+    const bool rows_match = x.rank == 2 && y.rank == 1 && y.e[0] == x.e[0];
+    if (!rows_match || (ce && x.e[1] < 1)) {
+        char tx[96], ty[96];
+        return reject(n, NC_ERR_SHAPE, "%s: expected %s [N, C] and labels [N], got %s and %s", n->op->name,
+                      ce ? "logits" : "log-probabilities", x.text(tx, sizeof tx), y.text(ty, sizeof ty));
     }
-    if (x->ndim != 2 || y->ndim != 1 || y->shape[0] != x->shape[0] || (ce && x->shape[1] < 1)) {
-        char sa[96], sb[96];
-        error(x->ctx, NC_ERR_SHAPE, "%s: expected %s [N, C] and labels [N], got %s and %s", n->op->name,
-              ce ? "logits" : "log-probabilities", shape_str(x->ndim, x->shape, sa, sizeof sa),
-              shape_str(y->ndim, y->shape, sb, sizeof sb));
-        return NC_ERR_SHAPE;
-    }
-    *dt = NC_F32;
-    *nd = 0;
+    out.dims = Dims{};  // a 0-d loss
     return NC_OK;
 }
 
@@ -178,7 +159,7 @@ static nc_status loss_fwd(nc_node *n) {
     // saved block: [row statistics N x {max, log-sum-exp} floats (cross entropy)][labels N int32]
     const size_t pbytes = ce ? (size_t)N * 2 * sizeof(float) : 0;
     const size_t sbytes = pbytes + (size_t)(N ? N : 1) * sizeof(int32_t);
-    char *saved = arena_alloc(ctx, sbytes);
+    char *saved = (char *)save_state(n, sbytes);
     const size_t ws_bytes = nc_hip_loss_workspace(N, C);
     char *ws = arena_alloc(ctx, ws_bytes ? ws_bytes : 8);
     uint64_t *bad = (uint64_t *)arena_alloc(ctx, sizeof(uint64_t));
@@ -200,8 +181,6 @@ static nc_status loss_fwd(nc_node *n) {
               (long long)(hb >> 32), (long long)C);
         return NC_ERR_ARG;
     }
-    n->saved = saved;
-    n->saved_bytes = sbytes;
     wrote_dev(n->out);
     return NC_OK;
 }
@@ -231,8 +210,8 @@ static void loss_bwd(nc_node *n) {
     wrote_dev(xt->grad);
 }
 
-const OpDef op_cross_entropy = {"cross_entropy", 0, LOSS_CE, loss_infer, nullptr, loss_fwd, loss_bwd};
-const OpDef op_nll_loss = {"nll_loss", 0, LOSS_NLL, loss_infer, nullptr, loss_fwd, loss_bwd};
+const OpDef op_cross_entropy = {"cross_entropy", 0, LOSS_CE, loss_shape, nullptr, loss_fwd, loss_bwd};
+const OpDef op_nll_loss = {"nll_loss", 0, LOSS_NLL, loss_shape, nullptr, loss_fwd, loss_bwd};
 
 }  // namespace nce
 

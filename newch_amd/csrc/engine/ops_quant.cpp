@@ -1,50 +1,57 @@
-// int8: symmetric per-row weight quantization and the int8 linear.  Reference: engine/src/ops/ops_quant.c:23-113
-// (nc_quantize_rows: not an autograd op; results follow persistent mode like nc_empty).
+// int8: symmetric per-row weight quantization and the int8 linear.  Reference: engine/src/ops/ops_quant.c:23-113.
+// nc_quantize_rows is not an autograd op: its two results follow persistent mode like nc_empty.
 #include "engine.hpp"
 
 using namespace nce;
 
-extern "C" nc_tensor *nc_quantize_rows(nc_tensor *w, nc_tensor **scale) {
-    if (!w) return nullptr;
+// w [rows, cols] f32 -> q i8 [rows, cols] and one f32 scale per row, in one kernel
+static bool quantize(nc_tensor *w, nc_tensor *q, nc_tensor *s) {
     nc_ctx *ctx = w->ctx;
-    if (w->dtype != NC_F32 || w->ndim != 2) {
-        error(ctx, NC_ERR_SHAPE, "quantize_rows: expected a 2-D f32 tensor");
-        return nullptr;
-    }
-    float *W = contig_f32(w);
-    nc_tensor *q = nc_empty(ctx, NC_I8, 2, w->shape);
-    nc_tensor *s = nc_empty(ctx, NC_F32, 1, w->shape);
-    if (!W || !q || !s) return nullptr;
-    int8_t *qp = (int8_t *)dptr(q);
-    float *sp = fptr(s);
-    if (!qp || !sp) return nullptr;
-    if (!hip_layer_ok(ctx, nc_hip_quantize_rows(w->shape[0], w->shape[1], W, qp, sp, stream(ctx)), "quantize_rows"))
-        return nullptr;
+    Scratch scratch(ctx);  // a packed copy of a strided w is handed back when the call ends
+    const float *W = contig_f32(w);
+    int8_t *Q = (int8_t *)dptr_overwrite(q);
+    float *S = (float *)dptr_overwrite(s);
+    if (!W || !Q || !S ||
+        !hip_layer_ok(ctx, nc_hip_quantize_rows(w->shape[0], w->shape[1], W, Q, S, stream(ctx)), "quantize_rows"))
+        return false;
     wrote_dev(q);
     wrote_dev(s);
+    return true;
+}
+
+extern "C" nc_tensor *nc_quantize_rows(nc_tensor *w, nc_tensor **scale) {
+    if (!w) return nullptr;
+    if (w->dtype != NC_F32 || w->ndim != 2) {
+        error(w->ctx, NC_ERR_SHAPE, "quantize_rows: expected a 2-D f32 tensor");
+        return nullptr;
+    }
+    const int64_t rows = w->shape[0];
+    nc_tensor *q = nc_empty(w->ctx, NC_I8, 2, w->shape);
+    nc_tensor *s = q ? nc_empty(w->ctx, NC_F32, 1, &rows) : nullptr;
+    if (!s || !quantize(w, q, s)) return nullptr;
     if (scale) *scale = s;
     return q;
 }
 
 // ---- linear_int8 (ops_quant.c:41-113): y = dequant(quant_rows(x) @ wq^T) + b, inference only ----
 // inputs: x f32 [..., in], wq i8 [out, in] (contiguous), w_scale f32 [out], optional bias f32 [out]
-static nc_status qlinear_infer(nc_node *n, nc_dtype *dt, int *nd, int64_t *shape) {
-    nc_tensor *x = n->in[0], *wq = n->in[1], *ws = n->in[2], *b = n->n_in > 3 ? n->in[3] : nullptr;
-    if (x->dtype != NC_F32 || wq->dtype != NC_I8 || ws->dtype != NC_F32 || (b && b->dtype != NC_F32)) {
-        error(x->ctx, NC_ERR_DTYPE, "linear_int8: expected x f32, weight i8, scale f32, bias f32");
-        return NC_ERR_DTYPE;
+static nc_status qlinear_shape(nc_node *n, OutSpec &out) {
+    const bool has_b = n->n_in > 3;
+    const nc_dtype want[4] = {NC_F32, NC_I8, NC_F32, NC_F32};
+    for (int i = 0; i < n->n_in; i++)
+        if (n->in[i]->dtype != want[i])
+            return reject(n, NC_ERR_DTYPE, "linear_int8: expected x f32, weight i8, scale f32, bias f32");
+    const Dims x = Dims::of(n->in[0]), w = Dims::of(n->in[1]), sc = Dims::of(n->in[2]);
+    const Dims b = has_b ? Dims::of(n->in[3]) : Dims{};
+    const auto per_out = [&](const Dims &v) { return v.rank == 1 && v.e[0] == w.e[0]; };
+    const bool ok = x.rank >= 1 && w.rank == 2 && x.back(0) == w.e[1] && per_out(sc) && (!has_b || per_out(b));
+    if (!ok) {
+        char tx[96], tw[96];
+        return reject(n, NC_ERR_SHAPE, "linear_int8: expected x [..., in], weight [out, in], scale/bias [out]; got %s, %s",
+                      x.text(tx, sizeof tx), w.text(tw, sizeof tw));
     }
-    if (x->ndim < 1 || wq->ndim != 2 || x->shape[x->ndim - 1] != wq->shape[1] || ws->ndim != 1 ||
-        ws->shape[0] != wq->shape[0] || (b && (b->ndim != 1 || b->shape[0] != wq->shape[0]))) {
-        char sx[96], sw[96];
-        error(x->ctx, NC_ERR_SHAPE, "linear_int8: expected x [..., in], weight [out, in], scale/bias [out]; got %s, %s",
-              shape_str(x->ndim, x->shape, sx, sizeof sx), shape_str(wq->ndim, wq->shape, sw, sizeof sw));
-        return NC_ERR_SHAPE;
-    }
-    *dt = NC_F32;
-    *nd = x->ndim;
-    memcpy(shape, x->shape, sizeof(int64_t) * (size_t)x->ndim);
-    shape[x->ndim - 1] = wq->shape[0];
+    out.dims = x;
+    out.dims.e[x.rank - 1] = w.e[0];
     return NC_OK;
 }
 
@@ -70,7 +77,7 @@ static nc_status qlinear_fwd(nc_node *n) {
     return NC_OK;
 }
 
-static const OpDef op_linear_int8 = {"linear_int8", OPF_NONDIFF, 0, qlinear_infer, nullptr, qlinear_fwd, nullptr};
+static const OpDef op_linear_int8 = {"linear_int8", OPF_NONDIFF, 0, qlinear_shape, nullptr, qlinear_fwd, nullptr};
 
 extern "C" nc_tensor *nc_linear_int8(nc_tensor *x, nc_tensor *wq, nc_tensor *w_scale, nc_tensor *bias) {
     nc_tensor *in[4] = {x, wq, w_scale, bias};

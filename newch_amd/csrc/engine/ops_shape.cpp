@@ -1,290 +1,266 @@
-// Shape ops (views where the layout allows) and dtype conversion.
-// Reference: engine/src/ops/ops_shape.c (views :12-294, to_dtype :463-515).
+// Shape ops (views where the layout allows, copies otherwise) and dtype conversion.
+// Reference: engine/src/ops/ops_shape.c (reshape / transpose / slice / contiguous / detach :12-294,
+// to_dtype :463-515); the error messages and the view-or-copy results are the reference's.
+//
+// Every shape op here is described by one function: the Layout of its output over its input's
+// storage (extents, element strides, offset of element 0).  The alias rule turns that layout into a
+// view; the forward, used when a view is not allowed (persistent mode) or not possible, gathers the
+// same layout into new contiguous storage; the backward scatters the output gradient back through
+// the layout's strides taken over the contiguous gradient of the input.
 #include "engine.hpp"
 
 namespace nce {
 
-static nc_tensor *alias_with(nc_node *n, int nd, const int64_t *shape, const int64_t *stride, int64_t offset) {
+struct Layout {
+    Dims dims;
+    int64_t st[NC_MAX_DIMS] = {};
+    int64_t offset = 0;
+
+    static Layout of(const nc_tensor *t) {
+        Layout L;
+        L.dims = Dims::of(t);
+        memcpy(L.st, t->stride, sizeof(int64_t) * (size_t)t->ndim);
+        L.offset = t->offset;
+        return L;
+    }
+};
+
+// the output as a view of in[0]'s storage
+static bool view_of(nc_node *n, const Layout &L) {
     nc_tensor *t = tensor_alias(n->in[0], false);
-    if (!t) return nullptr;
-    t->ndim = nd;
-    memcpy(t->shape, shape, sizeof(int64_t) * (size_t)nd);
-    memcpy(t->stride, stride, sizeof(int64_t) * (size_t)nd);
-    t->offset = offset;
+    if (!t) return false;
+    t->ndim = L.dims.rank;
+    memcpy(t->shape, L.dims.e, sizeof(int64_t) * (size_t)L.dims.rank);
+    memcpy(t->stride, L.st, sizeof(int64_t) * (size_t)L.dims.rank);
+    t->offset = L.offset;
     n->out = t;
-    return t;
+    return true;
 }
 
-static nc_status same_shape_infer(nc_node *n, nc_dtype *dt, int *nd, int64_t *shape) {
-    *dt = n->in[0]->dtype;
-    *nd = n->in[0]->ndim;
-    memcpy(shape, n->in[0]->shape, sizeof(int64_t) * (size_t)*nd);
-    return NC_OK;
-}
-
-// gather a strided source layout (shape/stride/offset relative to x's storage) into out
-static nc_status gather_into(nc_tensor *x, const int64_t *shape, const int64_t *stride, int64_t offset,
-                             nc_tensor *out) {
+// the elements L shows in in[0]'s storage, in row-major order of L, into the output's new storage
+static nc_status gather(nc_node *n, const Layout &L) {
+    nc_tensor *x = n->in[0], *out = n->out;
     nc_ctx *ctx = out->ctx;
-    nc_tensor *o = owner_of(x);
-    if (!dptr(x)) return NC_ERR_STATE;
     const size_t es = dtype_size(x->dtype);
-    char *src = o->dev + offset * (int64_t)es;
-    char *dst = dptr(out);
-    if (!dst) return NC_ERR_STATE;
-    if (!hip_layer_ok(ctx, nc_hip_copy_strided((int)es, out->ndim, shape, src, stride, dst, stream(ctx)), "copy"))
+    if (!dptr(x)) return NC_ERR_STATE;
+    const char *src = owner_of(x)->dev + L.offset * (int64_t)es;
+    char *dst = dptr_overwrite(out);
+    if (!dst ||
+        !hip_layer_ok(ctx, nc_hip_copy_strided((int)es, L.dims.rank, L.dims.e, src, L.st, dst, stream(ctx)),
+                      n->op->name))
         return NC_ERR_STATE;
     wrote_dev(out);
     return NC_OK;
 }
 
-static nc_status copy_fwd(nc_node *n) {
-    nc_tensor *x = n->in[0];
-    return gather_into(x, x->shape, x->stride, x->offset, n->out);
-}
+// ---- contiguous copy and flat gradient ---------------------------------------------------------
+static nc_status copy_fwd(nc_node *n) { return gather(n, Layout::of(n->in[0])); }
 
-// grad layout equals the input's logical layout: a flat accumulate (axpy with alpha 1, as the reference)
+// same logical layout on both sides: a flat accumulate (axpy with alpha 1)
 static void flat_bwd(nc_node *n) {
     nc_tensor *x = n->in[0];
-    nc_ctx *ctx = x->ctx;
-    if (!grad_buf(x)) return;
-    float *g = fptr(n->out->grad), *gi = fptr(x->grad);  // fptr gives a fresh buffer its zeros
-    if (!g || !gi) return;
-    if (!hip_layer_ok(ctx, nc_hip_axpy(nc_numel(x), 1.0f, g, gi, stream(ctx)), n->op->name)) return;
+    const float *g = grad_buf(x) ? fptr(n->out->grad) : nullptr;
+    float *gx = g ? fptr(x->grad) : nullptr;  // a fresh buffer gets its zeros here
+    if (!gx || !hip_layer_ok(x->ctx, nc_hip_axpy(nc_numel(x), 1.0f, g, gx, stream(x->ctx)), n->op->name)) return;
     wrote_dev(x->grad);
 }
 
-// ---- reshape ---------------------------------------------------------------------------------------
-static nc_status reshape_infer(nc_node *n, nc_dtype *dt, int *nd, int64_t *shape) {
-    nc_tensor *x = n->in[0];
-    const int r = (int)n->p.i[NC_MAX_DIMS];
-    int infer_at = -1;
-    int64_t known = 1;
-    for (int i = 0; i < r; i++) {
-        shape[i] = n->p.i[i];
-        if (shape[i] == -1 && infer_at < 0) infer_at = i;
-        else if (shape[i] < 0) {
-            error(x->ctx, NC_ERR_SHAPE, "reshape: invalid dimension %lld", (long long)shape[i]);
-            return NC_ERR_SHAPE;
-        } else known *= shape[i];
+// ---- reshape: p.i[0 .. rank) the requested extents (at most one -1), p.i[NC_MAX_DIMS] the rank ------
+static nc_status reshape_shape(nc_node *n, OutSpec &out) {
+    const Dims x = Dims::of(n->in[0]);
+    out.dtype = n->in[0]->dtype;
+    int free_at = -1;  // the extent to infer
+    int64_t fixed = 1;
+    for (int i = 0; i < (int)n->p.i[NC_MAX_DIMS]; i++) {
+        const int64_t e = n->p.i[i];
+        if (e == -1 && free_at < 0)
+            free_at = i;
+        else if (e < 0)
+            return reject(n, NC_ERR_SHAPE, "reshape: invalid dimension %lld", (long long)e);
+        else
+            fixed *= e;
+        out.dims.push(e);
     }
-    const int64_t total = nc_numel(x);
-    if (infer_at >= 0) shape[infer_at] = known ? total / known : 0;
-    if (shape_numel(r, shape) != total) {
-        char sa[96], sb[96];
-        error(x->ctx, NC_ERR_SHAPE, "reshape: cannot view %s as %s", shape_str(x->ndim, x->shape, sa, sizeof sa),
-              shape_str(r, shape, sb, sizeof sb));
-        return NC_ERR_SHAPE;
+    if (free_at >= 0) out.dims.e[free_at] = fixed ? x.numel() / fixed : 0;
+    if (out.dims.numel() != x.numel()) {
+        char tx[96], to[96];
+        return reject(n, NC_ERR_SHAPE, "reshape: cannot view %s as %s", x.text(tx, sizeof tx),
+                      out.dims.text(to, sizeof to));
     }
-    *dt = x->dtype;
-    *nd = r;
     return NC_OK;
 }
 
-// Strides that show x's elements in row-major order as `shape`, if such strides exist (the view
-// rule of torch's reshape).  x's non-unit dims are grouped into chunks, maximal runs stored back to
-// back (innermost first); the new dims, innermost first, must tile those chunks exactly.
-static bool view_strides(const nc_tensor *x, int nd, const int64_t *shape, int64_t *st) {
+// Strides that show x's elements in row-major order with the new extents, when they exist (the view
+// rule of torch's reshape): x's non-unit axes, innermost first, merge into runs stored back to back;
+// the new extents, innermost first, must split those runs exactly.
+static bool reshape_layout(const nc_tensor *x, const Dims &to, Layout &L) {
+    L.dims = to;
+    L.offset = x->offset;
     if (nc_is_contiguous(x) || nc_numel(x) == 0) {
-        contig_strides(nd, shape, st);
+        contig_strides(to.rank, to.e, L.st);
         return true;
     }
-    int64_t chunk_n[NC_MAX_DIMS], chunk_s[NC_MAX_DIMS];
-    int nchunks = 0;
+    struct Run {
+        int64_t len, step;
+    } runs[NC_MAX_DIMS];
+    int nruns = 0;
     for (int d = x->ndim - 1; d >= 0; d--) {
         if (x->shape[d] == 1) continue;
-        if (nchunks > 0 && x->stride[d] == chunk_s[nchunks - 1] * chunk_n[nchunks - 1]) {
-            chunk_n[nchunks - 1] *= x->shape[d];
-        } else {
-            chunk_s[nchunks] = x->stride[d];
-            chunk_n[nchunks] = x->shape[d];
-            nchunks++;
-        }
+        Run *last = nruns ? &runs[nruns - 1] : nullptr;
+        if (last && x->stride[d] == last->step * last->len)
+            last->len *= x->shape[d];
+        else
+            runs[nruns++] = {x->shape[d], x->stride[d]};
     }
-    int c = 0;
-    int64_t run = 1;
-    for (int d = nd - 1; d >= 0; d--) {
-        if (shape[d] == 1) {
-            st[d] = (c < nchunks ? chunk_s[c] : 1) * run;
+    int r = 0;
+    int64_t within = 1;  // elements of run r covered so far
+    for (int d = to.rank - 1; d >= 0; d--) {
+        const int64_t e = to.e[d];
+        if (e == 1) {  // any stride works: the one the next axis would have
+            L.st[d] = (r < nruns ? runs[r].step : 1) * within;
             continue;
         }
-        if (c >= nchunks) return false;
-        st[d] = chunk_s[c] * run;
-        run *= shape[d];
-        if (run > chunk_n[c]) return false;
-        if (run == chunk_n[c]) {
-            c++;
-            run = 1;
+        if (r == nruns) return false;
+        L.st[d] = runs[r].step * within;
+        within *= e;
+        if (within > runs[r].len || runs[r].len % within) return false;
+        if (within == runs[r].len) {
+            r++;
+            within = 1;
         }
     }
-    return c == nchunks;
+    return r == nruns;
 }
 
-static int reshape_view(nc_node *n, int nd, const int64_t *shape) {
-    int64_t st[NC_MAX_DIMS];
-    if (!view_strides(n->in[0], nd, shape, st)) return 0;
-    return alias_with(n, nd, shape, st, n->in[0]->offset) != nullptr;
+static bool reshape_alias(nc_node *n, const OutSpec &out) {
+    Layout L;
+    return reshape_layout(n->in[0], out.dims, L) && view_of(n, L);
 }
 
-// gather for reshape copies runs over x's own shape (the element order is the same)
-static nc_status reshape_copy(nc_node *n) {
-    nc_tensor *x = n->in[0], *out = n->out;
-    nc_ctx *ctx = out->ctx;
-    if (!dptr(x)) return NC_ERR_STATE;
-    const size_t es = dtype_size(x->dtype);
-    char *dst = dptr(out);
-    if (!dst) return NC_ERR_STATE;
-    if (!hip_layer_ok(ctx,
-                      nc_hip_copy_strided((int)es, x->ndim, x->shape, owner_of(x)->dev + x->offset * (int64_t)es,
-                                          x->stride, dst, stream(ctx)),
-                      "reshape"))
-        return NC_ERR_STATE;
-    wrote_dev(out);
-    return NC_OK;
-}
-const OpDef op_reshape = {"reshape", OPF_VIEW, 0, reshape_infer, reshape_view, reshape_copy, flat_bwd};
+// a reshape copy keeps the element order: gather x over its own extents
+const OpDef op_reshape = {"reshape", OPF_VIEW, 0, reshape_shape, reshape_alias, copy_fwd, flat_bwd};
 
-// ---- transpose -------------------------------------------------------------------------------------
-static nc_status transpose_infer(nc_node *n, nc_dtype *dt, int *nd, int64_t *shape) {
-    nc_tensor *x = n->in[0];
-    const int a0 = norm_axis((int)n->p.i[0], x->ndim), a1 = norm_axis((int)n->p.i[1], x->ndim);
-    if (a0 < 0 || a1 < 0) {
-        error(x->ctx, NC_ERR_ARG, "transpose: axes (%d, %d) out of range for %d-d tensor", (int)n->p.i[0],
-              (int)n->p.i[1], x->ndim);
-        return NC_ERR_ARG;
-    }
-    n->p.i[0] = a0;
-    n->p.i[1] = a1;
-    *dt = x->dtype;
-    *nd = x->ndim;
-    memcpy(shape, x->shape, sizeof(int64_t) * (size_t)x->ndim);
-    shape[a0] = x->shape[a1];
-    shape[a1] = x->shape[a0];
+// ---- transpose: p.i[0], p.i[1] the two axes (normalized by the shape rule) --------------------------
+static nc_status transpose_shape(nc_node *n, OutSpec &out) {
+    const Dims x = Dims::of(n->in[0]);
+    const int a = norm_axis((int)n->p.i[0], x.rank), b = norm_axis((int)n->p.i[1], x.rank);
+    if (a < 0 || b < 0)
+        return reject(n, NC_ERR_ARG, "transpose: axes (%d, %d) out of range for %d-d tensor", (int)n->p.i[0],
+                      (int)n->p.i[1], x.rank);
+    n->p.i[0] = a;
+    n->p.i[1] = b;
+    out.dtype = n->in[0]->dtype;
+    out.dims = x;
+    std::swap(out.dims.e[a], out.dims.e[b]);
     return NC_OK;
 }
 
-static void swapped_strides(const nc_node *n, int64_t *st) {
-    const nc_tensor *x = n->in[0];
-    memcpy(st, x->stride, sizeof(int64_t) * (size_t)x->ndim);
-    const int a0 = (int)n->p.i[0], a1 = (int)n->p.i[1];
-    st[a0] = x->stride[a1];
-    st[a1] = x->stride[a0];
+static Layout transposed(const nc_node *n) {
+    Layout L = Layout::of(n->in[0]);
+    const int a = (int)n->p.i[0], b = (int)n->p.i[1];
+    std::swap(L.dims.e[a], L.dims.e[b]);
+    std::swap(L.st[a], L.st[b]);
+    return L;
 }
 
-static int transpose_view(nc_node *n, int nd, const int64_t *shape) {
-    int64_t st[NC_MAX_DIMS];
-    swapped_strides(n, st);
-    return alias_with(n, nd, shape, st, n->in[0]->offset) != nullptr;
+static bool transpose_alias(nc_node *n, const OutSpec &) { return view_of(n, transposed(n)); }
+static nc_status transpose_fwd(nc_node *n) { return gather(n, transposed(n)); }
+
+// ---- slice: x[..., start : start + len*step : step, ...] along one axis ------------------------------
+// p.i[0] axis (normalized by the shape rule), p.i[1] start, p.i[2] length, p.i[3] step
+static nc_status slice_shape(nc_node *n, OutSpec &out) {
+    const Dims x = Dims::of(n->in[0]);
+    const int a = norm_axis((int)n->p.i[0], x.rank);
+    const int64_t start = n->p.i[1], len = n->p.i[2], step = n->p.i[3];
+    if (a < 0) return reject(n, NC_ERR_ARG, "slice: axis %d out of range for %d-d tensor", (int)n->p.i[0], x.rank);
+    const bool fits = step >= 1 && len >= 0 && start >= 0 && start <= x.e[a] &&
+                      (len == 0 || start + (len - 1) * step < x.e[a]);
+    if (!fits)
+        return reject(n, NC_ERR_ARG, "slice: start %lld, length %lld, step %lld do not fit axis %d of size %lld",
+                      (long long)start, (long long)len, (long long)step, a, (long long)x.e[a]);
+    n->p.i[0] = a;
+    out.dtype = n->in[0]->dtype;
+    out.dims = x;
+    out.dims.e[a] = len;
+    return NC_OK;
 }
 
-static nc_status transpose_fwd(nc_node *n) {
-    int64_t st[NC_MAX_DIMS];
-    swapped_strides(n, st);
-    return gather_into(n->in[0], n->out->shape, st, n->in[0]->offset, n->out);
+static Layout sliced(const nc_node *n) {
+    Layout L = Layout::of(n->in[0]);
+    const int a = (int)n->p.i[0];
+    if (n->p.i[2] > 0) L.offset += n->p.i[1] * L.st[a];
+    L.dims.e[a] = n->p.i[2];
+    L.st[a] *= n->p.i[3];
+    return L;
+}
+
+static bool slice_alias(nc_node *n, const OutSpec &) { return view_of(n, sliced(n)); }
+static nc_status slice_fwd(nc_node *n) { return gather(n, sliced(n)); }
+
+// transpose / slice backward: the output gradient (contiguous) is added into x's contiguous gradient
+// at the places the layout picked, i.e. through the layout rebuilt over x's contiguous strides
+static void layout_bwd(nc_node *n, const Layout &over_grad) {
+    nc_tensor *x = n->in[0], *o = n->out;
+    if (!grad_buf(x) || nc_numel(o) == 0) return;  // an empty output adds nothing to x's (zero) gradient
+    const float *g = fptr(o->grad);
+    float *gx = g ? fptr(x->grad) : nullptr;
+    if (!gx || !hip_layer_ok(x->ctx,
+                             nc_hip_accumulate_strided(o->ndim, o->shape, g, gx + over_grad.offset, over_grad.st,
+                                                       stream(x->ctx)),
+                             n->op->name))
+        return;
+    wrote_dev(x->grad);
+}
+
+// x's layout with contiguous strides and no offset: the layout of x's gradient buffer
+static Layout dense_of(const nc_tensor *x) {
+    Layout L;
+    L.dims = Dims::of(x);
+    contig_strides(x->ndim, x->shape, L.st);
+    return L;
 }
 
 static void transpose_bwd(nc_node *n) {
-    nc_tensor *x = n->in[0], *o = n->out;
-    nc_ctx *ctx = x->ctx;
-    if (!grad_buf(x)) return;
-    // walk the contiguous out grad; write through x's contiguous strides, swapped
-    int64_t st[NC_MAX_DIMS];
-    contig_strides(x->ndim, x->shape, st);
-    const int a0 = (int)n->p.i[0], a1 = (int)n->p.i[1];
-    const int64_t t = st[a0];
-    st[a0] = st[a1];
-    st[a1] = t;
-    float *g = fptr(o->grad), *gi = fptr(x->grad);
-    if (!g || !gi) return;
-    if (!hip_layer_ok(ctx, nc_hip_accumulate_strided(o->ndim, o->shape, g, gi, st, stream(ctx)), "transpose")) return;
-    wrote_dev(x->grad);
-}
-
-const OpDef op_transpose = {"transpose", OPF_VIEW, 0, transpose_infer, transpose_view, transpose_fwd, transpose_bwd};
-
-// ---- slice: x[..., start : start + len*step : step, ...] along one axis ----------------------------
-static nc_status slice_infer(nc_node *n, nc_dtype *dt, int *nd, int64_t *shape) {
-    nc_tensor *x = n->in[0];
-    const int a = norm_axis((int)n->p.i[0], x->ndim);
-    const int64_t start = n->p.i[1], len = n->p.i[2], step = n->p.i[3];
-    if (a < 0) {
-        error(x->ctx, NC_ERR_ARG, "slice: axis %d out of range for %d-d tensor", (int)n->p.i[0], x->ndim);
-        return NC_ERR_ARG;
-    }
-    if (step < 1 || len < 0 || start < 0 || start > x->shape[a] ||
-        (len > 0 && start + (len - 1) * step >= x->shape[a])) {
-        error(x->ctx, NC_ERR_ARG, "slice: start %lld, length %lld, step %lld do not fit axis %d of size %lld",
-              (long long)start, (long long)len, (long long)step, a, (long long)x->shape[a]);
-        return NC_ERR_ARG;
-    }
-    n->p.i[0] = a;
-    *dt = x->dtype;
-    *nd = x->ndim;
-    memcpy(shape, x->shape, sizeof(int64_t) * (size_t)x->ndim);
-    shape[a] = len;
-    return NC_OK;
-}
-
-static void sliced(const nc_node *n, int64_t *stride, int64_t *offset) {
-    const nc_tensor *x = n->in[0];
-    const int a = (int)n->p.i[0];
-    memcpy(stride, x->stride, sizeof(int64_t) * (size_t)x->ndim);
-    *offset = x->offset + (n->p.i[2] > 0 ? n->p.i[1] * x->stride[a] : 0);
-    stride[a] = x->stride[a] * n->p.i[3];
-}
-
-static int slice_view(nc_node *n, int nd, const int64_t *shape) {
-    int64_t st[NC_MAX_DIMS], off;
-    sliced(n, st, &off);
-    return alias_with(n, nd, shape, st, off) != nullptr;
-}
-
-static nc_status slice_fwd(nc_node *n) {
-    int64_t st[NC_MAX_DIMS], off;
-    sliced(n, st, &off);
-    return gather_into(n->in[0], n->out->shape, st, off, n->out);
+    Layout L = dense_of(n->in[0]);
+    const int a = (int)n->p.i[0], b = (int)n->p.i[1];
+    std::swap(L.st[a], L.st[b]);
+    layout_bwd(n, L);
 }
 
 static void slice_bwd(nc_node *n) {
-    nc_tensor *x = n->in[0], *o = n->out;
-    nc_ctx *ctx = x->ctx;
-    if (!grad_buf(x)) return;
+    Layout L = dense_of(n->in[0]);
     const int a = (int)n->p.i[0];
-    if (o->shape[a] == 0) return;
-    int64_t st[NC_MAX_DIMS];
-    contig_strides(x->ndim, x->shape, st);
-    float *g = fptr(o->grad), *gi = fptr(x->grad);
-    if (!g || !gi) return;
-    gi += n->p.i[1] * st[a];
-    st[a] *= n->p.i[3];
-    if (!hip_layer_ok(ctx, nc_hip_accumulate_strided(o->ndim, o->shape, g, gi, st, stream(ctx)), "slice")) return;
-    wrote_dev(x->grad);
+    if (n->p.i[2] > 0) L.offset = n->p.i[1] * L.st[a];
+    L.st[a] *= n->p.i[3];
+    layout_bwd(n, L);
 }
 
-const OpDef op_slice = {"slice", OPF_VIEW, 0, slice_infer, slice_view, slice_fwd, slice_bwd};
+const OpDef op_transpose = {"transpose", OPF_VIEW, 0, transpose_shape, transpose_alias, transpose_fwd, transpose_bwd};
+const OpDef op_slice = {"slice", OPF_VIEW, 0, slice_shape, slice_alias, slice_fwd, slice_bwd};
 
 // ---- contiguous / detach ---------------------------------------------------------------------------
-static int contiguous_view(nc_node *n, int nd, const int64_t *shape) {
-    if (!nc_is_contiguous(n->in[0])) return 0;
-    return alias_with(n, nd, shape, n->in[0]->stride, n->in[0]->offset) != nullptr;
+static nc_status keep_shape(nc_node *n, OutSpec &out) {
+    out.dtype = n->in[0]->dtype;
+    out.dims = Dims::of(n->in[0]);
+    return NC_OK;
 }
-const OpDef op_contiguous = {"contiguous", OPF_VIEW, 0, same_shape_infer, contiguous_view, copy_fwd, flat_bwd};
 
-static int detach_view(nc_node *n, int nd, const int64_t *shape) {
-    return alias_with(n, nd, shape, n->in[0]->stride, n->in[0]->offset) != nullptr;
+static bool contiguous_alias(nc_node *n, const OutSpec &) {
+    return nc_is_contiguous(n->in[0]) && view_of(n, Layout::of(n->in[0]));
 }
-const OpDef op_detach = {"detach", OPF_VIEW | OPF_NONDIFF, 0, same_shape_infer, detach_view, copy_fwd, nullptr};
+static bool detach_alias(nc_node *n, const OutSpec &) { return view_of(n, Layout::of(n->in[0])); }
 
-// ---- to_dtype --------------------------------------------------------------------------------------
-static nc_status to_dtype_infer(nc_node *n, nc_dtype *dt, int *nd, int64_t *shape) {
+const OpDef op_contiguous = {"contiguous", OPF_VIEW, 0, keep_shape, contiguous_alias, copy_fwd, flat_bwd};
+const OpDef op_detach = {"detach", OPF_VIEW | OPF_NONDIFF, 0, keep_shape, detach_alias, copy_fwd, nullptr};
+
+// ---- to_dtype: p.i[0] the target dtype ---------------------------------------------------------------
+static nc_status to_dtype_shape(nc_node *n, OutSpec &out) {
     const nc_dtype to = (nc_dtype)n->p.i[0], from = n->in[0]->dtype;
-    if (to == NC_F16 || from == NC_F16 || dtype_size(to) == 0) {
-        error(n->in[0]->ctx, NC_ERR_DTYPE, "to_dtype: %s -> %s is not supported", dtype_name(from), dtype_name(to));
-        return NC_ERR_DTYPE;
-    }
-    *dt = to;
-    nc_dtype ignored;
-    return same_shape_infer(n, &ignored, nd, shape);
+    if (to == NC_F16 || from == NC_F16 || dtype_size(to) == 0)
+        return reject(n, NC_ERR_DTYPE, "to_dtype: %s -> %s is not supported", dtype_name(from), dtype_name(to));
+    keep_shape(n, out);
+    out.dtype = to;
+    return NC_OK;
 }
 
 static nc_status to_dtype_fwd(nc_node *n) {
@@ -292,23 +268,24 @@ static nc_status to_dtype_fwd(nc_node *n) {
     nc_ctx *ctx = o->ctx;
     const size_t es = dtype_size(x->dtype);
     const int64_t N = nc_numel(x);
-    char *src = dptr(x);
-    if (!src) return NC_ERR_STATE;
-    if (!nc_is_contiguous(x)) {
-        char *buf = arena_alloc(ctx, (size_t)N * es + 1);
-        if (!buf || !hip_layer_ok(ctx, nc_hip_copy_strided((int)es, x->ndim, x->shape, src, x->stride, buf, stream(ctx)),
-                                  "to_dtype"))
+    const char *src = dptr(x);
+    if (src && !nc_is_contiguous(x)) {  // pack first: the converter reads a dense run
+        char *packed = arena_alloc(ctx, (size_t)N * es + 1);
+        if (!packed ||
+            !hip_layer_ok(ctx, nc_hip_copy_strided((int)es, x->ndim, x->shape, src, x->stride, packed, stream(ctx)),
+                          "to_dtype"))
             return NC_ERR_STATE;
-        src = buf;
+        src = packed;
     }
-    char *dst = dptr(o);
-    if (!dst || !hip_layer_ok(ctx, nc_hip_convert(x->dtype, o->dtype, N, src, dst, stream(ctx)), "to_dtype"))
+    char *dst = dptr_overwrite(o);
+    if (!src || !dst || !hip_layer_ok(ctx, nc_hip_convert(x->dtype, o->dtype, N, src, dst, stream(ctx)), "to_dtype"))
         return NC_ERR_STATE;
     wrote_dev(o);
     return NC_OK;
 }
 
-const OpDef op_to_dtype = {"to_dtype", 0, 0, to_dtype_infer, nullptr, to_dtype_fwd, flat_bwd};
+// only f32 -> f32 is on the tape (other targets detach first); its gradient passes straight through
+const OpDef op_to_dtype = {"to_dtype", 0, 0, to_dtype_shape, nullptr, to_dtype_fwd, flat_bwd};
 
 }  // namespace nce
 

@@ -64,10 +64,34 @@ const char *shape_str(int nd, const int64_t *shape, char *buf, size_t size) {
     return buf;
 }
 
-bool expect_f32(const nc_node *n, int i) {
-    if (n->in[i]->dtype == NC_F32) return true;
-    error(n->in[i]->ctx, NC_ERR_DTYPE, "%s: input %d must be f32, got %s", n->op->name, i, dtype_name(n->in[i]->dtype));
-    return false;
+Dims Dims::of(const nc_tensor *t) {
+    Dims d;
+    d.rank = t->ndim;
+    for (int i = 0; i < t->ndim; i++) d.e[i] = t->shape[i];
+    return d;
+}
+
+const char *Dims::text(char *buf, size_t size) const { return shape_str(rank, e, buf, size); }
+
+nc_status reject(const nc_node *n, nc_status code, const char *fmt, ...) {
+    nc_ctx *ctx = n->in[0]->ctx;
+    if (ctx->status == NC_OK) {
+        ctx->status = code;
+        va_list ap;
+        va_start(ap, fmt);
+        vsnprintf(ctx->err, sizeof ctx->err, fmt, ap);
+        va_end(ap);
+    }
+    return code;
+}
+
+bool inputs_f32(const nc_node *n, int first, int count) {
+    for (int i = first; i < first + count; i++)
+        if (n->in[i]->dtype != NC_F32) {
+            reject(n, NC_ERR_DTYPE, "%s: input %d must be f32, got %s", n->op->name, i, dtype_name(n->in[i]->dtype));
+            return false;
+        }
+    return true;
 }
 
 void bcast_strides_shape(int tn, const int64_t *tshape, int nd, const int64_t *shape, int64_t *out) {
@@ -123,7 +147,10 @@ nc_tensor *tensor_new(nc_ctx *ctx, nc_dtype dt, int nd, const int64_t *shape, bo
     contig_strides(nd, t->shape, t->stride);
     t->bytes = (size_t)shape_numel(nd, shape) * dtype_size(dt);
     if (ctx->device >= 0) {
+        const bool was = ctx->storage_alloc;
+        ctx->storage_alloc = true;  // tensor storage, never an op's scratch
         t->dev = dev_alloc(ctx, t->bytes, persistent);
+        ctx->storage_alloc = was;
         if (!t->dev) {
             if (persistent) free(t);
             return nullptr;
@@ -269,9 +296,7 @@ nc_tensor *grad_buf(nc_tensor *t) {
     }
     if (!t->grad) {
         const bool persistent = (t->flags & TF_PERSISTENT) != 0;
-        t->ctx->grad_alloc = true;  // not a backward temporary: it outlives the node
         t->grad = tensor_new(t->ctx, NC_F32, t->ndim, t->shape, persistent);
-        t->ctx->grad_alloc = false;
         if (!t->grad) return nullptr;
         // zeroed lazily: the first kernel writing it stores instead of accumulating (grad_acc)
         t->grad->flags |= TF_GRAD_FRESH;
