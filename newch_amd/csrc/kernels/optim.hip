@@ -167,8 +167,17 @@ __global__ __launch_bounds__(kSB) void k_sumsq(const float *__restrict__ x, int6
 
 __global__ __launch_bounds__(kSB) void k_sumsq_finish(const double *__restrict__ part, int nparts, double *ss,
                                                       int accumulate) {
+    // partials threadIdx.x, + kSB, ... added in that order, their loads issued kU at a time
+    constexpr int kU = 8;
     double t = 0.0;
-    for (int i = threadIdx.x; i < nparts; i += kSB) t += part[i];
+    for (int base = threadIdx.x; base < nparts; base += kSB * kU) {
+        double v[kU];
+#pragma unroll
+        for (int u = 0; u < kU; u++) v[u] = base + u * kSB < nparts ? part[base + u * kSB] : 0.0;
+#pragma unroll
+        for (int u = 0; u < kU; u++)
+            if (base + u * kSB < nparts) t += v[u];
+    }
     const double s = block_sum_waves(t);
     if (threadIdx.x == 0) *ss = (accumulate ? *ss : 0.0) + s;
 }
