@@ -68,7 +68,7 @@ def build(verbose: bool = True) -> Path:
         objs = list(ex.map(_compile, srcs))
     tmp = LIB.with_suffix(".so.tmp")
     cmd = [hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp), *map(str, objs),
-           "-Wl,-soname,libnc.so", f"-L{ROCM / 'lib'}", "-lhipblaslt", "-lrocblas"]
+           "-Wl,-soname,libnc.so"]
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
         raise RuntimeError(f"link failed\n{' '.join(cmd)}\n{res.stdout}{res.stderr}")

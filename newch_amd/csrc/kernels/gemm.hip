@@ -1,216 +1,304 @@
-// fp32 GEMM entry points (the reference's gemm_f32 kernel-table entry, kernels.h:36-41): dense GEMMs
-// on the matrix cores through hipBLASLt (rocBLAS for the cases it does not take), row-major interface.
+// fp32 GEMM on the matrix cores (the reference's gemm_f32 kernel-table entry, kernels.h:36-41, as
+// ops_linalg.c:58-330 calls it): hand-written for gfx950 around v_mfma_f32_16x16x4_f32.
 //
-// Row-major C (M x N) = op(A) op(B) is column-major C^T = op(B)^T op(A)^T, so the operands are passed
-// to the library swapped, each with its own transpose flag.  hipBLASLt runs with no workspace (no
-// split-k partial buffers; the same inputs give the same bits run after run) and its first heuristic
-// choice, planned once per shape and cached; measured on MI355X it reaches 148-154 TFLOP/s on
-// [8192,4096] x [4096,4096] and ~100 on 64 x [1024,128] x [128,1024], where rocBLAS ran 134-139 and
-// 46.  rocBLAS (one handle per device, atomics off, host pointer mode) covers K = 0, unaligned
-// operands, broadcast batch strides and pointer-array batches.
+// C (M x N, row-major, leading dim ldc) = alpha op(A) op(B) + beta C with op(A) M x K and op(B) K x N.
+// An operand is stored K-contiguous (A untransposed, B transposed) or M/N-contiguous (A transposed, B
+// untransposed), each with its own leading dim; batched forms take per-axis batch strides or pointer
+// arrays.  beta = 0 never reads C.
+//
+// Tiling.  A workgroup owns a BM x BN tile of C and each of its waves a (16 TM) x (16 TN) block of it,
+// held as TM x TN 16 x 16 accumulator tiles (4 floats per lane each).  K advances 16 at a time
+// through two LDS stages: the next step's panels are loaded into registers while the matrix cores
+// work on the current one, stored into the other stage, and one barrier per step separates the two.
+// Each operand keeps its global layout in LDS:
+//   * K-contiguous panel: BM (BN) rows of 16 floats, four 16-byte chunks per row, logical chunk c of
+//     row r stored at chunk c ^ ((r >> 2) & 3), so 16-byte reads of consecutive rows spread over the
+//     banks;
+//   * M/N-contiguous panel: 16 k-rows of BM (BN) floats, the row pitch padded by 4 floats so the four
+//     quarter-waves' reads (k-rows k, k + 4, k + 8, k + 12) land in different banks.
+//
+// k mapping.  One MFMA multiplies a 16 x 4 slice of A by a 4 x 16 slice of B, quarter-wave q (lanes
+// 16 q .. 16 q + 15) holding one k.  In each stage of 16 k, quarter q gives the s-th MFMA (s = 0..3)
+// the value at k = 4 q + s, for A and B alike, so a K-contiguous operand feeds four MFMAs from one
+// 16-byte LDS read.  Each k enters every output element exactly once, four products per instruction
+// (K / 4 roundings into the accumulator), and the order of the sum is a property of the kernel
+// alone: the same for every tile size and grid, so results are identical run to run and on any
+// device.  It differs from the reference's serial order, so the parity bar is the fp32 error bound of
+// a K-term dot product.
+//
+// Tile sizes: 256 x 256 (8 waves of 8 x 4 tiles) when the problem has at least as many such tiles as
+// the device has CUs, else 128 x 128 (4 waves of 4 x 4) or 64 x 64 (4 waves of 2 x 2).  Blocks are
+// remapped so each XCD (blocks b with b % 8 equal) works a contiguous run of tiles, and tiles run in
+// groups of 8 tile-rows so neighbouring blocks share panels in L2.
 #include "common.hpp"
 
-#include <hipblaslt/hipblaslt.h>
-#include <rocblas/rocblas.h>
-
-#include <mutex>
-#include <unordered_map>
-
 namespace nchip {
 
-static rocblas_handle blas_handle() {
-    static rocblas_handle handles[64] = {};
-    static std::mutex mu;
-    int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return nullptr;
-    std::lock_guard<std::mutex> lock(mu);
-    if (!handles[dev]) {
-        rocblas_handle h = nullptr;
-        if (rocblas_create_handle(&h) != rocblas_status_success) return nullptr;
-        rocblas_set_atomics_mode(h, rocblas_atomics_not_allowed);
-        rocblas_set_pointer_mode(h, rocblas_pointer_mode_host);
-        handles[dev] = h;
+
+constexpr int kSgBK = 16;      // k per stage
+constexpr int kSgGroupM = 8;   // tile-rows per group in the block order
+
+template <int TM_, int TN_, int WGM_, int WGN_>
+struct SgCfg {
+    static constexpr int TM = TM_, TN = TN_, WGM = WGM_, WGN = WGN_;
+    static constexpr int NT = 64 * WGM * WGN;
+    static constexpr int BM = 16 * TM * WGM, BN = 16 * TN * WGN;
+    // bytes of one operand panel in LDS (the larger of the two layouts)
+    static constexpr int SLAB_A = 64 * BM + 256, SLAB_B = 64 * BN + 256;
+    static constexpr int STAGE = SLAB_A + SLAB_B;
+    static constexpr size_t LDS = 2 * (size_t)STAGE;
+    static constexpr int CA = 4 * BM / NT, CB = 4 * BN / NT;  // 16-byte chunks per thread per panel
+    static_assert(4 * BM % NT == 0 && 4 * BN % NT == 0, "panel chunks must divide over the workgroup");
+};
+using SgBig = SgCfg<8, 4, 2, 4>;    // 256 x 256
+using SgMid = SgCfg<4, 4, 2, 2>;    // 128 x 128
+using SgSmall = SgCfg<2, 2, 2, 2>;  // 64 x 64
+
+struct SgBatch {
+    int nb;  // 0: one matrix per operand
+    int64_t shape[NC_HIP_MAX_DIMS];
+    int64_t st[3][NC_HIP_MAX_DIMS];  // element strides of A, B, C per batch axis
+};
+
+struct SgArgs {
+    const float *A, *B;
+    float *C;
+    const float *const *pa;  // pointer-array batches (instead of strides) when set
+    const float *const *pb;
+    float *const *pc;
+    int64_t lda, ldb, ldc;
+    int M, N, K;
+    float alpha, beta;
+    int tiles_m, tiles_n;
+    SgBatch bat;
+};
+
+// Chunk q of an R-row panel starting at (row r0, k k0): its 16-byte LDS position.
+template <int R, bool KC>
+__device__ __forceinline__ uint32_t chunk_lds(int q) {
+    if constexpr (KC) {
+        const int row = q >> 2, c = q & 3;
+        return (uint32_t)(row * 64 + ((c ^ ((row >> 2) & 3)) << 4));
+    } else {
+        constexpr int per_row = R / 4;
+        return (uint32_t)((q / per_row) * (R + 4) * 4 + (q % per_row) * 16);
     }
-    return handles[dev];
 }
 
-static int blas_error(rocblas_status s, const char *what) {
-    return set_error(NC_HIP_ERR_DEVICE, "%s: rocBLAS %s", what, rocblas_status_to_string(s));
+// Chunk q's four floats from global memory, zero past the matrix.  VEC: the operand's rows start
+// 16-byte aligned (aligned base, leading dim a multiple of 4), so a chunk wholly inside is one load.
+template <int R, bool KC, bool VEC>
+__device__ __forceinline__ f4 chunk_load(const float *p, int64_t ld, int rows, int K, int r0, int k0, int q) {
+    f4 v = {0.f, 0.f, 0.f, 0.f};
+    if constexpr (KC) {
+        const int row = r0 + (q >> 2), k = k0 + (q & 3) * 4;
+        if (row >= rows || k >= K) return v;
+        const float *s = p + (int64_t)row * ld + k;
+        if (VEC && k + 4 <= K) return *(const f4 *)s;
+#pragma unroll
+        for (int j = 0; j < 4; j++)
+            if (k + j < K) v[j] = s[j];
+    } else {
+        constexpr int per_row = R / 4;
+        const int k = k0 + q / per_row, row = r0 + (q % per_row) * 4;
+        if (k >= K || row >= rows) return v;
+        const float *s = p + (int64_t)k * ld + row;
+        if (VEC && row + 4 <= rows) return *(const f4 *)s;
+#pragma unroll
+        for (int j = 0; j < 4; j++)
+            if (row + j < rows) v[j] = s[j];
+    }
+    return v;
 }
 
-static rocblas_operation op_of(int t) { return t ? rocblas_operation_transpose : rocblas_operation_none; }
-
-// ---- hipBLASLt plans ----------------------------------------------------------------------------
-struct LtKey {
-    int dev, ta, tb;
-    int64_t M, N, K, lda, ldb, ldc, count, sa, sb, sc;
-    bool operator==(const LtKey &o) const {
-        return dev == o.dev && ta == o.ta && tb == o.tb && M == o.M && N == o.N && K == o.K && lda == o.lda &&
-               ldb == o.ldb && ldc == o.ldc && count == o.count && sa == o.sa && sb == o.sb && sc == o.sc;
+// The four values (s = 0..3) of panel row r that quarter-wave q gives the stage's MFMAs.
+template <int R, bool KC>
+__device__ __forceinline__ f4 fragment(const char *slab, int r, int q) {
+    if constexpr (KC) {
+        return *(const f4 *)(slab + r * 64 + ((q ^ ((r >> 2) & 3)) << 4));
+    } else {
+        const float *b = (const float *)slab + 4 * q * (R + 4) + r;
+        return f4{b[0], b[R + 4], b[2 * (R + 4)], b[3 * (R + 4)]};
     }
-};
-struct LtKeyHash {
-    size_t operator()(const LtKey &k) const {
-        const int64_t v[] = {k.dev, k.ta, k.tb, k.M, k.N, k.K, k.lda, k.ldb, k.ldc, k.count, k.sa, k.sb, k.sc};
-        size_t h = 1469598103934665603ull;
-        for (int64_t x : v) h = (h ^ (size_t)x) * 1099511628211ull;
-        return h;
-    }
-};
-struct LtPlan {
-    bool ok = false;
-    hipblasLtMatmulDesc_t desc{};
-    hipblasLtMatrixLayout_t la{}, lb{}, lc{};
-    hipblasLtMatmulAlgo_t algo{};
-};
+}
 
-static std::mutex lt_mu;
-static hipblasLtHandle_t lt_handles[64];
-static std::unordered_map<LtKey, LtPlan, LtKeyHash> lt_plans;
-
-// The plan for a key (created on first use; ok == false when hipBLASLt offers no algorithm).
-static const LtPlan *lt_plan(const LtKey &k) {
-    std::lock_guard<std::mutex> lock(lt_mu);
-    auto it = lt_plans.find(k);
-    if (it != lt_plans.end()) return &it->second;
-    LtPlan &p = lt_plans[k];
-    if (!lt_handles[k.dev] && hipblasLtCreate(&lt_handles[k.dev]) != HIPBLAS_STATUS_SUCCESS) {
-        lt_handles[k.dev] = nullptr;
-        return &p;
+// element offset of batch matrix `idx` for operand o (0 A, 1 B, 2 C)
+__device__ __forceinline__ int64_t batch_off(const SgBatch &bt, int o, int64_t idx) {
+    int64_t off = 0;
+    for (int d = bt.nb - 1; d >= 0; d--) {
+        const int64_t e = bt.shape[d];
+        off += (idx % e) * bt.st[o][d];
+        idx /= e;
     }
-    hipblasLtHandle_t h = lt_handles[k.dev];
-    // column-major D (N x M) = op(B) (N x K) op(A) (K x M)
-    const hipblasOperation_t oa = k.tb ? HIPBLAS_OP_T : HIPBLAS_OP_N, ob = k.ta ? HIPBLAS_OP_T : HIPBLAS_OP_N;
-    bool ok = hipblasLtMatmulDescCreate(&p.desc, HIPBLAS_COMPUTE_32F, HIP_R_32F) == HIPBLAS_STATUS_SUCCESS;
-    ok = ok && hipblasLtMatmulDescSetAttribute(p.desc, HIPBLASLT_MATMUL_DESC_TRANSA, &oa, sizeof oa) == HIPBLAS_STATUS_SUCCESS;
-    ok = ok && hipblasLtMatmulDescSetAttribute(p.desc, HIPBLASLT_MATMUL_DESC_TRANSB, &ob, sizeof ob) == HIPBLAS_STATUS_SUCCESS;
-    ok = ok && hipblasLtMatrixLayoutCreate(&p.la, HIP_R_32F, k.tb ? k.K : k.N, k.tb ? k.N : k.K, k.ldb) == HIPBLAS_STATUS_SUCCESS;
-    ok = ok && hipblasLtMatrixLayoutCreate(&p.lb, HIP_R_32F, k.ta ? k.M : k.K, k.ta ? k.K : k.M, k.lda) == HIPBLAS_STATUS_SUCCESS;
-    ok = ok && hipblasLtMatrixLayoutCreate(&p.lc, HIP_R_32F, k.N, k.M, k.ldc) == HIPBLAS_STATUS_SUCCESS;
-    if (ok && k.count > 1) {
-        const int32_t cnt = (int32_t)k.count;
-        const int64_t st[3] = {k.sb, k.sa, k.sc};
-        hipblasLtMatrixLayout_t ls[3] = {p.la, p.lb, p.lc};
-        for (int i = 0; i < 3 && ok; i++) {
-            ok = hipblasLtMatrixLayoutSetAttribute(ls[i], HIPBLASLT_MATRIX_LAYOUT_BATCH_COUNT, &cnt, sizeof cnt) ==
-                     HIPBLAS_STATUS_SUCCESS &&
-                 hipblasLtMatrixLayoutSetAttribute(ls[i], HIPBLASLT_MATRIX_LAYOUT_STRIDED_BATCH_OFFSET, &st[i],
-                                                   sizeof st[i]) == HIPBLAS_STATUS_SUCCESS;
+    return off;
+}
+
+template <class Cfg, bool AK, bool BK, bool VEC>
+__global__ __launch_bounds__(Cfg::NT, 1) void k_sgemm(SgArgs p) {
+    extern __shared__ __attribute__((aligned(16))) char smem[];
+    constexpr int kTM = Cfg::TM, kTN = Cfg::TN, kWGN = Cfg::WGN, kNT = Cfg::NT;
+    constexpr int kBM = Cfg::BM, kBN = Cfg::BN, kCA = Cfg::CA, kCB = Cfg::CB;
+
+    // block -> (batch matrix, tile): XCD-contiguous runs, then groups of kSgGroupM tile-rows
+    int64_t id = blockIdx.x;
+    const int64_t nblk = gridDim.x;
+    if ((nblk & 7) == 0) id = (id & 7) * (nblk >> 3) + (id >> 3);
+    const int64_t per_batch = (int64_t)p.tiles_m * p.tiles_n;
+    const int64_t batch = id / per_batch;
+    const int tile = (int)(id % per_batch);
+    const int per_group = kSgGroupM * p.tiles_n;
+    const int first_m = (tile / per_group) * kSgGroupM;
+    const int gsize = min(p.tiles_m - first_m, kSgGroupM);
+    const int tm = first_m + (tile % per_group) % gsize, tn = (tile % per_group) / gsize;
+    const int m0 = tm * kBM, n0 = tn * kBN;
+
+    const float *A, *B;
+    float *C;
+    if (p.pa) {
+        A = p.pa[batch], B = p.pb[batch], C = p.pc[batch];
+    } else {
+        A = p.A + batch_off(p.bat, 0, batch), B = p.B + batch_off(p.bat, 1, batch), C = p.C + batch_off(p.bat, 2, batch);
+    }
+
+    const int t = threadIdx.x, lane = t & (kWave - 1), wid = t / kWave;
+    const int wm = wid / kWGN, wn = wid % kWGN;
+
+    f4 ra[kCA], rb[kCB];
+    auto gload = [&](int k0) {
+#pragma unroll
+        for (int i = 0; i < kCA; i++) ra[i] = chunk_load<kBM, AK, VEC>(A, p.lda, p.M, p.K, m0, k0, t + i * kNT);
+#pragma unroll
+        for (int i = 0; i < kCB; i++) rb[i] = chunk_load<kBN, BK, VEC>(B, p.ldb, p.N, p.K, n0, k0, t + i * kNT);
+    };
+    auto sstore = [&](char *stage) {
+#pragma unroll
+        for (int i = 0; i < kCA; i++) *(f4 *)(stage + chunk_lds<kBM, AK>(t + i * kNT)) = ra[i];
+#pragma unroll
+        for (int i = 0; i < kCB; i++) *(f4 *)(stage + Cfg::SLAB_A + chunk_lds<kBN, BK>(t + i * kNT)) = rb[i];
+    };
+
+    f4 acc[kTM][kTN];
+#pragma unroll
+    for (int i = 0; i < kTM; i++)
+#pragma unroll
+        for (int j = 0; j < kTN; j++) acc[i][j] = f4{0.f, 0.f, 0.f, 0.f};
+
+    const int fr = lane & 15, fq = lane >> 4;
+    const int nk = (p.K + kSgBK - 1) / kSgBK;
+    if (nk > 0) {
+        gload(0);
+        sstore(smem);
+        __syncthreads();
+    }
+    for (int kt = 0; kt < nk; kt++) {
+        const char *cur = smem + (kt & 1) * Cfg::STAGE;
+        if (kt + 1 < nk) gload((kt + 1) * kSgBK);
+        {
+            f4 fa[kTM], fb[kTN];
+#pragma unroll
+            for (int i = 0; i < kTM; i++) fa[i] = fragment<kBM, AK>(cur, (wm * kTM + i) * 16 + fr, fq);
+#pragma unroll
+            for (int j = 0; j < kTN; j++) fb[j] = fragment<kBN, BK>(cur + Cfg::SLAB_A, (wn * kTN + j) * 16 + fr, fq);
+#pragma unroll
+            for (int s = 0; s < 4; s++)
+#pragma unroll
+                for (int i = 0; i < kTM; i++)
+#pragma unroll
+                    for (int j = 0; j < kTN; j++)
+                        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(fa[i][s], fb[j][s], acc[i][j], 0, 0, 0);
+        }
+        // the other stage was last read before the previous barrier, so it can be refilled now
+        if (kt + 1 < nk) sstore(smem + ((kt + 1) & 1) * Cfg::STAGE);
+        __syncthreads();
+    }
+
+    // accumulator layout of a 16 x 16 tile: lane l, element v holds row 4 (l / 16) + v, column l % 16
+#pragma unroll
+    for (int i = 0; i < kTM; i++) {
+#pragma unroll
+        for (int j = 0; j < kTN; j++) {
+            const int n = n0 + (wn * kTN + j) * 16 + fr;
+            if (n >= p.N) continue;
+#pragma unroll
+            for (int v = 0; v < 4; v++) {
+                const int m = m0 + (wm * kTM + i) * 16 + 4 * fq + v;
+                if (m >= p.M) continue;
+                float *c = C + (int64_t)m * p.ldc + n;
+                const float r = p.alpha * acc[i][j][v];
+                *c = p.beta != 0.0f ? r + p.beta * *c : r;
+            }
         }
     }
-    hipblasLtMatmulPreference_t pref{};
-    ok = ok && hipblasLtMatmulPreferenceCreate(&pref) == HIPBLAS_STATUS_SUCCESS;
-    const uint64_t no_ws = 0;
-    ok = ok && hipblasLtMatmulPreferenceSetAttribute(pref, HIPBLASLT_MATMUL_PREF_MAX_WORKSPACE_BYTES, &no_ws,
-                                                     sizeof no_ws) == HIPBLAS_STATUS_SUCCESS;
-    hipblasLtMatmulHeuristicResult_t res{};
-    int nres = 0;
-    ok = ok && hipblasLtMatmulAlgoGetHeuristic(h, p.desc, p.la, p.lb, p.lc, p.lc, pref, 1, &res, &nres) ==
-                   HIPBLAS_STATUS_SUCCESS &&
-         nres > 0 && res.workspaceSize == 0;
-    if (pref) hipblasLtMatmulPreferenceDestroy(pref);
-    if (ok) p.algo = res.algo;
-    p.ok = ok;
-    return &p;
 }
 
-// C = alpha op(A) op(B) + beta C through hipBLASLt (count > 1: strided batch).  Returns false when
-// the case is left to rocBLAS: K = 0, a zero or negative batch stride, operands not 16-byte aligned or
-// leading dims not multiples of 4, or no algorithm.
-static bool lt_gemm(int ta, int tb, int64_t M, int64_t N, int64_t K, float alpha, const float *A, int64_t lda,
-                    const float *B, int64_t ldb, float beta, float *C, int64_t ldc, int64_t count, int64_t sa,
-                    int64_t sb, int64_t sc, hipStream_t st, int *rc) {
-    if (K == 0 || count > INT32_MAX || !aligned16(A) || !aligned16(B) || !aligned16(C) || lda % 4 || ldb % 4 || ldc % 4)
-        return false;
-    if (count > 1 && (sa <= 0 || sb <= 0 || sc <= 0 || sa % 4 || sb % 4 || sc % 4)) return false;
+template <class Cfg, bool AK, bool BK, bool VEC>
+static void sg_attr() {
+    // dynamic LDS above 64 KiB has to be allowed per kernel, once per device
+    static bool done[64] = {};
     int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return false;
-    const LtKey key{dev, ta ? 1 : 0, tb ? 1 : 0, M, N, K, lda, ldb, ldc, count, count > 1 ? sa : 0,
-                    count > 1 ? sb : 0, count > 1 ? sc : 0};
-    const LtPlan *p = lt_plan(key);
-    if (!p->ok) return false;
-    const hipblasStatus_t s = hipblasLtMatmul(lt_handles[dev], p->desc, &alpha, B, p->la, A, p->lb, &beta, C, p->lc,
-                                              C, p->lc, &p->algo, nullptr, 0, st);
-    *rc = s == HIPBLAS_STATUS_SUCCESS ? NC_HIP_OK
-                                      : set_error(NC_HIP_ERR_DEVICE, "hipBLASLt matmul failed (status %d)", (int)s);
-    return true;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64 || done[dev]) return;
+    (void)hipFuncSetAttribute((const void *)k_sgemm<Cfg, AK, BK, VEC>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                              (int)Cfg::LDS);
+    done[dev] = true;
 }
 
-// With K = 0 no element of A or B is read, but rocBLAS still checks their leading dims against the
-// stored shapes (row-major A: M x K, or K x M when transposed); a [M, 0] tensor has leading dim 0.
-static void k0_leading_dims(int ta, int tb, int64_t M, int64_t N, int64_t K, int64_t *lda, int64_t *ldb) {
-    if (K != 0) return;
-    const int64_t need_a = ta ? M : K, need_b = tb ? K : N;
-    if (*lda < need_a || *lda < 1) *lda = need_a > 1 ? need_a : 1;
-    if (*ldb < need_b || *ldb < 1) *ldb = need_b > 1 ? need_b : 1;
+template <class Cfg, bool AK, bool BK, bool VEC>
+static int sg_launch(SgArgs &p, int64_t count, hipStream_t st, const char *what) {
+    p.tiles_m = (p.M + Cfg::BM - 1) / Cfg::BM;
+    p.tiles_n = (p.N + Cfg::BN - 1) / Cfg::BN;
+    const int64_t blocks = (int64_t)p.tiles_m * p.tiles_n * count;
+    if (blocks > INT32_MAX) return set_error(NC_HIP_ERR_ARG, "%s: %lld tiles exceed one launch", what, (long long)blocks);
+    sg_attr<Cfg, AK, BK, VEC>();
+    hipLaunchKernelGGL((k_sgemm<Cfg, AK, BK, VEC>), dim3((unsigned)blocks), dim3(Cfg::NT), Cfg::LDS, st, p);
+    return check_launch(what);
 }
 
-}  // namespace nchip
-
-using namespace nchip;
-
-extern "C" NC_HIP_API int nc_hip_gemm_f32(int ta, int tb, int64_t M, int64_t N, int64_t K, float alpha, const float *A,
-                                          int64_t lda, const float *B, int64_t ldb, float beta, float *C, int64_t ldc,
-                                          void *stream) {
-    if (M < 0 || N < 0 || K < 0) return set_error(NC_HIP_ERR_ARG, "nc_hip_gemm_f32: negative size");
-    if (M == 0 || N == 0) return NC_HIP_OK;
-    int rc = NC_HIP_OK;
-    if (lt_gemm(ta, tb, M, N, K, alpha, A, lda, B, ldb, beta, C, ldc, 1, 0, 0, 0, as_stream(stream), &rc)) return rc;
-    rocblas_handle h = blas_handle();
-    if (!h) return set_error(NC_HIP_ERR_DEVICE, "nc_hip_gemm_f32: no rocBLAS handle");
-    k0_leading_dims(ta, tb, M, N, K, &lda, &ldb);
-    rocblas_status s = rocblas_set_stream(h, as_stream(stream));
-    if (s == rocblas_status_success)
-        s = rocblas_sgemm_64(h, op_of(tb), op_of(ta), N, M, K, &alpha, B, ldb, A, lda, &beta, C, ldc);
-    return s == rocblas_status_success ? NC_HIP_OK : blas_error(s, "nc_hip_gemm_f32");
+template <class Cfg>
+static int sg_layouts(SgArgs &p, int ta, int tb, bool vec, int64_t count, hipStream_t st, const char *what) {
+    const bool ak = !ta, bk = tb != 0;
+#define NC_SG_CASE(AK_, BK_)                                                                \
+    if (ak == AK_ && bk == BK_)                                                             \
+        return vec ? sg_launch<Cfg, AK_, BK_, true>(p, count, st, what)                     \
+                   : sg_launch<Cfg, AK_, BK_, false>(p, count, st, what);
+    NC_SG_CASE(true, true)
+    NC_SG_CASE(true, false)
+    NC_SG_CASE(false, true)
+    NC_SG_CASE(false, false)
+#undef NC_SG_CASE
+    return NC_HIP_OK;
 }
 
-extern "C" NC_HIP_API int nc_hip_gemm_f32_batched(int ta, int tb, int64_t M, int64_t N, int64_t K, float alpha,
-                                                  const float *const *A, int64_t lda, const float *const *B,
-                                                  int64_t ldb, float beta, float *const *C, int64_t ldc, int64_t count,
-                                                  void *stream) {
-    if (M < 0 || N < 0 || K < 0 || count < 0) return set_error(NC_HIP_ERR_ARG, "nc_hip_gemm_f32_batched: negative size");
-    if (M == 0 || N == 0 || count == 0) return NC_HIP_OK;
-    rocblas_handle h = blas_handle();
-    if (!h) return set_error(NC_HIP_ERR_DEVICE, "nc_hip_gemm_f32_batched: no rocBLAS handle");
-    k0_leading_dims(ta, tb, M, N, K, &lda, &ldb);
-    rocblas_status s = rocblas_set_stream(h, as_stream(stream));
-    if (s == rocblas_status_success)
-        s = rocblas_sgemm_batched_64(h, op_of(tb), op_of(ta), N, M, K, &alpha, B, ldb, A, lda, &beta, C, ldc, count);
-    return s == rocblas_status_success ? NC_HIP_OK : blas_error(s, "nc_hip_gemm_f32_batched");
+static int64_t tiles_of(int64_t M, int64_t N, int bm, int bn) { return ((M + bm - 1) / bm) * ((N + bn - 1) / bn); }
+
+// the largest tile that still gives every CU a tile, else the smallest
+static int sg_run(SgArgs &p, int ta, int tb, int64_t count, hipStream_t st, const char *what) {
+    // 16-byte loads need every matrix's rows 16-byte aligned: the matrices behind a pointer array may
+    // start anywhere, so those take the scalar loads
+    bool vec = !p.pa && aligned16(p.A) && aligned16(p.B) && p.lda % 4 == 0 && p.ldb % 4 == 0;
+    for (int d = 0; d < p.bat.nb; d++) vec = vec && p.bat.st[0][d] % 4 == 0 && p.bat.st[1][d] % 4 == 0;
+    const int64_t cus = num_cus();
+    if (tiles_of(p.M, p.N, SgBig::BM, SgBig::BN) * count >= cus) return sg_layouts<SgBig>(p, ta, tb, vec, count, st, what);
+    if (tiles_of(p.M, p.N, SgMid::BM, SgMid::BN) * count >= cus) return sg_layouts<SgMid>(p, ta, tb, vec, count, st, what);
+    return sg_layouts<SgSmall>(p, ta, tb, vec, count, st, what);
+}
+
+static bool fits_int(int64_t v) { return v >= 0 && v <= INT32_MAX; }
+
+static SgArgs sg_args(int64_t M, int64_t N, int64_t K, float alpha, const float *A, int64_t lda, const float *B,
+                      int64_t ldb, float beta, float *C, int64_t ldc) {
+    SgArgs p{};
+    p.A = A, p.B = B, p.C = C;
+    p.lda = lda, p.ldb = ldb, p.ldc = ldc;
+    p.M = (int)M, p.N = (int)N, p.K = (int)K;
+    p.alpha = alpha, p.beta = beta;
+    return p;
 }
 
 // ------------------------------------------------------------------------------------------------
-// Batched matmul with broadcast batch dims (ops_linalg.c:89-252): one GEMM per batch matrix, batch
-// offsets given per operand as strides over the output's batch shape (0 = broadcast).
+// batch axes (ops_linalg.c:89-252): per-operand strides over the output's batch shape (0 = broadcast)
 // ------------------------------------------------------------------------------------------------
-namespace nchip {
-
-struct BatchDims {
-    int nb;
-    int64_t shape[NC_HIP_MAX_DIMS];
-    int64_t st[3][NC_HIP_MAX_DIMS];  // A, B, C
-};
-
-__global__ void k_batch_ptrs(const float *A, const float *B, float *C, BatchDims bd, int64_t count,
-                             const float **pa, const float **pb, float **pc) {
-    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (i >= count) return;
-    int64_t idx = i, oa = 0, ob = 0, oc = 0;
-    for (int d = bd.nb - 1; d >= 0; d--) {
-        const int64_t c = idx % bd.shape[d];
-        idx /= bd.shape[d];
-        oa += c * bd.st[0][d];
-        ob += c * bd.st[1][d];
-        oc += c * bd.st[2][d];
-    }
-    pa[i] = A + oa;
-    pb[i] = B + ob;
-    pc[i] = C + oc;
-}
-
-// drops size-1 batch dims and merges neighbours that step uniformly for all three operands
-static void coalesce_batch(BatchDims &bd) {
+// drops size-1 batch axes and merges neighbours that step uniformly for all three operands
+static void coalesce_batch(SgBatch &bd) {
     int w = 0;
     for (int d = 0; d < bd.nb; d++) {
         if (bd.shape[d] == 1) continue;
@@ -230,9 +318,9 @@ static void coalesce_batch(BatchDims &bd) {
     bd.nb = w;
 }
 
-// true when batch index idx is the first (in index order) to write its C block: zero on every dim
+// true when batch index idx is the first (in index order) to write its C block: zero on every axis
 // along which C is shared
-static bool first_writer(const BatchDims &bd, int64_t idx) {
+static bool first_writer(const SgBatch &bd, int64_t idx) {
     for (int d = bd.nb - 1; d >= 0; d--) {
         if (bd.st[2][d] == 0 && idx % bd.shape[d] != 0) return false;
         idx /= bd.shape[d];
@@ -240,7 +328,7 @@ static bool first_writer(const BatchDims &bd, int64_t idx) {
     return true;
 }
 
-static int64_t batch_offset(const BatchDims &bd, int o, int64_t idx) {
+static int64_t host_batch_off(const SgBatch &bd, int o, int64_t idx) {
     int64_t off = 0;
     for (int d = bd.nb - 1; d >= 0; d--) {
         off += (idx % bd.shape[d]) * bd.st[o][d];
@@ -251,8 +339,38 @@ static int64_t batch_offset(const BatchDims &bd, int o, int64_t idx) {
 
 }  // namespace nchip
 
+using namespace nchip;
+
+extern "C" NC_HIP_API int nc_hip_gemm_f32(int ta, int tb, int64_t M, int64_t N, int64_t K, float alpha, const float *A,
+                                          int64_t lda, const float *B, int64_t ldb, float beta, float *C, int64_t ldc,
+                                          void *stream) {
+    if (!fits_int(M) || !fits_int(N) || !fits_int(K)) return set_error(NC_HIP_ERR_ARG, "nc_hip_gemm_f32: bad size");
+    if (M == 0 || N == 0) return NC_HIP_OK;
+    if (ldc < N) return set_error(NC_HIP_ERR_ARG, "nc_hip_gemm_f32: ldc %lld < N %lld", (long long)ldc, (long long)N);
+    if (K > 0 && (lda < (ta ? M : K) || ldb < (tb ? K : N)))
+        return set_error(NC_HIP_ERR_ARG, "nc_hip_gemm_f32: leading dim too small");
+    SgArgs p = sg_args(M, N, K, alpha, A, lda, B, ldb, beta, C, ldc);
+    return sg_run(p, ta, tb, 1, as_stream(stream), "nc_hip_gemm_f32");
+}
+
+extern "C" NC_HIP_API int nc_hip_gemm_f32_batched(int ta, int tb, int64_t M, int64_t N, int64_t K, float alpha,
+                                                  const float *const *A, int64_t lda, const float *const *B,
+                                                  int64_t ldb, float beta, float *const *C, int64_t ldc, int64_t count,
+                                                  void *stream) {
+    if (!fits_int(M) || !fits_int(N) || !fits_int(K) || count < 0)
+        return set_error(NC_HIP_ERR_ARG, "nc_hip_gemm_f32_batched: bad size");
+    if (M == 0 || N == 0 || count == 0) return NC_HIP_OK;
+    if (!A || !B || !C) return set_error(NC_HIP_ERR_ARG, "nc_hip_gemm_f32_batched: NULL pointer array");
+    if (ldc < N || (K > 0 && (lda < (ta ? M : K) || ldb < (tb ? K : N))))
+        return set_error(NC_HIP_ERR_ARG, "nc_hip_gemm_f32_batched: leading dim too small");
+    SgArgs p = sg_args(M, N, K, alpha, nullptr, lda, nullptr, ldb, beta, nullptr, ldc);
+    p.pa = A, p.pb = B, p.pc = C;
+    return sg_run(p, ta, tb, count, as_stream(stream), "nc_hip_gemm_f32_batched");
+}
+
 extern "C" NC_HIP_API size_t nc_hip_gemm_f32_bmm_workspace(int64_t count) {
-    return count > 1 ? (size_t)count * 3 * sizeof(void *) : 0;
+    (void)count;
+    return 0;
 }
 
 extern "C" NC_HIP_API int nc_hip_gemm_f32_bmm(int ta, int tb, int64_t M, int64_t N, int64_t K, const float *A,
@@ -260,9 +378,10 @@ extern "C" NC_HIP_API int nc_hip_gemm_f32_bmm(int ta, int tb, int64_t M, int64_t
                                               int64_t ldc, int nb, const int64_t *bshape, const int64_t *sa,
                                               const int64_t *sb, const int64_t *sc, void *ws, size_t ws_bytes,
                                               void *stream) {
-    if (M < 0 || N < 0 || K < 0 || nb < 0 || nb > NC_HIP_MAX_DIMS)
+    (void)ws, (void)ws_bytes;
+    if (!fits_int(M) || !fits_int(N) || !fits_int(K) || nb < 0 || nb > NC_HIP_MAX_DIMS)
         return set_error(NC_HIP_ERR_ARG, "nc_hip_gemm_f32_bmm: bad sizes");
-    BatchDims bd;
+    SgBatch bd{};
     bd.nb = nb;
     int64_t count = 1;
     for (int d = 0; d < nb; d++) {
@@ -274,46 +393,22 @@ extern "C" NC_HIP_API int nc_hip_gemm_f32_bmm(int ta, int tb, int64_t M, int64_t
         count *= bshape[d];
     }
     if (M == 0 || N == 0 || count == 0) return NC_HIP_OK;
+    if (ldc < N || (K > 0 && (lda < (ta ? M : K) || ldb < (tb ? K : N))))
+        return set_error(NC_HIP_ERR_ARG, "nc_hip_gemm_f32_bmm: leading dim too small");
     coalesce_batch(bd);
-    const float one = 1.0f;
-    bool c_shared = false;  // several batch matrices accumulate into one C block
+    bool c_shared = false;  // several batch matrices add into one C block
     for (int d = 0; d < bd.nb; d++) c_shared = c_shared || bd.st[2][d] == 0;
-    if (bd.nb == 0) return nc_hip_gemm_f32(ta, tb, M, N, K, one, A, lda, B, ldb, beta, C, ldc, stream);
     if (c_shared) {
-        // ordered: batch index order, each GEMM after a block's first adding into what the earlier ones wrote
+        // in batch index order, every GEMM after a block's first adding into what the earlier ones wrote
         for (int64_t i = 0; i < count; i++) {
-            const int rc = nc_hip_gemm_f32(ta, tb, M, N, K, one, A + batch_offset(bd, 0, i), lda,
-                                           B + batch_offset(bd, 1, i), ldb, first_writer(bd, i) ? beta : 1.0f,
-                                           C + batch_offset(bd, 2, i), ldc, stream);
+            const int rc = nc_hip_gemm_f32(ta, tb, M, N, K, 1.0f, A + host_batch_off(bd, 0, i), lda,
+                                           B + host_batch_off(bd, 1, i), ldb, first_writer(bd, i) ? beta : 1.0f,
+                                           C + host_batch_off(bd, 2, i), ldc, stream);
             if (rc != NC_HIP_OK) return rc;
         }
         return NC_HIP_OK;
     }
-    k0_leading_dims(ta, tb, M, N, K, &lda, &ldb);
-    if (bd.nb == 1) {
-        int rc = NC_HIP_OK;
-        if (lt_gemm(ta, tb, M, N, K, one, A, lda, B, ldb, beta, C, ldc, count, bd.st[0][0], bd.st[1][0], bd.st[2][0],
-                    as_stream(stream), &rc))
-            return rc;
-    }
-    rocblas_handle h = blas_handle();
-    if (!h) return set_error(NC_HIP_ERR_DEVICE, "nc_hip_gemm_f32_bmm: no rocBLAS handle");
-    rocblas_status s = rocblas_set_stream(h, as_stream(stream));
-    if (s != rocblas_status_success) return blas_error(s, "nc_hip_gemm_f32_bmm");
-    if (bd.nb == 1) {
-        s = rocblas_sgemm_strided_batched_64(h, op_of(tb), op_of(ta), N, M, K, &one, B, ldb, bd.st[1][0], A, lda,
-                                             bd.st[0][0], &beta, C, ldc, bd.st[2][0], count);
-        return s == rocblas_status_success ? NC_HIP_OK : blas_error(s, "nc_hip_gemm_f32_bmm");
-    }
-    if (ws_bytes < nc_hip_gemm_f32_bmm_workspace(count) || !ws)
-        return set_error(NC_HIP_ERR_ARG, "nc_hip_gemm_f32_bmm: workspace of %zu bytes, need %zu", ws_bytes,
-                         nc_hip_gemm_f32_bmm_workspace(count));
-    const float **pa = (const float **)ws;
-    const float **pb = pa + count;
-    float **pc = (float **)(pb + count);
-    hipLaunchKernelGGL(k_batch_ptrs, dim3((unsigned)((count + 255) / 256)), dim3(256), 0, as_stream(stream), A, B, C,
-                       bd, count, pa, pb, pc);
-    if (int rc = check_launch("nc_hip_gemm_f32_bmm")) return rc;
-    s = rocblas_sgemm_batched_64(h, op_of(tb), op_of(ta), N, M, K, &one, pb, ldb, pa, lda, &beta, pc, ldc, count);
-    return s == rocblas_status_success ? NC_HIP_OK : blas_error(s, "nc_hip_gemm_f32_bmm");
+    SgArgs p = sg_args(M, N, K, 1.0f, A, lda, B, ldb, beta, C, ldc);
+    p.bat = bd;
+    return sg_run(p, ta, tb, count, as_stream(stream), "nc_hip_gemm_f32_bmm");
 }
