@@ -246,6 +246,18 @@ struct Strides {
 // Returns the new dim count; shape/strides are rewritten in place (nops operands).
 int coalesce(int nd, int64_t *shape, int nops, int64_t (*st)[NC_HIP_MAX_DIMS]);
 
+// global_load_lds_dwordx4: each lane's 16 bytes at g land in LDS at M0 + 16 * lane (M0 = lds, the
+// wave's destination; one wait state separates its write from the load).  Issued from inline assembly
+// so the compiler does not wait for these loads before every LDS read: callers wait with explicit
+// vmcnt counts.  The compiler treats M0 as reserved and does not honour the clobber: a kernel using
+// this must touch M0 nowhere else (checked in its compiled code).
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+__device__ __forceinline__ void dma16(const void *g, uint32_t lds) {
+    asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off" ::"s"(lds), "v"(g) : "memory", "m0");
+}
+#pragma clang diagnostic pop
+
 inline bool aligned16(const void *p) { return ((uintptr_t)p & 15u) == 0; }
 
 // grid size for a grid-stride streaming kernel: enough blocks to fill every CU `per_cu` times

@@ -10,12 +10,10 @@
 // held as TM x TN 16 x 16 accumulator tiles (4 floats per lane each).  K advances 16 at a time
 // through two LDS stages: the next step's panels are loaded into registers while the matrix cores
 // work on the current one, stored into the other stage, and one barrier per step separates the two.
-// Each operand keeps its global layout in LDS:
-//   * K-contiguous panel: BM (BN) rows of 16 floats, four 16-byte chunks per row, logical chunk c of
-//     row r stored at chunk c ^ ((r >> 2) & 3), so 16-byte reads of consecutive rows spread over the
-//     banks;
-//   * M/N-contiguous panel: 16 k-rows of BM (BN) floats, the row pitch padded by 4 floats so the four
-//     quarter-waves' reads (k-rows k, k + 4, k + 8, k + 12) land in different banks.
+// Each operand keeps its global layout in LDS (layouts at Panel below): a K-contiguous operand's
+// fragment is one 16-byte LDS read, an M/N-contiguous one's four 4-byte reads.  The MFMAs take the B
+// fragment first and so produce C^T tiles: each lane holds 4 consecutive columns of a row of C, and
+// the epilogue writes (and, for beta != 0, reads) C 16 bytes at a time.
 //
 // k mapping.  One MFMA multiplies a 16 x 4 slice of A by a 4 x 16 slice of B, quarter-wave q (lanes
 // 16 q .. 16 q + 15) holding one k.  In each stage of 16 k, quarter q gives the s-th MFMA (s = 0..3)
@@ -47,8 +45,6 @@ struct SgCfg {
     static constexpr int SLAB_A = 64 * BM + 256, SLAB_B = 64 * BN + 256;
     static constexpr int STAGE = SLAB_A + SLAB_B;
     static constexpr size_t LDS = 2 * (size_t)STAGE;
-    static constexpr int CA = 4 * BM / NT, CB = 4 * BN / NT;  // 16-byte chunks per thread per panel
-    static_assert(4 * BM % NT == 0 && 4 * BN % NT == 0, "panel chunks must divide over the workgroup");
 };
 using SgBig = SgCfg<8, 4, 2, 4>;    // 256 x 256
 using SgMid = SgCfg<4, 4, 2, 2>;    // 128 x 128
@@ -73,42 +69,70 @@ struct SgArgs {
     SgBatch bat;
 };
 
-// Chunk q of an R-row panel starting at (row r0, k k0): its 16-byte LDS position.
+// ---- operand panels ------------------------------------------------------------------------------
+// One stage of an operand: R rows (M or N) by 16 k, loaded as 16-byte chunks spread over the
+// workgroup's threads, kept in registers while the previous stage is multiplied, then stored to LDS.
+//   * K-contiguous operand: chunk u is row u / 4, k 4 (u % 4) .. + 3; in LDS rows of 64 bytes, logical
+//     chunk c of row r at chunk c ^ ((r >> 2) & 3), so the 16-byte fragment reads of 16 consecutive
+//     rows spread over all banks;
+//   * M/N-contiguous operand: chunk u is k-row u / (R / 4), rows 4 (u % (R / 4)) .. + 3; in LDS 16
+//     k-rows of R floats with a pitch of R + 4, so the four quarter-waves' fragment reads (k-rows k,
+//     k + 4, k + 8, k + 12 of 16 consecutive rows) land in different banks.
+template <int R, bool KC, int NT>
+struct Panel {
+    static constexpr int UNITS = 4 * R;
+    static constexpr int UPT = (UNITS + NT - 1) / NT;  // chunks per thread
+    static constexpr bool GUARD = UNITS % NT != 0;     // some threads own fewer chunks
+};
+
+// global-memory views, so loads are global_load (counted by vmcnt alone) rather than flat
+typedef const __attribute__((address_space(1))) float gfloat;
+typedef const __attribute__((address_space(1))) f4 gf4;
+
+// row and k of unit u's first chunk within the stage
 template <int R, bool KC>
-__device__ __forceinline__ uint32_t chunk_lds(int q) {
+__device__ __forceinline__ void unit_pos(int u, int &row, int &k) {
     if constexpr (KC) {
-        const int row = q >> 2, c = q & 3;
-        return (uint32_t)(row * 64 + ((c ^ ((row >> 2) & 3)) << 4));
+        row = u >> 2, k = (u & 3) * 4;
     } else {
-        constexpr int per_row = R / 4;
-        return (uint32_t)((q / per_row) * (R + 4) * 4 + (q % per_row) * 16);
+        row = (u % (R / 4)) * 4, k = u / (R / 4);
     }
 }
 
-// Chunk q's four floats from global memory, zero past the matrix.  VEC: the operand's rows start
-// 16-byte aligned (aligned base, leading dim a multiple of 4), so a chunk wholly inside is one load.
-template <int R, bool KC, bool VEC>
-__device__ __forceinline__ f4 chunk_load(const float *p, int64_t ld, int rows, int K, int r0, int k0, int q) {
+// 4 floats at (row .. row + 3 or k .. k + 3), zero past the matrix; VEC: 16-byte aligned rows, so a
+// chunk wholly inside is one load
+template <bool KC, bool VEC>
+__device__ __forceinline__ f4 load4(const float *p, int64_t ld, int rows, int K, int row, int k) {
     f4 v = {0.f, 0.f, 0.f, 0.f};
     if constexpr (KC) {
-        const int row = r0 + (q >> 2), k = k0 + (q & 3) * 4;
         if (row >= rows || k >= K) return v;
-        const float *s = p + (int64_t)row * ld + k;
-        if (VEC && k + 4 <= K) return *(const f4 *)s;
+        gfloat *s = (gfloat *)(p + (int64_t)row * ld + k);
+        if (VEC && k + 4 <= K) return *(gf4 *)s;
 #pragma unroll
         for (int j = 0; j < 4; j++)
             if (k + j < K) v[j] = s[j];
     } else {
-        constexpr int per_row = R / 4;
-        const int k = k0 + q / per_row, row = r0 + (q % per_row) * 4;
         if (k >= K || row >= rows) return v;
-        const float *s = p + (int64_t)k * ld + row;
-        if (VEC && row + 4 <= rows) return *(const f4 *)s;
+        gfloat *s = (gfloat *)(p + (int64_t)k * ld + row);
+        if (VEC && row + 4 <= rows) return *(gf4 *)s;
 #pragma unroll
         for (int j = 0; j < 4; j++)
             if (row + j < rows) v[j] = s[j];
     }
     return v;
+}
+
+// LDS store of one chunk
+template <int R, bool KC>
+__device__ __forceinline__ void unit_store(char *slab, int u, f4 v) {
+    int row, k;
+    unit_pos<R, KC>(u, row, k);
+    if constexpr (KC) {
+        const int c = k >> 2;
+        *(f4 *)(slab + row * 64 + ((c ^ ((row >> 2) & 3)) << 4)) = v;
+    } else {
+        *(f4 *)(slab + k * (R + 4) * 4 + row * 4) = v;
+    }
 }
 
 // The four values (s = 0..3) of panel row r that quarter-wave q gives the stage's MFMAs.
@@ -122,6 +146,52 @@ __device__ __forceinline__ f4 fragment(const char *slab, int r, int q) {
     }
 }
 
+// One operand's stage loads: registers, FAST source pointers, load and store.
+template <int R, bool KC, int NT, bool VEC, bool FAST>
+struct Loader {
+    using P = Panel<R, KC, NT>;
+    f4 reg[P::UPT];
+    gfloat *src[FAST ? P::UPT : 1];
+    const float *p;
+    int64_t ld;
+    int rows, K, r0, t;
+
+    // FAST problems (aligned rows, K a multiple of 16, an M/N-contiguous operand's row count a
+    // multiple of 4): rows past the matrix are clamped onto its last row (last 4-row chunk), so every
+    // load is in bounds and unconditional; what those rows produce is never stored
+    __device__ __forceinline__ void init(const float *p_, int64_t ld_, int rows_, int K_, int r0_, int t_) {
+        p = p_, ld = ld_, rows = rows_, K = K_, r0 = r0_, t = t_;
+        if constexpr (FAST) {
+#pragma unroll
+            for (int i = 0; i < P::UPT; i++) {
+                int row, k;
+                unit_pos<R, KC>(t + i * NT, row, k);
+                row = KC ? min(r0 + row, rows - 1) : min(r0 + row, rows - 4);
+                src[i] = (gfloat *)(KC ? p + (int64_t)row * ld + k : p + (int64_t)k * ld + row);
+            }
+        }
+    }
+    __device__ __forceinline__ bool owns(int i) const { return !P::GUARD || t + i * NT < P::UNITS; }
+    __device__ __forceinline__ void load(int k0) {
+#pragma unroll
+        for (int i = 0; i < P::UPT; i++) {
+            if (!owns(i)) continue;
+            if constexpr (FAST) {
+                reg[i] = *(gf4 *)(src[i] + (KC ? k0 : (int64_t)k0 * ld));
+            } else {
+                int row, k;
+                unit_pos<R, KC>(t + i * NT, row, k);
+                reg[i] = load4<KC, VEC>(p, ld, rows, K, r0 + row, k0 + k);
+            }
+        }
+    }
+    __device__ __forceinline__ void store(char *slab) const {
+#pragma unroll
+        for (int i = 0; i < P::UPT; i++)
+            if (owns(i)) unit_store<R, KC>(slab, t + i * NT, reg[i]);
+    }
+};
+
 // element offset of batch matrix `idx` for operand o (0 A, 1 B, 2 C)
 __device__ __forceinline__ int64_t batch_off(const SgBatch &bt, int o, int64_t idx) {
     int64_t off = 0;
@@ -133,13 +203,16 @@ __device__ __forceinline__ int64_t batch_off(const SgBatch &bt, int o, int64_t i
     return off;
 }
 
-template <class Cfg, bool AK, bool BK, bool VEC>
-__global__ __launch_bounds__(Cfg::NT, 1) void k_sgemm(SgArgs p) {
-    extern __shared__ __attribute__((aligned(16))) char smem[];
-    constexpr int kTM = Cfg::TM, kTN = Cfg::TN, kWGN = Cfg::WGN, kNT = Cfg::NT;
-    constexpr int kBM = Cfg::BM, kBN = Cfg::BN, kCA = Cfg::CA, kCB = Cfg::CB;
+// The workgroup's tile: block -> (batch matrix, tile) with XCD-contiguous runs and groups of
+// kSgGroupM tile-rows; the batch matrix's operands.
+struct TileAt {
+    int m0, n0;
+    const float *A, *B;
+    float *C;
+};
 
-    // block -> (batch matrix, tile): XCD-contiguous runs, then groups of kSgGroupM tile-rows
+template <int BM, int BN>
+__device__ __forceinline__ TileAt locate(const SgArgs &p) {
     int64_t id = blockIdx.x;
     const int64_t nblk = gridDim.x;
     if ((nblk & 7) == 0) id = (id & 7) * (nblk >> 3) + (id >> 3);
@@ -149,117 +222,239 @@ __global__ __launch_bounds__(Cfg::NT, 1) void k_sgemm(SgArgs p) {
     const int per_group = kSgGroupM * p.tiles_n;
     const int first_m = (tile / per_group) * kSgGroupM;
     const int gsize = min(p.tiles_m - first_m, kSgGroupM);
-    const int tm = first_m + (tile % per_group) % gsize, tn = (tile % per_group) / gsize;
-    const int m0 = tm * kBM, n0 = tn * kBN;
-
-    const float *A, *B;
-    float *C;
+    TileAt at;
+    at.m0 = (first_m + (tile % per_group) % gsize) * BM;
+    at.n0 = ((tile % per_group) / gsize) * BN;
     if (p.pa) {
-        A = p.pa[batch], B = p.pb[batch], C = p.pc[batch];
+        at.A = p.pa[batch], at.B = p.pb[batch], at.C = p.pc[batch];
     } else {
-        A = p.A + batch_off(p.bat, 0, batch), B = p.B + batch_off(p.bat, 1, batch), C = p.C + batch_off(p.bat, 2, batch);
+        at.A = p.A + batch_off(p.bat, 0, batch), at.B = p.B + batch_off(p.bat, 1, batch);
+        at.C = p.C + batch_off(p.bat, 2, batch);
     }
+    return at;
+}
 
-    const int t = threadIdx.x, lane = t & (kWave - 1), wid = t / kWave;
-    const int wm = wid / kWGN, wn = wid % kWGN;
+// The stage's MFMAs for this wave: fragments of its TM row blocks and TN column blocks, four k each.
+template <class Cfg, bool AK, bool BK>
+__device__ __forceinline__ void stage_mfma(const char *cur, f4 (&acc)[Cfg::TM][Cfg::TN], int wm, int wn, int fr, int fq) {
+    constexpr int kTM = Cfg::TM, kTN = Cfg::TN;
+    f4 fa[kTM], fb[kTN];
+#pragma unroll
+    for (int i = 0; i < kTM; i++) fa[i] = fragment<Cfg::BM, AK>(cur, (wm * kTM + i) * 16 + fr, fq);
+#pragma unroll
+    for (int j = 0; j < kTN; j++) fb[j] = fragment<Cfg::BN, BK>(cur + Cfg::SLAB_A, (wn * kTN + j) * 16 + fr, fq);
+#pragma unroll
+    for (int s = 0; s < 4; s++)
+#pragma unroll
+        for (int i = 0; i < kTM; i++)
+#pragma unroll
+            for (int j = 0; j < kTN; j++)
+                // B fragment first: the tile is C^T, so each lane ends up with 4 consecutive columns of a
+                // row of C
+                acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(fb[j][s], fa[i][s], acc[i][j], 0, 0, 0);
+}
 
-    f4 ra[kCA], rb[kCB];
-    auto gload = [&](int k0) {
-#pragma unroll
-        for (int i = 0; i < kCA; i++) ra[i] = chunk_load<kBM, AK, VEC>(A, p.lda, p.M, p.K, m0, k0, t + i * kNT);
-#pragma unroll
-        for (int i = 0; i < kCB; i++) rb[i] = chunk_load<kBN, BK, VEC>(B, p.ldb, p.N, p.K, n0, k0, t + i * kNT);
-    };
-    auto sstore = [&](char *stage) {
-#pragma unroll
-        for (int i = 0; i < kCA; i++) *(f4 *)(stage + chunk_lds<kBM, AK>(t + i * kNT)) = ra[i];
-#pragma unroll
-        for (int i = 0; i < kCB; i++) *(f4 *)(stage + Cfg::SLAB_A + chunk_lds<kBN, BK>(t + i * kNT)) = rb[i];
-    };
-
-    f4 acc[kTM][kTN];
-#pragma unroll
-    for (int i = 0; i < kTM; i++)
-#pragma unroll
-        for (int j = 0; j < kTN; j++) acc[i][j] = f4{0.f, 0.f, 0.f, 0.f};
-
-    const int fr = lane & 15, fq = lane >> 4;
-    const int nk = (p.K + kSgBK - 1) / kSgBK;
-    if (nk > 0) {
-        gload(0);
-        sstore(smem);
-        __syncthreads();
-    }
-    for (int kt = 0; kt < nk; kt++) {
-        const char *cur = smem + (kt & 1) * Cfg::STAGE;
-        if (kt + 1 < nk) gload((kt + 1) * kSgBK);
-        {
-            f4 fa[kTM], fb[kTN];
-#pragma unroll
-            for (int i = 0; i < kTM; i++) fa[i] = fragment<kBM, AK>(cur, (wm * kTM + i) * 16 + fr, fq);
-#pragma unroll
-            for (int j = 0; j < kTN; j++) fb[j] = fragment<kBN, BK>(cur + Cfg::SLAB_A, (wn * kTN + j) * 16 + fr, fq);
-#pragma unroll
-            for (int s = 0; s < 4; s++)
-#pragma unroll
-                for (int i = 0; i < kTM; i++)
-#pragma unroll
-                    for (int j = 0; j < kTN; j++)
-                        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(fa[i][s], fb[j][s], acc[i][j], 0, 0, 0);
-        }
-        // the other stage was last read before the previous barrier, so it can be refilled now
-        if (kt + 1 < nk) sstore(smem + ((kt + 1) & 1) * Cfg::STAGE);
-        __syncthreads();
-    }
-
-    // accumulator layout of a 16 x 16 tile: lane l, element v holds row 4 (l / 16) + v, column l % 16
+// C = alpha acc + beta C over the wave's tiles.  acc[i][j] is the 16 x 16 tile C^T: lane l, element v
+// holds row (tile row + l % 16), column (tile column + 4 (l / 16) + v).
+template <class Cfg>
+__device__ __forceinline__ void write_tiles(const SgArgs &p, const TileAt &at, const f4 (&acc)[Cfg::TM][Cfg::TN],
+                                            int wm, int wn, int fr, int fq) {
+    constexpr int kTM = Cfg::TM, kTN = Cfg::TN;
+    const bool vec_c = ((uintptr_t)at.C & 15) == 0 && p.ldc % 4 == 0;
 #pragma unroll
     for (int i = 0; i < kTM; i++) {
+        const int m = at.m0 + (wm * kTM + i) * 16 + fr;
+        if (m >= p.M) continue;
+        float *crow = at.C + (int64_t)m * p.ldc;
 #pragma unroll
         for (int j = 0; j < kTN; j++) {
-            const int n = n0 + (wn * kTN + j) * 16 + fr;
-            if (n >= p.N) continue;
+            const int n = at.n0 + (wn * kTN + j) * 16 + 4 * fq;
+            f4 r = p.alpha * acc[i][j];
+            if (vec_c && n + 4 <= p.N) {
+                f4 *c = (f4 *)(crow + n);
+                if (p.beta != 0.0f) r = r + p.beta * *c;
+                *c = r;
+            } else {
 #pragma unroll
-            for (int v = 0; v < 4; v++) {
-                const int m = m0 + (wm * kTM + i) * 16 + 4 * fq + v;
-                if (m >= p.M) continue;
-                float *c = C + (int64_t)m * p.ldc + n;
-                const float r = p.alpha * acc[i][j][v];
-                *c = p.beta != 0.0f ? r + p.beta * *c : r;
+                for (int v = 0; v < 4; v++) {
+                    if (n + v >= p.N) break;
+                    float *c = crow + n + v;
+                    *c = p.beta != 0.0f ? r[v] + p.beta * *c : r[v];
+                }
             }
         }
     }
 }
 
-template <class Cfg, bool AK, bool BK, bool VEC>
+template <class Cfg, bool AK, bool BK, bool VEC, bool FAST>
+__global__ __launch_bounds__(Cfg::NT, 1) void k_sgemm(SgArgs p) {
+    extern __shared__ __attribute__((aligned(16))) char smem[];
+    const TileAt at = locate<Cfg::BM, Cfg::BN>(p);
+    const int t = threadIdx.x, lane = t & (kWave - 1), wid = t / kWave;
+    const int wm = wid / Cfg::WGN, wn = wid % Cfg::WGN, fr = lane & 15, fq = lane >> 4;
+
+    Loader<Cfg::BM, AK, Cfg::NT, VEC, FAST> la;
+    Loader<Cfg::BN, BK, Cfg::NT, VEC, FAST> lb;
+    la.init(at.A, p.lda, p.M, p.K, at.m0, t);
+    lb.init(at.B, p.ldb, p.N, p.K, at.n0, t);
+
+    f4 acc[Cfg::TM][Cfg::TN];
+#pragma unroll
+    for (int i = 0; i < Cfg::TM; i++)
+#pragma unroll
+        for (int j = 0; j < Cfg::TN; j++) acc[i][j] = f4{0.f, 0.f, 0.f, 0.f};
+
+    const int nk = (p.K + kSgBK - 1) / kSgBK;
+    if (nk > 0) {
+        la.load(0);
+        lb.load(0);
+        la.store(smem);
+        lb.store(smem + Cfg::SLAB_A);
+        __syncthreads();
+    }
+    for (int kt = 0; kt < nk; kt++) {
+        if (kt + 1 < nk) {
+            la.load((kt + 1) * kSgBK);
+            lb.load((kt + 1) * kSgBK);
+        }
+        stage_mfma<Cfg, AK, BK>(smem + (kt & 1) * Cfg::STAGE, acc, wm, wn, fr, fq);
+        // the other stage was last read before the previous barrier, so it can be refilled now
+        if (kt + 1 < nk) {
+            char *next = smem + ((kt + 1) & 1) * Cfg::STAGE;
+            la.store(next);
+            lb.store(next + Cfg::SLAB_A);
+        }
+        __syncthreads();
+    }
+    write_tiles<Cfg>(p, at, acc, wm, wn, fr, fq);
+}
+
+// ------------------------------------------------------------------------------------------------
+// Large FAST problems: the same 256 x 256 tile, its panels loaded straight from global memory into
+// LDS (global_load_lds_dwordx4) three stages ahead through four LDS stages, with no staging registers
+// and no LDS write instructions; one barrier per stage.  A stage of a panel is 16 load instructions of
+// 1 KiB each: 16 rows of a K-contiguous panel (lane l: row l / 4, the chunk that belongs at position
+// l % 4 under the swizzle) or one k-row of a M/N-contiguous one (lane l: rows 4 l .. 4 l + 3).  Waves
+// 0-3 load A, waves 4-7 B, four instructions each.  Rows past the matrix are clamped as in the
+// staged kernel's FAST loads.
+constexpr int kSgDmaStages = 4;
+constexpr size_t kSgDmaLds = kSgDmaStages * (size_t)SgBig::STAGE;
+
+template <bool AK, bool BK>
+__global__ __launch_bounds__(SgBig::NT, 1) void k_sgemm_dma(SgArgs p) {
+    using Cfg = SgBig;
+    constexpr int kR = Cfg::BM;  // = BN
+    static_assert(Cfg::BM == Cfg::BN && Cfg::NT / kWave == 8, "one panel per half of the waves");
+    extern __shared__ __attribute__((aligned(16))) char smem[];
+    const TileAt at = locate<Cfg::BM, Cfg::BN>(p);
+    const int t = threadIdx.x, lane = t & (kWave - 1), wid = t / kWave;
+    const int wm = wid / Cfg::WGN, wn = wid % Cfg::WGN, fr = lane & 15, fq = lane >> 4;
+
+    // this wave's four load instructions per stage (wave-uniform panel)
+    const bool panel_b = wid >= 4;
+    const bool kc = panel_b ? BK : AK;
+    const float *base = panel_b ? at.B : at.A;
+    const int64_t ld = panel_b ? p.ldb : p.lda;
+    const int rows = panel_b ? p.N : p.M, r0 = panel_b ? at.n0 : at.m0;
+    const float *src[4];
+    uint32_t loff[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const int idx = (wid & 3) * 4 + i;
+        if (kc) {
+            const int prow = 16 * idx + (lane >> 2), c = (lane & 3) ^ ((prow >> 2) & 3);
+            src[i] = base + (int64_t)min(r0 + prow, rows - 1) * ld + 4 * c;
+            loff[i] = (uint32_t)(idx * 1024);
+        } else {
+            src[i] = base + (int64_t)idx * ld + min(r0 + 4 * lane, rows - 4);
+            loff[i] = (uint32_t)(idx * (kR + 4) * 4);
+        }
+        loff[i] += panel_b ? Cfg::SLAB_A : 0;
+    }
+    const int64_t kstep = kc ? kSgBK : kSgBK * ld;  // elements from one stage to the next
+    const uint32_t sbase = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) char *)smem;
+    auto issue = [&](int kt) {
+        const uint32_t st = sbase + (uint32_t)(kt % kSgDmaStages) * Cfg::STAGE;
+#pragma unroll
+        for (int i = 0; i < 4; i++) dma16(src[i] + kt * kstep, __builtin_amdgcn_readfirstlane(st + loff[i]));
+    };
+
+    f4 acc[Cfg::TM][Cfg::TN];
+#pragma unroll
+    for (int i = 0; i < Cfg::TM; i++)
+#pragma unroll
+        for (int j = 0; j < Cfg::TN; j++) acc[i][j] = f4{0.f, 0.f, 0.f, 0.f};
+
+    const int nk = p.K / kSgBK;
+    for (int kt = 0; kt < kSgDmaStages - 1 && kt < nk; kt++) issue(kt);
+    for (int kt = 0; kt < nk; kt++) {
+        // this wave's loads of stage kt are done once at most 4 per later stage in flight remain
+        const int ahead = min(nk - 1 - kt, kSgDmaStages - 2);
+        if (ahead == 2) asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
+        else if (ahead == 1) asm volatile("s_waitcnt vmcnt(4)" ::: "memory");
+        else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        __builtin_amdgcn_s_barrier();  // every wave's loads of stage kt have landed; stage kt-1's reads are done
+        asm volatile("" ::: "memory");
+        if (kt + kSgDmaStages - 1 < nk) issue(kt + kSgDmaStages - 1);  // into the stage kt-1 used
+        stage_mfma<Cfg, AK, BK>(smem + (kt % kSgDmaStages) * Cfg::STAGE, acc, wm, wn, fr, fq);
+    }
+    write_tiles<Cfg>(p, at, acc, wm, wn, fr, fq);
+}
+
+template <class Cfg, bool AK, bool BK, bool VEC, bool FAST>
 static void sg_attr() {
     // dynamic LDS above 64 KiB has to be allowed per kernel, once per device
     static bool done[64] = {};
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64 || done[dev]) return;
-    (void)hipFuncSetAttribute((const void *)k_sgemm<Cfg, AK, BK, VEC>, hipFuncAttributeMaxDynamicSharedMemorySize,
+    (void)hipFuncSetAttribute((const void *)k_sgemm<Cfg, AK, BK, VEC, FAST>, hipFuncAttributeMaxDynamicSharedMemorySize,
                               (int)Cfg::LDS);
     done[dev] = true;
 }
 
-template <class Cfg, bool AK, bool BK, bool VEC>
+template <class Cfg, bool AK, bool BK, bool VEC, bool FAST>
 static int sg_launch(SgArgs &p, int64_t count, hipStream_t st, const char *what) {
     p.tiles_m = (p.M + Cfg::BM - 1) / Cfg::BM;
     p.tiles_n = (p.N + Cfg::BN - 1) / Cfg::BN;
     const int64_t blocks = (int64_t)p.tiles_m * p.tiles_n * count;
     if (blocks > INT32_MAX) return set_error(NC_HIP_ERR_ARG, "%s: %lld tiles exceed one launch", what, (long long)blocks);
-    sg_attr<Cfg, AK, BK, VEC>();
-    hipLaunchKernelGGL((k_sgemm<Cfg, AK, BK, VEC>), dim3((unsigned)blocks), dim3(Cfg::NT), Cfg::LDS, st, p);
+    sg_attr<Cfg, AK, BK, VEC, FAST>();
+    hipLaunchKernelGGL((k_sgemm<Cfg, AK, BK, VEC, FAST>), dim3((unsigned)blocks), dim3(Cfg::NT), Cfg::LDS, st, p);
+    return check_launch(what);
+}
+
+#ifndef SG_DMA
+#define SG_DMA 1
+#endif
+template <bool AK, bool BK>
+static int sg_launch_dma(SgArgs &p, int64_t count, hipStream_t st, const char *what) {
+    p.tiles_m = (p.M + SgBig::BM - 1) / SgBig::BM;
+    p.tiles_n = (p.N + SgBig::BN - 1) / SgBig::BN;
+    const int64_t blocks = (int64_t)p.tiles_m * p.tiles_n * count;
+    if (blocks > INT32_MAX) return set_error(NC_HIP_ERR_ARG, "%s: %lld tiles exceed one launch", what, (long long)blocks);
+    static bool done[64] = {};
+    int dev = 0;
+    if (hipGetDevice(&dev) == hipSuccess && dev >= 0 && dev < 64 && !done[dev]) {
+        (void)hipFuncSetAttribute((const void *)k_sgemm_dma<AK, BK>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                  (int)kSgDmaLds);
+        done[dev] = true;
+    }
+    hipLaunchKernelGGL((k_sgemm_dma<AK, BK>), dim3((unsigned)blocks), dim3(SgBig::NT), kSgDmaLds, st, p);
     return check_launch(what);
 }
 
 template <class Cfg>
 static int sg_layouts(SgArgs &p, int ta, int tb, bool vec, int64_t count, hipStream_t st, const char *what) {
     const bool ak = !ta, bk = tb != 0;
+    const bool fast = vec && p.K % kSgBK == 0 && (ak || p.M % 4 == 0) && (bk || p.N % 4 == 0);
+    // the DMA kernel clamps M/N-contiguous chunks onto the last 4 rows: at least 4 rows there
+    const bool dma = SG_DMA && fast && p.K > 0 && Cfg::BM == SgBig::BM && (ak || p.M >= 4) && (bk || p.N >= 4);
 #define NC_SG_CASE(AK_, BK_)                                                                \
     if (ak == AK_ && bk == BK_)                                                             \
-        return vec ? sg_launch<Cfg, AK_, BK_, true>(p, count, st, what)                     \
-                   : sg_launch<Cfg, AK_, BK_, false>(p, count, st, what);
+        return dma   ? sg_launch_dma<AK_, BK_>(p, count, st, what)                          \
+               : fast ? sg_launch<Cfg, AK_, BK_, true, true>(p, count, st, what)            \
+               : vec  ? sg_launch<Cfg, AK_, BK_, true, false>(p, count, st, what)           \
+                      : sg_launch<Cfg, AK_, BK_, false, false>(p, count, st, what);
     NC_SG_CASE(true, true)
     NC_SG_CASE(true, false)
     NC_SG_CASE(false, true)

@@ -197,15 +197,6 @@ constexpr size_t kDmaLds = 4 * (size_t)kDmaStage;
 
 __device__ __forceinline__ int dma_swz(int row, int c) { return (c ^ ((row >> 2) & 3)) * 16; }
 
-// M0 holds the wave's LDS destination; one wait state separates its write from the load.  The
-// compiler treats M0 as reserved and does not honour the clobber: the kernels using this were checked
-// in their compiled code to touch M0 nowhere else.
-#pragma clang diagnostic push
-#pragma clang diagnostic ignored "-Winline-asm"
-__device__ __forceinline__ void dma16(const void *g, uint32_t lds) {
-    asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off" ::"s"(lds), "v"(g) : "memory", "m0");
-}
-#pragma clang diagnostic pop
 
 template <bool OUT_F32>
 __global__ __launch_bounds__(kDmaNT, 1) void k_qgemm_dma(QgArgs p) {

@@ -1475,7 +1475,13 @@ def test_kernel_linear_int8(K, M, Kd, N, has_b):
 
 
 GEMM_F32 = [(0, 0, 1000, 500, 300), (1, 0, 257, 129, 1000), (0, 1, 64, 4096, 512), (1, 1, 33, 65, 17),
-            (0, 1, 4096, 4096, 4096), (0, 0, 5, 7, 0)]
+            (0, 1, 4096, 4096, 4096), (0, 0, 5, 7, 0),
+            # 256 x 256 tiles with panels loaded straight into LDS, every operand layout, rows past M / N
+            # clamped onto the matrix
+            (0, 0, 4100, 4096, 256), (0, 1, 4100, 4096, 256), (1, 0, 4100, 4096, 256), (1, 1, 4100, 4096, 256),
+            (0, 0, 4096, 4100, 256),
+            # 256 x 256 tiles through registers: a K tail (16-byte loads) and an unaligned transposed A
+            (0, 1, 4096, 4096, 250), (1, 1, 4099, 4096, 256)]
 
 
 @pytest.mark.parametrize("ta,tb,M,N,Kd", GEMM_F32)
@@ -1515,6 +1521,25 @@ def test_kernel_gemm_f32_strided_batch_aligned_and_deterministic(K):
     terms = np.abs(A).astype(np.float64) @ np.abs(np.swapaxes(Bm, 1, 2)).astype(np.float64)
     assert O.gemm_excess(outs[0], want, terms, Kd) <= 1.0
     assert_bits(outs[1], outs[0], "second run")
+
+
+def test_kernel_gemm_f32_bmm_large_broadcast(K):
+    """A batch large enough for the 256 x 256 tiles loaded straight into LDS, A broadcast over the
+    batch (stride 0) and B a transposed view, as in attention scores against one shared query block."""
+    rng = np.random.default_rng(23)
+    Bc, M, N, Kd = 16, 1024, 1024, 128
+    A = rng.standard_normal((M, Kd)).astype(np.float32)
+    Bm = rng.standard_normal((Bc, N, Kd)).astype(np.float32)  # used transposed
+    Ad, Bd = dev(A), dev(Bm)
+    C = empty(4 * Bc * M * N)
+    K.gemm_f32_bmm(0, 1, M, N, Kd, Ad.ptr, Kd, Bd.ptr, Kd, 0.0, C.ptr, N, (Bc,), (0,), (N * Kd,), (M * N,))
+    sync()
+    got = C.to_numpy(np.float32, (Bc, M, N))
+    rows = _rows_sample(M, 32)
+    for b in (0, 7, Bc - 1):
+        want = A[rows].astype(np.float64) @ Bm[b].T.astype(np.float64)
+        terms = np.abs(A[rows]).astype(np.float64) @ np.abs(Bm[b].T).astype(np.float64)
+        assert O.gemm_excess(got[b][rows], want, terms, Kd) <= 1.0, f"batch {b}"
 
 
 BMM_LAYOUTS = [
