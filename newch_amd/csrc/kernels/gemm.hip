@@ -235,23 +235,37 @@ __device__ __forceinline__ TileAt locate(const SgArgs &p) {
 }
 
 // The stage's MFMAs for this wave: fragments of its TM row blocks and TN column blocks, four k each.
+template <class Cfg>
+struct Frags {
+    f4 a[Cfg::TM], b[Cfg::TN];
+};
+
+template <class Cfg, bool AK, bool BK>
+__device__ __forceinline__ void read_frags(const char *cur, Frags<Cfg> &F, int wm, int wn, int fr, int fq) {
+#pragma unroll
+    for (int i = 0; i < Cfg::TM; i++) F.a[i] = fragment<Cfg::BM, AK>(cur, (wm * Cfg::TM + i) * 16 + fr, fq);
+#pragma unroll
+    for (int j = 0; j < Cfg::TN; j++) F.b[j] = fragment<Cfg::BN, BK>(cur + Cfg::SLAB_A, (wn * Cfg::TN + j) * 16 + fr, fq);
+}
+
+// MFMAs S0 .. S1 - 1 of a stage.  The B fragment goes first: the tile is C^T, so each lane ends up
+// holding 4 consecutive columns of a row of C.
+template <class Cfg, int S0, int S1>
+__device__ __forceinline__ void mfma_steps(const Frags<Cfg> &F, f4 (&acc)[Cfg::TM][Cfg::TN]) {
+#pragma unroll
+    for (int s = S0; s < S1; s++)
+#pragma unroll
+        for (int i = 0; i < Cfg::TM; i++)
+#pragma unroll
+            for (int j = 0; j < Cfg::TN; j++)
+                acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(F.b[j][s], F.a[i][s], acc[i][j], 0, 0, 0);
+}
+
 template <class Cfg, bool AK, bool BK>
 __device__ __forceinline__ void stage_mfma(const char *cur, f4 (&acc)[Cfg::TM][Cfg::TN], int wm, int wn, int fr, int fq) {
-    constexpr int kTM = Cfg::TM, kTN = Cfg::TN;
-    f4 fa[kTM], fb[kTN];
-#pragma unroll
-    for (int i = 0; i < kTM; i++) fa[i] = fragment<Cfg::BM, AK>(cur, (wm * kTM + i) * 16 + fr, fq);
-#pragma unroll
-    for (int j = 0; j < kTN; j++) fb[j] = fragment<Cfg::BN, BK>(cur + Cfg::SLAB_A, (wn * kTN + j) * 16 + fr, fq);
-#pragma unroll
-    for (int s = 0; s < 4; s++)
-#pragma unroll
-        for (int i = 0; i < kTM; i++)
-#pragma unroll
-            for (int j = 0; j < kTN; j++)
-                // B fragment first: the tile is C^T, so each lane ends up with 4 consecutive columns of a
-                // row of C
-                acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(fb[j][s], fa[i][s], acc[i][j], 0, 0, 0);
+    Frags<Cfg> F;
+    read_frags<Cfg, AK, BK>(cur, F, wm, wn, fr, fq);
+    mfma_steps<Cfg, 0, 4>(F, acc);
 }
 
 // C = alpha acc + beta C over the wave's tiles.  acc[i][j] is the 16 x 16 tile C^T: lane l, element v
@@ -426,6 +440,9 @@ static int sg_launch(SgArgs &p, int64_t count, hipStream_t st, const char *what)
 #ifndef SG_DMA
 #define SG_DMA 1
 #endif
+#ifndef SG_DMA_MIN_K
+#define SG_DMA_MIN_K 512
+#endif
 template <bool AK, bool BK>
 static int sg_launch_dma(SgArgs &p, int64_t count, hipStream_t st, const char *what) {
     p.tiles_m = (p.M + SgBig::BM - 1) / SgBig::BM;
@@ -448,7 +465,7 @@ static int sg_layouts(SgArgs &p, int ta, int tb, bool vec, int64_t count, hipStr
     const bool ak = !ta, bk = tb != 0;
     const bool fast = vec && p.K % kSgBK == 0 && (ak || p.M % 4 == 0) && (bk || p.N % 4 == 0);
     // the DMA kernel clamps M/N-contiguous chunks onto the last 4 rows: at least 4 rows there
-    const bool dma = SG_DMA && fast && p.K > 0 && Cfg::BM == SgBig::BM && (ak || p.M >= 4) && (bk || p.N >= 4);
+    const bool dma = SG_DMA && fast && p.K >= SG_DMA_MIN_K && Cfg::BM == SgBig::BM && (ak || p.M >= 4) && (bk || p.N >= 4);
 #define NC_SG_CASE(AK_, BK_)                                                                \
     if (ak == AK_ && bk == BK_)                                                             \
         return dma   ? sg_launch_dma<AK_, BK_>(p, count, st, what)                          \
