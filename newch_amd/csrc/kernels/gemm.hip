@@ -73,8 +73,7 @@ struct SgArgs {
 // One stage of an operand: R rows (M or N) by 16 k, loaded as 16-byte chunks spread over the
 // workgroup's threads, kept in registers while the previous stage is multiplied, then stored to LDS.
 //   * K-contiguous operand: chunk u is row u / 4, k 4 (u % 4) .. + 3; in LDS rows of 64 bytes, logical
-//     chunk c of row r at chunk c ^ ((r >> 2) & 3), so the 16-byte fragment reads of 16 consecutive
-//     rows spread over all banks;
+//     chunk c of row r at chunk c ^ kc_swz(r), so the 16-byte fragment reads spread over all banks;
 //   * M/N-contiguous operand: chunk u is k-row u / (R / 4), rows 4 (u % (R / 4)) .. + 3; in LDS 16
 //     k-rows of R floats with a pitch of R + 4, so the four quarter-waves' fragment reads (k-rows k,
 //     k + 4, k + 8, k + 12 of 16 consecutive rows) land in different banks.
@@ -122,6 +121,11 @@ __device__ __forceinline__ f4 load4(const float *p, int64_t ld, int rows, int K,
     return v;
 }
 
+// The chunk permutation of K-contiguous panel row r (an XOR mask on its four 16-byte chunks).
+// (r >> 1) & 3 leaves the 16-byte fragment reads of the 16 rows and 4 quarter-waves free of bank
+// conflicts (SQ_LDS_BANK_CONFLICT reads 0; (r >> 2) & 3 read a third to a half of the LDS cycles).
+__device__ __forceinline__ int kc_swz(int r) { return (r >> 1) & 3; }
+
 // LDS store of one chunk
 template <int R, bool KC>
 __device__ __forceinline__ void unit_store(char *slab, int u, f4 v) {
@@ -129,7 +133,7 @@ __device__ __forceinline__ void unit_store(char *slab, int u, f4 v) {
     unit_pos<R, KC>(u, row, k);
     if constexpr (KC) {
         const int c = k >> 2;
-        *(f4 *)(slab + row * 64 + ((c ^ ((row >> 2) & 3)) << 4)) = v;
+        *(f4 *)(slab + row * 64 + ((c ^ kc_swz(row)) << 4)) = v;
     } else {
         *(f4 *)(slab + k * (R + 4) * 4 + row * 4) = v;
     }
@@ -139,7 +143,7 @@ __device__ __forceinline__ void unit_store(char *slab, int u, f4 v) {
 template <int R, bool KC>
 __device__ __forceinline__ f4 fragment(const char *slab, int r, int q) {
     if constexpr (KC) {
-        return *(const f4 *)(slab + r * 64 + ((q ^ ((r >> 2) & 3)) << 4));
+        return *(const f4 *)(slab + r * 64 + ((q ^ kc_swz(r)) << 4));
     } else {
         const float *b = (const float *)slab + 4 * q * (R + 4) + r;
         return f4{b[0], b[R + 4], b[2 * (R + 4)], b[3 * (R + 4)]};
@@ -348,7 +352,7 @@ __global__ __launch_bounds__(Cfg::NT, 1) void k_sgemm(SgArgs p) {
 // LDS (global_load_lds_dwordx4) three stages ahead through four LDS stages, with no staging registers
 // and no LDS write instructions; one barrier per stage.  A stage of a panel is 16 load instructions of
 // 1 KiB each: 16 rows of a K-contiguous panel (lane l: row l / 4, the chunk that belongs at position
-// l % 4 under the swizzle) or one k-row of a M/N-contiguous one (lane l: rows 4 l .. 4 l + 3).  Waves
+// l % 4 under the row's permutation) or one k-row of a M/N-contiguous one (lane l: rows 4 l .. 4 l + 3).  Waves
 // 0-3 load A, waves 4-7 B, four instructions each.  Rows past the matrix are clamped as in the
 // staged kernel's FAST loads.
 constexpr int kSgDmaStages = 4;
@@ -376,7 +380,7 @@ __global__ __launch_bounds__(SgBig::NT, 1) void k_sgemm_dma(SgArgs p) {
     for (int i = 0; i < 4; i++) {
         const int idx = (wid & 3) * 4 + i;
         if (kc) {
-            const int prow = 16 * idx + (lane >> 2), c = (lane & 3) ^ ((prow >> 2) & 3);
+            const int prow = 16 * idx + (lane >> 2), c = (lane & 3) ^ kc_swz(prow);
             src[i] = base + (int64_t)min(r0 + prow, rows - 1) * ld + 4 * c;
             loff[i] = (uint32_t)(idx * 1024);
         } else {
