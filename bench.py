@@ -456,6 +456,7 @@ def traffic_summary(root: Path) -> str:
     its run's dispatches minus its group's setup dispatches, divided by its launches (one warm +
     TIMED timed): KiB per launch, with the copy calibration's factors."""
     owner = {lab: g for g, (labels, _) in GROUPS.items() for lab in labels}
+    owner.update({lab: "gemm" for lab in GEMM_LABELS})
     setup = {d.name[len("_setup_"):]: _pmc_counts(d) for d in root.iterdir() if d.name.startswith("_setup_")}
     per = {}
     for d in sorted(p for p in root.iterdir() if p.is_dir() and not p.name.startswith("_")):
@@ -675,6 +676,10 @@ def only_mode(K, hm, labels, setup_only=False):
         if want:
             classes.update(run_group(K, hm, builder, set(want), setup_only))
     if setup_only:
+        if any(x in GEMM_LABELS for x in labels):
+            _, keep = group_gemm(K, hm)
+            hm.synchronize()
+            del keep
         print(json.dumps({"setup_only": sorted(labels)}), flush=True)
         return
     gemm = run_gemm(K, hm, set(labels)) if any(x in GEMM_LABELS for x in labels) else {}

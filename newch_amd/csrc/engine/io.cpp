@@ -15,6 +15,8 @@
 #include <stdlib.h>
 #include <string.h>
 
+#include <string>
+
 #include "engine.hpp"
 
 namespace nce {
@@ -146,6 +148,156 @@ static bool write_tensor(nc_ctx *ctx, FILE *f, nc_tensor *t, size_t bytes) {
     return ok;
 }
 
+
+// ---- the file, entry by entry -------------------------------------------------------------------------
+// One entry's header as stored: name, dtype, shape and the data byte count that follows it.
+struct EntryHeader {
+    std::string name;
+    uint32_t dtype = 0;
+    Dims dims;
+    uint64_t bytes = 0;
+};
+
+class NcwWriter {
+  public:
+    NcwWriter(nc_ctx *ctx, FILE *f) : ctx_(ctx), f_(f) {}
+    bool header(uint32_t count) {
+        const uint32_t version = kFileVersion;
+        return put(f_, "NCW1", 4) && put(f_, &version, 4) && put(f_, &count, 4);
+    }
+    bool entry(const char *name, nc_tensor *t) {
+        const uint32_t len = (uint32_t)strlen(name), dt = (uint32_t)t->dtype, nd = (uint32_t)t->ndim;
+        const uint64_t bytes = (uint64_t)nc_numel(t) * dtype_size(t->dtype);
+        return put(f_, &len, 4) && put(f_, name, len) && put(f_, &dt, 4) && put(f_, &nd, 4) &&
+               put(f_, t->shape, sizeof(int64_t) * nd) && put(f_, &bytes, 8) && write_tensor(ctx_, f_, t, (size_t)bytes);
+    }
+
+  private:
+    nc_ctx *ctx_;
+    FILE *f_;
+};
+
+class NcwReader {
+  public:
+    explicit NcwReader(FILE *f) : f_(f) {}
+    // magic and version; on failure the reference's message for the problem found
+    bool open(const char *path, nc_ctx *ctx) {
+        char magic[4];
+        uint32_t version = 0;
+        if (!get(f_, magic, 4) || memcmp(magic, "NCW1", 4) != 0 || !get(f_, &version, 4) || !get(f_, &count_, 4)) {
+            error(ctx, NC_ERR_ARG, "nc_load: '%s' is not an NCW1 tensor file", path);
+            return false;
+        }
+        if (version != kFileVersion) {
+            error(ctx, NC_ERR_ARG, "nc_load: '%s' has unsupported version %u", path, version);
+            return false;
+        }
+        return true;
+    }
+    uint32_t count() const { return count_; }
+    bool next(EntryHeader &h) {
+        uint32_t len = 0, nd = 0;
+        if (!get(f_, &len, 4) || len > kMaxName) return false;
+        h.name.resize(len);
+        if (!get(f_, &h.name[0], len) || !get(f_, &h.dtype, 4) || !get(f_, &nd, 4) || nd > NC_MAX_DIMS) return false;
+        h.dims.rank = (int)nd;
+        return get(f_, h.dims.e, sizeof(int64_t) * nd) && get(f_, &h.bytes, 8);
+    }
+    bool skip(uint64_t bytes) { return fseeko(f_, (off_t)bytes, SEEK_CUR) == 0; }
+    // the entry's data into t (contiguous, exactly its size): 1 ok, 0 short read, -1 device error
+    int read_into(nc_ctx *ctx, nc_tensor *t, uint64_t bytes) {
+        if (!bytes) return 1;
+        if (ctx->device < 0) {
+            char *h = hptr(t, true);
+            return h && get(f_, h, (size_t)bytes) ? 1 : 0;
+        }
+        // every byte of t is about to be written; the rest of its owner is made current first
+        char *dst = dptr_overwrite(t);
+        if (!dst) return 0;
+        const int rc = read_device(ctx, f_, dst, (size_t)bytes);
+        if (rc == 1) wrote_dev(t);
+        return rc;
+    }
+
+  private:
+    FILE *f_;
+    uint32_t count_ = 0;
+};
+
+// The requested tensors by name.  A name asked for twice takes the file's entries from its last
+// request backwards, as the reference's lookup does.
+class Wanted {
+  public:
+    Wanted(int n, const char *const *names) : done_((size_t)(n > 0 ? n : 0), 0) {
+        for (int i = 0; i < n; i++) by_name_[names[i]].push_back(i);
+    }
+    int claim(const std::string &name) {  // the index an entry of this name fills, or -1
+        auto it = by_name_.find(name);
+        if (it == by_name_.end()) return -1;
+        for (auto k = it->second.rbegin(); k != it->second.rend(); ++k)
+            if (!done_[(size_t)*k]) return *k;
+        return -1;
+    }
+    void fill(int i) { done_[(size_t)i] = 1; }
+    int first_missing() const {
+        for (size_t i = 0; i < done_.size(); i++)
+            if (!done_[i]) return (int)i;
+        return -1;
+    }
+
+  private:
+    std::unordered_map<std::string, std::vector<int>> by_name_;
+    std::vector<char> done_;
+};
+
+// Why entry h cannot go into t, as the reference reports it (NC_OK when it can).
+static nc_status check_entry(nc_ctx *ctx, const char *path, const EntryHeader &h, const nc_tensor *t) {
+    const Dims want = Dims::of(t);
+    bool same = t->dtype == (nc_dtype)h.dtype && want.rank == h.dims.rank;
+    for (int d = 0; same && d < want.rank; d++) same = want.e[d] == h.dims.e[d];
+    if (!same) {
+        char tw[96], tg[96];
+        error(ctx, NC_ERR_SHAPE, "nc_load: '%s' is %s %s in the file but %s %s in the model", h.name.c_str(),
+              dtype_name((nc_dtype)h.dtype), h.dims.text(tg, sizeof tg), dtype_name(t->dtype), want.text(tw, sizeof tw));
+        return NC_ERR_SHAPE;
+    }
+    // the byte count must be exactly the tensor's size: a larger one would overrun the storage
+    if (h.bytes != (uint64_t)want.numel() * dtype_size(t->dtype)) {
+        error(ctx, NC_ERR_ARG, "nc_load: '%s' in '%s' is corrupt (%llu data bytes for %s)", h.name.c_str(), path,
+              (unsigned long long)h.bytes, dtype_name(t->dtype));
+        return NC_ERR_ARG;
+    }
+    return NC_OK;
+}
+
+static nc_status load_entries(nc_ctx *ctx, const char *path, NcwReader &rd, Wanted &wanted, nc_tensor *const *tensors) {
+    EntryHeader h;
+    for (uint32_t e = 0; e < rd.count(); e++) {
+        if (!rd.next(h)) {
+            error(ctx, NC_ERR_ARG, "nc_load: '%s' is truncated or corrupt", path);
+            return ctx->status;
+        }
+        const int idx = wanted.claim(h.name);
+        if (idx < 0) {
+            if (!rd.skip(h.bytes)) {
+                error(ctx, NC_ERR_ARG, "nc_load: '%s' is truncated", path);
+                return ctx->status;
+            }
+            continue;
+        }
+        nc_tensor *t = tensors[idx];
+        if (check_entry(ctx, path, h, t) != NC_OK) return ctx->status;
+        const int rc = nc_is_contiguous(t) ? rd.read_into(ctx, t, h.bytes) : 0;
+        if (rc < 0) return ctx->status;  // the device error is recorded
+        if (rc == 0) {
+            error(ctx, NC_ERR_ARG, "nc_load: cannot read '%s' (truncated file or non-contiguous tensor)", h.name.c_str());
+            return ctx->status;
+        }
+        wanted.fill(idx);
+    }
+    return NC_OK;
+}
+
 }  // namespace nce
 
 using namespace nce;
@@ -154,27 +306,20 @@ extern "C" {
 
 nc_status nc_save(nc_ctx *ctx, const char *path, int n, const char *const *names, nc_tensor *const *tensors) {
     if (ctx->status != NC_OK) return ctx->status;
-    for (int i = 0; i < n; i++) {
+    for (int i = 0; i < n; i++)
         if (!tensors[i] || !names[i]) {
             error(ctx, NC_ERR_ARG, "nc_save: entry %d has a NULL name or tensor", i);
             return ctx->status;
         }
-    }
     FILE *f = fopen(path, "wb");
     if (!f) {
         error(ctx, NC_ERR_ARG, "nc_save: cannot open '%s' for writing", path);
         return ctx->status;
     }
-    const uint32_t version = kFileVersion, count = (uint32_t)n;
-    bool ok = put(f, "NCW1", 4) && put(f, &version, 4) && put(f, &count, 4);
-    for (int i = 0; ok && i < n; i++) {
-        nc_tensor *t = tensors[i];
-        const uint32_t len = (uint32_t)strlen(names[i]), dt = (uint32_t)t->dtype, nd = (uint32_t)t->ndim;
-        const uint64_t bytes = (uint64_t)nc_numel(t) * dtype_size(t->dtype);
-        ok = put(f, &len, 4) && put(f, names[i], len) && put(f, &dt, 4) && put(f, &nd, 4) &&
-             put(f, t->shape, sizeof(int64_t) * nd) && put(f, &bytes, 8) && write_tensor(ctx, f, t, (size_t)bytes);
-    }
-    if (fclose(f) != 0) ok = false;
+    NcwWriter w(ctx, f);
+    bool ok = w.header((uint32_t)n);
+    for (int i = 0; ok && i < n; i++) ok = w.entry(names[i], tensors[i]);
+    ok = fclose(f) == 0 && ok;
     if (!ok && ctx->status == NC_OK) error(ctx, NC_ERR_ARG, "nc_save: write to '%s' failed", path);
     return ctx->status;
 }
@@ -186,83 +331,11 @@ nc_status nc_load(nc_ctx *ctx, const char *path, int n, const char *const *names
         error(ctx, NC_ERR_ARG, "nc_load: cannot open '%s'", path);
         return ctx->status;
     }
-    std::vector<unsigned char> found((size_t)(n > 0 ? n : 1), 0);
-    std::vector<char> name(kMaxName + 1);
-    char magic[4];
-    uint32_t version = 0, count = 0;
-    if (!get(f, magic, 4) || memcmp(magic, "NCW1", 4) != 0 || !get(f, &version, 4) || !get(f, &count, 4)) {
-        error(ctx, NC_ERR_ARG, "nc_load: '%s' is not an NCW1 tensor file", path);
-        fclose(f);
-        return ctx->status;
-    }
-    if (version != kFileVersion) {
-        error(ctx, NC_ERR_ARG, "nc_load: '%s' has unsupported version %u", path, version);
-        fclose(f);
-        return ctx->status;
-    }
-    for (uint32_t e = 0; e < count; e++) {
-        uint32_t len, dt, nd;
-        int64_t shape[NC_MAX_DIMS];
-        uint64_t bytes;
-        if (!get(f, &len, 4) || len > kMaxName || !get(f, name.data(), len) || !get(f, &dt, 4) || !get(f, &nd, 4) ||
-            nd > NC_MAX_DIMS || !get(f, shape, sizeof(int64_t) * nd) || !get(f, &bytes, 8)) {
-            error(ctx, NC_ERR_ARG, "nc_load: '%s' is truncated or corrupt", path);
-            break;
-        }
-        name[len] = '\0';
-        int idx = -1;
-        for (int i = 0; i < n; i++)
-            if (!found[i] && strcmp(names[i], name.data()) == 0) idx = i;
-        if (idx < 0) {
-            if (fseeko(f, (off_t)bytes, SEEK_CUR) != 0) {
-                error(ctx, NC_ERR_ARG, "nc_load: '%s' is truncated", path);
-                break;
-            }
-            continue;
-        }
-        nc_tensor *t = tensors[idx];
-        bool same = t->dtype == (nc_dtype)dt && t->ndim == (int)nd;
-        for (uint32_t d = 0; same && d < nd; d++) same = t->shape[d] == shape[d];
-        if (!same) {
-            char want[96], got[96];
-            error(ctx, NC_ERR_SHAPE, "nc_load: '%s' is %s %s in the file but %s %s in the model", name.data(),
-                  dtype_name((nc_dtype)dt), shape_str((int)nd, shape, got, sizeof got), dtype_name(t->dtype),
-                  shape_str(t->ndim, t->shape, want, sizeof want));
-            break;
-        }
-        // the byte count must be exactly the tensor's size: a larger one would overrun the storage
-        if (bytes != (uint64_t)nc_numel(t) * dtype_size(t->dtype)) {
-            error(ctx, NC_ERR_ARG, "nc_load: '%s' in '%s' is corrupt (%llu data bytes for %s)", name.data(), path,
-                  (unsigned long long)bytes, dtype_name(t->dtype));
-            break;
-        }
-        bool ok = nc_is_contiguous(t);
-        if (ok && bytes) {
-            if (ctx->device >= 0) {
-                // every byte of t is about to be written; the rest of its owner is made current first
-                char *dst = dptr_overwrite(t);
-                const int rc = dst ? read_device(ctx, f, dst, (size_t)bytes) : 0;
-                if (rc < 0) break;
-                ok = rc == 1;
-                if (ok) wrote_dev(t);
-            } else {
-                char *h = hptr(t, true);
-                ok = h && get(f, h, (size_t)bytes);
-            }
-        }
-        if (!ok) {
-            error(ctx, NC_ERR_ARG, "nc_load: cannot read '%s' (truncated file or non-contiguous tensor)", name.data());
-            break;
-        }
-        found[idx] = 1;
-    }
-    if (ctx->status == NC_OK) {
-        for (int i = 0; i < n; i++) {
-            if (!found[i]) {
-                error(ctx, NC_ERR_ARG, "nc_load: '%s' not found in '%s'", names[i], path);
-                break;
-            }
-        }
+    NcwReader rd(f);
+    Wanted wanted(n, names);
+    if (rd.open(path, ctx) && load_entries(ctx, path, rd, wanted, tensors) == NC_OK) {
+        const int miss = wanted.first_missing();
+        if (miss >= 0) error(ctx, NC_ERR_ARG, "nc_load: '%s' not found in '%s'", names[miss], path);
     }
     fclose(f);
     return ctx->status;
