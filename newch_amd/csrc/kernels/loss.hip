@@ -10,9 +10,10 @@
 // same 12.
 //
 // cross entropy forward, one wave per row with the row in registers (C % 4 == 0, C <= 4096, 16-byte
-// aligned): the max, the fp64 row sum of exp(x - m) (hardware exponential: the sum is only compared at
-// the reductions' tolerance), logf, and the label's log-probability added to the holding lane's fp64
-// accumulator.  The next row is loaded before the current one is reduced.  Other
+// aligned): the max, the row sum of exp(x - m) (hardware exponential: the sum is only compared at the
+// reductions' tolerance), logf, and the label's log-probability (its logit read back as one uniform
+// load rather than picked out of the registers) added to lane 0's fp64 accumulator.  The next row is
+// loaded before the current one is reduced.  Other
 // shapes: one workgroup per row, the same arithmetic over the (L2-resident) row.
 //
 // Loss sums: fp64 per lane (or per thread), wave sums, workgroup partials added in wave order, and
@@ -77,20 +78,14 @@ __device__ __forceinline__ void ce_fwd_rows(const float *__restrict__ x, const i
         for (int k = 0; k < VPL; k++)
             if (lane + k * kWave < nv) v[k] = __builtin_nontemporal_load(xr + lane + k * kWave);
     };
-    double acc = 0.0;  // log-probabilities of the labels this lane holds
+    // the label's logit, one wave-uniform 4-byte load (the row is in cache); an out-of-range label
+    // reads column 0 and is not used
+    auto label_logit = [&](int64_t r, int32_t L) {
+        return x[r * C + (L >= 0 && L < C ? L : 0)];
+    };
+    double acc = 0.0;  // lane 0: the negated log-probabilities of this wave's labels
     unsigned long long mybad = kNoBad;  // first row with an out-of-range label among this wave's
-    const int64_t r0 = ((int64_t)blockIdx.x * kLB + threadIdx.x) / kWave;
-    f4 v[VPL], vn[VPL];
-    int32_t L = 0, Ln = 0;
-    if (r0 < N) {
-        load(r0, v);
-        L = lab[r0];
-    }
-    for (int64_t r = r0; r < N; r += stride) {
-        if (r + stride < N) {
-            load(r + stride, vn);
-            Ln = lab[r + stride];
-        }
+    auto row = [&](int64_t r, const f4 *v, int32_t L, float xl) {
         const bool ok = L >= 0 && L < C;
         if (!ok) mybad = bad_key(r, L) < mybad ? bad_key(r, L) : mybad;
         float m = -__builtin_inff();
@@ -101,28 +96,54 @@ __device__ __forceinline__ void ce_fwd_rows(const float *__restrict__ x, const i
         }
         m = wave_max_nan_skip(m);
         m = row_max_finish(m, lane0_f32(v[0].x));  // lane 0 holds the row's first element
-        // each lane's terms (at most 64, each in (0, 1]) in fp32, the 64 lane sums in fp64
+        // exp(x - m) as exp2(x log2e - m log2e), one fused multiply-add per element; each lane's terms
+        // (at most 64, each in (0, 1]) in fp32, the 64 lane sums in fp64
+        const float ml = m * NC_K_LOG2E;
         float s = 0.0f;
 #pragma unroll
         for (int k = 0; k < VPL; k++) {
             if (lane + k * kWave < nv)
-                s += (exp_sum_term(v[k].x - m) + exp_sum_term(v[k].y - m)) +
-                     (exp_sum_term(v[k].z - m) + exp_sum_term(v[k].w - m));
+                s += (__builtin_amdgcn_exp2f(fma_(v[k].x, NC_K_LOG2E, -ml)) +
+                      __builtin_amdgcn_exp2f(fma_(v[k].y, NC_K_LOG2E, -ml))) +
+                     (__builtin_amdgcn_exp2f(fma_(v[k].z, NC_K_LOG2E, -ml)) +
+                      __builtin_amdgcn_exp2f(fma_(v[k].w, NC_K_LOG2E, -ml)));
         }
         const float ls = logf((float)wave_sum((double)s));
-        if (ok) {  // the lane holding column L adds its log-probability
-#pragma unroll
-            for (int k = 0; k < VPL; k++) {
-                if (lane + k * kWave == (L >> 2)) {
-                    const float xl = (L & 3) == 0 ? v[k].x : (L & 3) == 1 ? v[k].y : (L & 3) == 2 ? v[k].z : v[k].w;
-                    acc -= (double)((xl - m) - ls);
-                }
-            }
+        if (lane == 0) {
+            stats[r] = f2{m, ls};
+            if (ok) acc -= (double)((xl - m) - ls);
         }
-        if (lane == 0) stats[r] = f2{m, ls};
-#pragma unroll
-        for (int k = 0; k < VPL; k++) v[k] = vn[k];
-        L = Ln;
+    };
+    // rows r0, r0 + stride, ... through two register sets in turn.  In the steady state every load is
+    // unconditional and issued in this order: the current row's label logit, then the next row and its
+    // label, so the waits for the current row never cover the next row's loads.
+    int64_t r = ((int64_t)blockIdx.x * kLB + threadIdx.x) / kWave;
+    f4 va[VPL], vb[VPL];
+    int32_t la = 0, lb = 0;
+    if (r < N) {
+        load(r, va);
+        la = lab[r];
+    }
+    while (r + 2 * stride < N) {
+        const float xa = label_logit(r, la);
+        load(r + stride, vb);
+        lb = lab[r + stride];
+        row(r, va, la, xa);
+        const float xb = label_logit(r + stride, lb);
+        load(r + 2 * stride, va);
+        la = lab[r + 2 * stride];
+        row(r + stride, vb, lb, xb);
+        r += 2 * stride;
+    }
+    if (r < N) {
+        const float xa = label_logit(r, la);
+        const bool more = r + stride < N;
+        if (more) {
+            load(r + stride, vb);
+            lb = lab[r + stride];
+        }
+        row(r, va, la, xa);
+        if (more) row(r + stride, vb, lb, label_logit(r + stride, lb));
     }
     const double t = block_sum_ordered(acc);
     const unsigned long long kb = block_min_key(mybad);
