@@ -15,8 +15,8 @@
 // 0-31 with k 0-15, lanes 32-63 the same rows with k 16-31) for A and for B alike, so whatever order
 // the instruction sums a lane's bytes in, A and B pair the same k.  Large problems run 256 x 256
 // tiles (8 waves of 4 x 2 MFMA tiles, BK 128, 147 KiB of LDS), smaller ones 128 x 128 (4 waves of
-// 2 x 2, BK 64).  Large problems with K a multiple of 64 and 16-byte aligned rows take k_qgemm_dma
-// instead: the same tile, its panels loaded straight into LDS three k steps ahead.
+// 2 x 2, BK 64).  Large problems with K a multiple of 128 and 16-byte aligned rows take k_qgemm_dma
+// instead: the same tile, its panels loaded straight into LDS one 128-byte k step ahead.
 // Blocks are remapped so each XCD (blocks b with b % 8 equal) works a contiguous run of tiles, and
 // tiles run in groups of 8 tile-rows so neighbouring blocks share panels in L2.
 //
@@ -182,27 +182,39 @@ __global__ __launch_bounds__(C::NT, C::OCC) void k_qgemm(QgArgs p) {
 }
 
 // ------------------------------------------------------------------------------------------------
-// Deep-prefetch variant for large aligned problems (K a multiple of 64, 16-byte aligned rows): the
+// Direct-to-LDS variant for large aligned problems (K a multiple of 128, 16-byte aligned rows): the
 // same 256 x 256 tile and 8 waves of 4 x 2 MFMA tiles, but the A and B panels go straight from global
-// memory into LDS (global_load_lds_dwordx4: lane i's 16 bytes land at M0 + 16 i) three k steps ahead,
-// through four 32 KiB stages.  No staging registers and no LDS write instructions; one barrier per k
-// step.  Rows are 64 bytes without padding; logical 16-byte chunk c of row r sits at chunk
-// c ^ ((r >> 2) & 3), so the fragment reads of 16 consecutive rows hit distinct banks and every load
-// instruction still fills 1 KiB of consecutive LDS (16 rows).  Rows past M or N load row M-1 / N-1
+// memory into LDS (global_load_lds_dwordx4: lane i's 16 bytes land at M0 + 16 i) one k step ahead,
+// through two 64 KiB stages of 128 k-bytes.  No staging registers and no LDS write instructions; one
+// barrier per k step.  Rows are 128 bytes (whole cache lines: 64-byte row segments, four 32 KiB
+// stages three steps ahead, ran 4-6% slower) without padding; logical 16-byte chunk c of row r sits at
+// chunk c ^ ((r >> 1) & 7), so the fragment reads of 16 consecutive rows hit distinct banks and every
+// load instruction still fills 1 KiB of consecutive LDS (8 rows).  Rows past M or N load row M-1 / N-1
 // (in bounds; those accumulators are never stored).  The loads are issued from inline assembly so
 // the compiler does not wait for them before every LDS read; the waits are explicit vmcnt counts.
-constexpr int kDmaBK = 64, kDmaRows = 256, kDmaNT = 512;
+#ifndef QG_BK
+#define QG_BK 128
+#endif
+constexpr int kDmaBK = QG_BK, kDmaRows = 256, kDmaNT = 512;
+constexpr int kDmaChunks = kDmaBK / 16;        // 16-byte chunks per staged row
+constexpr int kDmaRowsPerLoad = 1024 / kDmaBK;  // rows one 1 KiB load instruction fills
 constexpr int kDmaStage = 2 * kDmaRows * kDmaBK;  // A rows, then B rows
-constexpr size_t kDmaLds = 4 * (size_t)kDmaStage;
+#ifndef QG_STAGES
+#define QG_STAGES 2
+#endif
+constexpr int kDmaStages = QG_STAGES;  // LDS stages; kDmaStages - 1 in flight ahead of the one in use
+constexpr size_t kDmaLds = kDmaStages * (size_t)kDmaStage;
 
-__device__ __forceinline__ int dma_swz(int row, int c) { return (c ^ ((row >> 2) & 3)) * 16; }
+__device__ __forceinline__ int dma_swz(int row, int c) {
+    return kDmaChunks == 4 ? (c ^ ((row >> 2) & 3)) * 16 : (c ^ ((row >> 1) & 7)) * 16;
+}
 
 
 template <bool OUT_F32>
 __global__ __launch_bounds__(kDmaNT, 1) void k_qgemm_dma(QgArgs p) {
     extern __shared__ __attribute__((aligned(16))) int8_t smem[];
     constexpr int kTM = 4, kTN = 2, kWGN = 4;
-    constexpr int kLoads = 32 / (kDmaNT / kWave);  // 1 KiB load instructions per wave per k step (32 per stage)
+    constexpr int kLoads = (2 * kDmaRows / kDmaRowsPerLoad) / (kDmaNT / kWave);  // 1 KiB loads per wave per stage
 
     int id = blockIdx.x;
     const int nblk = gridDim.x;
@@ -223,15 +235,17 @@ __global__ __launch_bounds__(kDmaNT, 1) void k_qgemm_dma(QgArgs p) {
     uint32_t loff[kLoads];
 #pragma unroll
     for (int q = 0; q < kLoads; q++) {
-        const int blk = wid * kLoads + q, panel = blk >> 4, r16 = (blk & 15) * 16, row = r16 + (lane >> 2);
-        const int c = (lane & 3) ^ ((row >> 2) & 3);
+        constexpr int kBlocks = kDmaRows / kDmaRowsPerLoad;  // load blocks per panel
+        const int blk = wid * kLoads + q, panel = blk / kBlocks, rb = (blk % kBlocks) * kDmaRowsPerLoad;
+        const int row = rb + lane / kDmaChunks;
+        const int c = dma_swz(row, lane % kDmaChunks) / 16;  // the chunk that belongs at this lane's place
         const int64_t grow = panel == 0 ? min(m0 + row, p.M - 1) : min(n0 + row, p.N - 1);
         src[q] = (panel == 0 ? p.A + grow * p.lda : p.B + grow * p.ldb) + c * 16;
-        loff[q] = (uint32_t)(panel * kDmaRows * kDmaBK + r16 * kDmaBK);
+        loff[q] = (uint32_t)(panel * kDmaRows * kDmaBK + rb * kDmaBK);
     }
     const uint32_t sbase = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) int8_t *)smem;
     auto issue = [&](int kt) {
-        const uint32_t st = sbase + (uint32_t)(kt & 3) * kDmaStage;
+        const uint32_t st = sbase + (uint32_t)(kt % kDmaStages) * kDmaStage;
 #pragma unroll
         for (int q = 0; q < kLoads; q++)
             dma16(src[q] + (int64_t)kt * kDmaBK, __builtin_amdgcn_readfirstlane(st + loff[q]));
@@ -244,18 +258,19 @@ __global__ __launch_bounds__(kDmaNT, 1) void k_qgemm_dma(QgArgs p) {
         for (int j = 0; j < kTN; j++) acc[i][j] = i16v{};
 
     const int nk = p.K / kDmaBK;
-    for (int kt = 0; kt < 3 && kt < nk; kt++) issue(kt);
+    for (int kt = 0; kt < kDmaStages - 1 && kt < nk; kt++) issue(kt);
     const int frow = lane & 31, fhalf = lane >> 5;
     for (int kt = 0; kt < nk; kt++) {
         // this wave's loads of step kt are done once at most 4 per later step in flight remain
-        const int ahead = min(nk - 1 - kt, 2);
-        if (ahead == 2) asm volatile("s_waitcnt vmcnt(%0)" ::"n"(2 * kLoads) : "memory");
+        const int ahead = min(nk - 1 - kt, kDmaStages - 2);
+        if (ahead == 3) asm volatile("s_waitcnt vmcnt(%0)" ::"n"(3 * kLoads) : "memory");
+        else if (ahead == 2) asm volatile("s_waitcnt vmcnt(%0)" ::"n"(2 * kLoads) : "memory");
         else if (ahead == 1) asm volatile("s_waitcnt vmcnt(%0)" ::"n"(kLoads) : "memory");
         else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         __builtin_amdgcn_s_barrier();  // every wave's loads of step kt have landed; step kt-1's reads are done
         asm volatile("" ::: "memory");
-        if (kt + 3 < nk) issue(kt + 3);  // into the stage step kt-1 used
-        const int8_t *cur = smem + (kt & 3) * kDmaStage;
+        if (kt + kDmaStages - 1 < nk) issue(kt + kDmaStages - 1);  // into the stage step kt-1 used
+        const int8_t *cur = smem + (kt % kDmaStages) * kDmaStage;
 #pragma unroll
         for (int s = 0; s < kDmaBK / 32; s++) {
             const int c = s * 2 + fhalf;

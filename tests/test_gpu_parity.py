@@ -1399,9 +1399,9 @@ def test_engine_linear_int8_errors(eng):
 
 S8_SIZES = [(1, 1, 16), (5, 6, 37), (128, 128, 64), (300, 260, 1040), (257, 129, 1000), (33, 517, 80), (7, 3, 0),
             (2048, 1024, 4096),
-            # >= 256 tiles of 256 x 256: the deep-prefetch kernel (K % 64 == 0; partial edge tiles) and,
-            # with K % 64 != 0, the register-staged 256 x 256 kernel
-            (4100, 4000, 512), (4096, 4352, 1040)]
+            # >= 256 tiles of 256 x 256: the direct-to-LDS kernel (K % 128 == 0; partial edge tiles) and,
+            # with K % 128 != 0, the register-staged 256 x 256 kernel
+            (4100, 4000, 512), (4096, 4352, 1040), (4096, 4096, 576)]
 
 
 def _rows_sample(M, n=48, seed=0):
