@@ -396,6 +396,7 @@ void nc_free_ctx(nc_ctx *ctx) {
     nc_step_end(ctx);
     while (!ctx->optims.empty()) nc_optim_free(ctx->optims.back());
     if (ctx->io_stage) (void)hipHostFree(ctx->io_stage);
+    if (ctx->loss_flag) (void)hipHostFree(ctx->loss_flag);
     for (nc_tensor *t : ctx->persistent) {
         if (t->dev && (t->flags & TF_OWNS_DATA)) (void)hipFree(t->dev);
         free(t->host);

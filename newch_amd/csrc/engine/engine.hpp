@@ -200,6 +200,8 @@ struct nc_ctx {
 
     std::vector<nc_optim *> optims;  // live optimizers, freed at nc_free_ctx
     char *io_stage = nullptr;        // pinned staging for NCW1 file I/O (two halves), allocated on first use
+    uint64_t *loss_flag = nullptr;   // pinned, device-mapped word: the loss forwards' first-bad-label key
+    uint64_t *loss_flag_dev = nullptr;  // the same word as the kernels address it
 
     uint64_t device_allocs = 0;  // hipMalloc calls made for this context (arena chunks, large blocks, persistent)
     bool poison = false;         // NC_DEBUG_POISON: released device blocks are filled with 0xCD

@@ -148,6 +148,28 @@ static nc_status loss_shape(nc_node *n, OutSpec &out) {
     return NC_OK;
 }
 
+// The loss forwards' bad-label key lands in a pinned host word the kernel writes directly (mapped
+// into the device's address space), so the host reads it after the stream synchronisation the
+// reference's synchronous error needs anyway, with no device-to-host copy.  Null when the host
+// allocation is refused: the key then goes through arena memory and a copy.
+static uint64_t *loss_flag_dev(nc_ctx *ctx) {
+    if (!ctx->loss_flag) {
+        void *h = nullptr, *d = nullptr;
+        if (hipHostMalloc(&h, sizeof(uint64_t), hipHostMallocMapped | hipHostMallocPortable) != hipSuccess || !h) {
+            (void)hipGetLastError();
+            return nullptr;
+        }
+        if (hipHostGetDevicePointer(&d, h, 0) != hipSuccess || !d) {
+            (void)hipGetLastError();
+            (void)hipHostFree(h);
+            return nullptr;
+        }
+        ctx->loss_flag = (uint64_t *)h;
+        ctx->loss_flag_dev = (uint64_t *)d;
+    }
+    return ctx->loss_flag_dev;
+}
+
 static nc_status loss_fwd(nc_node *n) {
     nc_tensor *xt = n->in[0], *yt = n->in[1];
     nc_ctx *ctx = xt->ctx;
@@ -162,7 +184,8 @@ static nc_status loss_fwd(nc_node *n) {
     char *saved = (char *)save_state(n, sbytes);
     const size_t ws_bytes = nc_hip_loss_workspace(N, C);
     char *ws = arena_alloc(ctx, ws_bytes ? ws_bytes : 8);
-    uint64_t *bad = (uint64_t *)arena_alloc(ctx, sizeof(uint64_t));
+    uint64_t *const mapped = loss_flag_dev(ctx);
+    uint64_t *bad = mapped ? mapped : (uint64_t *)arena_alloc(ctx, sizeof(uint64_t));
     if (!saved || !ws || !bad) return NC_ERR_STATE;
     float *stats = ce ? (float *)saved : nullptr;
     int32_t *lab = (int32_t *)(saved + pbytes);
@@ -173,9 +196,10 @@ static nc_status loss_fwd(nc_node *n) {
                       : nc_hip_nll_loss_fwd(N, C, x, lab, (int)n->p.i[0], loss, bad, ws, ws_bytes, stream(ctx));
     if (!hip_layer_ok(ctx, rc, n->op->name)) return NC_ERR_STATE;
     uint64_t hb = 0;
-    if (!hip_ok(ctx, hipMemcpyAsync(&hb, bad, sizeof hb, hipMemcpyDeviceToHost, stream(ctx)), n->op->name) ||
-        !hip_ok(ctx, hipStreamSynchronize(stream(ctx)), n->op->name))
+    if (!mapped && !hip_ok(ctx, hipMemcpyAsync(&hb, bad, sizeof hb, hipMemcpyDeviceToHost, stream(ctx)), n->op->name))
         return NC_ERR_STATE;
+    if (!hip_ok(ctx, hipStreamSynchronize(stream(ctx)), n->op->name)) return NC_ERR_STATE;
+    if (mapped) hb = *(volatile const uint64_t *)ctx->loss_flag;
     if (hb != ~(uint64_t)0) {
         error(ctx, NC_ERR_ARG, "%s: label %d at row %lld outside [0, %lld)", n->op->name, (int32_t)(uint32_t)hb,
               (long long)(hb >> 32), (long long)C);
