@@ -187,7 +187,9 @@ class BackwardPass {
     bool reach() {
         const std::vector<nc_node *> &tape = ctx_->tape;
         std::vector<char> on(tape.size(), 0);
-        if (loss_->node) on[loss_->node->seq] = 1;
+        // a node of this step's tape (a tensor kept past nc_step_end carries a stale one)
+        auto taped = [&](const nc_node *n) { return n && n->seq < tape.size() && tape[n->seq] == n; };
+        if (taped(loss_->node)) on[loss_->node->seq] = 1;
         for (size_t k = tape.size(); k-- > 0;) {
             if (!on[k]) continue;
             nc_node *n = tape[k];
@@ -200,7 +202,7 @@ class BackwardPass {
             live_.push_back(n);
             for (int i = 0; i < n->n_in; i++) {
                 const nc_tensor *x = n->in[i];
-                if (x->node && needs_grad(x)) on[x->node->seq] = 1;
+                if (taped(x->node) && needs_grad(x)) on[x->node->seq] = 1;
             }
         }
         return true;
