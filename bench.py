@@ -41,7 +41,8 @@ PEAK_I8_TOPS = 5000.0     # MI355X dense int8 matrix
 METRIC = "achieved HBM GB/s (% of MI355X peak) per op class; elements/s vs host CPU"
 ACTS = ["gelu", "silu", "sigmoid", "tanh", "hardswish", "relu6"]
 N_UNARY = 1 << 28
-TIMED = 5  # timed launches per op class (after one warm launch)
+TIMED = 10  # timed launches per op class (the median is reported)
+WARM = 2  # untimed launches of each op class first
 FLUSH_KERNEL = "k_fill16"  # the 1 GiB cache-flush fill between timed launches
 
 
@@ -340,17 +341,18 @@ GEMM_LABELS = ["linear_fwd_sgemm_nt", "linear_bwd_dx_sgemm_nn", "linear_bwd_dw_s
 
 
 def run_group(K, hm, builder, labels=None, setup_only=False):
-    """One warm launch of each op class, then TIMED launches each after a 1 GiB fill that evicts the
-    256 MB MALL (outside the launch's events): a cold-cache median per class.  setup_only: build the
-    group's inputs and stop (the profiler pass whose counters are subtracted from the labels')."""
+    """WARM untimed launches of each op class, then TIMED launches each after a 1 GiB fill that evicts
+    the 256 MB MALL (outside the launch's events): a cold-cache median per class.  setup_only: build
+    the group's inputs and stop (the profiler pass whose counters are subtracted from the labels')."""
     work, keep = builder(K, hm)
     if setup_only:
         hm.synchronize()
         return {}
     if labels is not None:
         work = [w for w in work if w[0] in labels]
-    for w in work:
-        w[3]()
+    for _ in range(WARM):
+        for w in work:
+            w[3]()
     hm.synchronize()
     flush = hm.DeviceBuffer(1 << 30)
     tl = Timeline(hm)
@@ -368,8 +370,9 @@ def run_gemm(K, hm, labels=None):
     work, keep = group_gemm(K, hm)
     if labels is not None:
         work = [w for w in work if w[0] in labels]
-    for w in work:
-        w[3]()
+    for _ in range(WARM):
+        for w in work:
+            w[3]()
     hm.synchronize()
     tl = Timeline(hm)
     for _ in range(TIMED):
@@ -453,7 +456,7 @@ def _pmc_counts(d: Path):
 def traffic_summary(root: Path) -> str:
     """root/<label>/{fetch,write}/: a `--only <label>` run under rocprofv3 --pmc FETCH_SIZE (WRITE_SIZE);
     root/_setup_<group>/{fetch,write}/: the same group built with --setup-only.  A label's traffic is
-    its run's dispatches minus its group's setup dispatches, divided by its launches (one warm +
+    its run's dispatches minus its group's setup dispatches, divided by its launches (WARM untimed +
     TIMED timed): KiB per launch, with the copy calibration's factors."""
     owner = {lab: g for g, (labels, _) in GROUPS.items() for lab in labels}
     owner.update({lab: "gemm" for lab in GEMM_LABELS})
@@ -470,7 +473,7 @@ def traffic_summary(root: Path) -> str:
                 kernels.append(k.replace("void ", "").replace("nchip::", ""))
             f += fv - bf
             w += wv - bw
-        per[d.name] = (f / (TIMED + 1), w / (TIMED + 1), sorted(kernels))
+        per[d.name] = (f / (WARM + TIMED), w / (WARM + TIMED), sorted(kernels))
     lines = []
     cal = per.get("copy_calibration")
     if cal and cal[0] and cal[1]:
@@ -478,7 +481,7 @@ def traffic_summary(root: Path) -> str:
         lines += [f"fetch_scale {cal[0] / kib:.4f}", f"write_scale {cal[1] / kib:.4f}"]
     lines.append(f"{'label':32s} {'launches':>8s} {'FETCH_KiB':>14s} {'WRITE_KiB':>14s}  kernels")
     for label, (f, w, ks) in per.items():
-        lines.append(f"{label:32s} {TIMED + 1:8d} {f:14.1f} {w:14.1f}  {', '.join(ks)}")
+        lines.append(f"{label:32s} {WARM + TIMED:8d} {f:14.1f} {w:14.1f}  {', '.join(ks)}")
     return "\n".join(lines) + "\n"
 
 
@@ -550,8 +553,8 @@ def chain_latency(lib_path=None, iters: int = 200, warmup: int = 10, threads: in
 
 def engine_leg(K, hm, classes):
     """Op classes called through nc.h on device tensors, as the reference's Python layer calls them:
-    host wall time per call with the device synchronised, after a warm call (the arena then reuses its
-    blocks).  `kernel_us` is the same class's kernel time from `classes`."""
+    host wall time per call with the device synchronised, after WARM warm calls (the arena then reuses
+    its blocks).  `kernel_us` is the same class's kernel time from `classes`."""
     import ctypes
     from ctypes import c_float, c_void_p
 
@@ -606,7 +609,7 @@ def engine_leg(K, hm, classes):
     out = {}
     for label, fn in calls:
         ts = []
-        for r in range(1 + TIMED):
+        for r in range(WARM + TIMED):
             L.nc_synchronize(ctx)
             t0 = time.perf_counter()
             fn()
@@ -615,7 +618,7 @@ def engine_leg(K, hm, classes):
             check()
             L.nc_zero_grad(Xp)
             L.nc_step_end(ctx)
-        us = float(np.median(ts[1:])) * 1e6
+        us = float(np.median(ts[WARM:])) * 1e6
         k = classes.get(label if label != "cross_entropy_fwd_bwd" else "cross_entropy_fwd")
         entry = {"us": round(us, 1)}
         if k:
@@ -669,7 +672,7 @@ def cpu_baseline(classes):
 
 
 def only_mode(K, hm, labels, setup_only=False):
-    """Just the named op classes (one warm + TIMED timed launches each): the per-label profiler passes."""
+    """Just the named op classes (WARM untimed + TIMED timed launches each): the per-label profiler passes."""
     classes = {}
     for gname, (glabels, builder) in GROUPS.items():
         want = [x for x in glabels if x in labels]
