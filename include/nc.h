@@ -7,7 +7,7 @@
  * host-visible accessors (nc_data_f32, nc_item, nc_get, nc_copy_to, nc_print) synchronise and copy
  * back, host writes (nc_copy_from, writes through nc_data_f32) are uploaded before the next op.
  * Ops on the hot path run hand-written gfx950 kernels (include/nc_hip.h); the other ops of the
- * reference API exist as symbols and fail cleanly with NC_ERR_STATE ("not in this build").
+ * reference API exist as symbols and fail cleanly with NC_ERR_STATE ("not in this engine").
  *
  * Memory and error model as the reference: persistent tensors live until nc_free_ctx / nc_release;
  * temporaries live in the step arena (here a device bump arena) until nc_step_end; ops never abort,
@@ -204,7 +204,7 @@ NC_API void nc_clear_grad(nc_tensor *t);
 typedef nc_tensor *(*nc_scalar_fn)(nc_ctx *ctx, nc_tensor **inputs, void *user);
 NC_API float nc_gradcheck(nc_ctx *ctx, nc_scalar_fn fn, nc_tensor **inputs, int n_inputs, void *user, float eps);
 
-/* ---- modules and optimizers (reference nc.h:352-416; not in this build) ------------------------ */
+/* ---- modules and optimizers (reference nc.h:352-416; not in this engine) ------------------------ */
 typedef enum { NC_ACT_RELU, NC_ACT_SIGMOID, NC_ACT_TANH } nc_activation;
 NC_API nc_module *nc_linear(nc_ctx *ctx, int64_t in_features, int64_t out_features, int bias);
 NC_API nc_module *nc_act(nc_ctx *ctx, nc_activation kind);
@@ -237,7 +237,7 @@ NC_API void nc_optim_set_opts(nc_optim *o, nc_optim_opts opts);
 NC_API void nc_optim_set_accumulation(nc_optim *o, int steps);
 NC_API float nc_clip_grad_norm(nc_tensor **params, int n, float max_norm);
 
-/* ---- device extensions of this build (additive; the reference bindings never call them) -------- */
+/* ---- device extensions of this engine (additive; the reference bindings never call them) -------- */
 /* Number of visible HIP devices.  The device of a context is chosen at nc_init from the environment
  * variable NC_DEVICE ("hip:N" or "N", default 0) or later with nc_set_device (before any tensor). */
 NC_API int nc_device_count(void);

@@ -4,7 +4,7 @@ The engine library this package builds (``newch_amd/libnc.so``) exports the same
 reference engine's ``libnc.so`` (``engine/include/nc.h``), so one signature table binds either of
 them.  The table below covers every ``NC_API`` function of that header, which is a superset of the
 111 names the reference's Python bindings resolve at import (``newch/_lib.py:78-177``), plus the
-additive device functions this build exports (``nc_device_*``, ``nc_set_stream``...), which are
+additive device functions this engine exports (``nc_device_*``, ``nc_set_stream``...), which are
 bound only when present.
 
 Struct layouts (``Config``, ``MemStats``, ``CpuInfo``, ``OptimOpts``) are frozen by that ABI:
@@ -160,7 +160,7 @@ NC_SIGNATURES: dict[str, tuple] = {
     "nc_clip_grad_norm": (c_float, [PP, c_int, c_float]),
 }
 
-# Additive functions of this build (not in the reference ABI): device selection, stream hand-over,
+# Additive functions of this engine (not in the reference ABI): device selection, stream hand-over,
 # synchronisation, device pointers of tensors.  Declared in include/nc.h under "device extensions".
 NC_DEVICE_SIGNATURES: dict[str, tuple] = {
     "nc_device_count": (c_int, []),

@@ -36,7 +36,7 @@ bool hip_layer_ok(nc_ctx *ctx, int rc, const char *what) {
 
 bool need_device(nc_ctx *ctx, const char *what) {
     if (ctx->device >= 0) return true;
-    error(ctx, NC_ERR_STATE, "%s: no HIP device (this build computes on an MI355X only)", what);
+    error(ctx, NC_ERR_STATE, "%s: no HIP device (this engine computes on an MI355X only)", what);
     return false;
 }
 

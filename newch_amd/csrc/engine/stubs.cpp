@@ -1,4 +1,4 @@
-// The rest of the reference ABI (engine/include/nc.h) outside this build's hot path: convolution,
+// The rest of the reference ABI (engine/include/nc.h) outside this engine's hot path: convolution,
 // pooling, masking and modules.  Every symbol exists, so the
 // reference's ctypes bindings resolve all their names at import (newch/_lib.py:174-177), and every
 // call fails cleanly the reference way -- a sticky NC_ERR_STATE in the context and a NULL / error
@@ -8,13 +8,13 @@
 using namespace nce;
 
 static nc_tensor *absent(nc_tensor *any, const char *name) {
-    if (any) error(any->ctx, NC_ERR_STATE, "%s: not in this build (the MI355X engine runs the elementwise, "
+    if (any) error(any->ctx, NC_ERR_STATE, "%s: not in this engine (the MI355X engine runs the elementwise, "
                                           "reduction, normalization, loss, optimizer, linear-algebra and int8 ops)", name);
     return nullptr;
 }
 
 static void absent_ctx(nc_ctx *ctx, const char *name) {
-    if (ctx) error(ctx, NC_ERR_STATE, "%s: not in this build", name);
+    if (ctx) error(ctx, NC_ERR_STATE, "%s: not in this engine", name);
 }
 
 extern "C" {

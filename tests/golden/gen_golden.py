@@ -404,7 +404,7 @@ OPTIM_SHAPES = [(7,), (3, 5)]
 def optim_scenario(e, lib, cfg, W, Gs):
     """Runs one optimizer configuration on params initialised to W with upstream grads Gs[step][param]
     (loss = sum_i sum(p_i * G_i), so each step's grads are exactly G); returns per-step weights and
-    state.  `e` is any context wrapper with tensor / param / read (the reference's or this build's)."""
+    state.  `e` is any context wrapper with tensor / param / read (the reference's or this engine's)."""
     name, ctor, opts, inside, accum, steps = cfg
     params = [e.param(w) for w in W]
     arr = (ctypes.c_void_p * len(params))(*params)

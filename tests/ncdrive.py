@@ -1,6 +1,6 @@
 """Drives any library with the nc.h C ABI through ctypes, the way the reference's Python package
 drives its engine (newch/tensor.py over newch/_lib.py).  The same driver runs the compiled reference
-(oracle/_ref/libnc_ref.so) and this build's engine (newch_amd/libnc.so), so a test reads the same
+(oracle/_ref/libnc_ref.so) and the MI355X engine (newch_amd/libnc.so), so a test reads the same
 for both."""
 
 from __future__ import annotations

@@ -9,7 +9,7 @@ The reference's contracts pinned here:
     reference's CI runs every test that way;
   * a steady-state step allocates nothing new: the arena keeps its chunks and its large blocks within
     the peak budget (ctx.c:113-149, 320-339).
-The device selection (NC_DEVICE, nc_set_device) is this build's additive contract (include/nc.h).
+The device selection (NC_DEVICE, nc_set_device) is this engine's additive contract (include/nc.h).
 """
 
 import ctypes

@@ -1,4 +1,4 @@
-"""GPU parity: this build's HIP path against the reference's golden vectors and the CPU oracle.
+"""GPU parity: this engine's HIP path against the reference's golden vectors and the CPU oracle.
 
 Two levels:
   * through the nc.h C ABI (tests/ncdrive.Engine on newch_amd/libnc.so), replaying the calls that

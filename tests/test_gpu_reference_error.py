@@ -1,4 +1,4 @@
-"""The reference's own error beside this build's, on the reductions whose fp32 accumulation order
+"""The reference's own error beside this engine's, on the reductions whose fp32 accumulation order
 decides the result.
 
 For each case the same inputs go through the nc.h API of both engines (tests/ncdrive.Engine): this

@@ -110,10 +110,10 @@ def test_off_path_ops_report_not_in_this_build(eng):
     L = eng.lib
     a = eng.tensor(np.ones((1, 1, 2, 2), np.float32))
     assert not L.nc_conv2d(a, a, None, 1, 1, 0, 0)
-    assert L.nc_status_code(eng.ctx) == abi.ERR_STATE and b"not in this build" in L.nc_error(eng.ctx)
+    assert L.nc_status_code(eng.ctx) == abi.ERR_STATE and b"not in this engine" in L.nc_error(eng.ctx)
     L.nc_clear_error(eng.ctx)
     assert not L.nc_dropout(a, c_float(0.5))
-    assert b"not in this build" in L.nc_error(eng.ctx)
+    assert b"not in this engine" in L.nc_error(eng.ctx)
 
 
 def test_optimizer_argument_errors_match_reference(eng):
@@ -209,7 +209,7 @@ def test_shape_errors_match_reference(eng):
         want = _errors(ref, SHAPE_ERRORS)
     got = _errors(eng, SHAPE_ERRORS)
     for i, (w, g) in enumerate(zip(want, got)):
-        assert w == g, f"case {i}: reference {w}, this build {g}"
+        assert w == g, f"case {i}: reference {w}, this engine {g}"
 
 
 def _views(e: Engine):
@@ -350,4 +350,4 @@ def test_ncw1_errors_match_reference(eng, tmp_path):
         want = _io_errors(ref, tmp_path / "r")
     got = _io_errors(eng, tmp_path / "o")
     for i, (w, g) in enumerate(zip(want, got)):
-        assert w == g, f"case {i}: reference {w}, this build {g}"
+        assert w == g, f"case {i}: reference {w}, this engine {g}"
