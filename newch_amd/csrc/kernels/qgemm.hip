@@ -16,7 +16,7 @@
 // the instruction sums a lane's bytes in, A and B pair the same k.  Large problems run 256 x 256
 // tiles (8 waves of 4 x 2 MFMA tiles, BK 128, 147 KiB of LDS), smaller ones 128 x 128 (4 waves of
 // 2 x 2, BK 64).  Large problems with K a multiple of 128 and 16-byte aligned rows take k_qgemm_dma
-// instead: the same tile, its panels loaded straight into LDS one 128-byte k step ahead.
+// instead: the same tile over 16 waves, its panels loaded straight into LDS one 128-byte k step ahead.
 // Blocks are remapped so each XCD (blocks b with b % 8 equal) works a contiguous run of tiles, and
 // tiles run in groups of 8 tile-rows so neighbouring blocks share panels in L2.
 //
@@ -183,7 +183,9 @@ __global__ __launch_bounds__(C::NT, C::OCC) void k_qgemm(QgArgs p) {
 
 // ------------------------------------------------------------------------------------------------
 // Direct-to-LDS variant for large aligned problems (K a multiple of 128, 16-byte aligned rows): the
-// same 256 x 256 tile and 8 waves of 4 x 2 MFMA tiles, but the A and B panels go straight from global
+// same 256 x 256 tile, but over 16 waves of 2 x 2 MFMA tiles (64 x 64 each, 64 accumulator registers,
+// four waves per SIMD: a third more fragment reads per MFMA than 8 waves of 4 x 2, but their latency
+// hides behind the other waves' MFMAs, 4-10% faster), and the A and B panels go straight from global
 // memory into LDS (global_load_lds_dwordx4: lane i's 16 bytes land at M0 + 16 i) one k step ahead,
 // through two 64 KiB stages of 128 k-bytes.  No staging registers and no LDS write instructions; one
 // barrier per k step.  Rows are 128 bytes (whole cache lines: 64-byte row segments, four 32 KiB
@@ -195,7 +197,7 @@ __global__ __launch_bounds__(C::NT, C::OCC) void k_qgemm(QgArgs p) {
 #ifndef QG_BK
 #define QG_BK 128
 #endif
-constexpr int kDmaBK = QG_BK, kDmaRows = 256, kDmaNT = 512;
+constexpr int kDmaBK = QG_BK, kDmaRows = 256, kDmaNT = 1024;
 constexpr int kDmaChunks = kDmaBK / 16;        // 16-byte chunks per staged row
 constexpr int kDmaRowsPerLoad = 1024 / kDmaBK;  // rows one 1 KiB load instruction fills
 constexpr int kDmaStage = 2 * kDmaRows * kDmaBK;  // A rows, then B rows
@@ -213,8 +215,10 @@ __device__ __forceinline__ int dma_swz(int row, int c) {
 template <bool OUT_F32>
 __global__ __launch_bounds__(kDmaNT, 1) void k_qgemm_dma(QgArgs p) {
     extern __shared__ __attribute__((aligned(16))) int8_t smem[];
-    constexpr int kTM = 4, kTN = 2, kWGN = 4;
+    constexpr int kTM = 2, kTN = 2, kWGN = 4;
     constexpr int kLoads = (2 * kDmaRows / kDmaRowsPerLoad) / (kDmaNT / kWave);  // 1 KiB loads per wave per stage
+    static_assert(kTM * 32 * (kDmaNT / kWave / kWGN) == kDmaRows && kTN * 32 * kWGN == kDmaRows,
+                  "the waves' MFMA tiles cover the workgroup tile");
 
     int id = blockIdx.x;
     const int nblk = gridDim.x;
@@ -229,8 +233,8 @@ __global__ __launch_bounds__(kDmaNT, 1) void k_qgemm_dma(QgArgs p) {
     const int t = threadIdx.x, lane = t & (kWave - 1), wid = t / kWave;
     const int wm = wid / kWGN, wn = wid % kWGN;
 
-    // the stage holds 32 blocks of 16 rows (A rows 0-255, then B rows 0-255); wave wid loads blocks
-    // wid * kLoads .. wid * kLoads + kLoads - 1
+    // the stage holds 64 blocks of 8 rows (one 1 KiB load each: A rows 0-255, then B rows 0-255);
+    // wave wid loads blocks wid * kLoads .. wid * kLoads + kLoads - 1
     const int8_t *src[kLoads];
     uint32_t loff[kLoads];
 #pragma unroll
