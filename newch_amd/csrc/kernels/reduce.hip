@@ -122,15 +122,45 @@ __global__ __launch_bounds__(kRB) void k_rows_wave(const float *__restrict__ x, 
             auto process = [&](int64_t o, const f4 *q) {
                 Acc<KIND> acc;
                 acc.init();
+                if constexpr (KIND == NC_HIP_RED_SUM || KIND == NC_HIP_RED_MEAN) {
 #pragma unroll
-                for (int k = 0; k < 4; k++) {
-                    const int v = lane + k * kWave;
-                    if (v < nv) {
-                        acc.push(q[k].x, 4 * v);
-                        acc.push(q[k].y, 4 * v + 1);
-                        acc.push(q[k].z, 4 * v + 2);
-                        acc.push(q[k].w, 4 * v + 3);
+                    for (int k = 0; k < 4; k++) {
+                        const int v = lane + k * kWave;
+                        if (v < nv) {
+                            acc.push(q[k].x, 4 * v);
+                            acc.push(q[k].y, 4 * v + 1);
+                            acc.push(q[k].z, 4 * v + 2);
+                            acc.push(q[k].w, 4 * v + 3);
+                        }
                     }
+                } else {
+                    // the lane's elements arrive in increasing index order, so its scan state is the
+                    // first element equal to their NaN-skipping maximum (-0 and +0 compare equal, and
+                    // the first of them is the one kept, with its sign): one max pass, then one
+                    // compare-and-select pass from the last element down, instead of a compare, a NaN
+                    // test and two selects per element
+                    float m = __builtin_nanf("");
+#pragma unroll
+                    for (int k = 0; k < 4; k++)
+                        if (lane + k * kWave < nv)
+                            m = __builtin_fmaxf(m, __builtin_fmaxf(__builtin_fmaxf(q[k].x, q[k].y),
+                                                                   __builtin_fmaxf(q[k].z, q[k].w)));
+                    int hit = 16;  // position 4 k + c of that element (16: every element is NaN)
+                    float hv = 0.0f;
+#pragma unroll
+                    for (int k = 3; k >= 0; k--) {
+                        if (lane + k * kWave < nv) {
+#pragma unroll
+                            for (int c = 3; c >= 0; c--) {
+                                const float e = c == 0 ? q[k].x : c == 1 ? q[k].y : c == 2 ? q[k].z : q[k].w;
+                                if (e == m) {
+                                    hit = 4 * k + c;
+                                    hv = e;
+                                }
+                            }
+                        }
+                    }
+                    if (hit < 16) acc.a = ArgState{hv, 4 * (lane + (hit >> 2) * kWave) + (hit & 3)};
                 }
                 acc.wave();
                 if (lane == 0) emit<KIND>(acc, q[0].x, scale, y, arg, o);
