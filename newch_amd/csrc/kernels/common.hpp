@@ -8,6 +8,7 @@
 #pragma once
 
 #include <hip/hip_runtime.h>
+#include <type_traits>
 #include <stdint.h>
 #include <stddef.h>
 
@@ -225,6 +226,24 @@ __device__ __forceinline__ float wave_max_nan_skip(float v) {  // fmaxf semantic
     v = __builtin_fmaxf(v, dpp_f32<kDppBcast15, 0xa>(v, v));
     v = __builtin_fmaxf(v, dpp_f32<kDppBcast31, 0xc>(v, v));
     return lane63_f32(v);
+}
+__device__ __forceinline__ unsigned long long wave_min_u64(unsigned long long v) {  // order-free
+    auto step = [](unsigned long long a, unsigned long long moved) { return moved < a ? moved : a; };
+    auto dpp = [](auto ctrl, unsigned long long x) {
+        constexpr int C = decltype(ctrl)::value;
+        constexpr int M = C == kDppBcast15 ? 0xa : C == kDppBcast31 ? 0xc : 0xf;
+        const int lo = dpp_i32<C, M>((int)(uint32_t)x, (int)(uint32_t)x);
+        const int hi = dpp_i32<C, M>((int)(uint32_t)(x >> 32), (int)(uint32_t)(x >> 32));
+        return ((unsigned long long)(uint32_t)hi << 32) | (uint32_t)lo;
+    };
+    v = step(v, dpp(std::integral_constant<int, kDppXor1>{}, v));
+    v = step(v, dpp(std::integral_constant<int, kDppXor2>{}, v));
+    v = step(v, dpp(std::integral_constant<int, kDppHalfMirror>{}, v));
+    v = step(v, dpp(std::integral_constant<int, kDppMirror>{}, v));
+    v = step(v, dpp(std::integral_constant<int, kDppBcast15>{}, v));
+    v = step(v, dpp(std::integral_constant<int, kDppBcast31>{}, v));
+    const uint32_t lo = (uint32_t)lane63_i32((int)(uint32_t)v), hi = (uint32_t)lane63_i32((int)(uint32_t)(v >> 32));
+    return ((unsigned long long)hi << 32) | lo;
 }
 // lane 0's value in every lane (the row's first element for the reference's NaN rule)
 __device__ __forceinline__ float lane0_f32(float v) { return __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(v))); }

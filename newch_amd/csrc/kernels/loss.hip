@@ -37,32 +37,29 @@ __device__ __forceinline__ unsigned long long bad_key(int64_t row, int32_t lab) 
     return ((unsigned long long)row << 32) | (uint32_t)lab;
 }
 
-// minimum over the workgroup of the lanes' first-bad-row keys; thread 0 returns it
-__device__ __forceinline__ unsigned long long block_min_key(unsigned long long v) {
+// the workgroup's loss sum (wave sums, then the waves added in order) and its minimum first-bad-row
+// key, both by DPP within each wave and one LDS exchange; thread 0 holds the results
+__device__ __forceinline__ void block_sum_min(double v, unsigned long long k, double &sum,
+                                              unsigned long long &key) {
+    __shared__ double shs[kLWaves];
     __shared__ unsigned long long shk[kLWaves];
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) {
-        const unsigned long long u = __shfl_xor(v, o, kWave);
-        v = u < v ? u : v;
-    }
-    if ((threadIdx.x & (kWave - 1)) == 0) shk[threadIdx.x / kWave] = v;
-    __syncthreads();
-    unsigned long long t = kNoBad;
-    if (threadIdx.x == 0)
-        for (int i = 0; i < kLWaves; i++) t = shk[i] < t ? shk[i] : t;
-    return t;
-}
-
-// sum of this workgroup's per-thread fp64 values, waves added in order; thread 0 returns it
-__device__ __forceinline__ double block_sum_ordered(double v) {
-    __shared__ double sh[kLWaves];
     v = wave_sum(v);
-    if ((threadIdx.x & (kWave - 1)) == 0) sh[threadIdx.x / kWave] = v;
+    k = wave_min_u64(k);
+    if ((threadIdx.x & (kWave - 1)) == 0) {
+        shs[threadIdx.x / kWave] = v;
+        shk[threadIdx.x / kWave] = k;
+    }
     __syncthreads();
-    double t = 0.0;
-    if (threadIdx.x == 0)
-        for (int i = 0; i < kLWaves; i++) t += sh[i];
-    return t;
+    if (threadIdx.x == 0) {
+        double t = 0.0;
+        unsigned long long m = kNoBad;
+        for (int i = 0; i < kLWaves; i++) {
+            t += shs[i];
+            m = shk[i] < m ? shk[i] : m;
+        }
+        sum = t;
+        key = m;
+    }
 }
 
 template <int VPL>
@@ -145,8 +142,9 @@ __device__ __forceinline__ void ce_fwd_rows(const float *__restrict__ x, const i
         row(r, va, la, xa);
         if (more) row(r + stride, vb, lb, label_logit(r + stride, lb));
     }
-    const double t = block_sum_ordered(acc);
-    const unsigned long long kb = block_min_key(mybad);
+    double t = 0.0;
+    unsigned long long kb = kNoBad;
+    block_sum_min(acc, mybad, t, kb);
     if (threadIdx.x == 0) {
         part[blockIdx.x] = t;
         badpart[blockIdx.x] = kb;
@@ -215,8 +213,9 @@ __global__ __launch_bounds__(kLB) void k_ce_fwd_blk(const float *__restrict__ x,
             stats[r] = f2{m, ls};
         }
     }
-    const double t = block_sum_ordered(acc);
-    const unsigned long long kb = block_min_key(mybad);
+    double t = 0.0;
+    unsigned long long kb = kNoBad;
+    block_sum_min(acc, mybad, t, kb);
     if (threadIdx.x == 0) {
         part[blockIdx.x] = t;
         badpart[blockIdx.x] = kb;
@@ -234,8 +233,9 @@ __global__ __launch_bounds__(kLB) void k_label_gather(const float *__restrict__ 
         if (L >= 0 && L < C) acc -= (double)x[r * C + L];
         else mybad = bad_key(r, L) < mybad ? bad_key(r, L) : mybad;
     }
-    const double t = block_sum_ordered(acc);
-    const unsigned long long kb = block_min_key(mybad);
+    double t = 0.0;
+    unsigned long long kb = kNoBad;
+    block_sum_min(acc, mybad, t, kb);
     if (threadIdx.x == 0) {
         part[blockIdx.x] = t;
         badpart[blockIdx.x] = kb;
@@ -268,8 +268,8 @@ __global__ __launch_bounds__(kLB) void k_loss_finish(const double *__restrict__ 
             kb = key[u] < kb ? key[u] : kb;
         }
     }
-    const double S = block_sum_ordered(t);
-    kb = block_min_key(kb);
+    double S = 0.0;
+    block_sum_min(t, kb, S, kb);
     if (threadIdx.x == 0) {
         *loss = sum ? (float)S : N ? (float)(S / (double)N) : __builtin_nanf("");
         *bad = kb;
