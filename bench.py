@@ -598,6 +598,23 @@ def engine_leg(K, hm, classes):
     L.nc_persistent_end(ctx)
     check()
     sc = c_void_p()
+    # Adam over 32 parameters of 65536 floats (gradients from one backward of the sum of their sums):
+    # the engine updates them in one multi-parameter launch
+    nps, pn = 32, 65536
+    Pb = hm.DeviceBuffer.from_numpy(np.random.default_rng(13).standard_normal(pn, dtype=np.float32))
+    pt = persistent_from(Pb, abi.F32, (pn,))
+    L.nc_persistent_begin(ctx)
+    params = [L.nc_parameter(ctx, pt, *abi.shape_arg((pn,))) for _ in range(nps)]
+    L.nc_persistent_end(ctx)
+    loss = None
+    for q in params:
+        t = L.nc_sum(q, 0, 0)
+        loss = t if loss is None else L.nc_add(loss, t)
+    L.nc_backward(loss)
+    check()
+    L.nc_step_end(ctx)
+    opt = L.nc_adam(ctx, (c_void_p * nps)(*params), nps, abi.OptimOpts(1e-3, 0, 0, 0.9, 0.999, 1e-8))
+    check()
     calls = [
         ("softmax_fwd", lambda: L.nc_softmax(X)),
         ("layer_norm_fwd", lambda: L.nc_layer_norm(X, 1, Wt, Bt, c_float(1e-5))),
@@ -605,6 +622,7 @@ def engine_leg(K, hm, classes):
         ("cross_entropy_fwd", lambda: L.nc_cross_entropy(X, LAB)),
         ("cross_entropy_fwd_bwd", lambda: L.nc_backward(L.nc_cross_entropy(Xp, LAB))),
         ("bcast_add_fwd_full", lambda: L.nc_add(A, Bv)),
+        ("adam_step_32_params", lambda: L.nc_optim_step(opt)),
     ]
     out = {}
     for label, fn in calls:

@@ -196,6 +196,22 @@ enum { NC_HIP_OPT_SGD = 0, NC_HIP_OPT_ADAM = 1, NC_HIP_OPT_ADAMW = 2, NC_HIP_OPT
 NC_HIP_API int nc_hip_optim_step(int kind, int64_t n, float *w, const float *g, float *s1, float *s2, float lr,
                                  float momentum, float weight_decay, float beta1, float beta2, float eps, float gs,
                                  float bc1, float bc2, int eps_inside_sqrt, void *stream);
+/* The same update for up to NC_HIP_OPT_MULTI_MAX parameters in one launch (no counterpart in the
+ * reference, whose step loops over its parameters one call each; for models with many small
+ * parameters, where one launch per parameter dominates the step).  Every parameter's n is a multiple
+ * of 4 and its arrays 16-byte aligned; s1 and s2 are present for every parameter or for none, as in
+ * one optimizer.  Bit-identical to one nc_hip_optim_step per parameter. */
+#define NC_HIP_OPT_MULTI_MAX 32
+typedef struct {
+    float *w;
+    const float *g;
+    float *s1;
+    float *s2;
+    int64_t n;
+} nc_hip_opt_param;
+NC_HIP_API int nc_hip_optim_step_multi(int kind, int count, const nc_hip_opt_param *params, float lr, float momentum,
+                                       float weight_decay, float beta1, float beta2, float eps, float gs, float bc1,
+                                       float bc2, int eps_inside_sqrt, void *stream);
 /* ss (+)= sum of x[i]^2 in fp64 (one double in device memory), clip_grad_norm's sum
  * (optim.c:219-225); fixed order.  Workspace: nc_hip_sumsq_workspace(n). */
 NC_HIP_API size_t nc_hip_sumsq_workspace(int64_t n);

@@ -2,9 +2,9 @@
 //
 // An optimizer is a list of parameter slots.  Each slot holds its parameter and up to two state
 // buffers in persistent device memory next to it (momentum, or Adam's m, in slot 0; Adam's v, or
-// RMSprop's square average, in slot 1), zeroed at creation.  A step is one nc_hip_optim_step launch
-// per parameter that has a gradient, with the reference's update expressions (bit-identical
-// results); gradient accumulation (every n-th step updates, with the mean of the summed
+// RMSprop's square average, in slot 1), zeroed at creation.  A step updates every parameter that has a gradient
+// with the reference's update expressions (bit-identical results): up to 32 parameters with 128-bit
+// aligned arrays per nc_hip_optim_step_multi launch, the others one nc_hip_optim_step launch each; gradient accumulation (every n-th step updates, with the mean of the summed
 // gradients), the step count and Adam's bias corrections (host powf, as the reference) are host
 // logic with the reference's semantics and messages.  nc_optim_state hands out a host copy of a
 // state buffer, read back on request and authoritative until the next step, which uploads it first
@@ -244,18 +244,38 @@ void nc_optim_step(nc_optim *o) {
     const float bc2 = is_adam(o->kind) ? 1.0f - powf(c.beta2, (float)o->t) : 1.0f;
     if (!o->upload_mapped()) return;
     nc_ctx *ctx = o->ctx;
+    // parameters whose arrays allow 128-bit access go up to NC_HIP_OPT_MULTI_MAX per launch, the rest
+    // one launch each (the same arithmetic either way)
+    nc_hip_opt_param batch[NC_HIP_OPT_MULTI_MAX];
+    int nb = 0;
+    auto flush = [&]() {
+        const int k = nb;
+        nb = 0;
+        return k == 0 || hip_layer_ok(ctx,
+                                      nc_hip_optim_step_multi(o->kind, k, batch, c.lr, c.momentum, c.weight_decay,
+                                                              c.beta1, c.beta2, c.eps, gs, bc1, bc2,
+                                                              o->eps_inside_sqrt, ctx->stream),
+                                      "optimizer step");
+    };
+    auto a16 = [](const void *p) { return p == nullptr || ((uintptr_t)p & 15u) == 0; };
     for (ParamSlot &s : o->slots) {
         nc_tensor *gt = nc_grad(s.p);
         if (!gt) continue;  // no gradient (never reached, or cleared)
         float *w = fptr(s.p), *g = fptr(gt);
-        if (!w || !g ||
-            !hip_layer_ok(ctx,
-                          nc_hip_optim_step(o->kind, s.n, w, g, s.dev[0], s.dev[1], c.lr, c.momentum, c.weight_decay,
-                                            c.beta1, c.beta2, c.eps, gs, bc1, bc2, o->eps_inside_sqrt, ctx->stream),
-                          "optimizer step"))
+        if (!w || !g) return;
+        if (s.n % 4 == 0 && a16(w) && a16(g) && a16(s.dev[0]) && a16(s.dev[1])) {
+            batch[nb++] = nc_hip_opt_param{w, g, s.dev[0], s.dev[1], s.n};
+            if (nb == NC_HIP_OPT_MULTI_MAX && !flush()) return;
+        } else if (!hip_layer_ok(ctx,
+                                 nc_hip_optim_step(o->kind, s.n, w, g, s.dev[0], s.dev[1], c.lr, c.momentum,
+                                                   c.weight_decay, c.beta1, c.beta2, c.eps, gs, bc1, bc2,
+                                                   o->eps_inside_sqrt, ctx->stream),
+                                 "optimizer step")) {
             return;
+        }
         wrote_dev(s.p);
     }
+    flush();
 }
 
 // torch.nn.utils.clip_grad_norm_: the 2-norm over all gradients together, from an fp64 sum of

@@ -76,25 +76,51 @@ __device__ __forceinline__ void opt_st(f4 v, f4 *p) {
     else *p = v;
 }
 
-// One float4 of every stream per lane and iteration.  Written as a single load-compute-store body:
-// with the loads and the stores in two separate unrolled loops, the optimizer rebuilt the stores
-// and dropped their non-temporal hint (plain stores: 18% slower at 2^26 parameters).
+// One float4 of every stream: a single load-compute-store body (with the loads and the stores in two
+// separate unrolled loops, the optimizer rebuilt the stores and dropped their non-temporal hint:
+// plain stores, 18% slower at 2^26 parameters).
+template <int KIND, bool S1, bool S2>
+__device__ __forceinline__ void opt_item4(f4 *__restrict__ w, const f4 *__restrict__ g, f4 *__restrict__ s1,
+                                          f4 *__restrict__ s2, int64_t e, const OptArgs &a) {
+    const f4 W = opt_ld(w + e), G = __builtin_nontemporal_load(g + e);
+    const f4 A = S1 ? opt_ld(s1 + e) : f4{0.f, 0.f, 0.f, 0.f};
+    const f4 B = S2 ? opt_ld(s2 + e) : f4{0.f, 0.f, 0.f, 0.f};
+    float wv[4] = {W.x, W.y, W.z, W.w}, av[4] = {A.x, A.y, A.z, A.w}, bv[4] = {B.x, B.y, B.z, B.w};
+    const float gv[4] = {G.x, G.y, G.z, G.w};
+#pragma unroll
+    for (int c = 0; c < 4; c++) opt1<KIND, S1>(wv[c], gv[c], av[c], bv[c], a);
+    opt_st(f4{wv[0], wv[1], wv[2], wv[3]}, w + e);
+    if constexpr (S1) opt_st(f4{av[0], av[1], av[2], av[3]}, s1 + e);
+    if constexpr (S2) opt_st(f4{bv[0], bv[1], bv[2], bv[3]}, s2 + e);
+}
+
 template <int KIND, bool S1, bool S2>
 __global__ __launch_bounds__(kOB) void k_optim4(f4 *__restrict__ w, const f4 *__restrict__ g, f4 *__restrict__ s1,
                                                 f4 *__restrict__ s2, int64_t n4, OptArgs a) {
     const int64_t step = (int64_t)gridDim.x * kOB;
-    for (int64_t e = (int64_t)blockIdx.x * kOB + threadIdx.x; e < n4; e += step) {
-        const f4 W = opt_ld(w + e), G = __builtin_nontemporal_load(g + e);
-        const f4 A = S1 ? opt_ld(s1 + e) : f4{0.f, 0.f, 0.f, 0.f};
-        const f4 B = S2 ? opt_ld(s2 + e) : f4{0.f, 0.f, 0.f, 0.f};
-        float wv[4] = {W.x, W.y, W.z, W.w}, av[4] = {A.x, A.y, A.z, A.w}, bv[4] = {B.x, B.y, B.z, B.w};
-        const float gv[4] = {G.x, G.y, G.z, G.w};
-#pragma unroll
-        for (int c = 0; c < 4; c++) opt1<KIND, S1>(wv[c], gv[c], av[c], bv[c], a);
-        opt_st(f4{wv[0], wv[1], wv[2], wv[3]}, w + e);
-        if constexpr (S1) opt_st(f4{av[0], av[1], av[2], av[3]}, s1 + e);
-        if constexpr (S2) opt_st(f4{bv[0], bv[1], bv[2], bv[3]}, s2 + e);
-    }
+    for (int64_t e = (int64_t)blockIdx.x * kOB + threadIdx.x; e < n4; e += step) opt_item4<KIND, S1, S2>(w, g, s1, s2, e, a);
+}
+
+// Several parameters in one launch: parameter t owns workgroups first[t] .. first[t + 1] - 1, one
+// float4 per lane, so a workgroup finds its parameter with a wave-uniform scan of the (at most
+// NC_HIP_OPT_MULTI_MAX) boundaries and every element gets the single-parameter kernel's arithmetic.
+struct OptMulti {
+    f4 *w[NC_HIP_OPT_MULTI_MAX];
+    const f4 *g[NC_HIP_OPT_MULTI_MAX];
+    f4 *s1[NC_HIP_OPT_MULTI_MAX];
+    f4 *s2[NC_HIP_OPT_MULTI_MAX];
+    int64_t n4[NC_HIP_OPT_MULTI_MAX];
+    int64_t first[NC_HIP_OPT_MULTI_MAX + 1];
+    int count;
+};
+
+template <int KIND, bool S1, bool S2>
+__global__ __launch_bounds__(kOB) void k_optim4_multi(OptMulti m, OptArgs a) {
+    const int64_t b = blockIdx.x;
+    int t = 0;
+    while (t + 1 < m.count && m.first[t + 1] <= b) t++;
+    const int64_t e = (b - m.first[t]) * kOB + threadIdx.x;
+    if (e < m.n4[t]) opt_item4<KIND, S1, S2>(m.w[t], m.g[t], S1 ? m.s1[t] : nullptr, S2 ? m.s2[t] : nullptr, e, a);
 }
 
 template <int KIND, bool S1, bool S2>
@@ -196,13 +222,8 @@ static unsigned sumsq_grid(int64_t n) {
 
 using namespace nchip;
 
-extern "C" NC_HIP_API int nc_hip_optim_step(int kind, int64_t n, float *w, const float *g, float *s1, float *s2,
-                                            float lr, float momentum, float weight_decay, float beta1, float beta2,
-                                            float eps, float gs, float bc1, float bc2, int eps_inside_sqrt,
-                                            void *stream) {
-    if (n < 0) return set_error(NC_HIP_ERR_ARG, "nc_hip_optim_step: negative size");
-    if (n == 0) return NC_HIP_OK;
-    if (!w || !g) return set_error(NC_HIP_ERR_ARG, "nc_hip_optim_step: NULL parameter or gradient");
+static OptArgs opt_args(int kind, float lr, float momentum, float weight_decay, float beta1, float beta2, float eps,
+                        float gs, float bc1, float bc2, int eps_inside_sqrt) {
     OptArgs a{};
     a.lr = lr;
     a.momentum = momentum;
@@ -216,6 +237,19 @@ extern "C" NC_HIP_API int nc_hip_optim_step(int kind, int64_t n, float *w, const
     a.one_m_b1 = 1.0f - beta1;
     a.one_m_b2 = 1.0f - beta2;
     a.inside = eps_inside_sqrt ? 1 : 0;
+    a.l2 = kind == NC_HIP_OPT_ADAM ? weight_decay : 0.0f;
+    a.decay = kind == NC_HIP_OPT_ADAMW ? 1.0f - lr * weight_decay : 1.0f;
+    return a;
+}
+
+extern "C" NC_HIP_API int nc_hip_optim_step(int kind, int64_t n, float *w, const float *g, float *s1, float *s2,
+                                            float lr, float momentum, float weight_decay, float beta1, float beta2,
+                                            float eps, float gs, float bc1, float bc2, int eps_inside_sqrt,
+                                            void *stream) {
+    if (n < 0) return set_error(NC_HIP_ERR_ARG, "nc_hip_optim_step: negative size");
+    if (n == 0) return NC_HIP_OK;
+    if (!w || !g) return set_error(NC_HIP_ERR_ARG, "nc_hip_optim_step: NULL parameter or gradient");
+    OptArgs a = opt_args(kind, lr, momentum, weight_decay, beta1, beta2, eps, gs, bc1, bc2, eps_inside_sqrt);
     hipStream_t st = as_stream(stream);
     switch (kind) {
     case NC_HIP_OPT_SGD:
@@ -225,8 +259,6 @@ extern "C" NC_HIP_API int nc_hip_optim_step(int kind, int64_t n, float *w, const
     case NC_HIP_OPT_ADAM:
     case NC_HIP_OPT_ADAMW:
         if (!s1 || !s2) return set_error(NC_HIP_ERR_ARG, "nc_hip_optim_step: Adam needs both state buffers");
-        a.l2 = kind == NC_HIP_OPT_ADAM ? weight_decay : 0.0f;
-        a.decay = kind == NC_HIP_OPT_ADAMW ? 1.0f - lr * weight_decay : 1.0f;
         launch_opt<K_ADAM, true, true>(w, g, s1, s2, n, a, st);
         break;
     case NC_HIP_OPT_RMSPROP:
@@ -237,6 +269,65 @@ extern "C" NC_HIP_API int nc_hip_optim_step(int kind, int64_t n, float *w, const
     default: return set_error(NC_HIP_ERR_ARG, "nc_hip_optim_step: unknown optimizer %d", kind);
     }
     return check_launch("nc_hip_optim_step");
+}
+
+extern "C" NC_HIP_API int nc_hip_optim_step_multi(int kind, int count, const nc_hip_opt_param *params, float lr,
+                                                  float momentum, float weight_decay, float beta1, float beta2,
+                                                  float eps, float gs, float bc1, float bc2, int eps_inside_sqrt,
+                                                  void *stream) {
+    if (count < 0 || count > NC_HIP_OPT_MULTI_MAX)
+        return set_error(NC_HIP_ERR_ARG, "nc_hip_optim_step_multi: %d parameters (1 to %d per call)", count,
+                         NC_HIP_OPT_MULTI_MAX);
+    if (count == 0) return NC_HIP_OK;
+    if (!params) return set_error(NC_HIP_ERR_ARG, "nc_hip_optim_step_multi: NULL parameter list");
+    const bool with1 = params[0].s1 != nullptr, with2 = params[0].s2 != nullptr;
+    OptMulti m{};
+    m.count = count;
+    m.first[0] = 0;
+    for (int t = 0; t < count; t++) {
+        const nc_hip_opt_param &q = params[t];
+        if (q.n == 0) {  // nothing to update: no workgroups
+            m.first[t + 1] = m.first[t];
+            continue;
+        }
+        if (q.n < 0 || q.n % 4 != 0 || !q.w || !q.g || !aligned16(q.w) || !aligned16(q.g) ||
+            (q.s1 != nullptr) != with1 || (q.s2 != nullptr) != with2 || (q.s1 && !aligned16(q.s1)) ||
+            (q.s2 && !aligned16(q.s2)))
+            return set_error(NC_HIP_ERR_ARG,
+                             "nc_hip_optim_step_multi: parameter %d needs n a multiple of 4, 16-byte aligned arrays "
+                             "and the same state buffers as parameter 0",
+                             t);
+        m.w[t] = (f4 *)q.w;
+        m.g[t] = (const f4 *)q.g;
+        m.s1[t] = (f4 *)q.s1;
+        m.s2[t] = (f4 *)q.s2;
+        m.n4[t] = q.n / 4;
+        m.first[t + 1] = m.first[t] + (m.n4[t] + kOB - 1) / kOB;
+    }
+    const int64_t blocks = m.first[count];
+    if (blocks == 0) return NC_HIP_OK;
+    if (blocks > INT32_MAX) return set_error(NC_HIP_ERR_ARG, "nc_hip_optim_step_multi: too many elements for one launch");
+    const OptArgs a = opt_args(kind, lr, momentum, weight_decay, beta1, beta2, eps, gs, bc1, bc2, eps_inside_sqrt);
+    hipStream_t st = as_stream(stream);
+    const dim3 grid((unsigned)blocks), block(kOB);
+    switch (kind) {
+    case NC_HIP_OPT_SGD:
+        if (with1) hipLaunchKernelGGL((k_optim4_multi<K_SGD, true, false>), grid, block, 0, st, m, a);
+        else hipLaunchKernelGGL((k_optim4_multi<K_SGD, false, false>), grid, block, 0, st, m, a);
+        break;
+    case NC_HIP_OPT_ADAM:
+    case NC_HIP_OPT_ADAMW:
+        if (!with1 || !with2) return set_error(NC_HIP_ERR_ARG, "nc_hip_optim_step_multi: Adam needs both state buffers");
+        hipLaunchKernelGGL((k_optim4_multi<K_ADAM, true, true>), grid, block, 0, st, m, a);
+        break;
+    case NC_HIP_OPT_RMSPROP:
+        if (!with2) return set_error(NC_HIP_ERR_ARG, "nc_hip_optim_step_multi: RMSprop needs its square average");
+        if (with1) hipLaunchKernelGGL((k_optim4_multi<K_RMS, true, true>), grid, block, 0, st, m, a);
+        else hipLaunchKernelGGL((k_optim4_multi<K_RMS, false, true>), grid, block, 0, st, m, a);
+        break;
+    default: return set_error(NC_HIP_ERR_ARG, "nc_hip_optim_step_multi: unknown optimizer %d", kind);
+    }
+    return check_launch("nc_hip_optim_step_multi");
 }
 
 extern "C" NC_HIP_API size_t nc_hip_sumsq_workspace(int64_t n) {

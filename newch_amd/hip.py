@@ -27,6 +27,11 @@ BWD_READS_NONE = {"neg", "scale", "add_scalar"}
 P = c_void_p
 I64P = POINTER(c_int64)
 
+
+class OptParam(ctypes.Structure):
+    """nc_hip_opt_param: one parameter of nc_hip_optim_step_multi."""
+    _fields_ = [("w", c_void_p), ("g", c_void_p), ("s1", c_void_p), ("s2", c_void_p), ("n", c_int64)]
+
 SIGNATURES = {
     "nc_hip_last_error": (c_char_p, []),
     "nc_hip_device_count": (c_int, []),
@@ -59,6 +64,8 @@ SIGNATURES = {
     "nc_hip_dequantize_rows": (c_int, [c_int64, c_int64, P, P, P, P]),
     "nc_hip_optim_step": (c_int, [c_int, c_int64, P, P, P, P, c_float, c_float, c_float, c_float, c_float, c_float,
                                   c_float, c_float, c_float, c_int, P]),
+    "nc_hip_optim_step_multi": (c_int, [c_int, c_int, P, c_float, c_float, c_float, c_float, c_float, c_float,
+                                        c_float, c_float, c_float, c_int, P]),
     "nc_hip_sumsq_workspace": (c_size_t, [c_int64]),
     "nc_hip_sumsq": (c_int, [c_int64, P, P, c_int, P, c_size_t, P]),
     "nc_hip_loss_workspace": (c_size_t, [c_int64, c_int64]),
@@ -179,6 +186,16 @@ class Kernels:
                    gs=1.0, bc1=1.0, bc2=1.0, eps_inside_sqrt=False, stream=None):
         self._ok(self.lib.nc_hip_optim_step(OPT[kind], n, w, g, s1, s2, lr, momentum, weight_decay, beta1, beta2, eps,
                                             gs, bc1, bc2, int(eps_inside_sqrt), stream), "optim_step")
+
+    def optim_step_multi(self, kind, params, lr, momentum=0.0, weight_decay=0.0, beta1=0.0, beta2=0.0, eps=0.0,
+                         gs=1.0, bc1=1.0, bc2=1.0, eps_inside_sqrt=False, stream=None):
+        """params: (w, g, s1, s2, n) per parameter (device addresses; s1 / s2 None when absent)."""
+        arr = (OptParam * max(len(params), 1))()
+        for i, (w, g, s1, s2, n) in enumerate(params):
+            arr[i] = OptParam(w, g, s1, s2, n)
+        self._ok(self.lib.nc_hip_optim_step_multi(OPT[kind], len(params), ctypes.addressof(arr), lr, momentum,
+                                                  weight_decay, beta1, beta2, eps, gs, bc1, bc2,
+                                                  int(eps_inside_sqrt), stream), "optim_step_multi")
 
     def sumsq_workspace(self, n):
         return self.lib.nc_hip_sumsq_workspace(n)

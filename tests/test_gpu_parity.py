@@ -1177,6 +1177,53 @@ def test_kernel_optim_step(K, kind, s1, s2, n, offset, inside):
         assert_bits(V.to_numpy(np.float32, n, pad), v, f"{kind} s2")
 
 
+@pytest.mark.parametrize("kind,s1,s2,inside", OPT_KERNEL_CASES)
+@pytest.mark.parametrize("sizes", [(4,), (64, 4096, 1_000_000, 8, 256 + 4, 65536 * 4), tuple(4 * (i + 1) * 97 for i in range(32))])
+def test_kernel_optim_step_multi(K, kind, s1, s2, inside, sizes):
+    """Several parameters in one launch: bit for bit the oracle's per-parameter update, two steps."""
+    rng = np.random.default_rng(zlib.crc32(f"optmulti/{kind}/{s1}/{s2}/{len(sizes)}".encode()))
+    ws = [rng.standard_normal(n).astype(np.float32) for n in sizes]
+    ms = [np.zeros(n, np.float32) if s1 else None for n in sizes]
+    vs = [np.zeros(n, np.float32) if s2 else None for n in sizes]
+    Wd = [dev(w) for w in ws]
+    Md = [dev(m) if s1 else None for m in ms]
+    Vd = [dev(v) if s2 else None for v in vs]
+    hp = dict(lr=np.float32(0.01), momentum=np.float32(0.9 if s1 and kind != "adam" and kind != "adamw" else 0.0),
+              weight_decay=np.float32(0.01), beta1=np.float32(0.9), beta2=np.float32(0.999 if "adam" in kind else 0.99),
+              eps=np.float32(1e-8), gs=np.float32(0.5))
+    adam = kind in ("adam", "adamw")
+    for t in range(1, 3):
+        gs_ = [(rng.standard_normal(n) * (10.0 ** rng.integers(-3, 3, n))).astype(np.float32) for n in sizes]
+        Gd = [dev(g) for g in gs_]
+        bc1 = np.float32(1) - O.powf(hp["beta1"], t) if adam else np.float32(1)
+        bc2 = np.float32(1) - O.powf(hp["beta2"], t) if adam else np.float32(1)
+        K.optim_step_multi(kind, [(Wd[i].ptr, Gd[i].ptr, Md[i].ptr if s1 else None, Vd[i].ptr if s2 else None, n)
+                                  for i, n in enumerate(sizes)], bc1=bc1, bc2=bc2, eps_inside_sqrt=inside, **hp)
+        for i in range(len(sizes)):
+            O.optim_step(kind, ws[i], gs_[i], ms[i], vs[i], bc1=bc1, bc2=bc2, eps_inside_sqrt=inside, **hp)
+    sync()
+    for i, n in enumerate(sizes):
+        assert_bits(Wd[i].to_numpy(np.float32, n), ws[i], f"{kind} w[{i}]")
+        if s1:
+            assert_bits(Md[i].to_numpy(np.float32, n), ms[i], f"{kind} s1[{i}]")
+        if s2:
+            assert_bits(Vd[i].to_numpy(np.float32, n), vs[i], f"{kind} s2[{i}]")
+
+
+def test_kernel_optim_step_multi_rejects(K):
+    """Sizes that are not a multiple of 4, misaligned arrays, mixed state buffers and too many
+    parameters are errors, not launches."""
+    from newch_amd.hip import HipLayerError
+    W, G, M = dev(np.zeros(16, np.float32)), dev(np.zeros(16, np.float32)), dev(np.zeros(16, np.float32))
+    hp = dict(lr=0.01, momentum=0.9)
+    bad = [[(W.ptr, G.ptr, None, None, 6)], [(W.ptr + 4, G.ptr, None, None, 8)],
+           [(W.ptr, G.ptr, M.ptr, None, 8), (W.ptr, G.ptr, None, None, 8)],
+           [(W.ptr, G.ptr, None, None, 4)] * 33]
+    for params in bad:
+        with pytest.raises(HipLayerError, match="nc_hip_optim_step_multi"):
+            K.optim_step_multi("sgd", params, **hp)
+
+
 @pytest.mark.parametrize("sizes", [(1_000_003, 7, 65536), (0, 5), (1 << 22,)])
 def test_kernel_sumsq(K, sizes):
     rng = np.random.default_rng(len(sizes))
