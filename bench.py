@@ -613,7 +613,8 @@ def engine_leg(K, hm, classes):
     L.nc_backward(loss)
     check()
     L.nc_step_end(ctx)
-    opt = L.nc_adam(ctx, (c_void_p * nps)(*params), nps, abi.OptimOpts(1e-3, 0, 0, 0.9, 0.999, 1e-8))
+    plist = (c_void_p * nps)(*params)
+    opt = L.nc_adam(ctx, plist, nps, abi.OptimOpts(1e-3, 0, 0, 0.9, 0.999, 1e-8))
     check()
     calls = [
         ("softmax_fwd", lambda: L.nc_softmax(X)),
@@ -623,6 +624,8 @@ def engine_leg(K, hm, classes):
         ("cross_entropy_fwd_bwd", lambda: L.nc_backward(L.nc_cross_entropy(Xp, LAB))),
         ("bcast_add_fwd_full", lambda: L.nc_add(A, Bv)),
         ("adam_step_32_params", lambda: L.nc_optim_step(opt)),
+        # the 32 gradients' norm (one sum launch, one read-back) and their rescale (one launch)
+        ("clip_grad_norm_32_params", lambda: L.nc_clip_grad_norm(plist, nps, c_float(1.0))),
     ]
     out = {}
     for label, fn in calls:

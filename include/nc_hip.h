@@ -217,6 +217,18 @@ NC_HIP_API int nc_hip_optim_step_multi(int kind, int count, const nc_hip_opt_par
 NC_HIP_API size_t nc_hip_sumsq_workspace(int64_t n);
 NC_HIP_API int nc_hip_sumsq(int64_t n, const float *x, double *ss, int accumulate, void *ws, size_t ws_bytes,
                             void *stream);
+/* The same sum over up to NC_HIP_OPT_MULTI_MAX tensors x[t] of n[t] floats in two launches (no
+ * counterpart in the reference, whose clip_grad_norm calls one sum per gradient; for models with
+ * many small gradients).  Bit-identical to one nc_hip_sumsq per tensor in turn, the first with the
+ * given accumulate and the others accumulating.  The tables are host memory.  Workspace:
+ * nc_hip_sumsq_multi_workspace(count, n) = the sum of the tensors' nc_hip_sumsq_workspace. */
+NC_HIP_API size_t nc_hip_sumsq_multi_workspace(int count, const int64_t *n);
+NC_HIP_API int nc_hip_sumsq_multi(int count, const float *const *x, const int64_t *n, double *ss, int accumulate,
+                                  void *ws, size_t ws_bytes, void *stream);
+/* x[t] = coef * x[t] in place for up to NC_HIP_OPT_MULTI_MAX tensors in one launch (no counterpart
+ * in the reference: clip_grad_norm's rescale of every gradient, scale_f32 at optim.c:226-231); the
+ * bits of nc_hip_unary_fwd(NC_HIP_UN_SCALE, coef) per tensor. */
+NC_HIP_API int nc_hip_scale_multi(int count, float *const *x, const int64_t *n, float coef, void *stream);
 
 /* Row-major fp32 GEMM: C = alpha * op(A) op(B) + beta * C, op(X) = X^T when its flag is set; op(A) is
  * M x K, op(B) K x N, leading dims in elements.  The reference's gemm_f32 (kernels.h:36-41) as used by

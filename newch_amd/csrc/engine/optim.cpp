@@ -2,11 +2,13 @@
 //
 // An optimizer is a list of parameter slots.  Each slot holds its parameter and up to two state
 // buffers in persistent device memory next to it (momentum, or Adam's m, in slot 0; Adam's v, or
-// RMSprop's square average, in slot 1), zeroed at creation.  A step updates every parameter that has a gradient
-// with the reference's update expressions (bit-identical results): up to 32 parameters with 128-bit
-// aligned arrays per nc_hip_optim_step_multi launch, the others one nc_hip_optim_step launch each; gradient accumulation (every n-th step updates, with the mean of the summed
-// gradients), the step count and Adam's bias corrections (host powf, as the reference) are host
-// logic with the reference's semantics and messages.  nc_optim_state hands out a host copy of a
+// RMSprop's square average, in slot 1), zeroed at creation.  A step updates every parameter that
+// has a gradient with the reference's update expressions (bit-identical results): up to 32
+// parameters with 128-bit aligned arrays per nc_hip_optim_step_multi launch, the others one
+// nc_hip_optim_step launch each; gradient accumulation (every n-th step updates, with the mean of
+// the summed gradients), the step count and Adam's bias corrections (host powf, as the reference)
+// are host logic with the reference's semantics and messages.  clip_grad_norm sums and rescales 32
+// gradients per launch.  nc_optim_state hands out a host copy of a
 // state buffer, read back on request and authoritative until the next step, which uploads it first
 // (the contract nc_data_f32 has for tensors): checkpoint code that reads or writes it keeps working.
 #include <math.h>
@@ -288,22 +290,35 @@ float nc_clip_grad_norm(nc_tensor **params, int n, float max_norm) {
         nc_tensor *g = params[i] ? nc_grad(params[i]) : nullptr;
         return g && !(g->flags & TF_GRAD_FRESH) ? g : nullptr;
     };
+    // the gradients go to the device NC_HIP_OPT_MULTI_MAX at a time: one sum of squares (or one
+    // rescale) launch per group, with the bits of one call per gradient in parameter order
+    float *xs[NC_HIP_OPT_MULTI_MAX];
+    int64_t ns[NC_HIP_OPT_MULTI_MAX];
     double ss = 0.0;
     if (ctx && need_device(ctx, "clip_grad_norm")) {
         Scratch scratch(ctx);
         double *dss = (double *)arena_alloc(ctx, sizeof(double));
-        if (!dss || !hip_layer_ok(ctx, nc_hip_fill(dss, 8, 0, 1, ctx->stream), "clip_grad_norm")) return 0.0f;
+        if (!dss) return 0.0f;
+        int cnt = 0;
+        bool first = true;  // the first group overwrites *dss, the later ones add to it
+        auto flush = [&]() {
+            const size_t wsb = nc_hip_sumsq_multi_workspace(cnt, ns);
+            char *ws = wsb ? arena_alloc(ctx, wsb) : nullptr;
+            if (wsb && !ws) return false;
+            const int rc = nc_hip_sumsq_multi(cnt, (const float *const *)xs, ns, dss, first ? 0 : 1, ws, wsb,
+                                              ctx->stream);
+            first = false;
+            cnt = 0;
+            return hip_layer_ok(ctx, rc, "clip_grad_norm");
+        };
         for (int i = 0; i < n; i++) {
             nc_tensor *g = live_grad(i);
             if (!g) continue;
-            const int64_t N = nc_numel(g);
-            const size_t wsb = nc_hip_sumsq_workspace(N);
-            char *ws = wsb ? arena_alloc(ctx, wsb) : nullptr;
-            float *d = fptr(g);
-            if (!d || (wsb && !ws) ||
-                !hip_layer_ok(ctx, nc_hip_sumsq(N, d, dss, 1, ws, wsb, ctx->stream), "clip_grad_norm"))
-                return 0.0f;
+            if (!(xs[cnt] = fptr(g))) return 0.0f;
+            ns[cnt] = nc_numel(g);
+            if (++cnt == NC_HIP_OPT_MULTI_MAX && !flush()) return 0.0f;
         }
+        if ((cnt || first) && !flush()) return 0.0f;  // no gradient at all: *dss = 0
         if (!hip_ok(ctx, hipMemcpyAsync(&ss, dss, sizeof ss, hipMemcpyDeviceToHost, ctx->stream), "clip_grad_norm") ||
             !hip_ok(ctx, hipStreamSynchronize(ctx->stream), "clip_grad_norm"))
             return 0.0f;
@@ -311,15 +326,21 @@ float nc_clip_grad_norm(nc_tensor **params, int n, float max_norm) {
     const float total = (float)sqrt(ss);
     const float coef = max_norm / (total + 1e-6f);
     if (coef < 1.0f && ctx) {
+        int cnt = 0;
+        auto flush = [&]() {
+            const int rc = nc_hip_scale_multi(cnt, xs, ns, coef, ctx->stream);
+            cnt = 0;
+            return hip_layer_ok(ctx, rc, "clip_grad_norm");
+        };
         for (int i = 0; i < n; i++) {
             nc_tensor *g = live_grad(i);
             if (!g) continue;
-            float *d = fptr(g);
-            if (!d || !hip_layer_ok(ctx, nc_hip_unary_fwd(NC_HIP_UN_SCALE, coef, d, d, nc_numel(g), ctx->stream),
-                                    "clip_grad_norm"))
-                return total;
+            if (!(xs[cnt] = fptr(g))) return total;
+            ns[cnt] = nc_numel(g);
             wrote_dev(g);
+            if (++cnt == NC_HIP_OPT_MULTI_MAX && !flush()) return total;
         }
+        if (cnt && !flush()) return total;
     }
     return total;
 }

@@ -164,13 +164,14 @@ __device__ __forceinline__ double block_sum_waves(double v) {
 }
 
 // float4 items (kSU per lane in flight) into four fp64 accumulators per lane, one per item slot,
-// added in slot order at the end; the scalar tail (n % 4, or an unaligned x) goes to slot 0
-__global__ __launch_bounds__(kSB) void k_sumsq(const float *__restrict__ x, int64_t n, int64_t n4,
-                                               double *__restrict__ part) {
+// added in slot order at the end; the scalar tail (n % 4, or an unaligned x) goes to slot 0.
+// Workgroup blk of nblk; thread 0 gets the workgroup's partial.
+__device__ __forceinline__ double sumsq_block(const float *__restrict__ x, int64_t n, int64_t n4, int64_t blk,
+                                              int64_t nblk) {
     double acc[kSU] = {0.0, 0.0, 0.0, 0.0};
     const f4 *x4 = (const f4 *)x;
-    const int64_t step = (int64_t)gridDim.x * kSB * kSU;
-    for (int64_t base = (int64_t)blockIdx.x * kSB * kSU + threadIdx.x; base < n4; base += step) {
+    const int64_t step = nblk * kSB * kSU;
+    for (int64_t base = blk * kSB * kSU + threadIdx.x; base < n4; base += step) {
         f4 v[kSU];
 #pragma unroll
         for (int u = 0; u < kSU; u++)
@@ -183,17 +184,22 @@ __global__ __launch_bounds__(kSB) void k_sumsq(const float *__restrict__ x, int6
             }
         }
     }
-    for (int64_t e = n4 * 4 + (int64_t)blockIdx.x * kSB + threadIdx.x; e < n; e += (int64_t)gridDim.x * kSB) {
+    for (int64_t e = n4 * 4 + blk * kSB + threadIdx.x; e < n; e += nblk * kSB) {
         const double v = (double)x[e];
         acc[0] += v * v;
     }
-    const double t = block_sum_waves((acc[0] + acc[1]) + (acc[2] + acc[3]));
+    return block_sum_waves((acc[0] + acc[1]) + (acc[2] + acc[3]));
+}
+
+__global__ __launch_bounds__(kSB) void k_sumsq(const float *__restrict__ x, int64_t n, int64_t n4,
+                                               double *__restrict__ part) {
+    const double t = sumsq_block(x, n, n4, blockIdx.x, gridDim.x);
     if (threadIdx.x == 0) part[blockIdx.x] = t;
 }
 
-__global__ __launch_bounds__(kSB) void k_sumsq_finish(const double *__restrict__ part, int nparts, double *ss,
-                                                      int accumulate) {
-    // partials threadIdx.x, + kSB, ... added in that order, their loads issued kU at a time
+// partials threadIdx.x, + kSB, ... of part[0, nparts) added in that order, their loads issued kU at a
+// time; the workgroup total comes back in thread 0
+__device__ __forceinline__ double sum_parts(const double *__restrict__ part, int nparts) {
     constexpr int kU = 8;
     double t = 0.0;
     for (int base = threadIdx.x; base < nparts; base += kSB * kU) {
@@ -204,8 +210,76 @@ __global__ __launch_bounds__(kSB) void k_sumsq_finish(const double *__restrict__
         for (int u = 0; u < kU; u++)
             if (base + u * kSB < nparts) t += v[u];
     }
-    const double s = block_sum_waves(t);
+    return block_sum_waves(t);
+}
+
+__global__ __launch_bounds__(kSB) void k_sumsq_finish(const double *__restrict__ part, int nparts, double *ss,
+                                                      int accumulate) {
+    const double s = sum_parts(part, nparts);
     if (threadIdx.x == 0) *ss = (accumulate ? *ss : 0.0) + s;
+}
+
+// Up to NC_HIP_OPT_MULTI_MAX tensors in one launch: workgroups [first[t], first[t + 1]) are the grid
+// k_sumsq would launch for tensor t alone (workgroup b plays workgroup b - first[t]), so every
+// partial is the one-tensor partial.
+struct SumsqMulti {
+    const float *x[NC_HIP_OPT_MULTI_MAX];
+    int64_t n[NC_HIP_OPT_MULTI_MAX], n4[NC_HIP_OPT_MULTI_MAX];
+    int first[NC_HIP_OPT_MULTI_MAX + 1];
+    int count;
+};
+
+__global__ __launch_bounds__(kSB) void k_sumsq_multi(SumsqMulti m, double *__restrict__ part) {
+    const int b = blockIdx.x;
+    int t = 0;  // workgroup-uniform
+    while (t + 1 < m.count && m.first[t + 1] <= b) t++;
+    const double s = sumsq_block(m.x[t], m.n[t], m.n4[t], b - m.first[t], m.first[t + 1] - m.first[t]);
+    if (threadIdx.x == 0) part[b] = s;
+}
+
+// ss = (((ss or 0) + S_0) + S_1) + ..., S_t tensor t's partials summed as k_sumsq_finish sums them:
+// the bits of one nc_hip_sumsq per tensor in turn
+__global__ __launch_bounds__(kSB) void k_sumsq_multi_finish(const double *__restrict__ part, SumsqMulti m, double *ss,
+                                                            int accumulate) {
+    double acc = accumulate ? *ss : 0.0;
+    for (int t = 0; t < m.count; t++) {
+        const double s = sum_parts(part + m.first[t], m.first[t + 1] - m.first[t]);
+        if (threadIdx.x == 0) acc = acc + s;
+        __syncthreads();  // the wave sums' LDS slots are written again for the next tensor
+    }
+    if (threadIdx.x == 0) *ss = acc;
+}
+
+// x[t] = coef * x[t] for up to NC_HIP_OPT_MULTI_MAX tensors, the unary scale kernel's expression;
+// a workgroup scales kSB float4 items of one tensor (kSB floats of a tensor not 16-byte aligned)
+struct ScaleMulti {
+    float *x[NC_HIP_OPT_MULTI_MAX];
+    int64_t n[NC_HIP_OPT_MULTI_MAX];
+    int first[NC_HIP_OPT_MULTI_MAX + 1];
+    int vec[NC_HIP_OPT_MULTI_MAX];
+    int count;
+};
+
+__global__ __launch_bounds__(kSB) void k_scale_multi(ScaleMulti m, float coef) {
+    const int b = blockIdx.x;
+    int t = 0;
+    while (t + 1 < m.count && m.first[t + 1] <= b) t++;
+    float *x = m.x[t];
+    const int64_t n = m.n[t], i = (int64_t)(b - m.first[t]) * kSB + threadIdx.x;
+    if (m.vec[t]) {
+        if (4 * i + 3 < n) {
+            f4 v = ((f4 *)x)[i];
+            v.x = coef * v.x;
+            v.y = coef * v.y;
+            v.z = coef * v.z;
+            v.w = coef * v.w;
+            ((f4 *)x)[i] = v;
+        } else {
+            for (int64_t e = 4 * i; e < n; e++) x[e] = coef * x[e];
+        }
+    } else if (i < n) {
+        x[i] = coef * x[i];
+    }
 }
 
 #ifndef NC_SUMSQ_GRID_PER_CU
@@ -350,4 +424,69 @@ extern "C" NC_HIP_API int nc_hip_sumsq(int64_t n, const float *x, double *ss, in
     }
     hipLaunchKernelGGL(k_sumsq_finish, 1, kSB, 0, st, (const double *)ws, nparts, ss, accumulate ? 1 : 0);
     return check_launch("nc_hip_sumsq");
+}
+
+// checks a multi-tensor table and lays the tensors' workgroup ranges end to end: tensor t gets
+// blocks(t) workgroups from first[t] (false, with the error set, when the table is bad)
+template <class Blocks>
+static bool multi_spans(const char *fn, int count, const int64_t *n, const void *const *x, int *first, Blocks blocks) {
+    if (count < 0 || count > NC_HIP_OPT_MULTI_MAX || (count && (!n || !x)))
+        return set_error(NC_HIP_ERR_ARG, "%s: count %d outside [0, %d] or NULL table", fn, count,
+                         NC_HIP_OPT_MULTI_MAX), false;
+    int64_t total = 0;
+    for (int t = 0; t < count; t++) {
+        if (n[t] < 0 || (n[t] > 0 && !x[t]))
+            return set_error(NC_HIP_ERR_ARG, "%s: tensor %d: negative size or NULL pointer", fn, t), false;
+        first[t] = (int)total;
+        total += n[t] > 0 ? blocks(t) : 0;
+        if (total > INT32_MAX) return set_error(NC_HIP_ERR_ARG, "%s: more than 2^31 - 1 workgroups", fn), false;
+    }
+    first[count] = (int)total;
+    return true;
+}
+
+extern "C" NC_HIP_API size_t nc_hip_sumsq_multi_workspace(int count, const int64_t *n) {
+    size_t b = 0;
+    for (int t = 0; n && t < count && t < NC_HIP_OPT_MULTI_MAX; t++) b += nc_hip_sumsq_workspace(n[t]);
+    return b;
+}
+
+extern "C" NC_HIP_API int nc_hip_sumsq_multi(int count, const float *const *x, const int64_t *n, double *ss,
+                                             int accumulate, void *ws, size_t ws_bytes, void *stream) {
+    SumsqMulti m{};
+    if (!ss) return set_error(NC_HIP_ERR_ARG, "nc_hip_sumsq_multi: NULL ss");
+    if (!multi_spans("nc_hip_sumsq_multi", count, n, (const void *const *)x, m.first,
+                     [&](int t) { return (int64_t)sumsq_grid(n[t]); }))
+        return NC_HIP_ERR_ARG;
+    const size_t need = nc_hip_sumsq_multi_workspace(count, n);
+    if (need && (!ws || ws_bytes < need))
+        return set_error(NC_HIP_ERR_WORKSPACE, "nc_hip_sumsq_multi: workspace of %zu bytes needed", need);
+    m.count = count;
+    for (int t = 0; t < count; t++) {
+        m.x[t] = x[t];
+        m.n[t] = n[t];
+        m.n4[t] = n[t] > 0 && aligned16(x[t]) ? n[t] / 4 : 0;  // as nc_hip_sumsq
+    }
+    hipStream_t st = as_stream(stream);
+    if (m.first[count] > 0) hipLaunchKernelGGL(k_sumsq_multi, m.first[count], kSB, 0, st, m, (double *)ws);
+    hipLaunchKernelGGL(k_sumsq_multi_finish, 1, kSB, 0, st, (const double *)ws, m, ss, accumulate ? 1 : 0);
+    return check_launch("nc_hip_sumsq_multi");
+}
+
+extern "C" NC_HIP_API int nc_hip_scale_multi(int count, float *const *x, const int64_t *n, float coef, void *stream) {
+    ScaleMulti m{};
+    // a workgroup per kSB float4 items (kSB floats for a tensor that is not 16-byte aligned)
+    if (!multi_spans("nc_hip_scale_multi", count, n, (const void *const *)x, m.first, [&](int t) {
+            m.vec[t] = aligned16(x[t]) ? 1 : 0;
+            const int64_t items = m.vec[t] ? (n[t] + 3) / 4 : n[t];
+            return (items + kSB - 1) / kSB;
+        }))
+        return NC_HIP_ERR_ARG;
+    m.count = count;
+    for (int t = 0; t < count; t++) {
+        m.x[t] = x[t];
+        m.n[t] = n[t];
+    }
+    if (m.first[count] > 0) hipLaunchKernelGGL(k_scale_multi, m.first[count], kSB, 0, as_stream(stream), m, coef);
+    return check_launch("nc_hip_scale_multi");
 }

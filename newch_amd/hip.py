@@ -68,6 +68,9 @@ SIGNATURES = {
                                         c_float, c_float, c_float, c_int, P]),
     "nc_hip_sumsq_workspace": (c_size_t, [c_int64]),
     "nc_hip_sumsq": (c_int, [c_int64, P, P, c_int, P, c_size_t, P]),
+    "nc_hip_sumsq_multi_workspace": (c_size_t, [c_int, P]),
+    "nc_hip_sumsq_multi": (c_int, [c_int, P, P, P, c_int, P, c_size_t, P]),
+    "nc_hip_scale_multi": (c_int, [c_int, P, P, c_float, P]),
     "nc_hip_loss_workspace": (c_size_t, [c_int64, c_int64]),
     "nc_hip_cross_entropy_fwd": (c_int, [c_int64, c_int64, P, P, P, P, P, P, c_size_t, P]),
     "nc_hip_cross_entropy_bwd": (c_int, [c_int64, c_int64, P, P, P, P, P, c_int, P]),
@@ -202,6 +205,29 @@ class Kernels:
 
     def sumsq(self, n, x, ss, accumulate, ws, ws_bytes, stream=None):
         self._ok(self.lib.nc_hip_sumsq(n, x, ss, int(accumulate), ws, ws_bytes, stream), "sumsq")
+
+    @staticmethod
+    def _tables(tensors):
+        k = max(len(tensors), 1)
+        ptrs, ns = (ctypes.c_void_p * k)(), (ctypes.c_int64 * k)()
+        for i, (x, n) in enumerate(tensors):
+            ptrs[i], ns[i] = x, n
+        return ptrs, ns
+
+    def sumsq_multi_workspace(self, sizes):
+        ns = (ctypes.c_int64 * max(len(sizes), 1))(*sizes)
+        return self.lib.nc_hip_sumsq_multi_workspace(len(sizes), ctypes.addressof(ns))
+
+    def sumsq_multi(self, tensors, ss, accumulate, ws, ws_bytes, stream=None):
+        """tensors: (device address, n) per tensor."""
+        ptrs, ns = self._tables(tensors)
+        self._ok(self.lib.nc_hip_sumsq_multi(len(tensors), ctypes.addressof(ptrs), ctypes.addressof(ns), ss,
+                                             int(accumulate), ws, ws_bytes, stream), "sumsq_multi")
+
+    def scale_multi(self, tensors, coef, stream=None):
+        ptrs, ns = self._tables(tensors)
+        self._ok(self.lib.nc_hip_scale_multi(len(tensors), ctypes.addressof(ptrs), ctypes.addressof(ns), coef,
+                                             stream), "scale_multi")
 
     def loss_workspace(self, N, C):
         return self.lib.nc_hip_loss_workspace(N, C)

@@ -1090,6 +1090,38 @@ def test_engine_clip_grad_norm_golden(eng, case):
     eng.step_end()
 
 
+@pytest.mark.parametrize("max_norm", [1.0, 1e6])
+def test_engine_clip_grad_norm_many(eng, max_norm):
+    """70 parameter slots (a NULL one and one without a gradient among them), so the gradients go to
+    the device in three groups: the norm against fp64, every rescaled gradient bit for bit."""
+    L = eng.lib
+    rng = np.random.default_rng(70)
+    sizes = [int(n) for n in rng.integers(1, 5000, 70)]
+    Gs = [(rng.standard_normal(n) * 0.05).astype(np.float32) for n in sizes]
+    params = [eng.param(np.zeros(n, np.float32)) for n in sizes]
+    loss = None
+    for i, p in enumerate(params):
+        if i == 40:
+            continue  # no gradient
+        term = L.nc_sum(L.nc_mul(p, eng.tensor(Gs[i])), abi.ALL_AXES, 0)
+        loss = term if loss is None else L.nc_add(loss, term)
+    assert L.nc_backward_ex(loss, 0, None, 0) == 0
+    slots = list(params)
+    slots[17] = None
+    arr = (c_void_p * len(slots))(*slots)
+    total = np.float32(L.nc_clip_grad_norm(arr, len(slots), c_float(max_norm)))
+    live = [i for i in range(len(slots)) if i not in (17, 40)]
+    exact = np.sqrt(sum(float(np.sum(Gs[i].astype(np.float64) ** 2)) for i in live))
+    assert abs(float(total) - exact) <= 1e-6 * exact, (total, exact)
+    coef = np.float32(max_norm) / (total + np.float32(1e-6))
+    assert (coef < 1) == (max_norm == 1.0)
+    for i in live:
+        want = (Gs[i] * coef).astype(np.float32) if coef < 1 else Gs[i]
+        assert_bits(eng.grad(params[i]), want, f"grad {i}")
+    assert_bits(eng.grad(params[17]), Gs[17], "grad of the NULL slot's parameter")
+    eng.step_end()
+
+
 def test_engine_optim_state_roundtrip(eng):
     """nc_optim_state's host copy is authoritative until the next step: a value written there is
     what the step uses (checkpoint restore)."""
@@ -1239,6 +1271,83 @@ def test_kernel_sumsq(K, sizes):
     want = sum(O.sumsq(x) for x in xs)
     exact = sum(float(np.sum(x.astype(np.float64) ** 2)) for x in xs)
     assert abs(got - want) <= 1e-12 * max(want, 1.0) and abs(got - exact) <= 1e-12 * max(exact, 1.0)
+
+
+MULTI_SIZES = [(1_000_003, 7, 65536), (0, 5, 0), (1 << 22,), tuple(range(1, 33)),
+               tuple(int(n) for n in np.random.default_rng(32).integers(0, 300_000, 32))]
+
+
+def _multi_tensors(sizes, seed):
+    """Device copies of seeded tensors; every third one starts 4 bytes past a 16-byte boundary."""
+    rng = np.random.default_rng(seed)
+    xs = [(rng.standard_normal(n) * 3).astype(np.float32) for n in sizes]
+    bufs, ptrs = [], []
+    for i, x in enumerate(xs):
+        off = 1 if i % 3 == 2 else 0
+        B = dev(np.concatenate([np.zeros(off, np.float32), x]))
+        bufs.append(B)
+        ptrs.append(B.ptr + 4 * off)
+    return xs, bufs, ptrs
+
+
+@pytest.mark.parametrize("sizes", MULTI_SIZES)
+@pytest.mark.parametrize("accumulate", [False, True])
+def test_kernel_sumsq_multi(K, sizes, accumulate):
+    """Many tensors in one launch: the bits of one nc_hip_sumsq per tensor in turn."""
+    xs, bufs, ptrs = _multi_tensors(sizes, len(sizes))
+    A, B = dev(np.array([123.0], np.float64)), dev(np.array([123.0], np.float64))
+    for i, (p, x) in enumerate(zip(ptrs, xs)):
+        wsb = K.sumsq_workspace(x.size)
+        ws = empty(max(wsb, 8))
+        K.sumsq(x.size, p, A.ptr, accumulate or i > 0, ws.ptr, wsb)
+        sync()
+    wsb = K.sumsq_multi_workspace(list(sizes))
+    assert wsb == sum(K.sumsq_workspace(n) for n in sizes)
+    ws = empty(max(wsb, 8))
+    K.sumsq_multi(list(zip(ptrs, sizes)), B.ptr, accumulate, ws.ptr, wsb)
+    sync()
+    got, want = B.to_numpy(np.float64, 1), A.to_numpy(np.float64, 1)
+    assert got.view(np.uint64)[0] == want.view(np.uint64)[0], (got, want)
+    exact = sum(float(np.sum(x.astype(np.float64) ** 2)) for x in xs) + (123.0 if accumulate else 0.0)
+    assert abs(got[0] - exact) <= 1e-12 * max(exact, 1.0)
+
+
+@pytest.mark.parametrize("sizes", MULTI_SIZES)
+def test_kernel_scale_multi(K, sizes):
+    """Many tensors rescaled in one launch: the unary scale kernel's bits per tensor."""
+    coef = np.float32(0.3712)
+    xs, bufs, ptrs = _multi_tensors(sizes, 7 + len(sizes))
+    K.scale_multi(list(zip(ptrs, sizes)), float(coef))
+    refs = []
+    for x in xs:
+        X, Y = dev(x), empty(max(4 * x.size, 4))
+        if x.size:
+            K.unary_fwd("scale", X.ptr, Y.ptr, x.size, s=float(coef))
+        refs.append(Y)
+    sync()
+    for i, (B, x, Y) in enumerate(zip(bufs, xs, refs)):
+        off = 1 if i % 3 == 2 else 0
+        got = B.to_numpy(np.float32, x.size + off)[off:]
+        assert_bits(got, Y.to_numpy(np.float32, x.size), f"scale_multi[{i}]")
+        assert_bits(got, coef * x, f"scale_multi[{i}] vs numpy")
+
+
+def test_kernel_sum_scale_multi_rejects(K):
+    """Too many tensors, negative sizes, NULL tensors and short workspaces are errors, not launches."""
+    from newch_amd.hip import HipLayerError
+    X, SS = dev(np.zeros(16, np.float32)), dev(np.zeros(1, np.float64))
+    ws = empty(1 << 16)
+    for tensors in ([(X.ptr, 4)] * 33, [(X.ptr, -1)], [(None, 4)]):
+        with pytest.raises(HipLayerError, match="nc_hip_sumsq_multi"):
+            K.sumsq_multi(tensors, SS.ptr, False, ws.ptr, 1 << 16)
+        with pytest.raises(HipLayerError, match="nc_hip_scale_multi"):
+            K.scale_multi(tensors, 0.5)
+    with pytest.raises(HipLayerError, match="workspace"):
+        K.sumsq_multi([(X.ptr, 16)], SS.ptr, False, ws.ptr, 0)
+    K.sumsq_multi([], SS.ptr, False, None, 0)  # no tensor: ss = 0
+    K.scale_multi([], 0.5)
+    sync()
+    assert SS.to_numpy(np.float64, 1)[0] == 0.0
 
 
 # ------------------------------------------------------------------------------------------------
