@@ -106,7 +106,7 @@ def test_no_device_compute_fails_loudly(eng):
         L.nc_clear_error(eng.ctx)
 
 
-def test_off_path_ops_report_not_in_this_build(eng):
+def test_off_path_ops_report_not_in_this_engine(eng):
     L = eng.lib
     a = eng.tensor(np.ones((1, 1, 2, 2), np.float32))
     assert not L.nc_conv2d(a, a, None, 1, 1, 0, 0)
