@@ -716,8 +716,8 @@ def only_mode(K, hm, labels, setup_only=False):
 def main():
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=20)
-    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--steps", type=int, default=500)
+    ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--classes", choices=["all", "none"], default="all")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--only", default=None, help="comma-separated op-class labels: run just those")
