@@ -213,7 +213,7 @@ NC_HIP_API int nc_hip_optim_step_multi(int kind, int count, const nc_hip_opt_par
                                        float weight_decay, float beta1, float beta2, float eps, float gs, float bc1,
                                        float bc2, int eps_inside_sqrt, void *stream);
 /* ss (+)= sum of x[i]^2 in fp64 (one double in device memory), clip_grad_norm's sum
- * (optim.c:219-225); fixed order.  Workspace: nc_hip_sumsq_workspace(n). */
+ * (optim.c:217-223); fixed order.  Workspace: nc_hip_sumsq_workspace(n). */
 NC_HIP_API size_t nc_hip_sumsq_workspace(int64_t n);
 NC_HIP_API int nc_hip_sumsq(int64_t n, const float *x, double *ss, int accumulate, void *ws, size_t ws_bytes,
                             void *stream);

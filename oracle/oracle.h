@@ -100,7 +100,7 @@ enum { OR_OPT_SGD = 0, OR_OPT_ADAM = 1, OR_OPT_ADAMW = 2, OR_OPT_RMSPROP = 3 };
 void or_optim_step(int kind, int64_t n, float *w, const float *g, float *s1, float *s2, float lr, float momentum,
                    float weight_decay, float beta1, float beta2, float eps, float gs, float bc1, float bc2,
                    int eps_inside_sqrt);
-/* sum of squares in double, as clip_grad_norm accumulates it (optim.c:219-225) */
+/* sum of squares in double, as clip_grad_norm accumulates it (optim.c:217-223) */
 double or_sumsq(int64_t n, const float *x);
 
 #ifdef __cplusplus

@@ -356,7 +356,7 @@ def optim_replay(cfg, W, Gs):
 
 
 def clip_grad_norm(grads, max_norm):
-    """(total, scaled grads) as nc_clip_grad_norm (optim.c:219-233): fp64 sum of squares in order."""
+    """(total, scaled grads) as nc_clip_grad_norm (optim.c:216-233): fp64 sum of squares in order."""
     ss = 0.0
     for g in grads:
         ss += sumsq(g)
