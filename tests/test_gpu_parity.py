@@ -562,6 +562,86 @@ def test_kernel_binary_bwd_fused(K, case, ash, aview, bsh, op, accumulate):
         assert_close64(got, base + red, scale + (np.abs(init) if accumulate else 0), f"{case} {op} grad {name}")
 
 
+def _random_bcast_case(seed):
+    """A seeded broadcast problem: output rank 1-6, each operand full, size 1 or absent per dim, a
+    sometimes stored transposed (a permuted view of its own storage)."""
+    rng = np.random.default_rng(seed)
+    nd = int(rng.integers(1, 7))
+    while True:
+        out = [int(rng.choice([1, 2, 3, 5, 8, 13, 64, 100, 257])) for _ in range(nd)]
+        if np.prod(out) <= 300_000:
+            break
+    def operand():
+        lead = int(rng.integers(0, nd))  # leading dims left out
+        return tuple(1 if rng.random() < 0.4 else d for d in out[lead:])
+    ash, bsh = operand(), operand()
+    perm = tuple(rng.permutation(len(ash))) if len(ash) > 1 and rng.random() < 0.35 else None
+    return tuple(out), ash, bsh, perm
+
+
+@pytest.mark.parametrize("seed", range(200))
+def test_kernel_binary_random_shapes(K, seed):
+    """Seeded random broadcasts of every rank up to 6: forward bit for bit against the oracle, both
+    gradients through the per-operand and the fused backward against fp64 (unreduced ones bit for
+    bit), for all four ops."""
+    out_req, ash, bsh, perm = _random_bcast_case(seed)
+    rng = np.random.default_rng(1000 + seed)
+    if perm is None:
+        A = rng.standard_normal(ash).astype(np.float32)
+        a = A
+    else:  # storage in permuted order, a = its transposed view with the logical shape ash
+        inv = np.argsort(perm)
+        A = np.ascontiguousarray(rng.standard_normal(ash).astype(np.float32).transpose(perm))
+        a = A.transpose(inv)
+    B = (0.5 + 1.5 * rng.random(bsh)).astype(np.float32)
+    out_shape = O.broadcast_shape(a.shape, B.shape)
+    n_out = int(np.prod(out_shape))
+    sa = bcast_strides(a.shape, strides_of(a), out_shape)
+    sb = bcast_strides(B.shape, strides_of(B), out_shape)
+    so = [s // 4 for s in np.empty(out_shape, np.float32).strides]
+    sga = bcast_strides(a.shape, [s // 4 for s in np.empty(a.shape, np.float32).strides], out_shape)
+    sgb = bcast_strides(B.shape, [s // 4 for s in np.empty(B.shape, np.float32).strides], out_shape)
+    G = rng.standard_normal(out_shape).astype(np.float32)
+    Ad, Bd, Gd, Od = dev(A), dev(B), dev(G), empty(4 * max(n_out, 1))
+    for op in ("add", "sub", "mul", "div"):
+        what = f"seed {seed} {op} out {tuple(out_shape)} a {ash} perm {perm} b {bsh}"
+        K.binary_fwd(op, out_shape, Ad.ptr, sa, Bd.ptr, sb, Od.ptr, so)
+        sync()
+        assert_bits(Od.to_numpy(np.float32, out_shape), O.binary_fwd(op, a, B), what + " fwd")
+        ta, tb = grad_terms64(op, a, B, G)
+        inits = [rng.standard_normal(a.shape).astype(np.float32), rng.standard_normal(B.shape).astype(np.float32)]
+        # per operand
+        got1 = []
+        for which, sgx in ((0, sga), (1, sgb)):
+            GX = dev(inits[which])
+            wsb = K.binary_bwd_workspace(out_shape, sgx)
+            ws = empty(max(wsb, 1))
+            K.binary_bwd(op, which, out_shape, Gd.ptr, so, Ad.ptr, sa, Bd.ptr, sb, GX.ptr, sgx, ws.ptr, wsb,
+                         accumulate=True)
+            sync()
+            got1.append(GX.to_numpy(np.float32, (a, B)[which].shape))
+        # both from one pass
+        GA, GB = dev(inits[0]), dev(inits[1])
+        wsb = K.binary_bwd2_workspace(out_shape, sga, sgb)
+        ws = empty(max(wsb, 1))
+        K.binary_bwd2(op, out_shape, Gd.ptr, so, Ad.ptr, sa, Bd.ptr, sb, GA.ptr, sga, GB.ptr, sgb, ws.ptr, wsb,
+                      accumulate=True)
+        sync()
+        got2 = [GA.to_numpy(np.float32, a.shape), GB.to_numpy(np.float32, B.shape)]
+        for which, (x, t) in enumerate(((a, ta), (B, tb))):
+            init = inits[which]
+            if tuple(x.shape) == tuple(out_shape):
+                want = O.binary_bwd(op, a, B, G, need_a=which == 0, need_b=which == 1,
+                                    ga0=init if which == 0 else None, gb0=init if which == 1 else None)[which]
+                assert_bits(got1[which], want, f"{what} grad {which}")
+                assert_bits(got2[which], want, f"{what} fused grad {which}")
+            else:
+                red = sum_to(t, x.shape).reshape(x.shape)
+                scale = sum_to(np.abs(t), x.shape).reshape(x.shape) / np.sqrt(max(t.size // max(red.size, 1), 1))
+                assert_close64(got1[which], init + red, scale + np.abs(init), f"{what} grad {which}")
+                assert_close64(got2[which], init + red, scale + np.abs(init), f"{what} fused grad {which}")
+
+
 def test_reductions_deterministic(K):
     """Every fp64 partial is combined in a fixed order: the fused broadcast backward and the LayerNorm
     backward give the same bits on a repeated call."""
