@@ -103,6 +103,21 @@ def np_view(storage, view):
     return v.reshape(view[3]) if view[0] == "t_reshape" else v
 
 
+def random_rows(seed, n, max_el=1_000_000):
+    """Seeded (rows, cols) pairs for the row kernels' sweeps: cols from every register-path width
+    (multiples of 4 up to 4096), odd and just-past-a-boundary widths, and the long-row fallbacks."""
+    rng = np.random.default_rng(seed)
+    widths = [1, 2, 3, 4, 5, 7, 8, 12, 63, 64, 65, 100, 127, 128, 129, 255, 256, 260, 511, 512, 513, 1000, 1020,
+              1024, 1028, 2047, 2048, 2052, 3000, 4092, 4096, 4100, 5000, 8192, 9999]
+    out = []
+    while len(out) < n:
+        c = int(rng.choice(widths))
+        r = int(rng.integers(1, 1500))
+        if r * c <= max_el:
+            out.append((r, c))
+    return out
+
+
 BINARY_CASES = [
     ("bias4d", None), ("row", None), ("outer", None), ("scalar_lhs", None), ("scalar_rhs", None),
     ("cfg2_small", None), ("cfg2_batch_t", ("t", 0, 1)), ("cfg2_inner_strided", ("t_reshape", 1, 2, (5, 6, 1, 8))),
@@ -738,6 +753,11 @@ def test_kernel_binary_bwd_single(K, case, ash, aview, bsh, op, accumulate):
 
 REDUCE_SHAPES = [((4096, 1024), 1), ((3, 1 << 20), 1), ((64, 1000, 33), 1), ((2, 5000, 3), 1), ((1 << 22,), None),
                  ((7, 13), 0), ((1000, 3), 1), ((5, 4097), 1)]
+# seeded random [outer, R, inner] problems reduced over R (inner 1: the row kernels; else columns)
+REDUCE_SHAPES += [((r, c), 1) for r, c in random_rows(15, 12)] + [
+    ((int(o), int(R), int(i)), 1) for o, R, i in zip(np.random.default_rng(16).integers(1, 40, 8),
+                                                      np.random.default_rng(17).integers(1, 3000, 8),
+                                                      np.random.default_rng(18).integers(2, 70, 8))]
 
 
 @pytest.mark.parametrize("shape,axis", REDUCE_SHAPES)
@@ -791,7 +811,7 @@ def test_kernel_reduce(K, shape, axis):
 
 
 @pytest.mark.parametrize("rows,C", [(4096, 1024), (3, 1), (33, 7), (100, 64), (257, 100), (64, 4096), (5, 5000),
-                                    (9, 4098)])
+                                    (9, 4098)] + random_rows(11, 24))
 @pytest.mark.parametrize("log_form", [False, True])
 def test_kernel_softmax(K, rows, C, log_form):
     rng = np.random.default_rng(rows * C + log_form)
@@ -828,7 +848,8 @@ def test_kernel_softmax(K, rows, C, log_form):
     assert_close64(GI.to_numpy(np.float32, (rows, C)), gref, sc, "softmax bwd")
 
 
-@pytest.mark.parametrize("rows,D", [(2048, 1024), (7, 10), (300, 64), (33, 4096), (5, 5000), (17, 333)])
+@pytest.mark.parametrize("rows,D", [(2048, 1024), (7, 10), (300, 64), (33, 4096), (5, 5000), (17, 333)]
+                         + random_rows(12, 24))
 def test_kernel_layer_norm(K, rows, D):
     rng = np.random.default_rng(rows + D)
     x = (rng.standard_normal((rows, D)) * 2 + 0.3).astype(np.float32)
@@ -1000,7 +1021,7 @@ def test_engine_mse_loss(eng):
     eng.step_end()
 
 
-LOSS_SHAPES = [(2048, 1024), (1000, 32), (64, 4096), (300, 100), (17, 8192), (5, 1), (129, 260)]
+LOSS_SHAPES = [(2048, 1024), (1000, 32), (64, 4096), (300, 100), (17, 8192), (5, 1), (129, 260)] + random_rows(13, 16)
 
 
 def ce_prob(x, stats):
@@ -1483,7 +1504,7 @@ def test_engine_ncw1_load_into_parameters(eng, tmp_path):
 
 
 @pytest.mark.parametrize("rows,cols", [(512, 4096), (96, 70), (64, 8192), (33, 10000), (8, 16), (17, 1024), (9, 3072),
-                                       (3, 5120), (40, 256)])
+                                       (3, 5120), (40, 256)] + random_rows(14, 16))
 def test_kernel_quantize(K, rows, cols):
     rng = np.random.default_rng(rows * cols)
     w = (rng.standard_normal((rows, cols)) * 0.02).astype(np.float32)
@@ -1493,8 +1514,8 @@ def test_kernel_quantize(K, rows, cols):
     if rows > 3:
         w[1, : min(cols, 9)] = [127.0, 0.5, 1.5, 2.5, -0.5, -1.5, -2.5, 126.5, -126.5][: min(cols, 9)]
         w[1, 9:] = 0.25
-        w[2, 1] = np.nan
-        w[3, 2] = np.inf
+        w[2, min(1, cols - 1)] = np.nan
+        w[3, min(2, cols - 1)] = np.inf
     Wd = dev(w)
     Q = empty(rows * cols)
     S = empty(4 * rows)
