@@ -1654,11 +1654,25 @@ def test_engine_linear_int8_errors(eng):
     eng.step_end()
 
 
+def random_gemms(seed, n, max_mnk=3e9):
+    """Seeded (M, N, K) triples over the tile regimes: tiny, single-tile, ragged edges, the 128- and
+    256-wide tiles and K tails (K % 16, % 128 != 0)."""
+    rng = np.random.default_rng(seed)
+    dims = [1, 2, 3, 7, 16, 31, 64, 100, 127, 128, 129, 255, 256, 257, 300, 511, 512, 640, 1000, 1024, 1031,
+            2048, 2100, 3000, 4096]
+    out = []
+    while len(out) < n:
+        m, nn, k = (int(rng.choice(dims)) for _ in range(3))
+        if m * nn * k <= max_mnk:
+            out.append((m, nn, k))
+    return out
+
+
 S8_SIZES = [(1, 1, 16), (5, 6, 37), (128, 128, 64), (300, 260, 1040), (257, 129, 1000), (33, 517, 80), (7, 3, 0),
             (2048, 1024, 4096),
             # >= 256 tiles of 256 x 256: the direct-to-LDS kernel (K % 128 == 0; partial edge tiles) and,
             # with K % 128 != 0, the register-staged 256 x 256 kernel
-            (4100, 4000, 512), (4096, 4352, 1040), (4096, 4096, 576)]
+            (4100, 4000, 512), (4096, 4352, 1040), (4096, 4096, 576)] + random_gemms(21, 16)
 
 
 def _rows_sample(M, n=48, seed=0):
@@ -1704,7 +1718,8 @@ def test_kernel_gemm_s8_leading_dims(K):
 
 
 QLIN_SIZES = [(7, 70, 13, True), (37, 128, 70, False), (300, 1024, 520, True), (129, 4000, 257, True),
-              (8192, 4096, 4096, True), (1, 64, 1, False), (5, 0, 3, True)]
+              (8192, 4096, 4096, True), (1, 64, 1, False), (5, 0, 3, True)] + [
+    (m, k, nn, bool(i % 2)) for i, (m, nn, k) in enumerate(random_gemms(22, 10))]
 
 
 @pytest.mark.parametrize("M,Kd,N,has_b", QLIN_SIZES)
@@ -1738,7 +1753,8 @@ GEMM_F32 = [(0, 0, 1000, 500, 300), (1, 0, 257, 129, 1000), (0, 1, 64, 4096, 512
             (0, 0, 4100, 4096, 256), (0, 1, 4100, 4096, 256), (1, 0, 4100, 4096, 256), (1, 1, 4100, 4096, 256),
             (0, 0, 4096, 4100, 256),
             # 256 x 256 tiles through registers: a K tail (16-byte loads) and an unaligned transposed A
-            (0, 1, 4096, 4096, 250), (1, 1, 4099, 4096, 256)]
+            (0, 1, 4096, 4096, 250), (1, 1, 4099, 4096, 256)] + [
+    (i % 2, (i // 2) % 2, m, nn, k) for i, (m, nn, k) in enumerate(random_gemms(23, 16))]
 
 
 @pytest.mark.parametrize("ta,tb,M,N,Kd", GEMM_F32)
