@@ -445,7 +445,9 @@ KINDS = ["relu", "leaky_relu", "relu6", "hardsigmoid", "hardswish", "silu", "gel
 
 
 @pytest.mark.parametrize("kind", KINDS)
-@pytest.mark.parametrize("n,offset", [(1_000_003, 0), (4099, 1), (7, 0)])
+@pytest.mark.parametrize("n,offset", [(1_000_003, 0), (4099, 1), (7, 0)] + [
+    (int(n), int(o)) for n, o in zip(np.random.default_rng(31).integers(1, 300_000, 6),
+                                     np.random.default_rng(32).integers(0, 4, 6))])
 def test_kernel_unary(K, kind, n, offset):
     rng = np.random.default_rng(n + len(kind))
     x = np.concatenate([SPECIAL, (rng.standard_normal(n) * 4).astype(np.float32)])[:n].astype(np.float32)
@@ -1318,7 +1320,9 @@ OPT_KERNEL_CASES = [("sgd", False, False, False), ("sgd", True, False, False), (
 
 
 @pytest.mark.parametrize("kind,s1,s2,inside", OPT_KERNEL_CASES)
-@pytest.mark.parametrize("n,offset", [(1_000_003, 0), (4097, 1)])
+@pytest.mark.parametrize("n,offset", [(1_000_003, 0), (4097, 1)] + [
+    (int(n), int(o)) for n, o in zip(np.random.default_rng(33).integers(1, 200_000, 4),
+                                     np.random.default_rng(34).integers(0, 4, 4))])
 def test_kernel_optim_step(K, kind, s1, s2, n, offset, inside):
     """Three updates at a large and a misaligned size, bit for bit against the oracle."""
     rng = np.random.default_rng(zlib.crc32(f"opt/{kind}/{s1}/{s2}/{n}".encode()))
