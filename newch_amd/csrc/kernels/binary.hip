@@ -685,7 +685,17 @@ __global__ __launch_bounds__(kB) void k_grad_finalize(const double *__restrict__
     int64_t ko[4];
     offsets<4>(kept, mi, ko);
     double t = ACC ? (double)gx[ko[3]] : 0.0;
-    for (uint32_t p = 0; p < P; p++) t += part[(size_t)p * M + mi];
+    // the partials in order, their loads issued kU at a time (49 partials: 9.5 -> ~2 us)
+    constexpr uint32_t kU = 8;
+    uint32_t p = 0;
+    for (; p + kU <= P; p += kU) {
+        double v[kU];
+#pragma unroll
+        for (uint32_t u = 0; u < kU; u++) v[u] = part[(size_t)(p + u) * M + mi];
+#pragma unroll
+        for (uint32_t u = 0; u < kU; u++) t += v[u];
+    }
+    for (; p < P; p++) t += part[(size_t)p * M + mi];
     gx[ko[3]] = (float)t;
 }
 

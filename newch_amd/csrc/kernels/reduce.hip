@@ -318,12 +318,23 @@ __global__ __launch_bounds__(kRB) void k_cols_combine(const float *__restrict__ 
     for (int64_t c = (int64_t)blockIdx.x * kRB + threadIdx.x; c < cols; c += (int64_t)gridDim.x * kRB) {
         Acc<KIND> acc;
         acc.init();
-        for (int p = 0; p < P; p++) {
-            Acc<KIND> t;
-            t.init();
-            if constexpr (KIND == NC_HIP_RED_SUM || KIND == NC_HIP_RED_MEAN) t.sum = psum[(int64_t)p * cols + c];
-            else t.a = parg[(int64_t)p * cols + c];
-            acc.combine(t);
+        // the partials in order, their loads issued kU at a time
+        constexpr int kU = 8;
+        for (int p0 = 0; p0 < P; p0 += kU) {
+            Acc<KIND> t[kU];
+#pragma unroll
+            for (int u = 0; u < kU; u++) {
+                t[u].init();
+                if (p0 + u < P) {
+                    if constexpr (KIND == NC_HIP_RED_SUM || KIND == NC_HIP_RED_MEAN)
+                        t[u].sum = psum[(int64_t)(p0 + u) * cols + c];
+                    else
+                        t[u].a = parg[(int64_t)(p0 + u) * cols + c];
+                }
+            }
+#pragma unroll
+            for (int u = 0; u < kU; u++)
+                if (p0 + u < P) acc.combine(t[u]);
         }
         const int64_t o = c / inner, i = c % inner;
         emit<KIND>(acc, x[o * R * inner + i], scale, y, arg, c);
