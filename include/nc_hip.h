@@ -232,8 +232,9 @@ NC_HIP_API int nc_hip_scale_multi(int count, float *const *x, const int64_t *n, 
 
 /* Row-major fp32 GEMM: C = alpha * op(A) op(B) + beta * C, op(X) = X^T when its flag is set; op(A) is
  * M x K, op(B) K x N, leading dims in elements.  The reference's gemm_f32 (kernels.h:36-41) as used by
- * matmul / linear (ops_linalg.c:64-99,296-330); dense GEMM on the matrix cores through rocBLAS,
- * deterministic.  The batched form takes device arrays of `count` matrix pointers. */
+ * matmul / linear (ops_linalg.c:64-99,296-330); hand-written fp32 matrix-core kernels, each output
+ * summing its K products in one fixed order (the same for every tile size, grid and device).  The
+ * batched form takes device arrays of `count` matrix pointers. */
 NC_HIP_API int nc_hip_gemm_f32(int ta, int tb, int64_t M, int64_t N, int64_t K, float alpha, const float *A,
                                int64_t lda, const float *B, int64_t ldb, float beta, float *C, int64_t ldc,
                                void *stream);
@@ -244,8 +245,8 @@ NC_HIP_API int nc_hip_gemm_f32_batched(int ta, int tb, int64_t M, int64_t N, int
  * of the batch shape bshape[nb], C_i = op(A_i) op(B_i) + beta C_i with A_i = A + sum_d idx_d sa[d]
  * (likewise B, C; stride 0 = broadcast).  When several batch indices share one C block (sc has a 0 on
  * a dim > 1, a broadcast operand's gradient) they run in batch order, each adding into the block; the
- * others run as one batched rocBLAS call.  Workspace: device pointer arrays (0 bytes when the batch
- * dims collapse to one uniform stride). */
+ * others run as one launch that decodes the batch strides per workgroup.  Workspace: none
+ * (nc_hip_gemm_f32_bmm_workspace returns 0; the argument pair is kept for callers that pass one). */
 NC_HIP_API size_t nc_hip_gemm_f32_bmm_workspace(int64_t count);
 NC_HIP_API int nc_hip_gemm_f32_bmm(int ta, int tb, int64_t M, int64_t N, int64_t K, const float *A, int64_t lda,
                                    const float *B, int64_t ldb, float beta, float *C, int64_t ldc, int nb,

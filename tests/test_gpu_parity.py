@@ -1827,8 +1827,8 @@ def test_kernel_gemm_f32(K, ta, tb, M, N, Kd):
 
 
 def test_kernel_gemm_f32_strided_batch_aligned_and_deterministic(K):
-    """A strided batch with 16-byte aligned rows (the hipBLASLt path, B a transposed view as in
-    attention scores): within the GEMM tolerance of fp64, and bit-identical when run again."""
+    """A strided batch with 16-byte aligned rows (B a transposed view, as in attention scores):
+    within the GEMM tolerance of fp64, and bit-identical when run again."""
     rng = np.random.default_rng(17)
     Bc, M, N, Kd = 6, 64, 96, 128
     A = rng.standard_normal((Bc, M, Kd)).astype(np.float32)
