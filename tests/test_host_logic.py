@@ -58,6 +58,17 @@ def test_kernel_layer_binds(lib):
     hip.bind(ctypes.CDLL(str(abi.LIB_PATH)))
 
 
+def test_multi_tensor_workspace_queries(lib):
+    """Host-only queries of the multi-tensor entry points: the sum-of-squares workspace of a table is
+    the sum of its tensors' one-tensor workspaces (no device needed)."""
+    from newch_amd import hip
+    K = hip.Kernels(ctypes.CDLL(str(abi.LIB_PATH)))
+    sizes = [0, 1, 7, 65536, 1_000_003, 1 << 26]
+    assert K.sumsq_multi_workspace(sizes) == sum(K.sumsq_workspace(n) for n in sizes)
+    assert K.sumsq_multi_workspace([]) == 0
+    assert K.sumsq_workspace(0) == 0 and K.sumsq_workspace(1) >= 8
+
+
 def test_index_divider_matches_integer_division(lib):
     from newch_amd import hip
     L = hip.bind(ctypes.CDLL(str(abi.LIB_PATH)))
