@@ -281,6 +281,55 @@ def test_engine_reduce_golden(eng, case):
         eng.step_end()
 
 
+@pytest.mark.parametrize("seed", range(40 * SWEEP))
+def test_engine_reduce_random(eng, seed):
+    """Seeded random tensors (rank 1-4, values on a quarter grid so maxima tie, sometimes a transposed
+    view) reduced through nc.h over a random axis or all of them: sum / mean within the bar of fp64,
+    max / argmax and every gradient bit for bit against the oracle."""
+    rng = np.random.default_rng(3000 + seed)
+    nd = int(rng.integers(1, 5))
+    while True:
+        shape = tuple(int(rng.choice([1, 2, 3, 5, 17, 64, 100, 257])) for _ in range(nd))
+        if np.prod(shape) <= 200_000:
+            break
+    view, store = None, shape
+    if nd > 1 and rng.random() < 0.5:
+        i, j = sorted(int(v) for v in rng.choice(nd, 2, replace=False))
+        st = list(shape)
+        st[i], st[j] = st[j], st[i]
+        view, store = ("t", i, j), tuple(st)
+    X = (np.round(rng.standard_normal(store) * 4) / 4).astype(np.float32)
+    x = np.ascontiguousarray(np_view(X, view))
+    L = eng.lib
+    axis = int(rng.integers(0, nd)) if rng.random() < 0.8 else abi.ALL_AXES
+    ax = None if axis == abi.ALL_AXES else axis
+    what = f"seed {seed} shape {shape} view {view} axis {axis}"
+    for kind, fn in (("sum", L.nc_sum), ("mean", L.nc_mean), ("max", L.nc_max)):
+        p = eng.param(X)
+        v = eng.view(p, view)
+        out = fn(v, axis, 0)
+        y = eng.read(out)
+        want, arg = O.reduce_fwd("max" if kind == "max" else kind, x, ax)
+        if kind == "max":
+            assert_bits(y, want.reshape(y.shape), f"{what} max")
+        else:
+            X64 = x.astype(np.float64)
+            ref64 = X64.sum(axis=ax) if kind == "sum" else X64.mean(axis=ax)
+            n = x.size if ax is None else x.shape[ax]
+            scale = np.abs(X64).sum(axis=ax) / (np.sqrt(n) if kind == "sum" else n * np.sqrt(n))
+            assert_close64(y, ref64, scale, f"{what} {kind}")
+        G = rng.standard_normal(y.shape).astype(np.float32)
+        eng.backward_with(out, G)
+        _, arg = O.reduce_fwd("max", x, ax)
+        assert_bits(eng.grad(v), O.reduce_bwd(kind, x.shape, ax, G, arg), f"{what} {kind} grad")
+        eng.step_end()
+    p = eng.param(X)
+    got = eng.read(L.nc_argmax(eng.view(p, view), axis))
+    want, _ = O.reduce_fwd("argmax", x, ax)
+    assert_bits(got.reshape(-1).astype(np.int64), want.astype(np.int64), f"{what} argmax")
+    eng.step_end()
+
+
 def test_engine_reduce_empty(eng):
     L = eng.lib
     e = eng.tensor(np.zeros((0, 3), np.float32))
