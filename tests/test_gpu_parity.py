@@ -368,6 +368,67 @@ def test_engine_softmax_golden(eng, key):
         eng.step_end()
 
 
+@pytest.mark.parametrize("seed", range(30 * SWEEP))
+def test_engine_rowops_random(eng, K, seed):
+    """Seeded random tensors (rank 2-4, last dims across the register-path widths) through nc.h, a
+    transposed view where one is drawn (its rows gathered by the engine): softmax, log_softmax and
+    LayerNorm outputs and gradients bit for bit equal to the kernel layer on the contiguous copy."""
+    rng = np.random.default_rng(4000 + seed)
+    nd = int(rng.integers(2, 5))
+    while True:
+        shape = [int(rng.choice([1, 2, 3, 5, 17, 64])) for _ in range(nd - 1)]
+        shape.append(int(rng.choice([1, 4, 7, 64, 100, 256, 1000, 1024, 2048, 4096, 5000])))
+        if np.prod(shape) <= 300_000:
+            break
+    shape = tuple(shape)
+    view, store = None, shape
+    if rng.random() < 0.5:
+        i, j = sorted(int(v) for v in rng.choice(nd, 2, replace=False))
+        st = list(shape)
+        st[i], st[j] = st[j], st[i]
+        view, store = ("t", i, j), tuple(st)
+    X = (rng.standard_normal(store) * 2).astype(np.float32)
+    x = np.ascontiguousarray(np_view(X, view))
+    C = shape[-1]
+    rows = x.size // C
+    G = rng.standard_normal(shape).astype(np.float32)
+    L = eng.lib
+    what = f"seed {seed} shape {shape} view {view}"
+    for form, fn in (("softmax", L.nc_softmax), ("log_softmax", L.nc_log_softmax)):
+        p = eng.param(X)
+        v = eng.view(p, view)
+        out = fn(v)
+        y = eng.read(out)
+        Xd, Yd, Gd, GI = dev(x), empty(x.nbytes), dev(G), dev(np.zeros(shape, np.float32))
+        K.softmax_fwd(form == "log_softmax", rows, C, Xd.ptr, Yd.ptr)
+        K.softmax_bwd(form == "log_softmax", rows, C, Yd.ptr, Gd.ptr, GI.ptr, accumulate=True)
+        sync()
+        assert_bits(y, Yd.to_numpy(np.float32, shape), f"{what} {form} fwd")
+        eng.backward_with(out, G)
+        assert_bits(eng.grad(v), GI.to_numpy(np.float32, shape), f"{what} {form} bwd")
+        eng.step_end()
+    w = (1 + 0.1 * rng.standard_normal(C)).astype(np.float32)
+    b = (0.1 * rng.standard_normal(C)).astype(np.float32)
+    p, pw, pb = eng.param(X), eng.param(w), eng.param(b)
+    v = eng.view(p, view)
+    out = L.nc_layer_norm(v, 1, pw, pb, c_float(1e-5))
+    y = eng.read(out)
+    Xd, Wd, Bd, Gd = dev(x), dev(w), dev(b), dev(G)
+    Yd, Sd = empty(x.nbytes), empty(8 * rows)
+    K.layer_norm_fwd(rows, C, Xd.ptr, Wd.ptr, Bd.ptr, 1e-5, Yd.ptr, Sd.ptr)
+    GX, GW, GB = dev(np.zeros(shape, np.float32)), dev(np.zeros(C, np.float32)), dev(np.zeros(C, np.float32))
+    wsb = K.layer_norm_bwd_workspace(rows, C)
+    ws = empty(max(wsb, 1))
+    K.layer_norm_bwd(rows, C, Xd.ptr, Wd.ptr, Sd.ptr, Gd.ptr, GX.ptr, GW.ptr, GB.ptr, ws.ptr, wsb, accumulate=True)
+    sync()
+    assert_bits(y, Yd.to_numpy(np.float32, shape), f"{what} layer_norm fwd")
+    eng.backward_with(out, G)
+    assert_bits(eng.grad(v), GX.to_numpy(np.float32, shape), f"{what} layer_norm dx")
+    assert_bits(eng.grad(pw), GW.to_numpy(np.float32, C), f"{what} layer_norm dw")
+    assert_bits(eng.grad(pb), GB.to_numpy(np.float32, C), f"{what} layer_norm db")
+    eng.step_end()
+
+
 @pytest.mark.parametrize("key", ["6x10", "3x4x5", "4x1024", "2x3"])
 def test_engine_layer_norm_golden(eng, key):
     d = load("layernorm")
