@@ -92,6 +92,40 @@ UNARY = [("relu", 0.0), ("leaky_relu", 0.01), ("leaky_relu_02", 0.2), ("relu6", 
          ("exp", 0.0)]
 
 
+@pytest.mark.parametrize("seed", range(36 * SWEEP))
+def test_engine_unary_random(eng, seed):
+    """Each activation (in turn by seed) on a seeded random tensor of rank 1-4, through nc.h, often a
+    transposed view: forward and gradient bit for bit against the oracle on the contiguous copy."""
+    name, sv = UNARY[seed % len(UNARY)]
+    rng = np.random.default_rng(5000 + seed)
+    nd = int(rng.integers(1, 5))
+    while True:
+        shape = tuple(int(rng.choice([1, 2, 3, 5, 17, 64, 100, 257, 1000])) for _ in range(nd))
+        if np.prod(shape) <= 400_000:
+            break
+    view, store = None, shape
+    if nd > 1 and rng.random() < 0.6:
+        i, j = sorted(int(v) for v in rng.choice(nd, 2, replace=False))
+        st = list(shape)
+        st[i], st[j] = st[j], st[i]
+        view, store = ("t", i, j), tuple(st)
+    X = (rng.standard_normal(store) * 4).astype(np.float32)
+    x = np.ascontiguousarray(np_view(X, view))
+    G = rng.standard_normal(shape).astype(np.float32)
+    kind = "leaky_relu" if name.startswith("leaky") else name
+    L = eng.lib
+    p = eng.param(X)
+    v = eng.view(p, view)
+    out = eng.UNARY_CALLS[name](L, v, sv)
+    y = eng.read(out)
+    what = f"seed {seed} {name} shape {shape} view {view}"
+    y_o = O.unary_fwd(kind, x, sv)
+    assert_bits(y, y_o, what + " fwd")
+    eng.backward_with(out, G)
+    assert_bits(eng.grad(v), O.unary_bwd(kind, x, y_o, G, None, sv), what + " bwd")
+    eng.step_end()
+
+
 @pytest.mark.parametrize("name,s", UNARY)
 def test_engine_unary_golden(eng, name, s):
     d = load("unary")
