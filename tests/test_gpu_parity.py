@@ -1179,6 +1179,59 @@ def test_engine_loss_golden(eng, key):
         eng.step_end()
 
 
+@pytest.mark.parametrize("seed", range(24 * SWEEP))
+def test_engine_loss_quantize_random(eng, K, seed):
+    """Seeded random logits [N, C] (often a transposed view of their storage) through nc.h: the
+    cross-entropy loss and gradient and the nll losses and gradients equal to the kernel layer on the
+    contiguous copy, bit for bit; quantize_rows of the same view likewise."""
+    rng = np.random.default_rng(6000 + seed)
+    N = int(rng.choice([1, 3, 17, 64, 300, 1000]))
+    C = int(rng.choice([1, 4, 7, 12, 64, 100, 256, 1000, 1024]))
+    view, store = (("t", 0, 1), (C, N)) if rng.random() < 0.5 else (None, (N, C))
+    X = (rng.standard_normal(store) * 3).astype(np.float32)
+    x = np.ascontiguousarray(np_view(X, view))
+    lab = rng.integers(0, C, N).astype(np.int32)
+    gl = np.float32(rng.standard_normal())
+    L = eng.lib
+    what = f"seed {seed} N {N} C {C} view {view}"
+    # the kernel layer on the contiguous copy
+    Xd, Ld = dev(x), dev(lab)
+    S, LS, BAD = empty(8 * N), empty(4), empty(8)
+    wsb = K.loss_workspace(N, C)
+    ws = empty(max(wsb, 8))
+    K.cross_entropy_fwd(N, C, Xd.ptr, Ld.ptr, S.ptr, LS.ptr, BAD.ptr, ws.ptr, wsb)
+    GO, GI = dev(np.array([gl], np.float32)), dev(np.zeros((N, C), np.float32))
+    K.cross_entropy_bwd(N, C, Xd.ptr, S.ptr, Ld.ptr, GO.ptr, GI.ptr, accumulate=True)
+    sync()
+    p = eng.param(X)
+    v = eng.view(p, view)
+    out = L.nc_cross_entropy(v, eng.tensor(lab))
+    assert_bits(eng.read(out), LS.to_numpy(np.float32, 1).reshape(()), what + " ce loss")
+    eng.backward_with(out, np.asarray(gl))
+    assert_bits(eng.grad(v), GI.to_numpy(np.float32, (N, C)), what + " ce grad")
+    eng.step_end()
+    for sum_ in (False, True):
+        K.nll_loss_fwd(N, C, Xd.ptr, Ld.ptr, sum_, LS.ptr, BAD.ptr, ws.ptr, wsb)
+        GI = dev(np.zeros((N, C), np.float32))
+        K.nll_loss_bwd(N, C, Ld.ptr, GO.ptr, sum_, GI.ptr)
+        sync()
+        p = eng.param(X)
+        v = eng.view(p, view)
+        out = L.nc_nll_loss(v, eng.tensor(lab), int(sum_))
+        assert_bits(eng.read(out), LS.to_numpy(np.float32, 1).reshape(()), f"{what} nll sum={sum_} loss")
+        eng.backward_with(out, np.asarray(gl))
+        assert_bits(eng.grad(v), GI.to_numpy(np.float32, (N, C)), f"{what} nll sum={sum_} grad")
+        eng.step_end()
+    Q, Sc = empty(N * C), empty(4 * N)
+    K.quantize_rows(N, C, Xd.ptr, Q.ptr, Sc.ptr)
+    sync()
+    sc = ctypes.c_void_p()
+    q = L.nc_quantize_rows(eng.view(eng.param(X), view), ctypes.byref(sc))
+    assert_bits(eng.read(q), Q.to_numpy(np.int8, (N, C)), what + " quantize q")
+    assert_bits(eng.read(sc.value), Sc.to_numpy(np.float32, N), what + " quantize scale")
+    eng.step_end()
+
+
 @pytest.mark.parametrize("which", ["high", "negative"])
 def test_engine_loss_bad_label(eng, which):
     """An out-of-range label fails the call with the reference's status and message."""
