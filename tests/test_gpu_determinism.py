@@ -175,3 +175,28 @@ def test_losses_independent_of_cus(K, N, C):
         return LS.to_numpy(np.float32, 1), NL.to_numpy(np.float32, 1), S.to_numpy(np.float32, (N, 2))
 
     across_cus(K, run)
+
+
+# fp32 GEMM: the tile size follows the CU count (256 x 256 tiles when they give every CU one, else
+# 128 x 128 or 64 x 64), and every tile size sums an output's K products in the same order, so the
+# bits do not change; shapes straddle the tile-size thresholds for 32 .. 1024 CUs, with K below and
+# above the direct-to-LDS threshold and a ragged one
+GEMM = [(1024, 1024, 512, 0, 1), (2048, 1536, 256, 0, 0), (512, 768, 1040, 1, 1), (3000, 1000, 300, 1, 0),
+        (4096, 2048, 64, 0, 1)]
+
+
+@pytest.mark.parametrize("M,N,Kd,ta,tb", GEMM)
+def test_gemm_f32_independent_of_cus(K, M, N, Kd, ta, tb):
+    rng = np.random.default_rng(M + N + Kd)
+    A = rng.standard_normal((Kd, M) if ta else (M, Kd)).astype(np.float32)
+    B = rng.standard_normal((N, Kd) if tb else (Kd, N)).astype(np.float32)
+    C0 = rng.standard_normal((M, N)).astype(np.float32)
+    Ad, Bd = dev(A), dev(B)
+
+    def run():
+        Cd = dev(C0)
+        K.gemm_f32(ta, tb, M, N, Kd, 0.5, Ad.ptr, A.shape[1], Bd.ptr, B.shape[1], 1.0, Cd.ptr, N)
+        sync()
+        return (Cd.to_numpy(np.float32, (M, N)),)
+
+    across_cus(K, run)
