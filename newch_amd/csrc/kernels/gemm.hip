@@ -18,37 +18,50 @@
 // k mapping.  One MFMA multiplies a 16 x 4 slice of A by a 4 x 16 slice of B, quarter-wave q (lanes
 // 16 q .. 16 q + 15) holding one k.  In each stage of 16 k, quarter q gives the s-th MFMA (s = 0..3)
 // the value at k = 4 q + s, for A and B alike, so a K-contiguous operand feeds four MFMAs from one
-// 16-byte LDS read.  Each k enters every output element exactly once, four products per instruction
-// (K / 4 roundings into the accumulator), and the order of the sum is a property of the kernel
-// alone: the same for every tile size and grid, so results are identical run to run and on any
+// 16-byte LDS read.
+//
+// Summation order (blocked like the reference's KC = 256 panels, kernels_avx2.c:234-247): K is cut
+// into panels of 256 k (16 stages).  Each panel's products are summed from zero in the accumulator
+// tiles, four per MFMA (64 roundings per panel); the first panel's sum is the running total and each
+// later panel's sum is added into it (one fp32 add per panel).  A small panel sum is not rounded
+// against the whole running total, so the error of a K-term dot product grows like that of the
+// reference's blocked sum rather than like K sequential additions.  The order is a property of the
+// kernel alone: the same for every tile size and grid, so results are identical run to run and on any
 // device.  It differs from the reference's serial order, so the parity bar is the fp32 error bound of
 // a K-term dot product.
 //
-// Tile sizes: 256 x 256 (8 waves of 8 x 4 tiles) when the problem has at least as many such tiles as
-// the device has CUs, else 128 x 128 (4 waves of 4 x 4) or 64 x 64 (4 waves of 2 x 2).  Blocks are
-// remapped so each XCD (blocks b with b % 8 equal) works a contiguous run of tiles, and tiles run in
-// groups of 8 tile-rows so neighbouring blocks share panels in L2.
+// Tile sizes: 256 x 256 (8 waves of 8 x 4 tiles) for single-panel problems (K <= 256) that have at
+// least as many such tiles as the device has CUs; 256 x 128 (8 waves of 4 x 4 tiles, whose running
+// totals fit beside the panel accumulators) for larger K; else 128 x 128 (4 waves of 4 x 4) or 64 x 64
+// (4 waves of 2 x 2).  Blocks are remapped so each XCD (blocks b with b % 8 equal) works a contiguous
+// run of tiles, and tiles run in groups of 8 tile-rows so neighbouring blocks share panels in L2.
 #include "common.hpp"
 
 namespace nchip {
 
 
 constexpr int kSgBK = 16;      // k per stage
+constexpr int kSgPanel = 16;   // stages per summation panel (256 k)
 constexpr int kSgGroupM = 8;   // tile-rows per group in the block order
 
-template <int TM_, int TN_, int WGM_, int WGN_>
+// TOTAL: the kernel keeps a running total beside the panel accumulators (more than one panel);
+// MINB: workgroups per CU the register allocation leaves room for
+template <int TM_, int TN_, int WGM_, int WGN_, bool TOTAL_, int MINB_>
 struct SgCfg {
     static constexpr int TM = TM_, TN = TN_, WGM = WGM_, WGN = WGN_;
+    static constexpr bool TOTAL = TOTAL_;
+    static constexpr int MINB = MINB_;
     static constexpr int NT = 64 * WGM * WGN;
     static constexpr int BM = 16 * TM * WGM, BN = 16 * TN * WGN;
-    // bytes of one operand panel in LDS (the larger of the two layouts)
-    static constexpr int SLAB_A = 64 * BM + 256, SLAB_B = 64 * BN + 256;
+    // bytes of one stage of an operand panel in LDS (R rows by 16 k, either layout)
+    static constexpr int SLAB_A = 64 * BM, SLAB_B = 64 * BN;
     static constexpr int STAGE = SLAB_A + SLAB_B;
     static constexpr size_t LDS = 2 * (size_t)STAGE;
 };
-using SgBig = SgCfg<8, 4, 2, 4>;    // 256 x 256
-using SgMid = SgCfg<4, 4, 2, 2>;    // 128 x 128
-using SgSmall = SgCfg<2, 2, 2, 2>;  // 64 x 64
+using SgBig = SgCfg<8, 4, 2, 4, false, 1>;  // 256 x 256, K <= 256 only
+using SgWide = SgCfg<4, 4, 4, 2, true, 1>;  // 256 x 128
+using SgMid = SgCfg<4, 4, 2, 2, true, 2>;   // 128 x 128
+using SgSmall = SgCfg<2, 2, 2, 2, true, 4>; // 64 x 64
 
 struct SgBatch {
     int nb;  // 0: one matrix per operand
@@ -75,8 +88,10 @@ struct SgArgs {
 //   * K-contiguous operand: chunk u is row u / 4, k 4 (u % 4) .. + 3; in LDS rows of 64 bytes, logical
 //     chunk c of row r at chunk c ^ kc_swz(r), so the 16-byte fragment reads spread over all banks;
 //   * M/N-contiguous operand: chunk u is k-row u / (R / 4), rows 4 (u % (R / 4)) .. + 3; in LDS 16
-//     k-rows of R floats with a pitch of R + 4, so the four quarter-waves' fragment reads (k-rows k,
-//     k + 4, k + 8, k + 12 of 16 consecutive rows) land in different banks.
+//     k-rows of R floats (R >= 64), the chunk of rows 4 c .. 4 c + 3 of k-row k at chunk c ^ mn_swz(k),
+//     so the four quarter-waves' fragment reads (k-rows k, k + 4, k + 8, k + 12 of 16 consecutive
+//     rows) land in different banks.  Either layout is 64 R bytes per stage, with no padding, so a
+//     load straight into LDS fills it 1 KiB at a time.
 template <int R, bool KC, int NT>
 struct Panel {
     static constexpr int UNITS = 4 * R;
@@ -126,6 +141,11 @@ __device__ __forceinline__ f4 load4(const float *p, int64_t ld, int rows, int K,
 // conflicts (SQ_LDS_BANK_CONFLICT reads 0; (r >> 2) & 3 read a third to a half of the LDS cycles).
 __device__ __forceinline__ int kc_swz(int r) { return (r >> 1) & 3; }
 
+// The chunk permutation of M/N-contiguous panel k-row k: quarter-wave q reads k-rows 4 q .. 4 q + 3,
+// so XOR-ing bits 2-3 of the chunk index with q puts the four quarters' 16 rows in four disjoint
+// groups of 16 banks (the 64 banks of 4 bytes, since a k-row's 4 R bytes are a multiple of 256).
+__device__ __forceinline__ int mn_swz(int k) { return ((k >> 2) & 3) << 2; }
+
 // LDS store of one chunk
 template <int R, bool KC>
 __device__ __forceinline__ void unit_store(char *slab, int u, f4 v) {
@@ -135,7 +155,7 @@ __device__ __forceinline__ void unit_store(char *slab, int u, f4 v) {
         const int c = k >> 2;
         *(f4 *)(slab + row * 64 + ((c ^ kc_swz(row)) << 4)) = v;
     } else {
-        *(f4 *)(slab + k * (R + 4) * 4 + row * 4) = v;
+        *(f4 *)(slab + k * R * 4 + (((row >> 2) ^ mn_swz(k)) << 4)) = v;
     }
 }
 
@@ -145,8 +165,9 @@ __device__ __forceinline__ f4 fragment(const char *slab, int r, int q) {
     if constexpr (KC) {
         return *(const f4 *)(slab + r * 64 + ((q ^ kc_swz(r)) << 4));
     } else {
-        const float *b = (const float *)slab + 4 * q * (R + 4) + r;
-        return f4{b[0], b[R + 4], b[2 * (R + 4)], b[3 * (R + 4)]};
+        static_assert(R >= 64, "the k-row permutation needs 16 chunks");
+        const float *b = (const float *)slab + 4 * q * R + 4 * ((r >> 2) ^ (q << 2)) + (r & 3);
+        return f4{b[0], b[R], b[2 * R], b[3 * R]};
     }
 }
 
@@ -272,6 +293,38 @@ __device__ __forceinline__ void stage_mfma(const char *cur, f4 (&acc)[Cfg::TM][C
     mfma_steps<Cfg, 0, 4>(F, acc);
 }
 
+// The end of a panel that another panel follows: its sum becomes the running total (first panel) or
+// is added into it, and the accumulators restart from zero.
+template <class Cfg>
+__device__ __forceinline__ void fold_panel(f4 (&tot)[Cfg::TM][Cfg::TN], f4 (&acc)[Cfg::TM][Cfg::TN], bool first) {
+    if (first) {
+#pragma unroll
+        for (int i = 0; i < Cfg::TM; i++)
+#pragma unroll
+            for (int j = 0; j < Cfg::TN; j++) tot[i][j] = acc[i][j];
+    } else {
+#pragma unroll
+        for (int i = 0; i < Cfg::TM; i++)
+#pragma unroll
+            for (int j = 0; j < Cfg::TN; j++) tot[i][j] = tot[i][j] + acc[i][j];
+    }
+#pragma unroll
+    for (int i = 0; i < Cfg::TM; i++)
+#pragma unroll
+        for (int j = 0; j < Cfg::TN; j++) acc[i][j] = f4{0.f, 0.f, 0.f, 0.f};
+}
+
+// After the last stage: with more than one panel, the last panel's sum is added into the running
+// total, and the result is left in acc.
+template <class Cfg>
+__device__ __forceinline__ void finish_panels(const f4 (&tot)[Cfg::TM][Cfg::TN], f4 (&acc)[Cfg::TM][Cfg::TN], int nk) {
+    if (nk <= kSgPanel) return;
+#pragma unroll
+    for (int i = 0; i < Cfg::TM; i++)
+#pragma unroll
+        for (int j = 0; j < Cfg::TN; j++) acc[i][j] = tot[i][j] + acc[i][j];
+}
+
 // C = alpha acc + beta C over the wave's tiles.  acc[i][j] is the 16 x 16 tile C^T: lane l, element v
 // holds row (tile row + l % 16), column (tile column + 4 (l / 16) + v).
 template <class Cfg>
@@ -305,7 +358,7 @@ __device__ __forceinline__ void write_tiles(const SgArgs &p, const TileAt &at, c
 }
 
 template <class Cfg, bool AK, bool BK, bool VEC, bool FAST>
-__global__ __launch_bounds__(Cfg::NT, 1) void k_sgemm(SgArgs p) {
+__global__ __launch_bounds__(Cfg::NT, Cfg::MINB) void k_sgemm(SgArgs p) {
     extern __shared__ __attribute__((aligned(16))) char smem[];
     const TileAt at = locate<Cfg::BM, Cfg::BN>(p);
     const int t = threadIdx.x, lane = t & (kWave - 1), wid = t / kWave;
@@ -317,6 +370,7 @@ __global__ __launch_bounds__(Cfg::NT, 1) void k_sgemm(SgArgs p) {
     lb.init(at.B, p.ldb, p.N, p.K, at.n0, t);
 
     f4 acc[Cfg::TM][Cfg::TN];
+    f4 tot[Cfg::TOTAL ? Cfg::TM : 1][Cfg::TOTAL ? Cfg::TN : 1];
 #pragma unroll
     for (int i = 0; i < Cfg::TM; i++)
 #pragma unroll
@@ -336,6 +390,9 @@ __global__ __launch_bounds__(Cfg::NT, 1) void k_sgemm(SgArgs p) {
             lb.load((kt + 1) * kSgBK);
         }
         stage_mfma<Cfg, AK, BK>(smem + (kt & 1) * Cfg::STAGE, acc, wm, wn, fr, fq);
+        if constexpr (Cfg::TOTAL) {
+            if (kt % kSgPanel == kSgPanel - 1 && kt + 1 < nk) fold_panel<Cfg>(tot, acc, kt < kSgPanel);
+        }
         // the other stage was last read before the previous barrier, so it can be refilled now
         if (kt + 1 < nk) {
             char *next = smem + ((kt + 1) & 1) * Cfg::STAGE;
@@ -344,60 +401,78 @@ __global__ __launch_bounds__(Cfg::NT, 1) void k_sgemm(SgArgs p) {
         }
         __syncthreads();
     }
+    if constexpr (Cfg::TOTAL) finish_panels<Cfg>(tot, acc, nk);
     write_tiles<Cfg>(p, at, acc, wm, wn, fr, fq);
 }
 
 // ------------------------------------------------------------------------------------------------
-// Large FAST problems: the same 256 x 256 tile, its panels loaded straight from global memory into
-// LDS (global_load_lds_dwordx4) three stages ahead through four LDS stages, with no staging registers
-// and no LDS write instructions; one barrier per stage.  A stage of a panel is 16 load instructions of
-// 1 KiB each: 16 rows of a K-contiguous panel (lane l: row l / 4, the chunk that belongs at position
-// l % 4 under the row's permutation) or one k-row of a M/N-contiguous one (lane l: rows 4 l .. 4 l + 3).  Waves
-// 0-3 load A, waves 4-7 B, four instructions each.  Rows past the matrix are clamped as in the
-// staged kernel's FAST loads.
+// Large FAST problems: the 256 x 128 tile, its panels loaded straight from global memory into LDS
+// (global_load_lds_dwordx4) three stages ahead through four LDS stages, with no staging registers and
+// no LDS write instructions; one barrier per stage.  A stage of an R-row panel is R / 16 load
+// instructions of 1 KiB each: 16 rows of a K-contiguous panel (lane l: row l / 4, the chunk that
+// belongs at position l % 4 under the row's permutation) or 256 / R k-rows of a M/N-contiguous one
+// (lane l: k-row l / (R / 4), position l % (R / 4), loading the rows the k-row's permutation puts
+// there).  The 24 instructions of a stage (16 for A, 8 for B) are dealt three to a wave.  Rows past
+// the matrix are clamped as in the staged kernel's FAST loads.
 constexpr int kSgDmaStages = 4;
-constexpr size_t kSgDmaLds = kSgDmaStages * (size_t)SgBig::STAGE;
 
-template <bool AK, bool BK>
-__global__ __launch_bounds__(SgBig::NT, 1) void k_sgemm_dma(SgArgs p) {
-    using Cfg = SgBig;
-    constexpr int kR = Cfg::BM;  // = BN
-    static_assert(Cfg::BM == Cfg::BN && Cfg::NT / kWave == 8, "one panel per half of the waves");
+template <class Cfg>
+struct SgDma {
+    static constexpr int NW = Cfg::NT / kWave;
+    static constexpr int IA = Cfg::BM / 16, IB = Cfg::BN / 16;  // load instructions per stage
+    static constexpr int PER = (IA + IB) / NW;                    // per wave
+    static_assert((IA + IB) % NW == 0, "the stage's loads deal evenly over the waves");
+    static constexpr size_t LDS = kSgDmaStages * (size_t)Cfg::STAGE;
+};
+
+// s_waitcnt vmcnt(N) for a compile-time N
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+    static_assert(N >= 0 && N <= 15, "vmcnt immediate");
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+
+template <class Cfg, bool AK, bool BK>
+__global__ __launch_bounds__(Cfg::NT, 1) void k_sgemm_dma(SgArgs p) {
+    using D = SgDma<Cfg>;
     extern __shared__ __attribute__((aligned(16))) char smem[];
     const TileAt at = locate<Cfg::BM, Cfg::BN>(p);
     const int t = threadIdx.x, lane = t & (kWave - 1), wid = t / kWave;
     const int wm = wid / Cfg::WGN, wn = wid % Cfg::WGN, fr = lane & 15, fq = lane >> 4;
 
-    // this wave's four load instructions per stage (wave-uniform panel)
-    const bool panel_b = wid >= 4;
-    const bool kc = panel_b ? BK : AK;
-    const float *base = panel_b ? at.B : at.A;
-    const int64_t ld = panel_b ? p.ldb : p.lda;
-    const int rows = panel_b ? p.N : p.M, r0 = panel_b ? at.n0 : at.m0;
-    const float *src[4];
-    uint32_t loff[4];
+    // this wave's load instructions per stage (each one wave-uniform in its panel)
+    const float *src[D::PER];
+    int64_t kstep[D::PER];  // elements from one stage to the next
+    uint32_t loff[D::PER];
 #pragma unroll
-    for (int i = 0; i < 4; i++) {
-        const int idx = (wid & 3) * 4 + i;
+    for (int i = 0; i < D::PER; i++) {
+        const int j = wid * D::PER + i;
+        const bool pb = j >= D::IA;
+        const int idx = pb ? j - D::IA : j;
+        const bool kc = pb ? BK : AK;
+        const float *base = pb ? at.B : at.A;
+        const int64_t ld = pb ? p.ldb : p.lda;
+        const int rows = pb ? p.N : p.M, r0 = pb ? at.n0 : at.m0;
+        const int R = pb ? Cfg::BN : Cfg::BM;
         if (kc) {
             const int prow = 16 * idx + (lane >> 2), c = (lane & 3) ^ kc_swz(prow);
             src[i] = base + (int64_t)min(r0 + prow, rows - 1) * ld + 4 * c;
-            loff[i] = (uint32_t)(idx * 1024);
         } else {
-            src[i] = base + (int64_t)idx * ld + min(r0 + 4 * lane, rows - 4);
-            loff[i] = (uint32_t)(idx * (kR + 4) * 4);
+            const int per_row = R / 4;  // chunks per k-row
+            const int k = idx * (kWave / per_row) + lane / per_row, c = (lane % per_row) ^ mn_swz(k);
+            src[i] = base + (int64_t)k * ld + min(r0 + 4 * c, rows - 4);
         }
-        loff[i] += panel_b ? Cfg::SLAB_A : 0;
+        kstep[i] = kc ? kSgBK : kSgBK * ld;
+        loff[i] = (uint32_t)(idx * 1024) + (pb ? Cfg::SLAB_A : 0);
     }
-    const int64_t kstep = kc ? kSgBK : kSgBK * ld;  // elements from one stage to the next
     const uint32_t sbase = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) char *)smem;
     auto issue = [&](int kt) {
         const uint32_t st = sbase + (uint32_t)(kt % kSgDmaStages) * Cfg::STAGE;
 #pragma unroll
-        for (int i = 0; i < 4; i++) dma16(src[i] + kt * kstep, __builtin_amdgcn_readfirstlane(st + loff[i]));
+        for (int i = 0; i < D::PER; i++) dma16(src[i] + kt * kstep[i], __builtin_amdgcn_readfirstlane(st + loff[i]));
     };
 
-    f4 acc[Cfg::TM][Cfg::TN];
+    f4 acc[Cfg::TM][Cfg::TN], tot[Cfg::TM][Cfg::TN];
 #pragma unroll
     for (int i = 0; i < Cfg::TM; i++)
 #pragma unroll
@@ -406,16 +481,18 @@ __global__ __launch_bounds__(SgBig::NT, 1) void k_sgemm_dma(SgArgs p) {
     const int nk = p.K / kSgBK;
     for (int kt = 0; kt < kSgDmaStages - 1 && kt < nk; kt++) issue(kt);
     for (int kt = 0; kt < nk; kt++) {
-        // this wave's loads of stage kt are done once at most 4 per later stage in flight remain
+        // this wave's loads of stage kt are done once at most PER per later stage in flight remain
         const int ahead = min(nk - 1 - kt, kSgDmaStages - 2);
-        if (ahead == 2) asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
-        else if (ahead == 1) asm volatile("s_waitcnt vmcnt(4)" ::: "memory");
-        else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        if (ahead == 2) wait_vmcnt<2 * D::PER>();
+        else if (ahead == 1) wait_vmcnt<D::PER>();
+        else wait_vmcnt<0>();
         __builtin_amdgcn_s_barrier();  // every wave's loads of stage kt have landed; stage kt-1's reads are done
         asm volatile("" ::: "memory");
         if (kt + kSgDmaStages - 1 < nk) issue(kt + kSgDmaStages - 1);  // into the stage kt-1 used
         stage_mfma<Cfg, AK, BK>(smem + (kt % kSgDmaStages) * Cfg::STAGE, acc, wm, wn, fr, fq);
+        if (kt % kSgPanel == kSgPanel - 1 && kt + 1 < nk) fold_panel<Cfg>(tot, acc, kt < kSgPanel);
     }
+    finish_panels<Cfg>(tot, acc, nk);
     write_tiles<Cfg>(p, at, acc, wm, wn, fr, fq);
 }
 
@@ -432,6 +509,8 @@ static void sg_attr() {
 
 template <class Cfg, bool AK, bool BK, bool VEC, bool FAST>
 static int sg_launch(SgArgs &p, int64_t count, hipStream_t st, const char *what) {
+    if (!Cfg::TOTAL && p.K > kSgBK * kSgPanel)
+        return set_error(NC_HIP_ERR_ARG, "%s: K %d needs a running total this tile keeps none of", what, p.K);
     p.tiles_m = (p.M + Cfg::BM - 1) / Cfg::BM;
     p.tiles_n = (p.N + Cfg::BN - 1) / Cfg::BN;
     const int64_t blocks = (int64_t)p.tiles_m * p.tiles_n * count;
@@ -447,20 +526,20 @@ static int sg_launch(SgArgs &p, int64_t count, hipStream_t st, const char *what)
 #ifndef SG_DMA_MIN_K
 #define SG_DMA_MIN_K 512
 #endif
-template <bool AK, bool BK>
+template <class Cfg, bool AK, bool BK>
 static int sg_launch_dma(SgArgs &p, int64_t count, hipStream_t st, const char *what) {
-    p.tiles_m = (p.M + SgBig::BM - 1) / SgBig::BM;
-    p.tiles_n = (p.N + SgBig::BN - 1) / SgBig::BN;
+    p.tiles_m = (p.M + Cfg::BM - 1) / Cfg::BM;
+    p.tiles_n = (p.N + Cfg::BN - 1) / Cfg::BN;
     const int64_t blocks = (int64_t)p.tiles_m * p.tiles_n * count;
     if (blocks > INT32_MAX) return set_error(NC_HIP_ERR_ARG, "%s: %lld tiles exceed one launch", what, (long long)blocks);
     static bool done[64] = {};
     int dev = 0;
     if (hipGetDevice(&dev) == hipSuccess && dev >= 0 && dev < 64 && !done[dev]) {
-        (void)hipFuncSetAttribute((const void *)k_sgemm_dma<AK, BK>, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                  (int)kSgDmaLds);
+        (void)hipFuncSetAttribute((const void *)k_sgemm_dma<Cfg, AK, BK>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                  (int)SgDma<Cfg>::LDS);
         done[dev] = true;
     }
-    hipLaunchKernelGGL((k_sgemm_dma<AK, BK>), dim3((unsigned)blocks), dim3(SgBig::NT), kSgDmaLds, st, p);
+    hipLaunchKernelGGL((k_sgemm_dma<Cfg, AK, BK>), dim3((unsigned)blocks), dim3(Cfg::NT), SgDma<Cfg>::LDS, st, p);
     return check_launch(what);
 }
 
@@ -469,10 +548,11 @@ static int sg_layouts(SgArgs &p, int ta, int tb, bool vec, int64_t count, hipStr
     const bool ak = !ta, bk = tb != 0;
     const bool fast = vec && p.K % kSgBK == 0 && (ak || p.M % 4 == 0) && (bk || p.N % 4 == 0);
     // the DMA kernel clamps M/N-contiguous chunks onto the last 4 rows: at least 4 rows there
-    const bool dma = SG_DMA && fast && p.K >= SG_DMA_MIN_K && Cfg::BM == SgBig::BM && (ak || p.M >= 4) && (bk || p.N >= 4);
+    const bool dma = SG_DMA && std::is_same<Cfg, SgWide>::value && fast && p.K >= SG_DMA_MIN_K && (ak || p.M >= 4) &&
+                     (bk || p.N >= 4);
 #define NC_SG_CASE(AK_, BK_)                                                                \
     if (ak == AK_ && bk == BK_)                                                             \
-        return dma   ? sg_launch_dma<AK_, BK_>(p, count, st, what)                          \
+        return dma   ? sg_launch_dma<SgWide, AK_, BK_>(p, count, st, what)                  \
                : fast ? sg_launch<Cfg, AK_, BK_, true, true>(p, count, st, what)            \
                : vec  ? sg_launch<Cfg, AK_, BK_, true, false>(p, count, st, what)           \
                       : sg_launch<Cfg, AK_, BK_, false, false>(p, count, st, what);
@@ -486,14 +566,17 @@ static int sg_layouts(SgArgs &p, int ta, int tb, bool vec, int64_t count, hipStr
 
 static int64_t tiles_of(int64_t M, int64_t N, int bm, int bn) { return ((M + bm - 1) / bm) * ((N + bn - 1) / bn); }
 
-// the largest tile that still gives every CU a tile, else the smallest
+// the largest tile that still gives every CU a tile (256 x 256 only for a single panel), else the
+// smallest
 static int sg_run(SgArgs &p, int ta, int tb, int64_t count, hipStream_t st, const char *what) {
     // 16-byte loads need every matrix's rows 16-byte aligned: the matrices behind a pointer array may
     // start anywhere, so those take the scalar loads
     bool vec = !p.pa && aligned16(p.A) && aligned16(p.B) && p.lda % 4 == 0 && p.ldb % 4 == 0;
     for (int d = 0; d < p.bat.nb; d++) vec = vec && p.bat.st[0][d] % 4 == 0 && p.bat.st[1][d] % 4 == 0;
     const int64_t cus = num_cus();
-    if (tiles_of(p.M, p.N, SgBig::BM, SgBig::BN) * count >= cus) return sg_layouts<SgBig>(p, ta, tb, vec, count, st, what);
+    if (p.K <= kSgBK * kSgPanel && tiles_of(p.M, p.N, SgBig::BM, SgBig::BN) * count >= cus)
+        return sg_layouts<SgBig>(p, ta, tb, vec, count, st, what);
+    if (tiles_of(p.M, p.N, SgWide::BM, SgWide::BN) * count >= cus) return sg_layouts<SgWide>(p, ta, tb, vec, count, st, what);
     if (tiles_of(p.M, p.N, SgMid::BM, SgMid::BN) * count >= cus) return sg_layouts<SgMid>(p, ta, tb, vec, count, st, what);
     return sg_layouts<SgSmall>(p, ta, tb, vec, count, st, what);
 }

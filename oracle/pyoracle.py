@@ -456,15 +456,16 @@ def linear_grads64(x, W, G):
     return gx, G2.T @ x2, G2.sum(0), tx, np.abs(G2.T) @ np.abs(x2), np.abs(G2).sum(0)
 
 
-def gemm_excess(got, truth, terms, K, rtol=1e-5, kcap=2048):
-    """max over elements of |got - truth| / (rtol * max(|truth|, terms / sqrt(min(K, kcap)))); <= 1 passes.
+def gemm_excess(got, truth, terms, K, rtol=1e-5):
+    """max over elements of |got - truth| / (rtol * max(|truth|, terms / sqrt(K))); <= 1 passes.
 
-    terms / sqrt(K) is the scale of a K-term sum whose rounding errors cancel like a random walk. An
-    fp32 dot product accumulated one product at a time rounds K running sums of size ~sqrt(K) terms,
-    so its error scales with terms itself rather than terms / sqrt(K); past kcap terms the floor
-    therefore stays at terms / sqrt(kcap)."""
+    terms / sqrt(K) is the scale of a K-term sum whose rounding errors cancel like a random walk.  A
+    blocked fp32 sum (panels of 256 products summed from zero, each added into the running total, as
+    the reference's KC = 256 panels at kernels_avx2.c:234-247) stays well inside it; an fp32 sum that
+    adds one product at a time to the running total rounds K sums of size ~sqrt(K) terms, so its error
+    grows like terms itself and leaves the bound past a few thousand terms."""
     got = np.asarray(got, np.float64)
-    bound = rtol * np.maximum(np.abs(truth), np.asarray(terms) / np.sqrt(max(min(K, kcap), 1)))
+    bound = rtol * np.maximum(np.abs(truth), np.asarray(terms) / np.sqrt(max(K, 1)))
     err = np.abs(got - truth)
     with np.errstate(divide="ignore", invalid="ignore"):
         r = np.where(err == 0, 0.0, err / bound)  # a nonzero error on a zero bound is inf; NaN stays NaN

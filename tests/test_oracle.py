@@ -282,6 +282,35 @@ def test_matmul_golden(case, aview, bview):
     assert O.gemm_excess(d[f"{case}/gb"], gb, tb, nb) <= 1.0
 
 
+def _fp32_dot_rows(A, B, panel):
+    """fp32 products of A (M x K) and B (K x N) summed one k at a time; with `panel`, each panel of
+    that many k summed from zero and added into a running total."""
+    K = A.shape[1]
+    acc = np.zeros((A.shape[0], B.shape[1]), np.float32)
+    tot = None
+    for k in range(K):
+        acc = (acc + np.outer(A[:, k], B[k])).astype(np.float32)
+        if panel and (k + 1) % panel == 0 and k + 1 < K:
+            tot = acc.copy() if tot is None else (tot + acc).astype(np.float32)
+            acc[:] = 0
+    return acc if tot is None else (tot + acc).astype(np.float32)
+
+
+def test_gemm_bar_separates_blocked_from_sequential_sums():
+    """The GEMM bar (terms / sqrt(K) floor, no cap) tells the reference's blocked sum from a plain
+    running fp32 sum: at K = 16384 a sum adding each product to the running total leaves the bound,
+    while 256-product panels added into a running total (the reference's KC = 256,
+    kernels_avx2.c:234-247, and the matrix-core kernels' order) stay far inside it."""
+    rng = np.random.default_rng(16384)
+    K = 16384
+    A = rng.standard_normal((64, K)).astype(np.float32)
+    B = rng.standard_normal((K, 256)).astype(np.float32)
+    want = A.astype(np.float64) @ B.astype(np.float64)
+    terms = np.abs(A.astype(np.float64)) @ np.abs(B.astype(np.float64))
+    assert O.gemm_excess(_fp32_dot_rows(A, B, 0), want, terms, K) > 1.2
+    assert O.gemm_excess(_fp32_dot_rows(A, B, 256), want, terms, K) < 0.4
+
+
 @pytest.mark.parametrize("case,xview,has_b", LINEAR_CASES, ids=[c[0] for c in LINEAR_CASES])
 def test_linear_golden(case, xview, has_b):
     d = load("linalg")
