@@ -1176,7 +1176,7 @@ static size_t bwd2_ws(const Bwd2Plan &pl, int out = 3) {
 
 template <int MODE, int OUT>
 static int launch_bwd2(const float *g, const float *a, const float *b, float *ga, float *gb, const Bwd2Plan &pl,
-                       double alpha_b, int acc, void *ws, size_t ws_bytes, hipStream_t st) {
+                       double alpha_b, int acc, int acc_b, void *ws, size_t ws_bytes, hipStream_t st) {
     const size_t need = bwd2_ws(pl, OUT);
     if (ws_bytes < need || (need && !ws))
         return set_error(NC_HIP_ERR_WORKSPACE, "binary_bwd2: workspace of %zu bytes needed, %zu given", need, ws_bytes);
@@ -1211,22 +1211,23 @@ static int launch_bwd2(const float *g, const float *a, const float *b, float *ga
     }
     if (OUT & 2) {
         const uint32_t n = pl.H * pl.W4 * 4;
-        if (acc) hipLaunchKernelGGL((k_bwd2_gb_combine<MODE, true>), dim3((n + 63) / 64), dim3(1024), 0, st, gb_part, b, gb, n, pl.ranges);
+        if (acc_b) hipLaunchKernelGGL((k_bwd2_gb_combine<MODE, true>), dim3((n + 63) / 64), dim3(1024), 0, st, gb_part, b, gb, n, pl.ranges);
         else hipLaunchKernelGGL((k_bwd2_gb_combine<MODE, false>), dim3((n + 63) / 64), dim3(1024), 0, st, gb_part, b, gb, n, pl.ranges);
     }
     return check_launch("nc_hip_binary_bwd2");
 }
 
-// op -> kernel mode (add and sub share the kernel; sub scales grad_b by -1)
+// op -> kernel mode (add and sub share the kernel; sub scales grad_b by -1); acc applies to grad_a,
+// acc_b to grad_b
 template <int OUT>
 static int launch_bwd2_op(int op, const float *g, const float *a, const float *b, float *ga, float *gb,
-                          const Bwd2Plan &pl, int acc, void *ws, size_t ws_bytes, hipStream_t st) {
+                          const Bwd2Plan &pl, int acc, int acc_b, void *ws, size_t ws_bytes, hipStream_t st) {
     const double alpha_b = op == NC_HIP_BIN_SUB ? -1.0 : 1.0;
     switch (op) {
     case NC_HIP_BIN_ADD:
-    case NC_HIP_BIN_SUB: return launch_bwd2<0, OUT>(g, a, b, ga, gb, pl, alpha_b, acc, ws, ws_bytes, st);
-    case NC_HIP_BIN_MUL: return launch_bwd2<1, OUT>(g, a, b, ga, gb, pl, alpha_b, acc, ws, ws_bytes, st);
-    default: return launch_bwd2<3, OUT>(g, a, b, ga, gb, pl, alpha_b, acc, ws, ws_bytes, st);
+    case NC_HIP_BIN_SUB: return launch_bwd2<0, OUT>(g, a, b, ga, gb, pl, alpha_b, acc, acc_b, ws, ws_bytes, st);
+    case NC_HIP_BIN_MUL: return launch_bwd2<1, OUT>(g, a, b, ga, gb, pl, alpha_b, acc, acc_b, ws, ws_bytes, st);
+    default: return launch_bwd2<3, OUT>(g, a, b, ga, gb, pl, alpha_b, acc, acc_b, ws, ws_bytes, st);
     }
 }
 
@@ -1297,8 +1298,25 @@ extern "C" NC_HIP_API int nc_hip_binary_fwd(int op, int nd, const int64_t *shape
     }
 }
 
+static size_t bwd_workspace_run(int nd, const int64_t *shape, const int64_t *sgx);
+
+// Broadcast gradients of 2^32 elements or more run as runs of at most 2^30 elements (for_each_run), so
+// the workspace is the largest any run needs.
 extern "C" NC_HIP_API size_t nc_hip_binary_bwd_workspace(int nd, const int64_t *shape, const int64_t *sgx) {
-    if (nd < 0 || nd > NC_HIP_MAX_DIMS) return 0;
+    if (nd < 0 || nd > NC_HIP_MAX_DIMS || !shape || !sgx) return 0;
+    for (int d = 0; d < nd; d++)
+        if (shape[d] < 0) return 0;
+    if (numel_of(nd, shape) < (int64_t)UINT32_MAX) return bwd_workspace_run(nd, shape, sgx);
+    size_t need = 0;
+    const int64_t *st[1] = {sgx};
+    for_each_run(nd, shape, 1, st, kRunLimit, [&](const int64_t *rs, const int64_t *, const bool *) {
+        need = std::max(need, bwd_workspace_run(nd, rs, sgx));
+        return 0;
+    });
+    return need;
+}
+
+static size_t bwd_workspace_run(int nd, const int64_t *shape, const int64_t *sgx) {
     // the plan depends only on the shape and on which dims gx keeps: use unit strides elsewhere
     int64_t cs[NC_HIP_MAX_DIMS], s = 1;
     for (int d = nd - 1; d >= 0; d--) {
@@ -1338,17 +1356,39 @@ static int try_bwd_fused_single(int op, int which, int nd, const int64_t *shape,
         return -1;
     const size_t need = bwd2_ws(pl, which == 0 ? 1 : 2);
     if (ws_bytes < need || (need && !ws)) return -1;
-    if (which == 0) return launch_bwd2_op<1>(op, g, a, b, gx, nullptr, pl, accumulate, ws, ws_bytes, st);
+    if (which == 0) return launch_bwd2_op<1>(op, g, a, b, gx, nullptr, pl, accumulate, accumulate, ws, ws_bytes, st);
     if (reads_ab && NC_BIN_WARM) warm_operand(a, p, 1, st);  // grad_b's terms read a
-    return launch_bwd2_op<2>(op, g, a, b, nullptr, gx, pl, accumulate, ws, ws_bytes, st);
+    return launch_bwd2_op<2>(op, g, a, b, nullptr, gx, pl, accumulate, accumulate, ws, ws_bytes, st);
 }
 
+static int binary_bwd_run(int op, int which, int nd, const int64_t *shape, const float *g, const int64_t *sg,
+                          const float *a, const int64_t *sa, const float *b, const int64_t *sb, float *gx,
+                          const int64_t *sgx, int accumulate, void *ws, size_t ws_bytes, void *stream);
+
+// Gradients of 2^32 elements or more: runs of at most 2^30 elements of g in index order, each through
+// the ordinary paths; a run adds into what an earlier run wrote where gx is reduced over a cut dim.
 extern "C" NC_HIP_API int nc_hip_binary_bwd(int op, int which, int nd, const int64_t *shape, const float *g,
                                             const int64_t *sg, const float *a, const int64_t *sa, const float *b,
                                             const int64_t *sb, float *gx, const int64_t *sgx, int accumulate,
                                             void *ws, size_t ws_bytes, void *stream) {
     if (op < 0 || op > 3 || (which != 0 && which != 1))
         return set_error(NC_HIP_ERR_ARG, "nc_hip_binary_bwd: bad op/which");
+    if (nd < 0 || nd > NC_HIP_MAX_DIMS || !shape || !sg || !sa || !sb || !sgx)
+        return set_error(NC_HIP_ERR_ARG, "nc_hip_binary_bwd: bad shape or strides");
+    for (int d = 0; d < nd; d++)
+        if (shape[d] < 0) return set_error(NC_HIP_ERR_ARG, "nc_hip_binary_bwd: negative dim");
+    if (numel_of(nd, shape) < (int64_t)UINT32_MAX)
+        return binary_bwd_run(op, which, nd, shape, g, sg, a, sa, b, sb, gx, sgx, accumulate, ws, ws_bytes, stream);
+    const int64_t *st[4] = {sg, sa, sb, sgx};
+    return for_each_run(nd, shape, 4, st, kRunLimit, [&](const int64_t *rs, const int64_t *off, const bool *first) {
+        return binary_bwd_run(op, which, nd, rs, adv(g, off[0]), sg, adv(a, off[1]), sa, adv(b, off[2]), sb,
+                              adv(gx, off[3]), sgx, first[3] ? accumulate : 1, ws, ws_bytes, stream);
+    });
+}
+
+static int binary_bwd_run(int op, int which, int nd, const int64_t *shape, const float *g, const int64_t *sg,
+                          const float *a, const int64_t *sa, const float *b, const int64_t *sb, float *gx,
+                          const int64_t *sgx, int accumulate, void *ws, size_t ws_bytes, void *stream) {
     Prepared p;
     int mode;
     float alpha;
@@ -1376,8 +1416,25 @@ static int prepare_bwd2(int nd, const int64_t *shape, const int64_t *sg, const i
     return prepare(nd, shape, 5, strides, p, "nc_hip_binary_bwd2");
 }
 
+static size_t bwd2_workspace_run(int nd, const int64_t *shape, const int64_t *sga, const int64_t *sgb);
+
 extern "C" NC_HIP_API size_t nc_hip_binary_bwd2_workspace(int nd, const int64_t *shape, const int64_t *sga,
                                                           const int64_t *sgb) {
+    if (nd < 0 || nd > NC_HIP_MAX_DIMS || !shape) return 0;
+    for (int d = 0; d < nd; d++)
+        if (shape[d] < 0) return 0;
+    if (numel_of(nd, shape) < (int64_t)UINT32_MAX) return bwd2_workspace_run(nd, shape, sga, sgb);
+    size_t need = 0;
+    const int64_t zeros[NC_HIP_MAX_DIMS] = {0, 0, 0, 0, 0, 0};
+    const int64_t *st[1] = {zeros};
+    for_each_run(nd, shape, 1, st, kRunLimit, [&](const int64_t *rs, const int64_t *, const bool *) {
+        need = std::max(need, bwd2_workspace_run(nd, rs, sga, sgb));
+        return 0;
+    });
+    return need;
+}
+
+static size_t bwd2_workspace_run(int nd, const int64_t *shape, const int64_t *sga, const int64_t *sgb) {
     size_t wa = sga ? nc_hip_binary_bwd_workspace(nd, shape, sga) : 0;
     size_t wb = sgb ? nc_hip_binary_bwd_workspace(nd, shape, sgb) : 0;
     size_t need = wa > wb ? wa : wb;
@@ -1398,12 +1455,41 @@ extern "C" NC_HIP_API size_t nc_hip_binary_bwd2_workspace(int nd, const int64_t 
     return need;
 }
 
+static int binary_bwd2_run(int op, int nd, const int64_t *shape, const float *g, const int64_t *sg,
+                           const float *a, const int64_t *sa, const float *b, const int64_t *sb, float *ga,
+                           const int64_t *sga, float *gb, const int64_t *sgb, int acc_a, int acc_b, void *ws,
+                           size_t ws_bytes, void *stream);
+
+// Both gradients of 2^32 elements or more: runs of at most 2^30 elements of g in index order (each the
+// one-pass kernel where the broadcast has its pattern); grad_a and grad_b each add into what an earlier
+// run wrote where they are reduced over a cut dim (config-sized a[256,512,1,64] + b[1,1,512,64]: four
+// runs of 64 planes; grad_a written by each, grad_b stored by the first and added to by the rest).
 extern "C" NC_HIP_API int nc_hip_binary_bwd2(int op, int nd, const int64_t *shape, const float *g,
                                              const int64_t *sg, const float *a, const int64_t *sa, const float *b,
                                              const int64_t *sb, float *ga, const int64_t *sga, float *gb,
                                              const int64_t *sgb, int accumulate, void *ws, size_t ws_bytes,
                                              void *stream) {
     if (op < 0 || op > 3) return set_error(NC_HIP_ERR_ARG, "nc_hip_binary_bwd2: bad op");
+    if (nd < 0 || nd > NC_HIP_MAX_DIMS || !shape || !sg || !sa || !sb || (ga && !sga) || (gb && !sgb))
+        return set_error(NC_HIP_ERR_ARG, "nc_hip_binary_bwd2: bad shape or strides");
+    for (int d = 0; d < nd; d++)
+        if (shape[d] < 0) return set_error(NC_HIP_ERR_ARG, "nc_hip_binary_bwd2: negative dim");
+    if (numel_of(nd, shape) < (int64_t)UINT32_MAX)
+        return binary_bwd2_run(op, nd, shape, g, sg, a, sa, b, sb, ga, sga, gb, sgb, accumulate, accumulate, ws,
+                               ws_bytes, stream);
+    const int64_t zeros[NC_HIP_MAX_DIMS] = {0, 0, 0, 0, 0, 0};
+    const int64_t *st[5] = {sg, sa, sb, ga ? sga : zeros, gb ? sgb : zeros};
+    return for_each_run(nd, shape, 5, st, kRunLimit, [&](const int64_t *rs, const int64_t *off, const bool *first) {
+        return binary_bwd2_run(op, nd, rs, adv(g, off[0]), sg, adv(a, off[1]), sa, adv(b, off[2]), sb,
+                               adv(ga, off[3]), sga, adv(gb, off[4]), sgb, first[3] ? accumulate : 1,
+                               first[4] ? accumulate : 1, ws, ws_bytes, stream);
+    });
+}
+
+static int binary_bwd2_run(int op, int nd, const int64_t *shape, const float *g, const int64_t *sg,
+                           const float *a, const int64_t *sa, const float *b, const int64_t *sb, float *ga,
+                           const int64_t *sga, float *gb, const int64_t *sgb, int acc_a, int acc_b, void *ws,
+                           size_t ws_bytes, void *stream) {
     if (ga && gb) {
         // add / sub read neither operand: plan with the gradients' layouts in their place
         const bool reads_ab = op == NC_HIP_BIN_MUL || op == NC_HIP_BIN_DIV;
@@ -1413,13 +1499,13 @@ extern "C" NC_HIP_API int nc_hip_binary_bwd2(int op, int nd, const int64_t *shap
         Bwd2Plan pl;
         if (p.numel > 0 && plan_bwd2(p, g, reads_ab ? a : ga, reads_ab ? b : gb, ga, gb, pl, 3)) {
             if (reads_ab && NC_BIN_WARM) warm_operand(a, p, 1, as_stream(stream));  // grad_b's terms read a
-            return launch_bwd2_op<3>(op, g, a, b, ga, gb, pl, accumulate, ws, ws_bytes, as_stream(stream));
+            return launch_bwd2_op<3>(op, g, a, b, ga, gb, pl, acc_a, acc_b, ws, ws_bytes, as_stream(stream));
         }
     }
     int rc = NC_HIP_OK;
-    if (ga) rc = nc_hip_binary_bwd(op, 0, nd, shape, g, sg, a, sa, b, sb, ga, sga, accumulate, ws, ws_bytes, stream);
+    if (ga) rc = binary_bwd_run(op, 0, nd, shape, g, sg, a, sa, b, sb, ga, sga, acc_a, ws, ws_bytes, stream);
     if (rc == NC_HIP_OK && gb)
-        rc = nc_hip_binary_bwd(op, 1, nd, shape, g, sg, a, sa, b, sb, gb, sgb, accumulate, ws, ws_bytes, stream);
+        rc = binary_bwd_run(op, 1, nd, shape, g, sg, a, sa, b, sb, gb, sgb, acc_b, ws, ws_bytes, stream);
     return rc;
 }
 
@@ -1492,13 +1578,22 @@ __global__ __launch_bounds__(kB) void k_convert(const S *__restrict__ src, D *__
 
 }  // namespace nchip
 
+// row-major (contiguous) element strides of shape
+static void contiguous_strides(int nd, const int64_t *shape, int64_t *cs) {
+    int64_t s = 1;
+    for (int d = nd - 1; d >= 0; d--) {
+        cs[d] = s;
+        s *= shape[d];
+    }
+}
+
+// Gathers of 2^32 elements or more: runs of at most 2^30 elements (for_each_run), each a launch of
+// its own; the destination is the contiguous tensor of the whole shape.
 extern "C" NC_HIP_API int nc_hip_copy_strided(int elem_bytes, int nd, const int64_t *shape, const void *src,
                                               const int64_t *ss, void *dst, void *stream) {
     Prepared p;
-    int64_t cs[NC_HIP_MAX_DIMS];
     const int64_t *strides[1] = {ss};
     int rc = prepare(nd, shape, 1, strides, p, "nc_hip_copy_strided");
-    (void)cs;
     if (rc) return rc;
     if (p.numel == 0) return NC_HIP_OK;
     hipStream_t st = as_stream(stream);
@@ -1507,7 +1602,17 @@ extern "C" NC_HIP_API int nc_hip_copy_strided(int elem_bytes, int nd, const int6
             return check_launch("nc_hip_copy_strided");
         return NC_HIP_OK;
     }
-    if (p.numel >= (int64_t)UINT32_MAX) return set_error(NC_HIP_ERR_ARG, "copy_strided: too many elements");
+    if (elem_bytes != 1 && elem_bytes != 2 && elem_bytes != 4 && elem_bytes != 8)
+        return set_error(NC_HIP_ERR_ARG, "copy_strided: element size %d", elem_bytes);
+    if (p.numel >= (int64_t)UINT32_MAX) {
+        int64_t cs[NC_HIP_MAX_DIMS];
+        contiguous_strides(nd, shape, cs);
+        const int64_t *st2[2] = {ss, cs};
+        return for_each_run(nd, shape, 2, st2, kRunLimit, [&](const int64_t *rs, const int64_t *off, const bool *) {
+            return nc_hip_copy_strided(elem_bytes, nd, rs, (const char *)src + off[0] * elem_bytes, ss,
+                                       (char *)dst + off[1] * elem_bytes, stream);
+        });
+    }
     IdxMap<1> m;
     make_map<1>(p, 1, m);
     const unsigned grid = stream_grid(p.numel, kB, 16);
@@ -1529,7 +1634,14 @@ extern "C" NC_HIP_API int nc_hip_accumulate_strided(int nd, const int64_t *shape
     int rc = prepare(nd, shape, 1, strides, p, "nc_hip_accumulate_strided");
     if (rc) return rc;
     if (p.numel == 0) return NC_HIP_OK;
-    if (p.numel >= (int64_t)UINT32_MAX) return set_error(NC_HIP_ERR_ARG, "accumulate_strided: too many elements");
+    if (p.numel >= (int64_t)UINT32_MAX) {  // runs of at most 2^30 elements; src is contiguous over shape
+        int64_t cs[NC_HIP_MAX_DIMS];
+        contiguous_strides(nd, shape, cs);
+        const int64_t *st2[2] = {cs, sd};
+        return for_each_run(nd, shape, 2, st2, kRunLimit, [&](const int64_t *rs, const int64_t *off, const bool *) {
+            return nc_hip_accumulate_strided(nd, rs, src + off[0], dst + off[1], sd, stream);
+        });
+    }
     if (p.nd == 0) {
         p.nd = 1;
         p.shape[0] = 1;

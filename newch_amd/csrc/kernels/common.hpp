@@ -279,6 +279,69 @@ __device__ __forceinline__ void dma16(const void *g, uint32_t lds) {
 
 inline bool aligned16(const void *p) { return ((uintptr_t)p & 15u) == 0; }
 
+// ------------------------------------------------------------------------------------------------
+// Problems past the 32-bit kernels' reach, cut into runs.  A problem of `nd` dims over `nops`
+// operands (element strides st[o][d]) is tiled in index order by runs of at most `limit` elements:
+// slabs of the outermost dim where a whole index of it fits, else, for each index of the outermost
+// dim, the same cut one dim further in.  fn(run_shape, off, first) is called per run with the run's
+// shape (the dims outside the cut dim become 1), each operand's element offset of the run's first
+// element, and per operand whether the run is the first, in index order, to touch the elements that
+// operand maps it to: false exactly when an earlier run differs from it only along dims where the
+// operand's stride is 0 (an output reduced over a cut dim, which later runs add into).  Returns the
+// first nonzero return of fn.
+// ------------------------------------------------------------------------------------------------
+constexpr int64_t kRunLimit = int64_t(1) << 30;
+
+template <class F>
+int for_each_run_from(int nd, const int64_t *shape, int nops, const int64_t *const *st, int64_t limit, int d,
+                      const int64_t *off, const bool *first, F &fn) {
+    int64_t inner = 1;
+    for (int e = d + 1; e < nd; e++) inner *= shape[e];
+    int64_t rs[NC_HIP_MAX_DIMS];
+    for (int e = 0; e < nd; e++) rs[e] = e < d ? 1 : shape[e];
+    int64_t o2[8];
+    bool f2[8];
+    if (inner <= limit || d == nd - 1) {
+        const int64_t L = inner <= limit ? limit / inner : 1;
+        for (int64_t r0 = 0; r0 < shape[d]; r0 += L) {
+            rs[d] = shape[d] - r0 < L ? shape[d] - r0 : L;
+            for (int o = 0; o < nops; o++) {
+                o2[o] = off[o] + r0 * st[o][d];
+                f2[o] = first[o] && (st[o][d] != 0 || r0 == 0);
+            }
+            const int rc = fn((const int64_t *)rs, (const int64_t *)o2, (const bool *)f2);
+            if (rc) return rc;
+        }
+        return 0;
+    }
+    for (int64_t i = 0; i < shape[d]; i++) {
+        for (int o = 0; o < nops; o++) {
+            o2[o] = off[o] + i * st[o][d];
+            f2[o] = first[o] && (st[o][d] != 0 || i == 0);
+        }
+        const int rc = for_each_run_from(nd, shape, nops, st, limit, d + 1, o2, f2, fn);
+        if (rc) return rc;
+    }
+    return 0;
+}
+
+template <class F>
+int for_each_run(int nd, const int64_t *shape, int nops, const int64_t *const *st, int64_t limit, F &&fn) {
+    const int64_t off[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    const bool first[8] = {true, true, true, true, true, true, true, true};
+    return nd > 0 ? for_each_run_from(nd, shape, nops, st, limit, 0, off, first, fn) : fn(shape, off, first);
+}
+
+inline int64_t numel_of(int nd, const int64_t *shape) {
+    int64_t n = 1;
+    for (int d = 0; d < nd; d++) n *= shape[d];
+    return n;
+}
+
+// p advanced by off elements (NULL stays NULL)
+template <typename T>
+inline T *adv(T *p, int64_t off) { return p ? p + off : p; }
+
 // grid size for a grid-stride streaming kernel: enough blocks to fill every CU `per_cu` times
 inline unsigned stream_grid(int64_t work_items, int block, int per_cu = 8) {
     int64_t need = (work_items + block - 1) / block;

@@ -554,20 +554,9 @@ extern "C" NC_HIP_API int nc_hip_reduce_fwd_noalloc(int kind, int64_t outer, int
     return nc_hip_reduce_fwd(kind, outer, R, inner, x, y, arg, ws, need, stream);
 }
 
-extern "C" NC_HIP_API int nc_hip_reduce_bwd(int kind, int64_t outer, int64_t R, int64_t inner, const float *g,
-                                            const int32_t *arg, float *gi, int accumulate, void *stream) {
-    hipStream_t st = as_stream(stream);
+static int reduce_bwd_sum_run(int64_t outer, int64_t R, int64_t inner, const float *g, float *gi, float scale,
+                              int accumulate, hipStream_t st) {
     const int64_t n = outer * R * inner;
-    if (n <= 0) return NC_HIP_OK;
-    if (kind == NC_HIP_RED_MAX) {
-        if (!accumulate) hipLaunchKernelGGL(k_fill_f32, stream_grid(n, kRB, 16), kRB, 0, st, gi, 0.0f, n);
-        hipLaunchKernelGGL(k_max_bwd, stream_grid(outer * inner, kRB, 16), kRB, 0, st, g, arg, gi, outer, R, inner);
-        return check_launch("nc_hip_reduce_bwd");
-    }
-    if (kind != NC_HIP_RED_SUM && kind != NC_HIP_RED_MEAN)
-        return set_error(NC_HIP_ERR_ARG, "nc_hip_reduce_bwd: kind %d has no gradient", kind);
-    if (n >= (int64_t)UINT32_MAX) return set_error(NC_HIP_ERR_ARG, "nc_hip_reduce_bwd: 2^32 or more elements");
-    const float scale = kind == NC_HIP_RED_MEAN ? 1.0f / (float)(R ? R : 1) : 1.0f;
     const uint32_t RI = (uint32_t)(R * inner);
     const IntDiv dRI(RI), dI((uint32_t)inner);
     const unsigned grid = stream_grid(n, kRB, 16);
@@ -583,6 +572,30 @@ extern "C" NC_HIP_API int nc_hip_reduce_bwd(int kind, int64_t outer, int64_t R, 
             hipLaunchKernelGGL((k_red_bwd<false, false>), grid, kRB, 0, st, g, gi, n, RI, dRI, (uint32_t)inner, dI, scale);
     }
     return check_launch("nc_hip_reduce_bwd");
+}
+
+// sum / mean gradients of 2^32 elements or more run as runs of at most 2^30 elements of gi
+// (for_each_run over [outer, R, inner]), each a broadcast-back launch with mean's 1/R of the whole R.
+extern "C" NC_HIP_API int nc_hip_reduce_bwd(int kind, int64_t outer, int64_t R, int64_t inner, const float *g,
+                                            const int32_t *arg, float *gi, int accumulate, void *stream) {
+    hipStream_t st = as_stream(stream);
+    if (outer < 0 || R < 0 || inner < 0) return set_error(NC_HIP_ERR_ARG, "nc_hip_reduce_bwd: negative size");
+    const int64_t n = outer * R * inner;
+    if (n <= 0) return NC_HIP_OK;
+    if (kind == NC_HIP_RED_MAX) {
+        if (!accumulate) hipLaunchKernelGGL(k_fill_f32, stream_grid(n, kRB, 16), kRB, 0, st, gi, 0.0f, n);
+        hipLaunchKernelGGL(k_max_bwd, stream_grid(outer * inner, kRB, 16), kRB, 0, st, g, arg, gi, outer, R, inner);
+        return check_launch("nc_hip_reduce_bwd");
+    }
+    if (kind != NC_HIP_RED_SUM && kind != NC_HIP_RED_MEAN)
+        return set_error(NC_HIP_ERR_ARG, "nc_hip_reduce_bwd: kind %d has no gradient", kind);
+    const float scale = kind == NC_HIP_RED_MEAN ? 1.0f / (float)(R ? R : 1) : 1.0f;
+    if (n < (int64_t)UINT32_MAX) return reduce_bwd_sum_run(outer, R, inner, g, gi, scale, accumulate, st);
+    const int64_t shape[3] = {outer, R, inner}, sgi[3] = {R * inner, inner, 1}, sg[3] = {inner, 0, 1};
+    const int64_t *strides[2] = {sg, sgi};
+    return for_each_run(3, shape, 2, strides, kRunLimit, [&](const int64_t *rs, const int64_t *off, const bool *) {
+        return reduce_bwd_sum_run(rs[0], rs[1], rs[2], g + off[0], gi + off[1], scale, accumulate, st);
+    });
 }
 
 extern "C" NC_HIP_API int nc_hip_reduce_sum_i32(int64_t outer, int64_t R, int64_t inner, const int32_t *x,
