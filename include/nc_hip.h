@@ -176,7 +176,9 @@ NC_HIP_API size_t nc_hip_loss_workspace(int64_t N, int64_t C);
 NC_HIP_API int nc_hip_cross_entropy_fwd(int64_t N, int64_t C, const float *x, const int32_t *lab, float *stats,
                                         float *loss, uint64_t *bad, void *ws, size_t ws_bytes, void *stream);
 /* gi (+)= s * prob, then gi[i, lab_i] -= s, with s = gout / N and prob = exp8((x - m) - ls) from the
- * forward's stats: ce_bwd, ops_nn.c:133-147, bit for bit. */
+ * forward's stats: ce_bwd, ops_nn.c:133-147, with the reference's fp32 operations (bit for bit given
+ * the stats; the stats' ls is an fp64 row sum, so prob is within the reductions' tolerance of the
+ * probabilities the reference's forward saves).  x must hold the values the forward read. */
 NC_HIP_API int nc_hip_cross_entropy_bwd(int64_t N, int64_t C, const float *x, const float *stats,
                                         const int32_t *lab, const float *gout, float *gi, int accumulate,
                                         void *stream);
@@ -200,7 +202,8 @@ NC_HIP_API int nc_hip_optim_step(int kind, int64_t n, float *w, const float *g, 
  * reference, whose step loops over its parameters one call each; for models with many small
  * parameters, where one launch per parameter dominates the step).  Every parameter's n is a multiple
  * of 4 and its arrays 16-byte aligned; s1 and s2 are present for every parameter or for none, as in
- * one optimizer.  Bit-identical to one nc_hip_optim_step per parameter. */
+ * one optimizer.  Bit-identical to one nc_hip_optim_step per parameter.  The parameters are updated
+ * concurrently: no parameter's w may share memory with another's w or g. */
 #define NC_HIP_OPT_MULTI_MAX 32
 typedef struct {
     float *w;

@@ -69,6 +69,7 @@ struct nc_tensor {
     char *host;       // host mirror base (lazily allocated)
     size_t bytes;     // storage bytes
     uint32_t res;     // RES_DEV | RES_HOST: which copies are current
+    uint64_t wgen;    // write generation: bumped by every device write and every host pointer handed out for writing
     nc_tensor *grad;  // contiguous, same logical shape
     nc_node *node;
     nc_tensor *owner;  // views: the storage owner

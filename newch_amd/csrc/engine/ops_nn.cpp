@@ -206,6 +206,8 @@ static nc_status loss_fwd(nc_node *n) {
         return NC_ERR_ARG;
     }
     wrote_dev(n->out);
+    // the backward recomputes the probabilities from these logits: it refuses logits written since
+    n->p.i[1] = (int64_t)owner_of(xt)->wgen;
     return NC_OK;
 }
 
@@ -214,6 +216,12 @@ static void loss_bwd(nc_node *n) {
     nc_ctx *ctx = xt->ctx;
     const bool ce = n->op->kind == LOSS_CE;
     const int64_t N = xt->shape[0], C = xt->shape[1];
+    if (ce && owner_of(xt)->wgen != (uint64_t)n->p.i[1]) {
+        error(ctx, NC_ERR_STATE,
+              "cross_entropy: the logits were written after the forward (the backward recomputes the "
+              "probabilities from them)");
+        return;
+    }
     if (!grad_buf(xt)) return;
     float *g = fptr(n->out->grad);
     if (!g) return;

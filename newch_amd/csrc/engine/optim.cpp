@@ -237,6 +237,9 @@ void nc_optim_set_opts(nc_optim *o, nc_optim_opts opts) {
     o->o = opts;
 }
 
+// [p, p + n) and [q, q + m) share an element
+static bool overlaps(const float *p, int64_t n, const float *q, int64_t m) { return p < q + m && q < p + n; }
+
 void nc_optim_step(nc_optim *o) {
     if (!o || !nc_ok(o->ctx) || !o->due()) return;
     const nc_optim_opts &c = o->o;
@@ -247,7 +250,9 @@ void nc_optim_step(nc_optim *o) {
     if (!o->upload_mapped()) return;
     nc_ctx *ctx = o->ctx;
     // parameters whose arrays allow 128-bit access go up to NC_HIP_OPT_MULTI_MAX per launch, the rest
-    // one launch each (the same arithmetic either way)
+    // one launch each (the same arithmetic either way).  A parameter listed again (or sharing memory
+    // with one already in the batch) first flushes the batch: the reference updates the slots in
+    // turn, so the later slot reads the earlier one's result (optim.c:172-213).
     nc_hip_opt_param batch[NC_HIP_OPT_MULTI_MAX];
     int nb = 0;
     auto flush = [&]() {
@@ -266,6 +271,12 @@ void nc_optim_step(nc_optim *o) {
         float *w = fptr(s.p), *g = fptr(gt);
         if (!w || !g) return;
         if (s.n % 4 == 0 && a16(w) && a16(g) && a16(s.dev[0]) && a16(s.dev[1])) {
+            for (int i = 0; i < nb; i++)
+                if (overlaps(batch[i].w, batch[i].n, w, s.n) || overlaps(batch[i].w, batch[i].n, g, s.n) ||
+                    overlaps(batch[i].g, batch[i].n, w, s.n)) {
+                    if (!flush()) return;
+                    break;
+                }
             batch[nb++] = nc_hip_opt_param{w, g, s.dev[0], s.dev[1], s.n};
             if (nb == NC_HIP_OPT_MULTI_MAX && !flush()) return;
         } else if (!hip_layer_ok(ctx,
@@ -326,6 +337,8 @@ float nc_clip_grad_norm(nc_tensor **params, int n, float max_norm) {
     const float total = (float)sqrt(ss);
     const float coef = max_norm / (total + 1e-6f);
     if (coef < 1.0f && ctx) {
+        // a gradient listed twice is scaled twice, in turn, as the reference's loop does
+        // (optim.c:216-233): it goes into a later launch than its first listing
         int cnt = 0;
         auto flush = [&]() {
             const int rc = nc_hip_scale_multi(cnt, xs, ns, coef, ctx->stream);
@@ -335,8 +348,16 @@ float nc_clip_grad_norm(nc_tensor **params, int n, float max_norm) {
         for (int i = 0; i < n; i++) {
             nc_tensor *g = live_grad(i);
             if (!g) continue;
-            if (!(xs[cnt] = fptr(g))) return total;
-            ns[cnt] = nc_numel(g);
+            float *gp = fptr(g);
+            if (!gp) return total;
+            const int64_t gn = nc_numel(g);
+            for (int j = 0; j < cnt; j++)
+                if (overlaps(xs[j], ns[j], gp, gn)) {
+                    if (!flush()) return total;
+                    break;
+                }
+            xs[cnt] = gp;
+            ns[cnt] = gn;
             wrote_dev(g);
             if (++cnt == NC_HIP_OPT_MULTI_MAX && !flush()) return total;
         }

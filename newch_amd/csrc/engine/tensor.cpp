@@ -233,7 +233,11 @@ char *dptr(nc_tensor *t) {
     return o->dev + t->offset * (int64_t)dtype_size(t->dtype);
 }
 
-void wrote_dev(nc_tensor *t) { owner_of(t)->res = RES_DEV; }
+void wrote_dev(nc_tensor *t) {
+    nc_tensor *o = owner_of(t);
+    o->res = RES_DEV;
+    o->wgen++;
+}
 
 char *hptr(nc_tensor *t, bool write) {
     nc_tensor *o = owner_of(t);
@@ -255,6 +259,7 @@ char *hptr(nc_tensor *t, bool write) {
         o->res |= RES_HOST;
     }
     if (write && o->dev) o->res = RES_HOST | RES_MAPPED;
+    if (write) o->wgen++;
     return o->host + t->offset * (int64_t)dtype_size(t->dtype);
 }
 

@@ -5,9 +5,12 @@
 // element.  prob is a function of x and two numbers per row: logp = (x - m) - ls with m the row
 // maximum (the reference's scan rule) and ls = logf(sum exp8(x - m)), and prob = exp8(logp).  So
 // the forward here reads x once and writes only stats = [N][2] {m, ls}; the backward recomputes
-// prob from x with those same fp32 operations, bit for bit what the reference stores, and reads x
-// where the reference reads prob: the forward moves 4 B/element instead of 8, the backward the
-// same 12.
+// prob = exp8((x - m) - ls) from x with the reference's fp32 operations and reads x where the
+// reference reads prob: the forward moves 4 B/element instead of 8, the backward the same 12.  Given
+// the stats, prob is bit for bit that expression.  ls itself comes from an fp64 sum of hardware
+// exponentials (the reductions' tolerance), where the reference takes logf of an fp32 sum of exp8
+// terms, so the recomputed prob can differ from the probabilities the reference saves in its last
+// bits: the gradient matches the reference's at the reductions' tolerance, not bit for bit.
 //
 // cross entropy forward, one wave per row with the row in registers (C % 4 == 0, C <= 4096, 16-byte
 // aligned): the max, the row sum of exp(x - m) (hardware exponential: the sum is only compared at the

@@ -1370,6 +1370,31 @@ def test_kernel_cross_entropy_nan_rows(K):
     assert np.isnan(LS.to_numpy(np.float32, 1)[0]) and np.isnan(loss_o)
 
 
+def test_engine_cross_entropy_logits_written_after_forward(eng):
+    """The cross-entropy backward recomputes the probabilities from the logits and the forward's row
+    statistics: a retained-graph second backward with the logits unchanged adds the same gradient
+    again, and after the logits were written (nc_copy_from) the backward refuses with NC_ERR_STATE
+    instead of mixing new logits with old statistics."""
+    L = eng.lib
+    rng = np.random.default_rng(44)
+    x = rng.standard_normal((64, 1024)).astype(np.float32)
+    lab = rng.integers(0, 1024, 64).astype(np.int32)
+    p = eng.param(x)
+    loss = L.nc_cross_entropy(p, eng.tensor(lab))
+    eng.check()
+    assert L.nc_backward_ex(loss, abi.BACKWARD_RETAIN, None, 0) == 0
+    g1 = eng.grad(p)
+    assert L.nc_backward_ex(loss, abi.BACKWARD_RETAIN, None, 0) == 0
+    assert_bits(eng.grad(p), (g1 + g1).astype(np.float32), "second backward, logits unchanged")
+    x2 = (x * 2).astype(np.float32)
+    assert L.nc_copy_from(p, x2.ctypes.data_as(c_void_p), x2.nbytes)
+    L.nc_backward_ex(loss, abi.BACKWARD_RETAIN, None, 0)
+    assert L.nc_status_code(eng.ctx) == abi.ERR_STATE
+    assert "logits were written after the forward" in L.nc_error(eng.ctx).decode()
+    L.nc_clear_error(eng.ctx)
+    eng.step_end()
+
+
 def test_kernel_loss_bad_labels(K):
     """The first row with an out-of-range label, packed (row << 32) | label, whatever the launch order."""
     N, C = 5000, 64
@@ -1492,6 +1517,79 @@ def test_engine_optim_state_roundtrip(eng):
     assert L.nc_optim_state(o, 0, 1) is None and L.nc_optim_get_step(o) == 1
     L.nc_optim_free(o)
     eng.step_end()
+
+
+@pytest.mark.parametrize("kind", ["sgd_momentum", "adam"])
+def test_engine_optim_duplicate_params_match_reference(eng, kind):
+    """A parameter listed twice (and a third parameter between): the reference updates the slots in
+    turn, so the second slot steps from the first one's result with its own state
+    (optim.c:172-213); the engine's multi-parameter launch must not run both on the same weights at
+    once.  Weights after two steps bit for bit against the compiled reference."""
+    if not O.REF_LIB.exists():
+        pytest.skip("oracle/_ref/libnc_ref.so not built")
+    rng = np.random.default_rng(91)
+    w0, w1 = (rng.standard_normal(4096).astype(np.float32) for _ in range(2))
+    Gs = [(rng.standard_normal(4096).astype(np.float32), rng.standard_normal(4096).astype(np.float32))
+          for _ in range(2)]
+    opts = (abi.OptimOpts(0.05, 0.9, 0.01, 0, 0, 0) if kind == "sgd_momentum"
+            else abi.OptimOpts(1e-2, 0, 0, 0.9, 0.999, 1e-8))
+
+    def run(e):
+        L = e.lib
+        p, q = e.param(w0), e.param(w1)
+        arr = (c_void_p * 3)(p, q, p)
+        o = (L.nc_sgd if kind == "sgd_momentum" else L.nc_adam)(e.ctx, arr, 3, opts)
+        assert o
+        for G0, G1 in Gs:
+            L.nc_optim_zero_grad(o)
+            loss = L.nc_add(L.nc_sum(L.nc_mul(p, e.tensor(G0)), abi.ALL_AXES, 0),
+                            L.nc_sum(L.nc_mul(q, e.tensor(G1)), abi.ALL_AXES, 0))
+            assert L.nc_backward_ex(loss, 0, None, 0) == 0
+            L.nc_optim_step(o)
+            e.check()
+        out = (e.read(p), e.read(q))
+        L.nc_optim_free(o)
+        e.step_end()
+        return out
+    with Engine(O.REF_LIB) as ref:
+        want = run(ref)
+    got = run(eng)
+    assert_bits(got[0], want[0], "parameter listed twice")
+    assert_bits(got[1], want[1], "parameter between")
+
+
+def test_engine_clip_grad_norm_duplicate_matches_reference(eng):
+    """clip_grad_norm over [p, q, p]: the reference counts p's squares twice and scales its
+    gradient twice (optim.c:216-233); total and gradients bit for bit against the compiled
+    reference."""
+    if not O.REF_LIB.exists():
+        pytest.skip("oracle/_ref/libnc_ref.so not built")
+    rng = np.random.default_rng(92)
+    G0, G1 = (rng.standard_normal(4096).astype(np.float32) for _ in range(2))
+
+    def run(e):
+        L = e.lib
+        p, q = e.param(np.zeros(4096, np.float32)), e.param(np.zeros(4096, np.float32))
+        loss = L.nc_add(L.nc_sum(L.nc_mul(p, e.tensor(G0)), abi.ALL_AXES, 0),
+                        L.nc_sum(L.nc_mul(q, e.tensor(G1)), abi.ALL_AXES, 0))
+        assert L.nc_backward_ex(loss, 0, None, 0) == 0
+        arr = (c_void_p * 3)(p, q, p)
+        total = np.float32(L.nc_clip_grad_norm(arr, 3, c_float(1.0)))
+        e.check()
+        out = (total, e.grad(p), e.grad(q))
+        e.step_end()
+        return out
+    with Engine(O.REF_LIB) as ref:
+        t_ref, gp_ref, gq_ref = run(ref)
+    t, gp, gq = run(eng)
+    exact = np.sqrt(2 * np.sum(G0.astype(np.float64) ** 2) + np.sum(G1.astype(np.float64) ** 2))
+    assert abs(float(t) - exact) <= 1e-6 * exact and abs(float(t_ref) - exact) <= 1e-6 * exact
+    coef = np.float32(1.0) / (t + np.float32(1e-6))
+    assert_bits(gp, ((G0 * coef).astype(np.float32) * coef).astype(np.float32), "p scaled twice")
+    assert_bits(gq, (G1 * coef).astype(np.float32), "q scaled once")
+    if t == t_ref:
+        assert_bits(gp, gp_ref, "p vs reference")
+        assert_bits(gq, gq_ref, "q vs reference")
 
 
 def test_engine_optim_errors_match_reference(eng):

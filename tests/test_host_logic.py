@@ -362,3 +362,36 @@ def test_ncw1_errors_match_reference(eng, tmp_path):
     got = _io_errors(eng, tmp_path / "o")
     for i, (w, g) in enumerate(zip(want, got)):
         assert w == g, f"case {i}: reference {w}, this engine {g}"
+
+
+def test_reduce_plans_fit_the_no_alloc_scratch(lib):
+    """nc_hip_reduce_fwd_noalloc keeps its partials in an 8 MiB static array: every reduction plan
+    needs at most that.  The plan (host arithmetic, no device) is evaluated at the boundaries of each
+    mode -- column scans whose column count sits just past target / k for k = 1..2048 (the chunk count
+    P = ceil(target / cols) steps there, cols * P is largest), few long rows just past and below the
+    wave-per-row cutoffs -- and over a seeded random sweep."""
+    from newch_amd.hip import RED
+    fn = lib.nc_hip_reduce_workspace
+    fn.restype = ctypes.c_size_t
+    fn.argtypes = [ctypes.c_int, ctypes.c_int64, ctypes.c_int64, ctypes.c_int64]
+    limit = 8 << 20
+    target = 256 * 2048  # columns the column-scan plan aims its partials at
+    shapes = []
+    for k in range(1, 2049):
+        for cols in (target // k - 1, target // k, target // k + 1):
+            if cols >= 2:
+                shapes += [(1, 1 << 20, cols), (2, 1 << 20, max(cols // 2, 2))]
+    for outer in (1, 2, 3, 255, 256, 257, 4095, 4096):
+        for R in (4097, 65536, 1 << 20, 1 << 24, 1 << 30, 1 << 32):
+            shapes.append((outer, R, 1))
+    rng = np.random.default_rng(8)
+    for _ in range(4000):
+        outer, R, inner = (int(v) for v in np.exp(rng.uniform(0, [9, 24, 16])).astype(np.int64) + 1)
+        shapes.append((outer, R, inner))
+    worst = 0
+    for outer, R, inner in shapes:
+        for kind in ("sum", "max"):
+            need = fn(RED[kind], outer, R, inner)
+            worst = max(worst, need)
+            assert need <= limit, (kind, outer, R, inner, need)
+    assert worst > limit // 2  # the boundary shapes come close to the bound

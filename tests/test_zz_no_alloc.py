@@ -1,7 +1,8 @@
 """nc_hip_reduce_fwd_noalloc, the reduction entry point that allocates nothing (called through the
 C ABI), against nc_hip_reduce_fwd with a caller's workspace: the same bits for every kind and plan (a
 full sum split into chunk partials, few long rows, column scans with chunk partials, short rows with
-no partials), two calls in a row on the shared scratch, the second on a smaller input."""
+no partials), two calls in a row on the shared scratch, the second on a smaller input; the device's
+free memory is unchanged across calls that need partials."""
 
 import ctypes
 from ctypes import c_int, c_int64, c_void_p
@@ -58,3 +59,24 @@ def test_reduce_noalloc_matches_workspace_entry(libs, kind):
                 assert_bits(Y1.to_numpy(np.float32, n), Y2.to_numpy(np.float32, n), f"{kind} values")
             if want_a:
                 assert_bits(A1.to_numpy(np.int32, n), A2.to_numpy(np.int32, n), f"{kind} indices")
+
+
+def test_reduce_noalloc_takes_no_device_memory(libs):
+    """After a first call (which looks up the scratch address), calls that need partials leave the
+    device's free memory as it was: the partials live in the static scratch."""
+    from newch_amd import hipmem as hm
+    lib, K, RED = libs
+    outer, R, inner = 7, 3000, 130  # column scans with chunk partials
+    print(f"reduce_fwd_noalloc sum outer={outer} R={R} inner={inner}: free memory around 5 calls", flush=True)
+    assert K.reduce_workspace("sum", outer, R, inner) > 0
+    x = np.random.default_rng(5).standard_normal((outer, R, inner)).astype(np.float32)
+    X, Y = dev(x), empty(4 * outer * inner)
+    assert lib.nc_hip_reduce_fwd_noalloc(RED["sum"], outer, R, inner, X.ptr, Y.ptr, None, None) == 0
+    sync()
+    free0, _ = hm.mem_info()
+    for _ in range(5):
+        rc = lib.nc_hip_reduce_fwd_noalloc(RED["sum"], outer, R, inner, X.ptr, Y.ptr, None, None)
+        assert rc == 0, lib.nc_hip_last_error().decode()
+    sync()
+    free1, _ = hm.mem_info()
+    assert free1 == free0, (free0, free1)
