@@ -167,14 +167,23 @@ def group_bcast(K, hm):
 
 def group_bcast_full(K, hm):
     """The whole configuration in one call: a[256,512,1,64] + b[1,1,512,64] -> 2^32 outputs (16 GiB),
-    which the kernel layer cuts into 2^30-output launches."""
+    forward and the sum-to-shape backward of both operands, which the kernel layer cuts into
+    2^30-element launches."""
     A = hm.DeviceBuffer.from_numpy(np.random.default_rng(3).standard_normal(1 << 23, dtype=np.float32))
     Bv = hm.DeviceBuffer.from_numpy((0.5 + 1.5 * np.random.default_rng(4).random(512 * 64)).astype(np.float32))
     n_out = 1 << 32
     O = hm.DeviceBuffer(4 * n_out)
-    fn = lambda: K.binary_fwd("add", (256, 512, 512, 64), A.ptr, (32768, 64, 0, 1), Bv.ptr, (0, 0, 64, 1),  # noqa: E731
-                              O.ptr, (1 << 24, 1 << 15, 64, 1))
-    return [("bcast_add_fwd_full", 4 * n_out + 4 * (1 << 23) + 4 * 512 * 64, n_out, fn)], [A, Bv, O]
+    shape = (256, 512, 512, 64)
+    sa, sb, so = (32768, 64, 0, 1), (0, 0, 64, 1), (1 << 24, 1 << 15, 64, 1)
+    fwd = lambda: K.binary_fwd("add", shape, A.ptr, sa, Bv.ptr, sb, O.ptr, so)  # noqa: E731
+    GA, GB = hm.DeviceBuffer(4 * (1 << 23)), hm.DeviceBuffer(4 * 512 * 64)
+    GA.zero(), GB.zero()
+    wsb = K.binary_bwd2_workspace(shape, sa, sb)
+    WS = hm.DeviceBuffer(max(wsb, 1))
+    bwd = lambda: K.binary_bwd2("add", shape, O.ptr, so, A.ptr, sa, Bv.ptr, sb, GA.ptr, sa, GB.ptr, sb,  # noqa: E731
+                                WS.ptr, wsb)
+    return [("bcast_add_fwd_full", 4 * n_out + 4 * (1 << 23) + 4 * 512 * 64, n_out, fwd),
+            ("bcast_add_bwd_full", 4 * n_out + 8 * (1 << 23) + 8 * 512 * 64, n_out, bwd)], [A, Bv, O, GA, GB, WS]
 
 
 ROWS, COLS = 65536, 1024
@@ -329,7 +338,7 @@ GROUPS = {
     "bcast": (["bcast_add_fwd", "bcast_mul_fwd", "bcast_div_fwd", "bcast_add_fwd_transposed_a",
                "bcast_add_fwd_inner_strided_a", "bcast_add_bwd", "bcast_mul_bwd", "bcast_div_bwd",
                "bcast_add_bwd_grad_a", "bcast_add_bwd_grad_b"], group_bcast),
-    "bcast_full": (["bcast_add_fwd_full"], group_bcast_full),
+    "bcast_full": (["bcast_add_fwd_full", "bcast_add_bwd_full"], group_bcast_full),
     "rows": (["softmax_fwd", "softmax_bwd", "log_softmax_fwd", "log_softmax_bwd", "layer_norm_fwd",
               "layer_norm_bwd", "max_argmax", "cross_entropy_fwd", "cross_entropy_bwd"], group_rows),
     "int8": (["quantize_rows", "dequantize_rows"], group_int8),
@@ -595,6 +604,8 @@ def engine_leg(K, hm, classes):
     del Ab
     L.nc_persistent_begin(ctx)
     Xp = L.nc_parameter(ctx, X, *abi.shape_arg((rows, C)))
+    Ap = L.nc_parameter(ctx, A, *abi.shape_arg((256, 512, 1, 64)))
+    Bp = L.nc_parameter(ctx, Bv, *abi.shape_arg((1, 1, 512, 64)))
     L.nc_persistent_end(ctx)
     check()
     sc = c_void_p()
@@ -623,6 +634,9 @@ def engine_leg(K, hm, classes):
         ("cross_entropy_fwd", lambda: L.nc_cross_entropy(X, LAB)),
         ("cross_entropy_fwd_bwd", lambda: L.nc_backward(L.nc_cross_entropy(Xp, LAB))),
         ("bcast_add_fwd_full", lambda: L.nc_add(A, Bv)),
+        # the configuration's full shape through autograd: forward, full sum, its 2^32-element
+        # gradient and the fused sum-to-shape backward of both operands
+        ("bcast_add_fwd_sum_bwd_full", lambda: L.nc_backward(L.nc_sum(L.nc_add(Ap, Bp), abi.ALL_AXES, 0))),
         ("adam_step_32_params", lambda: L.nc_optim_step(opt)),
         # the 32 gradients' norm (one sum launch, one read-back) and their rescale (one launch)
         ("clip_grad_norm_32_params", lambda: L.nc_clip_grad_norm(plist, nps, c_float(1.0))),
@@ -637,7 +651,8 @@ def engine_leg(K, hm, classes):
             L.nc_synchronize(ctx)
             ts.append(time.perf_counter() - t0)
             check()
-            L.nc_zero_grad(Xp)
+            for q in (Xp, Ap, Bp):
+                L.nc_zero_grad(q)
             L.nc_step_end(ctx)
         us = float(np.median(ts[WARM:])) * 1e6
         k = classes.get(label if label != "cross_entropy_fwd_bwd" else "cross_entropy_fwd")

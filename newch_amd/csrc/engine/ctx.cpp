@@ -95,8 +95,20 @@ static void poison(nc_ctx *ctx, char *p, size_t bytes) {
     if (ctx->poison && p && bytes && ctx->device >= 0) (void)nc_hip_fill(p, 1, 0xCD, (int64_t)bytes, ctx->stream);
 }
 
+// NC_FAIL_ALLOC_AT=N (read at nc_init): the context's N-th storage allocation request -- device
+// allocations and, without a device, host tensor storage, counted from 1 -- fails as out of memory,
+// so the sticky NC_ERR_OOM path and the recovery after it (nc_clear_error, nc_step_end) can be tested
+// without exhausting the device.
+static uint64_t fail_alloc_env() {
+    const char *v = getenv("NC_FAIL_ALLOC_AT");
+    return v && *v ? strtoull(v, nullptr, 10) : 0;
+}
+
+bool forced_alloc_failure(nc_ctx *ctx) { return ++ctx->storage_requests == ctx->fail_alloc_at; }
+
 // every device allocation the context makes goes through here (counted for nc_device_alloc_count)
 static hipError_t device_malloc(nc_ctx *ctx, char **p, size_t bytes) {
+    if (forced_alloc_failure(ctx)) return hipErrorOutOfMemory;
     const hipError_t e = hipMalloc((void **)p, bytes);
     if (e == hipSuccess) ctx->device_allocs++;
     return e;
@@ -329,6 +341,7 @@ nc_ctx *nc_init(const nc_config *cfg) {
     if (c.arena_chunk_bytes) ctx->darena.chunk_bytes = align_up(c.arena_chunk_bytes, kDevAlign);
     nc_manual_seed(ctx, c.seed);
     ctx->poison = poison_env();
+    ctx->fail_alloc_at = fail_alloc_env();
     detect_cpu(&ctx->cpu);
     ctx->n_threads = c.threads > 0 ? c.threads : ctx->cpu.n_cores;
     ctx->n_threads = std::min(std::max(ctx->n_threads, 1), 64);

@@ -206,6 +206,8 @@ struct nc_ctx {
 
     uint64_t device_allocs = 0;  // hipMalloc calls made for this context (arena chunks, large blocks, persistent)
     bool poison = false;         // NC_DEBUG_POISON: released device blocks are filled with 0xCD
+    uint64_t storage_requests = 0;  // storage allocations asked for (device allocations, host storage)
+    uint64_t fail_alloc_at = 0;     // NC_FAIL_ALLOC_AT: this request fails as out of memory (0: none)
     int device = -1;  // -1: no HIP device
     hipStream_t stream = nullptr;
     bool own_stream = false;
@@ -253,6 +255,8 @@ inline float *fptr(nc_tensor *t) { return (float *)dptr(t); }
 char *dptr_overwrite(nc_tensor *t);
 // marks a tensor's storage as written on the device (host mirror stale)
 void wrote_dev(nc_tensor *t);
+// counts a storage allocation request; true for the one NC_FAIL_ALLOC_AT names (a forced failure)
+bool forced_alloc_failure(nc_ctx *ctx);
 // host address of element 0 with the host copy current; write = the caller may write through it
 char *hptr(nc_tensor *t, bool write);
 void bcast_strides(const nc_tensor *t, int nd, const int64_t *shape, int64_t *out);

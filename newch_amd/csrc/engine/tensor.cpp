@@ -158,7 +158,7 @@ nc_tensor *tensor_new(nc_ctx *ctx, nc_dtype dt, int nd, const int64_t *shape, bo
         t->res = RES_DEV;
     } else {
         // no device: host storage only (shape logic works, compute ops report the missing device)
-        t->host = (char *)calloc(1, t->bytes ? t->bytes : 1);
+        t->host = forced_alloc_failure(ctx) ? nullptr : (char *)calloc(1, t->bytes ? t->bytes : 1);
         if (!t->host) {
             error(ctx, NC_ERR_OOM, "out of host memory");
             return nullptr;

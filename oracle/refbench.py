@@ -247,7 +247,7 @@ def _int8_and_sums(e: RefEngine, out: dict, mats: int, sum_n: int):
     L.nc_release(px)
 
 
-def reference_classes(threads: int, unary_n: int = 1 << 26, quant_mats: int = 8, sum_n: int = 1 << 28,
+def reference_classes(threads: int, unary_n: int = 1 << 26, quant_mats: int = 48, sum_n: int = 1 << 30,
                       groups=("unary", "broadcast", "rows", "int8")) -> dict:
     """{label: (seconds per launch, elements, sample description)} plus '_meta'."""
     e = RefEngine(threads)
@@ -257,11 +257,17 @@ def reference_classes(threads: int, unary_n: int = 1 << 26, quant_mats: int = 8,
         if "unary" in groups:
             _unary(e, out, unary_n)
         if "broadcast" in groups:
-            # add forward and backward over a whole 2^30-output chunk; the other variants on 2^28
-            _broadcast(e, out, 64, {"bcast_add_fwd", "bcast_add_bwd"})
-            _broadcast(e, out, 16, {"bcast_mul_fwd", "bcast_mul_bwd", "bcast_div_fwd", "bcast_div_bwd",
-                                    "bcast_add_fwd_transposed_a", "bcast_add_fwd_inner_strided_a",
-                                    "bcast_add_bwd_grad_a", "bcast_add_bwd_grad_b"})
+            # every variant over one whole 2^30-output chunk; the full 2^32-output shape is the
+            # configuration's 4 chunks through the same serial path (x4 time)
+            _broadcast(e, out, 64, {"bcast_add_fwd", "bcast_add_bwd", "bcast_mul_fwd", "bcast_mul_bwd",
+                                    "bcast_div_fwd", "bcast_div_bwd", "bcast_add_fwd_transposed_a",
+                                    "bcast_add_fwd_inner_strided_a", "bcast_add_bwd_grad_a",
+                                    "bcast_add_bwd_grad_b"})
+            for d in ("fwd", "bwd"):
+                s, n, _ = out[f"bcast_add_{d}"]
+                out[f"bcast_add_{d}_full"] = (4 * s, 4 * n, "a[64,512,1,64] + b[1,1,512,64] (one 2^30-output chunk) "
+                                              "timed, x4 for the configuration's 4 chunks = 2^32 outputs"
+                                              + ("; both gradients" if d == "bwd" else ""))
         if "rows" in groups:
             _rows(e, out)
         if "int8" in groups:

@@ -277,3 +277,32 @@ def test_engine_golden_with_poison(poisoned):
     for case, xview, has_b in T.LINEAR_CASES:
         T.test_engine_linear_golden(e, case, xview, has_b)
     e.check()
+
+
+def test_forced_device_out_of_memory_is_sticky_and_recovers(monkeypatch):
+    """NC_FAIL_ALLOC_AT=4: the context's fourth device allocation fails.  A parameter of 32 MiB (its
+    staging tensor and its persistent storage: allocations 1 and 2) and relu's output (3) succeed; the
+    add's output (4) fails: NULL and a sticky NC_ERR_OOM, another op returns NULL with the first
+    message kept; after nc_clear_error and nc_step_end the same op computes (the reference's sticky
+    errors, engine/src/core/ctx.c:375-390)."""
+    print("engine: NC_FAIL_ALLOC_AT=4, 32 MiB tensors", flush=True)
+    monkeypatch.setenv("NC_FAIL_ALLOC_AT", "4")
+    x = np.random.default_rng(12).standard_normal(1 << 23).astype(np.float32)
+    with Engine(lib=abi.load(abi.LIB_PATH)) as eng:
+        L = eng.lib
+        p = eng.param(x)
+        y = L.nc_relu(p)
+        eng.check()
+        assert L.nc_device_alloc_count(eng.ctx) == 3
+        assert not L.nc_add(p, y)
+        assert L.nc_status_code(eng.ctx) == abi.ERR_OOM
+        first = L.nc_error(eng.ctx).decode()
+        assert "out of memory" in first
+        assert not L.nc_mul(p, p)
+        assert L.nc_status_code(eng.ctx) == abi.ERR_OOM and L.nc_error(eng.ctx).decode() == first
+        L.nc_clear_error(eng.ctx)
+        L.nc_step_end(eng.ctx)
+        z = L.nc_add(p, p)
+        eng.check()
+        assert (eng.read(z).view(np.uint32) == (x + x).view(np.uint32)).all()
+        eng.step_end()

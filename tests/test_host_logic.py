@@ -395,3 +395,32 @@ def test_reduce_plans_fit_the_no_alloc_scratch(lib):
             worst = max(worst, need)
             assert need <= limit, (kind, outer, R, inner, need)
     assert worst > limit // 2  # the boundary shapes come close to the bound
+
+
+def test_forced_out_of_memory_is_sticky_and_recovers(lib, monkeypatch):
+    """NC_FAIL_ALLOC_AT=2 makes the context's second storage allocation fail: the call returns NULL
+    with NC_ERR_OOM, later calls keep the first error (the reference's sticky errors,
+    engine/src/core/ctx.c:375-390; ops return NULL while it stands, autograd.c:16), and
+    nc_clear_error plus nc_step_end recover."""
+    monkeypatch.setenv("NC_FAIL_ALLOC_AT", "2")
+    with Engine(lib=lib) as eng:
+        L = eng.lib
+        if has_device(L):
+            pytest.skip("host storage path: the device's allocations are tested on the GPU")
+        a = eng.tensor(np.arange(6, dtype=np.float32))
+        b = np.ones(6, np.float32)
+        nd, shp = abi.shape_arg((6,))
+        assert not L.nc_from_data(eng.ctx, abi.F32, b.ctypes.data_as(c_void_p), nd, shp)
+        assert L.nc_status_code(eng.ctx) == abi.ERR_OOM
+        first = L.nc_error(eng.ctx).decode()
+        assert "out of host memory" in first
+        nd2, shp2 = abi.shape_arg((2, 3))
+        assert not L.nc_reshape(a, nd2, shp2)  # an op while the error stands
+        assert L.nc_status_code(eng.ctx) == abi.ERR_OOM and L.nc_error(eng.ctx).decode() == first
+        L.nc_clear_error(eng.ctx)
+        L.nc_step_end(eng.ctx)
+        t = L.nc_from_data(eng.ctx, abi.F32, b.ctypes.data_as(c_void_p), nd, shp)
+        assert t and L.nc_ok(eng.ctx)
+        r = L.nc_reshape(t, nd2, shp2)
+        assert r and eng.shape(r) == (2, 3)
+        assert (eng.read(r) == 1).all()
