@@ -20,36 +20,33 @@
 // the value at k = 4 q + s, for A and B alike, so a K-contiguous operand feeds four MFMAs from one
 // 16-byte LDS read.
 //
-// Summation order (blocked like the reference's KC = 256 panels, kernels_avx2.c:234-247): K is cut
-// into panels of 256 k (16 stages).  Each panel's products are summed from zero in the accumulator
-// tiles, four per MFMA (64 roundings per panel); the first panel's sum is the running total and each
-// later panel's sum is added into it (one fp32 add per panel).  A small panel sum is not rounded
-// against the whole running total, so the error of a K-term dot product grows like that of the
-// reference's blocked sum rather than like K sequential additions.  The order is a property of the
-// kernel alone: the same for every tile size and grid, so results are identical run to run and on any
-// device.  It differs from the reference's serial order, so the parity bar is the fp32 error bound of
-// a K-term dot product.
+// Summation order (blocked, like the reference's register blocks summed from zero and added into C,
+// kernels_avx2.c:234-247): K is cut into panels of 32 k (two stages).  A panel's 32 products of an
+// output element are summed from zero, four per MFMA (eight MFMAs), and the panel sum is added into the
+// element's running total (one fp32 add per 32 k).  A small panel sum is not rounded against the whole
+// running total, so the error of a K-term dot product grows like that of a blocked sum rather than like
+// K sequential additions.  The order is a property of the kernel alone: the same for every tile size
+// and grid, so results are identical run to run and on any device.  It differs from the reference's
+// serial order, so the parity bar is the fp32 error bound of a K-term dot product.
 //
-// Tile sizes: 256 x 256 (8 waves of 8 x 4 tiles) for single-panel problems (K <= 256) that have at
-// least as many such tiles as the device has CUs; 256 x 128 (8 waves of 4 x 4 tiles, whose running
-// totals fit beside the panel accumulators) for larger K; else 128 x 128 (4 waves of 4 x 4) or 64 x 64
-// (4 waves of 2 x 2).  Blocks are remapped so each XCD (blocks b with b % 8 equal) works a contiguous
-// run of tiles, and tiles run in groups of 8 tile-rows so neighbouring blocks share panels in L2.
+// Tile sizes: 256 x 256 (8 waves of 8 x 4 tiles) when the problem has at least as many such tiles as
+// the device has CUs, else 128 x 128 (4 waves of 4 x 4) or 64 x 64 (4 waves of 2 x 2).  Blocks are
+// remapped so each XCD (blocks b with b % 8 equal) works a contiguous run of tiles, and tiles run in
+// groups of 8 tile-rows so neighbouring blocks share panels in L2.
 #include "common.hpp"
 
 namespace nchip {
 
 
 constexpr int kSgBK = 16;      // k per stage
-constexpr int kSgPanel = 16;   // stages per summation panel (256 k)
+constexpr int kSgPanel = 2;    // stages per summation panel (32 k)
+
 constexpr int kSgGroupM = 8;   // tile-rows per group in the block order
 
-// TOTAL: the kernel keeps a running total beside the panel accumulators (more than one panel);
 // MINB: workgroups per CU the register allocation leaves room for
-template <int TM_, int TN_, int WGM_, int WGN_, bool TOTAL_, int MINB_>
+template <int TM_, int TN_, int WGM_, int WGN_, int MINB_>
 struct SgCfg {
     static constexpr int TM = TM_, TN = TN_, WGM = WGM_, WGN = WGN_;
-    static constexpr bool TOTAL = TOTAL_;
     static constexpr int MINB = MINB_;
     static constexpr int NT = 64 * WGM * WGN;
     static constexpr int BM = 16 * TM * WGM, BN = 16 * TN * WGN;
@@ -58,10 +55,9 @@ struct SgCfg {
     static constexpr int STAGE = SLAB_A + SLAB_B;
     static constexpr size_t LDS = 2 * (size_t)STAGE;
 };
-using SgBig = SgCfg<8, 4, 2, 4, false, 1>;  // 256 x 256, K <= 256 only
-using SgWide = SgCfg<4, 4, 4, 2, true, 1>;  // 256 x 128
-using SgMid = SgCfg<4, 4, 2, 2, true, 2>;   // 128 x 128
-using SgSmall = SgCfg<2, 2, 2, 2, true, 4>; // 64 x 64
+using SgBig = SgCfg<8, 4, 2, 4, 1>;    // 256 x 256
+using SgMid = SgCfg<4, 4, 2, 2, 2>;    // 128 x 128
+using SgSmall = SgCfg<2, 2, 2, 2, 4>;  // 64 x 64
 
 struct SgBatch {
     int nb;  // 0: one matrix per operand
@@ -259,70 +255,85 @@ __device__ __forceinline__ TileAt locate(const SgArgs &p) {
     return at;
 }
 
-// The stage's MFMAs for this wave: fragments of its TM row blocks and TN column blocks, four k each.
-template <class Cfg>
-struct Frags {
+// The register-staged kernels keep a panel accumulator per tile beside the running totals: the
+// stage's fragments are read, its MFMAs (s = 0..3, the B fragment first: the tile is C^T, so each lane
+// ends up holding 4 consecutive columns of a row of C) add into the accumulators, and after a panel's
+// last stage the accumulators are added into the totals and cleared.
+template <class Cfg, bool AK, bool BK>
+__device__ __forceinline__ void stage_acc(const char *cur, f4 (&acc)[Cfg::TM][Cfg::TN], int wm, int wn, int fr, int fq) {
     f4 a[Cfg::TM], b[Cfg::TN];
-};
-
-template <class Cfg, bool AK, bool BK>
-__device__ __forceinline__ void read_frags(const char *cur, Frags<Cfg> &F, int wm, int wn, int fr, int fq) {
 #pragma unroll
-    for (int i = 0; i < Cfg::TM; i++) F.a[i] = fragment<Cfg::BM, AK>(cur, (wm * Cfg::TM + i) * 16 + fr, fq);
+    for (int i = 0; i < Cfg::TM; i++) a[i] = fragment<Cfg::BM, AK>(cur, (wm * Cfg::TM + i) * 16 + fr, fq);
 #pragma unroll
-    for (int j = 0; j < Cfg::TN; j++) F.b[j] = fragment<Cfg::BN, BK>(cur + Cfg::SLAB_A, (wn * Cfg::TN + j) * 16 + fr, fq);
-}
-
-// MFMAs S0 .. S1 - 1 of a stage.  The B fragment goes first: the tile is C^T, so each lane ends up
-// holding 4 consecutive columns of a row of C.
-template <class Cfg, int S0, int S1>
-__device__ __forceinline__ void mfma_steps(const Frags<Cfg> &F, f4 (&acc)[Cfg::TM][Cfg::TN]) {
+    for (int j = 0; j < Cfg::TN; j++) b[j] = fragment<Cfg::BN, BK>(cur + Cfg::SLAB_A, (wn * Cfg::TN + j) * 16 + fr, fq);
 #pragma unroll
-    for (int s = S0; s < S1; s++)
+    for (int s = 0; s < 4; s++)
 #pragma unroll
         for (int i = 0; i < Cfg::TM; i++)
 #pragma unroll
-            for (int j = 0; j < Cfg::TN; j++)
-                acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(F.b[j][s], F.a[i][s], acc[i][j], 0, 0, 0);
+            for (int j = 0; j < Cfg::TN; j++) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(b[j][s], a[i][s], acc[i][j], 0, 0, 0);
 }
 
-template <class Cfg, bool AK, bool BK>
-__device__ __forceinline__ void stage_mfma(const char *cur, f4 (&acc)[Cfg::TM][Cfg::TN], int wm, int wn, int fr, int fq) {
-    Frags<Cfg> F;
-    read_frags<Cfg, AK, BK>(cur, F, wm, wn, fr, fq);
-    mfma_steps<Cfg, 0, 4>(F, acc);
-}
-
-// The end of a panel that another panel follows: its sum becomes the running total (first panel) or
-// is added into it, and the accumulators restart from zero.
 template <class Cfg>
-__device__ __forceinline__ void fold_panel(f4 (&tot)[Cfg::TM][Cfg::TN], f4 (&acc)[Cfg::TM][Cfg::TN], bool first) {
-    if (first) {
+__device__ __forceinline__ void fold(f4 (&tot)[Cfg::TM][Cfg::TN], f4 (&acc)[Cfg::TM][Cfg::TN]) {
 #pragma unroll
-        for (int i = 0; i < Cfg::TM; i++)
+    for (int i = 0; i < Cfg::TM; i++)
 #pragma unroll
-            for (int j = 0; j < Cfg::TN; j++) tot[i][j] = acc[i][j];
-    } else {
+        for (int j = 0; j < Cfg::TN; j++) {
+            tot[i][j] = tot[i][j] + acc[i][j];
+            acc[i][j] = f4{0.f, 0.f, 0.f, 0.f};
+        }
+}
+
+// The direct-to-LDS kernel has a whole panel in LDS and works it row block by row block, so only one
+// row block's TN panel sums are live beside the totals: the B fragments of the panel's stages are read
+// once; per row block the A fragments are read, each tile sums its panel's products from zero (stage
+// 0's four MFMAs, then stage 1's), and the sums are added into the totals.  TWO: the panel has its
+// second stage (every panel but a last one of an odd stage count).
+template <class Cfg, bool AK, bool BK>
+__device__ __forceinline__ void panel_mfma(const char *c0, const char *c1, f4 (&tot)[Cfg::TM][Cfg::TN], int wm, int wn,
+                                           int fr, int fq) {
+    static_assert(Cfg::TN == 4, "one previous-row-block add per k step");
+    f4 b0[Cfg::TN], b1[Cfg::TN];
 #pragma unroll
-        for (int i = 0; i < Cfg::TM; i++)
+    for (int j = 0; j < Cfg::TN; j++) {
+        b0[j] = fragment<Cfg::BN, BK>(c0 + Cfg::SLAB_A, (wn * Cfg::TN + j) * 16 + fr, fq);
+        b1[j] = fragment<Cfg::BN, BK>(c1 + Cfg::SLAB_A, (wn * Cfg::TN + j) * 16 + fr, fq);
+    }
+    f4 a0 = fragment<Cfg::BM, AK>(c0, wm * Cfg::TM * 16 + fr, fq);
+    f4 a1 = fragment<Cfg::BM, AK>(c1, wm * Cfg::TM * 16 + fr, fq);
+    // Issue order, pinned by scheduling barriers: per row block, 8 k steps of the TN tiles' independent
+    // MFMAs; in each of the first TN steps one tile of the previous row block adds its finished sum
+    // into its total (the sum's last MFMA was issued at least TN MFMAs earlier, so the add needs no
+    // wait states and issues between MFMAs); the next row block's A fragments are read meanwhile.
+    f4 tp[Cfg::TN];
 #pragma unroll
-            for (int j = 0; j < Cfg::TN; j++) tot[i][j] = tot[i][j] + acc[i][j];
+    for (int i = 0; i < Cfg::TM; i++) {
+        f4 na0 = a0, na1 = a1;
+        if (i + 1 < Cfg::TM) {
+            const int row = (wm * Cfg::TM + i + 1) * 16 + fr;
+            na0 = fragment<Cfg::BM, AK>(c0, row, fq);
+            na1 = fragment<Cfg::BM, AK>(c1, row, fq);
+        }
+        f4 t[Cfg::TN];
+#pragma unroll
+        for (int s = 0; s < 8; s++) {
+            const f4 &a = s < 4 ? a0 : a1;
+#pragma unroll
+            for (int j = 0; j < Cfg::TN; j++) {
+                const f4 &b = s < 4 ? b0[j] : b1[j];
+                t[j] = __builtin_amdgcn_mfma_f32_16x16x4f32(b[s & 3], a[s & 3], s == 0 ? f4{0.f, 0.f, 0.f, 0.f} : t[j],
+                                                            0, 0, 0);
+            }
+            if (i > 0 && s < Cfg::TN) tot[i - 1][s] = tot[i - 1][s] + tp[s];
+            __builtin_amdgcn_sched_barrier(0);
+        }
+#pragma unroll
+        for (int j = 0; j < Cfg::TN; j++) tp[j] = t[j];
+        a0 = na0, a1 = na1;
     }
 #pragma unroll
-    for (int i = 0; i < Cfg::TM; i++)
-#pragma unroll
-        for (int j = 0; j < Cfg::TN; j++) acc[i][j] = f4{0.f, 0.f, 0.f, 0.f};
-}
-
-// After the last stage: with more than one panel, the last panel's sum is added into the running
-// total, and the result is left in acc.
-template <class Cfg>
-__device__ __forceinline__ void finish_panels(const f4 (&tot)[Cfg::TM][Cfg::TN], f4 (&acc)[Cfg::TM][Cfg::TN], int nk) {
-    if (nk <= kSgPanel) return;
-#pragma unroll
-    for (int i = 0; i < Cfg::TM; i++)
-#pragma unroll
-        for (int j = 0; j < Cfg::TN; j++) acc[i][j] = tot[i][j] + acc[i][j];
+    for (int j = 0; j < Cfg::TN; j++) tot[Cfg::TM - 1][j] = tot[Cfg::TM - 1][j] + tp[j];
 }
 
 // C = alpha acc + beta C over the wave's tiles.  acc[i][j] is the 16 x 16 tile C^T: lane l, element v
@@ -369,12 +380,11 @@ __global__ __launch_bounds__(Cfg::NT, Cfg::MINB) void k_sgemm(SgArgs p) {
     la.init(at.A, p.lda, p.M, p.K, at.m0, t);
     lb.init(at.B, p.ldb, p.N, p.K, at.n0, t);
 
-    f4 acc[Cfg::TM][Cfg::TN];
-    f4 tot[Cfg::TOTAL ? Cfg::TM : 1][Cfg::TOTAL ? Cfg::TN : 1];
+    f4 acc[Cfg::TM][Cfg::TN], tot[Cfg::TM][Cfg::TN];  // panel accumulators, running totals
 #pragma unroll
     for (int i = 0; i < Cfg::TM; i++)
 #pragma unroll
-        for (int j = 0; j < Cfg::TN; j++) acc[i][j] = f4{0.f, 0.f, 0.f, 0.f};
+        for (int j = 0; j < Cfg::TN; j++) acc[i][j] = tot[i][j] = f4{0.f, 0.f, 0.f, 0.f};
 
     const int nk = (p.K + kSgBK - 1) / kSgBK;
     if (nk > 0) {
@@ -389,10 +399,8 @@ __global__ __launch_bounds__(Cfg::NT, Cfg::MINB) void k_sgemm(SgArgs p) {
             la.load((kt + 1) * kSgBK);
             lb.load((kt + 1) * kSgBK);
         }
-        stage_mfma<Cfg, AK, BK>(smem + (kt & 1) * Cfg::STAGE, acc, wm, wn, fr, fq);
-        if constexpr (Cfg::TOTAL) {
-            if (kt % kSgPanel == kSgPanel - 1 && kt + 1 < nk) fold_panel<Cfg>(tot, acc, kt < kSgPanel);
-        }
+        stage_acc<Cfg, AK, BK>(smem + (kt & 1) * Cfg::STAGE, acc, wm, wn, fr, fq);
+        if (kt % kSgPanel == kSgPanel - 1 || kt + 1 == nk) fold<Cfg>(tot, acc);
         // the other stage was last read before the previous barrier, so it can be refilled now
         if (kt + 1 < nk) {
             char *next = smem + ((kt + 1) & 1) * Cfg::STAGE;
@@ -401,18 +409,17 @@ __global__ __launch_bounds__(Cfg::NT, Cfg::MINB) void k_sgemm(SgArgs p) {
         }
         __syncthreads();
     }
-    if constexpr (Cfg::TOTAL) finish_panels<Cfg>(tot, acc, nk);
-    write_tiles<Cfg>(p, at, acc, wm, wn, fr, fq);
+    write_tiles<Cfg>(p, at, tot, wm, wn, fr, fq);
 }
 
 // ------------------------------------------------------------------------------------------------
-// Large FAST problems: the 256 x 128 tile, its panels loaded straight from global memory into LDS
-// (global_load_lds_dwordx4) three stages ahead through four LDS stages, with no staging registers and
-// no LDS write instructions; one barrier per stage.  A stage of an R-row panel is R / 16 load
+// Large FAST problems: the 256 x 256 tile, its operand panels loaded straight from global memory into
+// LDS (global_load_lds_dwordx4) a summation panel (two stages) ahead through four LDS stages, with no
+// staging registers and no LDS write instructions; one barrier per summation panel.  A stage of an R-row panel is R / 16 load
 // instructions of 1 KiB each: 16 rows of a K-contiguous panel (lane l: row l / 4, the chunk that
 // belongs at position l % 4 under the row's permutation) or 256 / R k-rows of a M/N-contiguous one
 // (lane l: k-row l / (R / 4), position l % (R / 4), loading the rows the k-row's permutation puts
-// there).  The 24 instructions of a stage (16 for A, 8 for B) are dealt three to a wave.  Rows past
+// there).  The 32 instructions of a stage (16 for A, 16 for B) are dealt four to a wave.  Rows past
 // the matrix are clamped as in the staged kernel's FAST loads.
 constexpr int kSgDmaStages = 4;
 
@@ -472,28 +479,30 @@ __global__ __launch_bounds__(Cfg::NT, 1) void k_sgemm_dma(SgArgs p) {
         for (int i = 0; i < D::PER; i++) dma16(src[i] + kt * kstep[i], __builtin_amdgcn_readfirstlane(st + loff[i]));
     };
 
-    f4 acc[Cfg::TM][Cfg::TN], tot[Cfg::TM][Cfg::TN];
+    f4 tot[Cfg::TM][Cfg::TN];  // running totals
 #pragma unroll
     for (int i = 0; i < Cfg::TM; i++)
 #pragma unroll
-        for (int j = 0; j < Cfg::TN; j++) acc[i][j] = f4{0.f, 0.f, 0.f, 0.f};
+        for (int j = 0; j < Cfg::TN; j++) tot[i][j] = f4{0.f, 0.f, 0.f, 0.f};
 
-    const int nk = p.K / kSgBK;
-    for (int kt = 0; kt < kSgDmaStages - 1 && kt < nk; kt++) issue(kt);
-    for (int kt = 0; kt < nk; kt++) {
-        // this wave's loads of stage kt are done once at most PER per later stage in flight remain
-        const int ahead = min(nk - 1 - kt, kSgDmaStages - 2);
-        if (ahead == 2) wait_vmcnt<2 * D::PER>();
-        else if (ahead == 1) wait_vmcnt<D::PER>();
-        else wait_vmcnt<0>();
-        __builtin_amdgcn_s_barrier();  // every wave's loads of stage kt have landed; stage kt-1's reads are done
+    // LDS stage slots 0-1 and 2-3 alternate between panels: panel q + 1 loads while panel q is worked
+    // (K is a multiple of 32: whole panels)
+    const int npanel = p.K / (kSgBK * kSgPanel);
+    auto issue_panel = [&](int q) {
+        issue(kSgPanel * q);
+        issue(kSgPanel * q + 1);
+    };
+    if (npanel > 0) issue_panel(0);
+    for (int q = 0; q < npanel; q++) {
+        wait_vmcnt<0>();               // this wave's loads of panel q (the only ones in flight)
+        __builtin_amdgcn_s_barrier();  // every wave's loads of panel q have landed; panel q - 1 is read
         asm volatile("" ::: "memory");
-        if (kt + kSgDmaStages - 1 < nk) issue(kt + kSgDmaStages - 1);  // into the stage kt-1 used
-        stage_mfma<Cfg, AK, BK>(smem + (kt % kSgDmaStages) * Cfg::STAGE, acc, wm, wn, fr, fq);
-        if (kt % kSgPanel == kSgPanel - 1 && kt + 1 < nk) fold_panel<Cfg>(tot, acc, kt < kSgPanel);
+        if (q + 1 < npanel) issue_panel(q + 1);  // into the slots panel q - 1 used
+        const int k0 = kSgPanel * q;
+        panel_mfma<Cfg, AK, BK>(smem + (k0 % kSgDmaStages) * Cfg::STAGE,
+                                      smem + ((k0 + 1) % kSgDmaStages) * Cfg::STAGE, tot, wm, wn, fr, fq);
     }
-    finish_panels<Cfg>(tot, acc, nk);
-    write_tiles<Cfg>(p, at, acc, wm, wn, fr, fq);
+    write_tiles<Cfg>(p, at, tot, wm, wn, fr, fq);
 }
 
 template <class Cfg, bool AK, bool BK, bool VEC, bool FAST>
@@ -509,8 +518,6 @@ static void sg_attr() {
 
 template <class Cfg, bool AK, bool BK, bool VEC, bool FAST>
 static int sg_launch(SgArgs &p, int64_t count, hipStream_t st, const char *what) {
-    if (!Cfg::TOTAL && p.K > kSgBK * kSgPanel)
-        return set_error(NC_HIP_ERR_ARG, "%s: K %d needs a running total this tile keeps none of", what, p.K);
     p.tiles_m = (p.M + Cfg::BM - 1) / Cfg::BM;
     p.tiles_n = (p.N + Cfg::BN - 1) / Cfg::BN;
     const int64_t blocks = (int64_t)p.tiles_m * p.tiles_n * count;
@@ -522,9 +529,6 @@ static int sg_launch(SgArgs &p, int64_t count, hipStream_t st, const char *what)
 
 #ifndef SG_DMA
 #define SG_DMA 1
-#endif
-#ifndef SG_DMA_MIN_K
-#define SG_DMA_MIN_K 512
 #endif
 template <class Cfg, bool AK, bool BK>
 static int sg_launch_dma(SgArgs &p, int64_t count, hipStream_t st, const char *what) {
@@ -543,17 +547,13 @@ static int sg_launch_dma(SgArgs &p, int64_t count, hipStream_t st, const char *w
     return check_launch(what);
 }
 
+// the register-staged kernels (128 x 128 and 64 x 64 tiles), by operand layout and load width
 template <class Cfg>
-static int sg_layouts(SgArgs &p, int ta, int tb, bool vec, int64_t count, hipStream_t st, const char *what) {
+static int sg_layouts(SgArgs &p, int ta, int tb, bool vec, bool fast, int64_t count, hipStream_t st, const char *what) {
     const bool ak = !ta, bk = tb != 0;
-    const bool fast = vec && p.K % kSgBK == 0 && (ak || p.M % 4 == 0) && (bk || p.N % 4 == 0);
-    // the DMA kernel clamps M/N-contiguous chunks onto the last 4 rows: at least 4 rows there
-    const bool dma = SG_DMA && std::is_same<Cfg, SgWide>::value && fast && p.K >= SG_DMA_MIN_K && (ak || p.M >= 4) &&
-                     (bk || p.N >= 4);
 #define NC_SG_CASE(AK_, BK_)                                                                \
     if (ak == AK_ && bk == BK_)                                                             \
-        return dma   ? sg_launch_dma<SgWide, AK_, BK_>(p, count, st, what)                  \
-               : fast ? sg_launch<Cfg, AK_, BK_, true, true>(p, count, st, what)            \
+        return fast ? sg_launch<Cfg, AK_, BK_, true, true>(p, count, st, what)              \
                : vec  ? sg_launch<Cfg, AK_, BK_, true, false>(p, count, st, what)           \
                       : sg_launch<Cfg, AK_, BK_, false, false>(p, count, st, what);
     NC_SG_CASE(true, true)
@@ -566,19 +566,31 @@ static int sg_layouts(SgArgs &p, int ta, int tb, bool vec, int64_t count, hipStr
 
 static int64_t tiles_of(int64_t M, int64_t N, int bm, int bn) { return ((M + bm - 1) / bm) * ((N + bn - 1) / bn); }
 
-// the largest tile that still gives every CU a tile (256 x 256 only for a single panel), else the
-// smallest
+// The 256 x 256 direct-to-LDS kernel for aligned problems (16-byte rows, K a multiple of 16) with at
+// least a tile per CU; otherwise the largest register-staged tile that still gives every CU a tile,
+// else the smallest.
 static int sg_run(SgArgs &p, int ta, int tb, int64_t count, hipStream_t st, const char *what) {
     // 16-byte loads need every matrix's rows 16-byte aligned: the matrices behind a pointer array may
     // start anywhere, so those take the scalar loads
     bool vec = !p.pa && aligned16(p.A) && aligned16(p.B) && p.lda % 4 == 0 && p.ldb % 4 == 0;
     for (int d = 0; d < p.bat.nb; d++) vec = vec && p.bat.st[0][d] % 4 == 0 && p.bat.st[1][d] % 4 == 0;
+    const bool ak = !ta, bk = tb != 0;
+    const bool fast = vec && p.K % kSgBK == 0 && (ak || p.M % 4 == 0) && (bk || p.N % 4 == 0);
     const int64_t cus = num_cus();
-    if (p.K <= kSgBK * kSgPanel && tiles_of(p.M, p.N, SgBig::BM, SgBig::BN) * count >= cus)
-        return sg_layouts<SgBig>(p, ta, tb, vec, count, st, what);
-    if (tiles_of(p.M, p.N, SgWide::BM, SgWide::BN) * count >= cus) return sg_layouts<SgWide>(p, ta, tb, vec, count, st, what);
-    if (tiles_of(p.M, p.N, SgMid::BM, SgMid::BN) * count >= cus) return sg_layouts<SgMid>(p, ta, tb, vec, count, st, what);
-    return sg_layouts<SgSmall>(p, ta, tb, vec, count, st, what);
+    // the DMA kernel clamps M/N-contiguous chunks onto the last 4 rows: at least 4 rows there
+    const bool dma = SG_DMA && fast && p.K > 0 && p.K % (kSgBK * kSgPanel) == 0 && (ak || p.M >= 4) && (bk || p.N >= 4);
+    if (dma && tiles_of(p.M, p.N, SgBig::BM, SgBig::BN) * count >= cus) {
+#define NC_SG_DMA(AK_, BK_) \
+    if (ak == AK_ && bk == BK_) return sg_launch_dma<SgBig, AK_, BK_>(p, count, st, what);
+        NC_SG_DMA(true, true)
+        NC_SG_DMA(true, false)
+        NC_SG_DMA(false, true)
+        NC_SG_DMA(false, false)
+#undef NC_SG_DMA
+    }
+    if (tiles_of(p.M, p.N, SgMid::BM, SgMid::BN) * count >= cus)
+        return sg_layouts<SgMid>(p, ta, tb, vec, fast, count, st, what);
+    return sg_layouts<SgSmall>(p, ta, tb, vec, fast, count, st, what);
 }
 
 static bool fits_int(int64_t v) { return v >= 0 && v <= INT32_MAX; }

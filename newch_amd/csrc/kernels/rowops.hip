@@ -662,6 +662,144 @@ __global__ __launch_bounds__(kLnB, NC_LN_BWD_WAVES_PER_EU) void k_ln_bwd_pp(cons
     }
 }
 
+// Backward for full rows of 512 VH floats (VH = 1, 2) that write gx, each row split between the two
+// waves of a pair: wave 2p + h of the workgroup holds columns [h D / 2, (h + 1) D / 2) of the pair's
+// rows, so a wave's bundle (x, g and the old gx) is half a row and two bundles fit in 128 VGPRs: four
+// waves per SIMD instead of the two of k_ln_bwd_pp.  Per row the two halves' fp64 sums (sum of g w,
+// sum of g w xhat) meet in LDS: each wave writes its wave sum, one barrier, and both waves add half 0
+// then half 1.  The workgroup's pairs step through their rows together (pair p of workgroup b takes
+// rows P b + p, P b + p + P G, ...), so every wave meets the same barriers; the sum slots alternate
+// between two sets, since a set is rewritten only after the next barrier, which every wave reaches
+// after reading it.  Rows stream through two bundles as in k_ln_bwd_pp.  gw / gb: each wave's column
+// partials in fp32 in row order; at the end a column's partials of the workgroup's pairs are added in
+// pair order in fp64 (the workgroup's partial, added up by k_ln_cols_combine).
+constexpr int kLnPairWaves = 16;  // one 1024-lane workgroup per CU
+constexpr int kLnPairs = kLnPairWaves / 2;
+template <int VH, bool ACC, bool HW>
+__global__ __launch_bounds__(kLnPairWaves *kWave, 4) void k_ln_bwd_pair(const float *__restrict__ x,
+                                                                        const float *__restrict__ w,
+                                                                        const float *__restrict__ stats,
+                                                                        const float *__restrict__ g,
+                                                                        float *__restrict__ gx,
+                                                                        double *__restrict__ part, int64_t rows) {
+    constexpr int D = 512 * VH, nh = VH * kWave;  // row length, float4 per half row
+    __shared__ f4 wsh[2 * nh];
+    __shared__ double xch[2][kLnPairWaves][2];
+    __shared__ float colp[kLnPairWaves][2][4 * nh];  // each wave's gw / gb column partials
+    const int lane = threadIdx.x & (kWave - 1);
+    const int wv = threadIdx.x / kWave, h = wv & 1, pr = wv >> 1;
+    const bool cols = part != nullptr;
+    if constexpr (HW) {
+        for (int j = threadIdx.x; j < 2 * nh; j += kLnPairWaves * kWave) wsh[j] = ((const f4 *)w)[j];
+        __syncthreads();
+    }
+    const int c0 = h * nh;  // this wave's first float4 of a row
+    f4 aw[VH], ab[VH];
+#pragma unroll
+    for (int k = 0; k < VH; k++) aw[k] = ab[k] = f4{0.f, 0.f, 0.f, 0.f};
+    struct Bundle {
+        f4 x[VH], g[VH], o[VH];
+        f2 st;
+    };
+    auto load = [&](int64_t r, Bundle &b) {
+        const f4 *xr = (const f4 *)(x + r * D) + c0, *gr = (const f4 *)(g + r * D) + c0;
+        const f4 *orow = (const f4 *)(gx + r * D) + c0;
+#pragma unroll
+        for (int k = 0; k < VH; k++) {
+            b.x[k] = __builtin_nontemporal_load(xr + lane + k * kWave);
+            b.g[k] = __builtin_nontemporal_load(gr + lane + k * kWave);
+            if (ACC) b.o[k] = __builtin_nontemporal_load(orow + lane + k * kWave);
+        }
+        b.st = *(const f2 *)(stats + 2 * r);
+    };
+    auto terms = [&](const Bundle &b, int k, f4 &xh, f4 &gw) {
+        const float mean = b.st.x, rstd = b.st.y;
+        const f4 ww = HW ? wsh[c0 + lane + k * kWave] : f4{1.f, 1.f, 1.f, 1.f};
+        xh.x = (b.x[k].x - mean) * rstd;
+        xh.y = (b.x[k].y - mean) * rstd;
+        xh.z = (b.x[k].z - mean) * rstd;
+        xh.w = (b.x[k].w - mean) * rstd;
+        gw.x = HW ? b.g[k].x * ww.x : b.g[k].x;
+        gw.y = HW ? b.g[k].y * ww.y : b.g[k].y;
+        gw.z = HW ? b.g[k].z * ww.z : b.g[k].z;
+        gw.w = HW ? b.g[k].w * ww.w : b.g[k].w;
+    };
+    // one row of the pair: called by every wave of the workgroup at the same step (one barrier)
+    auto step = [&](int64_t r, const Bundle &b, int par) {
+        const bool valid = r < rows;
+        double sg = 0.0, sgx = 0.0;
+        if (valid) {
+#pragma unroll
+            for (int k = 0; k < VH; k++) {
+                f4 xh, gw4;
+                terms(b, k, xh, gw4);
+                sg += ((double)gw4.x + (double)gw4.y) + ((double)gw4.z + (double)gw4.w);
+                sgx += ((double)(gw4.x * xh.x) + (double)(gw4.y * xh.y)) + ((double)(gw4.z * xh.z) + (double)(gw4.w * xh.w));
+                if (cols) {
+                    aw[k].x += b.g[k].x * xh.x;
+                    aw[k].y += b.g[k].y * xh.y;
+                    aw[k].z += b.g[k].z * xh.z;
+                    aw[k].w += b.g[k].w * xh.w;
+                    ab[k] += b.g[k];
+                }
+            }
+        }
+        sg = wave_sum(sg);
+        sgx = wave_sum(sgx);
+        if (lane == 0) {
+            xch[par][wv][0] = sg;
+            xch[par][wv][1] = sgx;
+        }
+        __syncthreads();
+        if (!valid) return;
+        const double tg = xch[par][2 * pr][0] + xch[par][2 * pr + 1][0];
+        const double tgx = xch[par][2 * pr][1] + xch[par][2 * pr + 1][1];
+        const float mg = (float)(tg / (double)D), mgx = (float)(tgx / (double)D);
+        const float rstd = b.st.y;
+        f4 *dx = (f4 *)(gx + r * D) + c0;
+#pragma unroll
+        for (int k = 0; k < VH; k++) {
+            f4 xh, gw4;
+            terms(b, k, xh, gw4);
+            f4 o = ACC ? b.o[k] : f4{0.f, 0.f, 0.f, 0.f};
+            o.x = o.x + rstd * ((gw4.x - mg) - xh.x * mgx);
+            o.y = o.y + rstd * ((gw4.y - mg) - xh.y * mgx);
+            o.z = o.z + rstd * ((gw4.z - mg) - xh.z * mgx);
+            o.w = o.w + rstd * ((gw4.w - mg) - xh.w * mgx);
+            __builtin_nontemporal_store(o, dx + lane + k * kWave);
+        }
+    };
+    const int64_t Q = (int64_t)gridDim.x * kLnPairs;       // rows per step over the grid
+    const int64_t q0 = (int64_t)blockIdx.x * kLnPairs;     // this workgroup's first pair
+    const int64_t nsteps = q0 < rows ? (rows - q0 + Q - 1) / Q : 0;  // pair 0 has the most rows
+    const int64_t myq = q0 + pr;
+    Bundle A, B;
+    if (nsteps > 0 && myq < rows) load(myq, A);
+    for (int64_t k = 0; k < nsteps; k += 2) {
+        const int64_t ra = myq + k * Q, rb = ra + Q, ra2 = rb + Q;
+        const bool has_b = k + 1 < nsteps;  // uniform over the workgroup
+        if (has_b && rb < rows) load(rb, B);
+        step(ra, A, 0);
+        if (k + 2 < nsteps && ra2 < rows) load(ra2, A);
+        if (has_b) step(rb, B, 1);
+    }
+    if (!cols) return;
+#pragma unroll
+    for (int k = 0; k < VH; k++) {
+        ((f4 *)colp[wv][0])[lane + k * kWave] = aw[k];
+        ((f4 *)colp[wv][1])[lane + k * kWave] = ab[k];
+    }
+    __syncthreads();
+    double *out = part + (size_t)blockIdx.x * 2 * D;
+    for (int i = threadIdx.x; i < 2 * D; i += kLnPairWaves * kWave) {
+        const int which = i / D, c = i % D, hh = c / (4 * nh), cc = c % (4 * nh);
+        double t = 0.0;
+#pragma unroll
+        for (int p = 0; p < kLnPairs; p++) t += (double)colp[2 * p + hh][which][cc];
+        out[i] = t;
+    }
+}
+
 // Generic backward: one workgroup per row for gx, and column partials for gw/gb.
 template <bool ACC>
 __global__ __launch_bounds__(kRowB) void k_ln_bwd_blk(const float *__restrict__ x, const float *__restrict__ w,
@@ -757,6 +895,9 @@ static int vpl_for(int64_t C) {
 #ifndef NC_LN_BWD_PP_BLOCKS_PER_CU
 #define NC_LN_BWD_PP_BLOCKS_PER_CU 1  // k_ln_bwd_pp
 #endif
+#ifndef NC_LN_BWD_PAIR
+#define NC_LN_BWD_PAIR 1  // k_ln_bwd_pair for rows of 512 and 1024 floats
+#endif
 #ifndef NC_ROWS_GRID_PER_CU
 #define NC_ROWS_GRID_PER_CU 65536
 #endif
@@ -795,6 +936,7 @@ struct LnPlan {
     bool reg;
     int vpl;
     bool full;                       // k_ln_bwd_pp (full rows of up to 1024 floats, gx written)
+    bool pair;                       // k_ln_bwd_pair (rows of 512 or 1024 floats, gx written)
     int64_t blocks, rows_per_block;  // register path
     int64_t chunk;
     int P;                           // generic path
@@ -808,6 +950,14 @@ static LnPlan ln_plan(int64_t rows, int64_t D, bool aligned, bool has_gx) {
     p.reg = p.vpl != 0;
     if (p.reg) {
         p.full = has_gx && p.vpl <= 4 && D == (int64_t)p.vpl * 4 * kWave;
+        p.pair = NC_LN_BWD_PAIR && p.full && (p.vpl == 2 || p.vpl == 4);
+        if (p.pair) {  // one workgroup per CU of a 256-CU part, rows dealt to its pairs in turn
+            p.blocks = std::min<int64_t>(kPlanCUs, (rows + kLnPairs - 1) / kLnPairs);
+            if (p.blocks < 1) p.blocks = 1;
+            p.rows_per_block = 0;
+            p.ws = (size_t)p.blocks * 2 * D * sizeof(double);
+            return p;
+        }
         const int per_cu = p.full ? NC_LN_BWD_PP_BLOCKS_PER_CU : p.vpl <= 4 ? NC_LN_BWD_BLOCKS_PER_CU : 1;
         // the resident workgroups of a 256-CU part: rows_per_block fixes which rows each gw/gb
         // partial holds, so it depends on the shape only
@@ -907,7 +1057,21 @@ extern "C" NC_HIP_API int nc_hip_layer_norm_bwd(int64_t rows, int64_t D, const f
     if (cols && (ws_bytes < p.ws || !ws))
         return set_error(NC_HIP_ERR_WORKSPACE, "nc_hip_layer_norm_bwd: workspace of %zu bytes needed", p.ws);
     double *part = cols ? (double *)ws : nullptr;
-    if (p.reg) {
+    if (p.pair) {
+        const dim3 grid((unsigned)p.blocks), block(kLnPairWaves * kWave);
+#define NC_LN_PAIR(VH_, ACC_)                                                                                     \
+    do {                                                                                                          \
+        if (w) hipLaunchKernelGGL((k_ln_bwd_pair<VH_, ACC_, true>), grid, block, 0, st, x, w, stats, g, gx, part, rows); \
+        else hipLaunchKernelGGL((k_ln_bwd_pair<VH_, ACC_, false>), grid, block, 0, st, x, w, stats, g, gx, part, rows); \
+    } while (0)
+        if (p.vpl == 4 && accumulate) NC_LN_PAIR(2, true);
+        else if (p.vpl == 4) NC_LN_PAIR(2, false);
+        else if (accumulate) NC_LN_PAIR(1, true);
+        else NC_LN_PAIR(1, false);
+#undef NC_LN_PAIR
+        if (cols)
+            hipLaunchKernelGGL(k_ln_cols_combine, dim3((unsigned)((D + kCombCols - 1) / kCombCols), 2), kCombCols * kCombSlices, 0, st, part, gw, gb, D, (int)p.blocks);
+    } else if (p.reg) {
         const size_t lds = ln_bwd_lds(p.vpl, D, cols);
         if (lds > 65536) return set_error(NC_HIP_ERR_ARG, "nc_hip_layer_norm_bwd: D too large for LDS combine");
         const bool full = p.full;
