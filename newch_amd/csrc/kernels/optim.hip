@@ -238,10 +238,41 @@ __global__ __launch_bounds__(kSB) void k_sumsq_multi(SumsqMulti m, double *__res
 }
 
 // ss = (((ss or 0) + S_0) + S_1) + ..., S_t tensor t's partials summed as k_sumsq_finish sums them:
-// the bits of one nc_hip_sumsq per tensor in turn
+// the bits of one nc_hip_sumsq per tensor in turn.  ONE: every tensor has at most kSB partials (one
+// per thread), so the loads of all tensors go out at once and their wave sums interleave (the
+// tensor-by-tensor loop waited for each tensor's loads and barrier in turn: 20 us for 32 tensors);
+// per tensor the arithmetic is sum_parts' (the thread's partial added to 0, the wave sum, the waves
+// added in order).
+template <bool ONE>
 __global__ __launch_bounds__(kSB) void k_sumsq_multi_finish(const double *__restrict__ part, SumsqMulti m, double *ss,
                                                             int accumulate) {
     double acc = accumulate ? *ss : 0.0;
+    if constexpr (ONE) {
+        __shared__ double sh[NC_HIP_OPT_MULTI_MAX][kSB / kWave];
+        double v[NC_HIP_OPT_MULTI_MAX];
+#pragma unroll
+        for (int t = 0; t < NC_HIP_OPT_MULTI_MAX; t++) {
+            const int i = m.first[t] + (int)threadIdx.x;
+            v[t] = t < m.count && i < m.first[t + 1] ? part[i] : 0.0;
+        }
+#pragma unroll
+        for (int t = 0; t < NC_HIP_OPT_MULTI_MAX; t++) {
+            if (t < m.count) {
+                const double w = wave_sum(0.0 + v[t]);
+                if ((threadIdx.x & (kWave - 1)) == 0) sh[t][threadIdx.x / kWave] = w;
+            }
+        }
+        __syncthreads();
+        if (threadIdx.x == 0) {
+            for (int t = 0; t < m.count; t++) {
+                double s = 0.0;
+                for (int w = 0; w < kSB / kWave; w++) s += sh[t][w];
+                acc = acc + s;
+            }
+            *ss = acc;
+        }
+        return;
+    }
     for (int t = 0; t < m.count; t++) {
         const double s = sum_parts(part + m.first[t], m.first[t + 1] - m.first[t]);
         if (threadIdx.x == 0) acc = acc + s;
@@ -469,7 +500,10 @@ extern "C" NC_HIP_API int nc_hip_sumsq_multi(int count, const float *const *x, c
     }
     hipStream_t st = as_stream(stream);
     if (m.first[count] > 0) hipLaunchKernelGGL(k_sumsq_multi, m.first[count], kSB, 0, st, m, (double *)ws);
-    hipLaunchKernelGGL(k_sumsq_multi_finish, 1, kSB, 0, st, (const double *)ws, m, ss, accumulate ? 1 : 0);
+    bool one = true;
+    for (int t = 0; t < count; t++) one = one && m.first[t + 1] - m.first[t] <= kSB;
+    if (one) hipLaunchKernelGGL(k_sumsq_multi_finish<true>, 1, kSB, 0, st, (const double *)ws, m, ss, accumulate ? 1 : 0);
+    else hipLaunchKernelGGL(k_sumsq_multi_finish<false>, 1, kSB, 0, st, (const double *)ws, m, ss, accumulate ? 1 : 0);
     return check_launch("nc_hip_sumsq_multi");
 }
 
