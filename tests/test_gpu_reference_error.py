@@ -11,7 +11,12 @@ everywhere; the reference's own result is reported beside it and flagged where i
   * a sum-to-shape gradient of 131,072 terms per element (grad_b of a[131072,1,64] + b[1,32,64], the
     term count of the configuration's grad_b[512,64]): the reference's row_acc adds them one by one in
     fp32 (engine/src/ops/ops_elementwise.c:33-36, 166-168);
-  * LayerNorm gw / gb over 65,536 rows: fp32 sums across rows (engine/src/ops/ops_nn.c:511-512).
+  * LayerNorm gw / gb over 65,536 rows: fp32 sums across rows (engine/src/ops/ops_nn.c:511-512);
+  * fp32 matmul with 4096 and 16384-term dot products: the reference sums KC = 256 register panels
+    into C (engine/src/kernels/x86/kernels_avx2.c:234-247), this build 32-k panels into running totals
+    on the matrix cores (a 4096 x 4096 output through the direct-to-LDS kernel, a 2048 x 2048 one
+    through the register-staged 128 x 128 tiles); error on 64 sampled rows against the GEMM bar
+    (scale = sum|a b| / sqrt(K)).
 The table is printed (pytest -s) and written to $NC_REFERR_OUT when that is set.
 """
 
@@ -129,3 +134,21 @@ def test_layer_norm_column_sums_65536_rows(engines):
     record("LayerNorm gw over 65536 rows", rows, gw, cw, terms.sum(0), np.abs(terms).sum(0) / np.sqrt(rows))
     record("LayerNorm gb over 65536 rows", rows, gbv, cbv, G.sum(0, dtype=np.float64),
            np.abs(G).sum(0, dtype=np.float64) / np.sqrt(rows))
+
+
+@pytest.mark.parametrize("M,N,K", [(4096, 4096, 4096), (2048, 2048, 16384)])
+def test_matmul_large_k(engines, M, N, K):
+    print(f"matmul [{M},{K}] x [{K},{N}] on both engines", flush=True)
+    rng = np.random.default_rng(M + K)
+    a = rng.standard_normal((M, K), dtype=np.float32)
+    b = rng.standard_normal((K, N), dtype=np.float32)
+
+    def fn(e):
+        return e.read(e.lib.nc_matmul(e.tensor(a), e.tensor(b)))
+
+    g, c = run_both(engines, fn)
+    rows = np.unique(np.linspace(0, M - 1, 64).astype(int))
+    A64, B64 = a[rows].astype(np.float64), b.astype(np.float64)
+    ref64 = A64 @ B64
+    scale = (np.abs(A64) @ np.abs(B64)) / np.sqrt(K)
+    record(f"matmul {M}x{N}, K = {K}", K, g[rows], c[rows], ref64, scale)
