@@ -413,9 +413,10 @@ __global__ __launch_bounds__(Cfg::NT, Cfg::MINB) void k_sgemm(SgArgs p) {
 }
 
 // ------------------------------------------------------------------------------------------------
-// Large FAST problems: the 256 x 256 tile, its operand panels loaded straight from global memory into
-// LDS (global_load_lds_dwordx4) a summation panel (two stages) ahead through four LDS stages, with no
-// staging registers and no LDS write instructions; one barrier per summation panel.  A stage of an R-row panel is R / 16 load
+// Large FAST problems with K a multiple of 32: the 256 x 256 tile, its operand panels loaded straight
+// from global memory into LDS (global_load_lds_dwordx4) a summation panel (two stages) ahead through
+// four LDS stages, with no staging registers and no LDS write instructions; one barrier per summation
+// panel.  A stage of an R-row panel is R / 16 load
 // instructions of 1 KiB each: 16 rows of a K-contiguous panel (lane l: row l / 4, the chunk that
 // belongs at position l % 4 under the row's permutation) or 256 / R k-rows of a M/N-contiguous one
 // (lane l: k-row l / (R / 4), position l % (R / 4), loading the rows the k-row's permutation puts
@@ -566,9 +567,9 @@ static int sg_layouts(SgArgs &p, int ta, int tb, bool vec, bool fast, int64_t co
 
 static int64_t tiles_of(int64_t M, int64_t N, int bm, int bn) { return ((M + bm - 1) / bm) * ((N + bn - 1) / bn); }
 
-// The 256 x 256 direct-to-LDS kernel for aligned problems (16-byte rows, K a multiple of 16) with at
-// least a tile per CU; otherwise the largest register-staged tile that still gives every CU a tile,
-// else the smallest.
+// The 256 x 256 direct-to-LDS kernel for aligned problems (16-byte rows, K a multiple of 32: whole
+// summation panels) with at least a tile per CU; otherwise the largest register-staged tile that still
+// gives every CU a tile, else the smallest.
 static int sg_run(SgArgs &p, int ta, int tb, int64_t count, hipStream_t st, const char *what) {
     // 16-byte loads need every matrix's rows 16-byte aligned: the matrices behind a pointer array may
     // start anywhere, so those take the scalar loads
