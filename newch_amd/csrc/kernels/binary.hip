@@ -1306,10 +1306,11 @@ extern "C" NC_HIP_API size_t nc_hip_binary_bwd_workspace(int nd, const int64_t *
     if (nd < 0 || nd > NC_HIP_MAX_DIMS || !shape || !sgx) return 0;
     for (int d = 0; d < nd; d++)
         if (shape[d] < 0) return 0;
-    if (numel_of(nd, shape) < (int64_t)UINT32_MAX) return bwd_workspace_run(nd, shape, sgx);
+    const RunSplit rsp = run_split();
+    if (numel_of(nd, shape) <= rsp.above) return bwd_workspace_run(nd, shape, sgx);
     size_t need = 0;
     const int64_t *st[1] = {sgx};
-    for_each_run(nd, shape, 1, st, kRunLimit, [&](const int64_t *rs, const int64_t *, const bool *) {
+    for_each_run(nd, shape, 1, st, rsp.limit, [&](const int64_t *rs, const int64_t *, const bool *) {
         need = std::max(need, bwd_workspace_run(nd, rs, sgx));
         return 0;
     });
@@ -1377,10 +1378,11 @@ extern "C" NC_HIP_API int nc_hip_binary_bwd(int op, int which, int nd, const int
         return set_error(NC_HIP_ERR_ARG, "nc_hip_binary_bwd: bad shape or strides");
     for (int d = 0; d < nd; d++)
         if (shape[d] < 0) return set_error(NC_HIP_ERR_ARG, "nc_hip_binary_bwd: negative dim");
-    if (numel_of(nd, shape) < (int64_t)UINT32_MAX)
+    const RunSplit rsp = run_split();
+    if (numel_of(nd, shape) <= rsp.above)
         return binary_bwd_run(op, which, nd, shape, g, sg, a, sa, b, sb, gx, sgx, accumulate, ws, ws_bytes, stream);
     const int64_t *st[4] = {sg, sa, sb, sgx};
-    return for_each_run(nd, shape, 4, st, kRunLimit, [&](const int64_t *rs, const int64_t *off, const bool *first) {
+    return for_each_run(nd, shape, 4, st, rsp.limit, [&](const int64_t *rs, const int64_t *off, const bool *first) {
         return binary_bwd_run(op, which, nd, rs, adv(g, off[0]), sg, adv(a, off[1]), sa, adv(b, off[2]), sb,
                               adv(gx, off[3]), sgx, first[3] ? accumulate : 1, ws, ws_bytes, stream);
     });
@@ -1423,11 +1425,12 @@ extern "C" NC_HIP_API size_t nc_hip_binary_bwd2_workspace(int nd, const int64_t 
     if (nd < 0 || nd > NC_HIP_MAX_DIMS || !shape) return 0;
     for (int d = 0; d < nd; d++)
         if (shape[d] < 0) return 0;
-    if (numel_of(nd, shape) < (int64_t)UINT32_MAX) return bwd2_workspace_run(nd, shape, sga, sgb);
+    const RunSplit rsp = run_split();
+    if (numel_of(nd, shape) <= rsp.above) return bwd2_workspace_run(nd, shape, sga, sgb);
     size_t need = 0;
     const int64_t zeros[NC_HIP_MAX_DIMS] = {0, 0, 0, 0, 0, 0};
     const int64_t *st[1] = {zeros};
-    for_each_run(nd, shape, 1, st, kRunLimit, [&](const int64_t *rs, const int64_t *, const bool *) {
+    for_each_run(nd, shape, 1, st, rsp.limit, [&](const int64_t *rs, const int64_t *, const bool *) {
         need = std::max(need, bwd2_workspace_run(nd, rs, sga, sgb));
         return 0;
     });
@@ -1474,12 +1477,13 @@ extern "C" NC_HIP_API int nc_hip_binary_bwd2(int op, int nd, const int64_t *shap
         return set_error(NC_HIP_ERR_ARG, "nc_hip_binary_bwd2: bad shape or strides");
     for (int d = 0; d < nd; d++)
         if (shape[d] < 0) return set_error(NC_HIP_ERR_ARG, "nc_hip_binary_bwd2: negative dim");
-    if (numel_of(nd, shape) < (int64_t)UINT32_MAX)
+    const RunSplit rsp = run_split();
+    if (numel_of(nd, shape) <= rsp.above)
         return binary_bwd2_run(op, nd, shape, g, sg, a, sa, b, sb, ga, sga, gb, sgb, accumulate, accumulate, ws,
                                ws_bytes, stream);
     const int64_t zeros[NC_HIP_MAX_DIMS] = {0, 0, 0, 0, 0, 0};
     const int64_t *st[5] = {sg, sa, sb, ga ? sga : zeros, gb ? sgb : zeros};
-    return for_each_run(nd, shape, 5, st, kRunLimit, [&](const int64_t *rs, const int64_t *off, const bool *first) {
+    return for_each_run(nd, shape, 5, st, rsp.limit, [&](const int64_t *rs, const int64_t *off, const bool *first) {
         return binary_bwd2_run(op, nd, rs, adv(g, off[0]), sg, adv(a, off[1]), sa, adv(b, off[2]), sb,
                                adv(ga, off[3]), sga, adv(gb, off[4]), sgb, first[3] ? accumulate : 1,
                                first[4] ? accumulate : 1, ws, ws_bytes, stream);
@@ -1604,11 +1608,12 @@ extern "C" NC_HIP_API int nc_hip_copy_strided(int elem_bytes, int nd, const int6
     }
     if (elem_bytes != 1 && elem_bytes != 2 && elem_bytes != 4 && elem_bytes != 8)
         return set_error(NC_HIP_ERR_ARG, "copy_strided: element size %d", elem_bytes);
-    if (p.numel >= (int64_t)UINT32_MAX) {
+    const RunSplit rsp = run_split();
+    if (p.numel > rsp.above) {
         int64_t cs[NC_HIP_MAX_DIMS];
         contiguous_strides(nd, shape, cs);
         const int64_t *st2[2] = {ss, cs};
-        return for_each_run(nd, shape, 2, st2, kRunLimit, [&](const int64_t *rs, const int64_t *off, const bool *) {
+        return for_each_run(nd, shape, 2, st2, rsp.limit, [&](const int64_t *rs, const int64_t *off, const bool *) {
             return nc_hip_copy_strided(elem_bytes, nd, rs, (const char *)src + off[0] * elem_bytes, ss,
                                        (char *)dst + off[1] * elem_bytes, stream);
         });
@@ -1634,11 +1639,12 @@ extern "C" NC_HIP_API int nc_hip_accumulate_strided(int nd, const int64_t *shape
     int rc = prepare(nd, shape, 1, strides, p, "nc_hip_accumulate_strided");
     if (rc) return rc;
     if (p.numel == 0) return NC_HIP_OK;
-    if (p.numel >= (int64_t)UINT32_MAX) {  // runs of at most 2^30 elements; src is contiguous over shape
+    const RunSplit rsp = run_split();
+    if (p.numel > rsp.above) {  // runs of at most 2^30 elements; src is contiguous over shape
         int64_t cs[NC_HIP_MAX_DIMS];
         contiguous_strides(nd, shape, cs);
         const int64_t *st2[2] = {cs, sd};
-        return for_each_run(nd, shape, 2, st2, kRunLimit, [&](const int64_t *rs, const int64_t *off, const bool *) {
+        return for_each_run(nd, shape, 2, st2, rsp.limit, [&](const int64_t *rs, const int64_t *off, const bool *) {
             return nc_hip_accumulate_strided(nd, rs, src + off[0], dst + off[1], sd, stream);
         });
     }

@@ -11,6 +11,7 @@
 #include <type_traits>
 #include <stdint.h>
 #include <stddef.h>
+#include <stdlib.h>
 
 #include "nc_hip.h"
 
@@ -291,6 +292,20 @@ inline bool aligned16(const void *p) { return ((uintptr_t)p & 15u) == 0; }
 // first nonzero return of fn.
 // ------------------------------------------------------------------------------------------------
 constexpr int64_t kRunLimit = int64_t(1) << 30;
+
+// When a problem runs as runs: above `above` elements, in runs of at most `limit`.  By default problems
+// of 2^32 elements or more (past the 32-bit index kernels) run as runs of at most 2^30.  The test hook
+// NC_HIP_RUN_LIMIT=n (0 < n < 2^30) lowers both to n, so that small problems take the split path.
+struct RunSplit {
+    int64_t above, limit;
+};
+inline RunSplit run_split() {
+    if (const char *e = getenv("NC_HIP_RUN_LIMIT")) {
+        const long long v = atoll(e);
+        if (v > 0 && v < kRunLimit) return {(int64_t)v, (int64_t)v};
+    }
+    return {(int64_t)UINT32_MAX - 1, kRunLimit};
+}
 
 template <class F>
 int for_each_run_from(int nd, const int64_t *shape, int nops, const int64_t *const *st, int64_t limit, int d,

@@ -554,13 +554,16 @@ extern "C" NC_HIP_API int nc_hip_reduce_fwd_noalloc(int kind, int64_t outer, int
     return nc_hip_reduce_fwd(kind, outer, R, inner, x, y, arg, ws, need, stream);
 }
 
+// inner1: the whole problem's inner extent is 1, where the reference adds scale * g (rounded) to gi
+// instead of its axpy's fused multiply-add.  A run cut from a longer inner dim keeps the fused form even
+// where it is one element wide.
 static int reduce_bwd_sum_run(int64_t outer, int64_t R, int64_t inner, const float *g, float *gi, float scale,
-                              int accumulate, hipStream_t st) {
+                              int accumulate, bool inner1, hipStream_t st) {
     const int64_t n = outer * R * inner;
     const uint32_t RI = (uint32_t)(R * inner);
     const IntDiv dRI(RI), dI((uint32_t)inner);
     const unsigned grid = stream_grid(n, kRB, 16);
-    if (inner == 1) {
+    if (inner1) {
         if (accumulate)
             hipLaunchKernelGGL((k_red_bwd<true, true>), grid, kRB, 0, st, g, gi, n, RI, dRI, (uint32_t)inner, dI, scale);
         else
@@ -590,11 +593,12 @@ extern "C" NC_HIP_API int nc_hip_reduce_bwd(int kind, int64_t outer, int64_t R, 
     if (kind != NC_HIP_RED_SUM && kind != NC_HIP_RED_MEAN)
         return set_error(NC_HIP_ERR_ARG, "nc_hip_reduce_bwd: kind %d has no gradient", kind);
     const float scale = kind == NC_HIP_RED_MEAN ? 1.0f / (float)(R ? R : 1) : 1.0f;
-    if (n < (int64_t)UINT32_MAX) return reduce_bwd_sum_run(outer, R, inner, g, gi, scale, accumulate, st);
+    const RunSplit rsp = run_split();
+    if (n <= rsp.above) return reduce_bwd_sum_run(outer, R, inner, g, gi, scale, accumulate, inner == 1, st);
     const int64_t shape[3] = {outer, R, inner}, sgi[3] = {R * inner, inner, 1}, sg[3] = {inner, 0, 1};
     const int64_t *strides[2] = {sg, sgi};
-    return for_each_run(3, shape, 2, strides, kRunLimit, [&](const int64_t *rs, const int64_t *off, const bool *) {
-        return reduce_bwd_sum_run(rs[0], rs[1], rs[2], g + off[0], gi + off[1], scale, accumulate, st);
+    return for_each_run(3, shape, 2, strides, rsp.limit, [&](const int64_t *rs, const int64_t *off, const bool *) {
+        return reduce_bwd_sum_run(rs[0], rs[1], rs[2], g + off[0], gi + off[1], scale, accumulate, inner == 1, st);
     });
 }
 
