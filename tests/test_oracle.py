@@ -435,6 +435,34 @@ def test_loss_vs_live_reference(N, C):
             ref.step_end()
 
 
+@ref_only
+@pytest.mark.parametrize("shape,axis", [((5, 13, 9), 1), ((7, 300), 1), ((300, 7), 0), ((4, 6, 11), 2),
+                                        ((3, 1000), -128)])
+def test_reduce_bwd_accumulates_vs_live_reference(shape, axis):
+    """sum / mean gradients added into a gradient that already holds values (a second backward): the
+    reference adds scale * g, rounded, where the reduced extent is innermost (inner == 1,
+    ops_reduce.c:133-135) and otherwise calls its axpy, fused multiply-adds to the end of each row
+    (kernels_avx2.c:39-45).  Golden vectors start from a zero gradient, where both forms agree; this
+    pins the accumulating forms, with inner rows of 9, 7 and 11 floats so the axpy's 8-wide loop has a
+    tail."""
+    from tests.ncdrive import Engine
+    rng = np.random.default_rng(sum(shape) + axis)
+    x = rng.standard_normal(shape).astype(np.float32)
+    for kind in ("sum", "mean"):
+        with Engine(O.REF_LIB) as ref:
+            fn = ref.lib.nc_sum if kind == "sum" else ref.lib.nc_mean
+            p = ref.param(x)
+            Gs = []
+            for _ in range(2):
+                out = fn(p, axis, 0)
+                G = rng.standard_normal(ref.read(out).shape).astype(np.float32)
+                ref.backward_with(out, G)
+                Gs.append(G)
+            got = ref.grad(p).reshape(shape)
+        want = O.reduce_bwd(kind, shape, axis, Gs[1], None, O.reduce_bwd(kind, shape, axis, Gs[0]))
+        assert_bits(want, got, f"{kind} {shape} axis {axis}")
+
+
 # ------------------------------------------------------------------------------------------------
 # closed forms, invariants and the reference's own known answers
 # ------------------------------------------------------------------------------------------------
