@@ -463,6 +463,71 @@ def test_reduce_bwd_accumulates_vs_live_reference(shape, axis):
         assert_bits(want, got, f"{kind} {shape} axis {axis}")
 
 
+def _twice(ref, params, make, rng):
+    """Two forward + backward passes of make(params) on the reference engine, each with its own
+    upstream gradient, the second adding into the gradients the first left: (grads, [G1, G2])."""
+    Gs = []
+    for _ in range(2):
+        out = make(*params)
+        G = rng.standard_normal(ref.read(out).shape).astype(np.float32)
+        ref.backward_with(out, G)
+        Gs.append(G)
+    return [ref.grad(p) for p in params], Gs
+
+
+@ref_only
+def test_bit_exact_backwards_accumulate_vs_live_reference():
+    """Every bit-exact backward, run twice on the reference so that the second adds into gradients
+    that already hold values: unary activations, the four broadcast binary ops (one operand reduced),
+    softmax / log_softmax, max, cross entropy and nll.  The oracle's accumulating forms (gi + term,
+    in the reference's association) must give the same bits; golden vectors, which start from zero
+    gradients, cannot tell those forms from a fused or reassociated one."""
+    from tests.ncdrive import Engine
+    rng = np.random.default_rng(20261202)
+    x = (rng.standard_normal((37, 29)) * 3).astype(np.float32)
+    with Engine(O.REF_LIB) as ref:
+        L = ref.lib
+        for name, kind, s in UNARY:
+            (gx,), (G1, G2) = _twice(ref, [ref.param(x)], lambda p: Engine.UNARY_CALLS[name](L, p, s), rng)
+            y = O.unary_fwd(kind, x, s)
+            want = O.unary_bwd(kind, x, y, G2, O.unary_bwd(kind, x, y, G1, s=s), s)
+            assert_bits(want, gx.reshape(x.shape), f"{name} accumulated")
+            ref.step_end()
+        for bshape in ((1, 29), (37, 29)):  # b broadcast over rows (grad b reduced), and the same shape
+            b = (0.5 + rng.random(bshape)).astype(np.float32)
+            for op, fn in (("add", L.nc_add), ("sub", L.nc_sub), ("mul", L.nc_mul), ("div", L.nc_div)):
+                (ga, gb), (G1, G2) = _twice(ref, [ref.param(x), ref.param(b)], fn, rng)
+                a1, b1 = O.binary_bwd(op, x, b, G1)
+                a2, b2 = O.binary_bwd(op, x, b, G2, ga0=a1, gb0=b1)
+                assert_bits(a2, ga.reshape(x.shape), f"{op} b{bshape} grad a accumulated")
+                # a reduced grad b sums 37 rows in the reference's row_acc order, restated by the oracle
+                assert_bits(b2, gb.reshape(b.shape), f"{op} b{bshape} grad b accumulated")
+                ref.step_end()
+        for log_form, fn in ((False, L.nc_softmax), (True, L.nc_log_softmax)):
+            (gx,), (G1, G2) = _twice(ref, [ref.param(x)], fn, rng)
+            y = O.softmax_fwd(x, log_form)
+            want = O.softmax_bwd(y, G2, log_form, O.softmax_bwd(y, G1, log_form))
+            assert_bits(want, gx.reshape(x.shape), f"softmax log={log_form} accumulated")
+            ref.step_end()
+        for axis in (0, 1):
+            (gx,), (G1, G2) = _twice(ref, [ref.param(x)], lambda p: L.nc_max(p, axis, 0), rng)
+            _, arg = O.reduce_fwd("max", x, axis)
+            want = O.reduce_bwd("max", x.shape, axis, G2, arg, O.reduce_bwd("max", x.shape, axis, G1, arg))
+            assert_bits(want, gx.reshape(x.shape), f"max axis {axis} accumulated")
+            ref.step_end()
+        lab = rng.integers(0, x.shape[1], x.shape[0]).astype(np.int32)
+        _, prob = O.cross_entropy_fwd(x, lab)
+        (gx,), (G1, G2) = _twice(ref, [ref.param(x)], lambda p: L.nc_cross_entropy(p, ref.tensor(lab)), rng)
+        want = O.cross_entropy_bwd(prob, lab, float(G2), O.cross_entropy_bwd(prob, lab, float(G1)))
+        assert_bits(want, gx.reshape(x.shape), "cross_entropy accumulated")
+        ref.step_end()
+        for sm in (0, 1):
+            (gx,), (G1, G2) = _twice(ref, [ref.param(x)], lambda p: L.nc_nll_loss(p, ref.tensor(lab), sm), rng)
+            want = O.nll_loss_bwd(x.shape, lab, float(G2), bool(sm), O.nll_loss_bwd(x.shape, lab, float(G1), bool(sm)))
+            assert_bits(want, gx.reshape(x.shape), f"nll sum={sm} accumulated")
+            ref.step_end()
+
+
 # ------------------------------------------------------------------------------------------------
 # closed forms, invariants and the reference's own known answers
 # ------------------------------------------------------------------------------------------------
