@@ -1,0 +1,172 @@
+"""Random chains of hot-path ops through both engines' nc.h API, compared with each other.
+
+A seeded plan of 3-7 ops (activations, broadcast binary ops against parameters, sum / mean / max over
+an axis with or without keepdim, softmax / log_softmax, LayerNorm with weight and bias, transposed and
+reshaped views, matmul with a parameter) is built from a parameter x, the same plan runs in this
+engine (tests/ncdrive.Engine over newch_amd/libnc.so, on the GPU) and in the reference engine compiled
+from its sources (oracle/_ref/libnc_ref.so, on the CPU), then loss = sum(out * G) goes backward in
+both.  The output and every parameter's gradient are compared: bit for bit when every op of the chain
+is one whose result does not depend on a summation order (activations, same-shape binary ops and
+their gradients, views, max), otherwise within 2e-4 of the tensor's largest magnitude or 2e-5 of the
+chain's largest result, whichever is larger (these chains contain fp64-vs-fp32 reductions and fp32
+GEMMs whose orders differ by design; the bar catches a wrong index, operand, axis or gradient path,
+not last-bit differences, which the per-op parity tests pin).
+This is the reference's Python-layer usage (newch/tensor.py over newch/_lib.py) replayed on both.
+"""
+
+from ctypes import c_float
+
+import numpy as np
+import pytest
+
+from newch_amd import abi
+from oracle import pyoracle as O
+from tests.ncdrive import Engine
+
+pytestmark = pytest.mark.gpu
+
+UNARY = ["relu", "relu6", "leaky_relu", "hardsigmoid", "hardswish", "silu", "gelu", "gelu_tanh", "sigmoid", "tanh"]
+BINARY = ["add", "sub", "mul", "div"]
+
+
+@pytest.fixture(scope="module")
+def engines():
+    if not O.REF_LIB.exists():
+        pytest.skip("oracle/_ref/libnc_ref.so is not built (make -C oracle ref)")
+    gpu, cpu = Engine(), Engine(O.REF_LIB)
+    yield gpu, cpu
+    gpu.close()
+    cpu.close()
+
+
+def make_plan(seed, exact_only=False):
+    """(x shape, [ops], exact, output shape): each op a tuple whose first element names it; shapes
+    tracked here.  exact_only: only ops whose results do not depend on a summation order (binary ops
+    against a parameter of the full shape, max as the only reduction)."""
+    rng = np.random.default_rng(seed + (50_000 if exact_only else 0))
+    while True:
+        shape = [int(rng.choice([2, 3, 5, 8, 13, 32])) for _ in range(int(rng.integers(2, 5)))]
+        if np.prod(shape) <= 6000:
+            break
+    x_shape = tuple(shape)
+    ops, exact = [], True
+    for _ in range(int(rng.integers(3, 8))):
+        nd = len(shape)
+        kinds = ["unary", "binary", "binary", "transpose"]
+        if nd >= 2:
+            kinds += ["reduce", "reshape"]
+        if shape[-1] >= 8 and not exact_only:
+            kinds += ["softmax", "layer_norm"]
+        if nd >= 2 and np.prod(shape) <= 4096 and not exact_only:
+            kinds += ["matmul"]
+        k = str(rng.choice(kinds))
+        if k == "unary":
+            ops.append(("unary", str(rng.choice(UNARY)), float(rng.choice([0.01, 0.2]))))
+        elif k == "binary":
+            lead = 0 if exact_only else int(rng.integers(0, nd))
+            bshape = tuple(d if exact_only or rng.random() >= 0.4 else 1 for d in shape[lead:])
+            ops.append(("binary", str(rng.choice(BINARY)), bshape))
+            if tuple(bshape) != tuple(shape):
+                exact = False  # the broadcast operand's gradient is a reduction
+        elif k == "transpose":
+            if nd < 2:
+                continue
+            a0, a1 = (int(v) for v in rng.choice(nd, 2, replace=False))
+            ops.append(("transpose", a0, a1))
+            shape[a0], shape[a1] = shape[a1], shape[a0]
+        elif k == "reshape":
+            ops.append(("reshape", tuple(shape[:-2]) + (shape[-2] * shape[-1],)))
+            shape = shape[:-2] + [shape[-2] * shape[-1]]
+        elif k == "reduce":
+            kind = "max" if exact_only else str(rng.choice(["sum", "mean", "max"]))
+            axis, keep = int(rng.integers(0, nd)), int(rng.integers(0, 2))
+            ops.append(("reduce", kind, axis, keep))
+            shape = shape[:axis] + ([1] if keep else []) + shape[axis + 1:]
+            if kind != "max":
+                exact = False
+        elif k == "softmax":
+            ops.append(("softmax", bool(rng.integers(0, 2))))
+            exact = False
+        elif k == "layer_norm":
+            ops.append(("layer_norm", shape[-1]))
+            exact = False
+        elif k == "matmul":
+            n_out = int(rng.choice([3, 8, 17]))
+            ops.append(("matmul", shape[-1], n_out))
+            shape = shape[:-1] + [n_out]
+            exact = False
+    return x_shape, ops, exact, tuple(shape)
+
+
+def run_plan(e, seed, x_shape, ops):
+    """Builds the plan's parameters from the seed, runs it forward and backward in engine e:
+    (output, [parameter gradients])."""
+    L = e.lib
+    rng = np.random.default_rng(10_000 + seed)
+    params = [e.param(rng.standard_normal(x_shape).astype(np.float32))]
+    t = params[0]
+    for op in ops:
+        if op[0] == "unary":
+            t = Engine.UNARY_CALLS[op[1]](L, t, op[2])
+        elif op[0] == "binary":
+            vals = rng.standard_normal(op[2]).astype(np.float32)
+            if op[1] == "div":
+                vals = (0.5 + 1.5 * rng.random(op[2])).astype(np.float32)
+            p = e.param(vals)
+            params.append(p)
+            t = {"add": L.nc_add, "sub": L.nc_sub, "mul": L.nc_mul, "div": L.nc_div}[op[1]](t, p)
+        elif op[0] == "transpose":
+            t = L.nc_transpose(t, op[1], op[2])
+        elif op[0] == "reshape":
+            nd, shp = abi.shape_arg(op[1])
+            t = L.nc_reshape(t, nd, shp)
+        elif op[0] == "reduce":
+            t = {"sum": L.nc_sum, "mean": L.nc_mean, "max": L.nc_max}[op[1]](t, op[2], op[3])
+        elif op[0] == "softmax":
+            t = L.nc_log_softmax(t) if op[1] else L.nc_softmax(t)
+        elif op[0] == "layer_norm":
+            w = e.param((1 + 0.1 * rng.standard_normal(op[1])).astype(np.float32))
+            b = e.param((0.1 * rng.standard_normal(op[1])).astype(np.float32))
+            params += [w, b]
+            t = L.nc_layer_norm(t, 1, w, b, c_float(1e-5))
+        elif op[0] == "matmul":
+            W = e.param((rng.standard_normal((op[1], op[2])) / np.sqrt(op[1])).astype(np.float32))
+            params.append(W)
+            t = L.nc_matmul(t, W)
+        e.check()
+    out = e.read(t)
+    G = rng.standard_normal(out.shape).astype(np.float32)
+    e.backward_with(t, G)
+    grads = [e.grad(p) for p in params]
+    e.step_end()
+    return out, grads
+
+
+def _same(got, want, exact, what, chain_scale):
+    got, want = np.asarray(got, np.float32), np.asarray(want, np.float32)
+    assert got.shape == want.shape, f"{what}: shape {got.shape} vs {want.shape}"
+    if exact:
+        ok = (got.view(np.uint32) == want.view(np.uint32)) | (np.isnan(got) & np.isnan(want))
+        assert ok.all(), f"{what}: {int((~ok).sum())} of {ok.size} differ (exact chain)"
+        return
+    # 2e-4 of the tensor's own largest magnitude, and never less than 2e-5 of the chain's largest
+    # result: a parameter the chain is invariant to (a shift or scale ahead of a normalisation over
+    # the dims it is constant along) has a true gradient of ~0, and both engines return rounding
+    # noise of the size of the terms that cancel
+    tol = max(2e-4 * float(np.abs(want).max(initial=0.0)), 2e-5 * chain_scale, 1e-30)
+    err = np.abs(got.astype(np.float64) - want.astype(np.float64))
+    assert np.isfinite(got).all() == np.isfinite(want).all() and (err <= tol).all(), \
+        f"{what}: max error {float(err.max(initial=0.0)):.3g} over the bar {tol:.3g}"
+
+
+@pytest.mark.parametrize("exact_only,seed", [(False, s) for s in range(80)] + [(True, s) for s in range(40)])
+def test_random_chain_matches_reference_engine(engines, exact_only, seed):
+    x_shape, ops, exact, out_shape = make_plan(seed, exact_only)
+    assert exact or not exact_only
+    what = f"seed {seed} x {x_shape} ops {ops}"
+    (gout, ggrads), (rout, rgrads) = (run_plan(e, seed, x_shape, ops) for e in engines)
+    assert len(ggrads) == len(rgrads)
+    scale = max(float(np.abs(r).max(initial=0.0)) for r in [rout] + rgrads)
+    _same(gout, rout, exact, what + " output", scale)
+    for i, (g, r) in enumerate(zip(ggrads, rgrads)):
+        _same(g, r, exact, f"{what} grad of parameter {i}", scale)
