@@ -96,17 +96,15 @@ __device__ __forceinline__ void ce_fwd_rows(const float *__restrict__ x, const i
         }
         m = wave_max_nan_skip(m);
         m = row_max_finish(m, lane0_f32(v[0].x));  // lane 0 holds the row's first element
-        // exp(x - m) as exp2(x log2e - m log2e), one fused multiply-add per element; each lane's terms
-        // (at most 64, each in (0, 1]) in fp32, the 64 lane sums in fp64
-        const float ml = m * NC_K_LOG2E;
+        // exp(x - m) as exp2((x - m) log2e): the difference first, so the exponent's error is relative
+        // to x - m, not to m (x log2e - m log2e would carry m log2e's rounding, 1e-4 at |m| = 1e3); each
+        // lane's terms (at most 64, each in (0, 1]) in fp32, the 64 lane sums in fp64
         float s = 0.0f;
 #pragma unroll
         for (int k = 0; k < VPL; k++) {
             if (lane + k * kWave < nv)
-                s += (__builtin_amdgcn_exp2f(fma_(v[k].x, NC_K_LOG2E, -ml)) +
-                      __builtin_amdgcn_exp2f(fma_(v[k].y, NC_K_LOG2E, -ml))) +
-                     (__builtin_amdgcn_exp2f(fma_(v[k].z, NC_K_LOG2E, -ml)) +
-                      __builtin_amdgcn_exp2f(fma_(v[k].w, NC_K_LOG2E, -ml)));
+                s += (exp_sum_term(v[k].x - m) + exp_sum_term(v[k].y - m)) +
+                     (exp_sum_term(v[k].z - m) + exp_sum_term(v[k].w - m));
         }
         const float ls = logf((float)wave_sum((double)s));
         if (lane == 0) {

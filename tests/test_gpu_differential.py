@@ -1,8 +1,10 @@
 """Random chains of hot-path ops through both engines' nc.h API, compared with each other.
 
-A seeded plan of 3-7 ops (activations, broadcast binary ops against parameters, sum / mean / max over
-an axis with or without keepdim, softmax / log_softmax, LayerNorm with weight and bias, transposed and
-reshaped views, matmul with a parameter) is built from a parameter x, the same plan runs in this
+A seeded plan of 3-7 ops (activations, broadcast binary ops against parameters, a tensor combined with
+itself (t op t) or with an activation of itself (t + f(t)), so that its gradient receives two terms,
+sum / mean / max over an axis with or without keepdim, softmax / log_softmax, LayerNorm with weight and
+bias, transposed and reshaped views, matmul and linear with parameters, and sometimes a cross-entropy or
+nll loss head) is built from a parameter x, the same plan runs in this
 engine (tests/ncdrive.Engine over newch_amd/libnc.so, on the GPU) and in the reference engine compiled
 from its sources (oracle/_ref/libnc_ref.so, on the CPU), then loss = sum(out * G) goes backward in
 both.  The output and every parameter's gradient are compared: bit for bit when every op of the chain
@@ -22,6 +24,7 @@ import pytest
 from newch_amd import abi
 from oracle import pyoracle as O
 from tests.ncdrive import Engine
+from tests.test_gpu_parity import SWEEP
 
 pytestmark = pytest.mark.gpu
 
@@ -52,13 +55,13 @@ def make_plan(seed, exact_only=False):
     ops, exact = [], True
     for _ in range(int(rng.integers(3, 8))):
         nd = len(shape)
-        kinds = ["unary", "binary", "binary", "transpose"]
+        kinds = ["unary", "binary", "binary", "transpose", "self", "residual"]
         if nd >= 2:
             kinds += ["reduce", "reshape"]
         if shape[-1] >= 8 and not exact_only:
             kinds += ["softmax", "layer_norm"]
         if nd >= 2 and np.prod(shape) <= 4096 and not exact_only:
-            kinds += ["matmul"]
+            kinds += ["matmul", "linear"]
         k = str(rng.choice(kinds))
         if k == "unary":
             ops.append(("unary", str(rng.choice(UNARY)), float(rng.choice([0.01, 0.2]))))
@@ -68,6 +71,10 @@ def make_plan(seed, exact_only=False):
             ops.append(("binary", str(rng.choice(BINARY)), bshape))
             if tuple(bshape) != tuple(shape):
                 exact = False  # the broadcast operand's gradient is a reduction
+        elif k == "self":  # both operands the same tensor: its gradient receives both terms
+            ops.append(("self", str(rng.choice(["add", "sub", "mul"]))))
+        elif k == "residual":  # t + f(t): the gradient reaches t along two paths
+            ops.append(("residual", str(rng.choice(UNARY)), float(rng.choice([0.01, 0.2]))))
         elif k == "transpose":
             if nd < 2:
                 continue
@@ -90,10 +97,17 @@ def make_plan(seed, exact_only=False):
         elif k == "layer_norm":
             ops.append(("layer_norm", shape[-1]))
             exact = False
-        elif k == "matmul":
+        elif k in ("matmul", "linear"):
             n_out = int(rng.choice([3, 8, 17]))
-            ops.append(("matmul", shape[-1], n_out))
+            ops.append((k, shape[-1], n_out))
             shape = shape[:-1] + [n_out]
+            exact = False
+    if not exact_only and rng.random() < 0.3:
+        # a loss head over rows of the last dim: cross entropy, or nll over log_softmax
+        C = shape[-1]
+        if C >= 2:
+            ops.append(("loss", bool(rng.integers(0, 2)), int(np.prod(shape[:-1])), C))
+            shape = []
             exact = False
     return x_shape, ops, exact, tuple(shape)
 
@@ -103,6 +117,7 @@ def run_plan(e, seed, x_shape, ops):
     (output, [parameter gradients])."""
     L = e.lib
     rng = np.random.default_rng(10_000 + seed)
+    logits_max = 0.0
     params = [e.param(rng.standard_normal(x_shape).astype(np.float32))]
     t = params[0]
     for op in ops:
@@ -115,6 +130,10 @@ def run_plan(e, seed, x_shape, ops):
             p = e.param(vals)
             params.append(p)
             t = {"add": L.nc_add, "sub": L.nc_sub, "mul": L.nc_mul, "div": L.nc_div}[op[1]](t, p)
+        elif op[0] == "self":
+            t = {"add": L.nc_add, "sub": L.nc_sub, "mul": L.nc_mul}[op[1]](t, t)
+        elif op[0] == "residual":
+            t = L.nc_add(t, Engine.UNARY_CALLS[op[1]](L, t, op[2]))
         elif op[0] == "transpose":
             t = L.nc_transpose(t, op[1], op[2])
         elif op[0] == "reshape":
@@ -133,16 +152,28 @@ def run_plan(e, seed, x_shape, ops):
             W = e.param((rng.standard_normal((op[1], op[2])) / np.sqrt(op[1])).astype(np.float32))
             params.append(W)
             t = L.nc_matmul(t, W)
+        elif op[0] == "linear":
+            W = e.param((rng.standard_normal((op[2], op[1])) / np.sqrt(op[1])).astype(np.float32))
+            bias = e.param((0.1 * rng.standard_normal(op[2])).astype(np.float32))
+            params += [W, bias]
+            t = L.nc_linear_fn(t, W, bias)
+        elif op[0] == "loss":
+            rows, C = op[2], op[3]
+            nd, shp = abi.shape_arg((rows, C))
+            t2 = L.nc_reshape(t, nd, shp)
+            logits_max = float(np.abs(e.read(t2)).max(initial=0.0))
+            lab = e.tensor(rng.integers(0, C, rows).astype(np.int32))
+            t = L.nc_cross_entropy(t2, lab) if op[1] else L.nc_nll_loss(L.nc_log_softmax(t2), lab, 0)
         e.check()
     out = e.read(t)
     G = rng.standard_normal(out.shape).astype(np.float32)
     e.backward_with(t, G)
     grads = [e.grad(p) for p in params]
     e.step_end()
-    return out, grads
+    return out, grads, logits_max
 
 
-def _same(got, want, exact, what, chain_scale):
+def _same(got, want, exact, what, chain_scale, loss_floor=0.0):
     got, want = np.asarray(got, np.float32), np.asarray(want, np.float32)
     assert got.shape == want.shape, f"{what}: shape {got.shape} vs {want.shape}"
     if exact:
@@ -153,20 +184,23 @@ def _same(got, want, exact, what, chain_scale):
     # result: a parameter the chain is invariant to (a shift or scale ahead of a normalisation over
     # the dims it is constant along) has a true gradient of ~0, and both engines return rounding
     # noise of the size of the terms that cancel
-    tol = max(2e-4 * float(np.abs(want).max(initial=0.0)), 2e-5 * chain_scale, 1e-30)
+    tol = max(2e-4 * float(np.abs(want).max(initial=0.0)), 2e-5 * chain_scale, loss_floor, 1e-30)
     err = np.abs(got.astype(np.float64) - want.astype(np.float64))
     assert np.isfinite(got).all() == np.isfinite(want).all() and (err <= tol).all(), \
         f"{what}: max error {float(err.max(initial=0.0)):.3g} over the bar {tol:.3g}"
 
 
-@pytest.mark.parametrize("exact_only,seed", [(False, s) for s in range(80)] + [(True, s) for s in range(40)])
+@pytest.mark.parametrize("exact_only,seed",
+                         [(False, s) for s in range(160 * SWEEP)] + [(True, s) for s in range(80 * SWEEP)])
 def test_random_chain_matches_reference_engine(engines, exact_only, seed):
     x_shape, ops, exact, out_shape = make_plan(seed, exact_only)
     assert exact or not exact_only
     what = f"seed {seed} x {x_shape} ops {ops}"
-    (gout, ggrads), (rout, rgrads) = (run_plan(e, seed, x_shape, ops) for e in engines)
+    (gout, ggrads, _), (rout, rgrads, logits_max) = (run_plan(e, seed, x_shape, ops) for e in engines)
     assert len(ggrads) == len(rgrads)
     scale = max(float(np.abs(r).max(initial=0.0)) for r in [rout] + rgrads)
-    _same(gout, rout, exact, what + " output", scale)
+    # a loss head's value carries the fp32 rounding of log-probabilities of logits this large (the
+    # reference sums its exponentials in fp32, this engine in fp64)
+    _same(gout, rout, exact, what + " output", scale, 1e-6 * logits_max)
     for i, (g, r) in enumerate(zip(ggrads, rgrads)):
         _same(g, r, exact, f"{what} grad of parameter {i}", scale)

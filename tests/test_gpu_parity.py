@@ -1284,6 +1284,22 @@ def test_kernel_cross_entropy(K, N, C):
     if C >= 8:
         x[1, 5] = -np.inf  # a zero probability
     lab = rng.integers(0, C, N).astype(np.int32)
+    _ce_case(K, x, lab, rng)
+
+
+@pytest.mark.parametrize("N,C", [(64, 1024), (33, 7), (5, 4096)])
+@pytest.mark.parametrize("scale,offset", [(1.0, 3000.0), (400.0, 0.0), (1.0, -5000.0)])
+def test_kernel_cross_entropy_large_logits(K, N, C, scale, offset):
+    """Logits of magnitude 10^3: the row sum's exponentials must keep their accuracy relative to
+    x - max, not to max (an exponent formed as x log2e - max log2e loses 1e-4 there)."""
+    rng = np.random.default_rng(N + C + int(scale) + abs(int(offset)))
+    x = (rng.standard_normal((N, C)) * 3 * scale + offset).astype(np.float32)
+    lab = rng.integers(0, C, N).astype(np.int32)
+    _ce_case(K, x, lab, rng)
+
+
+def _ce_case(K, x, lab, rng):
+    N, C = x.shape
     Xd, Ld = dev(x), dev(lab)
     S, LS, BAD = empty(8 * N), empty(4), empty(8)
     wsb = K.loss_workspace(N, C)
