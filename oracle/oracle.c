@@ -162,6 +162,10 @@ void or_unary_fwd(int kind, float s, const float *x, float *y, int64_t n) {
         case OR_UN_NEG: r = -1.0f * v; break; /* scale_f32(-1) */
         case OR_UN_SCALE: r = s * v; break;
         case OR_UN_ADD_SCALAR: r = v + s; break;
+        /* the reference's scalar libm calls (ops_elementwise.c:233-234, 240) */
+        case OR_UN_LOG: r = logf(v); break;
+        case OR_UN_SQRT: r = sqrtf(v); break;
+        case OR_UN_POW: r = powf(v, s); break;
         default: r = NAN; break;
         }
         y[i] = r;
@@ -207,6 +211,10 @@ void or_unary_bwd(int kind, float s, const float *x, const float *y, const float
         case OR_UN_NEG: gi[i] = fmaf(-1.0f, gg, gi[i]); break;      /* axpy_f32(-1) */
         case OR_UN_SCALE: gi[i] = fmaf(s, gg, gi[i]); break;        /* axpy_f32(s) */
         case OR_UN_ADD_SCALAR: gi[i] = fmaf(1.0f, gg, gi[i]); break; /* axpy_f32(1) */
+        /* ops_elementwise.c:305-306, 312: g / x, g * 0.5 / y, g * s * powf(x, s - 1), left to right */
+        case OR_UN_LOG: t = gg / v; gi[i] = gi[i] + t; break;
+        case OR_UN_SQRT: t = (gg * 0.5f) / y[i]; gi[i] = gi[i] + t; break;
+        case OR_UN_POW: t = (gg * s) * powf(v, s - 1.0f); gi[i] = gi[i] + t; break;
         default: gi[i] = NAN; break;
         }
     }

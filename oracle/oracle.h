@@ -27,7 +27,7 @@ extern "C" {
 enum {
     OR_UN_RELU = 0, OR_UN_LEAKY_RELU, OR_UN_RELU6, OR_UN_HARDSIGMOID, OR_UN_HARDSWISH,
     OR_UN_SILU, OR_UN_GELU, OR_UN_GELU_TANH, OR_UN_SIGMOID, OR_UN_TANH, OR_UN_EXP,
-    OR_UN_NEG, OR_UN_SCALE, OR_UN_ADD_SCALAR, OR_UN_COUNT
+    OR_UN_NEG, OR_UN_SCALE, OR_UN_ADD_SCALAR, OR_UN_LOG, OR_UN_SQRT, OR_UN_POW, OR_UN_COUNT
 };
 enum { OR_BIN_ADD = 0, OR_BIN_SUB, OR_BIN_MUL, OR_BIN_DIV };
 enum { OR_RED_SUM = 0, OR_RED_MEAN, OR_RED_MAX, OR_RED_ARGMAX };

@@ -18,7 +18,8 @@ LIB = HERE / "_build" / "liboracle.so"
 REF_LIB = HERE / "_ref" / "libnc_ref.so"
 
 UN = {"relu": 0, "leaky_relu": 1, "relu6": 2, "hardsigmoid": 3, "hardswish": 4, "silu": 5, "gelu": 6,
-      "gelu_tanh": 7, "sigmoid": 8, "tanh": 9, "exp": 10, "neg": 11, "scale": 12, "add_scalar": 13}
+      "gelu_tanh": 7, "sigmoid": 8, "tanh": 9, "exp": 10, "neg": 11, "scale": 12, "add_scalar": 13, "log": 14,
+      "sqrt": 15, "pow": 16}
 BIN = {"add": 0, "sub": 1, "mul": 2, "div": 3}
 RED = {"sum": 0, "mean": 1, "max": 2, "argmax": 3}
 

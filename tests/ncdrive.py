@@ -123,6 +123,12 @@ class Engine:
         "sigmoid": lambda L, t, s: L.nc_sigmoid(t),
         "tanh": lambda L, t, s: L.nc_tanh(t),
         "exp": lambda L, t, s: L.nc_exp(t),
+        "neg": lambda L, t, s: L.nc_neg(t),
+        "scale": lambda L, t, s: L.nc_scale(t, c_float(s)),
+        "add_scalar": lambda L, t, s: L.nc_add_scalar(t, c_float(s)),
+        "log": lambda L, t, s: L.nc_log(t),
+        "sqrt": lambda L, t, s: L.nc_sqrt(t),
+        "pow": lambda L, t, s: L.nc_pow_scalar(t, c_float(s)),
     }
 
     def unary(self, name, x, g, s=0.0):

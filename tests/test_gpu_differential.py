@@ -2,6 +2,7 @@
 
 A seeded plan of 3-7 ops (activations, broadcast binary ops against parameters, a tensor combined with
 itself (t op t) or with an activation of itself (t + f(t)), so that its gradient receives two terms,
+sqrt / log / pow of t * t + 0.5,
 sum / mean / max over an axis with or without keepdim, softmax / log_softmax, LayerNorm with weight and
 bias, transposed and reshaped views, matmul and linear with parameters, and sometimes a cross-entropy or
 nll loss head) is built from a parameter x, the same plan runs in this
@@ -28,7 +29,8 @@ from tests.test_gpu_parity import SWEEP
 
 pytestmark = pytest.mark.gpu
 
-UNARY = ["relu", "relu6", "leaky_relu", "hardsigmoid", "hardswish", "silu", "gelu", "gelu_tanh", "sigmoid", "tanh"]
+UNARY = ["relu", "relu6", "leaky_relu", "hardsigmoid", "hardswish", "silu", "gelu", "gelu_tanh", "sigmoid", "tanh",
+         "neg", "scale", "add_scalar"]
 BINARY = ["add", "sub", "mul", "div"]
 
 
@@ -55,7 +57,7 @@ def make_plan(seed, exact_only=False):
     ops, exact = [], True
     for _ in range(int(rng.integers(3, 8))):
         nd = len(shape)
-        kinds = ["unary", "binary", "binary", "transpose", "self", "residual"]
+        kinds = ["unary", "binary", "binary", "transpose", "self", "residual", "positive"]
         if nd >= 2:
             kinds += ["reduce", "reshape"]
         if shape[-1] >= 8 and not exact_only:
@@ -71,8 +73,15 @@ def make_plan(seed, exact_only=False):
             ops.append(("binary", str(rng.choice(BINARY)), bshape))
             if tuple(bshape) != tuple(shape):
                 exact = False  # the broadcast operand's gradient is a reduction
-        elif k == "self":  # both operands the same tensor: its gradient receives both terms
-            ops.append(("self", str(rng.choice(["add", "sub", "mul"]))))
+        elif k == "self":  # both operands the same tensor: its gradient receives both terms (not t - t,
+            # whose exact zeros make a later LayerNorm's rows constant: rstd = eps^-1/2 then magnifies
+            # the rounding noise of gradients the chain is invariant to past any fixed bar)
+            ops.append(("self", str(rng.choice(["add", "mul"]))))
+        elif k == "positive":  # f(t * t + 0.5) for the functions that need a positive argument
+            f = str(rng.choice(["sqrt"] if exact_only else ["sqrt", "log", "pow"]))
+            ops.append(("positive", f, 1.5))
+            if f != "sqrt":
+                exact = False  # log and pow: the host libm is off by an ulp on ~0.05% of inputs
         elif k == "residual":  # t + f(t): the gradient reaches t along two paths
             ops.append(("residual", str(rng.choice(UNARY)), float(rng.choice([0.01, 0.2]))))
         elif k == "transpose":
@@ -132,6 +141,8 @@ def run_plan(e, seed, x_shape, ops):
             t = {"add": L.nc_add, "sub": L.nc_sub, "mul": L.nc_mul, "div": L.nc_div}[op[1]](t, p)
         elif op[0] == "self":
             t = {"add": L.nc_add, "sub": L.nc_sub, "mul": L.nc_mul}[op[1]](t, t)
+        elif op[0] == "positive":
+            t = Engine.UNARY_CALLS[op[1]](L, L.nc_add_scalar(L.nc_mul(t, t), c_float(0.5)), op[2])
         elif op[0] == "residual":
             t = L.nc_add(t, Engine.UNARY_CALLS[op[1]](L, t, op[2]))
         elif op[0] == "transpose":

@@ -126,6 +126,53 @@ def test_engine_unary_random(eng, seed):
     eng.step_end()
 
 
+SCALAR_UNARY = [("neg", 0.0), ("scale", -2.5), ("add_scalar", 0.75), ("sqrt", 0.0), ("log", 0.0), ("pow", 3.0),
+                ("pow", 0.5), ("pow", -1.5)]
+
+
+@pytest.mark.parametrize("seed", range(24 * SWEEP))
+def test_engine_scalar_unary_random(eng, seed):
+    """neg, scale, add_scalar, sqrt, log and pow (in turn by seed) on a seeded positive tensor of rank
+    1-4 through nc.h, often a transposed view: forward and gradient against the oracle on the
+    contiguous copy, bit for bit for the first four; log and pow within an ulp of the host libm
+    (correctly rounded where it is not; see test_kernel_unary_libm)."""
+    name, sv = SCALAR_UNARY[seed % len(SCALAR_UNARY)]
+    rng = np.random.default_rng(7000 + seed)
+    nd = int(rng.integers(1, 5))
+    while True:
+        shape = tuple(int(rng.choice([1, 2, 3, 5, 17, 64, 100, 257])) for _ in range(nd))
+        if np.prod(shape) <= 200_000:
+            break
+    view, store = None, shape
+    if nd > 1 and rng.random() < 0.6:
+        i, j = sorted(int(v) for v in rng.choice(nd, 2, replace=False))
+        st = list(shape)
+        st[i], st[j] = st[j], st[i]
+        view, store = ("t", i, j), tuple(st)
+    X = np.exp(rng.uniform(-20, 20, store)).astype(np.float32)
+    x = np.ascontiguousarray(np_view(X, view))
+    G = rng.standard_normal(shape).astype(np.float32)
+    L = eng.lib
+    p = eng.param(X)
+    v = eng.view(p, view)
+    out = eng.UNARY_CALLS[name](L, v, sv)
+    y = eng.read(out)
+    eng.backward_with(out, G)
+    gx = eng.grad(v)
+    eng.step_end()
+    what = f"seed {seed} {name} {sv} shape {shape} view {view}"
+    y_o = O.unary_fwd(name, x, sv)
+    gx_o = O.unary_bwd(name, x, y_o, G, None, sv)
+    if name in ("log", "pow"):
+        assert ulp_distance(y, y_o).max() <= 1, what + " fwd"
+        fin = np.isfinite(gx_o)
+        bound = 2 * np.spacing(np.abs(gx_o[fin])).astype(np.float64)
+        assert (np.abs(gx[fin].astype(np.float64) - gx_o[fin]) <= bound).all(), what + " bwd"
+    else:
+        assert_bits(y, y_o, what + " fwd")
+        assert_bits(gx, gx_o, what + " bwd")
+
+
 @pytest.mark.parametrize("name,s", UNARY)
 def test_engine_unary_golden(eng, name, s):
     d = load("unary")
@@ -2229,3 +2276,67 @@ def test_kernel_fill(K, elem, n, offset):
     want = buf.copy()
     want[offset:offset + n] = pattern
     assert_bits(got, want, f"fill elem={elem} n={n} offset={offset}")
+
+
+def ulp_distance(a, b):
+    """Distance in units in the last place between float32 arrays (0 where both are NaN or equal)."""
+    a, b = np.asarray(a, np.float32), np.asarray(b, np.float32)
+    def ordered(v):
+        i = v.view(np.int32).astype(np.int64)
+        return np.where(i < 0, -(i & 0x7FFFFFFF), i)
+    d = np.abs(ordered(a) - ordered(b))
+    return np.where(np.isnan(a) & np.isnan(b), 0, d)
+
+
+LIBM_ULP = {"log": 1, "pow": 1}
+
+
+@pytest.mark.parametrize("name,s", [("log", 0.0), ("sqrt", 0.0), ("pow", 2.0), ("pow", 3.0), ("pow", 0.5),
+                                    ("pow", -1.5), ("pow", 1.7)])
+def test_kernel_unary_libm(K, name, s):
+    """log, sqrt and pow: the reference calls the host libm (logf, sqrtf, powf; ops_elementwise.c:233-234,
+    240), these kernels the device's.  sqrt is correctly rounded on both, so it and its backward
+    (g * 0.5 / y) are bit-exact, as is log's backward (g / x, a correctly rounded division); log and pow
+    are evaluated in double precision and rounded once, and agree with the host libm within LIBM_ULP
+    units in the last place (on a few hundred of the 10^6 inputs: there the kernel holds the correctly
+    rounded value), pow's backward (g * s * powf(x, s - 1)) within one more."""
+    rng = np.random.default_rng(zlib.crc32(f"libm/{name}/{s}".encode()))
+    x = np.concatenate([np.exp(rng.uniform(-85, 85, 1_000_000)).astype(np.float32),
+                        rng.standard_normal(10_000).astype(np.float32),
+                        np.array([0.0, -0.0, 1.0, -1.0, np.inf, -np.inf, np.nan, 1e-40, 1e-45, 4.0, 0.25],
+                                 np.float32)])
+    n = x.size
+    g = rng.standard_normal(n).astype(np.float32)
+    gi0 = rng.standard_normal(n).astype(np.float32)
+    X, Gd, GI, Y = dev(x), dev(g), dev(gi0), empty(4 * n)
+    K.unary_fwd(name, X.ptr, Y.ptr, n, s)
+    K.unary_bwd(name, X.ptr, Y.ptr, Gd.ptr, GI.ptr, n, s, accumulate=True)
+    sync()
+    y, gi = Y.to_numpy(np.float32, n), GI.to_numpy(np.float32, n)
+    y_o = O.unary_fwd(name, x, s)
+    gi_o = O.unary_bwd(name, x, y_o, g, gi0, s)
+    if name == "sqrt":
+        assert_bits(y, y_o, "sqrt")
+        assert_bits(gi, gi_o, "sqrt bwd")
+        return
+    d = ulp_distance(y, y_o)
+    print(f"\n{name} {s}: {int((d > 0).sum())} of {n} differ from the host libm, at most {int(d.max())} ulp")
+    assert d.max() <= LIBM_ULP[name], f"{name} {s}: {int(d.max())} ulp at x = {x[int(np.argmax(d))]!r}"
+    # where they differ, the kernel holds the correctly rounded value (the fp64 result rounded once)
+    # and the host's single-precision function is the one off by an ulp
+    i = np.flatnonzero(d)
+    with np.errstate(all="ignore"):
+        exact = (np.log(x[i].astype(np.float64)) if name == "log"
+                 else np.power(x[i].astype(np.float64), np.float64(np.float32(s)))).astype(np.float32)
+    assert_bits(y[i], exact, f"{name} {s}: the kernel's value where the host libm differs")
+    if name == "log":
+        assert_bits(gi, gi_o, "log bwd")
+    else:
+        # the term g * s * powf(x, s - 1) carries powf's difference (a few ulp of the term), then one
+        # rounding adding it to gi (an ulp of the sum)
+        t_o = O.unary_bwd(name, x, y_o, g, None, s)
+        fin = np.isfinite(gi_o)
+        err = np.abs(gi[fin].astype(np.float64) - gi_o[fin])
+        bound = np.spacing(np.abs(gi_o[fin])) + 4 * np.spacing(np.abs(t_o[fin])).astype(np.float64)
+        assert (err <= bound).all(), f"pow {s} bwd: {int((err > bound).sum())} over the bound"
+        assert ((np.isnan(gi) == np.isnan(gi_o)) & (np.isinf(gi) == np.isinf(gi_o))).all(), "pow bwd specials"

@@ -714,3 +714,48 @@ def test_argmax_first_index_and_nan_rule():
     assert list(got) == [1, 0, 2, 0]
     mx, _ = O.reduce_fwd("max", x, 1)
     assert mx[0] == 3 and np.isnan(mx[1]) and mx[2] == 9 and np.signbit(mx[3])
+
+
+LIBM = [("log", 0.0), ("sqrt", 0.0), ("pow", 2.0), ("pow", 3.0), ("pow", 0.5), ("pow", -1.5), ("pow", 1.7),
+        ("neg", 0.0), ("scale", -2.5), ("add_scalar", 0.75)]
+
+
+@ref_only
+@pytest.mark.parametrize("name,s", LIBM)
+def test_libm_unary_vs_live_reference(name, s):
+    """log, sqrt and pow call libm in the reference (ops_elementwise.c:233-234, 240; backward :305-306,
+    312), neg / scale / add_scalar its scale and axpy kernels: forward and accumulated backward against
+    the oracle bit for bit, positive inputs across the exponent range plus zero, negative, infinite,
+    subnormal and NaN values."""
+    from tests.ncdrive import Engine
+    rng = np.random.default_rng(zlib.crc32(f"{name}/{s}".encode()))
+    x = np.concatenate([np.exp(rng.uniform(-80, 80, 20_000)).astype(np.float32),
+                        rng.standard_normal(2_000).astype(np.float32),
+                        np.array([0.0, -0.0, 1.0, -1.0, np.inf, -np.inf, np.nan, 1e-40, 1e-45, 4.0, 0.25],
+                                 np.float32)])
+    with Engine(O.REF_LIB) as ref:
+        (gx,), (G1, G2) = _twice(ref, [ref.param(x)], lambda p: Engine.UNARY_CALLS[name](ref.lib, p, s), rng)
+        y_ref = ref.read(Engine.UNARY_CALLS[name](ref.lib, ref.param(x), s))
+    y = O.unary_fwd(name, x, s)
+    assert_bits(y, y_ref, f"{name} {s} fwd")
+    assert_bits(O.unary_bwd(name, x, y, G2, O.unary_bwd(name, x, y, G1, s=s), s), gx, f"{name} {s} bwd accumulated")
+
+
+def test_libm_unary_closed_forms():
+    """sqrt of exact squares is exact; log(1) = 0, log(e^k) within an ulp of k; pow(x, 1) = x,
+    pow(x, 2) within an ulp of x*x; the backward of log is g / x and of sqrt g * 0.5 / sqrt(x)."""
+    rng = np.random.default_rng(9)
+    r = rng.integers(1, 4096, 1000).astype(np.float32)
+    assert_bits(O.unary_fwd("sqrt", r * r), r, "sqrt of squares")
+    assert O.unary_fwd("log", np.array([1.0], np.float32))[0] == 0.0
+    k = np.arange(-20, 21).astype(np.float32)
+    lg = O.unary_fwd("log", np.exp(k.astype(np.float64)).astype(np.float32))
+    assert np.all(np.abs(lg - k) <= 4 * np.spacing(np.maximum(np.abs(k), 1))), "log(e^k)"
+    x = (rng.random(1000) * 100).astype(np.float32)
+    assert_bits(O.unary_fwd("pow", x, 1.0), x, "pow(x, 1)")
+    sq = O.unary_fwd("pow", x, 2.0)
+    assert np.all(np.abs(sq - x * x) <= np.spacing(x * x)), "pow(x, 2)"
+    g = rng.standard_normal(1000).astype(np.float32)
+    assert_bits(O.unary_bwd("log", x, None, g), g / x, "d log")
+    y = O.unary_fwd("sqrt", x)
+    assert_bits(O.unary_bwd("sqrt", x, y, g), (g * np.float32(0.5)) / y, "d sqrt")
