@@ -2,10 +2,10 @@
 
 A seeded plan of 3-7 ops (activations, broadcast binary ops against parameters, a tensor combined with
 itself (t op t) or with an activation of itself (t + f(t)), so that its gradient receives two terms,
-sqrt / log / pow of t * t + 0.5,
+sqrt / log / pow of t * t + 0.5, exp of tanh(t), strided slices,
 sum / mean / max over an axis with or without keepdim, softmax / log_softmax, LayerNorm with weight and
-bias, transposed and reshaped views, matmul and linear with parameters, and sometimes a cross-entropy or
-nll loss head) is built from a parameter x, the same plan runs in this
+bias, transposed and reshaped views, matmul and linear with parameters, and sometimes a cross-entropy,
+nll or mse loss head) is built from a parameter x, the same plan runs in this
 engine (tests/ncdrive.Engine over newch_amd/libnc.so, on the GPU) and in the reference engine compiled
 from its sources (oracle/_ref/libnc_ref.so, on the CPU), then loss = sum(out * G) goes backward in
 both.  The output and every parameter's gradient are compared: bit for bit when every op of the chain
@@ -58,7 +58,7 @@ def make_plan(seed, exact_only=False):
     ops, exact = [], True
     for _ in range(int(rng.integers(3, 8))):
         nd = len(shape)
-        kinds = ["unary", "binary", "binary", "transpose", "self", "residual", "positive"]
+        kinds = ["unary", "binary", "binary", "transpose", "self", "residual", "positive", "slice", "bounded_exp"]
         if nd >= 2:
             kinds += ["reduce", "reshape"]
         if shape[-1] >= 8 and not exact_only:
@@ -83,6 +83,16 @@ def make_plan(seed, exact_only=False):
             ops.append(("positive", f, 1.5))
             if f != "sqrt":
                 exact = False  # log and pow: the host libm is off by an ulp on ~0.05% of inputs
+        elif k == "slice":  # a strided view along one axis: its gradient scatters into the base
+            axis = int(rng.integers(0, nd))
+            dim = shape[axis]
+            step = int(rng.choice([1, 2, 3])) if dim > 2 else 1
+            start = int(rng.integers(0, dim))
+            length = int(rng.integers(1, (dim - 1 - start) // step + 2))
+            ops.append(("slice", axis, start, length, step))
+            shape[axis] = length
+        elif k == "bounded_exp":  # exp(tanh(t)): the reference's exp replica on a bounded argument
+            ops.append(("bounded_exp",))
         elif k == "residual":  # t + f(t): the gradient reaches t along two paths
             ops.append(("residual", str(rng.choice(UNARY)), float(rng.choice([0.01, 0.2]))))
         elif k == "transpose":
@@ -97,6 +107,8 @@ def make_plan(seed, exact_only=False):
         elif k == "reduce":
             kind = "max" if exact_only else str(rng.choice(["sum", "mean", "max"]))
             axis, keep = int(rng.integers(0, nd)), int(rng.integers(0, 2))
+            if kind != "max" and axis == nd - 1 and ops and ops[-1] == ("softmax", False):
+                kind = "max"  # a sum of softmax over its own axis is constant: every gradient ~0
             ops.append(("reduce", kind, axis, keep))
             shape = shape[:axis] + ([1] if keep else []) + shape[axis + 1:]
             if kind != "max":
@@ -119,6 +131,10 @@ def make_plan(seed, exact_only=False):
             ops.append(("loss", bool(rng.integers(0, 2)), int(np.prod(shape[:-1])), C))
             shape = []
             exact = False
+    elif not exact_only and rng.random() < 0.15:
+        ops.append(("mse", tuple(shape)))  # mse_loss against a fixed target of the same shape
+        shape = []
+        exact = False
     return x_shape, ops, exact, tuple(shape)
 
 
@@ -148,6 +164,12 @@ def run_plan(e, seed, x_shape, ops):
             t = L.nc_add(t, Engine.UNARY_CALLS[op[1]](L, t, op[2]))
         elif op[0] == "transpose":
             t = L.nc_transpose(t, op[1], op[2])
+        elif op[0] == "slice":
+            t = L.nc_slice(t, op[1], op[2], op[3], op[4])
+        elif op[0] == "bounded_exp":
+            t = L.nc_exp(L.nc_tanh(t))
+        elif op[0] == "mse":
+            t = L.nc_mse_loss(t, e.tensor(rng.standard_normal(op[1]).astype(np.float32)))
         elif op[0] == "reshape":
             nd, shp = abi.shape_arg(op[1])
             t = L.nc_reshape(t, nd, shp)
@@ -252,6 +274,8 @@ def build_model(e, seed, x_shape, ops):
             steps.append((op, params[-2:]))
         elif op[0] == "loss":
             steps.append((op, [e.tensor(rng.integers(0, op[3], op[2]).astype(np.int32))]))
+        elif op[0] == "mse":
+            steps.append((op, [e.tensor(rng.standard_normal(op[1]).astype(np.float32))]))
         else:
             steps.append((op, []))
     L.nc_persistent_end(e.ctx)
@@ -272,6 +296,12 @@ def build_model(e, seed, x_shape, ops):
                 t = L.nc_add(t, Engine.UNARY_CALLS[op[1]](L, t, op[2]))
             elif op[0] == "transpose":
                 t = L.nc_transpose(t, op[1], op[2])
+            elif op[0] == "slice":
+                t = L.nc_slice(t, op[1], op[2], op[3], op[4])
+            elif op[0] == "bounded_exp":
+                t = L.nc_exp(L.nc_tanh(t))
+            elif op[0] == "mse":
+                t = L.nc_mse_loss(t, ts[0])
             elif op[0] == "reshape":
                 nd, shp = abi.shape_arg(op[1])
                 t = L.nc_reshape(t, nd, shp)
