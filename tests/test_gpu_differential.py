@@ -387,3 +387,54 @@ def test_training_steps_match_reference_engine(engines, exact_only, seed):
     scale = max(float(np.abs(r[np.isfinite(r)]).max(initial=0.0)) for r in rp)
     for i, (g, r) in enumerate(zip(gp, rp)):
         _same(g, r, exact, f"{what} parameter {i} after the steps", scale)
+
+
+def run_twice(e, seed, x_shape, ops):
+    """The plan once forward, then two backward passes over it (sum(out * G1), then sum(out * G2),
+    the graph retained), the second adding into the gradients the first left."""
+    params, forward = build_model(e, seed, x_shape, ops)
+    out = forward()
+    rng = np.random.default_rng(30_000 + seed)
+    shape = e.read(out).shape
+    for _ in range(2):
+        e.backward_with(out, rng.standard_normal(shape).astype(np.float32))
+    grads = [e.grad(p) for p in params]
+    e.step_end()
+    return grads
+
+
+@pytest.mark.parametrize("exact_only,seed", [(False, s) for s in range(30 * SWEEP)] + [(True, s) for s in range(30 * SWEEP)])
+def test_retained_graph_backward_twice(engines, exact_only, seed):
+    """Two backward passes over one retained graph: every parameter's gradient holds both passes'
+    sums, as the reference's (bit for bit for order-independent chains)."""
+    x_shape, ops, exact, _ = make_plan(seed + 1400, exact_only)
+    what = f"seed {seed} x {x_shape} ops {ops}"
+    gg, rg = (run_twice(e, seed, x_shape, ops) for e in engines)
+    scale = max(float(np.abs(r[np.isfinite(r)]).max(initial=0.0)) for r in rg)
+    for i, (g, r) in enumerate(zip(gg, rg)):
+        _same(g, r, exact, f"{what} grad of parameter {i} after two passes", scale)
+
+
+@pytest.mark.parametrize("seed", range(12 * SWEEP))
+def test_linear_int8_matches_reference(engines, seed):
+    """quantize_rows of a weight, then linear_int8 of activations against it (with and without bias),
+    on random shapes in both engines: quantized weights, scales and outputs bit for bit."""
+    rng = np.random.default_rng(40_000 + seed)
+    M, K, N = (int(v) for v in rng.integers(1, 300, 3))
+    x = (rng.standard_normal((M, K)) * 2).astype(np.float32)
+    w = rng.standard_normal((N, K)).astype(np.float32)
+    b = rng.standard_normal(N).astype(np.float32) if seed % 2 else None
+    outs = []
+    for e in engines:
+        L = e.lib
+        sc = ctypes.c_void_p()
+        wq = L.nc_quantize_rows(e.tensor(w), ctypes.byref(sc))
+        e.check()
+        y = L.nc_linear_int8(e.tensor(x), wq, sc, e.tensor(b) if b is not None else None)
+        outs.append((e.read(wq), e.read(sc), e.read(y)))
+        e.step_end()
+    (gq, gs, gy), (rq, rs, ry) = outs
+    what = f"seed {seed} M {M} K {K} N {N} bias {b is not None}"
+    assert (gq == rq).all(), what + " quantized weight"
+    _same(gs, rs, True, what + " scales", 0.0)
+    _same(gy, ry, True, what + " linear_int8 output", 0.0)
