@@ -17,8 +17,10 @@
 // tiles (8 waves of 4 x 2 MFMA tiles, BK 128, 147 KiB of LDS), smaller ones 128 x 128 (4 waves of
 // 2 x 2, BK 64).  Large problems with K a multiple of 128 and 16-byte aligned rows take k_qgemm_dma
 // instead: the same tile over 16 waves, its panels loaded straight into LDS one 128-byte k step ahead.
-// Blocks are remapped so each XCD (blocks b with b % 8 equal) works a contiguous run of tiles, and
-// tiles run in groups of 8 tile-rows so neighbouring blocks share panels in L2.
+// When K is also a multiple of 256, k_qgemm_pipe runs that tile over 8 waves with the k loop written
+// as one software-pipelined assembly block (below).  Blocks are remapped so each XCD (blocks b with
+// b % 8 equal) works a contiguous run of tiles, and tiles run in groups of 8 tile-rows so neighbouring
+// blocks share panels in L2.
 //
 // linear_int8 epilogue (ops_quant.c:75-79): y = (float)acc * xs[m] * ws[n] + (bias ? bias[n] : 0),
 // evaluated left to right in fp32 without contraction (the reference's scalar glue), so the fused
@@ -29,7 +31,10 @@ namespace nchip {
 
 typedef int i16v __attribute__((ext_vector_type(16)));
 
-constexpr int kQgGroupM = 8;
+#ifndef QG_GROUP_M
+#define QG_GROUP_M 8
+#endif
+constexpr int kQgGroupM = QG_GROUP_M;
 
 // Tile configurations: TM x TN MFMA tiles (32 x 32) per wave, WGM x WGN waves per workgroup, BK
 // k-bytes per stage, two LDS stages.  Large problems use a 256 x 256 tile (8 waves, 147 KiB of LDS,
@@ -212,6 +217,79 @@ __device__ __forceinline__ int dma_swz(int row, int c) {
 }
 
 
+// Epilogue of a wave's TM x TN block of 32 x 32 MFMA tiles whose first row and column are mb and nb:
+// lane l, element v of a tile holds row 8 (v / 4) + 4 (l / 32) + v % 4, column l % 32, so each store
+// instruction writes two 128-byte row segments.  (Issuing the B fragment first gives C^T tiles whose
+// lanes hold four consecutive columns, one 16-byte store each; 32 rows of 32 bytes per instruction
+// ran slower.)
+template <int TM, int TN, bool OUT_F32>
+__device__ __forceinline__ void qg_store(const QgArgs &p, const i16v (&acc)[TM][TN], int mb, int nb, int lane) {
+    // the row scales a lane needs for tile row i, xs[mb + 32 i + 8 g + 4 (l / 32) .. + 3], loaded four
+    // at a time before the tile row's first store (rows past M read row M - 1; they are not stored)
+    const bool xs_vec = OUT_F32 && (((uintptr_t)p.xs) & 15) == 0;
+#pragma unroll
+    for (int i = 0; i < TM; i++) {
+        f4 xs4[4];
+        if (OUT_F32) {
+#pragma unroll
+            for (int g = 0; g < 4; g++) {
+                const int m = mb + i * 32 + 8 * g + 4 * (lane >> 5);
+                if (xs_vec && m + 4 <= p.M) {
+                    xs4[g] = *(const f4 *)(p.xs + m);
+                } else {
+#pragma unroll
+                    for (int e = 0; e < 4; e++) xs4[g][e] = p.xs[min(m + e, p.M - 1)];
+                }
+            }
+        }
+#pragma unroll
+        for (int j = 0; j < TN; j++) {
+            const int n = nb + j * 32 + (lane & 31);
+            if (n >= p.N) continue;
+            float wsn = 0.0f, bn = 0.0f;
+            if (OUT_F32) {
+                wsn = p.ws[n];
+                bn = p.bias ? p.bias[n] : 0.0f;
+            }
+#pragma unroll
+            for (int v = 0; v < 16; v++) {
+                const int m = mb + i * 32 + 8 * (v >> 2) + 4 * (lane >> 5) + (v & 3);
+                if (m >= p.M) continue;
+                if (OUT_F32)
+                    p.Y[(int64_t)m * p.ldc + n] = (float)acc[i][j][v] * xs4[v >> 2][v & 3] * wsn + bn;
+                else
+                    p.C[(int64_t)m * p.ldc + n] = acc[i][j][v];
+            }
+        }
+    }
+}
+
+// qg_store's fp32 epilogue with the scales and bias of the workgroup's 256 rows and columns in LDS
+// (sxs[r] = xs[m0 + r], sws[c] = ws[n0 + c], sb[c] = bias or 0); mb, nb relative to the tile
+template <int TM, int TN>
+__device__ __forceinline__ void qg_store_f32_lds(const QgArgs &p, const i16v (&acc)[TM][TN], int m0, int n0, int mb,
+                                                 int nb, const float *sxs, const float *sws, const float *sb,
+                                                 int lane) {
+#pragma unroll
+    for (int i = 0; i < TM; i++) {
+        f4 xs4[4];
+#pragma unroll
+        for (int g = 0; g < 4; g++) xs4[g] = *(const f4 *)(sxs + mb + i * 32 + 8 * g + 4 * (lane >> 5));
+#pragma unroll
+        for (int j = 0; j < TN; j++) {
+            const int c = nb + j * 32 + (lane & 31), n = n0 + c;
+            if (n >= p.N) continue;
+            const float wsn = sws[c], bn = sb[c];
+#pragma unroll
+            for (int v = 0; v < 16; v++) {
+                const int m = m0 + mb + i * 32 + 8 * (v >> 2) + 4 * (lane >> 5) + (v & 3);
+                if (m >= p.M) continue;
+                p.Y[(int64_t)m * p.ldc + n] = (float)acc[i][j][v] * xs4[v >> 2][v & 3] * wsn + bn;
+            }
+        }
+    }
+}
+
 template <bool OUT_F32>
 __global__ __launch_bounds__(kDmaNT, 1) void k_qgemm_dma(QgArgs p) {
     extern __shared__ __attribute__((aligned(16))) int8_t smem[];
@@ -297,29 +375,203 @@ __global__ __launch_bounds__(kDmaNT, 1) void k_qgemm_dma(QgArgs p) {
         }
     }
 
+    qg_store<kTM, kTN, OUT_F32>(p, acc, m0 + wm * kTM * 32, n0 + wn * kTN * 32, lane);
+}
+
+// ------------------------------------------------------------------------------------------------
+// Software-pipelined variant of the direct-to-LDS kernel: the same 256 x 256 tile and 128-byte k steps
+// over 8 waves of 4 x 2 MFMA tiles (128 x 64 each) whose 128 accumulator registers are AGPRs.  The
+// whole k loop is one inline-assembly block (so the accumulators stay in place: split into one
+// block per substep, the compiler moved them between register files at every block), in which a k
+// step is four 32-k substeps: each issues the next substep's six fragment reads into the second of
+// two register sets, interleaved with its own eight MFMAs on the first, and ends by waiting for those
+// reads, so the LDS latency runs under the matrix work instead of between its instructions.  The
+// barrier of a k step sits after the reads of its last substep and before that substep's MFMAs: every
+// wave has finished reading the stage the barrier frees, and the MFMAs after it need no LDS; the next
+// step's panel loads, into the stage just freed, are issued between those MFMAs.  LDS:
+// [A stage 0 | A stage 1 | B stage 0 | B stage 1], 32 KiB each, rows of 128 bytes with logical chunk c
+// of row r at c ^ ((r >> 1) & 7); a fragment address is one register per substep and operand (the
+// permutation depends on r only through the fragment row's bits 1-3, the same for all of a wave's
+// tiles), stage and tile offsets immediate.  Waves 0-3 load A's panels, 4-7 B's, each eight 1 KiB
+// loads per step from the tile's first row (a scalar base) at one 32-bit lane offset per load, which
+// advances 128 bytes a step.  K is a multiple of 256 (whole pairs of steps, one per stage).  The fp32
+// epilogue's row and column scales and bias are loaded before the loop and put in LDS past the stages
+// after it.  Against the 16-wave kernel on the same boxes: 136-141 against 160-180 us for the int8
+// GEMM of [8192, 4096] x [4096, 4096]^T, 168-179 against 196-214 us for linear_int8 of that shape;
+// one wave per SIMD of 4 x 4 MFMA tiles (256 AGPRs) ran 161-177 us.
+#ifndef QG_PIPE
+#define QG_PIPE 1
+#endif
+constexpr int kPipeNT = 512;
+constexpr int kPipePanel = kDmaRows * kDmaBK;  // bytes of one operand's stage
+
+#define QG_RD(dst, addr, off) "ds_read_b128 %[" #dst "], %[" #addr "] offset:" #off "\n\t"
+#define QG_MF(c, a, b) "v_mfma_i32_32x32x32_i8 %[" #c "], %[" #a "], %[" #b "], %[" #c "]\n\t"
+// eight MFMAs on register set M while set R is read from substep S at stage offsets O0..O3
+#define QG_SUB(R, M, S, O0, O1, O2, O3)                                                                   \
+    QG_RD(R##a0, aA##S, O0) QG_RD(R##b0, aB##S, O0) QG_MF(c00, M##a0, M##b0) QG_RD(R##a1, aA##S, O1)      \
+    QG_MF(c01, M##a0, M##b1) QG_RD(R##b1, aB##S, O1) QG_MF(c10, M##a1, M##b0) QG_RD(R##a2, aA##S, O2)      \
+    QG_MF(c11, M##a1, M##b1) QG_RD(R##a3, aA##S, O3) QG_MF(c20, M##a2, M##b0) QG_MF(c21, M##a2, M##b1)    \
+    QG_MF(c30, M##a3, M##b0) QG_MF(c31, M##a3, M##b1) "s_waitcnt lgkmcnt(0)\n\t"
+#define QG_SUB0(R, M, S) QG_SUB(R, M, S, 0, 4096, 8192, 12288)
+#define QG_SUB1(R, M, S) QG_SUB(R, M, S, 32768, 36864, 40960, 45056)
+#define QG_LAST(M)                                                                                         \
+    QG_MF(c00, M##a0, M##b0) QG_MF(c01, M##a0, M##b1) QG_MF(c10, M##a1, M##b0) QG_MF(c11, M##a1, M##b1)     \
+    QG_MF(c20, M##a2, M##b0) QG_MF(c21, M##a2, M##b1) QG_MF(c30, M##a3, M##b0) QG_MF(c31, M##a3, M##b1)
+#define QG_READ0(R)                                                                                        \
+    QG_RD(R##a0, aA0, 0) QG_RD(R##b0, aB0, 0) QG_RD(R##a1, aA0, 4096) QG_RD(R##b1, aB0, 4096)            \
+    QG_RD(R##a2, aA0, 8192) QG_RD(R##a3, aA0, 12288) "s_waitcnt lgkmcnt(0)\n\t"
+// one 1 KiB panel load into LDS at lo + OFF (M0), 16 bytes per lane from tb + V
+#define QG_LD(V, OFF) "s_add_u32 m0, %[lo], " #OFF "\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %[" #V "], %[tb]\n\t"
+#define QG_ADV(V) "v_add_u32 %[" #V "], 0x80, %[" #V "]\n\t"
+#define QG_DMA(O0, O1, O2, O3, O4, O5, O6, O7)                                                           \
+    QG_LD(v0, O0) QG_LD(v1, O1) QG_LD(v2, O2) QG_LD(v3, O3) QG_LD(v4, O4) QG_LD(v5, O5) QG_LD(v6, O6)     \
+    QG_LD(v7, O7) QG_ADV(v0) QG_ADV(v1) QG_ADV(v2) QG_ADV(v3) QG_ADV(v4) QG_ADV(v5) QG_ADV(v6) QG_ADV(v7)
+#define QG_DMA0 QG_DMA(0, 1024, 2048, 3072, 4096, 5120, 6144, 7168)
+#define QG_DMA1 QG_DMA(32768, 33792, 34816, 35840, 36864, 37888, 38912, 39936)
+// QG_SUB with a step's eight panel loads (LDS offsets D0..D7) issued between its MFMAs
+#define QG_SUBD(R, M, S, O0, O1, O2, O3, D0, D1, D2, D3, D4, D5, D6, D7)                                  \
+    QG_RD(R##a0, aA##S, O0) QG_RD(R##b0, aB##S, O0) QG_MF(c00, M##a0, M##b0) QG_LD(v0, D0)                \
+    QG_RD(R##a1, aA##S, O1) QG_MF(c01, M##a0, M##b1) QG_LD(v1, D1) QG_RD(R##b1, aB##S, O1)               \
+    QG_MF(c10, M##a1, M##b0) QG_LD(v2, D2) QG_RD(R##a2, aA##S, O2) QG_MF(c11, M##a1, M##b1)              \
+    QG_LD(v3, D3) QG_RD(R##a3, aA##S, O3) QG_MF(c20, M##a2, M##b0) QG_LD(v4, D4)                         \
+    QG_MF(c21, M##a2, M##b1) QG_LD(v5, D5) QG_MF(c30, M##a3, M##b0) QG_LD(v6, D6)                        \
+    QG_MF(c31, M##a3, M##b1) QG_LD(v7, D7) QG_ADV(v0) QG_ADV(v1) QG_ADV(v2) QG_ADV(v3) QG_ADV(v4)        \
+    QG_ADV(v5) QG_ADV(v6) QG_ADV(v7) "s_waitcnt lgkmcnt(0)\n\t"
+// substep 0 of stage 1 with the loads of stage 0, and substep 0 of stage 0 with those of stage 1
+#define QG_SUBD1(R, M) QG_SUBD(R, M, 0, 32768, 36864, 40960, 45056, 0, 1024, 2048, 3072, 4096, 5120, 6144, 7168)
+#define QG_SUBD0(R, M)                                                                                     \
+    QG_SUBD(R, M, 0, 0, 4096, 8192, 12288, 32768, 33792, 34816, 35840, 36864, 37888, 38912, 39936)
+
+
+template <bool OUT_F32>
+__global__ __launch_bounds__(kPipeNT, 1) void k_qgemm_pipe(QgArgs p) {
+    extern __shared__ __attribute__((aligned(16))) int8_t smem[];
+    constexpr int kTM = 4, kTN = 2, kWGN = 4;
+    constexpr int kWaves = kPipeNT / kWave;
+    constexpr int kLoads = 8;  // 1 KiB loads per wave per step
+    static_assert(kDmaBK == 128 && kDmaRowsPerLoad == 8 && kPipePanel == 32768,
+                  "the assembly's offsets are written for 128-byte steps of 256 rows");
+    static_assert(kLoads * kDmaRowsPerLoad * (kWaves / 2) == kDmaRows, "each half of the waves loads one operand");
+    static_assert(kTM * 32 * (kWaves / kWGN) == kDmaRows && kTN * 32 * kWGN == kDmaRows,
+                  "the waves' MFMA tiles cover the workgroup tile");
+
+    int id = blockIdx.x;
+    const int nblk = gridDim.x;
+    if ((nblk & 7) == 0) id = (id & 7) * (nblk >> 3) + (id >> 3);
+    const int per_group = kQgGroupM * p.tiles_n;
+    const int first_m = (id / per_group) * kQgGroupM;
+    const int gsize = min(p.tiles_m - first_m, kQgGroupM);
+    const int tm = first_m + (id % per_group) % gsize;
+    const int tn = (id % per_group) / gsize;
+    const int m0 = tm * kDmaRows, n0 = tn * kDmaRows;
+
+    const int t = threadIdx.x, lane = t & (kWave - 1), wid = __builtin_amdgcn_readfirstlane(t / kWave);
+    const int wm = wid / kWGN, wn = wid % kWGN;
+
+    // panel loads: wave w's load q covers rows 64 (w % 4) + 8 q .. + 7 of its operand's panel; rows
+    // past M / N read the last row (in bounds; those accumulators are never stored)
+    const bool pb = wid >= kWaves / 2;
+    const int r0 = pb ? n0 : m0, rows = pb ? p.N : p.M;
+    const int64_t ld = pb ? p.ldb : p.lda;
+    const int8_t *tb = (pb ? p.B : p.A) + (int64_t)r0 * ld;  // the tile's first row
+    uint32_t vo[kLoads];
 #pragma unroll
-    for (int i = 0; i < kTM; i++) {
+    for (int q = 0; q < kLoads; q++) {
+        const int row = (wid % (kWaves / 2)) * (kLoads * kDmaRowsPerLoad) + q * kDmaRowsPerLoad + lane / kDmaChunks;
+        const int c = dma_swz(row, lane % kDmaChunks) / 16;  // the chunk that belongs at this lane's place
+        vo[q] = (uint32_t)((int64_t)(min(r0 + row, rows - 1) - r0) * ld) + (uint32_t)(c * 16);
+    }
+    const uint32_t sbase = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) int8_t *)smem;
+    const uint32_t lo = sbase + (pb ? 2 * kPipePanel : 0) + (uint32_t)(wid % (kWaves / 2)) * (kLoads * 1024);
+
+    // fragment addresses (stage 0): lane reads row (tile row) + frow, logical chunk 2 s + fh
+    const int frow = lane & 31, fh = lane >> 5, x = (frow >> 1) & 7;
+    uint32_t aA[4], aB[4];
 #pragma unroll
-        for (int j = 0; j < kTN; j++) {
-            const int n = n0 + (wn * kTN + j) * 32 + (lane & 31);
-            if (n >= p.N) continue;
-            float wsn = 0.0f, bn = 0.0f;
-            if (OUT_F32) {
-                wsn = p.ws[n];
-                bn = p.bias ? p.bias[n] : 0.0f;
-            }
+    for (int s = 0; s < 4; s++) {
+        const uint32_t sw = (uint32_t)(((2 * s + fh) ^ x) * 16);
+        aA[s] = sbase + (uint32_t)(wm * kTM * 32 + frow) * kDmaBK + sw;
+        aB[s] = sbase + (uint32_t)(2 * kPipePanel) + (uint32_t)(wn * kTN * 32 + frow) * kDmaBK + sw;
+    }
+
+    i16v acc[kTM][kTN];
 #pragma unroll
-            for (int v = 0; v < 16; v++) {
-                const int m = m0 + (wm * kTM + i) * 32 + 8 * (v >> 2) + 4 * (lane >> 5) + (v & 3);
-                if (m >= p.M) continue;
-                if (OUT_F32)
-                    p.Y[(int64_t)m * p.ldc + n] = (float)acc[i][j][v] * p.xs[m] * wsn + bn;
-                else
-                    p.C[(int64_t)m * p.ldc + n] = acc[i][j][v];
-            }
+    for (int i = 0; i < kTM; i++)
+#pragma unroll
+        for (int j = 0; j < kTN; j++) acc[i][j] = i16v{};
+
+    // fp32 epilogue: the tile's 256 row scales, 256 column scales and 256 biases, loaded now (the k loop
+    // hides their latency) and put in LDS past the stages once the loop is done
+    float sv[2] = {0.0f, 0.0f};
+    if (OUT_F32) {
+#pragma unroll
+        for (int h = 0; h < 2; h++) {
+            const int u = min(t + h * kPipeNT, 3 * kDmaRows - 1);  // unconditional loads: no wait before the loop
+            const int which = u / kDmaRows, idx = u % kDmaRows;
+            const int m = min(m0 + idx, p.M - 1), n = min(n0 + idx, p.N - 1);
+            const float *src = which == 0 ? p.xs + m : which == 1 || !p.bias ? p.ws + n : p.bias + n;
+            const float v = *src;
+            sv[h] = which == 2 && !p.bias ? 0.0f : v;
         }
     }
+
+    int np = p.K / (2 * kDmaBK);  // pairs of k steps, >= 1
+    i4 f0[6], f1[6];              // the two fragment register sets: a0-a3, b0-b1
+    asm volatile(
+        "s_nop 7\n\ts_nop 7\n\t"  // the accumulators' zeroing before the first MFMA
+        QG_DMA0 "s_waitcnt vmcnt(0)\n\ts_barrier\n\t" QG_DMA1 QG_READ0(p0)
+        "L_top_%=:\n\t"
+        "s_sub_u32 %[np], %[np], 1\n\t"
+        QG_SUB0(p1, p0, 1) QG_SUB0(p0, p1, 2) QG_SUB0(p1, p0, 3)
+        "s_waitcnt vmcnt(0)\n\ts_barrier\n\t"
+        "s_cmp_eq_u32 %[np], 0\n\ts_cbranch_scc1 L_nodma_%=\n\t"
+        QG_SUBD1(p0, p1)
+        "s_branch L_s1_%=\n\t"
+        "L_nodma_%=:\n\t"
+        QG_SUB1(p0, p1, 0)
+        "L_s1_%=:\n\t"
+        QG_SUB1(p1, p0, 1) QG_SUB1(p0, p1, 2) QG_SUB1(p1, p0, 3)
+        "s_cmp_eq_u32 %[np], 0\n\ts_cbranch_scc1 L_last_%=\n\t"
+        "s_waitcnt vmcnt(0)\n\ts_barrier\n\t"
+        QG_SUBD0(p0, p1)
+        "s_branch L_top_%=\n\t"
+        "L_last_%=:\n\t"
+        QG_LAST(p1)
+        "s_nop 7\n\ts_nop 7\n\ts_nop 7"  // the last MFMAs' results before they are read
+        : [c00] "+a"(acc[0][0]), [c01] "+a"(acc[0][1]), [c10] "+a"(acc[1][0]), [c11] "+a"(acc[1][1]),
+          [c20] "+a"(acc[2][0]), [c21] "+a"(acc[2][1]), [c30] "+a"(acc[3][0]), [c31] "+a"(acc[3][1]),
+          [p0a0] "=&v"(f0[0]), [p0a1] "=&v"(f0[1]), [p0a2] "=&v"(f0[2]), [p0a3] "=&v"(f0[3]), [p0b0] "=&v"(f0[4]),
+          [p0b1] "=&v"(f0[5]), [p1a0] "=&v"(f1[0]), [p1a1] "=&v"(f1[1]), [p1a2] "=&v"(f1[2]), [p1a3] "=&v"(f1[3]),
+          [p1b0] "=&v"(f1[4]), [p1b1] "=&v"(f1[5]), [v0] "+v"(vo[0]), [v1] "+v"(vo[1]), [v2] "+v"(vo[2]),
+          [v3] "+v"(vo[3]), [v4] "+v"(vo[4]), [v5] "+v"(vo[5]), [v6] "+v"(vo[6]), [v7] "+v"(vo[7]), [np] "+s"(np)
+        : [aA0] "v"(aA[0]), [aA1] "v"(aA[1]), [aA2] "v"(aA[2]), [aA3] "v"(aA[3]), [aB0] "v"(aB[0]),
+          [aB1] "v"(aB[1]), [aB2] "v"(aB[2]), [aB3] "v"(aB[3]), [lo] "s"(lo), [tb] "s"(tb)
+        : "memory", "m0", "scc");
+
+    if (OUT_F32) {
+        float *sc = (float *)(smem + 4 * kPipePanel);
+#pragma unroll
+        for (int h = 0; h < 2; h++)
+            if (t + h * kPipeNT < 3 * kDmaRows) sc[t + h * kPipeNT] = sv[h];
+        __syncthreads();
+        qg_store_f32_lds<kTM, kTN>(p, acc, m0, n0, wm * kTM * 32, wn * kTN * 32, sc, sc + kDmaRows, sc + 2 * kDmaRows,
+                                   lane);
+    } else {
+        qg_store<kTM, kTN, OUT_F32>(p, acc, m0 + wm * kTM * 32, n0 + wn * kTN * 32, lane);
+    }
 }
+
+constexpr size_t kPipeLds = 4 * (size_t)kPipePanel + 3 * kDmaRows * sizeof(float);
+
+#if QG_PIPE
+static bool done_pipe(int dev) {
+    static bool done[64] = {};
+    if (dev < 0 || dev >= 64 || done[dev]) return true;
+    done[dev] = true;
+    return false;
+}
+#endif
 
 static int launch_qgemm_dma(QgArgs p, bool out_f32, hipStream_t st, const char *what) {
     p.tiles_m = (p.M + kDmaRows - 1) / kDmaRows;
@@ -333,6 +585,19 @@ static int launch_qgemm_dma(QgArgs p, bool out_f32, hipStream_t st, const char *
         (void)hipFuncSetAttribute((const void *)k_qgemm_dma<false>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)kDmaLds);
         done[dev] = true;
     }
+#if QG_PIPE
+    // whole pairs of k steps, and every lane offset of a tile's panel loads within 32 bits
+    const bool pipe = p.K % (2 * kDmaBK) == 0 && 256 * (p.lda > p.ldb ? p.lda : p.ldb) + p.K < ((int64_t)1 << 32);
+    if (pipe) {
+        if (!done_pipe(dev)) {
+            (void)hipFuncSetAttribute((const void *)k_qgemm_pipe<true>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)kPipeLds);
+            (void)hipFuncSetAttribute((const void *)k_qgemm_pipe<false>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)kDmaLds);
+        }
+        if (out_f32) hipLaunchKernelGGL(k_qgemm_pipe<true>, dim3((unsigned)blocks), dim3(kPipeNT), kPipeLds, st, p);
+        else hipLaunchKernelGGL(k_qgemm_pipe<false>, dim3((unsigned)blocks), dim3(kPipeNT), kDmaLds, st, p);
+        return check_launch(what);
+    }
+#endif
     if (out_f32) hipLaunchKernelGGL(k_qgemm_dma<true>, dim3((unsigned)blocks), dim3(kDmaNT), kDmaLds, st, p);
     else hipLaunchKernelGGL(k_qgemm_dma<false>, dim3((unsigned)blocks), dim3(kDmaNT), kDmaLds, st, p);
     return check_launch(what);
