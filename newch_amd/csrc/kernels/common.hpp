@@ -91,7 +91,8 @@ __device__ __forceinline__ float exp8(float x) {
     return x0 != x0 ? x0 : res;
 }
 
-// exp8 for arguments that are <= 0 or NaN (x minus its row maximum, log-probabilities): there the
+// exp8 for arguments that are <= 0 or NaN (x minus its row maximum, log-probabilities, erf's and
+// tanh's exponentials, GELU's Gaussian): there the
 // upper clamp is inactive and n <= 0, so the 2^128 split multiplies by 1; both are dropped, and the
 // result is bit-identical to exp8 on that domain.
 __device__ __forceinline__ float exp8_nonpos(float x) {
@@ -115,7 +116,7 @@ __device__ __forceinline__ float exp_sum_term(float x) { return __builtin_amdgcn
 __device__ __forceinline__ float tanh8(float x) {
     const unsigned sign = __float_as_uint(x) & 0x80000000u;
     const float ax = __uint_as_float(__float_as_uint(x) & 0x7fffffffu);
-    const float e = exp8(ax * -2.0f);
+    const float e = exp8_nonpos(ax * -2.0f);  // ax * -2 <= 0 (or NaN)
     float big = (1.0f - e) / (1.0f + e);
     big = __uint_as_float(__float_as_uint(big) | sign);
     const float z = x * x;
@@ -134,7 +135,7 @@ __device__ __forceinline__ float erf8(float x) {
     p = fma_(p, t, 1.421413741f);
     p = fma_(p, t, -0.284496736f);
     p = fma_(p, t, 0.254829592f);
-    const float e = exp8(0.0f - ax * ax);
+    const float e = exp8_nonpos(0.0f - ax * ax);  // <= 0 (or NaN)
     const float r = fma_(-(p * t), e, 1.0f);
     return __uint_as_float(__float_as_uint(r) | sign);
 }

@@ -71,7 +71,7 @@ __device__ __forceinline__ float act_bwd(float gi, float v, float y, float g, fl
             t = (g * sg) * (1.0f + v * (1.0f - sg));
         } else if constexpr (K == NC_HIP_UN_GELU) {
             const float e = erf8(NC_K_SQRT1_2 * v);
-            const float q = exp8((-0.5f * v) * v);
+            const float q = exp8_nonpos((-0.5f * v) * v);  // -v^2 / 2 <= 0 (or NaN)
             t = g * (0.5f * (1.0f + e) + (v * NC_K_INV_SQRT_2PI) * q);
         } else if constexpr (K == NC_HIP_UN_GELU_TANH) {
             const float th = tanh8(NC_K_SQRT_2_PI * (v + ((NC_K_GELU_C * v) * v) * v));
