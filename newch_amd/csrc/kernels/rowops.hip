@@ -864,6 +864,8 @@ __global__ __launch_bounds__(kCombCols *kCombSlices) void k_ln_cols_combine(cons
     float *out = which == 0 ? gw : gb;
     if (!out) return;  // uniform over the workgroup
     const double *src = part + (size_t)which * D;
+    // the gradient being added into, loaded beside the partials rather than after their sum
+    const float o = y == 0 && i < D ? out[i] : 0.0f;
     double t = 0.0;
     if (i < D) {
 #pragma unroll 4
@@ -875,7 +877,7 @@ __global__ __launch_bounds__(kCombCols *kCombSlices) void k_ln_cols_combine(cons
         double s = 0.0;
 #pragma unroll
         for (int k = 0; k < kCombSlices; k++) s += sh[k][x];
-        out[i] = (float)((double)out[i] + s);
+        out[i] = (float)((double)o + s);
     }
 }
 
