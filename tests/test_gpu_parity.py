@@ -2076,13 +2076,27 @@ def random_gemms(seed, n, max_mnk=3e9):
     return out
 
 
+def pipe_gemms(seed, n):
+    """Seeded (M, N, K) in the software-pipelined int8 kernel's domain: at least a 256 x 256 tile per CU
+    (256 CUs), K a multiple of 256 (one to eight pairs of 128-byte steps), M and N ragged or whole tiles."""
+    rng = np.random.default_rng(seed)
+    out = []
+    while len(out) < n:
+        m = int(rng.integers(16, 40)) * 256 + int(rng.choice([0, 0, 1, 37, 255]))
+        nn = int(rng.integers(16, 40)) * 256 + int(rng.choice([0, 0, 3, 129, 200]))
+        k = 256 * int(rng.integers(1, 9))
+        if ((m + 255) // 256) * ((nn + 255) // 256) >= 256:
+            out.append((m, nn, k))
+    return out
+
+
 S8_SIZES = [(1, 1, 16), (5, 6, 37), (128, 128, 64), (300, 260, 1040), (257, 129, 1000), (33, 517, 80), (7, 3, 0),
             (2048, 1024, 4096),
             # >= 256 tiles of 256 x 256: K a multiple of 256, the software-pipelined kernel (one pair of k
             # steps, the shortest loop, and more; full and partial edge tiles); K % 256 == 128, the 16-wave
             # direct-to-LDS kernel; K % 128 != 0, the register-staged 256 x 256 kernel
             (4100, 4000, 512), (4096, 4096, 256), (4352, 4000, 1280), (4100, 4000, 384), (4096, 4096, 640),
-            (4096, 4352, 1040), (4096, 4096, 576)] + random_gemms(21, 16 * SWEEP)
+            (4096, 4352, 1040), (4096, 4096, 576)] + random_gemms(21, 16 * SWEEP) + pipe_gemms(27, 4 * SWEEP)
 
 
 def _rows_sample(M, n=48, seed=0):
