@@ -114,7 +114,13 @@ __device__ __forceinline__ void ce_fwd_rows(const float *__restrict__ x, const i
     };
     // rows r0, r0 + stride, ... through two register sets in turn.  In the steady state every load is
     // unconditional and issued in this order: the current row's label logit, then the next row and its
-    // label, so the waits for the current row never cover the next row's loads.
+    // label, so the waits for the current row never cover the next row's loads.  Where the workgroup's
+    // four waves run the steady-state loop the same number of times (every workgroup unless N ends
+    // inside its last stride), they meet at a barrier before each pair of rows: waves kept in step read
+    // neighbouring rows together (45.9 -> 45.4 us over X[65536, 1024]).
+    auto trips = [&](int64_t r) { return r < N ? (N - r - 1) / (2 * stride) : (int64_t)0; };
+    const int64_t rw = (int64_t)blockIdx.x * kLWaves;  // the workgroup's first row
+    const bool lock = trips(rw) == trips(rw + kLWaves - 1);  // uniform over the workgroup
     int64_t r = ((int64_t)blockIdx.x * kLB + threadIdx.x) / kWave;
     f4 va[VPL], vb[VPL];
     int32_t la = 0, lb = 0;
@@ -123,6 +129,7 @@ __device__ __forceinline__ void ce_fwd_rows(const float *__restrict__ x, const i
         la = lab[r];
     }
     while (r + 2 * stride < N) {
+        if (lock) __syncthreads();
         const float xa = label_logit(r, la);
         load(r + stride, vb);
         lb = lab[r + stride];
