@@ -45,6 +45,7 @@ TIMED = 10  # timed launches per op class (the median is reported)
 WARM = 2  # untimed launches of each op class first
 GEMM_RAMP_S = 0.25  # untimed seconds of the first contraction before the GEMM leg is timed
 FLUSH_KERNEL = "k_fill16"  # the 1 GiB cache-flush fill between timed launches
+CLASS_ORDER = "blocked"  # a group's timed launches class by class ("blocked") or round-robin ("interleaved")
 
 
 def log(*a):
@@ -352,8 +353,13 @@ GEMM_LABELS = ["linear_fwd_sgemm_nt", "linear_bwd_dx_sgemm_nn", "linear_bwd_dw_s
 
 def run_group(K, hm, builder, labels=None, setup_only=False):
     """WARM untimed launches of each op class, then TIMED launches each after a 1 GiB fill that evicts
-    the 256 MB MALL (outside the launch's events): a cold-cache median per class.  setup_only: build
-    the group's inputs and stop (the profiler pass whose counters are subtracted from the labels')."""
+    the 256 MB MALL (outside the launch's events): a cold-cache median per class.  The timed launches
+    run class by class, so a class's time does not depend on which classes share its group or their
+    order: round-robin over the classes, a short kernel ran slower after some neighbours than after
+    others despite the fill (the cross-entropy forward 45.7 us after itself, 47.3-49.0 after the
+    LayerNorm backward or the whole group; --class-order interleaved keeps that order for comparison).
+    setup_only: build the group's inputs and stop (the profiler pass whose counters are subtracted
+    from the labels')."""
     work, keep = builder(K, hm)
     if setup_only:
         hm.synchronize()
@@ -366,10 +372,16 @@ def run_group(K, hm, builder, labels=None, setup_only=False):
     hm.synchronize()
     flush = hm.DeviceBuffer(1 << 30)
     tl = Timeline(hm)
-    for _ in range(TIMED):
+    if CLASS_ORDER == "interleaved":
+        for _ in range(TIMED):
+            for label, nbytes, elements, fn in work:
+                K.fill(flush.ptr, 4, 0, 1 << 28)
+                tl.run(label, nbytes, elements, fn)
+    else:
         for label, nbytes, elements, fn in work:
-            K.fill(flush.ptr, 4, 0, 1 << 28)
-            tl.run(label, nbytes, elements, fn)
+            for _ in range(TIMED):
+                K.fill(flush.ptr, 4, 0, 1 << 28)
+                tl.run(label, nbytes, elements, fn)
     hm.synchronize()
     tl.collect()
     del keep, flush
@@ -739,17 +751,21 @@ def only_mode(K, hm, labels, setup_only=False):
 
 
 def main():
+    global CLASS_ORDER
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=500)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--classes", choices=["all", "none"], default="all")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--class-order", choices=["interleaved", "blocked"], default=CLASS_ORDER,
+                    help="a group's timed launches round-robin over its classes, or class by class")
     ap.add_argument("--only", default=None, help="comma-separated op-class labels: run just those")
     ap.add_argument("--setup-only", action="store_true", help="with --only: build the inputs, launch nothing")
     ap.add_argument("--traffic-summary", default=None, help="print the per-label HBM traffic table of the "
                     "PMC passes under this directory (no GPU work)")
     args = ap.parse_args()
+    CLASS_ORDER = args.class_order
     if args.traffic_summary:
         sys.stdout.write(traffic_summary(Path(args.traffic_summary)))
         return
