@@ -185,6 +185,40 @@ GEMM = [(1024, 1024, 512, 0, 1), (2048, 1536, 256, 0, 0), (512, 768, 1040, 1, 1)
         (4096, 2048, 64, 0, 1)]
 
 
+# short-K batched products of whole 256 x 256 tiles (as attention scores: B a transposed view, A
+# strided or broadcast over the batch, C = alpha A B), tiles from one to several per CU over the grids,
+# against fp64 too.  batch, M, N, K, alpha, A batch stride (0: broadcast)
+GEMM_PT = [(24, 1280, 1280, 128, 1.0, 1), (32, 1024, 1024, 64, 1.0, 1), (1, 8192, 4096, 512, 0.5, 1),
+           (20, 1024, 512, 192, 1.0, 0)]
+
+
+@pytest.mark.parametrize("bc,M,N,Kd,alpha,sa", GEMM_PT)
+def test_gemm_f32_short_k_batch_independent_of_cus(K, bc, M, N, Kd, alpha, sa):
+    rng = np.random.default_rng(bc * 7 + M + N + Kd)
+    A = rng.standard_normal((max(bc * sa, 1), M, Kd)).astype(np.float32)
+    B = rng.standard_normal((bc, N, Kd)).astype(np.float32)  # used transposed
+    Ad, Bd = dev(A), dev(B)
+    print(f"short-K GEMM batch {bc} {M}x{N}x{Kd}", flush=True)
+
+    def run():
+        C = empty(4 * bc * M * N)
+        if bc == 1:
+            K.gemm_f32(0, 1, M, N, Kd, alpha, Ad.ptr, Kd, Bd.ptr, Kd, 0.0, C.ptr, N)
+        else:
+            K.gemm_f32_bmm(0, 1, M, N, Kd, Ad.ptr, Kd, Bd.ptr, Kd, 0.0, C.ptr, N, (bc,), (sa * M * Kd,), (N * Kd,),
+                           (M * N,))
+        sync()
+        return (C.to_numpy(np.float32, (bc, M, N)),)
+
+    out = across_cus(K, run)[0]
+    for b in (0, bc - 1):
+        rows = np.arange(0, M, 97)
+        a = A[b * sa][rows].astype(np.float64)
+        want = alpha * (a @ B[b].T.astype(np.float64))
+        terms = abs(alpha) * (np.abs(a) @ np.abs(B[b].T).astype(np.float64))
+        assert O.gemm_excess(out[b][rows], want, terms, Kd) <= 1.0, f"batch {b}"
+
+
 @pytest.mark.parametrize("M,N,Kd,ta,tb", GEMM)
 def test_gemm_f32_independent_of_cus(K, M, N, Kd, ta, tb):
     rng = np.random.default_rng(M + N + Kd)
