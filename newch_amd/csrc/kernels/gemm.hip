@@ -285,14 +285,39 @@ __device__ __forceinline__ void fold(f4 (&tot)[Cfg::TM][Cfg::TN], f4 (&acc)[Cfg:
         }
 }
 
+// A wave's stores of one row block's final totals during the last panel: C row (tile row + fr) of row
+// block 0 at byte offset `off` from the tile's C (lane's four columns), row block i `rb` bytes further.
+struct RbStore {
+    const float *base;  // the batch matrix's C (wave-uniform)
+    uint32_t off;       // this lane's first element, row block 0, tile column 0, in bytes
+    uint32_t rb;        // 16 rows of C, in bytes
+    float alpha;
+};
+
+// One 16-byte store at a wave-uniform base plus a 32-bit offset.  The store reads its data registers
+// after it issues, and a VALU instruction may overwrite them only two wait states later on this
+// family; the compiler inserts those after its own stores, not after inline assembly, so the s_nop
+// (three wait states) is part of the statement (without it the next value's fourth component reached
+// memory now and then).
+__device__ __forceinline__ void store16(const float *base, uint32_t off, f4 v) {
+    asm volatile("global_store_dwordx4 %0, %1, %2\n\ts_nop 2" ::"v"(off), "v"(v), "s"(base) : "memory");
+}
+
 // The direct-to-LDS kernel has a whole panel in LDS and works it row block by row block, so only one
 // row block's TN panel sums are live beside the totals: the B fragments of the panel's stages are read
 // once; per row block the A fragments are read, each tile sums its panel's products from zero (stage
 // 0's four MFMAs, then stage 1's), and the sums are added into the totals.  TWO: the panel has its
 // second stage (every panel but a last one of an odd stage count).
+// ST (the last panel of a tile stored as it completes): once the next row block's adds have made a row
+// block's totals final, its TN tiles are stored between that row block's MFMAs, so a tile's 256 x 256
+// output leaves spread over its last panel instead of all CUs storing at the same moment after it.
 template <class Cfg, bool AK, bool BK>
 __device__ __forceinline__ void panel_mfma(const char *c0, const char *c1, f4 (&tot)[Cfg::TM][Cfg::TN], int wm, int wn,
-                                           int fr, int fq) {
+                                           int fr, int fq, const RbStore *rs = nullptr, bool st = false) {
+    auto store_rb = [&](int i) {
+#pragma unroll
+        for (int j = 0; j < Cfg::TN; j++) store16(rs->base, rs->off + (uint32_t)i * rs->rb + (uint32_t)(j * 64), rs->alpha * tot[i][j]);
+    };
     static_assert(Cfg::TN == 4, "one previous-row-block add per k step");
     f4 b0[Cfg::TN], b1[Cfg::TN];
 #pragma unroll
@@ -326,6 +351,7 @@ __device__ __forceinline__ void panel_mfma(const char *c0, const char *c1, f4 (&
                                                             0, 0, 0);
             }
             if (i > 0 && s < Cfg::TN) tot[i - 1][s] = tot[i - 1][s] + tp[s];
+            if (st && i > 0 && s == Cfg::TN) store_rb(i - 1);
             __builtin_amdgcn_sched_barrier(0);
         }
 #pragma unroll
@@ -334,6 +360,7 @@ __device__ __forceinline__ void panel_mfma(const char *c0, const char *c1, f4 (&
     }
 #pragma unroll
     for (int j = 0; j < Cfg::TN; j++) tot[Cfg::TM - 1][j] = tot[Cfg::TM - 1][j] + tp[j];
+    if (st) store_rb(Cfg::TM - 1);
 }
 
 // C = alpha acc + beta C over the wave's tiles.  acc[i][j] is the 16 x 16 tile C^T: lane l, element v
@@ -489,6 +516,18 @@ __global__ __launch_bounds__(Cfg::NT, 1) void k_sgemm_dma(SgArgs p) {
     // LDS stage slots 0-1 and 2-3 alternate between panels: panel q + 1 loads while panel q is worked
     // (K is a multiple of 32: whole panels)
     const int npanel = p.K / (kSgBK * kSgPanel);
+    // both operands K-contiguous (the layouts with registers to spare for it), a whole tile, C = alpha A B
+    // with 16-byte rows and the tile within 4 GiB of the matrix's start: the last panel stores its row
+    // blocks as they complete (uniform over the workgroup).  39% of the 64 x [1024,128] x [128,1024]
+    // batched product's time was its output leaving in one burst per tile round: 185 -> 162-166 us.
+    const bool stream_st = AK && BK && p.beta == 0.0f && ((uintptr_t)at.C & 15) == 0 && p.ldc % 4 == 0 &&
+                           at.m0 + Cfg::BM <= p.M && at.n0 + Cfg::BN <= p.N &&
+                           ((int64_t)at.m0 + Cfg::BM) * p.ldc * 4 < ((int64_t)1 << 32);
+    RbStore rs;
+    rs.base = at.C;
+    rs.off = (uint32_t)(((int64_t)(at.m0 + wm * Cfg::TM * 16 + fr) * p.ldc + at.n0 + wn * Cfg::TN * 16 + 4 * fq) * 4);
+    rs.rb = (uint32_t)(16 * p.ldc * 4);
+    rs.alpha = p.alpha;
     auto issue_panel = [&](int q) {
         issue(kSgPanel * q);
         issue(kSgPanel * q + 1);
@@ -501,9 +540,10 @@ __global__ __launch_bounds__(Cfg::NT, 1) void k_sgemm_dma(SgArgs p) {
         if (q + 1 < npanel) issue_panel(q + 1);  // into the slots panel q - 1 used
         const int k0 = kSgPanel * q;
         panel_mfma<Cfg, AK, BK>(smem + (k0 % kSgDmaStages) * Cfg::STAGE,
-                                      smem + ((k0 + 1) % kSgDmaStages) * Cfg::STAGE, tot, wm, wn, fr, fq);
+                                smem + ((k0 + 1) % kSgDmaStages) * Cfg::STAGE, tot, wm, wn, fr, fq, &rs,
+                                stream_st && q + 1 == npanel);
     }
-    write_tiles<Cfg>(p, at, tot, wm, wn, fr, fq);
+    if (!stream_st) write_tiles<Cfg>(p, at, tot, wm, wn, fr, fq);
 }
 
 template <class Cfg, bool AK, bool BK, bool VEC, bool FAST>
