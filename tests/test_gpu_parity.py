@@ -2241,27 +2241,30 @@ def test_kernel_gemm_f32_bmm_large_broadcast(K):
 
 # both operands K-contiguous, whole 256 x 256 tiles, C = alpha A B: the direct-to-LDS kernel stores each
 # row block of its last panel as soon as it is final; with ldc = N + 1 (rows not 16-byte aligned) the
-# same products go through the ordinary epilogue.  batch, M, N, K
-STREAMED = [(16, 1024, 1024, 128), (1, 4096, 4096, 256), (24, 1280, 1280, 64), (1, 4100, 4096, 512), (2, 2048, 4096, 1024)]
+# same products go through the ordinary epilogue.  batch, M, N, K, extra elements in the batch stride
+# of C (2: every other batch matrix 8-byte aligned, so its tiles keep the epilogue in the same launch)
+STREAMED = [(16, 1024, 1024, 128, 0), (1, 4096, 4096, 256, 0), (24, 1280, 1280, 64, 0), (1, 4100, 4096, 512, 0),
+            (2, 2048, 4096, 1024, 0), (16, 1024, 1024, 128, 2)]
 
 
-@pytest.mark.parametrize("bc,M,N,Kd", STREAMED)
-def test_kernel_gemm_f32_streamed_stores_match_epilogue(K, bc, M, N, Kd):
+@pytest.mark.parametrize("bc,M,N,Kd,cpad", STREAMED)
+def test_kernel_gemm_f32_streamed_stores_match_epilogue(K, bc, M, N, Kd, cpad):
     rng = np.random.default_rng(bc + M + 3 * Kd)
     A = rng.standard_normal((bc, M, Kd)).astype(np.float32)
     Bm = rng.standard_normal((bc, N, Kd)).astype(np.float32)  # used transposed
     Ad, Bd = dev(A), dev(Bm)
     print(f"streamed-store GEMM batch {bc} {M}x{N}x{Kd}", flush=True)
     outs = []
-    for ldc in (N, N + 1):
-        C = empty(4 * bc * M * ldc)
+    for ldc, pad in ((N, cpad), (N + 1, 0)):
+        cs = M * ldc + pad  # batch stride of C
+        C = empty(4 * bc * cs)
         if bc == 1:
             K.gemm_f32(0, 1, M, N, Kd, 0.5, Ad.ptr, Kd, Bd.ptr, Kd, 0.0, C.ptr, ldc)
         else:
-            K.gemm_f32_bmm(0, 1, M, N, Kd, Ad.ptr, Kd, Bd.ptr, Kd, 0.0, C.ptr, ldc, (bc,), (M * Kd,), (N * Kd,),
-                           (M * ldc,))
+            K.gemm_f32_bmm(0, 1, M, N, Kd, Ad.ptr, Kd, Bd.ptr, Kd, 0.0, C.ptr, ldc, (bc,), (M * Kd,), (N * Kd,), (cs,))
         sync()
-        outs.append(C.to_numpy(np.float32, (bc, M, ldc))[:, :, :N])
+        flat = C.to_numpy(np.float32, bc * cs).reshape(bc, cs)[:, :M * ldc]
+        outs.append(flat.reshape(bc, M, ldc)[:, :, :N])
     assert_bits(outs[0], outs[1], "streamed stores against the epilogue")
     alpha = 0.5 if bc == 1 else 1.0  # the batched entry point has no alpha
     rows = np.arange(0, M, 61)
