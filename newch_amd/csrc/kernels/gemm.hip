@@ -306,11 +306,10 @@ __device__ __forceinline__ void store16(const float *base, uint32_t off, f4 v) {
 // The direct-to-LDS kernel has a whole panel in LDS and works it row block by row block, so only one
 // row block's TN panel sums are live beside the totals: the B fragments of the panel's stages are read
 // once; per row block the A fragments are read, each tile sums its panel's products from zero (stage
-// 0's four MFMAs, then stage 1's), and the sums are added into the totals.  TWO: the panel has its
-// second stage (every panel but a last one of an odd stage count).
-// ST (the last panel of a tile stored as it completes): once the next row block's adds have made a row
-// block's totals final, its TN tiles are stored between that row block's MFMAs, so a tile's 256 x 256
-// output leaves spread over its last panel instead of all CUs storing at the same moment after it.
+// 0's four MFMAs, then stage 1's), and the sums are added into the totals.  st (the tile's last panel,
+// stored as it completes, through rs): once the next row block's adds have made a row block's totals
+// final, its TN tiles are stored between that row block's MFMAs, so a tile's 256 x 256 output leaves
+// spread over its last panel instead of all CUs storing at the same moment after it.
 template <class Cfg, bool AK, bool BK>
 __device__ __forceinline__ void panel_mfma(const char *c0, const char *c1, f4 (&tot)[Cfg::TM][Cfg::TN], int wm, int wn,
                                            int fr, int fq, const RbStore *rs = nullptr, bool st = false) {
