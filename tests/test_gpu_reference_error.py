@@ -13,7 +13,7 @@ everywhere; the reference's own result is reported beside it and flagged where i
     fp32 (engine/src/ops/ops_elementwise.c:33-36, 166-168);
   * LayerNorm gw / gb over 65,536 rows: fp32 sums across rows (engine/src/ops/ops_nn.c:511-512);
   * fp32 matmul with 4096 and 16384-term dot products: the reference sums KC = 256 register panels
-    into C (engine/src/kernels/x86/kernels_avx2.c:234-247), this build 32-k panels into running totals
+    into C (engine/src/kernels/x86/kernels_avx2.c:234-247), this engine 32-k panels into running totals
     on the matrix cores (a 4096 x 4096 output through the direct-to-LDS kernel, a 2048 x 2048 one
     through the register-staged 128 x 128 tiles); error on 64 sampled rows against the GEMM bar
     (scale = sum|a b| / sqrt(K)).
