@@ -241,6 +241,12 @@ NC_HIP_API int nc_hip_scale_multi(int count, float *const *x, const int64_t *n, 
 NC_HIP_API int nc_hip_gemm_f32(int ta, int tb, int64_t M, int64_t N, int64_t K, float alpha, const float *A,
                                int64_t lda, const float *B, int64_t ldb, float beta, float *C, int64_t ldc,
                                void *stream);
+/* C = alpha * op(A) op(B) + bias, bias[N] added to every row (NULL: none): the bits of nc_hip_gemm_f32
+ * with beta 0 followed by a broadcast add of the bias, in one pass over C.  linear's forward
+ * (ops_linalg.c:296-330, x W^T then the bias) uses it. */
+NC_HIP_API int nc_hip_gemm_f32_bias(int ta, int tb, int64_t M, int64_t N, int64_t K, float alpha, const float *A,
+                                    int64_t lda, const float *B, int64_t ldb, const float *bias, float *C, int64_t ldc,
+                                    void *stream);
 NC_HIP_API int nc_hip_gemm_f32_batched(int ta, int tb, int64_t M, int64_t N, int64_t K, float alpha,
                                        const float *const *A, int64_t lda, const float *const *B, int64_t ldb,
                                        float beta, float *const *C, int64_t ldc, int64_t count, void *stream);

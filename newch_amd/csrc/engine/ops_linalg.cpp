@@ -104,9 +104,15 @@ void grad_steps(const nc_tensor *t, const Dims &batch, int64_t *out) {
     batch_steps(t, cs, batch, out);
 }
 
-// C (+)= A @ B, A [M, K], B [K, N], C [M, N] with leading dim ldc; batched when batch has axes
+// C (+)= A @ B, A [M, K], B [K, N], C [M, N] with leading dim ldc; batched when batch has axes.  bias
+// (one matrix, beta 0): N floats added to every row of the product in the same pass.
 bool product(nc_ctx *ctx, const Dims &batch, int64_t M, int64_t N, int64_t K, const Operand &a, const Operand &b,
-             float beta, float *C, int64_t ldc, const int64_t *cst, const char *what) {
+             float beta, float *C, int64_t ldc, const int64_t *cst, const char *what, const float *bias = nullptr) {
+    if (batch.rank == 0 && bias)
+        return hip_layer_ok(ctx,
+                            nc_hip_gemm_f32_bias(a.m.trans, b.m.trans, M, N, K, 1.0f, a.m.p, a.m.ld, b.m.p, b.m.ld,
+                                                 bias, C, ldc, stream(ctx)),
+                            what);
     if (batch.rank == 0)
         return hip_layer_ok(ctx,
                             nc_hip_gemm_f32(a.m.trans, b.m.trans, M, N, K, 1.0f, a.m.p, a.m.ld, b.m.p, b.m.ld, beta, C,
@@ -297,12 +303,8 @@ nc_status linear_fwd(nc_node *n) {
     const float *B = bias ? contig_f32(bias) : nullptr;
     float *Y = fptr(n->out);
     if (!as_rows(x, a.m) || !last_two(w, wt.m, &unused, packed) || (bias && !B) || !Y) return NC_ERR_STATE;
-    if (!product(ctx, Dims{}, M, out, in, a, wt.transposed(), 0.0f, Y, out, nullptr, "linear")) return NC_ERR_STATE;
-    if (B && M > 0 && out > 0) {  // y = (x W^T) + b: the sum rounded once, as a beta = 1 GEMM over b rows would
-        const int64_t shape[2] = {M, out}, sy[2] = {out, 1}, sb[2] = {0, 1};
-        if (!hip_layer_ok(ctx, nc_hip_binary_fwd(NC_HIP_BIN_ADD, 2, shape, Y, sy, B, sb, Y, sy, stream(ctx)), "linear"))
-            return NC_ERR_STATE;
-    }
+    // y = (x W^T) + b: the product rounded, then the bias added, in the GEMM's own pass over y
+    if (!product(ctx, Dims{}, M, out, in, a, wt.transposed(), 0.0f, Y, out, nullptr, "linear", B)) return NC_ERR_STATE;
     wrote_dev(n->out);
     return NC_OK;
 }

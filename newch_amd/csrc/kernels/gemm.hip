@@ -74,6 +74,7 @@ struct SgArgs {
     int64_t lda, ldb, ldc;
     int M, N, K;
     float alpha, beta;
+    const float *bias;  // N floats added to every row after alpha A B + beta C, or none
     int tiles_m, tiles_n;
     SgBatch bat;
 };
@@ -362,13 +363,15 @@ __device__ __forceinline__ void panel_mfma(const char *c0, const char *c1, f4 (&
     if (st) store_rb(Cfg::TM - 1);
 }
 
-// C = alpha acc + beta C over the wave's tiles.  acc[i][j] is the 16 x 16 tile C^T: lane l, element v
-// holds row (tile row + l % 16), column (tile column + 4 (l / 16) + v).
+// C = alpha acc + beta C (+ bias[n]) over the wave's tiles.  acc[i][j] is the 16 x 16 tile C^T: lane l,
+// element v holds row (tile row + l % 16), column (tile column + 4 (l / 16) + v).  The bias is added to
+// the rounded alpha acc + beta C, as a separate broadcast add of it would.
 template <class Cfg>
 __device__ __forceinline__ void write_tiles(const SgArgs &p, const TileAt &at, const f4 (&acc)[Cfg::TM][Cfg::TN],
                                             int wm, int wn, int fr, int fq) {
     constexpr int kTM = Cfg::TM, kTN = Cfg::TN;
     const bool vec_c = ((uintptr_t)at.C & 15) == 0 && p.ldc % 4 == 0;
+    const bool vec_b = ((uintptr_t)p.bias & 15) == 0;
 #pragma unroll
     for (int i = 0; i < kTM; i++) {
         const int m = at.m0 + (wm * kTM + i) * 16 + fr;
@@ -381,13 +384,18 @@ __device__ __forceinline__ void write_tiles(const SgArgs &p, const TileAt &at, c
             if (vec_c && n + 4 <= p.N) {
                 f4 *c = (f4 *)(crow + n);
                 if (p.beta != 0.0f) r = r + p.beta * *c;
+                if (p.bias) {
+                    if (vec_b) r = r + *(const f4 *)(p.bias + n);
+                    else r = r + f4{p.bias[n], p.bias[n + 1], p.bias[n + 2], p.bias[n + 3]};
+                }
                 *c = r;
             } else {
 #pragma unroll
                 for (int v = 0; v < 4; v++) {
                     if (n + v >= p.N) break;
                     float *c = crow + n + v;
-                    *c = p.beta != 0.0f ? r[v] + p.beta * *c : r[v];
+                    const float t = p.beta != 0.0f ? r[v] + p.beta * *c : r[v];
+                    *c = p.bias ? t + p.bias[n + v] : t;
                 }
             }
         }
@@ -520,7 +528,7 @@ __global__ __launch_bounds__(Cfg::NT, 1) void k_sgemm_dma(SgArgs p) {
     // blocks as they complete (uniform over the workgroup).  The 64 x [1024,128] x [128,1024] batched
     // product spent a quarter of its time (185 us against 141 without stores) on its output leaving in one
     // burst per tile round: 185 -> 162-166 us.
-    const bool stream_st = AK && BK && p.beta == 0.0f && ((uintptr_t)at.C & 15) == 0 && p.ldc % 4 == 0 &&
+    const bool stream_st = AK && BK && p.beta == 0.0f && !p.bias && ((uintptr_t)at.C & 15) == 0 && p.ldc % 4 == 0 &&
                            at.m0 + Cfg::BM <= p.M && at.n0 + Cfg::BN <= p.N &&
                            ((int64_t)at.m0 + Cfg::BM) * p.ldc * 4 < ((int64_t)1 << 32);
     RbStore rs;
@@ -703,6 +711,19 @@ extern "C" NC_HIP_API int nc_hip_gemm_f32(int ta, int tb, int64_t M, int64_t N, 
         return set_error(NC_HIP_ERR_ARG, "nc_hip_gemm_f32: leading dim too small");
     SgArgs p = sg_args(M, N, K, alpha, A, lda, B, ldb, beta, C, ldc);
     return sg_run(p, ta, tb, 1, as_stream(stream), "nc_hip_gemm_f32");
+}
+
+extern "C" NC_HIP_API int nc_hip_gemm_f32_bias(int ta, int tb, int64_t M, int64_t N, int64_t K, float alpha,
+                                               const float *A, int64_t lda, const float *B, int64_t ldb,
+                                               const float *bias, float *C, int64_t ldc, void *stream) {
+    if (!fits_int(M) || !fits_int(N) || !fits_int(K)) return set_error(NC_HIP_ERR_ARG, "nc_hip_gemm_f32_bias: bad size");
+    if (M == 0 || N == 0) return NC_HIP_OK;
+    if (ldc < N) return set_error(NC_HIP_ERR_ARG, "nc_hip_gemm_f32_bias: ldc %lld < N %lld", (long long)ldc, (long long)N);
+    if (K > 0 && (lda < (ta ? M : K) || ldb < (tb ? K : N)))
+        return set_error(NC_HIP_ERR_ARG, "nc_hip_gemm_f32_bias: leading dim too small");
+    SgArgs p = sg_args(M, N, K, alpha, A, lda, B, ldb, 0.0f, C, ldc);
+    p.bias = bias;
+    return sg_run(p, ta, tb, 1, as_stream(stream), "nc_hip_gemm_f32_bias");
 }
 
 extern "C" NC_HIP_API int nc_hip_gemm_f32_batched(int ta, int tb, int64_t M, int64_t N, int64_t K, float alpha,

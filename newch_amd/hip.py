@@ -78,6 +78,8 @@ SIGNATURES = {
     "nc_hip_nll_loss_bwd": (c_int, [c_int64, c_int64, P, P, c_int, P, P]),
     "nc_hip_gemm_f32": (c_int, [c_int, c_int, c_int64, c_int64, c_int64, c_float, P, c_int64, P, c_int64, c_float, P,
                                 c_int64, P]),
+    "nc_hip_gemm_f32_bias": (c_int, [c_int, c_int, c_int64, c_int64, c_int64, c_float, P, c_int64, P, c_int64, P, P,
+                                     c_int64, P]),
     "nc_hip_gemm_f32_batched": (c_int, [c_int, c_int, c_int64, c_int64, c_int64, c_float, P, c_int64, P, c_int64,
                                         c_float, P, c_int64, c_int64, P]),
     "nc_hip_gemm_f32_bmm_workspace": (c_size_t, [c_int64]),
@@ -254,6 +256,10 @@ class Kernels:
     def gemm_f32(self, ta, tb, M, N, K, alpha, A, lda, B, ldb, beta, C, ldc, stream=None):
         self._ok(self.lib.nc_hip_gemm_f32(int(ta), int(tb), M, N, K, alpha, A, lda, B, ldb, beta, C, ldc, stream),
                  "gemm_f32")
+
+    def gemm_f32_bias(self, ta, tb, M, N, K, alpha, A, lda, B, ldb, bias, C, ldc, stream=None):
+        self._ok(self.lib.nc_hip_gemm_f32_bias(int(ta), int(tb), M, N, K, alpha, A, lda, B, ldb, bias, C, ldc, stream),
+                 "gemm_f32_bias")
 
     def gemm_f32_batched(self, ta, tb, M, N, K, alpha, A, lda, B, ldb, beta, C, ldc, count, stream=None):
         self._ok(self.lib.nc_hip_gemm_f32_batched(int(ta), int(tb), M, N, K, alpha, A, lda, B, ldb, beta, C, ldc, count,

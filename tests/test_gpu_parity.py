@@ -2242,6 +2242,30 @@ def test_kernel_gemm_f32_bmm_large_broadcast(K):
         assert O.gemm_excess(got[b][rows], want, terms, Kd) <= 1.0, f"batch {b}"
 
 
+# C = alpha op(A) op(B) + bias in the GEMM's epilogue against the GEMM followed by a broadcast add of the
+# bias (linear's forward before the fusion): every layout, the register-staged and direct-to-LDS kernels,
+# ragged tiles, K = 0, and a bias that is not 16-byte aligned.  ta, tb, M, N, K, bias offset (floats)
+GEMM_BIAS = [(0, 1, 4096, 4096, 256, 0), (0, 0, 4100, 4096, 256, 0), (1, 0, 4096, 4100, 512, 1), (1, 1, 4096, 4096, 256, 0),
+             (0, 1, 1000, 500, 300, 0), (0, 1, 33, 65, 17, 3), (1, 0, 257, 129, 1000, 1), (0, 1, 64, 96, 0, 0),
+             (0, 1, 8192, 4096, 128, 0)]
+
+
+@pytest.mark.parametrize("ta,tb,M,N,Kd,boff", GEMM_BIAS)
+def test_kernel_gemm_f32_bias_matches_separate_add(K, ta, tb, M, N, Kd, boff):
+    rng = np.random.default_rng(M + N + Kd + ta + 2 * tb + boff)
+    A = rng.standard_normal((Kd, M) if ta else (M, Kd)).astype(np.float32)
+    B = rng.standard_normal((N, Kd) if tb else (Kd, N)).astype(np.float32)
+    bias = np.concatenate([np.zeros(boff, np.float32), rng.standard_normal(N).astype(np.float32)])
+    Ad, Bd, bd = dev(A), dev(B), dev(bias)
+    print(f"gemm_f32_bias ta={ta} tb={tb} {M}x{N}x{Kd} bias offset {boff}", flush=True)
+    C1, C2 = empty(4 * M * N), empty(4 * M * N)
+    K.gemm_f32_bias(ta, tb, M, N, Kd, 0.5, Ad.ptr, A.shape[1], Bd.ptr, B.shape[1], bd.ptr + 4 * boff, C1.ptr, N)
+    K.gemm_f32(ta, tb, M, N, Kd, 0.5, Ad.ptr, A.shape[1], Bd.ptr, B.shape[1], 0.0, C2.ptr, N)
+    K.binary_fwd("add", (M, N), C2.ptr, (N, 1), bd.ptr + 4 * boff, (0, 1), C2.ptr, (N, 1))
+    sync()
+    assert_bits(C1.to_numpy(np.float32, (M, N)), C2.to_numpy(np.float32, (M, N)), "fused bias against the separate add")
+
+
 # both operands K-contiguous, whole 256 x 256 tiles, C = alpha A B: the direct-to-LDS kernel stores each
 # row block of its last panel as soon as it is final; with ldc = N + 1 (rows not 16-byte aligned) the
 # same products go through the ordinary epilogue.  batch, M, N, K, extra elements in the batch stride
