@@ -624,6 +624,15 @@ def engine_leg(K, hm, classes):
     Bv = persistent_from(hm.DeviceBuffer.from_numpy((0.5 + 1.5 * np.random.default_rng(4).random(512 * 64))
                                                     .astype(np.float32)), abi.F32, (1, 1, 512, 64))
     del Ab
+    # the linear forward of the GEMM leg's shape, bias included: x[8192,4096] W[4096,4096]^T + b
+    XLb = tiled(hm, K, 8192 * 4096, 11)
+    XL = persistent_from(XLb, abi.F32, (8192, 4096))
+    del XLb
+    WLb = tiled(hm, K, 4096 * 4096, 12, scale=0.02)
+    WL = persistent_from(WLb, abi.F32, (4096, 4096))
+    del WLb
+    BL = persistent_from(hm.DeviceBuffer.from_numpy(np.random.default_rng(13).standard_normal(4096, dtype=np.float32)),
+                         abi.F32, (4096,))
     L.nc_persistent_begin(ctx)
     Xp = L.nc_parameter(ctx, X, *abi.shape_arg((rows, C)))
     Ap = L.nc_parameter(ctx, A, *abi.shape_arg((256, 512, 1, 64)))
@@ -662,6 +671,8 @@ def engine_leg(K, hm, classes):
         ("adam_step_32_params", lambda: L.nc_optim_step(opt)),
         # the 32 gradients' norm (one sum launch, one read-back) and their rescale (one launch)
         ("clip_grad_norm_32_params", lambda: L.nc_clip_grad_norm(plist, nps, c_float(1.0))),
+        # the GEMM with the bias added in its epilogue
+        ("linear_fwd_bias", lambda: L.nc_linear_fn(XL, WL, BL)),
     ]
     out = {}
     for label, fn in calls:
